@@ -1,0 +1,339 @@
+#!/usr/bin/env python3
+"""Benchmark of the yllm attention hot path on one MI355X (gfx950).
+
+Metric: attention decode GB/s (% of HBM peak) and prefill attention TFLOP/s
+(% of bf16/f16 MFMA peak).  One "step" is one pass of the hot path over one
+batch of synthetic input, with all inputs resident in HBM:
+
+  prefill2k   (default) causal GQA prefill, 2048 tokens, 28 query / 4 KV
+              heads, head_dim 128, f16 Q/K/V drawn N(0,1)*0.5 from seed
+              0x5EED0002, f32 output -- one yhip_attn_prefill launch.
+  prefill8k   the same at 8192 tokens, 32 / 8 heads.
+  decode32k   one query token per head over a 32768-key cache, 32 / 8 heads,
+              head_dim 128 -- one yhip_attn_decode call (split + merge
+              kernels).  Steps rotate over 6 layer caches (768 MiB) so the
+              256 MB MALL cannot serve repeats.
+  decode128k  131072 keys, 32 / 8 heads (config 4), 2 layer caches.
+  decode_batch 64 sequences, lengths uniform in [1024, 32768] from seed,
+              32 / 8 heads -- one yhip_attn_decode_batch call.
+
+The default line reports prefill2k as `value` and decode32k under
+"secondary".  The CPU baseline is the oracle restatement of the reference's
+OpenMP loops (oracle/), timed on this host on a bounded sample, and the same
+run checks the GPU output against it (relative L2).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
+MFMA_F16_PEAK = 2.5e15   # FLOP/s, dense f16/bf16 MFMA
+METRIC = "attn decode GB/s (% HBM peak); prefill attn TFLOP/s (% MFMA peak)"
+SEED = 0x5EED0000
+
+
+def synth(seed: int, n: int, first: int = 0) -> np.ndarray:
+    from yllm_amd.attention import round_f16, synth_normal
+
+    return round_f16(synth_normal(seed, n, 0.5, first))
+
+
+def prefill_flops(L: int, nh: int, hd: int, pos_start: int = 0) -> float:
+    # QK^T + PV over the causal triangle: 4 * n_q * d * sum_t (keys of token t)
+    keys = sum(range(pos_start + 1, pos_start + L + 1))
+    return 4.0 * nh * hd * keys
+
+
+def time_steps(fn, steps: int, warmup: int):
+    """Run fn(i) warmup times, then time `steps` calls with HIP events on the
+    launch stream (torch's current stream).  Returns (ms_per_step, mean launch
+    ms, wall seconds)."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn(warmup + i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = starts[0].elapsed_time(ends[-1])
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return total_ms / steps, float(np.mean(per)), wall
+
+
+# ------------------------------------------------------------------ workloads
+
+def run_prefill(L: int, nh: int, nkv: int, hd: int, cfg: int, steps: int, warmup: int, cpu: bool):
+    import torch
+
+    from yllm_amd.attention import LayerKV, attn_prefill, kv_store
+
+    dev = torch.device("cuda:0")
+    seed = SEED + cfg
+    nq, nk = L * nh * hd, L * nkv * hd
+    q = torch.from_numpy(synth(seed, nq).reshape(L, nh * hd)).to(dev).half()
+    k = torch.from_numpy(synth(seed, nk, nq).reshape(L, nkv * hd)).to(dev).half()
+    v = torch.from_numpy(synth(seed, nk, nq + nk).reshape(L, nkv * hd)).to(dev).half()
+    cache = LayerKV.empty(nkv, hd, L, device=dev)
+    kv_store(cache, k, v, 0)
+    out = torch.empty((L, nh * hd), dtype=torch.float32, device=dev)
+    ms, kern_ms, _ = time_steps(lambda i: attn_prefill(q, cache, 0, nh, out=out), steps, warmup)
+    flops = prefill_flops(L, nh, hd)
+    achieved = flops / (kern_ms * 1e-3)
+    res = {
+        "value": flops / (ms * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "ms_per_step": ms,
+        "tokens_per_s": L / (ms * 1e-3),
+        "config": {"workload": f"causal GQA prefill attention, {L} tokens, {nh} query / {nkv} KV heads, "
+                               f"head_dim {hd}, f16 Q/K/V N(0,1)*0.5 seed {hex(seed)}, f32 out",
+                   "tokens": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd},
+        "roofline": {"bound": "mfma", "kernel": "prefill_kernel<%d>" % hd, "achieved": achieved / 1e12,
+                     "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s", "frac": achieved / MFMA_F16_PEAK,
+                     "flops_per_launch": flops, "launch_ms": kern_ms, "traffic": traffic_of(f"prefill{L}")},
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_prefill(q, k, v, out, L, nh, nkv, hd)
+    return res
+
+
+def decode_bytes(L: int, nkv: int, nh: int, hd: int) -> float:
+    return float(L) * nkv * hd * 2 * 2 + 2.0 * nh * hd * 4  # K,V once (GQA-aware) + q in + out
+
+
+def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, steps: int, warmup: int,
+               cpu: bool, label: str):
+    import torch
+
+    from yllm_amd.attention import LayerKV, attn_decode, decode_workspace_bytes, kv_store
+
+    dev = torch.device("cuda:0")
+    seed = SEED + cfg
+    nk = L * nkv * hd
+    k = torch.from_numpy(synth(seed, nk).reshape(L, nkv * hd)).to(dev).half()
+    v = torch.from_numpy(synth(seed, nk, nk).reshape(L, nkv * hd)).to(dev).half()
+    q = torch.from_numpy(synth(seed, nh * hd, 2 * nk)).to(dev)
+    caches = []
+    for _ in range(n_layers):  # distinct HBM regions with the same contents
+        c = LayerKV.empty(nkv, hd, L, device=dev, zero=False)
+        kv_store(c, k, v, 0)
+        caches.append(c)
+    del k, v
+    ws = torch.empty(max(decode_workspace_bytes(1, L, L, nh, nkv, hd), 1), dtype=torch.uint8, device=dev)
+    out = torch.empty(nh * hd, dtype=torch.float32, device=dev)
+    ms, kern_ms, _ = time_steps(lambda i: attn_decode(q, caches[i % n_layers], L - 1, nh, out=out, workspace=ws),
+                                steps, warmup)
+    nbytes = decode_bytes(L, nkv, nh, hd)
+    achieved = nbytes / (kern_ms * 1e-3)
+    res = {
+        "value": nbytes / (ms * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "ms_per_step": ms,
+        "tokens_per_s": 1.0 / (ms * 1e-3),
+        "config": {"workload": f"{label}: decode attention, 1 sequence, {L} keys, {nh} query / {nkv} KV heads, "
+                               f"head_dim {hd}, f16 KV N(0,1)*0.5 seed {hex(seed)}, split-K + LSE merge, "
+                               f"{n_layers} rotating layer caches",
+                   "keys": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd},
+        "roofline": {"bound": "hbm", "kernel": "decode_split_kernel<%d> + decode_merge_kernel<%d>" % (hd, hd),
+                     "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK, "bytes_per_launch": nbytes, "launch_ms": kern_ms,
+                     "traffic": traffic_of(label)},
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_decode(q, caches[0], out, L, nh, nkv, hd)
+    return res
+
+
+def run_decode_batch(nh: int, nkv: int, hd: int, n_seq: int, steps: int, warmup: int):
+    import torch
+
+    from yllm_amd.attention import DecodeBatch, LayerKV, attn_decode_batch, decode_workspace_bytes, kv_store
+
+    dev = torch.device("cuda:0")
+    seed = SEED + 3
+    # L_i = 1024 + floor(u * 31745), u from the yrng stream (splitmix64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + np.arange(1, n_seq + 1, dtype=np.uint64) * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        r = z ^ (z >> np.uint64(31))
+    u = ((r >> np.uint64(40)).astype(np.float64) + 0.5) / 16777216.0
+    lens = np.minimum((1024 + np.floor(u * 31745)).astype(np.int64), 32768)
+    kvd = nkv * hd
+    base_k = torch.from_numpy(synth(seed, 32768 * kvd).reshape(32768, kvd)).to(dev).half()
+    base_v = torch.from_numpy(synth(seed, 32768 * kvd, 32768 * kvd).reshape(32768, kvd)).to(dev).half()
+    caches = []
+    for L in lens:
+        c = LayerKV.empty(nkv, hd, int(L), device=dev, zero=False)
+        kv_store(c, base_k[: int(L)], base_v[: int(L)], 0)
+        caches.append(c)
+    batch = DecodeBatch(caches)
+    q = torch.from_numpy(synth(seed + 100, n_seq * nh * hd).reshape(n_seq, nh * hd)).to(dev)
+    lens_dev = torch.tensor(lens.astype(np.int32), device=dev)
+    ws = torch.empty(max(decode_workspace_bytes(n_seq, int(lens.max()), int(lens.sum()), nh, nkv, hd), 1),
+                     dtype=torch.uint8, device=dev)
+    out = torch.empty((n_seq, nh * hd), dtype=torch.float32, device=dev)
+    ms, kern_ms, _ = time_steps(lambda i: attn_decode_batch(q, batch, lens, nh, out=out, workspace=ws,
+                                                            lens_dev=lens_dev), steps, warmup)
+    nbytes = float(lens.sum()) * kvd * 2 * 2 + 2.0 * n_seq * nh * hd * 4
+    achieved = nbytes / (kern_ms * 1e-3)
+    return {
+        "value": nbytes / (ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms,
+        "tokens_per_s": n_seq / (ms * 1e-3),
+        "config": {"workload": f"batched decode, {n_seq} sequences, lengths U[1024,32768] (sum {int(lens.sum())}), "
+                               f"{nh} query / {nkv} KV heads, head_dim {hd}, f16 KV",
+                   "n_seq": n_seq, "sum_len": int(lens.sum()), "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd},
+        "roofline": {"bound": "hbm", "kernel": "decode_split_kernel<%d> + decode_merge_kernel<%d>" % (hd, hd),
+                     "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK, "bytes_per_launch": nbytes, "launch_ms": kern_ms,
+                     "traffic": traffic_of("decode_batch")},
+    }
+
+
+# ---------------------------------------------------------------- CPU leg
+
+def _oracle():
+    sys.path.insert(0, str(ROOT / "oracle"))
+    from oracle_lib import Oracle
+
+    return Oracle()
+
+
+def _host_desc(O) -> tuple[int, str]:
+    cores = int(O.L.yo_threads())
+    model = "unknown CPU"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return cores, model
+
+
+def cpu_prefill(q, k, v, out, L, nh, nkv, hd):
+    """Full workload on the CPU oracle (OpenMP over heads, as the reference)."""
+    from oracle_lib import rel_l2
+
+    O = _oracle()
+    qn = q.float().cpu().numpy()
+    kc = O.f32_to_f16(k.float().cpu().numpy())
+    vc = O.f32_to_f16(v.float().cpu().numpy())
+    t0 = time.perf_counter()
+    want = O.prefill(qn, kc, vc, 0, L, nh, nkv, hd)
+    dt = time.perf_counter() - t0
+    cores, model = _host_desc(O)
+    return {"value": prefill_flops(L, nh, hd) / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"the whole workload ({L} tokens, all heads), one pass, {dt:.2f} s; effective "
+                      f"parallelism <= {nh} heads; {model}",
+            "seconds": dt, "parity_rel_l2": rel_l2(out.cpu().numpy(), want)}
+
+
+def cpu_decode(q, cache, out, L, nh, nkv, hd):
+    from oracle_lib import rel_l2
+
+    from yllm_amd.attention import kv_to_engine
+
+    O = _oracle()
+    ek, ev = kv_to_engine(cache, L)
+    kc = ek.view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+    vc = ev.view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+    qn = q.cpu().numpy()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        want = O.decode(qn, kc, vc, L - 1, nh, nkv, hd)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt > 3.0 or reps >= 20:
+            break
+    cores, model = _host_desc(O)
+    per = dt / reps
+    return {"value": decode_bytes(L, nkv, nh, hd) / per / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{reps} decode step(s) of the same workload, {per:.3f} s each; {model}",
+            "seconds": dt, "parity_rel_l2": rel_l2(out.cpu().numpy(), want)}
+
+
+# -------------------------------------------------------------- traffic
+
+def traffic_of(label: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    p = ROOT / "profiles" / "traffic.json"
+    try:
+        data = json.loads(p.read_text())
+        return data.get(label)
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="prefill2k",
+                    choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k secondary line")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}): the attention "
+              "path is built and measured per GPU; multi-GPU sharding is a design note, not a run.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    from yllm_amd import lib
+
+    lib()  # fails loudly when the HIP library is missing
+    cpu = not args.no_cpu
+    w = args.workload
+    if w == "prefill2k":
+        res = run_prefill(2048, 28, 4, 128, 2, args.steps, args.warmup, cpu)
+    elif w == "prefill8k":
+        res = run_prefill(8192, 32, 8, 128, 4, args.steps, args.warmup, cpu)
+    elif w == "decode32k":
+        res = run_decode(32768, 32, 8, 128, 4, 6, args.steps, args.warmup, cpu, "decode32k")
+    elif w == "decode128k":
+        res = run_decode(131072, 32, 8, 128, 4, 2, args.steps, args.warmup, cpu, "decode128k")
+    else:
+        res = run_decode_batch(32, 8, 128, 64, args.steps, args.warmup)
+
+    line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f16 MFMA, f32 accumulate/softmax", "data": "synthetic",
+            "config": res["config"], "tokens_per_s": res["tokens_per_s"], "roofline": res["roofline"]}
+    if "cpu_baseline" in res:
+        line["cpu_baseline"] = res["cpu_baseline"]
+    if w == "prefill2k" and not args.no_secondary:
+        sec = run_decode(32768, 32, 8, 128, 4, 6, 200, 20, cpu, "decode32k")
+        line["secondary"] = [{"metric": "attn decode GB/s", **{k: sec[k] for k in sec}}]
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,152 @@
+/* yllm_hip.h -- C ABI of the MI355X (gfx950) attention backend for yllm.
+ *
+ * Kernel-level entry points that an engine device layer calls per layer.
+ * They replace the attention part of the reference's CUDA kernel ABI
+ * (inference/cuda/cuda_kernels.h:50-63: cuda_k_store_kv, cuda_k_store_kv_batch,
+ * cuda_k_attn_decode, cuda_k_attn_prefill) and the CPU loops it mirrors
+ * (inference/core/engine.c:1068-1096, 518-563, 928-960; matvec.c:942-1004).
+ *
+ * Conventions (all entry points):
+ *   - extern "C", plain pointers and sizes, fixed-width integers;
+ *   - every pointer argument is DEVICE memory unless its comment says host;
+ *   - `stream` is a hipStream_t (NULL = the default stream); work is queued
+ *     asynchronously on it and nothing synchronises;
+ *   - return 0 on success, a negative YHIP_E* code otherwise, with a message
+ *     available from yhip_last_error() (per host thread).  Unlike the
+ *     reference (void, silent no-op for head_dim > 256), bad shapes are
+ *     reported, never ignored.
+ *
+ * KV cache layout in HBM (per sequence, per layer), designed for coalesced
+ * per-head streaming and for the MFMA operand shapes of the kernels:
+ *   K : u16 f16 bits [n_kv_heads][kv_stride][head_dim]   (row = position)
+ *   V : u16 f16 bits [n_kv_heads][head_dim][kv_stride]   (transposed: column
+ *                                                         = position)
+ * kv_stride is the position capacity, a multiple of 64 (>= the engine's
+ * max_seq).  The reference's engine layout ([max_seq][n_kv*head_dim] per
+ * layer, yllm.h:109 / engine.c:261) converts with yhip_kv_from_engine /
+ * yhip_kv_to_engine.  Values are stored with the reference CPU rounding
+ * (platform.c:340-379: ties away from zero, f32 subnormals to zero), not RNE.
+ *
+ * Grouped-query mapping is the reference's: query head h reads kv head
+ * h*n_kv_heads/n_heads (engine.c:537,940,1079).  head_dim is 64, 128 or 256.
+ */
+#ifndef YLLM_HIP_H
+#define YLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types: the LLF codes DT_F16 / DT_F32 / DT_BF16 (llf.h:15-17) */
+#define YHIP_F16 0u
+#define YHIP_F32 1u
+#define YHIP_BF16 2u
+
+#define YHIP_OK 0
+#define YHIP_EINVAL (-22)   /* bad shape, stride, dtype or null pointer */
+#define YHIP_ENOSPC (-28)   /* workspace too small */
+#define YHIP_EDEVICE (-5)   /* HIP runtime error (launch, copy, device) */
+
+/* Message for the last non-zero return on this host thread ("" if none). */
+const char* yhip_last_error(void);
+
+/* Library version string and the gfx target it was built for. */
+const char* yhip_version(void);
+
+/* Elements (u16) of one layer's K (or V) cache for one sequence. */
+uint64_t yhip_kv_layer_elems(uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride);
+
+/* ---- KV store ------------------------------------------------------------
+ * Replaces cuda_k_store_kv / cuda_k_store_kv_batch (cuda_kernels.h:50-53),
+ * semantics of engine.c:1068-1072 / 518-529 / 928-934: rows pos_start ..
+ * pos_start+B-1 of K and V, from k, v [B][n_kv_heads*head_dim] of element
+ * type src_dtype (YHIP_F32 as the engine, or YHIP_F16 / YHIP_BF16).  The
+ * rows must fit: pos_start + B <= kv_stride. */
+int yhip_kv_store(uint16_t* kcache, uint16_t* vcache, const void* k, const void* v,
+                  uint32_t src_dtype, uint32_t pos_start, uint32_t B, uint32_t n_kv_heads,
+                  uint32_t head_dim, uint32_t kv_stride, void* stream);
+
+/* Engine layout <-> head-major layout for n_rows positions of one layer
+ * (session save / restore, cache.c:174-247; host-written KV,
+ * device_cuda.c:534-549).  eng_k/eng_v: [n_rows][n_kv_heads*head_dim]. */
+int yhip_kv_from_engine(uint16_t* kcache, uint16_t* vcache, const uint16_t* eng_k,
+                        const uint16_t* eng_v, uint32_t n_rows, uint32_t n_kv_heads,
+                        uint32_t head_dim, uint32_t kv_stride, void* stream);
+int yhip_kv_to_engine(uint16_t* eng_k, uint16_t* eng_v, const uint16_t* kcache,
+                      const uint16_t* vcache, uint32_t n_rows, uint32_t n_kv_heads,
+                      uint32_t head_dim, uint32_t kv_stride, void* stream);
+
+/* ---- Decode (split-K flash decoding) -------------------------------------
+ * Replaces cuda_k_attn_decode (cuda_kernels.h:55-58); semantics of
+ * engine.c:1074-1096: one query token per head at position pos attends to
+ * keys 0..pos.  q, att_out: [n_heads*head_dim] fp32.  gate: NULL, or
+ * [n_heads*head_dim] fp32 and att_out is multiplied by sigmoid(gate) (the
+ * qwen35 gated attention, engine.c:959-960).  Needs
+ * yhip_attn_decode_workspace(1, pos+1, pos+1, ...) bytes of workspace. */
+int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
+                     const uint16_t* vcache, uint32_t pos, uint32_t n_heads,
+                     uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
+                     const float* gate, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Ragged batch of independent sequences (one query token each).  No
+ * reference counterpart beyond calling the decode once per engine; it is the
+ * multi-sequence form of the same computation.
+ *   kcaches/vcaches: device arrays [n_seq] of device pointers, each one
+ *                    sequence's layer cache in the layout above;
+ *   lens:            device [n_seq], keys per sequence (>= 1);
+ *   max_len, total_len: host values, the maximum and the sum of lens (they
+ *                    size the split; max_len must bound every lens[i]);
+ *   q/att_out rows:  q_stride / out_stride floats apart per sequence;
+ *   gate:            NULL or rows gate_stride floats apart. */
+int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
+                           uint32_t q_stride, const uint16_t* const* kcaches,
+                           const uint16_t* const* vcaches, const uint32_t* lens,
+                           uint32_t n_seq, uint32_t max_len, uint64_t total_len,
+                           uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                           uint32_t kv_stride, const float* gate, uint32_t gate_stride,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes the two decode entry points need for these shapes. */
+size_t yhip_attn_decode_workspace(uint32_t n_seq, uint32_t max_len, uint64_t total_len,
+                                  uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
+
+/* ---- Prefill (causal GQA, MFMA) ------------------------------------------
+ * Replaces cuda_k_attn_prefill (cuda_kernels.h:59-63); semantics of
+ * engine.c:532-563 (and 935-960 with gate): B query tokens at positions
+ * pos_start+b, b < B, each attending causally to keys 0..pos_start+b, all of
+ * which must already be stored.  q rows are q_stride elements of q_dtype
+ * apart (head h at h*head_dim), out rows out_stride elements of out_dtype;
+ * dtypes YHIP_F32 / YHIP_F16 / YHIP_BF16.  gate: NULL or fp32 rows
+ * gate_stride apart.  Computes QK^T and PV on f16 MFMA with fp32
+ * accumulation and an fp32 online softmax. */
+int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, const void* q,
+                      uint32_t q_dtype, uint32_t q_stride, const uint16_t* kcache,
+                      const uint16_t* vcache, uint32_t pos_start, uint32_t B, uint32_t n_heads,
+                      uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
+                      const float* gate, uint32_t gate_stride, void* stream);
+
+/* ---- Synthetic inputs (host) ----------------------------------------------
+ * Seeded generator shared by the tests and the benchmark so that the CPU
+ * oracle and the GPU see identical bits: splitmix64 as the reference's yrng
+ * (platform.c:405-417), uniforms u = ((r>>40)+0.5)*2^-24, Box-Muller in
+ * double, value = (float)(sigma*z).  Draw i of a stream uses generator state
+ * seed + (i+1)*0x9e3779b97f4a7c15, so chunks can be generated independently. */
+void yhip_synth_normal(uint64_t seed, uint64_t first, float sigma, float* out, uint64_t n);
+/* Round in place to f16-representable values with the reference rounding
+ * (platform.c:340-379), or to bf16 with round-to-nearest-even. */
+void yhip_synth_round_f16(float* x, uint64_t n);
+void yhip_synth_round_bf16(float* x, uint64_t n);
+/* Host conversions used to prepare inputs: reference f32->f16 rounding,
+ * exact f16->f32, f32->bf16 RNE bits. */
+void yhip_host_f32_to_f16(const float* src, uint16_t* dst, uint64_t n);
+void yhip_host_f16_to_f32(const uint16_t* src, float* dst, uint64_t n);
+void yhip_host_f32_to_bf16(const float* src, uint16_t* dst, uint64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YLLM_HIP_H */

@@ -1,0 +1,213 @@
+/* attn_ref.c -- CPU oracle for the attention hot path (TEST INFRASTRUCTURE).
+ *
+ * Restates, in the reference's arithmetic order, the CPU loops of
+ * evilbinary/yllm that the HIP kernels replace.  Used only by tests/ as the
+ * checker and by bench.py as the timed CPU baseline.  See yref.h for the
+ * pinning of each function.
+ */
+#include "yref.h"
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+int yo_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* matvec.c:1023-1031: max, exp(x - max) with a running sum, divide */
+void yo_softmax(float* v, uint32_t n)
+{
+    float mx = v[0];
+    float sum = 0.0f;
+    uint32_t i;
+    for (i = 1; i < n; i++)
+        if (v[i] > mx) mx = v[i];
+    for (i = 0; i < n; i++) {
+        v[i] = expf(v[i] - mx);
+        sum += v[i];
+    }
+    for (i = 0; i < n; i++) v[i] /= sum;
+}
+
+/* matvec.c:942-949: x / max(||x||, eps) */
+void yo_l2norm(float* v, uint32_t n, float eps)
+{
+    float ss = 0.0f;
+    uint32_t i;
+    for (i = 0; i < n; i++) ss += v[i] * v[i];
+    float r = 1.0f / fmaxf(sqrtf(ss), eps);
+    for (i = 0; i < n; i++) v[i] *= r;
+}
+
+/* engine.c:1068-1072 / 518-529 / 928-934 */
+void yo_kv_store(uint16_t* kcache, uint16_t* vcache, const float* k, const float* v,
+                 uint32_t pos_start, uint32_t B, uint32_t kv_dim)
+{
+    uint32_t b, j;
+    for (b = 0; b < B; b++) {
+        uint16_t* kr = kcache + (size_t)(pos_start + b) * kv_dim;
+        uint16_t* vr = vcache + (size_t)(pos_start + b) * kv_dim;
+        const float* ks = k + (size_t)b * kv_dim;
+        const float* vs = v + (size_t)b * kv_dim;
+        for (j = 0; j < kv_dim; j++) {
+            kr[j] = yo_f32_to_f16(ks[j]);
+            vr[j] = yo_f32_to_f16(vs[j]);
+        }
+    }
+}
+
+/* One query head against keys 0..n_keys-1 of one kv head, in the order of
+ * engine.c:1082-1095: scores acc=0, += q*k in dimension order, times
+ * 1/sqrtf(d); softmax over the n_keys scores; out = sum_s a_s * v_s in key
+ * order, dimension by dimension.  kh/vh point at the head's first element of
+ * row 0; rows are row_stride u16 apart.  att: n_keys floats of scratch. */
+static void attend_one_head(float* out, const float* qh, const uint16_t* kh, const uint16_t* vh,
+                            size_t row_stride, uint32_t n_keys, uint32_t hd, float inv_d, float* att)
+{
+    uint32_t s, j;
+    for (s = 0; s < n_keys; s++) {
+        const uint16_t* kr = kh + (size_t)s * row_stride;
+        float acc = 0.0f;
+        for (j = 0; j < hd; j++) acc += qh[j] * yo_f16_to_f32(kr[j]);
+        att[s] = acc * inv_d;
+    }
+    yo_softmax(att, n_keys);
+    memset(out, 0, (size_t)hd * sizeof(float));
+    for (s = 0; s < n_keys; s++) {
+        const uint16_t* vr = vh + (size_t)s * row_stride;
+        float a = att[s];
+        for (j = 0; j < hd; j++) out[j] += a * yo_f16_to_f32(vr[j]);
+    }
+}
+
+/* engine.c:1074-1096 */
+void yo_attn_decode(float* out, const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                    uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim)
+{
+    size_t kv_dim = (size_t)n_kv_heads * head_dim;
+    uint32_t n_keys = pos + 1;
+    float inv_d = 1.0f / sqrtf((float)head_dim);
+    float* att = (float*)malloc((size_t)n_heads * n_keys * sizeof(float));
+    int hh;
+    if (!att) return;
+#pragma omp parallel for schedule(static)
+    for (hh = 0; hh < (int)n_heads; hh++) {
+        uint32_t kvh = (uint32_t)hh * n_kv_heads / n_heads;      /* engine.c:1079 */
+        attend_one_head(out + (size_t)hh * head_dim, q + (size_t)hh * head_dim,
+                        kcache + (size_t)kvh * head_dim, vcache + (size_t)kvh * head_dim,
+                        kv_dim, n_keys, head_dim, inv_d, att + (size_t)hh * n_keys);
+    }
+    free(att);
+}
+
+/* engine.c:532-563 */
+void yo_attn_prefill(float* out, const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                     uint32_t pos_start, uint32_t B, uint32_t n_heads, uint32_t n_kv_heads,
+                     uint32_t head_dim, uint32_t q_stride)
+{
+    size_t kv_dim = (size_t)n_kv_heads * head_dim;
+    uint32_t max_keys = pos_start + B;
+    float inv_d = 1.0f / sqrtf((float)head_dim);
+    float* att = (float*)malloc((size_t)n_heads * max_keys * sizeof(float));
+    int hh;
+    if (!att) return;
+#pragma omp parallel for schedule(static)
+    for (hh = 0; hh < (int)n_heads; hh++) {
+        uint32_t kvh = (uint32_t)hh * n_kv_heads / n_heads;      /* engine.c:537 */
+        uint32_t bb;
+        for (bb = 0; bb < B; bb++) {
+            attend_one_head(out + (size_t)bb * q_stride + (size_t)hh * head_dim,
+                            q + (size_t)bb * q_stride + (size_t)hh * head_dim,
+                            kcache + (size_t)kvh * head_dim, vcache + (size_t)kvh * head_dim,
+                            kv_dim, pos_start + bb + 1, head_dim, inv_d,
+                            att + (size_t)hh * max_keys);
+        }
+    }
+    free(att);
+}
+
+/* engine.c:959-960 */
+void yo_gate_sigmoid(float* x, const float* gate, uint32_t n)
+{
+    uint32_t i;
+    for (i = 0; i < n; i++) x[i] *= 1.0f / (1.0f + expf(-gate[i]));
+}
+
+/* engine.c:788-793 */
+void yo_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt,
+                  const float* a, uint32_t n_vheads)
+{
+    uint32_t h;
+    for (h = 0; h < n_vheads; h++) {
+        beta[h] = 1.0f / (1.0f + expf(-beta[h]));
+        float z = alpha[h] + dt[h];
+        float softplus = log1pf(expf(z));
+        gate[h] = softplus * a[h];
+    }
+}
+
+/* matvec.c:975-1004.  Column j of head h (length hk, contiguous) is decayed
+ * by g = expf(gate[h]) while its dot with k accumulates; delta_j =
+ * (v_j - dot) * beta; the column gains k * delta_j; after all columns are
+ * updated, o_j = (column_j . q) * (1/sqrtf(hv)). */
+void yo_gdn_state_update(float* S, float* out, const float* q, const float* k, const float* v,
+                         const float* gate, const float* beta, uint32_t num_k_heads, uint32_t hk,
+                         uint32_t n_vheads, uint32_t hv)
+{
+    const float scale = 1.0f / sqrtf((float)hv);
+    uint32_t h, j, i;
+    for (h = 0; h < n_vheads; h++) {
+        uint32_t kh = h % num_k_heads;                           /* matvec.c:983 */
+        const float* qh = q + (size_t)kh * hk;
+        const float* kv = k + (size_t)kh * hk;
+        const float* vh = v + (size_t)h * hv;
+        float* Sh = S + (size_t)h * hk * hv;
+        float* oh = out + (size_t)h * hv;
+        float g = expf(gate[h]);
+        float bt = beta[h];
+        for (j = 0; j < hv; j++) {
+            float* col = Sh + (size_t)j * hv;
+            float dot = 0.0f;
+            float delta;
+            for (i = 0; i < hk; i++) {
+                col[i] *= g;
+                dot += col[i] * kv[i];
+            }
+            delta = (vh[j] - dot) * bt;
+            for (i = 0; i < hk; i++) col[i] += kv[i] * delta;
+        }
+        for (j = 0; j < hv; j++) {
+            const float* col = Sh + (size_t)j * hv;
+            float dot = 0.0f;
+            for (i = 0; i < hk; i++) dot += col[i] * qh[i];
+            oh[j] = dot * scale;
+        }
+    }
+}
+
+/* engine.c:826-831 per token, T tokens in order */
+void yo_gdn_sequence(float* S, float* out, float* q, float* k, const float* v,
+                     const float* gate, const float* beta, uint32_t T, uint32_t num_k_heads,
+                     uint32_t hk, uint32_t n_vheads, uint32_t hv, float eps)
+{
+    uint32_t t, i;
+    size_t qk_dim = (size_t)num_k_heads * hk;
+    size_t v_dim = (size_t)n_vheads * hv;
+    for (t = 0; t < T; t++) {
+        float* qt = q + t * qk_dim;
+        float* kt = k + t * qk_dim;
+        for (i = 0; i < num_k_heads; i++) yo_l2norm(qt + (size_t)i * hk, hk, eps);
+        for (i = 0; i < num_k_heads; i++) yo_l2norm(kt + (size_t)i * hk, hk, eps);
+        yo_gdn_state_update(S, out + t * v_dim, qt, kt, v + t * v_dim,
+                            gate + (size_t)t * n_vheads, beta + (size_t)t * n_vheads,
+                            num_k_heads, hk, n_vheads, hv);
+    }
+}

@@ -1,0 +1,236 @@
+"""ctypes wrappers for the CPU oracle (oracle/liboracle.so) and for the
+reference built from its own sources (oracle/_ref/libyref.so).
+
+TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and the
+CPU-baseline leg of bench.py, always as the checker / the timed CPU path,
+never as part of the product."""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_float, c_int, c_uint16, c_uint32, c_uint64
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_SO = ROOT / "oracle" / "liboracle.so"
+REF_SO = ROOT / "oracle" / "_ref" / "libyref.so"
+
+FP = POINTER(c_float)
+HP = POINTER(c_uint16)
+
+
+def fp(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(FP)
+
+
+def hp(a: np.ndarray):
+    assert a.dtype == np.uint16 and a.flags.c_contiguous
+    return a.ctypes.data_as(HP)
+
+
+class Oracle:
+    def __init__(self, path: Path = ORACLE_SO):
+        if not path.exists():
+            raise FileNotFoundError(f"{path} not built (make -C oracle)")
+        L = ctypes.CDLL(str(path))
+        L.yo_threads.restype = c_int
+        L.yo_threads.argtypes = []
+        L.yo_f16_to_f32.restype = c_float
+        L.yo_f16_to_f32.argtypes = [c_uint16]
+        L.yo_f32_to_f16.restype = c_uint16
+        L.yo_f32_to_f16.argtypes = [c_float]
+        L.yo_bf16_to_f16.restype = c_uint16
+        L.yo_bf16_to_f16.argtypes = [c_uint16]
+        L.yo_f32_to_f16_buf.argtypes = [FP, HP, ctypes.c_size_t]
+        L.yo_softmax.argtypes = [FP, c_uint32]
+        L.yo_l2norm.argtypes = [FP, c_uint32, c_float]
+        L.yo_kv_store.argtypes = [HP, HP, FP, FP, c_uint32, c_uint32, c_uint32]
+        L.yo_attn_decode.argtypes = [FP, FP, HP, HP, c_uint32, c_uint32, c_uint32, c_uint32]
+        L.yo_attn_prefill.argtypes = [FP, FP, HP, HP, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
+                                      c_uint32]
+        L.yo_gate_sigmoid.argtypes = [FP, FP, c_uint32]
+        L.yo_gdn_gates.argtypes = [FP, FP, FP, FP, FP, c_uint32]
+        L.yo_gdn_state_update.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32]
+        L.yo_gdn_sequence.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32,
+                                      c_uint32, c_float]
+        self.L = L
+
+    # conversions
+    def f32_to_f16(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, dtype=np.uint16)
+        self.L.yo_f32_to_f16_buf(fp(x), hp(out), x.size)
+        return out
+
+    def f16_to_f32(self, h: np.ndarray) -> np.ndarray:
+        return np.array([self.L.yo_f16_to_f32(int(v)) for v in np.ravel(h)], dtype=np.float32).reshape(h.shape)
+
+    def softmax(self, v: np.ndarray) -> np.ndarray:
+        v = np.array(v, dtype=np.float32)
+        self.L.yo_softmax(fp(v), v.size)
+        return v
+
+    def kv_store(self, kc, vc, k, v, pos_start, kv_dim):
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        self.L.yo_kv_store(hp(kc), hp(vc), fp(k), fp(v), pos_start, k.size // kv_dim, kv_dim)
+
+    def decode(self, q, kc, vc, pos, n_heads, n_kv, hd) -> np.ndarray:
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        out = np.empty(n_heads * hd, dtype=np.float32)
+        self.L.yo_attn_decode(fp(out), fp(q), hp(kc), hp(vc), pos, n_heads, n_kv, hd)
+        return out
+
+    def prefill(self, q, kc, vc, pos_start, B, n_heads, n_kv, hd) -> np.ndarray:
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        out = np.empty((B, n_heads * hd), dtype=np.float32)
+        self.L.yo_attn_prefill(fp(out), fp(q), hp(kc), hp(vc), pos_start, B, n_heads, n_kv, hd, n_heads * hd)
+        return out
+
+    def gate_sigmoid(self, x, gate) -> np.ndarray:
+        x = np.array(x, dtype=np.float32)
+        gate = np.ascontiguousarray(gate, dtype=np.float32)
+        self.L.yo_gate_sigmoid(fp(x), fp(gate), x.size)
+        return x
+
+    def gdn_gates(self, alpha_raw, beta_raw, dt, a):
+        beta = np.array(beta_raw, dtype=np.float32)
+        gate = np.empty_like(beta)
+        self.L.yo_gdn_gates(fp(beta), fp(gate), fp(np.ascontiguousarray(alpha_raw, dtype=np.float32)),
+                            fp(np.ascontiguousarray(dt, dtype=np.float32)),
+                            fp(np.ascontiguousarray(a, dtype=np.float32)), beta.size)
+        return beta, gate
+
+    def gdn_step(self, S, q, k, v, gate, beta, n_k, hk, n_v, hv):
+        S = np.array(S, dtype=np.float32)
+        out = np.empty(n_v * hv, dtype=np.float32)
+        self.L.yo_gdn_state_update(fp(S), fp(out), fp(np.ascontiguousarray(q, np.float32)),
+                                   fp(np.ascontiguousarray(k, np.float32)), fp(np.ascontiguousarray(v, np.float32)),
+                                   fp(np.ascontiguousarray(gate, np.float32)),
+                                   fp(np.ascontiguousarray(beta, np.float32)), n_k, hk, n_v, hv)
+        return S, out
+
+    def gdn_sequence(self, S, q, k, v, gate, beta, T, n_k, hk, n_v, hv, eps):
+        S = np.array(S, dtype=np.float32)
+        q = np.array(q, dtype=np.float32)
+        k = np.array(k, dtype=np.float32)
+        out = np.empty((T, n_v * hv), dtype=np.float32)
+        self.L.yo_gdn_sequence(fp(S), fp(out), fp(q), fp(k), fp(np.ascontiguousarray(v, np.float32)),
+                               fp(np.ascontiguousarray(gate, np.float32)),
+                               fp(np.ascontiguousarray(beta, np.float32)), T, n_k, hk, n_v, hv, eps)
+        return S, out, q, k
+
+
+class Ref:
+    """The reference compiled from its own sources (oracle/_ref)."""
+
+    def __init__(self, path: Path = REF_SO):
+        if not path.exists():
+            raise FileNotFoundError(f"{path} not built (make -C oracle ref)")
+        L = ctypes.CDLL(str(path))
+        L.f16_to_f32.restype = c_float
+        L.f16_to_f32.argtypes = [c_uint16]
+        L.f32_to_f16_buf.argtypes = [FP, HP, ctypes.c_size_t]
+        L.bf16_to_f16.restype = c_uint16
+        L.bf16_to_f16.argtypes = [c_uint16]
+        L.softmax.argtypes = [FP, c_uint32]
+        L.l2norm_inplace.argtypes = [FP, c_uint32, c_float]
+        L.gdn_state_update.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32]
+        L.yrng.restype = c_uint64
+        L.yrng.argtypes = [POINTER(c_uint64)]
+        L.ysrand.restype = c_uint64
+        L.ysrand.argtypes = [c_uint64]
+        L.yr_decode.restype = c_int
+        L.yr_decode.argtypes = [c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, HP, HP, FP, FP, FP, c_float,
+                                FP, HP, HP, FP]
+        L.yr_prefill.restype = c_int
+        L.yr_prefill.argtypes = [c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, HP, HP, FP, FP, FP,
+                                 c_float, FP, HP, HP, FP]
+        L.yr_gated.restype = c_int
+        L.yr_gated.argtypes = [c_uint32, c_uint32, c_uint32, c_uint32, HP, HP, FP, FP, FP, FP, c_float, FP, FP,
+                               HP, HP, FP]
+        L.yr_gdn.restype = c_int
+        L.yr_gdn.argtypes = [c_uint32, c_uint32, c_uint32, FP, FP, FP, FP, FP, c_float, FP, FP, FP, FP, FP, FP,
+                             FP, FP]
+        self.L = L
+
+    def f32_to_f16(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, dtype=np.uint16)
+        self.L.f32_to_f16_buf(fp(x), hp(out), x.size)
+        return out
+
+    def decode(self, arch, n_heads, n_kv, hd, pos, kprev, vprev, wq, wk, wv, xval=1.0):
+        hidden, kvd = n_heads * hd, n_kv * hd
+        q = np.empty(hidden, np.float32)
+        kr = np.empty((pos + 1, kvd), np.uint16)
+        vr = np.empty((pos + 1, kvd), np.uint16)
+        att = np.empty(hidden, np.float32)
+        kp = np.ascontiguousarray(kprev if pos else np.zeros((1, kvd), np.uint16), np.uint16)
+        vp = np.ascontiguousarray(vprev if pos else np.zeros((1, kvd), np.uint16), np.uint16)
+        rc = self.L.yr_decode(arch, n_heads, n_kv, hd, pos, hp(kp), hp(vp), fp(np.float32(wq)), fp(np.float32(wk)),
+                              fp(np.float32(wv)), xval, fp(q), hp(kr), hp(vr), fp(att))
+        assert rc == 0, f"yr_decode rc={rc}"
+        return q, kr, vr, att
+
+    def prefill(self, arch, n_heads, n_kv, hd, pos_start, B, kprev, vprev, wq, wk, wv, xval=1.0):
+        hidden, kvd = n_heads * hd, n_kv * hd
+        q = np.empty((B, hidden), np.float32)
+        kr = np.empty((pos_start + B, kvd), np.uint16)
+        vr = np.empty((pos_start + B, kvd), np.uint16)
+        att = np.empty((B, hidden), np.float32)
+        kp = np.ascontiguousarray(kprev if pos_start else np.zeros((1, kvd), np.uint16), np.uint16)
+        vp = np.ascontiguousarray(vprev if pos_start else np.zeros((1, kvd), np.uint16), np.uint16)
+        rc = self.L.yr_prefill(arch, n_heads, n_kv, hd, pos_start, B, hp(kp), hp(vp),
+                               fp(np.ascontiguousarray(wq, np.float32)), fp(np.ascontiguousarray(wk, np.float32)),
+                               fp(np.ascontiguousarray(wv, np.float32)), xval, fp(q), hp(kr), hp(vr), fp(att))
+        assert rc == 0, f"yr_prefill rc={rc}"
+        return q, kr, vr, att
+
+    def gated(self, n_heads, n_kv, hd, pos, kprev, vprev, wq, wg, wk, wv, xval=1.0):
+        hidden, kvd = n_heads * hd, n_kv * hd
+        q = np.empty(hidden, np.float32)
+        g = np.empty(hidden, np.float32)
+        kr = np.empty((pos + 1, kvd), np.uint16)
+        vr = np.empty((pos + 1, kvd), np.uint16)
+        att = np.empty(hidden, np.float32)
+        kp = np.ascontiguousarray(kprev if pos else np.zeros((1, kvd), np.uint16), np.uint16)
+        vp = np.ascontiguousarray(vprev if pos else np.zeros((1, kvd), np.uint16), np.uint16)
+        rc = self.L.yr_gated(n_heads, n_kv, hd, pos, hp(kp), hp(vp), fp(np.float32(wq)), fp(np.float32(wg)),
+                             fp(np.float32(wk)), fp(np.float32(wv)), xval, fp(q), fp(g), hp(kr), hp(vr), fp(att))
+        assert rc == 0, f"yr_gated rc={rc}"
+        return q, g, kr, vr, att
+
+    def gdn(self, n_k, n_v, hd, wqkv, walpha, wbeta, dt, a, S, xval=1.0):
+        S = np.array(S, dtype=np.float32)
+        q = np.empty(n_k * hd, np.float32)
+        k = np.empty(n_k * hd, np.float32)
+        v = np.empty(n_v * hd, np.float32)
+        ar = np.empty(n_v, np.float32)
+        br = np.empty(n_v, np.float32)
+        beta = np.empty(n_v, np.float32)
+        gate = np.empty(n_v, np.float32)
+        rc = self.L.yr_gdn(n_k, n_v, hd, fp(np.float32(wqkv)), fp(np.float32(walpha)), fp(np.float32(wbeta)),
+                           fp(np.float32(dt)), fp(np.float32(a)), xval, fp(S), fp(q), fp(k), fp(v), fp(ar),
+                           fp(br), fp(beta), fp(gate))
+        assert rc == 0, f"yr_gdn rc={rc}"
+        return dict(S=S, q=q, k=k, v=v, alpha_raw=ar, beta_raw=br, beta=beta, gate=gate)
+
+
+def engine_to_headmajor(kc: np.ndarray, vc: np.ndarray, n_kv: int, hd: int, stride: int):
+    """Engine rows [n, n_kv*hd] (u16) -> (K [n_kv, stride, hd], V^T [n_kv, hd, stride]) zero padded."""
+    n = kc.shape[0]
+    K = np.zeros((n_kv, stride, hd), np.uint16)
+    V = np.zeros((n_kv, hd, stride), np.uint16)
+    K[:, :n, :] = kc.reshape(n, n_kv, hd).transpose(1, 0, 2)
+    V[:, :, :n] = vc.reshape(n, n_kv, hd).transpose(1, 2, 0)
+    return K, V
+
+
+def rel_l2(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.asarray(a, dtype=np.float64).ravel()
+    b = np.asarray(b, dtype=np.float64).ravel()
+    den = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))

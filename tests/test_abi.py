@@ -1,0 +1,120 @@
+"""CPU checks of the C-ABI library: it loads, exports every declared symbol,
+validates arguments before touching the GPU, and its host-side helpers
+(generator, conversions) agree with the oracle and the reference fixtures."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from inputs import splitmix
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_symbols() -> set[str]:
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(yhip_\w+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_symbol(hiplib):
+    from yllm_amd._lib import SIGNATURES
+
+    names = declared_symbols()
+    assert names, "no declarations found"
+    for n in sorted(names):
+        assert hasattr(hiplib, n), f"{n} declared in include/ but not exported"
+    assert names == set(SIGNATURES), "binding table and header disagree"
+
+
+def test_version(hiplib):
+    assert b"gfx950" in hiplib.yhip_version()
+
+
+def _err(hiplib):
+    return hiplib.yhip_last_error().decode()
+
+
+P = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("hd,nh,nkv,stride,msg", [
+    (96, 8, 2, 128, "head_dim"),
+    (128, 8, 0, 128, "n_kv_heads"),
+    (128, 2, 4, 128, "n_kv_heads"),
+    (128, 34, 2, 128, "16 query heads"),
+    (128, 8, 2, 100, "multiple of 64"),
+])
+def test_decode_rejects_bad_shapes(hiplib, hd, nh, nkv, stride, msg):
+    rc = hiplib.yhip_attn_decode(P, P, P, P, 3, nh, nkv, hd, stride, None, None, 0, None)
+    assert rc == -22 and msg in _err(hiplib)
+
+
+def test_decode_rejects_null_and_range(hiplib):
+    assert hiplib.yhip_attn_decode(None, P, P, P, 3, 8, 2, 128, 128, None, None, 0, None) == -22
+    assert hiplib.yhip_attn_decode(P, P, P, P, 128, 8, 2, 128, 128, None, None, 0, None) == -22
+    assert "pos" in _err(hiplib)
+
+
+def test_decode_workspace_is_checked(hiplib):
+    need = hiplib.yhip_attn_decode_workspace(1, 100000, 100000, 32, 8, 128)
+    assert need > 0
+    rc = hiplib.yhip_attn_decode(P, P, P, P, 99999, 32, 8, 128, 131072, None, P, need - 1, None)
+    assert rc == -28 and "workspace" in _err(hiplib)
+    # a short context needs no split and no workspace
+    assert hiplib.yhip_attn_decode_workspace(1, 64, 64, 32, 8, 128) == 0
+
+
+def test_prefill_rejects_bad_args(hiplib):
+    # positions past the cache
+    rc = hiplib.yhip_attn_prefill(P, 1, 1024, P, 1, 1024, P, P, 100, 64, 8, 2, 128, 128, None, 0, None)
+    assert rc == -22 and "exceed" in _err(hiplib)
+    # dtype
+    rc = hiplib.yhip_attn_prefill(P, 7, 1024, P, 1, 1024, P, P, 0, 64, 8, 2, 128, 128, None, 0, None)
+    assert rc == -22 and "dtype" in _err(hiplib)
+    # stride
+    rc = hiplib.yhip_attn_prefill(P, 1, 1000, P, 1, 1024, P, P, 0, 64, 8, 2, 128, 128, None, 0, None)
+    assert rc == -22 and "stride" in _err(hiplib)
+    # empty batch is a no-op
+    assert hiplib.yhip_attn_prefill(P, 1, 1024, P, 1, 1024, P, P, 0, 0, 8, 2, 128, 128, None, 0, None) == 0
+
+
+def test_kv_store_rejects_overflow(hiplib):
+    rc = hiplib.yhip_kv_store(P, P, P, P, 1, 120, 9, 2, 128, 128, None)
+    assert rc == -22 and "exceed" in _err(hiplib)
+    assert hiplib.yhip_kv_store(P, P, P, P, 1, 0, 0, 2, 128, 128, None) == 0
+
+
+def test_host_f16_rounding_matches_reference(hiplib, golden):
+    from yllm_amd.attention import f32_to_f16_bits
+
+    # the same __host__ __device__ routine rounds on the GPU
+    assert np.array_equal(f32_to_f16_bits(golden["conv_f32"]), golden["conv_f32_to_f16"])
+
+
+def test_synth_normal_is_splitmix_box_muller(hiplib, golden):
+    from yllm_amd.attention import synth_normal
+
+    seed = int(golden["yrng_seed"][0])
+    x = synth_normal(seed, 16, 0.5)
+    r = golden["yrng_first16"]  # the reference yrng stream for this seed
+    u = ((r >> np.uint64(40)).astype(np.float64) + 0.5) / 16777216.0
+    rad = np.sqrt(-2.0 * np.log(u[0::2]))
+    z = np.empty(16)
+    z[0::2] = rad * np.cos(2 * np.pi * u[1::2])
+    z[1::2] = rad * np.sin(2 * np.pi * u[1::2])
+    assert np.allclose(x, (0.5 * z).astype(np.float32), rtol=1e-6, atol=1e-7)
+    # chunks are independent of where generation starts
+    full = synth_normal(7, 1000)
+    assert np.array_equal(full[333:777], synth_normal(7, 444, first=333))
+    # the portable fixture generator walks the same stream
+    assert np.array_equal(splitmix(seed, 16), r)
+    # moments
+    big = synth_normal(123, 200000, 0.5)
+    assert abs(big.mean()) < 0.01 and abs(big.std() - 0.5) < 0.01

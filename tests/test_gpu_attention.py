@@ -1,0 +1,253 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle on
+identical seeded inputs.
+
+Bars: KV cache bits are identical (integer work); attention outputs are
+within a relative L2 error of 1e-3 of the oracle (fp32 CPU reference of the
+same loops), the north-star tolerance.  Full-size cases are checked through
+properties that do not need the whole O(L^2) oracle: sampled prefill rows
+against the oracle's decode at the same position (the two are the same
+arithmetic, tests/test_oracle.py::test_prefill_causality)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle_lib import engine_to_headmajor, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # max relative L2 error vs the fp32 CPU oracle
+
+
+def gen(seed, shape, sigma=0.5, f16=True):
+    from yllm_amd.attention import round_f16, synth_normal
+
+    n = int(np.prod(shape))
+    x = synth_normal(seed, n, sigma)
+    if f16:
+        round_f16(x)
+    return x.reshape(shape)
+
+
+def make_cache(cuda, oracle, K, V, n_kv, hd, stride_rows=None, src=torch.float32):
+    """Store rows through the HIP kv_store; return the cache and the oracle's engine-layout bits."""
+    from yllm_amd.attention import LayerKV, kv_store
+
+    L = K.shape[0]
+    cache = LayerKV.empty(n_kv, hd, stride_rows or L, device=cuda)
+    kt = torch.from_numpy(K).to(cuda).to(src)
+    vt = torch.from_numpy(V).to(cuda).to(src)
+    kv_store(cache, kt, vt, 0)
+    kc, vc = oracle.f32_to_f16(K), oracle.f32_to_f16(V)
+    return cache, kc, vc
+
+
+def cache_bits(cache):
+    torch.cuda.synchronize()
+    return cache.k.view(torch.int16).cpu().numpy().view(np.uint16), cache.v.view(torch.int16).cpu().numpy().view(
+        np.uint16)
+
+
+# ------------------------------------------------------------------- KV store
+
+@pytest.mark.parametrize("src", [torch.float32, torch.float16, torch.bfloat16])
+def test_kv_store_bits_match_reference_rounding(cuda, oracle, golden, src):
+    from yllm_amd.attention import LayerKV, kv_store
+
+    n_kv, hd = 2, 64
+    kvd = n_kv * hd
+    vals = np.concatenate([golden["conv_f32"], gen(5, (4096,), 4.0, f16=False)])
+    rows = len(vals) // kvd
+    K = vals[: rows * kvd].reshape(rows, kvd).astype(np.float32)
+    V = -K[::-1].copy()
+    kt = torch.from_numpy(K).to(cuda).to(src)
+    vt = torch.from_numpy(V).to(cuda).to(src)
+    # what the engine would store: the reference rounding of the (already src-typed) values
+    Kx, Vx = kt.float().cpu().numpy(), vt.float().cpu().numpy()
+    cache = LayerKV.empty(n_kv, hd, rows + 5, device=cuda)
+    kv_store(cache, kt[:17], vt[:17], 0)
+    kv_store(cache, kt[17:], vt[17:], 17)  # second call continues at pos_start
+    Kb, Vb = cache_bits(cache)
+    Kw, Vw = engine_to_headmajor(oracle.f32_to_f16(Kx), oracle.f32_to_f16(Vx), n_kv, hd, cache.kv_stride)
+    nan = np.isnan(Kx).any(axis=1)
+    assert np.array_equal(Kb[:, : rows][:, ~nan], Kw[:, : rows][:, ~nan])
+    assert np.array_equal(Vb[:, :, : rows][:, :, ~nan[::-1]], Vw[:, :, : rows][:, :, ~nan[::-1]])
+
+
+def test_kv_engine_layout_round_trip(cuda, oracle):
+    from yllm_amd.attention import LayerKV, kv_from_engine, kv_to_engine
+
+    n_kv, hd, n = 4, 128, 300
+    eng = oracle.f32_to_f16(gen(7, (2, n, n_kv * hd), f16=False))
+    ek = torch.from_numpy(eng[0].view(np.int16)).to(cuda)
+    ev = torch.from_numpy(eng[1].view(np.int16)).to(cuda)
+    cache = LayerKV.empty(n_kv, hd, n, device=cuda)
+    kv_from_engine(cache, ek, ev)
+    Kb, Vb = cache_bits(cache)
+    Kw, Vw = engine_to_headmajor(eng[0], eng[1], n_kv, hd, cache.kv_stride)
+    assert np.array_equal(Kb, Kw) and np.array_equal(Vb, Vw)
+    bk, bv = kv_to_engine(cache, n)
+    assert np.array_equal(bk.view(torch.int16).cpu().numpy().view(np.uint16), eng[0])
+    assert np.array_equal(bv.view(torch.int16).cpu().numpy().view(np.uint16), eng[1])
+
+
+# --------------------------------------------------------------------- decode
+
+def test_decode_reference_config1_fixture(cuda, oracle, golden):
+    """Config 1 (14q/2kv, d=64, 512 keys) with the query and rows the reference engine produced."""
+    from yllm_amd.attention import LayerKV, attn_decode, kv_from_engine
+    from test_oracle import _decode_case
+
+    (nh, nkv, hd, pos), q, kc, vc = _decode_case(oracle, golden, "dec_cfg1")
+    cache = LayerKV.empty(nkv, hd, pos + 1, device=cuda)
+    kv_from_engine(cache, torch.from_numpy(kc.view(np.int16)).to(cuda), torch.from_numpy(vc.view(np.int16)).to(cuda))
+    out = attn_decode(torch.from_numpy(q).to(cuda), cache, pos, nh).cpu().numpy()
+    err = rel_l2(out, golden["dec_cfg1_att"])
+    print(f"config1 decode rel_l2 vs reference engine = {err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("nh,nkv,hd,L", [
+    (14, 2, 64, 512), (32, 8, 128, 1), (32, 8, 128, 31), (32, 8, 128, 33), (32, 8, 128, 4097),
+    (28, 4, 128, 2048), (6, 4, 64, 300), (16, 2, 256, 777), (8, 8, 128, 20000)])
+def test_decode_parity(cuda, oracle, nh, nkv, hd, L):
+    from yllm_amd.attention import attn_decode
+
+    kvd = nkv * hd
+    K = gen(100 + L, (L, kvd))
+    V = gen(200 + L, (L, kvd))
+    q = gen(300 + L, (nh * hd,), f16=False)
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    want = oracle.decode(q, kc, vc, L - 1, nh, nkv, hd)
+    got = attn_decode(torch.from_numpy(q).to(cuda), cache, L - 1, nh).cpu().numpy()
+    err = rel_l2(got, want)
+    print(f"decode {nh}/{nkv} d={hd} L={L}: rel_l2={err:.3e}")
+    assert err <= TOL
+
+
+def test_decode_gated_parity(cuda, oracle):
+    from yllm_amd.attention import attn_decode
+
+    nh, nkv, hd, L = 16, 2, 256, 1500
+    kvd = nkv * hd
+    K, V = gen(11, (L, kvd)), gen(12, (L, kvd))
+    q = gen(13, (nh * hd,))
+    gate = gen(14, (nh * hd,), 1.0, f16=False)
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd, src=torch.bfloat16)
+    want = oracle.gate_sigmoid(oracle.decode(q, kc, vc, L - 1, nh, nkv, hd), gate)
+    got = attn_decode(torch.from_numpy(q).to(cuda), cache, L - 1, nh, gate=torch.from_numpy(gate).to(cuda))
+    err = rel_l2(got.cpu().numpy(), want)
+    print(f"gated decode rel_l2={err:.3e}")
+    assert err <= TOL
+
+
+def test_decode_batch_ragged_parity(cuda, oracle):
+    from yllm_amd.attention import DecodeBatch, LayerKV, attn_decode_batch, kv_store
+
+    nh, nkv, hd = 32, 8, 128
+    kvd = nkv * hd
+    lens = [1, 95, 1024, 3001, 777, 64, 8191]
+    stride = 8192
+    caches, wants, qs = [], [], []
+    for i, L in enumerate(lens):
+        K, V = gen(400 + i, (L, kvd)), gen(500 + i, (L, kvd))
+        q = gen(600 + i, (nh * hd,), f16=False)
+        c = LayerKV.empty(nkv, hd, stride, device=cuda)
+        kv_store(c, torch.from_numpy(K).to(cuda), torch.from_numpy(V).to(cuda), 0)
+        caches.append(c)
+        qs.append(q)
+        wants.append(oracle.decode(q, oracle.f32_to_f16(K), oracle.f32_to_f16(V), L - 1, nh, nkv, hd))
+    batch = DecodeBatch(caches)
+    got = attn_decode_batch(torch.from_numpy(np.stack(qs)).to(cuda), batch, lens, nh).cpu().numpy()
+    for i, L in enumerate(lens):
+        err = rel_l2(got[i], wants[i])
+        print(f"batch seq {i} L={L}: rel_l2={err:.3e}")
+        assert err <= TOL
+
+
+def test_decode_long_context_full_size(cuda, oracle):
+    """Config 4 decode at its full size: 131072 keys, 32q/8kv, d=128 (split-K + LSE merge)."""
+    from yllm_amd.attention import attn_decode
+
+    nh, nkv, hd, L = 32, 8, 128, 131072
+    kvd = nkv * hd
+    K, V = gen(0x5EED0004, (L, kvd)), gen(0x5EED0104, (L, kvd))
+    q = gen(0x5EED0204, (nh * hd,))
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    Kb, _ = cache_bits(cache)
+    assert np.array_equal(Kb[3, 77777], kc[77777, 3 * hd:4 * hd])
+    want = oracle.decode(q, kc, vc, L - 1, nh, nkv, hd)
+    got = attn_decode(torch.from_numpy(q).to(cuda), cache, L - 1, nh).cpu().numpy()
+    err = rel_l2(got, want)
+    print(f"decode 131072 rel_l2={err:.3e}")
+    assert err <= TOL
+
+
+# -------------------------------------------------------------------- prefill
+
+@pytest.mark.parametrize("nh,nkv,hd,ps,B,qdt,odt", [
+    (28, 4, 128, 0, 300, torch.float16, torch.float32),
+    (28, 4, 128, 100, 77, torch.float32, torch.float32),
+    (14, 2, 64, 0, 129, torch.float32, torch.float16),
+    (32, 8, 128, 5, 64, torch.bfloat16, torch.bfloat16),
+    (6, 4, 64, 0, 1, torch.float32, torch.float32),
+    (16, 2, 256, 30, 200, torch.bfloat16, torch.float32),
+])
+def test_prefill_parity(cuda, oracle, nh, nkv, hd, ps, B, qdt, odt):
+    from yllm_amd.attention import attn_prefill
+
+    kvd = nkv * hd
+    L = ps + B
+    K, V = gen(700 + L, (L, kvd)), gen(800 + L, (L, kvd))
+    q = gen(900 + L, (B, nh * hd))
+    if qdt == torch.bfloat16:
+        from yllm_amd.attention import round_bf16
+
+        q = round_bf16(q.ravel().copy()).reshape(B, nh * hd)
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    want = oracle.prefill(q, kc, vc, ps, B, nh, nkv, hd)
+    qt = torch.from_numpy(q).to(cuda).to(qdt)
+    got = attn_prefill(qt, cache, ps, nh, out_dtype=odt).float().cpu().numpy()
+    err = rel_l2(got, want)
+    print(f"prefill {nh}/{nkv} d={hd} ps={ps} B={B} q={qdt} out={odt}: rel_l2={err:.3e}")
+    assert err <= TOL
+    # every row on its own, so one bad query cannot hide in the average
+    rows = [rel_l2(got[i], want[i]) for i in range(B)]
+    assert max(rows) <= 3 * TOL
+
+
+def test_prefill_gated_parity(cuda, oracle):
+    from yllm_amd.attention import attn_prefill
+
+    nh, nkv, hd, B = 16, 2, 256, 96
+    kvd = nkv * hd
+    K, V = gen(31, (B, kvd)), gen(32, (B, kvd))
+    q = gen(33, (B, nh * hd))
+    gate = gen(34, (B, nh * hd), 1.0, f16=False)
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    want = oracle.gate_sigmoid(oracle.prefill(q, kc, vc, 0, B, nh, nkv, hd).ravel(), gate.ravel())
+    got = attn_prefill(torch.from_numpy(q).to(cuda), cache, 0, nh, gate=torch.from_numpy(gate).to(cuda))
+    err = rel_l2(got.cpu().numpy().ravel(), want)
+    print(f"gated prefill rel_l2={err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("nh,nkv,hd,L", [(28, 4, 128, 2048), (32, 8, 128, 8192)])
+def test_prefill_full_size_sampled_rows(cuda, oracle, nh, nkv, hd, L):
+    """Configs 2 and 4-prefill at full size: sampled rows against the oracle at their position,
+    plus rows compared with the GPU decode kernel at the same position."""
+    from yllm_amd.attention import attn_decode, attn_prefill
+
+    kvd = nkv * hd
+    K, V = gen(0x5EED0002 + L, (L, kvd)), gen(0x5EED0102 + L, (L, kvd))
+    q = gen(0x5EED0202 + L, (L, nh * hd))
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    got = attn_prefill(torch.from_numpy(q).to(cuda).half(), cache, 0, nh).cpu().numpy()
+    assert np.isfinite(got).all()
+    for t in (0, 1, 63, 64, 127, 128, 1000, L // 2 + 17, L - 2, L - 1):
+        want = oracle.decode(q[t], kc[: t + 1], vc[: t + 1], t, nh, nkv, hd)
+        err = rel_l2(got[t], want)
+        dec = attn_decode(torch.from_numpy(q[t]).to(cuda), cache, t, nh).cpu().numpy()
+        assert err <= TOL, f"row {t}: rel_l2={err:.3e}"
+        assert rel_l2(got[t], dec) <= TOL

@@ -1,0 +1,324 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+
+Each oracle function is compared bit for bit with (a) golden vectors that the
+reference's own compiled code produced (tests/golden/make_golden.py), (b) the
+reference built from its sources, live, when oracle/_ref is present, and
+(c) closed forms / textbook routines that a plausible slip (wrong GQA index,
+missing scale, transposed state, wrong rounding direction) would fail.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from inputs import splitmix, uniform_pm1
+from oracle_lib import rel_l2
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def prev_rows(oracle, seed, n, kvd):
+    return oracle.f32_to_f16(uniform_pm1(seed, max(n, 1) * kvd).reshape(max(n, 1), kvd))[:n]
+
+
+# ---------------------------------------------------------------- conversions
+
+def test_f32_to_f16_golden(oracle, golden):
+    got = oracle.f32_to_f16(golden["conv_f32"])
+    assert np.array_equal(got, golden["conv_f32_to_f16"])
+
+
+def test_f32_to_f16_rounds_ties_away_from_zero(oracle):
+    # 1 + 2^-11 is exactly half way between 1 and 1+2^-10: RNE gives 0x3c00, the reference 0x3c01
+    assert oracle.f32_to_f16(np.float32([1.0 + 2.0 ** -11]))[0] == 0x3C01
+    assert oracle.f32_to_f16(np.float32([-(1.0 + 2.0 ** -11)]))[0] == 0xBC01
+    # f32 subnormals flush to signed zero, overflow to inf
+    assert list(oracle.f32_to_f16(np.float32([1e-40, -1e-40, 1e6, -1e6]))) == [0x0000, 0x8000, 0x7C00, 0xFC00]
+
+
+def test_f32_to_f16_matches_numpy_off_ties(oracle):
+    # away from exact ties the reference rounding equals IEEE round-to-nearest
+    x = uniform_pm1(5, 20000, 4.0)
+    np_bits = x.astype(np.float16).view(np.uint16)
+    got = oracle.f32_to_f16(x)
+    mant = x.view(np.uint32) & 0x1FFF
+    not_tie = mant != 0x1000
+    assert np.array_equal(got[not_tie], np_bits[not_tie])
+
+
+def test_f16_to_f32_exhaustive(oracle):
+    codes = np.arange(65536, dtype=np.uint16)
+    got = oracle.f16_to_f32(codes)
+    want = codes.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(bits(got)[~nan], bits(want)[~nan])
+    assert np.isnan(got[nan]).all()
+
+
+def test_f16_reference_known_answers(oracle):
+    # tests/test_matvec.c:34-54 of the reference
+    cases = {0x0000: 0.0, 0x3C00: 1.0, 0xBC00: -1.0, 0x0001: 5.960464477539063e-8,
+             0x8001: -5.960464477539063e-8, 0x03F7: 6.049871444702148e-5, 0x83F7: -6.049871444702148e-5,
+             0x0400: 6.103515625e-5}
+    for h, v in cases.items():
+        assert abs(float(oracle.L.yo_f16_to_f32(h)) - v) <= 1e-12
+    assert np.isinf(oracle.L.yo_f16_to_f32(0x7C00)) and oracle.L.yo_f16_to_f32(0xFC00) < 0
+    for h in (0x0000, 0x3C00, 0xBC00, 0x0400, 0x7BFF, 0x03FF, 0x8003, 0x3555, 0xC555, 0x03F7):
+        assert oracle.L.yo_f32_to_f16(oracle.L.yo_f16_to_f32(h)) == h
+
+
+def test_bf16_to_f16_golden(oracle, golden):
+    got = np.array([oracle.L.yo_bf16_to_f16(int(v)) for v in golden["conv_bf16"]], np.uint16)
+    assert np.array_equal(got, golden["conv_bf16_to_f16"])
+
+
+def test_yrng_golden(golden):
+    # the portable splitmix used for fixture inputs reproduces the reference yrng stream
+    assert np.array_equal(splitmix(int(golden["yrng_seed"][0]), 16), golden["yrng_first16"])
+
+
+# ----------------------------------------------------------- softmax / l2norm
+
+def test_softmax_golden(oracle, golden):
+    for i in range(4):
+        got = oracle.softmax(golden[f"softmax{i}_in"])
+        assert np.array_equal(bits(got), bits(golden[f"softmax{i}_out"]))
+
+
+def test_softmax_reference_known_answer(oracle):
+    # tests/test_matvec.c:230-239 of the reference
+    v = oracle.softmax(np.float32([1.0, 2.0, 3.0]))
+    s = np.exp(1.0) + np.exp(2.0) + np.exp(3.0)
+    assert abs(v[0] - np.exp(1.0) / s) < 1e-6 and abs(v[2] - np.exp(3.0) / s) < 1e-6
+    assert abs(v.sum() - 1.0) < 1e-6
+
+
+def test_l2norm_golden(oracle, golden):
+    for i in range(2):
+        v = np.array(golden[f"l2norm{i}_in"], np.float32)
+        oracle.L.yo_l2norm(v.ctypes.data_as(__import__("oracle_lib").FP), v.size, np.float32(1e-6))
+        assert np.array_equal(bits(v), bits(golden[f"l2norm{i}_out"]))
+
+
+# ------------------------------------------------------------------ attention
+
+def _decode_case(oracle, golden, name):
+    arch, nh, nkv, hd, pos = (int(x) for x in golden[f"{name}_meta"])
+    seeds = golden[f"{name}_seeds"]
+    kvd = nkv * hd
+    kc = np.concatenate([prev_rows(oracle, int(seeds[0]), pos, kvd), golden[f"{name}_knew"]])
+    vc = np.concatenate([prev_rows(oracle, int(seeds[1]), pos, kvd), golden[f"{name}_vnew"]])
+    return (nh, nkv, hd, pos), golden[f"{name}_q"], kc, vc
+
+
+@pytest.mark.parametrize("name", ["dec_cfg1", "dec_qwen", "dec_pos0"])
+def test_decode_golden(oracle, golden, name):
+    (nh, nkv, hd, pos), q, kc, vc = _decode_case(oracle, golden, name)
+    out = oracle.decode(q, kc, vc, pos, nh, nkv, hd)
+    assert np.array_equal(bits(out), bits(golden[f"{name}_att"]))
+
+
+@pytest.mark.parametrize("name", ["pre_llama", "pre_qwen", "pre_ragged"])
+def test_prefill_golden(oracle, golden, name):
+    arch, nh, nkv, hd, ps, B = (int(x) for x in golden[f"{name}_meta"])
+    seeds = golden[f"{name}_seeds"]
+    kvd = nkv * hd
+    kc = np.concatenate([prev_rows(oracle, int(seeds[0]), ps, kvd), golden[f"{name}_knew"]])
+    vc = np.concatenate([prev_rows(oracle, int(seeds[1]), ps, kvd), golden[f"{name}_vnew"]])
+    out = oracle.prefill(golden[f"{name}_q"], kc, vc, ps, B, nh, nkv, hd)
+    assert np.array_equal(bits(out), bits(golden[f"{name}_att"]))
+
+
+@pytest.mark.parametrize("name", ["gat_small", "gat_cfg5"])
+def test_gated_golden(oracle, golden, name):
+    nh, nkv, hd, pos = (int(x) for x in golden[f"{name}_meta"])
+    seeds = golden[f"{name}_seeds"]
+    kvd = nkv * hd
+    kc = np.concatenate([prev_rows(oracle, int(seeds[0]), pos, kvd), golden[f"{name}_knew"]])
+    vc = np.concatenate([prev_rows(oracle, int(seeds[1]), pos, kvd), golden[f"{name}_vnew"]])
+    out = oracle.gate_sigmoid(oracle.decode(golden[f"{name}_q"], kc, vc, pos, nh, nkv, hd), golden[f"{name}_gate"])
+    assert np.array_equal(bits(out), bits(golden[f"{name}_att"]))
+
+
+def _attn_f64(q, kc, vc, positions, nh, nkv, hd):
+    """fp64 brute force of softmax(q k^T / sqrt(d)) v with the reference GQA map."""
+    K = kc.view(np.float16).astype(np.float64)
+    V = vc.view(np.float16).astype(np.float64)
+    q = np.asarray(q, np.float64).reshape(len(positions), nh, hd)
+    out = np.zeros_like(q)
+    for t, pos in enumerate(positions):
+        for h in range(nh):
+            kvh = h * nkv // nh
+            k = K[: pos + 1, kvh * hd:(kvh + 1) * hd]
+            v = V[: pos + 1, kvh * hd:(kvh + 1) * hd]
+            s = k @ q[t, h] / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            out[t, h] = p @ v / p.sum()
+    return out.reshape(len(positions), nh * hd)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos", [(4, 2, 64, 9), (6, 3, 64, 30), (8, 1, 128, 70), (3, 3, 64, 5)])
+def test_decode_fp64_brute_force(oracle, nh, nkv, hd, pos):
+    kvd = nkv * hd
+    kc = oracle.f32_to_f16(uniform_pm1(41, (pos + 1) * kvd).reshape(pos + 1, kvd))
+    vc = oracle.f32_to_f16(uniform_pm1(42, (pos + 1) * kvd).reshape(pos + 1, kvd))
+    q = uniform_pm1(43, nh * hd, 1.5)
+    out = oracle.decode(q, kc, vc, pos, nh, nkv, hd)
+    want = _attn_f64(q, kc, vc, [pos], nh, nkv, hd)[0]
+    assert rel_l2(out, want) < 1e-6
+
+
+def test_attention_closed_forms(oracle):
+    nh, nkv, hd = 4, 2, 64
+    kvd = nkv * hd
+    q = uniform_pm1(51, nh * hd, 2.0)
+    v = oracle.f32_to_f16(uniform_pm1(52, 10 * kvd).reshape(10, kvd))
+    k = oracle.f32_to_f16(uniform_pm1(53, 10 * kvd).reshape(10, kvd))
+    V = v.view(np.float16).astype(np.float32)
+    # one key: the output is that V row exactly
+    out = oracle.decode(q, k[:1], v[:1], 0, nh, nkv, hd).reshape(nh, hd)
+    for h in range(nh):
+        kvh = h * nkv // nh
+        assert np.array_equal(out[h], V[0, kvh * hd:(kvh + 1) * hd])
+    # identical keys: uniform weights, the output is the mean of V
+    kk = np.repeat(k[:1], 10, axis=0)
+    out = oracle.decode(q, kk, v, 9, nh, nkv, hd).reshape(nh, hd)
+    for h in range(nh):
+        kvh = h * nkv // nh
+        assert np.allclose(out[h], V[:, kvh * hd:(kvh + 1) * hd].mean(0), rtol=0, atol=1e-6)
+    # heads of one group with the same query give the same output; other groups differ
+    qq = np.tile(q[:hd], nh)
+    out = oracle.decode(qq, k, v, 9, nh, nkv, hd).reshape(nh, hd)
+    assert np.array_equal(out[0], out[1]) and np.array_equal(out[2], out[3])
+    assert not np.array_equal(out[0], out[2])
+
+
+def test_prefill_causality(oracle):
+    nh, nkv, hd, B = 4, 2, 64, 12
+    kvd = nkv * hd
+    q = uniform_pm1(61, B * nh * hd).reshape(B, nh * hd)
+    k = oracle.f32_to_f16(uniform_pm1(62, B * kvd).reshape(B, kvd))
+    v = oracle.f32_to_f16(uniform_pm1(63, B * kvd).reshape(B, kvd))
+    base = oracle.prefill(q, k, v, 0, B, nh, nkv, hd)
+    k2, v2 = k.copy(), v.copy()
+    k2[7:] ^= 0x1234
+    v2[7:] ^= 0x0F0F
+    pert = oracle.prefill(q, k2, v2, 0, B, nh, nkv, hd)
+    assert np.array_equal(bits(base[:7]), bits(pert[:7]))
+    assert not np.array_equal(base[7:], pert[7:])
+    # prefill row t equals decode at position t
+    for t in (0, 5, 11):
+        d = oracle.decode(q[t], k[: t + 1], v[: t + 1], t, nh, nkv, hd)
+        assert np.array_equal(bits(d), bits(base[t]))
+
+
+# ------------------------------------------------------------------------ GDN
+
+@pytest.mark.parametrize("name", ["gdn_2_4", "gdn_4_2", "gdn_3_3"])
+def test_gdn_golden(oracle, golden, name):
+    nk, nv, hd = (int(x) for x in golden[f"{name}_meta"])
+    seeds = golden[f"{name}_seeds"]
+    dt = uniform_pm1(int(seeds[1]), nv, 1.0)
+    a = -np.exp(uniform_pm1(int(seeds[2]), nv, 1.0)).astype(np.float32)
+    beta, gate = oracle.gdn_gates(golden[f"{name}_alpha_raw"], golden[f"{name}_beta_raw"], dt, a)
+    assert np.array_equal(bits(beta), bits(golden[f"{name}_beta"]))
+    assert np.array_equal(bits(gate), bits(golden[f"{name}_gate"]))
+    S0 = uniform_pm1(int(seeds[0]), nv * hd * hd, 0.2)
+    S1, _ = oracle.gdn_step(S0, golden[f"{name}_q"], golden[f"{name}_k"], golden[f"{name}_v"], gate, beta, nk, hd,
+                            nv, hd)
+    assert np.array_equal(bits(S1), bits(golden[f"{name}_S"]))
+
+
+def _gdn_f64(S, q, k, v, g, beta, nk, hk, nv, hv):
+    """fp64 statement of the recurrence in matrix form: S_h (hk x hv)."""
+    S = S.reshape(nv, hv, hk).transpose(0, 2, 1).astype(np.float64)  # [h][i][j] = state col j entry i
+    out = np.zeros((nv, hv))
+    for h in range(nv):
+        kh = h % nk
+        qq, kk = q[kh * hk:(kh + 1) * hk].astype(np.float64), k[kh * hk:(kh + 1) * hk].astype(np.float64)
+        Sh = S[h] * np.exp(np.float64(g[h]))
+        delta = (v[h * hv:(h + 1) * hv] - kk @ Sh) * beta[h]
+        Sh = Sh + np.outer(kk, delta)
+        S[h] = Sh
+        out[h] = (qq @ Sh) / np.sqrt(hv)
+    return S.transpose(0, 2, 1).reshape(-1), out.reshape(-1)
+
+
+def test_gdn_step_fp64_matrix_form(oracle):
+    nk, nv, hd = 2, 4, 32
+    S = uniform_pm1(71, nv * hd * hd, 0.3)
+    q, k = uniform_pm1(72, nk * hd, 0.2), uniform_pm1(73, nk * hd, 0.2)
+    v = uniform_pm1(74, nv * hd)
+    g = -np.abs(uniform_pm1(75, nv))
+    beta = np.abs(uniform_pm1(76, nv))
+    S1, out = oracle.gdn_step(S, q, k, v, g, beta, nk, hd, nv, hd)
+    S_ref, out_ref = _gdn_f64(S, q, k, v, g, beta, nk, hd, nv, hd)
+    assert rel_l2(S1, S_ref) < 1e-6 and rel_l2(out, out_ref) < 1e-5
+
+
+def test_gdn_closed_forms(oracle):
+    hd = 16
+    # beta = 0: pure decay S <- exp(g) S, output (S q)/sqrt(d)
+    S = uniform_pm1(81, hd * hd, 0.5)
+    q, k, v = uniform_pm1(82, hd), uniform_pm1(83, hd), uniform_pm1(84, hd)
+    S1, out = oracle.gdn_step(S, q, k, v, np.float32([-0.5]), np.float32([0.0]), 1, hd, 1, hd)
+    assert np.allclose(S1, S * np.exp(-0.5), rtol=1e-6, atol=0)
+    # g = 1 (log-gate 0), beta = 1, orthonormal keys from a zero state: S k_t returns v_t
+    basis = np.eye(hd, dtype=np.float32)
+    S = np.zeros(hd * hd, np.float32)
+    vs = uniform_pm1(85, 5 * hd).reshape(5, hd)
+    for t in range(5):
+        S, _ = oracle.gdn_step(S, basis[t], basis[t], vs[t], np.float32([0.0]), np.float32([1.0]), 1, hd, 1, hd)
+    for t in range(5):
+        _, o = oracle.gdn_step(S, basis[t], basis[t + 5], np.zeros(hd, np.float32), np.float32([0.0]),
+                               np.float32([0.0]), 1, hd, 1, hd)
+        assert np.allclose(o * np.sqrt(hd), vs[t], atol=1e-6)
+    # d = 1: scalar recursion s <- g s + beta (v - g s k) k
+    s, g, b, kk, vv = 0.3, np.exp(-0.2), 0.7, 0.9, -0.4
+    S1, o = oracle.gdn_step(np.float32([s]), np.float32([1.0]), np.float32([kk]), np.float32([vv]),
+                            np.float32([-0.2]), np.float32([b]), 1, 1, 1, 1)
+    want = g * s + b * (vv - g * s * kk) * kk
+    assert abs(S1[0] - want) < 1e-6 and abs(o[0] - want) < 1e-6
+
+
+# ----------------------------------------------------- live reference (if built)
+
+@pytest.mark.parametrize("arch,nh,nkv,hd,pos", [(0, 8, 4, 64, 33), (1, 12, 3, 128, 77), (0, 7, 7, 64, 1)])
+def test_decode_vs_reference_live(oracle, ref, arch, nh, nkv, hd, pos):
+    kvd, hidden = nkv * hd, nh * hd
+    kp = prev_rows(oracle, 91, pos, kvd)
+    vp = prev_rows(oracle, 92, pos, kvd)
+    sc = 1.0 / np.sqrt(hidden)
+    q, kr, vr, att = ref.decode(arch, nh, nkv, hd, pos, kp, vp, uniform_pm1(93, hidden, 2 * sc),
+                                uniform_pm1(94, kvd, 2 * sc), uniform_pm1(95, kvd, 2 * sc))
+    out = oracle.decode(q, kr, vr, pos, nh, nkv, hd)
+    assert np.array_equal(bits(out), bits(att))
+
+
+def test_prefill_vs_reference_live(oracle, ref):
+    nh, nkv, hd, ps, B = 8, 2, 64, 19, 21
+    kvd, hidden = nkv * hd, nh * hd
+    kp, vp = prev_rows(oracle, 101, ps, kvd), prev_rows(oracle, 102, ps, kvd)
+    sc = 1.0 / np.sqrt(hidden)
+    q, kr, vr, att = ref.prefill(1, nh, nkv, hd, ps, B, kp, vp,
+                                 uniform_pm1(103, B * hidden, 2 * sc).reshape(B, hidden),
+                                 uniform_pm1(104, B * kvd, 2 * sc).reshape(B, kvd),
+                                 uniform_pm1(105, B * kvd, 2 * sc).reshape(B, kvd))
+    # the rows the reference stored are the oracle's rounding of the same values
+    out = oracle.prefill(q, kr, vr, ps, B, nh, nkv, hd)
+    assert np.array_equal(bits(out), bits(att))
+
+
+def test_gdn_vs_reference_live(oracle, ref):
+    nk, nv, hd = 16, 16, 128
+    conv = 2 * nk * hd + nv * hd
+    S = uniform_pm1(111, nv * hd * hd, 0.2)
+    dt, a = uniform_pm1(112, nv), -np.exp(uniform_pm1(113, nv))
+    r = ref.gdn(nk, nv, hd, uniform_pm1(114, conv, 0.1), uniform_pm1(115, nv, 0.1), uniform_pm1(116, nv, 0.1),
+                dt, a.astype(np.float32), S)
+    beta, gate = oracle.gdn_gates(r["alpha_raw"], r["beta_raw"], dt, a.astype(np.float32))
+    assert np.array_equal(bits(beta), bits(r["beta"])) and np.array_equal(bits(gate), bits(r["gate"]))
+    S1, _ = oracle.gdn_step(S, r["q"], r["k"], r["v"], gate, beta, nk, hd, nv, hd)
+    assert np.array_equal(bits(S1), bits(r["S"]))

@@ -1,0 +1,236 @@
+"""Host-side mirror of the reference's per-layer attention operators, on HIP.
+
+Names and argument meaning follow the reference operators that the C ABI
+replaces (inference/cuda/cuda_kernels.h:50-63, inference/core/engine.c):
+
+    kv_store(cache, k, v, pos_start)          engine.c:1068-1072 / 518-529
+    attn_decode(q, cache, pos, n_heads)       engine.c:1074-1096
+    attn_decode_batch(q, caches, lens, ...)   the same per sequence, batched
+    attn_prefill(q, cache, pos_start, ...)    engine.c:532-563
+    gate=...                                  engine.c:959-960 (qwen35)
+
+Tensors are torch tensors on the GPU (torch is used for device memory and
+streams only); every call goes through libyllm_hip.so on the current torch
+stream.  Errors raise YhipError with the library's message; there is no CPU
+fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from ._lib import BF16, F16, F32, YhipError, check, lib
+
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise YhipError(-22, f"unsupported dtype {t.dtype}") from None
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _need_gpu(*ts: torch.Tensor | None) -> None:
+    for t in ts:
+        if t is not None:
+            if not t.is_cuda:
+                raise YhipError(-22, "tensor must be on the GPU")
+            if not t.is_contiguous():
+                raise YhipError(-22, "tensor must be contiguous")
+
+
+def round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+@dataclass
+class LayerKV:
+    """One layer's KV cache of one sequence in HBM.
+
+    k: f16 [n_kv, kv_stride, head_dim] (row = position)
+    v: f16 [n_kv, head_dim, kv_stride] (transposed: column = position)
+    """
+
+    k: torch.Tensor
+    v: torch.Tensor
+
+    @property
+    def n_kv(self) -> int:
+        return self.k.shape[0]
+
+    @property
+    def kv_stride(self) -> int:
+        return self.k.shape[1]
+
+    @property
+    def head_dim(self) -> int:
+        return self.k.shape[2]
+
+    @classmethod
+    def empty(cls, n_kv: int, head_dim: int, max_seq: int, device: str | torch.device = "cuda",
+              zero: bool = True) -> "LayerKV":
+        stride = round_up(max(max_seq, 1), 64)
+        alloc = torch.zeros if zero else torch.empty
+        k = alloc((n_kv, stride, head_dim), dtype=torch.float16, device=device)
+        v = alloc((n_kv, head_dim, stride), dtype=torch.float16, device=device)
+        return cls(k, v)
+
+
+def kv_store(cache: LayerKV, k: torch.Tensor, v: torch.Tensor, pos_start: int) -> None:
+    """Store rows pos_start..pos_start+B-1; k, v: [B, n_kv*head_dim] (f32/f16/bf16)."""
+    _need_gpu(k, v, cache.k, cache.v)
+    if k.dim() == 1:
+        k, v = k.unsqueeze(0), v.unsqueeze(0)
+    if k.shape != v.shape or k.dtype != v.dtype or k.shape[1] != cache.n_kv * cache.head_dim:
+        raise YhipError(-22, f"kv_store: k {tuple(k.shape)} / v {tuple(v.shape)} do not match the cache")
+    check(lib().yhip_kv_store(_ptr(cache.k), _ptr(cache.v), _ptr(k), _ptr(v), _dtype_code(k), pos_start,
+                              k.shape[0], cache.n_kv, cache.head_dim, cache.kv_stride, _stream()))
+
+
+def kv_from_engine(cache: LayerKV, eng_k: torch.Tensor, eng_v: torch.Tensor) -> None:
+    """Fill rows 0..n-1 from engine-layout f16 rows [n, n_kv*head_dim] (yllm.h:109)."""
+    _need_gpu(eng_k, eng_v)
+    check(lib().yhip_kv_from_engine(_ptr(cache.k), _ptr(cache.v), _ptr(eng_k), _ptr(eng_v), eng_k.shape[0],
+                                    cache.n_kv, cache.head_dim, cache.kv_stride, _stream()))
+
+
+def kv_to_engine(cache: LayerKV, n_rows: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rows 0..n_rows-1 in the engine layout, as f16 [n_rows, n_kv*head_dim]."""
+    kd = cache.n_kv * cache.head_dim
+    ek = torch.empty((n_rows, kd), dtype=torch.float16, device=cache.k.device)
+    ev = torch.empty_like(ek)
+    check(lib().yhip_kv_to_engine(_ptr(ek), _ptr(ev), _ptr(cache.k), _ptr(cache.v), n_rows, cache.n_kv,
+                                  cache.head_dim, cache.kv_stride, _stream()))
+    return ek, ev
+
+
+def decode_workspace_bytes(n_seq: int, max_len: int, total_len: int, n_heads: int, n_kv: int,
+                           head_dim: int) -> int:
+    return int(lib().yhip_attn_decode_workspace(n_seq, max_len, total_len, n_heads, n_kv, head_dim))
+
+
+def _workspace(nbytes: int, device: torch.device, ws: torch.Tensor | None) -> torch.Tensor | None:
+    if nbytes == 0:
+        return ws
+    if ws is not None and ws.numel() * ws.element_size() >= nbytes:
+        return ws
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def attn_decode(q: torch.Tensor, cache: LayerKV, pos: int, n_heads: int, gate: torch.Tensor | None = None,
+                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """One query token at position pos over keys 0..pos. q: f32 [n_heads*head_dim]."""
+    _need_gpu(q, gate)
+    d = cache.head_dim
+    if q.dtype != torch.float32 or q.numel() != n_heads * d:
+        raise YhipError(-22, "attn_decode: q must be f32 [n_heads*head_dim]")
+    if out is None:
+        out = torch.empty(n_heads * d, dtype=torch.float32, device=q.device)
+    nbytes = decode_workspace_bytes(1, pos + 1, pos + 1, n_heads, cache.n_kv, d)
+    ws = _workspace(nbytes, q.device, workspace)
+    check(lib().yhip_attn_decode(_ptr(out), _ptr(q), _ptr(cache.k), _ptr(cache.v), pos, n_heads, cache.n_kv,
+                                 d, cache.kv_stride, _ptr(gate), _ptr(ws), nbytes, _stream()))
+    return out
+
+
+class DecodeBatch:
+    """Device tables (K/V base pointers per sequence) for attn_decode_batch."""
+
+    def __init__(self, caches: list[LayerKV]):
+        if not caches:
+            raise YhipError(-22, "DecodeBatch: no sequences")
+        c0 = caches[0]
+        for c in caches:
+            if (c.n_kv, c.head_dim, c.kv_stride) != (c0.n_kv, c0.head_dim, c0.kv_stride):
+                raise YhipError(-22, "DecodeBatch: caches must share n_kv, head_dim and kv_stride")
+        dev = c0.k.device
+        self.caches = caches
+        self.kptrs = torch.tensor([c.k.data_ptr() for c in caches], dtype=torch.int64, device=dev)
+        self.vptrs = torch.tensor([c.v.data_ptr() for c in caches], dtype=torch.int64, device=dev)
+        self.n_kv, self.head_dim, self.kv_stride = c0.n_kv, c0.head_dim, c0.kv_stride
+
+
+def attn_decode_batch(q: torch.Tensor, batch: DecodeBatch, lens: list[int] | np.ndarray, n_heads: int,
+                      gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                      workspace: torch.Tensor | None = None,
+                      lens_dev: torch.Tensor | None = None) -> torch.Tensor:
+    """q: f32 [n_seq, n_heads*head_dim]; lens[i] keys for sequence i (>= 1)."""
+    _need_gpu(q, gate)
+    n_seq = len(batch.caches)
+    d = batch.head_dim
+    lens = np.asarray(lens, dtype=np.int64)
+    if q.dtype != torch.float32 or q.shape != (n_seq, n_heads * d) or lens.shape != (n_seq,):
+        raise YhipError(-22, "attn_decode_batch: q must be f32 [n_seq, n_heads*head_dim] and lens [n_seq]")
+    if lens_dev is None:
+        lens_dev = torch.tensor(lens.astype(np.int32), dtype=torch.int32, device=q.device)
+    if out is None:
+        out = torch.empty((n_seq, n_heads * d), dtype=torch.float32, device=q.device)
+    max_len, total = int(lens.max()), int(lens.sum())
+    nbytes = decode_workspace_bytes(n_seq, max_len, total, n_heads, batch.n_kv, d)
+    ws = _workspace(nbytes, q.device, workspace)
+    gstride = gate.shape[-1] if gate is not None else 0
+    check(lib().yhip_attn_decode_batch(_ptr(out), out.shape[1], _ptr(q), q.shape[1], _ptr(batch.kptrs),
+                                       _ptr(batch.vptrs), _ptr(lens_dev), n_seq, max_len, total, n_heads,
+                                       batch.n_kv, d, batch.kv_stride, _ptr(gate), gstride, _ptr(ws), nbytes,
+                                       _stream()))
+    return out
+
+
+def attn_prefill(q: torch.Tensor, cache: LayerKV, pos_start: int, n_heads: int,
+                 out_dtype: torch.dtype = torch.float32, gate: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """B prompt tokens at positions pos_start.. ; q: [B, n_heads*head_dim] (f32/f16/bf16)."""
+    _need_gpu(q, gate)
+    d = cache.head_dim
+    if q.dim() != 2 or q.shape[1] != n_heads * d:
+        raise YhipError(-22, "attn_prefill: q must be [B, n_heads*head_dim]")
+    B = q.shape[0]
+    if out is None:
+        out = torch.empty((B, n_heads * d), dtype=out_dtype, device=q.device)
+    _need_gpu(out)
+    gstride = gate.shape[-1] if gate is not None else 0
+    check(lib().yhip_attn_prefill(_ptr(out), _dtype_code(out), out.shape[1], _ptr(q), _dtype_code(q),
+                                  q.shape[1], _ptr(cache.k), _ptr(cache.v), pos_start, B, n_heads, cache.n_kv,
+                                  d, cache.kv_stride, _ptr(gate), gstride, _stream()))
+    return out
+
+
+# ---- seeded synthetic inputs (host) ----------------------------------------
+
+def synth_normal(seed: int, n: int, sigma: float = 0.5, first: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().yhip_synth_normal(seed, first, sigma, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n)
+    return out
+
+
+def round_f16(x: np.ndarray) -> np.ndarray:
+    """In place: nearest f16-representable values, reference rounding."""
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    lib().yhip_synth_round_f16(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), x.size)
+    return x
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    lib().yhip_synth_round_bf16(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), x.size)
+    return x
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().yhip_host_f32_to_f16(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                               out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), x.size)
+    return out

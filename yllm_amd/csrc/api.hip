@@ -1,0 +1,236 @@
+// api.hip -- the extern "C" entry points declared in include/yllm_hip.h:
+// argument validation, split planning and kernel launches.  No allocation
+// happens here: workspaces come from the caller.
+#include "../../include/yllm_hip.h"
+#include "internal.hpp"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace {
+
+thread_local char g_err[512];
+
+int fail(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int done(hipError_t e, const char* what)
+{
+    if (e != hipSuccess) return fail(YHIP_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+    g_err[0] = 0;
+    return YHIP_OK;
+}
+
+bool valid_head_dim(uint32_t d) { return d == 64 || d == 128 || d == 256; }
+bool valid_dtype(uint32_t t) { return t == YHIP_F16 || t == YHIP_F32 || t == YHIP_BF16; }
+
+// shared shape checks of the attention entry points
+int check_heads(const char* fn, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t kv_stride)
+{
+    if (!valid_head_dim(head_dim)) return fail(YHIP_EINVAL, "%s: head_dim %u not in {64,128,256}", fn, head_dim);
+    if (n_heads == 0 || n_kv == 0 || n_kv > n_heads)
+        return fail(YHIP_EINVAL, "%s: need 1 <= n_kv_heads (%u) <= n_heads (%u)", fn, n_kv, n_heads);
+    if ((n_heads + n_kv - 1) / n_kv > 16)
+        return fail(YHIP_EINVAL, "%s: more than 16 query heads per kv head (%u/%u)", fn, n_heads, n_kv);
+    if (kv_stride == 0 || kv_stride % 64 != 0)
+        return fail(YHIP_EINVAL, "%s: kv_stride %u must be a positive multiple of 64", fn, kv_stride);
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* yhip_last_error(void) { return g_err; }
+
+const char* yhip_version(void) { return "yllm-hip 0.1 (gfx950)"; }
+
+uint64_t yhip_kv_layer_elems(uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride)
+{
+    return (uint64_t)n_kv_heads * head_dim * kv_stride;
+}
+
+int yhip_kv_store(uint16_t* kcache, uint16_t* vcache, const void* k, const void* v,
+                  uint32_t src_dtype, uint32_t pos_start, uint32_t B, uint32_t n_kv_heads,
+                  uint32_t head_dim, uint32_t kv_stride, void* stream)
+{
+    if (!kcache || !vcache || !k || !v) return fail(YHIP_EINVAL, "yhip_kv_store: null pointer");
+    if (!valid_dtype(src_dtype)) return fail(YHIP_EINVAL, "yhip_kv_store: bad src_dtype %u", src_dtype);
+    if (!valid_head_dim(head_dim) || n_kv_heads == 0)
+        return fail(YHIP_EINVAL, "yhip_kv_store: bad n_kv_heads %u / head_dim %u", n_kv_heads, head_dim);
+    if (kv_stride == 0 || kv_stride % 64 != 0)
+        return fail(YHIP_EINVAL, "yhip_kv_store: kv_stride %u must be a positive multiple of 64", kv_stride);
+    if ((uint64_t)pos_start + B > kv_stride)
+        return fail(YHIP_EINVAL, "yhip_kv_store: rows %u..%u exceed kv_stride %u", pos_start,
+                    pos_start + B, kv_stride);
+    if (B == 0) return done(hipSuccess, "");
+    return done(yhip::launch_kv_store(kcache, vcache, k, v, src_dtype, pos_start, B, n_kv_heads,
+                                      head_dim, kv_stride, (hipStream_t)stream),
+                "yhip_kv_store");
+}
+
+int yhip_kv_from_engine(uint16_t* kcache, uint16_t* vcache, const uint16_t* eng_k,
+                        const uint16_t* eng_v, uint32_t n_rows, uint32_t n_kv_heads,
+                        uint32_t head_dim, uint32_t kv_stride, void* stream)
+{
+    if (!kcache || !vcache || !eng_k || !eng_v) return fail(YHIP_EINVAL, "yhip_kv_from_engine: null pointer");
+    if (!valid_head_dim(head_dim) || n_kv_heads == 0 || kv_stride % 64 != 0 || n_rows > kv_stride)
+        return fail(YHIP_EINVAL, "yhip_kv_from_engine: bad shape");
+    if (n_rows == 0) return done(hipSuccess, "");
+    return done(yhip::launch_kv_from_engine(kcache, vcache, eng_k, eng_v, n_rows, n_kv_heads, head_dim,
+                                            kv_stride, (hipStream_t)stream),
+                "yhip_kv_from_engine");
+}
+
+int yhip_kv_to_engine(uint16_t* eng_k, uint16_t* eng_v, const uint16_t* kcache,
+                      const uint16_t* vcache, uint32_t n_rows, uint32_t n_kv_heads,
+                      uint32_t head_dim, uint32_t kv_stride, void* stream)
+{
+    if (!kcache || !vcache || !eng_k || !eng_v) return fail(YHIP_EINVAL, "yhip_kv_to_engine: null pointer");
+    if (!valid_head_dim(head_dim) || n_kv_heads == 0 || kv_stride % 64 != 0 || n_rows > kv_stride)
+        return fail(YHIP_EINVAL, "yhip_kv_to_engine: bad shape");
+    if (n_rows == 0) return done(hipSuccess, "");
+    return done(yhip::launch_kv_to_engine(eng_k, eng_v, kcache, vcache, n_rows, n_kv_heads, head_dim,
+                                          kv_stride, (hipStream_t)stream),
+                "yhip_kv_to_engine");
+}
+
+size_t yhip_attn_decode_workspace(uint32_t n_seq, uint32_t max_len, uint64_t total_len,
+                                  uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim)
+{
+    uint32_t sk, ns;
+    if (n_kv_heads == 0) return 0;
+    return yhip::decode_plan(n_seq, max_len, total_len, n_heads, n_kv_heads, head_dim, &sk, &ns);
+}
+
+int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
+                           uint32_t q_stride, const uint16_t* const* kcaches,
+                           const uint16_t* const* vcaches, const uint32_t* lens,
+                           uint32_t n_seq, uint32_t max_len, uint64_t total_len,
+                           uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                           uint32_t kv_stride, const float* gate, uint32_t gate_stride,
+                           void* workspace, size_t workspace_bytes, void* stream)
+{
+    const char* fn = "yhip_attn_decode_batch";
+    if (!att_out || !q || !kcaches || !vcaches || !lens) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    int rc = check_heads(fn, n_heads, n_kv_heads, head_dim, kv_stride);
+    if (rc) return rc;
+    if (n_seq == 0) return done(hipSuccess, "");
+    if (n_seq > 65535) return fail(YHIP_EINVAL, "%s: n_seq %u > 65535", fn, n_seq);
+    if (max_len == 0 || max_len > kv_stride)
+        return fail(YHIP_EINVAL, "%s: max_len %u must be in 1..kv_stride (%u)", fn, max_len, kv_stride);
+    const uint32_t row = n_heads * head_dim;
+    if (q_stride < row || out_stride < row || q_stride % 4 || out_stride % 4)
+        return fail(YHIP_EINVAL, "%s: q_stride/out_stride must be >= n_heads*head_dim and a multiple of 4", fn);
+    if (gate && gate_stride < row) return fail(YHIP_EINVAL, "%s: gate_stride too small", fn);
+    yhip::DecodeArgs a = {};
+    const size_t need = yhip::decode_plan(n_seq, max_len, total_len, n_heads, n_kv_heads, head_dim,
+                                          &a.split_keys, &a.n_splits);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(YHIP_ENOSPC, "%s: workspace %zu < %zu bytes", fn, workspace_bytes, need);
+    a.q = q;
+    a.kptrs = kcaches;
+    a.vptrs = vcaches;
+    a.lens = lens;
+    a.out = att_out;
+    a.gate = gate;
+    a.part_o = reinterpret_cast<float*>(workspace);
+    a.part_ml = need ? a.part_o + (size_t)n_seq * n_heads * a.n_splits * head_dim : nullptr;
+    a.n_seq = n_seq;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.D = head_dim;
+    a.kv_stride = kv_stride;
+    a.q_stride = q_stride;
+    a.out_stride = out_stride;
+    a.gate_stride = gate_stride;
+    a.c = (float)(1.4426950408889634 / sqrt((double)head_dim));
+    return done(yhip::launch_decode(a, (hipStream_t)stream), fn);
+}
+
+int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
+                     const uint16_t* vcache, uint32_t pos, uint32_t n_heads,
+                     uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
+                     const float* gate, void* workspace, size_t workspace_bytes, void* stream)
+{
+    const char* fn = "yhip_attn_decode";
+    if (!att_out || !q || !kcache || !vcache) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    int rc = check_heads(fn, n_heads, n_kv_heads, head_dim, kv_stride);
+    if (rc) return rc;
+    if (pos >= kv_stride) return fail(YHIP_EINVAL, "%s: pos %u >= kv_stride %u", fn, pos, kv_stride);
+    yhip::DecodeArgs a = {};
+    const uint32_t len = pos + 1;
+    const size_t need = yhip::decode_plan(1, len, len, n_heads, n_kv_heads, head_dim, &a.split_keys,
+                                          &a.n_splits);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(YHIP_ENOSPC, "%s: workspace %zu < %zu bytes", fn, workspace_bytes, need);
+    a.q = q;
+    a.k0 = kcache;
+    a.v0 = vcache;
+    a.len0 = len;
+    a.out = att_out;
+    a.gate = gate;
+    a.part_o = reinterpret_cast<float*>(workspace);
+    a.part_ml = need ? a.part_o + (size_t)n_heads * a.n_splits * head_dim : nullptr;
+    a.n_seq = 1;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.D = head_dim;
+    a.kv_stride = kv_stride;
+    a.q_stride = n_heads * head_dim;
+    a.out_stride = n_heads * head_dim;
+    a.gate_stride = n_heads * head_dim;
+    a.c = (float)(1.4426950408889634 / sqrt((double)head_dim));
+    return done(yhip::launch_decode(a, (hipStream_t)stream), fn);
+}
+
+int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, const void* q,
+                      uint32_t q_dtype, uint32_t q_stride, const uint16_t* kcache,
+                      const uint16_t* vcache, uint32_t pos_start, uint32_t B, uint32_t n_heads,
+                      uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
+                      const float* gate, uint32_t gate_stride, void* stream)
+{
+    const char* fn = "yhip_attn_prefill";
+    if (!att_out || !q || !kcache || !vcache) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    if (!valid_dtype(out_dtype) || !valid_dtype(q_dtype)) return fail(YHIP_EINVAL, "%s: bad dtype", fn);
+    int rc = check_heads(fn, n_heads, n_kv_heads, head_dim, kv_stride);
+    if (rc) return rc;
+    if ((uint64_t)pos_start + B > kv_stride)
+        return fail(YHIP_EINVAL, "%s: positions %u..%u exceed kv_stride %u", fn, pos_start, pos_start + B,
+                    kv_stride);
+    const uint32_t row = n_heads * head_dim;
+    if (q_stride < row || out_stride < row || q_stride % 8 || out_stride % 8)
+        return fail(YHIP_EINVAL, "%s: q_stride/out_stride must be >= n_heads*head_dim and a multiple of 8", fn);
+    if (gate && gate_stride < row) return fail(YHIP_EINVAL, "%s: gate_stride too small", fn);
+    if (B == 0) return done(hipSuccess, "");
+    const uint64_t nblocks = (uint64_t)(B + 127) / 128 * n_heads;
+    if (nblocks > 0x7fffffffull) return fail(YHIP_EINVAL, "%s: grid too large", fn);
+    yhip::PrefillArgs a = {};
+    a.q = q;
+    a.q_dtype = q_dtype;
+    a.q_stride = q_stride;
+    a.kc = kcache;
+    a.vc = vcache;
+    a.kv_stride = kv_stride;
+    a.out = att_out;
+    a.out_dtype = out_dtype;
+    a.out_stride = out_stride;
+    a.gate = gate;
+    a.gate_stride = gate_stride;
+    a.pos_start = pos_start;
+    a.B = B;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.D = head_dim;
+    a.c = (float)(1.4426950408889634 / sqrt((double)head_dim));
+    return done(yhip::launch_prefill(a, (hipStream_t)stream), fn);
+}
+
+}  // extern "C"

@@ -1,0 +1,281 @@
+// attn_decode.hip -- split-K flash decoding over the head-major HBM KV cache.
+//
+// Semantics: engine.c:1074-1096 (one query token per head attends to keys
+// 0..pos, scores scaled by 1/sqrt(d), softmax, weighted sum of V), optionally
+// followed by the qwen35 sigmoid gate (engine.c:959-960).
+//
+// Work decomposition.  A workgroup (4 waves) owns one (sequence, kv head,
+// split of split_keys keys).  The whole GQA group of query heads that reads
+// that kv head is processed together, so every K/V byte is read from HBM
+// once.  The split's keys are walked in blocks of 32; wave w takes blocks
+// w, w+4, ... so the four waves stream neighbouring memory.
+//
+// MFMA formulation (v_mfma_f32_16x16x32_f16, per wave, per 32-key block):
+//   S^T[key][head] = K[key][:] . Q^T[:][head]       A = K rows, B = q (16 head
+//                                                    slots, group padded)
+//   O^T[d][head]  += V^T[d][key] . P^T[key][head]   A = V^T (the cache keeps V
+//                                                    transposed), B = P^T
+// Lane l owns head slot l%16 in every accumulator, so the softmax statistics
+// of a head live in one column of lanes: the max needs two cross-lane steps,
+// the running sum none until the end.  K rows are loaded in the order
+// 8*(m/4) + 4t + m%4 (row m of half t) so that the score layout of lane group
+// g is keys 8g..8g+7, exactly the k-slots of the P^T operand: P never leaves
+// registers.  q is split into f16 hi + lo parts (two MFMAs) so scores keep
+// ~fp32 accuracy for fp32 queries; the kernel is HBM-bound and the extra
+// MFMAs are free.
+//
+// Splits write (max, sum, unnormalised O) partials in the log2 domain; a
+// merge kernel combines them per (sequence, head).  With a single split the
+// workgroup writes the final output directly.
+#include "common.hpp"
+#include "internal.hpp"
+
+#include <math.h>
+
+namespace yhip {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kKeysPerBlock = 32;
+
+__device__ inline f32x4 mfma16(const f16x8& a, const f16x8& b, const f32x4& c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ inline float sigmoid_ref(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+template <int D>
+__global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(DecodeArgs a)
+{
+    constexpr int NC = D / 32;  // 32-wide d chunks of the QK contraction
+    constexpr int NB = D / 16;  // 16-row d blocks of the PV output
+    __shared__ float s_o[kWaves][16][D + 4];
+    __shared__ float s_m[kWaves][16];
+    __shared__ float s_l[kWaves][16];
+
+    const uint32_t seq = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
+    // a length beyond the planned maximum is clamped, never read past
+    const uint32_t len = min(min(a.lens ? a.lens[seq] : a.len0, a.kv_stride), a.split_keys * a.n_splits);
+    const uint32_t kbeg = split * a.split_keys;
+    if (kbeg >= len) return;  // uniform over the workgroup
+    const uint32_t kend = min(len, kbeg + a.split_keys);
+    // query heads h with h*n_kv/n_heads == kvh form [h0, h1) (engine.c:1079)
+    const uint32_t h0 = (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
+    const uint32_t h1 = ((kvh + 1) * a.n_heads + a.n_kv - 1) / a.n_kv;
+    const uint32_t G = h1 - h0;
+
+    const uint16_t* K = (a.kptrs ? a.kptrs[seq] : a.k0) + (size_t)kvh * a.kv_stride * D;
+    const uint16_t* VT = (a.vptrs ? a.vptrs[seq] : a.v0) + (size_t)kvh * D * a.kv_stride;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, g = lane >> 4;
+
+    // B operand of the score MFMA: head slot n, dims c*32 + 8g .. +7
+    f16x8 qhi[NC], qlo[NC];
+    {
+        const bool valid = (uint32_t)n < G;
+        const float* qrow = a.q + (size_t)seq * a.q_stride + (size_t)(h0 + (valid ? n : 0)) * D;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const f32x4 lo4 = *reinterpret_cast<const f32x4*>(qrow + c * 32 + g * 8);
+            const f32x4 hi4 = *reinterpret_cast<const f32x4*>(qrow + c * 32 + g * 8 + 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = valid ? (j < 4 ? lo4[j] : hi4[j - 4]) : 0.0f;
+                const _Float16 h = (_Float16)x;
+                qhi[c][j] = h;
+                qlo[c][j] = (_Float16)(x - (float)h);
+            }
+        }
+    }
+
+    float m = -INFINITY, l = 0.0f;
+    f32x4 o[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t nblk = (kend - kbeg + kKeysPerBlock - 1) / kKeysPerBlock;
+    const int krow_in_block = 8 * (n >> 2) + (n & 3);  // + 4t for half t
+    for (uint32_t blk = wave; blk < nblk; blk += kWaves) {
+        const uint32_t key0 = kbeg + blk * kKeysPerBlock;
+        f16x8 kf[2][NC];
+        f16x8 vf[NB];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint16_t* kp = K + (size_t)(key0 + krow_in_block + 4 * t) * D + g * 8;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) kf[t][c] = *reinterpret_cast<const f16x8*>(kp + c * 32);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            vf[b] = *reinterpret_cast<const f16x8*>(VT + (size_t)(b * 16 + n) * a.kv_stride + key0 + g * 8);
+
+        f32x4 s[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                s[t] = mfma16(kf[t][c], qhi[c], s[t]);
+                s[t] = mfma16(kf[t][c], qlo[c], s[t]);
+            }
+        }
+        // s[t][i] is head n, key key0 + 8g + 4t + i
+        float x[8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[4 * t + i] = s[t][i] * a.c;
+        const bool tail = key0 + kKeysPerBlock > kend;
+        if (tail) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (key0 + 8 * g + j >= kend) x[j] = -INFINITY;
+        }
+        float mx = x[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[j]);
+        mx = wave_max_xor(mx, 16);
+        mx = wave_max_xor(mx, 32);
+        const float mn = fmaxf(m, mx);
+        const float alpha = fast_exp2(m - mn);
+        float p[8], ps = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            p[j] = fast_exp2(x[j] - mn);
+            ps += p[j];
+        }
+        l = l * alpha + ps;
+        m = mn;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) o[b] *= alpha;
+        if (tail) {
+            // keys past the end carry P = 0; their V must not be NaN/inf
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (key0 + 8 * g + j >= kend) vf[b][j] = (_Float16)0.0f;
+        }
+        f16x8 pf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pf[j] = (_Float16)p[j];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) o[b] = mfma16(vf[b], pf, o[b]);
+    }
+
+    // per-lane partial sums -> per head (the four lane groups hold one head)
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (g == 0) {
+        s_m[wave][n] = m;
+        s_l[wave][n] = l;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_o[wave][n][b * 16 + 4 * g + i] = o[b][i];
+    __syncthreads();
+
+    for (uint32_t idx = threadIdx.x; idx < G * D; idx += 256u) {
+        const uint32_t hn = idx / D, d = idx - hn * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hn]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = s_m[w][hn];
+            if (mw != -INFINITY) {
+                const float sc = fast_exp2(mw - M);
+                L += s_l[w][hn] * sc;
+                O += s_o[w][hn][d] * sc;
+            }
+        }
+        const uint32_t h = h0 + hn;
+        if (a.n_splits == 1) {
+            float r = O / L;
+            if (a.gate) r *= sigmoid_ref(a.gate[(size_t)seq * a.gate_stride + (size_t)h * D + d]);
+            a.out[(size_t)seq * a.out_stride + (size_t)h * D + d] = r;
+        } else {
+            const size_t slot = ((size_t)seq * a.n_heads + h) * a.n_splits + split;
+            a.part_o[slot * D + d] = O;
+            if (d == 0) {
+                a.part_ml[slot * 2] = M;
+                a.part_ml[slot * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// one block per (head, sequence), one thread per output dimension
+template <int D>
+__global__ __launch_bounds__(D) void decode_merge_kernel(DecodeArgs a)
+{
+    const uint32_t h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+    const uint32_t len = a.lens ? a.lens[seq] : a.len0;
+    const uint32_t ns = min((len + a.split_keys - 1) / a.split_keys, a.n_splits);
+    const size_t base = ((size_t)seq * a.n_heads + h) * a.n_splits;
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[(base + s) * 2]);
+    float L = 0.0f, O = 0.0f;
+    for (uint32_t s = 0; s < ns; ++s) {
+        const float sc = fast_exp2(a.part_ml[(base + s) * 2] - M);
+        L += a.part_ml[(base + s) * 2 + 1] * sc;
+        O += a.part_o[(base + s) * D + d] * sc;
+    }
+    float r = ns ? O / L : 0.0f;
+    if (a.gate) r *= sigmoid_ref(a.gate[(size_t)seq * a.gate_stride + (size_t)h * D + d]);
+    a.out[(size_t)seq * a.out_stride + (size_t)h * D + d] = r;
+}
+
+template <int D>
+hipError_t launch_decode_d(const DecodeArgs& a, hipStream_t st)
+{
+    dim3 grid(a.n_splits, a.n_kv, a.n_seq);
+    hipLaunchKernelGGL(decode_split_kernel<D>, grid, dim3(256), 0, st, a);
+    if (a.n_splits > 1) {
+        dim3 mg(a.n_heads, a.n_seq);
+        hipLaunchKernelGGL(decode_merge_kernel<D>, mg, dim3(D), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
+                   uint32_t n_kv, uint32_t D, uint32_t* split_keys, uint32_t* n_splits)
+{
+    // aim at ~1024 workgroups (4 per CU on 256 CUs) streaming equal key counts
+    const uint64_t target_wg = 1024;
+    uint64_t work = total_len * (uint64_t)n_kv;
+    uint64_t sk = (work + target_wg - 1) / target_wg;
+    sk = (sk + 127) / 128 * 128;
+    if (sk < 128) sk = 128;
+    if (sk > 16384) sk = 16384;
+    uint32_t ns;
+    if (sk >= max_len) {
+        sk = ((uint64_t)max_len + 31) / 32 * 32;
+        if (sk < 32) sk = 32;
+        ns = 1;
+    } else {
+        ns = (uint32_t)((max_len + sk - 1) / sk);
+    }
+    *split_keys = (uint32_t)sk;
+    *n_splits = ns;
+    if (ns == 1) return 0;
+    return (size_t)n_seq * n_heads * ns * ((size_t)D + 2) * sizeof(float);
+}
+
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t st)
+{
+    switch (a.D) {
+    case 64: return launch_decode_d<64>(a, st);
+    case 128: return launch_decode_d<128>(a, st);
+    case 256: return launch_decode_d<256>(a, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace yhip

@@ -1,0 +1,303 @@
+// attn_prefill.hip -- causal grouped-query attention for a batch of prompt
+// tokens on gfx950 MFMA.
+//
+// Semantics: engine.c:532-563 (token b at position pos_start+b attends to
+// keys 0..pos_start+b; scores scaled by 1/sqrt(d); softmax; weighted V),
+// with the optional qwen35 sigmoid gate (engine.c:959-960).
+//
+// Tiling.  A workgroup of 4 waves owns 128 consecutive queries of one query
+// head; wave w owns 32 of them.  Keys stream through LDS in tiles of 64
+// (K rows [64][D] and the transposed V^T [D][64] straight from the cache
+// layout), loaded cooperatively one tile ahead into registers.  Workgroups
+// are issued heaviest (latest queries) first so the causal triangle drains
+// evenly.
+//
+// MFMA formulation (v_mfma_f32_32x32x16_f16), everything transposed so that a
+// lane owns one query for the whole kernel:
+//   S^T[key][q] = K[key][:] . Q^T[:][q]        A = K tile (LDS), B = Q (regs)
+//   O^T[d][q]  += V^T[d][key] . P^T[key][q]    A = V^T tile (LDS), B = P (regs)
+// Softmax statistics of a query are in one lane pair (l, l+32): row max over
+// a tile is 31 in-lane maxes and one exchange, the running sum is per lane
+// until the end.  K rows are written to LDS with rows 4..7 and 8..11 of every
+// 16 swapped, which turns the 32x32 accumulator layout (rows 8(i/4)+4(l/32)+
+// i%4) into contiguous key runs 8(l/32)+i: the score registers are then
+// exactly the k-slots of the P^T operand and P stays in registers.
+// Scores use exp2 with log2(e)/sqrt(d) folded into one multiply.
+#include "common.hpp"
+#include "internal.hpp"
+
+#include <math.h>
+
+namespace yhip {
+namespace {
+
+constexpr int BM = 128;  // queries per workgroup
+constexpr int BN = 64;   // keys per tile
+
+__device__ inline f32x16 mfma32(const f16x8& a, const f16x8& b, const f32x16& c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ inline float sigmoid_ref(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+// key row r of a tile lives in LDS row perm(r): rows 4..7 <-> 8..11 of each 16
+__device__ inline int lds_row_of_key(int r)
+{
+    return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+}
+
+// key (within a 32-key half) of accumulator element i for lane half hh
+__device__ inline int key_of_acc(int i, int hh) { return i < 8 ? 8 * hh + i : 16 + 8 * hh + (i - 8); }
+
+__device__ inline void load_q8(f16x8& dst, const void* q, size_t off, uint32_t dt)
+{
+    if (dt == kF32) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(q) + off);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(q) + off + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            dst[j] = (_Float16)a[j];
+            dst[j + 4] = (_Float16)b[j];
+        }
+    } else if (dt == kF16) {
+        dst = *reinterpret_cast<const f16x8*>(reinterpret_cast<const uint16_t*>(q) + off);
+    } else {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(q) + off);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            dst[2 * j] = (_Float16)__builtin_bit_cast(float, w[j] << 16);
+            dst[2 * j + 1] = (_Float16)__builtin_bit_cast(float, w[j] & 0xffff0000u);
+        }
+    }
+}
+
+__device__ inline void store_out4(void* out, size_t off, uint32_t dt, f32x4 v)
+{
+    if (dt == kF32) {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + off) = v;
+    } else if (dt == kF16) {
+        typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+        f16x4 h;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[j] = (_Float16)v[j];
+        *reinterpret_cast<f16x4*>(reinterpret_cast<uint16_t*>(out) + off) = h;
+    } else {
+        uint16_t b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t x = __builtin_bit_cast(uint32_t, v[j]);
+            b[j] = (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);  // RNE
+        }
+        uint16_t* p = reinterpret_cast<uint16_t*>(out) + off;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = b[j];
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(PrefillArgs a)
+{
+    constexpr int KS = D + 8;     // K tile row stride (halfs), 16 B pad
+    constexpr int VS = BN + 8;    // V^T tile row stride (halfs)
+    constexpr int NKK = D / 16;   // k-chunks of the score MFMA
+    constexpr int NDB = D / 32;   // d-blocks of the output MFMA
+    constexpr int CH = D / 32;    // 16-byte chunks per thread per tile (K and V each)
+    constexpr int KCH = D / 8;    // 16-byte chunks per K row
+    __shared__ _Float16 Kl[BN * KS];
+    __shared__ _Float16 Vl[D * VS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, hh = lane >> 5;
+
+    const uint32_t nqb = (a.B + BM - 1) / BM;
+    const uint32_t qb = nqb - 1 - blockIdx.x / a.n_heads;
+    const uint32_t h = blockIdx.x % a.n_heads;
+    const uint32_t kvh = h * a.n_kv / a.n_heads;  // engine.c:537
+
+    const uint32_t qi0 = qb * BM;
+    const uint32_t qlast = min(a.B, qi0 + BM) - 1;
+    const uint32_t kmax = a.pos_start + qlast;  // last key any query here reads
+    const uint32_t ntiles = kmax / BN + 1;
+
+    const uint32_t wq0 = qi0 + wave * 32;
+    const bool wave_active = wq0 < a.B;
+    const uint32_t wpos_first = a.pos_start + wq0;
+    const uint32_t wpos_last = a.pos_start + min(wq0 + 31, a.B - 1);
+    const uint32_t my_pos = a.pos_start + wq0 + r32;
+    const uint32_t my_q = min(wq0 + r32, a.B - 1);
+
+    f16x8 qf[NKK];
+    {
+        const size_t base = (size_t)my_q * a.q_stride + (size_t)h * D + hh * 8;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, base + kk * 16, a.q_dtype);
+    }
+
+    const uint16_t* Kg = a.kc + (size_t)kvh * a.kv_stride * D;
+    const uint16_t* Vg = a.vc + (size_t)kvh * D * a.kv_stride;
+
+    u32x4 kreg[CH], vreg[CH];
+    auto load_tile = [&](uint32_t kt) {
+        const uint32_t k0 = kt * BN;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = tid + 256 * i;
+            const int row = c / KCH, col = c % KCH;
+            kreg[i] = *reinterpret_cast<const u32x4*>(Kg + (size_t)(k0 + row) * D + col * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = tid + 256 * i;
+            const int row = c >> 3, col = c & 7;
+            vreg[i] = *reinterpret_cast<const u32x4*>(Vg + (size_t)row * a.kv_stride + k0 + col * 8);
+        }
+    };
+    auto store_tile = [&](uint32_t kt) {
+        const uint32_t k0 = kt * BN;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = tid + 256 * i;
+            const int row = c / KCH, col = c % KCH;
+            *reinterpret_cast<u32x4*>(&Kl[lds_row_of_key(row) * KS + col * 8]) = kreg[i];
+        }
+        const bool tail = k0 + BN - 1 > kmax;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = tid + 256 * i;
+            const int row = c >> 3, col = c & 7;
+            u32x4 v = vreg[i];
+            if (tail) {
+                // keys past kmax were never stored: their P is 0, their V must be finite
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t key = k0 + col * 8 + 2 * e;
+                    if (key > kmax) v[e] = 0u;
+                    else if (key + 1 > kmax) v[e] &= 0xffffu;
+                }
+            }
+            *reinterpret_cast<u32x4*>(&Vl[row * VS + col * 8]) = v;
+        }
+    };
+
+    float m = -INFINITY, l = 0.0f;
+    f32x16 o[NDB];
+#pragma unroll
+    for (int b = 0; b < NDB; ++b)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
+
+    load_tile(0);
+    for (uint32_t kt = 0; kt < ntiles; ++kt) {
+        __syncthreads();
+        store_tile(kt);
+        __syncthreads();
+        if (kt + 1 < ntiles) load_tile(kt + 1);
+
+        const uint32_t k0 = kt * BN;
+        if (!wave_active || k0 > wpos_last) continue;
+        const bool half1 = k0 + 32 <= wpos_last;
+
+        f32x16 s[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[j][i] = 0.0f;
+            if (j == 1 && !half1) break;
+            const _Float16* kr = &Kl[(32 * j + r32) * KS + hh * 8];
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk)
+                s[j] = mfma32(*reinterpret_cast<const f16x8*>(kr + kk * 16), qf[kk], s[j]);
+        }
+
+        float x[32];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[16 * j + i] = s[j][i] * a.c;
+        if (!half1) {
+#pragma unroll
+            for (int i = 16; i < 32; ++i) x[i] = -INFINITY;
+        }
+        if (k0 + BN - 1 > wpos_first) {  // tile crosses the diagonal of this wave
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (k0 + 32 * j + key_of_acc(i, hh) > my_pos) x[16 * j + i] = -INFINITY;
+        }
+        float mx = x[0];
+#pragma unroll
+        for (int i = 1; i < 32; ++i) mx = fmaxf(mx, x[i]);
+        mx = wave_max_xor(mx, 32);
+        const float mn = fmaxf(m, mx);
+        const float alpha = fast_exp2(m - mn);
+        m = mn;
+        float ps = 0.0f;
+        f16x8 pf[4];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const float p = fast_exp2(x[i] - mn);
+            ps += p;
+            pf[i >> 3][i & 7] = (_Float16)p;
+        }
+        l = l * alpha + ps;
+#pragma unroll
+        for (int b = 0; b < NDB; ++b) o[b] *= alpha;
+
+        const int nkc = half1 ? 4 : 2;
+#pragma unroll
+        for (int b = 0; b < NDB; ++b) {
+            const _Float16* vr = &Vl[(b * 32 + r32) * VS + hh * 8];
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) {
+                if (kc >= nkc) break;
+                o[b] = mfma32(*reinterpret_cast<const f16x8*>(vr + kc * 16), pf[kc], o[b]);
+            }
+        }
+    }
+
+    l += __shfl_xor(l, 32, 64);
+    if (!wave_active) return;
+    const uint32_t qi = wq0 + r32;
+    if (qi >= a.B) return;
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int b = 0; b < NDB; ++b) {
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const uint32_t d = b * 32 + 8 * i4 + 4 * hh;
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = o[b][4 * i4 + e] * inv;
+            if (a.gate) {
+                const float* gp = a.gate + (size_t)qi * a.gate_stride + (size_t)h * D + d;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] *= sigmoid_ref(gp[e]);
+            }
+            store_out4(a.out, (size_t)qi * a.out_stride + (size_t)h * D + d, a.out_dtype, v);
+        }
+    }
+}
+
+template <int D>
+hipError_t launch_prefill_d(const PrefillArgs& a, hipStream_t st)
+{
+    const uint32_t nqb = (a.B + BM - 1) / BM;
+    hipLaunchKernelGGL(prefill_kernel<D>, dim3(nqb * a.n_heads), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st)
+{
+    switch (a.D) {
+    case 64: return launch_prefill_d<64>(a, st);
+    case 128: return launch_prefill_d<128>(a, st);
+    case 256: return launch_prefill_d<256>(a, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace yhip

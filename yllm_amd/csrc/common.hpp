@@ -1,0 +1,70 @@
+// common.hpp -- shared device helpers for the gfx950 attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace yhip {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kF16 = 0, kF32 = 1, kBF16 = 2;
+
+// float -> f16 bits with the reference CPU rounding (platform.c:340-379):
+// the magnitude gets half an f16 ulp added and is truncated, so ties go away
+// from zero; f32 subnormals become signed zero; overflow becomes inf; NaN
+// keeps a quiet payload of 0x200.  Integer-only, identical on host and device.
+__host__ __device__ inline uint16_t f32_to_f16_ref(float f)
+{
+    uint32_t bits = __builtin_bit_cast(uint32_t, f);
+    uint32_t s = (bits >> 16) & 0x8000u;
+    uint32_t be = (bits >> 23) & 0xffu;
+    uint32_t frac = bits & 0x7fffffu;
+    if (be == 0u) return (uint16_t)s;
+    if (be == 0xffu) return (uint16_t)(s | 0x7c00u | (frac ? 0x0200u : 0u));
+    int he = (int)be - 112;
+    if (he >= 31) return (uint16_t)(s | 0x7c00u);
+    if (he <= 0) {
+        if (he < -10) return (uint16_t)s;
+        uint32_t m = frac | 0x800000u;
+        uint32_t sh = (uint32_t)(14 - he);
+        return (uint16_t)(s | ((m + (1u << (sh - 1))) >> sh));
+    }
+    uint32_t r = frac + 0x1000u;
+    if (r & 0x800000u) {
+        he += 1;
+        if (he >= 31) return (uint16_t)(s | 0x7c00u);
+        return (uint16_t)(s | ((uint32_t)he << 10));
+    }
+    return (uint16_t)(s | ((uint32_t)he << 10) | (r >> 13));
+}
+
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t b)
+{
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+__host__ __device__ inline float f16_bits_to_f32(uint16_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// one element of a q/k/v source of element type dt, widened to float exactly
+__device__ inline float load_as_f32(const void* p, size_t i, uint32_t dt)
+{
+    if (dt == kF32) return reinterpret_cast<const float*>(p)[i];
+    uint16_t b = reinterpret_cast<const uint16_t*>(p)[i];
+    return dt == kBF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline float wave_max_xor(float v, int mask)
+{
+    return fmaxf(v, __shfl_xor(v, mask, 64));
+}
+
+}  // namespace yhip

@@ -1,0 +1,60 @@
+// internal.hpp -- launchers shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace yhip {
+
+// ---- kv_store.hip ----
+hipError_t launch_kv_store(uint16_t* kc, uint16_t* vc, const void* k, const void* v, uint32_t dt,
+                           uint32_t pos_start, uint32_t B, uint32_t n_kv, uint32_t D,
+                           uint32_t kv_stride, hipStream_t st);
+hipError_t launch_kv_from_engine(uint16_t* kc, uint16_t* vc, const uint16_t* ek, const uint16_t* ev,
+                                 uint32_t rows, uint32_t n_kv, uint32_t D, uint32_t kv_stride,
+                                 hipStream_t st);
+hipError_t launch_kv_to_engine(uint16_t* ek, uint16_t* ev, const uint16_t* kc, const uint16_t* vc,
+                               uint32_t rows, uint32_t n_kv, uint32_t D, uint32_t kv_stride,
+                               hipStream_t st);
+
+// ---- attn_decode.hip ----
+struct DecodeArgs {
+    const float* q;                 // rows q_stride apart per sequence
+    const uint16_t* const* kptrs;   // per-sequence K bases (device array) or null
+    const uint16_t* const* vptrs;
+    const uint16_t* k0;             // single-sequence K/V when kptrs is null
+    const uint16_t* v0;
+    const uint32_t* lens;           // per-sequence key counts (device) or null
+    uint32_t len0;                  // key count when lens is null
+    float* out;
+    const float* gate;
+    float* part_o;                  // [n_seq][n_heads][n_splits][D]
+    float* part_ml;                 // [n_seq][n_heads][n_splits][2]
+    uint32_t n_seq, n_heads, n_kv, D, kv_stride;
+    uint32_t q_stride, out_stride, gate_stride;
+    uint32_t split_keys, n_splits;
+    float c;                        // log2(e)/sqrt(D)
+};
+// split plan for the shapes; returns workspace bytes
+size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
+                   uint32_t n_kv, uint32_t D, uint32_t* split_keys, uint32_t* n_splits);
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
+
+// ---- attn_prefill.hip ----
+struct PrefillArgs {
+    const void* q;
+    uint32_t q_dtype, q_stride;
+    const uint16_t* kc;
+    const uint16_t* vc;
+    uint32_t kv_stride;
+    void* out;
+    uint32_t out_dtype, out_stride;
+    const float* gate;
+    uint32_t gate_stride;
+    uint32_t pos_start, B, n_heads, n_kv, D;
+    float c;
+};
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
+
+}  // namespace yhip
