@@ -232,9 +232,9 @@ def _host_desc(O) -> tuple[int, str]:
 
 def cpu_prefill(q, k, v, out, L, nh, nkv, hd):
     """Full workload on the CPU oracle (OpenMP over heads, as the reference)."""
+    O = _oracle()
     from oracle_lib import rel_l2
 
-    O = _oracle()
     qn = q.float().cpu().numpy()
     kc = O.f32_to_f16(k.float().cpu().numpy())
     vc = O.f32_to_f16(v.float().cpu().numpy())
@@ -249,11 +249,11 @@ def cpu_prefill(q, k, v, out, L, nh, nkv, hd):
 
 
 def cpu_decode(q, cache, out, L, nh, nkv, hd):
-    from oracle_lib import rel_l2
-
     from yllm_amd.attention import kv_to_engine
 
     O = _oracle()
+    from oracle_lib import rel_l2
+
     ek, ev = kv_to_engine(cache, L)
     kc = ek.view(__import__("torch").int16).cpu().numpy().view(np.uint16)
     vc = ev.view(__import__("torch").int16).cpu().numpy().view(np.uint16)

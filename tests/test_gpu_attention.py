@@ -39,7 +39,8 @@ def make_cache(cuda, oracle, K, V, n_kv, hd, stride_rows=None, src=torch.float32
     kt = torch.from_numpy(K).to(cuda).to(src)
     vt = torch.from_numpy(V).to(cuda).to(src)
     kv_store(cache, kt, vt, 0)
-    kc, vc = oracle.f32_to_f16(K), oracle.f32_to_f16(V)
+    # the engine sees the src-typed values as floats and rounds them itself
+    kc, vc = oracle.f32_to_f16(kt.float().cpu().numpy()), oracle.f32_to_f16(vt.float().cpu().numpy())
     return cache, kc, vc
 
 
@@ -211,10 +212,12 @@ def test_prefill_parity(cuda, oracle, nh, nkv, hd, ps, B, qdt, odt):
     got = attn_prefill(qt, cache, ps, nh, out_dtype=odt).float().cpu().numpy()
     err = rel_l2(got, want)
     print(f"prefill {nh}/{nkv} d={hd} ps={ps} B={B} q={qdt} out={odt}: rel_l2={err:.3e}")
-    assert err <= TOL
+    # a bf16-typed output adds its own rounding (up to 2^-9 relative per element)
+    tol = TOL + (2.0 ** -8 if odt == torch.bfloat16 else 0.0)
+    assert err <= tol
     # every row on its own, so one bad query cannot hide in the average
     rows = [rel_l2(got[i], want[i]) for i in range(B)]
-    assert max(rows) <= 3 * TOL
+    assert max(rows) <= 3 * tol
 
 
 def test_prefill_gated_parity(cuda, oracle):

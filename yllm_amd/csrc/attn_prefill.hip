@@ -83,15 +83,20 @@ __device__ inline void store_out4(void* out, size_t off, uint32_t dt, f32x4 v)
         for (int j = 0; j < 4; ++j) h[j] = (_Float16)v[j];
         *reinterpret_cast<f16x4*>(reinterpret_cast<uint16_t*>(out) + off) = h;
     } else {
-        uint16_t b[4];
+        // round to nearest even; each element goes through a scalar float
+        // (bit-casting an ext-vector element directly reads element 0)
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        uint32_t h[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t x = __builtin_bit_cast(uint32_t, v[j]);
-            b[j] = (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);  // RNE
+            const float f = v[j];
+            const uint32_t x = __builtin_bit_cast(uint32_t, f);
+            h[j] = (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
         }
-        uint16_t* p = reinterpret_cast<uint16_t*>(out) + off;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = b[j];
+        u32x2 w;
+        w[0] = h[0] | (h[1] << 16);
+        w[1] = h[2] | (h[3] << 16);
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(out) + off) = w;
     }
 }
 
