@@ -56,27 +56,53 @@ def prefill_flops(L: int, nh: int, hd: int, pos_start: int = 0) -> float:
     return 4.0 * nh * hd * keys
 
 
-def time_steps(fn, steps: int, warmup: int):
-    """Run fn(i) warmup times, then time `steps` calls with HIP events on the
-    launch stream (torch's current stream).  Returns (ms_per_step, mean launch
-    ms, wall seconds)."""
+def time_steps(fn, steps: int, warmup: int, out=None):
+    """Run fn(i) `warmup` times eagerly, capture steps warmup..warmup+steps-1
+    in one HIP graph and time its replay with HIP events on the replay stream,
+    so host launch overhead is not part of the measurement.  The output of
+    the replayed last step is checked bit for bit against the same step run
+    eagerly.  Returns (ms_per_step, ms per step of the graph's kernels)."""
     import torch
 
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record()
-        fn(warmup + i)
-        ends[i].record()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(warmup + i)
+    g.replay()  # first replay uploads the graph
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    total_ms = starts[0].elapsed_time(ends[-1])
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return total_ms / steps, float(np.mean(per)), wall
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    if out is not None:
+        replayed = out.clone()
+        fn(warmup + steps - 1)
+        torch.cuda.synchronize()
+        if not torch.equal(replayed, out):
+            raise RuntimeError("graph replay and eager run of the same step differ")
+    return ms, ms
+
+
+def copy_ceiling_gbps() -> float:
+    """Measured device-to-device copy bandwidth (read + write bytes), 1 GiB."""
+    import torch
+
+    a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(10):
+        b.copy_(a)
+    end.record()
+    torch.cuda.synchronize()
+    return 2.0 * 10 * a.numel() / (start.elapsed_time(end) * 1e-3) / 1e9
 
 
 # ------------------------------------------------------------------ workloads
@@ -95,7 +121,7 @@ def run_prefill(L: int, nh: int, nkv: int, hd: int, cfg: int, steps: int, warmup
     cache = LayerKV.empty(nkv, hd, L, device=dev)
     kv_store(cache, k, v, 0)
     out = torch.empty((L, nh * hd), dtype=torch.float32, device=dev)
-    ms, kern_ms, _ = time_steps(lambda i: attn_prefill(q, cache, 0, nh, out=out), steps, warmup)
+    ms, kern_ms = time_steps(lambda i: attn_prefill(q, cache, 0, nh, out=out), steps, warmup, out)
     flops = prefill_flops(L, nh, hd)
     achieved = flops / (kern_ms * 1e-3)
     res = {
@@ -123,7 +149,7 @@ def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, step
                cpu: bool, label: str):
     import torch
 
-    from yllm_amd.attention import LayerKV, attn_decode, decode_workspace_bytes, kv_store
+    from yllm_amd.attention import LayerKV, attn_decode, decode_workspace, decode_workspace_bytes, kv_store
 
     dev = torch.device("cuda:0")
     seed = SEED + cfg
@@ -137,10 +163,10 @@ def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, step
         kv_store(c, k, v, 0)
         caches.append(c)
     del k, v
-    ws = torch.empty(max(decode_workspace_bytes(1, L, L, nh, nkv, hd), 1), dtype=torch.uint8, device=dev)
+    ws = decode_workspace(decode_workspace_bytes(1, L, L, nh, nkv, hd), dev)
     out = torch.empty(nh * hd, dtype=torch.float32, device=dev)
-    ms, kern_ms, _ = time_steps(lambda i: attn_decode(q, caches[i % n_layers], L - 1, nh, out=out, workspace=ws),
-                                steps, warmup)
+    ms, kern_ms = time_steps(lambda i: attn_decode(q, caches[i % n_layers], L - 1, nh, out=out, workspace=ws),
+                             steps, warmup, out)
     nbytes = decode_bytes(L, nkv, nh, hd)
     achieved = nbytes / (kern_ms * 1e-3)
     res = {
@@ -165,7 +191,8 @@ def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, step
 def run_decode_batch(nh: int, nkv: int, hd: int, n_seq: int, steps: int, warmup: int):
     import torch
 
-    from yllm_amd.attention import DecodeBatch, LayerKV, attn_decode_batch, decode_workspace_bytes, kv_store
+    from yllm_amd.attention import (DecodeBatch, LayerKV, attn_decode_batch, decode_workspace,
+                                    decode_workspace_bytes, kv_store)
 
     dev = torch.device("cuda:0")
     seed = SEED + 3
@@ -188,11 +215,10 @@ def run_decode_batch(nh: int, nkv: int, hd: int, n_seq: int, steps: int, warmup:
     batch = DecodeBatch(caches)
     q = torch.from_numpy(synth(seed + 100, n_seq * nh * hd).reshape(n_seq, nh * hd)).to(dev)
     lens_dev = torch.tensor(lens.astype(np.int32), device=dev)
-    ws = torch.empty(max(decode_workspace_bytes(n_seq, int(lens.max()), int(lens.sum()), nh, nkv, hd), 1),
-                     dtype=torch.uint8, device=dev)
+    ws = decode_workspace(decode_workspace_bytes(n_seq, int(lens.max()), int(lens.sum()), nh, nkv, hd), dev)
     out = torch.empty((n_seq, nh * hd), dtype=torch.float32, device=dev)
-    ms, kern_ms, _ = time_steps(lambda i: attn_decode_batch(q, batch, lens, nh, out=out, workspace=ws,
-                                                            lens_dev=lens_dev), steps, warmup)
+    ms, kern_ms = time_steps(lambda i: attn_decode_batch(q, batch, lens, nh, out=out, workspace=ws,
+                                                         lens_dev=lens_dev), steps, warmup, out)
     nbytes = float(lens.sum()) * kvd * 2 * 2 + 2.0 * n_seq * nh * hd * 4
     achieved = nbytes / (kern_ms * 1e-3)
     return {
@@ -325,7 +351,9 @@ def main() -> int:
     line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "f16 MFMA, f32 accumulate/softmax", "data": "synthetic",
-            "config": res["config"], "tokens_per_s": res["tokens_per_s"], "roofline": res["roofline"]}
+            "config": res["config"], "tokens_per_s": res["tokens_per_s"], "roofline": res["roofline"],
+            "timing": "K steps captured in one HIP graph, replay timed with HIP events on its stream",
+            "measured_copy_GBps": copy_ceiling_gbps()}
     if "cpu_baseline" in res:
         line["cpu_baseline"] = res["cpu_baseline"]
     if w == "prefill2k" and not args.no_secondary:

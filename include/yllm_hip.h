@@ -109,7 +109,11 @@ int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
                            uint32_t kv_stride, const float* gate, uint32_t gate_stride,
                            void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes the two decode entry points need for these shapes. */
+/* Workspace bytes the two decode entry points need for these shapes (0 when
+ * the context is short enough for one split).  It holds the per-split
+ * partial results; no initialisation is needed, and one workspace can serve
+ * calls of any shape that fits, provided they do not run concurrently (e.g.
+ * on two streams). */
 size_t yhip_attn_decode_workspace(uint32_t n_seq, uint32_t max_len, uint64_t total_len,
                                   uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
 

@@ -220,13 +220,21 @@ class Ref:
 
 
 def engine_to_headmajor(kc: np.ndarray, vc: np.ndarray, n_kv: int, hd: int, stride: int):
-    """Engine rows [n, n_kv*hd] (u16) -> (K [n_kv, stride, hd], V^T [n_kv, hd, stride]) zero padded."""
+    """Engine rows [n, n_kv*hd] (u16) -> the HIP cache geometry, zero padded:
+    K [n_kv, stride, hd] and V [n_kv, stride/32, hd, 32] (32-position tiles, d-major)."""
     n = kc.shape[0]
     K = np.zeros((n_kv, stride, hd), np.uint16)
-    V = np.zeros((n_kv, hd, stride), np.uint16)
+    Vt = np.zeros((n_kv, hd, stride), np.uint16)
     K[:, :n, :] = kc.reshape(n, n_kv, hd).transpose(1, 0, 2)
-    V[:, :, :n] = vc.reshape(n, n_kv, hd).transpose(1, 2, 0)
+    Vt[:, :, :n] = vc.reshape(n, n_kv, hd).transpose(1, 2, 0)
+    V = Vt.reshape(n_kv, hd, stride // 32, 32).transpose(0, 2, 1, 3).copy()
     return K, V
+
+
+def untile_v(V: np.ndarray) -> np.ndarray:
+    """V [n_kv, stride/32, hd, 32] -> [n_kv, hd, stride] (column = position)."""
+    n_kv, nt, hd, t = V.shape
+    return V.transpose(0, 2, 1, 3).reshape(n_kv, hd, nt * t)
 
 
 def rel_l2(a: np.ndarray, b: np.ndarray) -> float:

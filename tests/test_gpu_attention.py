@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle_lib import engine_to_headmajor, rel_l2
+from oracle_lib import engine_to_headmajor, rel_l2, untile_v
 
 pytestmark = pytest.mark.gpu
 
@@ -71,9 +71,12 @@ def test_kv_store_bits_match_reference_rounding(cuda, oracle, golden, src):
     kv_store(cache, kt[17:], vt[17:], 17)  # second call continues at pos_start
     Kb, Vb = cache_bits(cache)
     Kw, Vw = engine_to_headmajor(oracle.f32_to_f16(Kx), oracle.f32_to_f16(Vx), n_kv, hd, cache.kv_stride)
+    Vb, Vw = untile_v(Vb), untile_v(Vw)  # [n_kv, hd, position]
     nan = np.isnan(Kx).any(axis=1)
     assert np.array_equal(Kb[:, : rows][:, ~nan], Kw[:, : rows][:, ~nan])
     assert np.array_equal(Vb[:, :, : rows][:, :, ~nan[::-1]], Vw[:, :, : rows][:, :, ~nan[::-1]])
+    # nothing outside the stored rows was touched
+    assert not Kb[:, rows:].any() and not Vb[:, :, rows:].any()
 
 
 def test_kv_engine_layout_round_trip(cuda, oracle):
@@ -164,6 +167,25 @@ def test_decode_batch_ragged_parity(cuda, oracle):
     for i, L in enumerate(lens):
         err = rel_l2(got[i], wants[i])
         print(f"batch seq {i} L={L}: rel_l2={err:.3e}")
+        assert err <= TOL
+
+
+def test_decode_workspace_reuse_across_calls(cuda, oracle):
+    """One workspace serves many split-K calls of different lengths (stale
+    partials of a longer call must never leak into a shorter one)."""
+    from yllm_amd.attention import attn_decode, decode_workspace, decode_workspace_bytes
+
+    nh, nkv, hd, L = 32, 8, 128, 9000
+    kvd = nkv * hd
+    K, V = gen(21, (L, kvd)), gen(22, (L, kvd))
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    ws = decode_workspace(decode_workspace_bytes(1, L, L, nh, nkv, hd), cuda)
+    for i, n in enumerate([9000, 4500, 9000, 777, 8999, 9000]):
+        q = gen(23 + i, (nh * hd,), f16=False)
+        want = oracle.decode(q, kc[:n], vc[:n], n - 1, nh, nkv, hd)
+        got = attn_decode(torch.from_numpy(q).to(cuda), cache, n - 1, nh, workspace=ws).cpu().numpy()
+        err = rel_l2(got, want)
+        print(f"reuse call {i} keys={n}: rel_l2={err:.3e}")
         assert err <= TOL
 
 

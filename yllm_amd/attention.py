@@ -59,8 +59,8 @@ def round_up(x: int, m: int) -> int:
 class LayerKV:
     """One layer's KV cache of one sequence in HBM.
 
-    k: f16 [n_kv, kv_stride, head_dim] (row = position)
-    v: f16 [n_kv, head_dim, kv_stride] (transposed: column = position)
+    k: f16 [n_kv, kv_stride, head_dim]           (row = position)
+    v: f16 [n_kv, kv_stride // 32, head_dim, 32] (32-position tiles, d-major)
     """
 
     k: torch.Tensor
@@ -84,7 +84,7 @@ class LayerKV:
         stride = round_up(max(max_seq, 1), 64)
         alloc = torch.zeros if zero else torch.empty
         k = alloc((n_kv, stride, head_dim), dtype=torch.float16, device=device)
-        v = alloc((n_kv, head_dim, stride), dtype=torch.float16, device=device)
+        v = alloc((n_kv, stride // 32, head_dim, 32), dtype=torch.float16, device=device)
         return cls(k, v)
 
 
@@ -121,12 +121,17 @@ def decode_workspace_bytes(n_seq: int, max_len: int, total_len: int, n_heads: in
     return int(lib().yhip_attn_decode_workspace(n_seq, max_len, total_len, n_heads, n_kv, head_dim))
 
 
+def decode_workspace(nbytes: int, device: torch.device | str = "cuda") -> torch.Tensor:
+    """A decode workspace of at least nbytes (see yhip_attn_decode_workspace)."""
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
 def _workspace(nbytes: int, device: torch.device, ws: torch.Tensor | None) -> torch.Tensor | None:
     if nbytes == 0:
         return ws
     if ws is not None and ws.numel() * ws.element_size() >= nbytes:
         return ws
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return decode_workspace(nbytes, device)
 
 
 def attn_decode(q: torch.Tensor, cache: LayerKV, pos: int, n_heads: int, gate: torch.Tensor | None = None,

@@ -141,8 +141,6 @@ int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
     a.lens = lens;
     a.out = att_out;
     a.gate = gate;
-    a.part_o = reinterpret_cast<float*>(workspace);
-    a.part_ml = need ? a.part_o + (size_t)n_seq * n_heads * a.n_splits * head_dim : nullptr;
     a.n_seq = n_seq;
     a.n_heads = n_heads;
     a.n_kv = n_kv_heads;
@@ -152,6 +150,7 @@ int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
     a.out_stride = out_stride;
     a.gate_stride = gate_stride;
     a.c = (float)(1.4426950408889634 / sqrt((double)head_dim));
+    yhip::decode_bind_workspace(a, workspace);
     return done(yhip::launch_decode(a, (hipStream_t)stream), fn);
 }
 
@@ -177,8 +176,6 @@ int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
     a.len0 = len;
     a.out = att_out;
     a.gate = gate;
-    a.part_o = reinterpret_cast<float*>(workspace);
-    a.part_ml = need ? a.part_o + (size_t)n_heads * a.n_splits * head_dim : nullptr;
     a.n_seq = 1;
     a.n_heads = n_heads;
     a.n_kv = n_kv_heads;
@@ -188,6 +185,7 @@ int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
     a.out_stride = n_heads * head_dim;
     a.gate_stride = n_heads * head_dim;
     a.c = (float)(1.4426950408889634 / sqrt((double)head_dim));
+    yhip::decode_bind_workspace(a, workspace);
     return done(yhip::launch_decode(a, (hipStream_t)stream), fn);
 }
 

@@ -7,14 +7,16 @@
 // Work decomposition.  A workgroup (4 waves) owns one (sequence, kv head,
 // split of split_keys keys).  The whole GQA group of query heads that reads
 // that kv head is processed together, so every K/V byte is read from HBM
-// once.  The split's keys are walked in blocks of 32; wave w takes blocks
-// w, w+4, ... so the four waves stream neighbouring memory.
+// once.  The split's keys are walked in blocks of 32 -- one contiguous 8 KB
+// run of K and one of V for d = 128 -- and wave w takes blocks w, w+4, ...
+// with the next block's loads issued before the current block is computed
+// (register double buffering), so each wave keeps 16-32 KB in flight.
 //
 // MFMA formulation (v_mfma_f32_16x16x32_f16, per wave, per 32-key block):
 //   S^T[key][head] = K[key][:] . Q^T[:][head]       A = K rows, B = q (16 head
 //                                                    slots, group padded)
-//   O^T[d][head]  += V^T[d][key] . P^T[key][head]   A = V^T (the cache keeps V
-//                                                    transposed), B = P^T
+//   O^T[d][head]  += V^T[d][key] . P^T[key][head]   A = the V tile (stored
+//                                                    d-major), B = P^T
 // Lane l owns head slot l%16 in every accumulator, so the softmax statistics
 // of a head live in one column of lanes: the max needs two cross-lane steps,
 // the running sum none until the end.  K rows are loaded in the order
@@ -24,13 +26,17 @@
 // ~fp32 accuracy for fp32 queries; the kernel is HBM-bound and the extra
 // MFMAs are free.
 //
-// Splits write (max, sum, unnormalised O) partials in the log2 domain; a
-// merge kernel combines them per (sequence, head).  With a single split the
-// workgroup writes the final output directly.
+// Splits write (max, sum, unnormalised O) partials in the log2 domain to the
+// workspace; a merge kernel combines them per (sequence, head).  With a single
+// split the workgroup writes the final output directly.  (Merging inside the
+// split kernel, by the last workgroup to arrive, needs a device-scope release
+// per workgroup; on this part that writes back the whole L2 of the XCD each
+// time and was measured 4x slower than the separate merge.)
 #include "common.hpp"
 #include "internal.hpp"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace yhip {
 namespace {
@@ -44,6 +50,13 @@ __device__ inline f32x4 mfma16(const f16x8& a, const f16x8& b, const f32x4& c)
 }
 
 __device__ inline float sigmoid_ref(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+// one 32-key block of K and V as MFMA operands of one lane
+template <int D>
+struct Frag {
+    f16x8 k[2][D / 32];
+    f16x8 v[D / 16];
+};
 
 template <int D>
 __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(DecodeArgs a)
@@ -65,8 +78,8 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
     const uint32_t h1 = ((kvh + 1) * a.n_heads + a.n_kv - 1) / a.n_kv;
     const uint32_t G = h1 - h0;
 
-    const uint16_t* K = (a.kptrs ? a.kptrs[seq] : a.k0) + (size_t)kvh * a.kv_stride * D;
-    const uint16_t* VT = (a.vptrs ? a.vptrs[seq] : a.v0) + (size_t)kvh * D * a.kv_stride;
+    const uint16_t* K = (a.kptrs ? a.kptrs[seq] : a.k0) + k_index(kvh, 0, 0, D, a.kv_stride);
+    const uint16_t* Vt = (a.vptrs ? a.vptrs[seq] : a.v0) + v_index(kvh, 0, 0, D, a.kv_stride);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
@@ -95,30 +108,30 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
 #pragma unroll
     for (int b = 0; b < NB; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const uint32_t nblk = (kend - kbeg + kKeysPerBlock - 1) / kKeysPerBlock;
-    const int krow_in_block = 8 * (n >> 2) + (n & 3);  // + 4t for half t
-    for (uint32_t blk = wave; blk < nblk; blk += kWaves) {
-        const uint32_t key0 = kbeg + blk * kKeysPerBlock;
-        f16x8 kf[2][NC];
-        f16x8 vf[NB];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const uint16_t* kp = K + (size_t)(key0 + krow_in_block + 4 * t) * D + g * 8;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) kf[t][c] = *reinterpret_cast<const f16x8*>(kp + c * 32);
-        }
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-            vf[b] = *reinterpret_cast<const f16x8*>(VT + (size_t)(b * 16 + n) * a.kv_stride + key0 + g * 8);
+    const int krow = 8 * (n >> 2) + (n & 3);  // + 4t for half t
 
+    auto load = [&](Frag<D>& f, uint32_t key0) {
+        const uint16_t* kp = K + (size_t)(key0 + krow) * D + g * 8;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+                f.k[t][c] = *reinterpret_cast<const f16x8*>(kp + (size_t)4 * t * D + c * 32);
+        // the tile holding key0..key0+31, row d = b*16+n, positions 8g..8g+7
+        const uint16_t* vp = Vt + (size_t)(key0 / kVTile) * D * kVTile + n * kVTile + g * 8;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) f.v[b] = *reinterpret_cast<const f16x8*>(vp + b * 16 * kVTile);
+    };
+
+    auto compute = [&](Frag<D>& f, uint32_t key0) {
         f32x4 s[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                s[t] = mfma16(kf[t][c], qhi[c], s[t]);
-                s[t] = mfma16(kf[t][c], qlo[c], s[t]);
+                s[t] = mfma16(f.k[t][c], qhi[c], s[t]);
+                s[t] = mfma16(f.k[t][c], qlo[c], s[t]);
             }
         }
         // s[t][i] is head n, key key0 + 8g + 4t + i
@@ -156,13 +169,41 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
             for (int b = 0; b < NB; ++b)
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    if (key0 + 8 * g + j >= kend) vf[b][j] = (_Float16)0.0f;
+                    if (key0 + 8 * g + j >= kend) f.v[b][j] = (_Float16)0.0f;
         }
         f16x8 pf;
 #pragma unroll
         for (int j = 0; j < 8; ++j) pf[j] = (_Float16)p[j];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) o[b] = mfma16(vf[b], pf, o[b]);
+        for (int b = 0; b < NB; ++b) o[b] = mfma16(f.v[b], pf, o[b]);
+    };
+
+    const uint32_t nblk = (kend - kbeg + kKeysPerBlock - 1) / kKeysPerBlock;
+    uint32_t blk = wave;
+    if (blk < nblk) {
+        if constexpr (D <= 128) {
+            // two fragment sets in flight: load block i+4 while computing block i
+            Frag<D> fa, fb;
+            load(fa, kbeg + blk * kKeysPerBlock);
+            while (true) {
+                uint32_t nxt = blk + kWaves;
+                if (nxt < nblk) load(fb, kbeg + nxt * kKeysPerBlock);
+                compute(fa, kbeg + blk * kKeysPerBlock);
+                if (nxt >= nblk) break;
+                blk = nxt;
+                nxt = blk + kWaves;
+                if (nxt < nblk) load(fa, kbeg + nxt * kKeysPerBlock);
+                compute(fb, kbeg + blk * kKeysPerBlock);
+                if (nxt >= nblk) break;
+                blk = nxt;
+            }
+        } else {
+            Frag<D> f;
+            for (; blk < nblk; blk += kWaves) {
+                load(f, kbeg + blk * kKeysPerBlock);
+                compute(f, kbeg + blk * kKeysPerBlock);
+            }
+        }
     }
 
     // per-lane partial sums -> per head (the four lane groups hold one head)
@@ -178,6 +219,8 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
         for (int i = 0; i < 4; ++i) s_o[wave][n][b * 16 + 4 * g + i] = o[b][i];
     __syncthreads();
 
+    // combine the four waves; a single split writes the result directly
+    const size_t grp = (size_t)seq * a.n_kv + kvh;  // (sequence, kv head) group
     for (uint32_t idx = threadIdx.x; idx < G * D; idx += 256u) {
         const uint32_t hn = idx / D, d = idx - hn * D;
         float M = -INFINITY;
@@ -193,13 +236,13 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
                 O += s_o[w][hn][d] * sc;
             }
         }
-        const uint32_t h = h0 + hn;
         if (a.n_splits == 1) {
+            const uint32_t h = h0 + hn;
             float r = O / L;
             if (a.gate) r *= sigmoid_ref(a.gate[(size_t)seq * a.gate_stride + (size_t)h * D + d]);
             a.out[(size_t)seq * a.out_stride + (size_t)h * D + d] = r;
         } else {
-            const size_t slot = ((size_t)seq * a.n_heads + h) * a.n_splits + split;
+            const size_t slot = (grp * a.n_splits + split) * a.gmax + hn;
             a.part_o[slot * D + d] = O;
             if (d == 0) {
                 a.part_ml[slot * 2] = M;
@@ -209,25 +252,60 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
     }
 }
 
-// one block per (head, sequence), one thread per output dimension
+// One workgroup per (query head, sequence).  Wave 0 turns the split maxima
+// into weights 2^(m_s - M) and the total weight L; then every thread sums a
+// strided subset of splits for 4 output dimensions and the subsets are added
+// in LDS.
 template <int D>
-__global__ __launch_bounds__(D) void decode_merge_kernel(DecodeArgs a)
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
 {
-    const uint32_t h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
-    const uint32_t len = a.lens ? a.lens[seq] : a.len0;
-    const uint32_t ns = min((len + a.split_keys - 1) / a.split_keys, a.n_splits);
-    const size_t base = ((size_t)seq * a.n_heads + h) * a.n_splits;
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[(base + s) * 2]);
-    float L = 0.0f, O = 0.0f;
-    for (uint32_t s = 0; s < ns; ++s) {
-        const float sc = fast_exp2(a.part_ml[(base + s) * 2] - M);
-        L += a.part_ml[(base + s) * 2 + 1] * sc;
-        O += a.part_o[(base + s) * D + d] * sc;
+    constexpr uint32_t E4 = D / 4;       // float4 columns of one head
+    constexpr uint32_t NG = 256 / E4;    // split subsets summed in parallel
+    __shared__ float s_w[kMaxSplits];
+    __shared__ float s_L;
+    __shared__ f32x4 s_red[256];
+    const uint32_t h = blockIdx.x, seq = blockIdx.y, t = threadIdx.x;
+    const uint32_t kvh = h * a.n_kv / a.n_heads;
+    const uint32_t hn = h - (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
+    const uint32_t len = min(min(a.lens ? a.lens[seq] : a.len0, a.kv_stride), a.split_keys * a.n_splits);
+    const uint32_t ns = (len + a.split_keys - 1) / a.split_keys;
+    const size_t sbase = ((size_t)seq * a.n_kv + kvh) * a.n_splits;
+
+    if (t < 64) {
+        float mx = -INFINITY;
+        for (uint32_t s = t; s < ns; s += 64) mx = fmaxf(mx, a.part_ml[((sbase + s) * a.gmax + hn) * 2]);
+#pragma unroll
+        for (int k = 32; k >= 1; k >>= 1) mx = wave_max_xor(mx, k);
+        float sum = 0.0f;
+        for (uint32_t s = t; s < ns; s += 64) {
+            const size_t sl = ((sbase + s) * a.gmax + hn) * 2;
+            const float w = fast_exp2(a.part_ml[sl] - mx);
+            s_w[s] = w;
+            sum += a.part_ml[sl + 1] * w;
+        }
+#pragma unroll
+        for (int k = 32; k >= 1; k >>= 1) sum += __shfl_xor(sum, k, 64);
+        if (t == 0) s_L = sum;
     }
-    float r = ns ? O / L : 0.0f;
-    if (a.gate) r *= sigmoid_ref(a.gate[(size_t)seq * a.gate_stride + (size_t)h * D + d]);
-    a.out[(size_t)seq * a.out_stride + (size_t)h * D + d] = r;
+    __syncthreads();
+    const uint32_t e4 = t % E4, sg = t / E4;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s = sg; s < ns; s += NG)
+        acc += *reinterpret_cast<const f32x4*>(a.part_o + ((sbase + s) * a.gmax + hn) * D + 4 * e4) * s_w[s];
+    s_red[t] = acc;
+    __syncthreads();
+    if (t < E4) {
+#pragma unroll
+        for (uint32_t g2 = 1; g2 < NG; ++g2) acc += s_red[g2 * E4 + t];
+        f32x4 r = ns ? acc / s_L : f32x4{0.f, 0.f, 0.f, 0.f};
+        const uint32_t d = 4 * t;
+        if (a.gate) {
+            const float* gp = a.gate + (size_t)seq * a.gate_stride + (size_t)h * D + d;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] *= sigmoid_ref(gp[e]);
+        }
+        *reinterpret_cast<f32x4*>(a.out + (size_t)seq * a.out_stride + (size_t)h * D + d) = r;
+    }
 }
 
 template <int D>
@@ -235,25 +313,30 @@ hipError_t launch_decode_d(const DecodeArgs& a, hipStream_t st)
 {
     dim3 grid(a.n_splits, a.n_kv, a.n_seq);
     hipLaunchKernelGGL(decode_split_kernel<D>, grid, dim3(256), 0, st, a);
-    if (a.n_splits > 1) {
-        dim3 mg(a.n_heads, a.n_seq);
-        hipLaunchKernelGGL(decode_merge_kernel<D>, mg, dim3(D), 0, st, a);
-    }
+    if (a.n_splits > 1) hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.n_heads, a.n_seq), dim3(256), 0, st, a);
     return hipGetLastError();
 }
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 }  // namespace
 
 size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
                    uint32_t n_kv, uint32_t D, uint32_t* split_keys, uint32_t* n_splits)
 {
-    // aim at ~1024 workgroups (4 per CU on 256 CUs) streaming equal key counts
-    const uint64_t target_wg = 1024;
-    uint64_t work = total_len * (uint64_t)n_kv;
+    // About two resident workgroups per CU (256 CUs), each streaming an equal
+    // run of keys; YHIP_DECODE_WG overrides the target for tuning sweeps.
+    static const uint64_t target_wg = [] {
+        const char* e = getenv("YHIP_DECODE_WG");
+        const long v = e ? atol(e) : 0;
+        return (uint64_t)(v > 0 ? v : 512);
+    }();
+    const uint64_t work = total_len * (uint64_t)n_kv;
     uint64_t sk = (work + target_wg - 1) / target_wg;
+    sk = (sk + 127) / 128 * 128;  // whole 32-key blocks for each of the 4 waves
+    if (sk < 256) sk = 256;
+    if (sk < (max_len + kMaxSplits - 1) / kMaxSplits) sk = ((uint64_t)max_len + kMaxSplits - 1) / kMaxSplits;
     sk = (sk + 127) / 128 * 128;
-    if (sk < 128) sk = 128;
-    if (sk > 16384) sk = 16384;
     uint32_t ns;
     if (sk >= max_len) {
         sk = ((uint64_t)max_len + 31) / 32 * 32;
@@ -265,7 +348,23 @@ size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_
     *split_keys = (uint32_t)sk;
     *n_splits = ns;
     if (ns == 1) return 0;
-    return (size_t)n_seq * n_heads * ns * ((size_t)D + 2) * sizeof(float);
+    const size_t gmax = (n_heads + n_kv - 1) / n_kv;
+    const size_t groups = (size_t)n_seq * n_kv;
+    return align256(groups * ns * gmax * 2 * sizeof(float)) + groups * ns * gmax * D * sizeof(float);
+}
+
+void decode_bind_workspace(DecodeArgs& a, void* workspace)
+{
+    a.gmax = (a.n_heads + a.n_kv - 1) / a.n_kv;
+    if (a.n_splits == 1 || !workspace) {
+        a.part_ml = a.part_o = nullptr;
+        return;
+    }
+    const size_t groups = (size_t)a.n_seq * a.n_kv;
+    char* p = reinterpret_cast<char*>(workspace);
+    a.part_ml = reinterpret_cast<float*>(p);
+    p += align256(groups * a.n_splits * a.gmax * 2 * sizeof(float));
+    a.part_o = reinterpret_cast<float*>(p);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st)

@@ -139,9 +139,11 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
         for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, base + kk * 16, a.q_dtype);
     }
 
-    const uint16_t* Kg = a.kc + (size_t)kvh * a.kv_stride * D;
-    const uint16_t* Vg = a.vc + (size_t)kvh * D * a.kv_stride;
+    const uint16_t* Kg = a.kc + k_index(kvh, 0, 0, D, a.kv_stride);
+    const uint16_t* Vg = a.vc + v_index(kvh, 0, 0, D, a.kv_stride);
 
+    // A key tile is 64 rows of K (contiguous) and two consecutive 32-position
+    // V tiles [D][32] (contiguous).  V chunk c: tile c/(4D), row d, 8 positions.
     u32x4 kreg[CH], vreg[CH];
     auto load_tile = [&](uint32_t kt) {
         const uint32_t k0 = kt * BN;
@@ -151,11 +153,11 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
             const int row = c / KCH, col = c % KCH;
             kreg[i] = *reinterpret_cast<const u32x4*>(Kg + (size_t)(k0 + row) * D + col * 8);
         }
+        const uint16_t* vt = Vg + (size_t)(k0 / kVTile) * D * kVTile;
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
             const int c = tid + 256 * i;
-            const int row = c >> 3, col = c & 7;
-            vreg[i] = *reinterpret_cast<const u32x4*>(Vg + (size_t)row * a.kv_stride + k0 + col * 8);
+            vreg[i] = *reinterpret_cast<const u32x4*>(vt + (size_t)c * 8);
         }
     };
     auto store_tile = [&](uint32_t kt) {
@@ -170,18 +172,19 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
             const int c = tid + 256 * i;
-            const int row = c >> 3, col = c & 7;
+            const int t = c / (4 * D), r = c % (4 * D);
+            const int row = r >> 2, col = t * (int)kVTile + (r & 3) * 8;  // LDS column = key in tile
             u32x4 v = vreg[i];
             if (tail) {
                 // keys past kmax were never stored: their P is 0, their V must be finite
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t key = k0 + col * 8 + 2 * e;
+                    const uint32_t key = k0 + col + 2 * e;
                     if (key > kmax) v[e] = 0u;
                     else if (key + 1 > kmax) v[e] &= 0xffffu;
                 }
             }
-            *reinterpret_cast<u32x4*>(&Vl[row * VS + col * 8]) = v;
+            *reinterpret_cast<u32x4*>(&Vl[row * VS + col]) = v;
         }
     };
 

@@ -13,6 +13,27 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kF16 = 0, kF32 = 1, kBF16 = 2;
 
+// KV cache geometry (per sequence, per layer):
+//   K: [n_kv][kv_stride][D]                  row = position
+//   V: [n_kv][kv_stride/32][D][32]           32-position tiles, each stored
+//                                            transposed (d-major)
+// A block of 32 consecutive positions is then one contiguous run of 32*D
+// halfs in K and one in V, and a V tile is directly the A operand layout of
+// the P.V MFMA (a lane reads 8 consecutive positions of one dimension).
+constexpr uint32_t kVTile = 32;
+
+__host__ __device__ inline size_t k_index(uint32_t kvh, uint32_t pos, uint32_t d, uint32_t D,
+                                          uint32_t kv_stride)
+{
+    return ((size_t)kvh * kv_stride + pos) * D + d;
+}
+
+__host__ __device__ inline size_t v_index(uint32_t kvh, uint32_t pos, uint32_t d, uint32_t D,
+                                          uint32_t kv_stride)
+{
+    return (((size_t)kvh * (kv_stride / kVTile) + pos / kVTile) * D + d) * kVTile + (pos % kVTile);
+}
+
 // float -> f16 bits with the reference CPU rounding (platform.c:340-379):
 // the magnitude gets half an f16 ulp added and is truncated, so ties go away
 // from zero; f32 subnormals become signed zero; overflow becomes inf; NaN

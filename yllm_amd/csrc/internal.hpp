@@ -29,16 +29,19 @@ struct DecodeArgs {
     uint32_t len0;                  // key count when lens is null
     float* out;
     const float* gate;
-    float* part_o;                  // [n_seq][n_heads][n_splits][D]
-    float* part_ml;                 // [n_seq][n_heads][n_splits][2]
+    float* part_ml;                 // [n_seq][n_kv][n_splits][gmax][2]
+    float* part_o;                  // [n_seq][n_kv][n_splits][gmax][D]
     uint32_t n_seq, n_heads, n_kv, D, kv_stride;
     uint32_t q_stride, out_stride, gate_stride;
-    uint32_t split_keys, n_splits;
+    uint32_t split_keys, n_splits, gmax;
     float c;                        // log2(e)/sqrt(D)
 };
-// split plan for the shapes; returns workspace bytes
+constexpr uint32_t kMaxSplits = 256;
+// Split plan for the shapes; returns the workspace bytes (0 without splits).
 size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
                    uint32_t n_kv, uint32_t D, uint32_t* split_keys, uint32_t* n_splits);
+// carve the workspace into part_ml / part_o for a plan
+void decode_bind_workspace(DecodeArgs& a, void* workspace);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
 
 // ---- attn_prefill.hip ----

@@ -1,9 +1,9 @@
 // kv_store.hip -- writes K/V rows into the head-major HBM cache and converts
 // between the engine layout and the head-major layout.
 //
-// K cache: [n_kv][kv_stride][D] f16 bits; V cache: [n_kv][D][kv_stride].
-// Rounding is the reference CPU f32->f16 (platform.c:340-379), so a cache
-// filled here is bit-identical to the engine's (engine.c:1068-1072).
+// Geometry: common.hpp (K rows per head; V in 32-position tiles stored
+// d-major).  Rounding is the reference CPU f32->f16 (platform.c:340-379), so
+// a cache filled here holds the same bits as the engine's (engine.c:1068-1072).
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -31,16 +31,16 @@ __global__ __launch_bounds__(256) void k_store_kernel(uint16_t* __restrict__ kc,
     if (idx >= (uint64_t)B * kv_dim) return;
     const uint32_t b = (uint32_t)(idx / kv_dim), j = (uint32_t)(idx - (uint64_t)b * kv_dim);
     const uint32_t h = j / D, d = j - h * D;
-    kc[((size_t)h * kv_stride + pos_start + b) * D + d] = to_cache_bits(k, (size_t)b * kv_dim + j, dt);
+    kc[k_index(h, pos_start + b, d, D, kv_stride)] = to_cache_bits(k, (size_t)b * kv_dim + j, dt);
 }
 
-// V rows become columns of V^T.  A 64(pos) x 64(dim) tile is staged in LDS so
-// that reads walk the source rows and writes walk the destination columns.
-__global__ __launch_bounds__(256) void v_store_t_kernel(uint16_t* __restrict__ vc,
-                                                        const void* __restrict__ v, uint32_t dt,
-                                                        uint32_t pos_start, uint32_t B,
-                                                        uint32_t n_kv, uint32_t D,
-                                                        uint32_t kv_stride)
+// V rows go to d-major tiles.  A 64(pos) x 64(dim) block is staged in LDS so
+// that reads walk source rows and writes walk positions inside a tile.
+__global__ __launch_bounds__(256) void v_store_kernel(uint16_t* __restrict__ vc,
+                                                      const void* __restrict__ v, uint32_t dt,
+                                                      uint32_t pos_start, uint32_t B,
+                                                      uint32_t n_kv, uint32_t D,
+                                                      uint32_t kv_stride)
 {
     __shared__ uint16_t tile[64][66];
     const uint32_t kv_dim = n_kv * D;
@@ -55,40 +55,16 @@ __global__ __launch_bounds__(256) void v_store_t_kernel(uint16_t* __restrict__ v
         const uint32_t j = j0 + r, b = b0 + tx;
         if (b < B && j < kv_dim) {
             const uint32_t h = j / D, d = j - h * D;
-            vc[((size_t)h * D + d) * kv_stride + pos_start + b] = tile[tx][r];
+            vc[v_index(h, pos_start + b, d, D, kv_stride)] = tile[tx][r];
         }
     }
 }
 
-// engine V rows -> V^T (bits copied)
-__global__ __launch_bounds__(256) void v_engine_to_t_kernel(uint16_t* __restrict__ vc,
-                                                            const uint16_t* __restrict__ ev,
-                                                            uint32_t rows, uint32_t n_kv,
-                                                            uint32_t D, uint32_t kv_stride)
-{
-    __shared__ uint16_t tile[64][66];
-    const uint32_t kv_dim = n_kv * D;
-    const uint32_t j0 = blockIdx.x * 64u, b0 = blockIdx.y * 64u;
-    const uint32_t tx = threadIdx.x & 63u, ty = threadIdx.x >> 6;
-    for (uint32_t r = ty; r < 64u; r += 4u) {
-        const uint32_t b = b0 + r, j = j0 + tx;
-        if (b < rows && j < kv_dim) tile[r][tx] = ev[(size_t)b * kv_dim + j];
-    }
-    __syncthreads();
-    for (uint32_t r = ty; r < 64u; r += 4u) {
-        const uint32_t j = j0 + r, b = b0 + tx;
-        if (b < rows && j < kv_dim) {
-            const uint32_t h = j / D, d = j - h * D;
-            vc[((size_t)h * D + d) * kv_stride + b] = tile[tx][r];
-        }
-    }
-}
-
-// V^T -> engine V rows
-__global__ __launch_bounds__(256) void v_t_to_engine_kernel(uint16_t* __restrict__ ev,
-                                                            const uint16_t* __restrict__ vc,
-                                                            uint32_t rows, uint32_t n_kv,
-                                                            uint32_t D, uint32_t kv_stride)
+// V tiles -> engine V rows (bits copied)
+__global__ __launch_bounds__(256) void v_to_engine_kernel(uint16_t* __restrict__ ev,
+                                                          const uint16_t* __restrict__ vc,
+                                                          uint32_t rows, uint32_t n_kv, uint32_t D,
+                                                          uint32_t kv_stride)
 {
     __shared__ uint16_t tile[64][66];
     const uint32_t kv_dim = n_kv * D;
@@ -98,7 +74,7 @@ __global__ __launch_bounds__(256) void v_t_to_engine_kernel(uint16_t* __restrict
         const uint32_t j = j0 + r, b = b0 + tx;
         if (b < rows && j < kv_dim) {
             const uint32_t h = j / D, d = j - h * D;
-            tile[r][tx] = vc[((size_t)h * D + d) * kv_stride + b];
+            tile[r][tx] = vc[v_index(h, b, d, D, kv_stride)];
         }
     }
     __syncthreads();
@@ -119,7 +95,7 @@ __global__ __launch_bounds__(256) void k_copy_kernel(uint16_t* __restrict__ kc,
     if (idx >= (uint64_t)rows * kv_dim) return;
     const uint32_t b = (uint32_t)(idx / kv_dim), j = (uint32_t)(idx - (uint64_t)b * kv_dim);
     const uint32_t h = j / D, d = j - h * D;
-    const size_t hm = ((size_t)h * kv_stride + b) * D + d;
+    const size_t hm = k_index(h, b, d, D, kv_stride);
     const size_t en = (size_t)b * kv_dim + j;
     if (dir == 0) kc[hm] = ek[en];
     else ek[en] = kc[hm];
@@ -136,7 +112,7 @@ hipError_t launch_kv_store(uint16_t* kc, uint16_t* vc, const void* k, const void
     hipLaunchKernelGGL(k_store_kernel, gk, dim3(256), 0, st, kc, k, dt, pos_start, B, n_kv, D,
                        kv_stride);
     dim3 gv((kv_dim + 63u) / 64u, (B + 63u) / 64u);
-    hipLaunchKernelGGL(v_store_t_kernel, gv, dim3(256), 0, st, vc, v, dt, pos_start, B, n_kv, D,
+    hipLaunchKernelGGL(v_store_kernel, gv, dim3(256), 0, st, vc, v, dt, pos_start, B, n_kv, D,
                        kv_stride);
     return hipGetLastError();
 }
@@ -149,8 +125,10 @@ hipError_t launch_kv_from_engine(uint16_t* kc, uint16_t* vc, const uint16_t* ek,
     dim3 gk((uint32_t)(((uint64_t)rows * kv_dim + 255u) / 256u));
     hipLaunchKernelGGL(k_copy_kernel, gk, dim3(256), 0, st, kc, const_cast<uint16_t*>(ek), rows, n_kv,
                        D, kv_stride, 0);
+    // f16 bits through the same tiler as the store (f16 sources are copied)
     dim3 gv((kv_dim + 63u) / 64u, (rows + 63u) / 64u);
-    hipLaunchKernelGGL(v_engine_to_t_kernel, gv, dim3(256), 0, st, vc, ev, rows, n_kv, D, kv_stride);
+    hipLaunchKernelGGL(v_store_kernel, gv, dim3(256), 0, st, vc, (const void*)ev, kF16, 0u, rows, n_kv,
+                       D, kv_stride);
     return hipGetLastError();
 }
 
@@ -163,7 +141,7 @@ hipError_t launch_kv_to_engine(uint16_t* ek, uint16_t* ev, const uint16_t* kc, c
     hipLaunchKernelGGL(k_copy_kernel, gk, dim3(256), 0, st, const_cast<uint16_t*>(kc), ek, rows, n_kv,
                        D, kv_stride, 1);
     dim3 gv((kv_dim + 63u) / 64u, (rows + 63u) / 64u);
-    hipLaunchKernelGGL(v_t_to_engine_kernel, gv, dim3(256), 0, st, ev, vc, rows, n_kv, D, kv_stride);
+    hipLaunchKernelGGL(v_to_engine_kernel, gv, dim3(256), 0, st, ev, vc, rows, n_kv, D, kv_stride);
     return hipGetLastError();
 }
 
