@@ -208,8 +208,8 @@ def run_decode_batch(nh: int, nkv: int, hd: int, n_seq: int, steps: int, warmup:
     base_k = torch.from_numpy(synth(seed, 32768 * kvd).reshape(32768, kvd)).to(dev).half()
     base_v = torch.from_numpy(synth(seed, 32768 * kvd, 32768 * kvd).reshape(32768, kvd)).to(dev).half()
     caches = []
-    for L in lens:
-        c = LayerKV.empty(nkv, hd, int(L), device=dev, zero=False)
+    for L in lens:  # one engine-style cache of capacity 32768 per sequence
+        c = LayerKV.empty(nkv, hd, 32768, device=dev, zero=False)
         kv_store(c, base_k[: int(L)], base_v[: int(L)], 0)
         caches.append(c)
     batch = DecodeBatch(caches)

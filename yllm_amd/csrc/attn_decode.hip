@@ -4,13 +4,16 @@
 // 0..pos, scores scaled by 1/sqrt(d), softmax, weighted sum of V), optionally
 // followed by the qwen35 sigmoid gate (engine.c:959-960).
 //
-// Work decomposition.  A workgroup (4 waves) owns one (sequence, kv head,
+// Work decomposition.  A workgroup (4 waves; two per CU for d <= 128) owns
+// one (sequence, kv head,
 // split of split_keys keys).  The whole GQA group of query heads that reads
 // that kv head is processed together, so every K/V byte is read from HBM
 // once.  The split's keys are walked in blocks of 32 -- one contiguous 8 KB
-// run of K and one of V for d = 128 -- and wave w takes blocks w, w+4, ...
-// with the next block's loads issued before the current block is computed
-// (register double buffering), so each wave keeps 16-32 KB in flight.
+// run of K and one of V for d = 128 -- and wave w takes blocks w, w+W, ...
+// with the next block's loads in flight while the current one is computed
+// (two register fragment sets for d <= 128): two waves per SIMD, each with
+// up to 32 KB outstanding.  Measured on MI355X at 32k keys: this beats a
+// 4-deep ring at one wave per SIMD and 8-wave workgroups.
 //
 // MFMA formulation (v_mfma_f32_16x16x32_f16, per wave, per 32-key block):
 //   S^T[key][head] = K[key][:] . Q^T[:][head]       A = K rows, B = q (16 head
@@ -41,8 +44,12 @@
 namespace yhip {
 namespace {
 
-constexpr int kWaves = 4;
 constexpr int kKeysPerBlock = 32;
+
+// waves per workgroup, register fragment sets per wave, workgroups per CU
+template <int D> constexpr int waves_of() { return 4; }
+template <int D> constexpr int nbuf_of() { return D <= 128 ? 2 : 1; }
+template <int D> constexpr int wg_per_cu() { return D <= 128 ? 2 : 1; }
 
 __device__ inline f32x4 mfma16(const f16x8& a, const f16x8& b, const f32x4& c)
 {
@@ -59,8 +66,10 @@ struct Frag {
 };
 
 template <int D>
-__global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(DecodeArgs a)
+__global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_split_kernel(DecodeArgs a)
 {
+    constexpr int kWaves = waves_of<D>();
+    constexpr int kThreads = 64 * kWaves;
     constexpr int NC = D / 32;  // 32-wide d chunks of the QK contraction
     constexpr int NB = D / 16;  // 16-row d blocks of the PV output
     __shared__ float s_o[kWaves][16][D + 4];
@@ -84,25 +93,6 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
 
-    // B operand of the score MFMA: head slot n, dims c*32 + 8g .. +7
-    f16x8 qhi[NC], qlo[NC];
-    {
-        const bool valid = (uint32_t)n < G;
-        const float* qrow = a.q + (size_t)seq * a.q_stride + (size_t)(h0 + (valid ? n : 0)) * D;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const f32x4 lo4 = *reinterpret_cast<const f32x4*>(qrow + c * 32 + g * 8);
-            const f32x4 hi4 = *reinterpret_cast<const f32x4*>(qrow + c * 32 + g * 8 + 4);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float x = valid ? (j < 4 ? lo4[j] : hi4[j - 4]) : 0.0f;
-                const _Float16 h = (_Float16)x;
-                qhi[c][j] = h;
-                qlo[c][j] = (_Float16)(x - (float)h);
-            }
-        }
-    }
-
     float m = -INFINITY, l = 0.0f;
     f32x4 o[NB];
 #pragma unroll
@@ -122,6 +112,36 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
 #pragma unroll
         for (int b = 0; b < NB; ++b) f.v[b] = *reinterpret_cast<const f16x8*>(vp + b * 16 * kVTile);
     };
+
+    // Up to NBUF blocks of this wave in flight: the first ones are issued
+    // before q is read so the two latencies overlap.
+    constexpr int NBUF = nbuf_of<D>();
+    Frag<D> f[NBUF];
+    const uint32_t nblk = (kend - kbeg + kKeysPerBlock - 1) / kKeysPerBlock;
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i) {
+        const uint32_t b = wave + i * kWaves;
+        if (b < nblk) load(f[i], kbeg + b * kKeysPerBlock);
+    }
+
+    // B operand of the score MFMA: head slot n, dims c*32 + 8g .. +7
+    f16x8 qhi[NC], qlo[NC];
+    {
+        const bool valid = (uint32_t)n < G;
+        const float* qrow = a.q + (size_t)seq * a.q_stride + (size_t)(h0 + (valid ? n : 0)) * D;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const f32x4 lo4 = *reinterpret_cast<const f32x4*>(qrow + c * 32 + g * 8);
+            const f32x4 hi4 = *reinterpret_cast<const f32x4*>(qrow + c * 32 + g * 8 + 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = valid ? (j < 4 ? lo4[j] : hi4[j - 4]) : 0.0f;
+                const _Float16 h = (_Float16)x;
+                qhi[c][j] = h;
+                qlo[c][j] = (_Float16)(x - (float)h);
+            }
+        }
+    }
 
     auto compute = [&](Frag<D>& f, uint32_t key0) {
         f32x4 s[2];
@@ -178,32 +198,22 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
         for (int b = 0; b < NB; ++b) o[b] = mfma16(f.v[b], pf, o[b]);
     };
 
-    const uint32_t nblk = (kend - kbeg + kKeysPerBlock - 1) / kKeysPerBlock;
-    uint32_t blk = wave;
-    if (blk < nblk) {
-        if constexpr (D <= 128) {
-            // two fragment sets in flight: load block i+4 while computing block i
-            Frag<D> fa, fb;
-            load(fa, kbeg + blk * kKeysPerBlock);
-            while (true) {
-                uint32_t nxt = blk + kWaves;
-                if (nxt < nblk) load(fb, kbeg + nxt * kKeysPerBlock);
-                compute(fa, kbeg + blk * kKeysPerBlock);
-                if (nxt >= nblk) break;
-                blk = nxt;
-                nxt = blk + kWaves;
-                if (nxt < nblk) load(fa, kbeg + nxt * kKeysPerBlock);
-                compute(fb, kbeg + blk * kKeysPerBlock);
-                if (nxt >= nblk) break;
-                blk = nxt;
+    // ring of NBUF fragment sets: compute slot i, then refill it with the
+    // block NBUF*kWaves ahead
+    for (uint32_t base = 0;; base += NBUF) {
+        bool stop = false;
+#pragma unroll
+        for (int i = 0; i < NBUF; ++i) {
+            const uint32_t b = wave + (base + i) * kWaves;
+            if (b >= nblk) {
+                stop = true;
+                break;
             }
-        } else {
-            Frag<D> f;
-            for (; blk < nblk; blk += kWaves) {
-                load(f, kbeg + blk * kKeysPerBlock);
-                compute(f, kbeg + blk * kKeysPerBlock);
-            }
+            compute(f[i], kbeg + b * kKeysPerBlock);
+            const uint32_t nb = b + NBUF * kWaves;
+            if (nb < nblk) load(f[i], kbeg + nb * kKeysPerBlock);
         }
+        if (stop) break;
     }
 
     // per-lane partial sums -> per head (the four lane groups hold one head)
@@ -221,7 +231,7 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
 
     // combine the four waves; a single split writes the result directly
     const size_t grp = (size_t)seq * a.n_kv + kvh;  // (sequence, kv head) group
-    for (uint32_t idx = threadIdx.x; idx < G * D; idx += 256u) {
+    for (uint32_t idx = threadIdx.x; idx < G * D; idx += kThreads) {
         const uint32_t hn = idx / D, d = idx - hn * D;
         float M = -INFINITY;
 #pragma unroll
@@ -252,52 +262,58 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void decode_split_kernel(D
     }
 }
 
-// One workgroup per (query head, sequence).  Wave 0 turns the split maxima
-// into weights 2^(m_s - M) and the total weight L; then every thread sums a
-// strided subset of splits for 4 output dimensions and the subsets are added
-// in LDS.
+// One workgroup per (query head, sequence).  Thread t owns 4 output
+// dimensions and a strided subset of the splits; it loads the subset's
+// (max, sum) pairs and partial outputs together (one memory round trip),
+// combines them against its own running max, and the subsets are then
+// combined in LDS with one more rescale.
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
 {
     constexpr uint32_t E4 = D / 4;       // float4 columns of one head
-    constexpr uint32_t NG = 256 / E4;    // split subsets summed in parallel
-    __shared__ float s_w[kMaxSplits];
-    __shared__ float s_L;
-    __shared__ f32x4 s_red[256];
+    constexpr uint32_t NG = 256 / E4;    // split subsets combined in parallel
+    __shared__ f32x4 s_o[256];
+    __shared__ float s_m[256], s_l[256];
     const uint32_t h = blockIdx.x, seq = blockIdx.y, t = threadIdx.x;
     const uint32_t kvh = h * a.n_kv / a.n_heads;
     const uint32_t hn = h - (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
     const uint32_t len = min(min(a.lens ? a.lens[seq] : a.len0, a.kv_stride), a.split_keys * a.n_splits);
     const uint32_t ns = (len + a.split_keys - 1) / a.split_keys;
     const size_t sbase = ((size_t)seq * a.n_kv + kvh) * a.n_splits;
-
-    if (t < 64) {
-        float mx = -INFINITY;
-        for (uint32_t s = t; s < ns; s += 64) mx = fmaxf(mx, a.part_ml[((sbase + s) * a.gmax + hn) * 2]);
-#pragma unroll
-        for (int k = 32; k >= 1; k >>= 1) mx = wave_max_xor(mx, k);
-        float sum = 0.0f;
-        for (uint32_t s = t; s < ns; s += 64) {
-            const size_t sl = ((sbase + s) * a.gmax + hn) * 2;
-            const float w = fast_exp2(a.part_ml[sl] - mx);
-            s_w[s] = w;
-            sum += a.part_ml[sl + 1] * w;
-        }
-#pragma unroll
-        for (int k = 32; k >= 1; k >>= 1) sum += __shfl_xor(sum, k, 64);
-        if (t == 0) s_L = sum;
-    }
-    __syncthreads();
     const uint32_t e4 = t % E4, sg = t / E4;
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t s = sg; s < ns; s += NG)
-        acc += *reinterpret_cast<const f32x4*>(a.part_o + ((sbase + s) * a.gmax + hn) * D + 4 * e4) * s_w[s];
-    s_red[t] = acc;
+
+    float M = -INFINITY, L = 0.0f;
+    f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s = sg; s < ns; s += NG) {
+        const size_t slot = (sbase + s) * a.gmax + hn;
+        const float ms = a.part_ml[slot * 2], ls = a.part_ml[slot * 2 + 1];
+        const f32x4 os = *reinterpret_cast<const f32x4*>(a.part_o + slot * D + 4 * e4);
+        const float mn = fmaxf(M, ms);
+        const float c_old = fast_exp2(M - mn), c_new = fast_exp2(ms - mn);
+        L = L * c_old + ls * c_new;
+        O = O * c_old + os * c_new;
+        M = mn;
+    }
+    s_o[t] = O;
+    s_m[t] = M;
+    s_l[t] = L;
     __syncthreads();
     if (t < E4) {
+        float Mt = -INFINITY;
 #pragma unroll
-        for (uint32_t g2 = 1; g2 < NG; ++g2) acc += s_red[g2 * E4 + t];
-        f32x4 r = ns ? acc / s_L : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t g2 = 0; g2 < NG; ++g2) Mt = fmaxf(Mt, s_m[g2 * E4 + t]);
+        float Lt = 0.0f;
+        f32x4 Ot = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t g2 = 0; g2 < NG; ++g2) {
+            const float mg = s_m[g2 * E4 + t];
+            if (mg != -INFINITY) {
+                const float c = fast_exp2(mg - Mt);
+                Lt += s_l[g2 * E4 + t] * c;
+                Ot += s_o[g2 * E4 + t] * c;
+            }
+        }
+        f32x4 r = ns ? Ot / Lt : f32x4{0.f, 0.f, 0.f, 0.f};
         const uint32_t d = 4 * t;
         if (a.gate) {
             const float* gp = a.gate + (size_t)seq * a.gate_stride + (size_t)h * D + d;
@@ -312,7 +328,7 @@ template <int D>
 hipError_t launch_decode_d(const DecodeArgs& a, hipStream_t st)
 {
     dim3 grid(a.n_splits, a.n_kv, a.n_seq);
-    hipLaunchKernelGGL(decode_split_kernel<D>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL(decode_split_kernel<D>, grid, dim3(64 * waves_of<D>()), 0, st, a);
     if (a.n_splits > 1) hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.n_heads, a.n_seq), dim3(256), 0, st, a);
     return hipGetLastError();
 }
@@ -324,19 +340,19 @@ size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
                    uint32_t n_kv, uint32_t D, uint32_t* split_keys, uint32_t* n_splits)
 {
-    // About two resident workgroups per CU (256 CUs), each streaming an equal
+    // About one resident workgroup per CU (256 CUs), each streaming an equal
     // run of keys; YHIP_DECODE_WG overrides the target for tuning sweeps.
     static const uint64_t target_wg = [] {
         const char* e = getenv("YHIP_DECODE_WG");
         const long v = e ? atol(e) : 0;
-        return (uint64_t)(v > 0 ? v : 512);
+        return (uint64_t)(v > 0 ? v : 256);
     }();
     const uint64_t work = total_len * (uint64_t)n_kv;
     uint64_t sk = (work + target_wg - 1) / target_wg;
-    sk = (sk + 127) / 128 * 128;  // whole 32-key blocks for each of the 4 waves
+    sk = (sk + 255) / 256 * 256;  // whole 32-key blocks for each of up to 8 waves
     if (sk < 256) sk = 256;
     if (sk < (max_len + kMaxSplits - 1) / kMaxSplits) sk = ((uint64_t)max_len + kMaxSplits - 1) / kMaxSplits;
-    sk = (sk + 127) / 128 * 128;
+    sk = (sk + 255) / 256 * 256;
     uint32_t ns;
     if (sk >= max_len) {
         sk = ((uint64_t)max_len + 31) / 32 * 32;
