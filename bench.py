@@ -42,6 +42,7 @@ HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
 MFMA_F16_PEAK = 2.5e15   # FLOP/s, dense f16/bf16 MFMA
 METRIC = "attn decode GB/s (% HBM peak); prefill attn TFLOP/s (% MFMA peak)"
 SEED = 0x5EED0000
+EAGER = False  # --eager: launch each step from the host (for counter collection)
 
 
 def synth(seed: int, n: int, first: int = 0) -> np.ndarray:
@@ -67,6 +68,15 @@ def time_steps(fn, steps: int, warmup: int, out=None):
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    if EAGER:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            fn(warmup + i)
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / steps
+        return ms, ms
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(steps):
@@ -319,7 +329,11 @@ def main() -> int:
                     choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k secondary line")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every step from the host instead of replaying a HIP graph (profiling)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -352,7 +366,8 @@ def main() -> int:
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "f16 MFMA, f32 accumulate/softmax", "data": "synthetic",
             "config": res["config"], "tokens_per_s": res["tokens_per_s"], "roofline": res["roofline"],
-            "timing": "K steps captured in one HIP graph, replay timed with HIP events on its stream",
+            "timing": ("K eager launches" if EAGER else "K steps captured in one HIP graph") +
+                      ", timed with HIP events on the launch stream",
             "measured_copy_GBps": copy_ceiling_gbps()}
     if "cpu_baseline" in res:
         line["cpu_baseline"] = res["cpu_baseline"]

@@ -216,6 +216,11 @@ def test_decode_long_context_full_size(cuda, oracle):
     (32, 8, 128, 5, 64, torch.bfloat16, torch.bfloat16),
     (6, 4, 64, 0, 1, torch.float32, torch.float32),
     (16, 2, 256, 30, 200, torch.bfloat16, torch.float32),
+    # a query block with idle waves and three key tiles: the idle waves must
+    # not restage tile 0 while the busy one still scores it
+    (2, 1, 256, 0, 129, torch.float32, torch.float32),
+    (4, 1, 128, 0, 129, torch.float16, torch.float32),
+    (2, 2, 64, 0, 193, torch.float32, torch.float32),
 ])
 def test_prefill_parity(cuda, oracle, nh, nkv, hd, ps, B, qdt, odt):
     from yllm_amd.attention import attn_prefill

@@ -104,13 +104,19 @@ template <int D>
 __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(PrefillArgs a)
 {
     constexpr int KS = D + 8;     // K tile row stride (halfs), 16 B pad
-    constexpr int VS = BN + 8;    // V^T tile row stride (halfs)
+    constexpr int VS = BN + 8;    // V tile row stride (halfs)
     constexpr int NKK = D / 16;   // k-chunks of the score MFMA
     constexpr int NDB = D / 32;   // d-blocks of the output MFMA
     constexpr int CH = D / 32;    // 16-byte chunks per thread per tile (K and V each)
     constexpr int KCH = D / 8;    // 16-byte chunks per K row
-    __shared__ _Float16 Kl[BN * KS];
-    __shared__ _Float16 Vl[D * VS];
+    constexpr float kSlack = 8.0f;
+    // K and V tiles are double buffered separately: K is staged two tiles
+    // ahead (the score MFMAs of tile kt+1 run during the softmax of tile kt),
+    // V one tile ahead; every buffer is rewritten only after the barrier that
+    // ends its last reader's tile, so one barrier per tile suffices (plus one
+    // in the first tile, after the prologue's scores of tile 0).
+    __shared__ _Float16 Kl[2][BN * KS];
+    __shared__ _Float16 Vl[2][D * VS];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, hh = lane >> 5;
@@ -131,6 +137,8 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
     const uint32_t wpos_last = a.pos_start + min(wq0 + 31, a.B - 1);
     const uint32_t my_pos = a.pos_start + wq0 + r32;
     const uint32_t my_q = min(wq0 + r32, a.B - 1);
+    // tiles this wave computes: 0 .. wtiles-1
+    const uint32_t wtiles = wave_active ? wpos_last / BN + 1 : 0;
 
     f16x8 qf[NKK];
     {
@@ -139,52 +147,57 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
         for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, base + kk * 16, a.q_dtype);
     }
 
-    const uint16_t* Kg = a.kc + k_index(kvh, 0, 0, D, a.kv_stride);
-    const uint16_t* Vg = a.vc + v_index(kvh, 0, 0, D, a.kv_stride);
-
-    // A key tile is 64 rows of K (contiguous) and two consecutive 32-position
-    // V tiles [D][32] (contiguous).  V chunk c: tile c/(4D), row d, 8 positions.
+    // Buffer resources over this kv head's K rows and V tiles (reads past the
+    // cache return zeros).  Per-thread offsets are fixed; a tile adds the
+    // scalar kt*BN*D*2 bytes (the same for K rows and 32-position V tiles).
+    const uint32_t head_bytes = a.kv_stride * D * 2;
+    const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.kc + k_index(kvh, 0, 0, D, a.kv_stride)), 0, head_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.vc + v_index(kvh, 0, 0, D, a.kv_stride)), 0, head_bytes, 0x00020000);
+    int kgo[CH], klo[CH], vlo[CH], vkey[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int c = tid + 256 * i;
+        const int row = c / KCH, col = c % KCH;
+        kgo[i] = (row * D + col * 8) * 2;
+        klo[i] = lds_row_of_key(row) * KS + col * 8;
+        // V chunk c: 32-position tile c/(4D), row d, 8 positions
+        const int t = c / (4 * D), r = c % (4 * D);
+        vkey[i] = t * (int)kVTile + (r & 3) * 8;  // key of the chunk within the 64-key tile
+        vlo[i] = (r >> 2) * VS + vkey[i];
+    }
     u32x4 kreg[CH], vreg[CH];
-    auto load_tile = [&](uint32_t kt) {
-        const uint32_t k0 = kt * BN;
+    auto load_k = [&](uint32_t kt) {
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int c = tid + 256 * i;
-            const int row = c / KCH, col = c % KCH;
-            kreg[i] = *reinterpret_cast<const u32x4*>(Kg + (size_t)(k0 + row) * D + col * 8);
-        }
-        const uint16_t* vt = Vg + (size_t)(k0 / kVTile) * D * kVTile;
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int c = tid + 256 * i;
-            vreg[i] = *reinterpret_cast<const u32x4*>(vt + (size_t)c * 8);
-        }
+        for (int i = 0; i < CH; ++i)
+            kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rK, kgo[i], kt * BN * D * 2, 0));
     };
-    auto store_tile = [&](uint32_t kt) {
-        const uint32_t k0 = kt * BN;
+    auto load_v = [&](uint32_t kt) {
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int c = tid + 256 * i;
-            const int row = c / KCH, col = c % KCH;
-            *reinterpret_cast<u32x4*>(&Kl[lds_row_of_key(row) * KS + col * 8]) = kreg[i];
-        }
+        for (int i = 0; i < CH; ++i)
+            vreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rV, tid * 16 + i * 4096, kt * BN * D * 2, 0));
+    };
+    auto store_k = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) *reinterpret_cast<u32x4*>(&Kl[buf][klo[i]]) = kreg[i];
+    };
+    auto store_v = [&](int buf, uint32_t kt) {
+        const uint32_t k0 = kt * BN;
         const bool tail = k0 + BN - 1 > kmax;
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-            const int c = tid + 256 * i;
-            const int t = c / (4 * D), r = c % (4 * D);
-            const int row = r >> 2, col = t * (int)kVTile + (r & 3) * 8;  // LDS column = key in tile
             u32x4 v = vreg[i];
             if (tail) {
                 // keys past kmax were never stored: their P is 0, their V must be finite
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t key = k0 + col + 2 * e;
+                    const uint32_t key = k0 + vkey[i] + 2 * e;
                     if (key > kmax) v[e] = 0u;
                     else if (key + 1 > kmax) v[e] &= 0xffffu;
                 }
             }
-            *reinterpret_cast<u32x4*>(&Vl[row * VS + col]) = v;
+            *reinterpret_cast<u32x4*>(&Vl[buf][vlo[i]]) = v;
         }
     };
 
@@ -195,74 +208,139 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
 
-    load_tile(0);
-    for (uint32_t kt = 0; kt < ntiles; ++kt) {
-        __syncthreads();
-        store_tile(kt);
-        __syncthreads();
-        if (kt + 1 < ntiles) load_tile(kt + 1);
-
-        const uint32_t k0 = kt * BN;
-        if (!wave_active || k0 > wpos_last) continue;
-        const bool half1 = k0 + 32 <= wpos_last;
-
-        f32x16 s[2];
+    // scores of tile kt into S (both 32-key halves)
+    auto qk = [&](f32x16 (&S)[2], uint32_t kt) {
+        const _Float16* kr = &Kl[kt & 1][r32 * KS + hh * 8];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[j][i] = 0.0f;
-            if (j == 1 && !half1) break;
-            const _Float16* kr = &Kl[(32 * j + r32) * KS + hh * 8];
-#pragma unroll
-            for (int kk = 0; kk < NKK; ++kk)
-                s[j] = mfma32(*reinterpret_cast<const f16x8*>(kr + kk * 16), qf[kk], s[j]);
-        }
-
-        float x[32];
+            for (int j = 0; j < 2; ++j) {
+                const f16x8 kf = *reinterpret_cast<const f16x8*>(kr + 32 * j * KS + kk * 16);
+                S[j] = kk == 0 ? mfma32(kf, qf[0], f32x16{}) : mfma32(kf, qf[kk], S[j]);
+            }
+    };
+    // running max update of the lane's query from tile scores S (raw, masked)
+    auto update_max = [&](const f32x16 (&S)[2]) {
+        float mx = S[0][0];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) x[16 * j + i] = s[j][i] * a.c;
-        if (!half1) {
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, S[j][i]);
+        mx = wave_max_xor(mx, 32) * a.c;
+        if (__ballot(mx > m + kSlack)) {  // wave-uniform: some query's max moved
+            const float mn = mx > m + kSlack ? mx : m;
+            const float alpha = fast_exp2(m - mn);
+            m = mn;
+            l *= alpha;
 #pragma unroll
-            for (int i = 16; i < 32; ++i) x[i] = -INFINITY;
+            for (int b = 0; b < NDB; ++b) o[b] *= alpha;
         }
-        if (k0 + BN - 1 > wpos_first) {  // tile crosses the diagonal of this wave
+    };
+    auto probs = [&](const f32x16 (&S)[2], f16x8 (&pf)[4]) {
+        const float nm = -m;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const float p = fast_exp2(fmaf(S[i >> 4][i & 15], a.c, nm));
+            l += p;
+            pf[i >> 3][i & 7] = (_Float16)p;
+        }
+    };
+    auto pv = [&](const f16x8 (&pf)[4], uint32_t kt) {
+        const _Float16* vr = &Vl[kt & 1][r32 * VS + hh * 8];
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+            for (int b = 0; b < NDB; ++b)  // independent accumulators back to back
+                o[b] = mfma32(*reinterpret_cast<const f16x8*>(vr + b * 32 * VS + kc * 16), pf[kc], o[b]);
+    };
+    // scores of tile kt into Snext while the probabilities of Scur are formed:
+    // each score MFMA is followed by the exp2 work it can hide
+    auto qk_probs = [&](f32x16 (&Snext)[2], uint32_t kt, const f32x16 (&Scur)[2], f16x8 (&pf)[4]) {
+        constexpr int PPM = 32 / (2 * NKK);  // probabilities per MFMA
+        const _Float16* kr = &Kl[kt & 1][r32 * KS + hh * 8];
+        const float nm = -m;
+        // MFMA n = kk*2 + j (halves alternate, so neighbours are independent);
+        // its K fragment is read one MFMA ahead
+        f16x8 kf = *reinterpret_cast<const f16x8*>(kr);
+#pragma unroll
+        for (int n = 0; n < 2 * NKK; ++n) {
+            const int kk = n >> 1, j = n & 1;
+            f16x8 kn = kf;
+            if (n + 1 < 2 * NKK) {
+                const int kk1 = (n + 1) >> 1, j1 = (n + 1) & 1;
+                kn = *reinterpret_cast<const f16x8*>(kr + 32 * j1 * KS + kk1 * 16);
+            }
+            Snext[j] = kk == 0 ? mfma32(kf, qf[0], f32x16{}) : mfma32(kf, qf[kk], Snext[j]);
+#pragma unroll
+            for (int u = 0; u < PPM; ++u) {
+                const int i = n * PPM + u;
+                const float p = fast_exp2(fmaf(Scur[i >> 4][i & 15], a.c, nm));
+                l += p;
+                pf[i >> 3][i & 7] = (_Float16)p;
+            }
+            kf = kn;
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // next fragment's LDS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // this MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4 * PPM, 0);  // softmax work it hides
+        }
+    };
+    // the diagonal tile: keys beyond the lane's position get -inf
+    auto mask = [&](f32x16 (&S)[2], uint32_t kt) {
+        const uint32_t k0 = kt * BN;
+        if (k0 + BN - 1 > wpos_first) {
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
-                    if (k0 + 32 * j + key_of_acc(i, hh) > my_pos) x[16 * j + i] = -INFINITY;
+                    if (k0 + 32 * j + key_of_acc(i, hh) > my_pos) S[j][i] = -INFINITY;
         }
-        float mx = x[0];
-#pragma unroll
-        for (int i = 1; i < 32; ++i) mx = fmaxf(mx, x[i]);
-        mx = wave_max_xor(mx, 32);
-        const float mn = fmaxf(m, mx);
-        const float alpha = fast_exp2(m - mn);
-        m = mn;
-        float ps = 0.0f;
-        f16x8 pf[4];
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const float p = fast_exp2(x[i] - mn);
-            ps += p;
-            pf[i >> 3][i & 7] = (_Float16)p;
-        }
-        l = l * alpha + ps;
-#pragma unroll
-        for (int b = 0; b < NDB; ++b) o[b] *= alpha;
+    };
 
-        const int nkc = half1 ? 4 : 2;
-#pragma unroll
-        for (int b = 0; b < NDB; ++b) {
-            const _Float16* vr = &Vl[(b * 32 + r32) * VS + hh * 8];
-#pragma unroll
-            for (int kc = 0; kc < 4; ++kc) {
-                if (kc >= nkc) break;
-                o[b] = mfma32(*reinterpret_cast<const f16x8*>(vr + kc * 16), pf[kc], o[b]);
-            }
+    // prologue: K(0), V(0), K(1) in LDS; scores of tile 0
+    load_k(0);
+    load_v(0);
+    store_k(0);
+    store_v(0, 0);
+    if (ntiles > 1) {
+        load_k(1);
+        store_k(1);
+    }
+    __syncthreads();
+    f32x16 Sa[2], Sb[2];
+    if (wtiles > 0) qk(Sa, 0);
+
+    // tile kt: loads K(kt+2), V(kt+1); scores of kt+1 overlap the softmax of
+    // kt; P.V of kt; stores K(kt+2) over K(kt) and V(kt+1) over V(kt-1); one
+    // barrier.  With pos_start not a multiple of 32 a wave's queries straddle
+    // a tile boundary, so a tile with a successor may still need the mask.
+    auto step = [&](uint32_t kt, f32x16 (&Scur)[2], f32x16 (&Snext)[2]) {
+        if (kt + 2 < ntiles) load_k(kt + 2);
+        if (kt + 1 < ntiles) load_v(kt + 1);
+        if (kt + 1 < wtiles) {
+            mask(Scur, kt);
+            update_max(Scur);
+            f16x8 pf[4];
+            qk_probs(Snext, kt + 1, Scur, pf);
+            pv(pf, kt);
+        } else if (kt < wtiles) {
+            mask(Scur, kt);
+            update_max(Scur);
+            f16x8 pf[4];
+            probs(Scur, pf);
+            pv(pf, kt);
         }
+        if (kt + 2 < ntiles) {
+            // K(0)'s last reader is the prologue's score pass, which no
+            // barrier separates from this store yet
+            if (kt == 0) __syncthreads();
+            store_k(kt & 1);
+        }
+        if (kt + 1 < ntiles) store_v((kt + 1) & 1, kt + 1);
+        __syncthreads();
+    };
+    for (uint32_t kt = 0; kt < ntiles; kt += 2) {
+        step(kt, Sa, Sb);
+        if (kt + 1 < ntiles) step(kt + 1, Sb, Sa);
     }
 
     l += __shfl_xor(l, 32, 64);
