@@ -311,12 +311,14 @@ def cpu_decode(q, cache, out, L, nh, nkv, hd):
 # -------------------------------------------------------------- traffic
 
 def traffic_of(label: str):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    """HBM bytes per launch of the workload's kernels, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (each scaled by what the counter
+    reads for a 1 GiB copy kernel); None when that workload was not counted."""
     p = ROOT / "profiles" / "traffic.json"
     try:
-        data = json.loads(p.read_text())
-        return data.get(label)
-    except (OSError, ValueError):
+        entry = json.loads(p.read_text()).get(label)
+        return None if entry is None else float(entry["bytes"])
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
