@@ -19,8 +19,9 @@
  * KV cache layout in HBM (per sequence, per layer), designed for coalesced
  * per-head streaming and for the MFMA operand shapes of the kernels:
  *   K : u16 f16 bits [n_kv_heads][kv_stride][head_dim]   (row = position)
- *   V : u16 f16 bits [n_kv_heads][head_dim][kv_stride]   (transposed: column
- *                                                         = position)
+ *   V : u16 f16 bits [n_kv_heads][kv_stride/32][head_dim][32]
+ *       (tiles of 32 positions; within a tile, row = dimension, so one
+ *       16-byte load holds 8 consecutive positions of one dimension)
  * kv_stride is the position capacity, a multiple of 64 (>= the engine's
  * max_seq).  The reference's engine layout ([max_seq][n_kv*head_dim] per
  * layer, yllm.h:109 / engine.c:261) converts with yhip_kv_from_engine /

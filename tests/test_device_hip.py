@@ -1,0 +1,147 @@
+"""The HIP device backend inside the reference engine (end to end).
+
+The engine is the reference's own C (inference/core, device_cpu.c) compiled
+from its sources with yllm_amd/device/device_hip.c and a driver
+(oracle/e2e_driver.c) into oracle/_ref/libyref_e2e.so.  A synthetic model
+(llama, or qwen with q/k/v biases) is written with the reference's LLF
+writer (llf_emit, convert.c:31).
+Each case runs the same prompt (batched prefill, engine.c:590-709) and greedy
+decode steps (engine_forward, engine.c:1248) on the engine bound to the CPU
+device and bound to the HIP backend, and compares logits (max relative L2
+<= 1e-3 per step) and the chosen tokens (identical).  The backend's failure
+path (-1, CPU recompute, CPU for the rest) must give the CPU result.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from ctypes import POINTER, c_char_p, c_float, c_int, c_size_t, c_uint32
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+E2E_LIB = ROOT / "oracle" / "_ref" / "libyref_e2e.so"
+HEADER = ROOT / "include" / "yllm_device_hip.h"
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def e2e():
+    if not E2E_LIB.exists():
+        pytest.skip("oracle/_ref/libyref_e2e.so is not built (needs the reference sources: make -C oracle e2e)")
+    lib = ctypes.CDLL(str(E2E_LIB))
+    lib.ye_make_model.restype = c_int
+    lib.ye_make_model.argtypes = [c_char_p] + [c_uint32] * 8 + [c_char_p, c_size_t]
+    lib.ye_run.restype = c_int
+    lib.ye_run.argtypes = [c_char_p, c_int, c_int, c_int, POINTER(c_uint32), c_int, c_int, POINTER(c_float),
+                           POINTER(c_uint32), POINTER(c_int), c_char_p, c_size_t]
+    return lib
+
+
+ARCH_LLAMA, ARCH_QWEN = 0, 1  # llf.h:22-23
+
+
+def make_model(lib, path, blocks, hidden, heads, kv_heads, vocab=512, seq=256, seed=7, arch=ARCH_LLAMA):
+    err = ctypes.create_string_buffer(256)
+    rc = lib.ye_make_model(str(path).encode(), arch, blocks, hidden, heads, kv_heads, vocab, seq, seed, err, 256)
+    assert rc == 0, err.value.decode()
+    return path
+
+
+def run(lib, path, prompt, n_decode, use_hip, fail_after=-1, vocab=512):
+    prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+    logits = np.zeros((n_decode + 1, vocab), dtype=np.float32)
+    tokens = np.zeros(max(n_decode, 1), dtype=np.uint32)
+    status = np.zeros(2, dtype=np.int32)
+    err = ctypes.create_string_buffer(256)
+    rc = lib.ye_run(str(path).encode(), int(use_hip), 0, fail_after,
+                    prompt.ctypes.data_as(POINTER(c_uint32)), len(prompt), n_decode,
+                    logits.ctypes.data_as(POINTER(c_float)), tokens.ctypes.data_as(POINTER(c_uint32)),
+                    status.ctypes.data_as(POINTER(c_int)), err, 256)
+    assert rc == 0, err.value.decode()
+    return logits, tokens[:n_decode], status, err.value.decode()
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm((a - b).ravel()) / max(np.linalg.norm(b.ravel()), 1e-30))
+
+
+def prompt_of(n, vocab=512, seed=3):
+    return np.random.default_rng(seed).integers(1, vocab, size=n, dtype=np.uint32)
+
+
+# ------------------------------------------------------------------ CPU only
+
+def test_plugin_exports_every_declared_symbol(e2e):
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"\b(device_\w+)\s*\(", text)
+    assert set(names) == {"device_create_hip", "device_hip_kv_from_host", "device_hip_kv_to_host",
+                          "device_hip_fail_after"}
+    for n in names:
+        assert hasattr(e2e, n), n
+
+
+def test_bind_without_usable_gpu_falls_back_to_cpu(e2e, tmp_path):
+    """With no gfx950 device the factory fails with a message, the CPU device
+    is bound again and the outputs are the CPU engine's, bit for bit."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present; the GPU tests cover the bound backend")
+    path = make_model(e2e, tmp_path / "m.llf", 2, 256, 4, 2)
+    prompt = prompt_of(20)
+    want, wt, _, _ = run(e2e, path, prompt, 3, use_hip=False)
+    got, gt, status, msg = run(e2e, path, prompt, 3, use_hip=True)
+    assert status[0] == -1 and msg.startswith("hip:"), (status, msg)
+    assert np.array_equal(got, want) and np.array_equal(gt, wt)
+
+
+# ------------------------------------------------------------------------ GPU
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("arch,hidden,heads,kv_heads,n_prompt", [
+    (ARCH_LLAMA, 512, 8, 2, 83),    # head_dim 64, GQA 4:1; prefill chunks 64 + 19, both batched
+    (ARCH_LLAMA, 1024, 8, 2, 70),   # head_dim 128; chunk 64 batched, the 6-token tail on the CPU
+    (ARCH_QWEN, 512, 4, 4, 40),     # head_dim 128, no GQA, qwen RoPE and q/k/v biases
+    (ARCH_LLAMA, 1024, 4, 1, 33),   # head_dim 256, GQA 4:1
+])
+def test_engine_end_to_end_matches_cpu(e2e, cuda, tmp_path, arch, hidden, heads, kv_heads, n_prompt):
+    path = make_model(e2e, tmp_path / "m.llf", 2, hidden, heads, kv_heads, arch=arch)
+    prompt = prompt_of(n_prompt)
+    n_dec = 8
+    want, wt, _, _ = run(e2e, path, prompt, n_dec, use_hip=False)
+    got, gt, status, msg = run(e2e, path, prompt, n_dec, use_hip=True)
+    assert status[0] == 0, msg
+    errs = [rel_l2(got[i], want[i]) for i in range(n_dec + 1)]
+    print(f"e2e hidden={hidden} heads={heads}/{kv_heads} prompt={n_prompt}: max rel_l2 {max(errs):.3e}, "
+          f"tokens {gt.tolist()}")
+    assert max(errs) <= TOL
+    assert np.array_equal(np.argmax(got, axis=1), np.argmax(want, axis=1))
+    assert np.array_equal(gt, wt)
+    # the HBM cache holds exactly the engine's KV rows
+    assert status[1] == 0
+
+
+@pytest.mark.gpu
+def test_engine_failure_hook_first_call_gives_cpu_result(e2e, cuda, tmp_path):
+    path = make_model(e2e, tmp_path / "m.llf", 2, 512, 8, 2)
+    prompt = prompt_of(40)
+    want, wt, _, _ = run(e2e, path, prompt, 4, use_hip=False)
+    got, gt, status, msg = run(e2e, path, prompt, 4, use_hip=True, fail_after=0)
+    assert status[0] == 0, msg
+    assert np.array_equal(got, want) and np.array_equal(gt, wt)
+
+
+@pytest.mark.gpu
+def test_engine_failure_hook_mid_run_stays_within_tolerance(e2e, cuda, tmp_path):
+    """GPU for the prefill and two decode blocks, then the CPU: the CPU path
+    reads the host KV that the backend mirrored."""
+    path = make_model(e2e, tmp_path / "m.llf", 2, 512, 8, 2)
+    prompt = prompt_of(40)
+    want, wt, _, _ = run(e2e, path, prompt, 6, use_hip=False)
+    got, gt, status, msg = run(e2e, path, prompt, 6, use_hip=True, fail_after=4)
+    assert status[0] == 0, msg
+    assert max(rel_l2(got[i], want[i]) for i in range(7)) <= TOL
+    assert np.array_equal(gt, wt)

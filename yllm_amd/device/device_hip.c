@@ -1,0 +1,596 @@
+/* device_hip.c -- yllm device backend for MI355X (gfx950): the attention of
+ * every block runs on the GPU, the rest of the block on the engine's CPU
+ * operators.
+ *
+ * Drop-in for the Device plugin interface (inference/include/device.h:37-50,
+ * factory pattern of inference/device/device_cpu.c:82-110).  load_weights
+ * installs fwd_block / fwd_block_batch (yllm.h:115-116) in place of the CPU
+ * ones (engine_attach_cpu_fwd, engine.c:1111-1120).  The contract of those
+ * (engine.c:1156-1158, 652, 1404, 1460): the block input is e->x (decode) or
+ * e->pb rows (batch), the output replaces it in place, the layer's KV row for
+ * each position is written before attention, the return is 0 or -1.
+ *
+ * Per block this backend computes exactly the reference block
+ * (engine_fwd_block_at, engine.c:992-1109; forward_block_batch_default,
+ * engine.c:435-590) with the engine's own exported operators -- rmsnorm,
+ * matmul / matmul_batch, rope_inplace(_qwen), swiglu, f32_to_f16 -- in the
+ * same order, and replaces only the attention loop: q, k, v go to HBM, the
+ * K/V rows are stored into the head-major HBM cache (yhip_kv_store), and
+ * yhip_attn_decode / yhip_attn_prefill produce the attention output, which
+ * comes back for o_proj.  The f16 K/V rows are also written to the engine's
+ * host array e->kv, so host KV is always current: a CPU fallback, session
+ * save (cache.c:174-247) and the CPU path of any layer stay valid.
+ *
+ * Failure handling: any HIP error in a block marks the backend failed; that
+ * block is recomputed with the saved CPU forward (e->x is untouched until
+ * the attention output is back) and -1 is returned; every later block runs
+ * on the CPU.  device_mode stays DEV_MODE_CPU: the host holds x and a valid
+ * KV copy at every block boundary, so every CPU branch of the engine is
+ * correct with this backend bound.
+ */
+#include <hip/hip_runtime_api.h>
+
+#include <math.h>
+#include <stddef.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "llf.h"
+#include "matvec.h"
+#include "yllm.h"
+#include "yllm_device_hip.h"
+#include "yllm_hip.h"
+
+/* ABI pins: this file reads these fields of the reference structs; the
+ * offsets are those of the reference headers on x86-64 (gcc). */
+_Static_assert(sizeof(Device) == 48, "Device layout differs from device.h:37-50");
+_Static_assert(sizeof(Engine) == 576, "Engine layout differs from yllm.h");
+_Static_assert(offsetof(Engine, kv) == 264, "Engine.kv");
+_Static_assert(offsetof(Engine, kv_dim) == 272, "Engine.kv_dim");
+_Static_assert(offsetof(Engine, max_seq) == 276, "Engine.max_seq");
+_Static_assert(offsetof(Engine, fwd_block) == 288, "Engine.fwd_block");
+_Static_assert(offsetof(Engine, fwd_block_batch) == 296, "Engine.fwd_block_batch");
+_Static_assert(offsetof(Engine, layer_begin) == 304, "Engine.layer_begin");
+_Static_assert(offsetof(Engine, x) == 312, "Engine.x");
+_Static_assert(offsetof(Engine, hb) == 320, "Engine.hb");
+_Static_assert(offsetof(Engine, hb2) == 328, "Engine.hb2");
+_Static_assert(offsetof(Engine, ffn) == 336, "Engine.ffn");
+_Static_assert(offsetof(Engine, pb) == 384, "Engine.pb");
+_Static_assert(offsetof(Engine, pb2) == 392, "Engine.pb2");
+_Static_assert(offsetof(Engine, pbq) == 400, "Engine.pbq");
+_Static_assert(offsetof(Engine, pb_cap) == 448, "Engine.pb_cap");
+_Static_assert(offsetof(Engine, dev) == 528, "Engine.dev");
+_Static_assert(offsetof(Engine, d_kv) == 536, "Engine.d_kv");
+_Static_assert(offsetof(Engine, w_dev) == 544, "Engine.w_dev");
+_Static_assert(offsetof(Engine, weights_ready) == 552, "Engine.weights_ready");
+_Static_assert(offsetof(Engine, device_mode) == 556, "Engine.device_mode");
+
+/* DeviceKind has no HIP entry in the reference enum (device.h:15-19); an
+ * integrated build adds DEV_HIP there and compiles this file with
+ * -DYLLM_DEV_HIP_KIND=DEV_HIP.  Standalone, the kind is the next free value. */
+#ifndef YLLM_DEV_HIP_KIND
+#define YLLM_DEV_HIP_KIND 3
+#endif
+
+typedef int (*FwdFn)(Engine*, uint32_t, uint32_t);
+typedef int (*FwdBatchFn)(Engine*, uint32_t, uint32_t, uint32_t);
+
+typedef struct {
+    int device_id;
+    hipStream_t stream;
+    /* model shape */
+    uint32_t arch, hidden, n_heads, n_kv, head_dim, kv_dim, n_blocks, max_seq;
+    /* HBM KV: block layers first..last, K then V per layer */
+    uint32_t first, last, kv_stride;
+    uint64_t layer_elems;
+    uint16_t* d_cache;
+    uint32_t* dev_len;  /* per resident layer: rows 0..dev_len-1 are in HBM */
+    /* staging for one call: q / attention out [cap][hidden], k / v [cap][kv_dim] */
+    uint32_t cap;
+    float *d_q, *d_k, *d_v, *d_out;
+    uint16_t* d_rows;  /* host f16 rows on their way into HBM (catch-up) */
+    void* d_ws;
+    size_t ws_bytes;
+    /* fallback */
+    FwdFn cpu_fwd;
+    FwdBatchFn cpu_fwd_batch;
+    int failed;
+    int fail_after;
+} HipCtx;
+
+static HipCtx* ctx_of(const Engine* e)
+{
+    return e && e->dev ? (HipCtx*)e->dev->handle : NULL;
+}
+
+static int say(char* err, size_t errlen, const char* what, const char* detail)
+{
+    if (err && errlen) snprintf(err, errlen, "hip: %s%s%s", what, detail ? ": " : "", detail ? detail : "");
+    return -1;
+}
+
+static int hip_ok(hipError_t rc, char* err, size_t errlen, const char* what)
+{
+    return rc == hipSuccess ? 0 : say(err, errlen, what, hipGetErrorString(rc));
+}
+
+static uint16_t* layer_k(const HipCtx* c, uint32_t layer)
+{
+    return c->d_cache + (size_t)(layer - c->first) * 2 * c->layer_elems;
+}
+
+static uint16_t* layer_v(const HipCtx* c, uint32_t layer)
+{
+    return layer_k(c, layer) + c->layer_elems;
+}
+
+static void release(HipCtx* c)
+{
+    if (!c) return;
+    if (c->d_cache) hipFree(c->d_cache);
+    if (c->d_q) hipFree(c->d_q);
+    if (c->d_k) hipFree(c->d_k);
+    if (c->d_v) hipFree(c->d_v);
+    if (c->d_out) hipFree(c->d_out);
+    if (c->d_rows) hipFree(c->d_rows);
+    if (c->d_ws) hipFree(c->d_ws);
+    if (c->stream) hipStreamDestroy(c->stream);
+    free(c->dev_len);
+    {
+        int id = c->device_id;
+        memset(c, 0, sizeof(*c));
+        c->device_id = id;
+        c->fail_after = -1;
+    }
+}
+
+/* staging for up to `rows` tokens of one call */
+static int ensure_cap(HipCtx* c, uint32_t rows)
+{
+    if (rows <= c->cap) return 0;
+    if (c->d_q) hipFree(c->d_q);
+    if (c->d_k) hipFree(c->d_k);
+    if (c->d_v) hipFree(c->d_v);
+    if (c->d_out) hipFree(c->d_out);
+    if (c->d_rows) hipFree(c->d_rows);
+    c->d_q = c->d_k = c->d_v = c->d_out = NULL;
+    c->d_rows = NULL;
+    c->cap = 0;
+    if (hipMalloc((void**)&c->d_q, (size_t)rows * c->hidden * 4) != hipSuccess ||
+        hipMalloc((void**)&c->d_out, (size_t)rows * c->hidden * 4) != hipSuccess ||
+        hipMalloc((void**)&c->d_k, (size_t)rows * c->kv_dim * 4) != hipSuccess ||
+        hipMalloc((void**)&c->d_v, (size_t)rows * c->kv_dim * 4) != hipSuccess ||
+        hipMalloc((void**)&c->d_rows, (size_t)rows * c->kv_dim * 2 * 2) != hipSuccess)
+        return -1;
+    c->cap = rows;
+    return 0;
+}
+
+/* Rows dev_len..upto-1 of a layer exist only in host KV (written by a CPU
+ * block or restored from a session): bring them into HBM, in chunks of the
+ * staging capacity.  Host rows are f16 bits already; yhip_kv_store copies
+ * f16 sources bit for bit. */
+static int catch_up(HipCtx* c, Engine* e, uint32_t layer, uint32_t upto)
+{
+    uint32_t* have = &c->dev_len[layer - c->first];
+    const uint16_t* hk = e->kv + (size_t)layer * e->max_seq * c->kv_dim;
+    const uint16_t* hv = e->kv + (size_t)(c->n_blocks + layer) * e->max_seq * c->kv_dim;
+    while (*have < upto) {
+        uint32_t n = upto - *have;
+        size_t off = (size_t)*have * c->kv_dim, bytes;
+        if (n > c->cap) n = c->cap;
+        bytes = (size_t)n * c->kv_dim * 2;
+        if (hipMemcpyAsync(c->d_rows, hk + off, bytes, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+            hipMemcpyAsync(c->d_rows + (size_t)n * c->kv_dim, hv + off, bytes, hipMemcpyHostToDevice,
+                           c->stream) != hipSuccess)
+            return -1;
+        if (yhip_kv_store(layer_k(c, layer), layer_v(c, layer), c->d_rows, c->d_rows + (size_t)n * c->kv_dim,
+                          YHIP_F16, *have, n, c->n_kv, c->head_dim, c->kv_stride, c->stream) != YHIP_OK)
+            return -1;
+        *have += n;
+    }
+    return 0;
+}
+
+/* Whether this block call may use the GPU.  Returns 1 (yes), 0 (no: the
+ * layer is outside the resident range, or the backend failed earlier) or -1
+ * (the GPU fails at this call: the test hook's count ran out). */
+static int gpu_turn(HipCtx* c, uint32_t layer, uint32_t pos_end)
+{
+    if (layer < c->first || layer > c->last || pos_end > c->max_seq || c->failed) return 0;
+    if (c->fail_after == 0) {
+        c->failed = 1;
+        return -1;
+    }
+    if (c->fail_after > 0) c->fail_after--;
+    return 1;
+}
+
+static const uint8_t* layer_base(const Engine* e, uint32_t layer)
+{
+    return (const uint8_t*)e->ws.map.base + e->ws.model.dir[layer].offset;
+}
+
+static void rope_heads(uint32_t arch, float* v, uint32_t n, uint32_t d, uint32_t pos, float theta)
+{
+    uint32_t i;
+    for (i = 0; i < n; i++) {
+        if (arch == ARCH_QWEN)
+            rope_inplace_qwen(v + (size_t)i * d, d, pos, theta);
+        else
+            rope_inplace(v + (size_t)i * d, d, pos, theta);
+    }
+}
+
+static void add_bias(float* y, const LlfTensorMeta* t, const uint8_t* base, uint32_t n)
+{
+    if (t->size > 0) {
+        const float* b = (const float*)(base + t->offset);
+        uint32_t j;
+        for (j = 0; j < n; j++) y[j] += b[j];
+    }
+}
+
+static void head_norm(float* v, const LlfTensorMeta* t, const uint8_t* base, uint32_t n, uint32_t d, float eps)
+{
+    if (t->size > 0) {
+        uint32_t i;
+        for (i = 0; i < n; i++) rmsnorm(v + (size_t)i * d, v + (size_t)i * d, base + t->offset, d, eps, t->dtype);
+    }
+}
+
+/* q, k, v of one token after bias, QK-norm and RoPE; the f16 K/V row goes to
+ * host KV (engine.c:1015-1072) */
+static void token_qkv(Engine* e, const HipCtx* c, uint32_t layer, uint32_t pos, const uint8_t* base,
+                      const LlfTensorMeta* mt, float eps, float theta, float* q, float* k, float* v)
+{
+    uint16_t* hk = e->kv + (size_t)layer * e->max_seq * c->kv_dim + (size_t)pos * c->kv_dim;
+    uint16_t* hv = e->kv + (size_t)(c->n_blocks + layer) * e->max_seq * c->kv_dim + (size_t)pos * c->kv_dim;
+    uint32_t j;
+    add_bias(q, &mt[SLOT_QBIAS], base, c->hidden);
+    add_bias(k, &mt[SLOT_KBIAS], base, c->kv_dim);
+    add_bias(v, &mt[SLOT_VBIAS], base, c->kv_dim);
+    head_norm(q, &mt[SLOT_QNORM], base, c->n_heads, c->head_dim, eps);
+    head_norm(k, &mt[SLOT_KNORM], base, c->n_kv, c->head_dim, eps);
+    rope_heads(c->arch, q, c->n_heads, c->head_dim, pos, theta);
+    rope_heads(c->arch, k, c->n_kv, c->head_dim, pos, theta);
+    for (j = 0; j < c->kv_dim; j++) {
+        hk[j] = f32_to_f16(k[j]);
+        hv[j] = f32_to_f16(v[j]);
+    }
+}
+
+static void scalars(const Engine* e, float* eps, float* theta)
+{
+    memcpy(eps, &e->ws.model.h.norm_eps_bits, 4);
+    memcpy(theta, &e->ws.model.h.rope_theta_bits, 4);
+}
+
+/* decode attention on the GPU: q, k, v (contiguous floats, as engine.c
+ * lays them out in hb2) -> att_out */
+static int gpu_decode(HipCtx* c, Engine* e, uint32_t layer, uint32_t pos, const float* qkv, float* att_out)
+{
+    uint16_t *kc = layer_k(c, layer), *vc = layer_v(c, layer);
+    size_t nq = c->hidden, nkv = c->kv_dim;
+    if (ensure_cap(c, 1) != 0) return -1;
+    if (catch_up(c, e, layer, pos) != 0) return -1;
+    if (hipMemcpyAsync(c->d_q, qkv, nq * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        hipMemcpyAsync(c->d_k, qkv + nq, nkv * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        hipMemcpyAsync(c->d_v, qkv + nq + nkv, nkv * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
+        return -1;
+    if (yhip_kv_store(kc, vc, c->d_k, c->d_v, YHIP_F32, pos, 1, c->n_kv, c->head_dim, c->kv_stride,
+                      c->stream) != YHIP_OK)
+        return -1;
+    c->dev_len[layer - c->first] = pos + 1;
+    if (yhip_attn_decode(c->d_out, c->d_q, kc, vc, pos, c->n_heads, c->n_kv, c->head_dim, c->kv_stride, NULL,
+                         c->d_ws, c->ws_bytes, c->stream) != YHIP_OK)
+        return -1;
+    if (hipMemcpyAsync(att_out, c->d_out, nq * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return -1;
+    return hipStreamSynchronize(c->stream) == hipSuccess ? 0 : -1;
+}
+
+/* fwd_block: engine_fwd_block_at (engine.c:992-1109) with the attention
+ * loop (1074-1096) on the GPU */
+static int hip_fwd_block(Engine* e, uint32_t layer, uint32_t pos)
+{
+    HipCtx* c = ctx_of(e);
+    const uint8_t* base;
+    const LlfTensorMeta* mt;
+    float eps, theta, *x, *x2, *q, *k, *v, *att_out, *fg, *fu;
+    uint32_t hidden, kv_dim, inter, j;
+    int turn;
+    if (!c) return -1;
+    turn = gpu_turn(c, layer, pos + 1);
+    if (turn <= 0) {
+        c->cpu_fwd(e, layer, pos);
+        return turn;
+    }
+    base = layer_base(e, layer);
+    mt = &e->ws.model.metas[e->ws.model.base_idx[layer]];
+    hidden = c->hidden;
+    kv_dim = c->kv_dim;
+    inter = mt[SLOT_GATE].shape[0] * mt[SLOT_GATE].shape[1] / hidden;
+    scalars(e, &eps, &theta);
+    x = e->x;
+    x2 = e->hb;
+    q = e->hb2;
+    k = q + hidden;
+    v = k + kv_dim;
+    att_out = v + kv_dim;
+
+    rmsnorm(x2, x, base + mt[SLOT_NORM1].offset, hidden, eps, mt[SLOT_NORM1].dtype);
+    matmul(q, x2, base + mt[SLOT_Q].offset, hidden, hidden, mt[SLOT_Q].dtype);
+    matmul(k, x2, base + mt[SLOT_K].offset, kv_dim, hidden, mt[SLOT_K].dtype);
+    matmul(v, x2, base + mt[SLOT_V].offset, kv_dim, hidden, mt[SLOT_V].dtype);
+    token_qkv(e, c, layer, pos, base, mt, eps, theta, q, k, v);
+
+    if (gpu_decode(c, e, layer, pos, q, att_out) != 0) {
+        c->failed = 1;
+        c->cpu_fwd(e, layer, pos);  /* x is still the block input */
+        return -1;
+    }
+
+    /* o_proj, residual, norm2, SwiGLU FFN, residual (engine.c:1097-1108) */
+    memcpy(x2, att_out, (size_t)hidden * 4);
+    matmul(att_out, x2, base + mt[SLOT_O].offset, hidden, hidden, mt[SLOT_O].dtype);
+    for (j = 0; j < hidden; j++) x[j] += att_out[j];
+    rmsnorm(x2, x, base + mt[SLOT_NORM2].offset, hidden, eps, mt[SLOT_NORM2].dtype);
+    fg = e->ffn;
+    fu = e->ffn + inter;
+    matmul(fg, x2, base + mt[SLOT_GATE].offset, inter, hidden, mt[SLOT_GATE].dtype);
+    matmul(fu, x2, base + mt[SLOT_UP].offset, inter, hidden, mt[SLOT_UP].dtype);
+    swiglu(x2, fg, fu, inter);
+    matmul(att_out, x2, base + mt[SLOT_DOWN].offset, hidden, inter, mt[SLOT_DOWN].dtype);
+    for (j = 0; j < hidden; j++) x[j] += att_out[j];
+    return 0;
+}
+
+/* causal attention of B tokens at pos_start.. on the GPU: e->pbq, pbk, pbv
+ * -> e->pb2 */
+static int gpu_prefill(HipCtx* c, Engine* e, uint32_t layer, uint32_t pos_start, uint32_t B)
+{
+    uint16_t *kc = layer_k(c, layer), *vc = layer_v(c, layer);
+    size_t nq = (size_t)B * c->hidden, nkv = (size_t)B * c->kv_dim;
+    if (ensure_cap(c, B) != 0) return -1;
+    if (catch_up(c, e, layer, pos_start) != 0) return -1;
+    if (hipMemcpyAsync(c->d_q, e->pbq, nq * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        hipMemcpyAsync(c->d_k, e->pbk, nkv * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        hipMemcpyAsync(c->d_v, e->pbv, nkv * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
+        return -1;
+    if (yhip_kv_store(kc, vc, c->d_k, c->d_v, YHIP_F32, pos_start, B, c->n_kv, c->head_dim, c->kv_stride,
+                      c->stream) != YHIP_OK)
+        return -1;
+    c->dev_len[layer - c->first] = pos_start + B;
+    if (yhip_attn_prefill(c->d_out, YHIP_F32, c->hidden, c->d_q, YHIP_F32, c->hidden, kc, vc, pos_start, B,
+                          c->n_heads, c->n_kv, c->head_dim, c->kv_stride, NULL, 0, c->stream) != YHIP_OK)
+        return -1;
+    if (hipMemcpyAsync(e->pb2, c->d_out, nq * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return -1;
+    return hipStreamSynchronize(c->stream) == hipSuccess ? 0 : -1;
+}
+
+/* fwd_block_batch: forward_block_batch_default (engine.c:435-590) with the
+ * attention loop (532-563) on the GPU */
+static int hip_fwd_block_batch(Engine* e, uint32_t layer, uint32_t pos_start, uint32_t B)
+{
+    HipCtx* c = ctx_of(e);
+    const uint8_t* base;
+    const LlfTensorMeta* mt;
+    float eps, theta;
+    uint32_t hidden, kv_dim, inter, b, j;
+    int turn;
+    if (!c) return -1;
+    if (B == 0) return 0;
+    turn = gpu_turn(c, layer, pos_start + B);
+    if (turn <= 0) {
+        c->cpu_fwd_batch(e, layer, pos_start, B);
+        return turn;
+    }
+    base = layer_base(e, layer);
+    mt = &e->ws.model.metas[e->ws.model.base_idx[layer]];
+    hidden = c->hidden;
+    kv_dim = c->kv_dim;
+    inter = mt[SLOT_GATE].shape[0] * mt[SLOT_GATE].shape[1] / hidden;
+    scalars(e, &eps, &theta);
+
+    for (b = 0; b < B; b++)
+        rmsnorm(e->pb2 + (size_t)b * hidden, e->pb + (size_t)b * hidden, base + mt[SLOT_NORM1].offset, hidden,
+                eps, mt[SLOT_NORM1].dtype);
+    matmul_batch(e->pbq, e->pb2, base + mt[SLOT_Q].offset, hidden, hidden, mt[SLOT_Q].dtype, B);
+    matmul_batch(e->pbk, e->pb2, base + mt[SLOT_K].offset, kv_dim, hidden, mt[SLOT_K].dtype, B);
+    matmul_batch(e->pbv, e->pb2, base + mt[SLOT_V].offset, kv_dim, hidden, mt[SLOT_V].dtype, B);
+    for (b = 0; b < B; b++)
+        token_qkv(e, c, layer, pos_start + b, base, mt, eps, theta, e->pbq + (size_t)b * hidden,
+                  e->pbk + (size_t)b * kv_dim, e->pbv + (size_t)b * kv_dim);
+
+    if (gpu_prefill(c, e, layer, pos_start, B) != 0) {
+        c->failed = 1;
+        c->cpu_fwd_batch(e, layer, pos_start, B);  /* e->pb is still the block input */
+        return -1;
+    }
+
+    /* o_proj, residual, norm2, SwiGLU FFN, residual (engine.c:565-589) */
+    matmul_batch(e->pbq, e->pb2, base + mt[SLOT_O].offset, hidden, hidden, mt[SLOT_O].dtype, B);
+    for (b = 0; b < B; b++) {
+        float* xb = e->pb + (size_t)b * hidden;
+        const float* ob = e->pbq + (size_t)b * hidden;
+        for (j = 0; j < hidden; j++) xb[j] += ob[j];
+        rmsnorm(e->pb2 + (size_t)b * hidden, xb, base + mt[SLOT_NORM2].offset, hidden, eps, mt[SLOT_NORM2].dtype);
+    }
+    matmul_batch(e->pbg, e->pb2, base + mt[SLOT_GATE].offset, inter, hidden, mt[SLOT_GATE].dtype, B);
+    matmul_batch(e->pbu, e->pb2, base + mt[SLOT_UP].offset, inter, hidden, mt[SLOT_UP].dtype, B);
+    for (b = 0; b < B; b++)
+        swiglu(e->pbg + (size_t)b * inter, e->pbg + (size_t)b * inter, e->pbu + (size_t)b * inter, inter);
+    matmul_batch(e->pbq, e->pbg, base + mt[SLOT_DOWN].offset, hidden, inter, mt[SLOT_DOWN].dtype, B);
+    for (b = 0; b < B; b++) {
+        float* xb = e->pb + (size_t)b * hidden;
+        const float* db = e->pbq + (size_t)b * hidden;
+        for (j = 0; j < hidden; j++) xb[j] += db[j];
+    }
+    return 0;
+}
+
+static int hip_load_weights(Engine* e, char* err, size_t errlen)
+{
+    HipCtx* c = ctx_of(e);
+    const LlfHeader* h;
+    uint32_t first, last, nl;
+    size_t cache_bytes;
+    if (!c) return say(err, errlen, "no backend state", NULL);
+    h = &e->ws.model.h;
+    release(c);
+    if (h->arch == ARCH_QWEN35) return say(err, errlen, "ARCH_QWEN35 blocks are not offloaded by this backend", NULL);
+    if (h->n_heads * h->head_dim != h->hidden)
+        return say(err, errlen, "n_heads*head_dim != hidden is not supported", NULL);
+    if (h->head_dim != 64 && h->head_dim != 128 && h->head_dim != 256)
+        return say(err, errlen, "head_dim must be 64, 128 or 256", NULL);
+    if (h->n_kv_heads == 0 || h->n_heads % h->n_kv_heads || h->n_heads / h->n_kv_heads > 16)
+        return say(err, errlen, "need n_kv_heads | n_heads and at most 16 query heads per kv head", NULL);
+    if (e->kv_dim != h->n_kv_heads * h->head_dim) return say(err, errlen, "engine kv_dim mismatch", NULL);
+
+    /* block layers of this engine's range: [layer_begin, layer_end) ∩ [1, n_blocks] */
+    first = e->layer_begin > 1 ? e->layer_begin : 1;
+    last = e->layer_end > 0 && e->layer_end - 1 < h->n_blocks ? e->layer_end - 1 : h->n_blocks;
+    if (first > last) first = last = 1;
+    nl = last - first + 1;
+
+    if (hip_ok(hipSetDevice(c->device_id), err, errlen, "hipSetDevice") ||
+        hip_ok(hipStreamCreate(&c->stream), err, errlen, "hipStreamCreate"))
+        return -1;
+    c->arch = h->arch;
+    c->hidden = h->hidden;
+    c->n_heads = h->n_heads;
+    c->n_kv = h->n_kv_heads;
+    c->head_dim = h->head_dim;
+    c->kv_dim = e->kv_dim;
+    c->n_blocks = h->n_blocks;
+    c->max_seq = e->max_seq;
+    c->first = first;
+    c->last = last;
+    c->kv_stride = (e->max_seq + 63) / 64 * 64;
+    c->layer_elems = yhip_kv_layer_elems(c->n_kv, c->head_dim, c->kv_stride);
+    cache_bytes = (size_t)nl * 2 * c->layer_elems * 2;
+    if (hip_ok(hipMalloc((void**)&c->d_cache, cache_bytes), err, errlen, "KV cache allocation") ||
+        hip_ok(hipMemsetAsync(c->d_cache, 0, cache_bytes, c->stream), err, errlen, "KV cache clear"))
+        return -1;
+    c->dev_len = (uint32_t*)calloc(nl, sizeof(uint32_t));
+    if (!c->dev_len) return say(err, errlen, "out of host memory", NULL);
+    if (ensure_cap(c, e->pb_cap > 0 ? e->pb_cap : 64) != 0) return say(err, errlen, "staging allocation", NULL);
+    c->ws_bytes = yhip_attn_decode_workspace(1, c->max_seq, c->max_seq, c->n_heads, c->n_kv, c->head_dim);
+    if (c->ws_bytes && hip_ok(hipMalloc(&c->d_ws, c->ws_bytes), err, errlen, "decode workspace")) return -1;
+    if (hip_ok(hipStreamSynchronize(c->stream), err, errlen, "set-up")) return -1;
+    /* dev_len starts at 0: rows already in host KV (a CPU prefill before the
+     * bind, a restored session) are uploaded by the first block call that
+     * reads them */
+
+    engine_attach_cpu_fwd(e);
+    c->cpu_fwd = e->fwd_block;
+    c->cpu_fwd_batch = e->fwd_block_batch;
+    c->failed = 0;
+    e->fwd_block = hip_fwd_block;
+    e->fwd_block_batch = hip_fwd_block_batch;
+    e->w_dev = NULL;  /* weights stay in host memory */
+    e->d_kv = c->d_cache;
+    e->weights_ready = 1;
+    e->device_mode = DEV_MODE_CPU;
+    return 0;
+}
+
+static void hip_free_dev(Engine* e)
+{
+    HipCtx* c = ctx_of(e);
+    if (c) {
+        if (c->stream) hipStreamSynchronize(c->stream);
+        release(c);
+    }
+    if (e->fwd_block == hip_fwd_block) engine_attach_cpu_fwd(e);
+    e->w_dev = NULL;
+    e->d_kv = NULL;
+    e->weights_ready = 0;
+    e->device_mode = DEV_MODE_CPU;
+}
+
+Device* device_create_hip(int device_id, char* err, size_t errlen)
+{
+    int n = 0;
+    hipDeviceProp_t prop;
+    Device* d;
+    HipCtx* c;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        say(err, errlen, "no HIP device", NULL);
+        return NULL;
+    }
+    if (device_id < 0 || device_id >= n) {
+        say(err, errlen, "device id out of range", NULL);
+        return NULL;
+    }
+    if (hipGetDeviceProperties(&prop, device_id) != hipSuccess || strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        say(err, errlen, "device is not gfx950 (the kernels are built for MI355X only)", prop.gcnArchName);
+        return NULL;
+    }
+    d = (Device*)calloc(1, sizeof(Device));
+    c = (HipCtx*)calloc(1, sizeof(HipCtx));
+    if (!d || !c) {
+        free(d);
+        free(c);
+        say(err, errlen, "out of host memory", NULL);
+        return NULL;
+    }
+    c->device_id = device_id;
+    c->fail_after = -1;
+    d->kind = (DeviceKind)YLLM_DEV_HIP_KIND;
+    d->id = device_id;
+    d->handle = c;
+    d->load_weights = hip_load_weights;
+    d->free_dev = hip_free_dev;
+    d->prefetch_layer = NULL;
+    d->release_layer = NULL;
+    return d;
+}
+
+static int move_kv(Engine* e, uint32_t n_pos, int to_host)
+{
+    HipCtx* c = ctx_of(e);
+    uint32_t l;
+    if (!c || !c->d_cache || c->failed) return -1;
+    if (n_pos > c->max_seq) n_pos = c->max_seq;
+    for (l = c->first; l <= c->last && n_pos > 0; l++) {
+        uint16_t* hk = e->kv + (size_t)l * e->max_seq * c->kv_dim;
+        uint16_t* hv = e->kv + (size_t)(c->n_blocks + l) * e->max_seq * c->kv_dim;
+        if (to_host) {
+            uint16_t *dk, *dv;
+            size_t bytes = (size_t)n_pos * c->kv_dim * 2;
+            if (hipMalloc((void**)&dk, 2 * bytes) != hipSuccess) return -1;
+            dv = dk + (size_t)n_pos * c->kv_dim;
+            if (yhip_kv_to_engine(dk, dv, layer_k(c, l), layer_v(c, l), n_pos, c->n_kv, c->head_dim, c->kv_stride,
+                                  c->stream) != YHIP_OK ||
+                hipMemcpyAsync(hk, dk, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+                hipMemcpyAsync(hv, dv, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+                hipStreamSynchronize(c->stream) != hipSuccess) {
+                hipFree(dk);
+                return -1;
+            }
+            hipFree(dk);
+        } else {
+            c->dev_len[l - c->first] = 0;
+            if (catch_up(c, e, l, n_pos) != 0) return -1;
+        }
+    }
+    return hipStreamSynchronize(c->stream) == hipSuccess ? 0 : -1;
+}
+
+int device_hip_kv_from_host(Engine* e, uint32_t n_pos)
+{
+    return move_kv(e, n_pos, 0);
+}
+
+int device_hip_kv_to_host(Engine* e, uint32_t n_pos)
+{
+    return move_kv(e, n_pos, 1);
+}
+
+void device_hip_fail_after(Engine* e, int n_calls)
+{
+    HipCtx* c = ctx_of(e);
+    if (c) c->fail_after = n_calls < 0 ? -1 : n_calls;
+}
