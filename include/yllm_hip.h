@@ -4,7 +4,8 @@
  * They replace the attention part of the reference's CUDA kernel ABI
  * (inference/cuda/cuda_kernels.h:50-63: cuda_k_store_kv, cuda_k_store_kv_batch,
  * cuda_k_attn_decode, cuda_k_attn_prefill) and the CPU loops it mirrors
- * (inference/core/engine.c:1068-1096, 518-563, 928-960; matvec.c:942-1004).
+ * (inference/core/engine.c:1068-1096, 518-563, 928-960, 786-831;
+ * matvec.c:942-1004).
  *
  * Conventions (all entry points):
  *   - extern "C", plain pointers and sizes, fixed-width integers;
@@ -132,6 +133,39 @@ int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, co
                       const uint16_t* vcache, uint32_t pos_start, uint32_t B, uint32_t n_heads,
                       uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
                       const float* gate, uint32_t gate_stride, void* stream);
+
+/* ---- Gated DeltaNet (qwen35 linear attention) ------------------------------
+ * State S: fp32 [n_v_heads][head_dim][head_dim], S[h][j][i] = column j of
+ * v-head h (the reference's transposed storage, matvec.c:972-973); v-head h
+ * reads k-head h % n_k_heads (matvec.c:983).  gate is the log-decay
+ * (softplus(alpha+dt)*a, so g = exp(gate)) and beta the sigmoid, one per
+ * v-head and token, as yhip_gdn_gates produces them.  When l2_eps > 0, q and
+ * k are first L2-normalised per k-head with x / max(|x|, l2_eps)
+ * (l2norm_inplace, matvec.c:942-949, as engine.c:826-827 calls it); with
+ * l2_eps <= 0 they are used as given.  Arithmetic is fp32.  head_dim (d_k =
+ * d_v) is 64 or 128; S, q, k, v must be 16-byte aligned.
+ *
+ * One token: replaces gdn_state_update (matvec.c:975-1004) plus the l2norm
+ * before it.  q, k: [n_k_heads*head_dim]; v, out: [n_v_heads*head_dim];
+ * gate, beta: [n_v_heads]. */
+int yhip_gdn_step(float* S, float* out, const float* q, const float* k, const float* v, const float* gate,
+                  const float* beta, uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps,
+                  void* stream);
+
+/* T consecutive tokens (the per-token loop of the qwen35 batch forward,
+ * engine.c:723-734, for the recurrence part): rows of q/k are qk_stride
+ * floats apart, v rows v_stride, out rows out_stride (multiples of 4); gate
+ * and beta are [T][n_v_heads].  S is updated in place to the state after
+ * token T-1; out row t is the output of token t. */
+int yhip_gdn_chunk(float* S, float* out, uint32_t out_stride, const float* q, const float* k, uint32_t qk_stride,
+                   const float* v, uint32_t v_stride, const float* gate, const float* beta, uint32_t T,
+                   uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps, void* stream);
+
+/* The GDN gates of T tokens (engine.c:788-793), in place like the engine:
+ * beta[t][h] <- 1/(1+exp(-beta[t][h])), gate[t][h] <- log1p(exp(alpha[t][h]
+ * + dt_bias[h])) * ssm_a[h]. */
+int yhip_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt_bias, const float* ssm_a,
+                   uint32_t T, uint32_t n_v_heads, void* stream);
 
 /* ---- Synthetic inputs (host) ----------------------------------------------
  * Seeded generator shared by the tests and the benchmark so that the CPU

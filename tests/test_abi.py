@@ -118,3 +118,24 @@ def test_synth_normal_is_splitmix_box_muller(hiplib, golden):
     # moments
     big = synth_normal(123, 200000, 0.5)
     assert abs(big.mean()) < 0.01 and abs(big.std() - 0.5) < 0.01
+
+
+def test_gdn_rejects_bad_args(hiplib):
+    F = ctypes.c_float
+    # head_dim outside {64, 128}
+    rc = hiplib.yhip_gdn_chunk(P, P, 4096, P, P, 4096, P, 4096, P, P, 8, 16, 16, 256, F(1e-6), None)
+    assert rc == -22 and "head_dim" in _err(hiplib)
+    # strides that do not cover the heads
+    rc = hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 1024, P, 2048, P, P, 8, 16, 16, 128, F(1e-6), None)
+    assert rc == -22 and "strides" in _err(hiplib)
+    # misaligned q
+    rc = hiplib.yhip_gdn_chunk(P, P, 2048, ctypes.c_void_p(0x1004), P, 2048, P, 2048, P, P, 8, 16, 16, 128, F(1e-6), None)
+    assert rc == -22 and "aligned" in _err(hiplib)
+    # null pointers
+    rc = hiplib.yhip_gdn_step(None, P, P, P, P, P, P, 16, 16, 128, F(1e-6), None)
+    assert rc == -22 and "null" in _err(hiplib)
+    rc = hiplib.yhip_gdn_gates(P, None, P, P, P, 4, 16, None)
+    assert rc == -22 and "null" in _err(hiplib)
+    # no tokens is a no-op
+    assert hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 2048, P, 2048, P, P, 0, 16, 16, 128, F(1e-6), None) == 0
+    assert hiplib.yhip_gdn_gates(P, P, P, P, P, 0, 16, None) == 0

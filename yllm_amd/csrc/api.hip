@@ -231,4 +231,63 @@ int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, co
     return done(yhip::launch_prefill(a, (hipStream_t)stream), fn);
 }
 
+static int gdn_common(const char* fn, float* S, float* out, uint32_t out_stride, const float* q, const float* k,
+                      uint32_t qk_stride, const float* v, uint32_t v_stride, const float* gate, const float* beta,
+                      uint32_t T, uint32_t n_k, uint32_t n_v, uint32_t head_dim, float eps, void* stream)
+{
+    if (!S || !out || !q || !k || !v || !gate || !beta) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    if (head_dim != 64 && head_dim != 128) return fail(YHIP_EINVAL, "%s: head_dim %u not in {64,128}", fn, head_dim);
+    if (n_k == 0 || n_v == 0) return fail(YHIP_EINVAL, "%s: need n_k_heads >= 1 and n_v_heads >= 1", fn);
+    if (qk_stride < n_k * head_dim || v_stride < n_v * head_dim || out_stride < n_v * head_dim ||
+        qk_stride % 4 || v_stride % 4 || out_stride % 4)
+        return fail(YHIP_EINVAL, "%s: strides must cover the heads and be multiples of 4", fn);
+    if (((uintptr_t)S | (uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15)
+        return fail(YHIP_EINVAL, "%s: S, q, k, v must be 16-byte aligned", fn);
+    if (T == 0) return done(hipSuccess, "");
+    yhip::GdnArgs a = {};
+    a.S = S;
+    a.out = out;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.gate = gate;
+    a.beta = beta;
+    a.T = T;
+    a.n_k = n_k;
+    a.n_v = n_v;
+    a.D = head_dim;
+    a.qk_stride = qk_stride;
+    a.v_stride = v_stride;
+    a.out_stride = out_stride;
+    a.eps = eps;
+    return done(yhip::launch_gdn(a, (hipStream_t)stream), fn);
+}
+
+int yhip_gdn_step(float* S, float* out, const float* q, const float* k, const float* v, const float* gate,
+                  const float* beta, uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps,
+                  void* stream)
+{
+    return gdn_common("yhip_gdn_step", S, out, n_v_heads * head_dim, q, k, n_k_heads * head_dim, v,
+                      n_v_heads * head_dim, gate, beta, 1, n_k_heads, n_v_heads, head_dim, l2_eps, stream);
+}
+
+int yhip_gdn_chunk(float* S, float* out, uint32_t out_stride, const float* q, const float* k, uint32_t qk_stride,
+                   const float* v, uint32_t v_stride, const float* gate, const float* beta, uint32_t T,
+                   uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps, void* stream)
+{
+    return gdn_common("yhip_gdn_chunk", S, out, out_stride, q, k, qk_stride, v, v_stride, gate, beta, T, n_k_heads,
+                      n_v_heads, head_dim, l2_eps, stream);
+}
+
+int yhip_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt_bias, const float* ssm_a,
+                   uint32_t T, uint32_t n_v_heads, void* stream)
+{
+    const char* fn = "yhip_gdn_gates";
+    if (!beta || !gate || !alpha || !dt_bias || !ssm_a) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    if (n_v_heads == 0) return fail(YHIP_EINVAL, "%s: n_v_heads must be >= 1", fn);
+    if ((uint64_t)T * n_v_heads > 0x7fffffffull) return fail(YHIP_EINVAL, "%s: too many elements", fn);
+    if (T == 0) return done(hipSuccess, "");
+    return done(yhip::launch_gdn_gates(beta, gate, alpha, dt_bias, ssm_a, T, n_v_heads, (hipStream_t)stream), fn);
+}
+
 }  // extern "C"

@@ -60,4 +60,21 @@ struct PrefillArgs {
 };
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
 
+// ---- gdn.hip ----
+struct GdnArgs {
+    float* S;                        // [n_v][D][D] state, S[h][j][i]
+    float* out;                      // [T][out_stride], head h at h*D
+    const float* q;                  // [T][qk_stride], k-head at kh*D
+    const float* k;
+    const float* v;                  // [T][v_stride], v-head h at h*D
+    const float* gate;               // [T][n_v] log-decay
+    const float* beta;               // [T][n_v]
+    uint32_t T, n_k, n_v, D;
+    uint32_t qk_stride, v_stride, out_stride;
+    float eps;                       // <= 0: q, k are already normalised
+};
+hipError_t launch_gdn(const GdnArgs& a, hipStream_t st);
+hipError_t launch_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt, const float* ssm_a,
+                            uint32_t T, uint32_t n_v, hipStream_t st);
+
 }  // namespace yhip

@@ -1,0 +1,100 @@
+"""Host-side mirror of the qwen35 Gated-DeltaNet operators, on HIP.
+
+Names and argument meaning follow the reference (inference/core/matvec.c,
+inference/core/engine.c):
+
+    gdn_gates(alpha, beta, dt_bias, ssm_a)      engine.c:788-793
+    gdn_step(S, q, k, v, gate, beta, n_k)       l2norm (engine.c:826-827) +
+                                                gdn_state_update (matvec.c:975-1004)
+    gdn_chunk(S, q, k, v, gate, beta, n_k)      the same over T tokens in order
+
+S is the fp32 state [n_v, d, d] (S[h, j, :] is column j, the reference's
+transposed storage), updated in place.  Tensors are torch fp32 tensors on the
+GPU; every call goes through libyllm_hip.so on the current stream, with no CPU
+fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import YhipError, check, lib
+
+L2_EPS = 1e-6  # the qwen35 GDN l2norm epsilon (engine.c:826-827 passes the model's norm eps)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _f32_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda or t.dtype != torch.float32:
+            raise YhipError(-22, "GDN tensors must be fp32 on the GPU")
+
+
+def _rows(t: torch.Tensor) -> tuple[int, int]:
+    """(rows, row stride in floats) of a 2-D view with unit inner stride."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise YhipError(-22, "expected a 2-D tensor with contiguous rows")
+    return t.shape[0], t.stride(0)
+
+
+def gdn_gates(alpha: torch.Tensor, beta: torch.Tensor, dt_bias: torch.Tensor, ssm_a: torch.Tensor) -> torch.Tensor:
+    """alpha, beta: [T, n_v] (beta is replaced by sigmoid(beta)); returns the
+    log-decay gate [T, n_v] = softplus(alpha + dt_bias) * ssm_a."""
+    _f32_gpu(alpha, beta, dt_bias, ssm_a)
+    if alpha.dim() == 1:
+        alpha, beta = alpha.unsqueeze(0), beta.unsqueeze(0)
+    if not (alpha.is_contiguous() and beta.is_contiguous()) or alpha.shape != beta.shape:
+        raise YhipError(-22, "gdn_gates: alpha and beta must be contiguous [T, n_v]")
+    T, n_v = alpha.shape
+    if dt_bias.numel() != n_v or ssm_a.numel() != n_v:
+        raise YhipError(-22, "gdn_gates: dt_bias and ssm_a must have n_v elements")
+    gate = torch.empty_like(alpha)
+    check(lib().yhip_gdn_gates(beta.data_ptr(), gate.data_ptr(), alpha.data_ptr(), dt_bias.data_ptr(),
+                               ssm_a.data_ptr(), T, n_v, _stream()))
+    return gate
+
+
+def gdn_chunk(S: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor,
+              beta: torch.Tensor, n_k: int, eps: float = L2_EPS, out: torch.Tensor | None = None) -> torch.Tensor:
+    """T tokens in order.  q, k: [T, >= n_k*d]; v: [T, >= n_v*d]; gate, beta:
+    [T, n_v].  Returns out [T, n_v*d]; S is left at the state after the last
+    token.  eps <= 0 skips the q/k normalisation."""
+    _f32_gpu(S, q, k, v, gate, beta)
+    if S.dim() != 3 or S.shape[1] != S.shape[2] or not S.is_contiguous():
+        raise YhipError(-22, "gdn: S must be contiguous [n_v, d, d]")
+    n_v, d = S.shape[0], S.shape[1]
+    T, qs = _rows(q)
+    Tk, ks = _rows(k)
+    Tv, vs = _rows(v)
+    if Tk != T or Tv != T or ks != qs:
+        raise YhipError(-22, "gdn: q, k, v must have T rows, q and k the same row stride")
+    if gate.shape != (T, n_v) or beta.shape != (T, n_v) or not (gate.is_contiguous() and beta.is_contiguous()):
+        raise YhipError(-22, "gdn: gate and beta must be contiguous [T, n_v]")
+    if out is None:
+        out = torch.empty((T, n_v * d), dtype=torch.float32, device=S.device)
+    _f32_gpu(out)
+    To, os_ = _rows(out)
+    if To != T:
+        raise YhipError(-22, "gdn: out must have T rows")
+    check(lib().yhip_gdn_chunk(S.data_ptr(), out.data_ptr(), os_, q.data_ptr(), k.data_ptr(), qs, v.data_ptr(), vs,
+                               gate.data_ptr(), beta.data_ptr(), T, n_k, n_v, d, float(eps), _stream()))
+    return out
+
+
+def gdn_step(S: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor,
+             beta: torch.Tensor, n_k: int, eps: float = L2_EPS, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One token: q, k [n_k*d], v [n_v*d], gate, beta [n_v]; returns out [n_v*d]."""
+    _f32_gpu(S, q, k, v, gate, beta)
+    if S.dim() != 3 or S.shape[1] != S.shape[2] or not S.is_contiguous():
+        raise YhipError(-22, "gdn: S must be contiguous [n_v, d, d]")
+    n_v, d = S.shape[0], S.shape[1]
+    for t, n in ((q, n_k * d), (k, n_k * d), (v, n_v * d), (gate, n_v), (beta, n_v)):
+        if t.numel() != n or not t.is_contiguous():
+            raise YhipError(-22, "gdn_step: q, k [n_k*d], v [n_v*d], gate, beta [n_v], contiguous")
+    if out is None:
+        out = torch.empty(n_v * d, dtype=torch.float32, device=S.device)
+    check(lib().yhip_gdn_step(S.data_ptr(), out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                              gate.data_ptr(), beta.data_ptr(), n_k, n_v, d, float(eps), _stream()))
+    return out
