@@ -16,8 +16,11 @@ batch of synthetic input, with all inputs resident in HBM:
   decode128k  131072 keys, 32 / 8 heads (config 4), 2 layer caches.
   decode_batch 64 sequences, lengths uniform in [1024, 32768] from seed,
               32 / 8 heads -- one yhip_attn_decode_batch call.
+  gdn4k       one Gated DeltaNet layer over a 4096-token prompt, 16 heads,
+              d_k = d_v = 128, fp32 (the fifth configuration's GDN layer):
+              yhip_gdn_gates + yhip_gdn_chunk from a zero state.
 
-The default line reports prefill2k as `value` and decode32k under
+The default line reports prefill2k as `value`, decode32k and gdn4k under
 "secondary".  The CPU baseline is the oracle restatement of the reference's
 OpenMP loops (oracle/), timed on this host on a bounded sample, and the same
 run checks the GPU output against it (relative L2).
@@ -49,6 +52,12 @@ def synth(seed: int, n: int, first: int = 0) -> np.ndarray:
     from yllm_amd.attention import round_f16, synth_normal
 
     return round_f16(synth_normal(seed, n, 0.5, first))
+
+
+def synth_raw(seed: int, n: int, first: int = 0) -> np.ndarray:
+    from yllm_amd.attention import synth_normal
+
+    return synth_normal(seed, n, 0.5, first)
 
 
 def prefill_flops(L: int, nh: int, hd: int, pos_start: int = 0) -> float:
@@ -244,6 +253,61 @@ def run_decode_batch(nh: int, nkv: int, hd: int, n_seq: int, steps: int, warmup:
     }
 
 
+def gdn_bytes(T: int, n_k: int, n_v: int, d: int) -> float:
+    # q, k, v in, out, gates and beta in, state read + written (fp32)
+    return 4.0 * (T * (2 * n_k * d + 2 * n_v * d + 3 * n_v) + 2 * n_v * d * d)
+
+
+def gdn_flops(T: int, n_v: int, d: int) -> float:
+    return 7.0 * d * d * n_v * T  # decay, two dots, update: the sequential form's count
+
+
+def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
+    import torch
+
+    from yllm_amd.gdn import gdn_chunk, gdn_gates
+
+    dev = torch.device("cuda:0")
+    seed = SEED + 5
+    n = T * n_h * d
+    q = torch.from_numpy(synth_raw(seed, n).reshape(T, n_h * d)).to(dev)
+    k = torch.from_numpy(synth_raw(seed, n, n).reshape(T, n_h * d)).to(dev)
+    v = torch.from_numpy(synth_raw(seed, n, 2 * n).reshape(T, n_h * d)).to(dev)
+    alpha = torch.from_numpy(synth_raw(seed, T * n_h, 3 * n).reshape(T, n_h)).to(dev)
+    beta_raw = torch.from_numpy(synth_raw(seed, T * n_h, 3 * n + T * n_h).reshape(T, n_h)).to(dev)
+    dt = torch.zeros(n_h, device=dev)
+    a = -torch.ones(n_h, device=dev)
+    S = torch.zeros((n_h, d, d), device=dev)
+    beta = torch.empty_like(beta_raw)
+    gate = torch.empty_like(alpha)
+    out = torch.empty((T, n_h * d), device=dev)
+
+    def step(i):
+        S.zero_()
+        beta.copy_(beta_raw)
+        gdn_gates(alpha, beta, dt, a, gate=gate)
+        gdn_chunk(S, q, k, v, gate, beta, n_h, out=out)
+
+    ms, kern_ms = time_steps(step, steps, warmup, out)
+    nbytes, flops = gdn_bytes(T, n_h, n_h, d), gdn_flops(T, n_h, d)
+    t_roof = max(nbytes / HBM_PEAK, flops / MFMA_F16_PEAK)
+    res = {
+        "value": T / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
+        "config": {"workload": f"Gated DeltaNet layer prefill, {T} tokens, {n_h} heads, d_k = d_v = {d}, fp32, "
+                               f"q/k/v/alpha/beta N(0,1)*0.5 seed {hex(seed)}, dt_bias 0, ssm_a -1, "
+                               f"gates + l2norm + recurrence", "tokens": T, "heads": n_h, "head_dim": d},
+        "roofline": {"bound": "hbm", "kernel": "gdn_kernel<%d> (+ gdn_gates_kernel)" % d,
+                     "achieved": nbytes / (kern_ms * 1e-3) / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": t_roof / (kern_ms * 1e-3), "bytes_per_launch": nbytes, "flops_per_launch": flops,
+                     "launch_ms": kern_ms, "traffic": traffic_of(f"gdn{T}"),
+                     "note": "frac = max(bytes/HBM peak, flops/MFMA peak) / measured time"},
+        "gflops": flops / (ms * 1e-3) / 1e9,
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_gdn(q, k, v, alpha, beta_raw, out, T, n_h, d)
+    return res
+
+
 # ---------------------------------------------------------------- CPU leg
 
 def _oracle():
@@ -281,6 +345,30 @@ def cpu_prefill(q, k, v, out, L, nh, nkv, hd):
     return {"value": prefill_flops(L, nh, hd) / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"the whole workload ({L} tokens, all heads), one pass, {dt:.2f} s; effective "
                       f"parallelism <= {nh} heads; {model}",
+            "seconds": dt, "parity_rel_l2": rel_l2(out.cpu().numpy(), want)}
+
+
+def cpu_gdn(q, k, v, alpha, beta_raw, out, T, n_h, d):
+    """The oracle's single-threaded recurrence (the reference's gdn_state_update
+    has no OpenMP) over the whole sequence."""
+    O = _oracle()
+    from oracle_lib import rel_l2
+
+    qn, kn, vn = q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
+    al, br = alpha.cpu().numpy(), beta_raw.cpu().numpy()
+    t0 = time.perf_counter()
+    beta = np.empty_like(br)
+    gate = np.empty_like(al)
+    zeros, ones = np.zeros(n_h, np.float32), -np.ones(n_h, np.float32)
+    for t in range(T):
+        beta[t], gate[t] = O.gdn_gates(al[t], br[t], zeros, ones)
+    S = np.zeros(n_h * d * d, np.float32)
+    _, want, _, _ = O.gdn_sequence(S, qn, kn, vn, gate, beta, T, n_h, d, n_h, d, 1e-6)
+    dt = time.perf_counter() - t0
+    _, model = _host_desc(O)
+    return {"value": T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"the whole workload ({T} tokens, {n_h} heads), one pass, {dt:.2f} s, single thread as "
+                      f"the reference; {model}",
             "seconds": dt, "parity_rel_l2": rel_l2(out.cpu().numpy(), want)}
 
 
@@ -328,9 +416,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="prefill2k",
-                    choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch"])
+                    choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch", "gdn4k"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k secondary line")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k / gdn4k secondary lines")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step from the host instead of replaying a HIP graph (profiling)")
     args = ap.parse_args()
@@ -361,12 +449,15 @@ def main() -> int:
         res = run_decode(32768, 32, 8, 128, 4, 6, args.steps, args.warmup, cpu, "decode32k")
     elif w == "decode128k":
         res = run_decode(131072, 32, 8, 128, 4, 2, args.steps, args.warmup, cpu, "decode128k")
+    elif w == "gdn4k":
+        res = run_gdn(4096, 16, 128, args.steps, args.warmup, cpu)
     else:
         res = run_decode_batch(32, 8, 128, 64, args.steps, args.warmup)
+    dtype = "f32" if w == "gdn4k" else "f16 MFMA, f32 accumulate/softmax"
 
     line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "f16 MFMA, f32 accumulate/softmax", "data": "synthetic",
+            "vs_baseline": None, "dtype": dtype, "data": "synthetic",
             "config": res["config"], "tokens_per_s": res["tokens_per_s"], "roofline": res["roofline"],
             "timing": ("K eager launches" if EAGER else "K steps captured in one HIP graph") +
                       ", timed with HIP events on the launch stream",
@@ -375,7 +466,9 @@ def main() -> int:
         line["cpu_baseline"] = res["cpu_baseline"]
     if w == "prefill2k" and not args.no_secondary:
         sec = run_decode(32768, 32, 8, 128, 4, 6, 200, 20, cpu, "decode32k")
-        line["secondary"] = [{"metric": "attn decode GB/s", **{k: sec[k] for k in sec}}]
+        gdn = run_gdn(4096, 16, 128, 10, 2, cpu)
+        line["secondary"] = [{"metric": "attn decode GB/s", **sec},
+                             {"metric": "GDN prefill tokens/s", "dtype": "f32", **gdn}]
     print(json.dumps(line), flush=True)
     return 0
 

@@ -39,9 +39,11 @@ def _rows(t: torch.Tensor) -> tuple[int, int]:
     return t.shape[0], t.stride(0)
 
 
-def gdn_gates(alpha: torch.Tensor, beta: torch.Tensor, dt_bias: torch.Tensor, ssm_a: torch.Tensor) -> torch.Tensor:
+def gdn_gates(alpha: torch.Tensor, beta: torch.Tensor, dt_bias: torch.Tensor, ssm_a: torch.Tensor,
+              gate: torch.Tensor | None = None) -> torch.Tensor:
     """alpha, beta: [T, n_v] (beta is replaced by sigmoid(beta)); returns the
-    log-decay gate [T, n_v] = softplus(alpha + dt_bias) * ssm_a."""
+    log-decay gate [T, n_v] = softplus(alpha + dt_bias) * ssm_a (written to
+    `gate` when given)."""
     _f32_gpu(alpha, beta, dt_bias, ssm_a)
     if alpha.dim() == 1:
         alpha, beta = alpha.unsqueeze(0), beta.unsqueeze(0)
@@ -50,7 +52,10 @@ def gdn_gates(alpha: torch.Tensor, beta: torch.Tensor, dt_bias: torch.Tensor, ss
     T, n_v = alpha.shape
     if dt_bias.numel() != n_v or ssm_a.numel() != n_v:
         raise YhipError(-22, "gdn_gates: dt_bias and ssm_a must have n_v elements")
-    gate = torch.empty_like(alpha)
+    if gate is None:
+        gate = torch.empty_like(alpha)
+    elif gate.shape != alpha.shape or not gate.is_contiguous():
+        raise YhipError(-22, "gdn_gates: gate must be contiguous [T, n_v]")
     check(lib().yhip_gdn_gates(beta.data_ptr(), gate.data_ptr(), alpha.data_ptr(), dt_bias.data_ptr(),
                                ssm_a.data_ptr(), T, n_v, _stream()))
     return gate
