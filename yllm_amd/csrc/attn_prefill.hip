@@ -5,12 +5,15 @@
 // keys 0..pos_start+b; scores scaled by 1/sqrt(d); softmax; weighted V),
 // with the optional qwen35 sigmoid gate (engine.c:959-960).
 //
-// Tiling.  A workgroup of 4 waves owns 128 consecutive queries of one query
-// head; wave w owns 32 of them.  Keys stream through LDS in tiles of 64
-// (K rows [64][D] and the transposed V^T [D][64] straight from the cache
-// layout), loaded cooperatively one tile ahead into registers.  Workgroups
-// are issued heaviest (latest queries) first so the causal triangle drains
-// evenly.
+// Tiling.  A workgroup owns 128 consecutive queries of one query head; each
+// of its 4-wave key groups (one or two, see prefill_groups) gives wave w 32
+// of them.  Keys stream through LDS in tiles of 64 (K rows [64][D] and V^T
+// [D][64], straight from the cache layout), loaded with buffer
+// instructions into registers -- K two tiles ahead, V one -- and stored to
+// padded LDS rows.  With two groups, group g takes tiles g, g+2, ... and
+// the partial (max, sum, O) of the groups merge through LDS at the end.
+// Workgroups are issued heaviest (latest queries) first so the causal
+// triangle drains evenly.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_f16), everything transposed so that a
 // lane owns one query for the whole kernel:
@@ -27,6 +30,7 @@
 #include "internal.hpp"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace yhip {
 namespace {
@@ -100,8 +104,8 @@ __device__ inline void store_out4(void* out, size_t off, uint32_t dt, f32x4 v)
     }
 }
 
-template <int D>
-__global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(PrefillArgs a)
+template <int D, int NG>
+__global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefill_kernel(PrefillArgs a)
 {
     constexpr int KS = D + 8;     // K tile row stride (halfs), 16 B pad
     constexpr int VS = BN + 8;    // V tile row stride (halfs)
@@ -110,15 +114,20 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
     constexpr int CH = D / 32;    // 16-byte chunks per thread per tile (K and V each)
     constexpr int KCH = D / 8;    // 16-byte chunks per K row
     constexpr float kSlack = 8.0f;
-    // K and V tiles are double buffered separately: K is staged two tiles
-    // ahead (the score MFMAs of tile kt+1 run during the softmax of tile kt),
-    // V one tile ahead; every buffer is rewritten only after the barrier that
-    // ends its last reader's tile, so one barrier per tile suffices (plus one
-    // in the first tile, after the prologue's scores of tile 0).
-    __shared__ _Float16 Kl[2][BN * KS];
-    __shared__ _Float16 Vl[2][D * VS];
+    // NG key groups of 4 waves share the workgroup's 128 queries: group g
+    // walks key tiles g, g+NG, g+2NG, ... with its own LDS buffers, and the
+    // groups' partial results are merged at the end, so the longest chain
+    // of dependent tiles a wave walks is 1/NG of the causal row.  Within a
+    // group K is staged two of its tiles ahead (the score MFMAs of its next
+    // tile run during the softmax of the current one) and V one tile ahead,
+    // each double buffered; every buffer is rewritten only after the
+    // barrier that ends its last reader's step, so one barrier per step
+    // suffices (plus one in the first step, after the prologue's scores).
+    __shared__ _Float16 Kl[2][NG][BN * KS];
+    __shared__ _Float16 Vl[2][NG][D * VS];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int grp = tid >> 8, gtid = tid & 255, wave = gtid >> 6;
     const int r32 = lane & 31, hh = lane >> 5;
 
     const uint32_t nqb = (a.B + BM - 1) / BM;
@@ -130,6 +139,9 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
     const uint32_t qlast = min(a.B, qi0 + BM) - 1;
     const uint32_t kmax = a.pos_start + qlast;  // last key any query here reads
     const uint32_t ntiles = kmax / BN + 1;
+    const uint32_t nsteps = (ntiles + NG - 1) / NG;  // loop steps (workgroup-uniform)
+    // this group's tiles: kt = grp + NG*st for st < gsteps
+    const uint32_t gsteps = ntiles > (uint32_t)grp ? (ntiles - grp + NG - 1) / NG : 0;
 
     const uint32_t wq0 = qi0 + wave * 32;
     const bool wave_active = wq0 < a.B;
@@ -137,8 +149,10 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
     const uint32_t wpos_last = a.pos_start + min(wq0 + 31, a.B - 1);
     const uint32_t my_pos = a.pos_start + wq0 + r32;
     const uint32_t my_q = min(wq0 + r32, a.B - 1);
-    // tiles this wave computes: 0 .. wtiles-1
+    // tiles this wave computes: 0 .. wtiles-1, of which this group's are st < wsteps
     const uint32_t wtiles = wave_active ? wpos_last / BN + 1 : 0;
+    const uint32_t wsteps = wtiles > (uint32_t)grp ? (wtiles - grp + NG - 1) / NG : 0;
+    auto tile_of = [&](uint32_t st) { return (uint32_t)grp + NG * st; };
 
     f16x8 qf[NKK];
     {
@@ -158,7 +172,7 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
     int kgo[CH], klo[CH], vlo[CH], vkey[CH];
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
-        const int c = tid + 256 * i;
+        const int c = gtid + 256 * i;
         const int row = c / KCH, col = c % KCH;
         kgo[i] = (row * D + col * 8) * 2;
         klo[i] = lds_row_of_key(row) * KS + col * 8;
@@ -168,22 +182,24 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
         vlo[i] = (r >> 2) * VS + vkey[i];
     }
     u32x4 kreg[CH], vreg[CH];
-    auto load_k = [&](uint32_t kt) {
+    auto load_k = [&](uint32_t st) {
+        const uint32_t off = tile_of(st) * BN * D * 2;
 #pragma unroll
         for (int i = 0; i < CH; ++i)
-            kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rK, kgo[i], kt * BN * D * 2, 0));
+            kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rK, kgo[i], off, 0));
     };
-    auto load_v = [&](uint32_t kt) {
+    auto load_v = [&](uint32_t st) {
+        const uint32_t off = tile_of(st) * BN * D * 2;
 #pragma unroll
         for (int i = 0; i < CH; ++i)
-            vreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rV, tid * 16 + i * 4096, kt * BN * D * 2, 0));
+            vreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rV, gtid * 16 + i * 4096, off, 0));
     };
     auto store_k = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < CH; ++i) *reinterpret_cast<u32x4*>(&Kl[buf][klo[i]]) = kreg[i];
+        for (int i = 0; i < CH; ++i) *reinterpret_cast<u32x4*>(&Kl[buf][grp][klo[i]]) = kreg[i];
     };
-    auto store_v = [&](int buf, uint32_t kt) {
-        const uint32_t k0 = kt * BN;
+    auto store_v = [&](int buf, uint32_t st) {
+        const uint32_t k0 = tile_of(st) * BN;
         const bool tail = k0 + BN - 1 > kmax;
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
@@ -197,20 +213,23 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
                     else if (key + 1 > kmax) v[e] &= 0xffffu;
                 }
             }
-            *reinterpret_cast<u32x4*>(&Vl[buf][vlo[i]]) = v;
+            *reinterpret_cast<u32x4*>(&Vl[buf][grp][vlo[i]]) = v;
         }
     };
 
-    float m = -INFINITY, l = 0.0f;
+    // running max (log2 domain): finite so that a tile whose keys are all in
+    // the lane's future (possible as a group's first tile) leaves l and O at
+    // zero instead of forming -inf - -inf
+    float m = -1e30f, l = 0.0f;
     f32x16 o[NDB];
 #pragma unroll
     for (int b = 0; b < NDB; ++b)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
 
-    // scores of tile kt into S (both 32-key halves)
-    auto qk = [&](f32x16 (&S)[2], uint32_t kt) {
-        const _Float16* kr = &Kl[kt & 1][r32 * KS + hh * 8];
+    // scores of step st's tile into S (both 32-key halves)
+    auto qk = [&](f32x16 (&S)[2], uint32_t st) {
+        const _Float16* kr = &Kl[st & 1][grp][r32 * KS + hh * 8];
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
@@ -245,19 +264,19 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
             pf[i >> 3][i & 7] = (_Float16)p;
         }
     };
-    auto pv = [&](const f16x8 (&pf)[4], uint32_t kt) {
-        const _Float16* vr = &Vl[kt & 1][r32 * VS + hh * 8];
+    auto pv = [&](const f16x8 (&pf)[4], uint32_t st) {
+        const _Float16* vr = &Vl[st & 1][grp][r32 * VS + hh * 8];
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
             for (int b = 0; b < NDB; ++b)  // independent accumulators back to back
                 o[b] = mfma32(*reinterpret_cast<const f16x8*>(vr + b * 32 * VS + kc * 16), pf[kc], o[b]);
     };
-    // scores of tile kt into Snext while the probabilities of Scur are formed:
-    // each score MFMA is followed by the exp2 work it can hide
-    auto qk_probs = [&](f32x16 (&Snext)[2], uint32_t kt, const f32x16 (&Scur)[2], f16x8 (&pf)[4]) {
+    // scores of step st's tile into Snext while the probabilities of Scur are
+    // formed: each score MFMA is followed by the exp2 work it can hide
+    auto qk_probs = [&](f32x16 (&Snext)[2], uint32_t st, const f32x16 (&Scur)[2], f16x8 (&pf)[4]) {
         constexpr int PPM = 32 / (2 * NKK);  // probabilities per MFMA
-        const _Float16* kr = &Kl[kt & 1][r32 * KS + hh * 8];
+        const _Float16* kr = &Kl[st & 1][grp][r32 * KS + hh * 8];
         const float nm = -m;
         // MFMA n = kk*2 + j (halves alternate, so neighbours are independent);
         // its K fragment is read one MFMA ahead
@@ -284,9 +303,10 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
             __builtin_amdgcn_sched_group_barrier(0x002, 4 * PPM, 0);  // softmax work it hides
         }
     };
-    // the diagonal tile: keys beyond the lane's position get -inf
-    auto mask = [&](f32x16 (&S)[2], uint32_t kt) {
-        const uint32_t k0 = kt * BN;
+    // a tile that reaches past the wave's first query: keys beyond the
+    // lane's position get -inf
+    auto mask = [&](f32x16 (&S)[2], uint32_t st) {
+        const uint32_t k0 = tile_of(st) * BN;
         if (k0 + BN - 1 > wpos_first) {
 #pragma unroll
             for (int j = 0; j < 2; ++j)
@@ -296,54 +316,84 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
         }
     };
 
-    // prologue: K(0), V(0), K(1) in LDS; scores of tile 0
-    load_k(0);
-    load_v(0);
-    store_k(0);
-    store_v(0, 0);
-    if (ntiles > 1) {
+    // prologue: the group's first K, V and second K in LDS; scores of step 0
+    if (gsteps > 0) {
+        load_k(0);
+        load_v(0);
+        store_k(0);
+        store_v(0, 0);
+    }
+    if (gsteps > 1) {
         load_k(1);
         store_k(1);
     }
     __syncthreads();
     f32x16 Sa[2], Sb[2];
-    if (wtiles > 0) qk(Sa, 0);
+    if (wsteps > 0) qk(Sa, 0);
 
-    // tile kt: loads K(kt+2), V(kt+1); scores of kt+1 overlap the softmax of
-    // kt; P.V of kt; stores K(kt+2) over K(kt) and V(kt+1) over V(kt-1); one
+    // step st: loads K(st+2), V(st+1); scores of st+1 overlap the softmax of
+    // st; P.V of st; stores K(st+2) over K(st) and V(st+1) over V(st-1); one
     // barrier.  With pos_start not a multiple of 32 a wave's queries straddle
     // a tile boundary, so a tile with a successor may still need the mask.
-    auto step = [&](uint32_t kt, f32x16 (&Scur)[2], f32x16 (&Snext)[2]) {
-        if (kt + 2 < ntiles) load_k(kt + 2);
-        if (kt + 1 < ntiles) load_v(kt + 1);
-        if (kt + 1 < wtiles) {
-            mask(Scur, kt);
+    auto step = [&](uint32_t st, f32x16 (&Scur)[2], f32x16 (&Snext)[2]) {
+        if (st + 2 < gsteps) load_k(st + 2);
+        if (st + 1 < gsteps) load_v(st + 1);
+        if (st + 1 < wsteps) {
+            mask(Scur, st);
             update_max(Scur);
             f16x8 pf[4];
-            qk_probs(Snext, kt + 1, Scur, pf);
-            pv(pf, kt);
-        } else if (kt < wtiles) {
-            mask(Scur, kt);
+            qk_probs(Snext, st + 1, Scur, pf);
+            pv(pf, st);
+        } else if (st < wsteps) {
+            mask(Scur, st);
             update_max(Scur);
             f16x8 pf[4];
             probs(Scur, pf);
-            pv(pf, kt);
+            pv(pf, st);
         }
-        if (kt + 2 < ntiles) {
-            // K(0)'s last reader is the prologue's score pass, which no
-            // barrier separates from this store yet
-            if (kt == 0) __syncthreads();
-            store_k(kt & 1);
-        }
-        if (kt + 1 < ntiles) store_v((kt + 1) & 1, kt + 1);
+        // K(0)'s last reader is the prologue's score pass, which no barrier
+        // separates from the first store over it
+        if (st == 0) __syncthreads();
+        if (st + 2 < gsteps) store_k(st & 1);
+        if (st + 1 < gsteps) store_v((st + 1) & 1, st + 1);
         __syncthreads();
     };
-    for (uint32_t kt = 0; kt < ntiles; kt += 2) {
-        step(kt, Sa, Sb);
-        if (kt + 1 < ntiles) step(kt + 1, Sb, Sa);
+    for (uint32_t st = 0; st < nsteps; st += 2) {
+        step(st, Sa, Sb);
+        if (st + 1 < nsteps) step(st + 1, Sb, Sa);
     }
 
     l += __shfl_xor(l, 32, 64);
+    if (NG > 1) {
+        // groups 1..NG-1 hand (m, l, O) to group 0 through LDS; the tile
+        // buffers are free after the last step's barrier
+        constexpr int NV = NDB * 16 + 2;  // floats per lane
+        static_assert(NV * 256 * 4 * (NG - 1) <= (int)sizeof(Kl), "merge area");
+        float* xo = reinterpret_cast<float*>(&Kl[0][0][0]) + (size_t)(grp > 0 ? grp - 1 : 0) * NV * 256;
+        if (grp > 0) {
+            xo[gtid] = m;
+            xo[256 + gtid] = l;
+#pragma unroll
+            for (int b = 0; b < NDB; ++b)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) xo[(2 + b * 16 + i) * 256 + gtid] = o[b][i];
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int g = 1; g < NG; ++g) {
+            const float* xi = reinterpret_cast<const float*>(&Kl[0][0][0]) + (size_t)(g - 1) * NV * 256;
+            const float m1 = xi[gtid], l1 = xi[256 + gtid];
+            const float mg = fmaxf(m, m1);
+            const float a0 = fast_exp2(m - mg), a1 = fast_exp2(m1 - mg);
+            m = mg;
+            l = l * a0 + l1 * a1;
+#pragma unroll
+            for (int b = 0; b < NDB; ++b)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[b][i] = o[b][i] * a0 + xi[(2 + b * 16 + i) * 256 + gtid] * a1;
+        }
+    }
     if (!wave_active) return;
     const uint32_t qi = wq0 + r32;
     if (qi >= a.B) return;
@@ -366,22 +416,49 @@ __global__ __launch_bounds__(256, (D <= 128 ? 2 : 1)) void prefill_kernel(Prefil
     }
 }
 
-template <int D>
+template <int D, int NG>
 hipError_t launch_prefill_d(const PrefillArgs& a, hipStream_t st)
 {
     const uint32_t nqb = (a.B + BM - 1) / BM;
-    hipLaunchKernelGGL(prefill_kernel<D>, dim3(nqb * a.n_heads), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<D, NG>), dim3(nqb * a.n_heads), dim3(256 * NG), 0, st, a);
     return hipGetLastError();
+}
+
+// Key groups per workgroup.  Two groups halve the longest chain of tiles a
+// wave walks, which is what bounds a grid that fills the machine only once
+// (2048 tokens x 28 heads: 448 workgroups on 256 CUs, 420 -> 479 TFLOP/s);
+// with many workgroups per CU two independent 4-wave workgroups hide latency
+// better than one 8-wave workgroup under one barrier (8192 tokens: 888 vs
+// 790 TFLOP/s).  Two groups need the LDS of two groups' tiles (head_dim <=
+// 128).  YHIP_PREFILL_NG=1/2 forces the choice for comparisons.
+int prefill_groups(const PrefillArgs& a)
+{
+    static const int env = [] {
+        const char* e = getenv("YHIP_PREFILL_NG");
+        return e ? atoi(e) : 0;
+    }();
+    static const int n_cu = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    if (a.D > 128) return 1;
+    if (env == 1 || env == 2) return env;
+    const uint64_t wgs = (uint64_t)((a.B + BM - 1) / BM) * a.n_heads;
+    return wgs <= 2 * (uint64_t)n_cu ? 2 : 1;
 }
 
 }  // namespace
 
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st)
 {
+    const int ng = prefill_groups(a);
     switch (a.D) {
-    case 64: return launch_prefill_d<64>(a, st);
-    case 128: return launch_prefill_d<128>(a, st);
-    case 256: return launch_prefill_d<256>(a, st);
+    case 64: return ng == 2 ? launch_prefill_d<64, 2>(a, st) : launch_prefill_d<64, 1>(a, st);
+    case 128: return ng == 2 ? launch_prefill_d<128, 2>(a, st) : launch_prefill_d<128, 1>(a, st);
+    case 256: return launch_prefill_d<256, 1>(a, st);
     default: return hipErrorInvalidValue;
     }
 }
