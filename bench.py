@@ -46,6 +46,7 @@ MFMA_F16_PEAK = 2.5e15   # FLOP/s, dense f16/bf16 MFMA
 METRIC = "attn decode GB/s (% HBM peak); prefill attn TFLOP/s (% MFMA peak)"
 SEED = 0x5EED0000
 EAGER = False  # --eager: launch each step from the host (for counter collection)
+CHUNKED_GDN = True  # --gdn-tokenwise: time the token-by-token GDN kernel instead
 
 
 def synth(seed: int, n: int, first: int = 0) -> np.ndarray:
@@ -265,7 +266,7 @@ def gdn_flops(T: int, n_v: int, d: int) -> float:
 def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
     import torch
 
-    from yllm_amd.gdn import gdn_chunk, gdn_gates
+    from yllm_amd.gdn import gdn_chunk, gdn_chunk_workspace_bytes, gdn_gates
 
     dev = torch.device("cuda:0")
     seed = SEED + 5
@@ -281,12 +282,13 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
     beta = torch.empty_like(beta_raw)
     gate = torch.empty_like(alpha)
     out = torch.empty((T, n_h * d), device=dev)
+    ws = torch.empty(max(gdn_chunk_workspace_bytes(T, n_h, d) // 4, 1), device=dev)
 
     def step(i):
         S.zero_()
         beta.copy_(beta_raw)
         gdn_gates(alpha, beta, dt, a, gate=gate)
-        gdn_chunk(S, q, k, v, gate, beta, n_h, out=out)
+        gdn_chunk(S, q, k, v, gate, beta, n_h, out=out, workspace=ws, chunked=CHUNKED_GDN)
 
     ms, kern_ms = time_steps(step, steps, warmup, out)
     nbytes, flops = gdn_bytes(T, n_h, n_h, d), gdn_flops(T, n_h, d)
@@ -295,8 +297,11 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
         "value": T / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
         "config": {"workload": f"Gated DeltaNet layer prefill, {T} tokens, {n_h} heads, d_k = d_v = {d}, fp32, "
                                f"q/k/v/alpha/beta N(0,1)*0.5 seed {hex(seed)}, dt_bias 0, ssm_a -1, "
-                               f"gates + l2norm + recurrence", "tokens": T, "heads": n_h, "head_dim": d},
-        "roofline": {"bound": "hbm", "kernel": "gdn_kernel<%d> (+ gdn_gates_kernel)" % d,
+                               f"gates + l2norm + recurrence ({'chunked' if CHUNKED_GDN else 'token by token'})",
+                   "tokens": T, "heads": n_h, "head_dim": d},
+        "roofline": {"bound": "hbm",
+                     "kernel": ("gdn_prep_kernel<%d> + gdn_scan_kernel<%d>" % (d, d) if CHUNKED_GDN else
+                                "gdn_kernel<%d>" % d) + " (+ gdn_gates_kernel)",
                      "achieved": nbytes / (kern_ms * 1e-3) / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": t_roof / (kern_ms * 1e-3), "bytes_per_launch": nbytes, "flops_per_launch": flops,
                      "launch_ms": kern_ms, "traffic": traffic_of(f"gdn{T}"),
@@ -419,11 +424,14 @@ def main() -> int:
                     choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch", "gdn4k"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k / gdn4k secondary lines")
+    ap.add_argument("--gdn-tokenwise", action="store_true",
+                    help="gdn4k: time the token-by-token recurrence instead of the chunked form")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step from the host instead of replaying a HIP graph (profiling)")
     args = ap.parse_args()
-    global EAGER
+    global EAGER, CHUNKED_GDN
     EAGER = args.eager
+    CHUNKED_GDN = not args.gdn_tokenwise
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

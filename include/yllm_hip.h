@@ -156,10 +156,20 @@ int yhip_gdn_step(float* S, float* out, const float* q, const float* k, const fl
  * engine.c:723-734, for the recurrence part): rows of q/k are qk_stride
  * floats apart, v rows v_stride, out rows out_stride (multiples of 4); gate
  * and beta are [T][n_v_heads].  S is updated in place to the state after
- * token T-1; out row t is the output of token t. */
+ * token T-1; out row t is the output of token t.
+ *
+ * With a workspace of yhip_gdn_chunk_workspace(T, n_v_heads, head_dim)
+ * bytes (16-byte aligned, no initialisation) and T >= 64, the chunked form
+ * runs: 64-token chunks are reduced in parallel to matrix products (fp32
+ * MFMA) and only the chunk-to-chunk state hand-over is sequential.  With
+ * workspace NULL (or T < 64) the recurrence runs token by token. */
 int yhip_gdn_chunk(float* S, float* out, uint32_t out_stride, const float* q, const float* k, uint32_t qk_stride,
                    const float* v, uint32_t v_stride, const float* gate, const float* beta, uint32_t T,
-                   uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps, void* stream);
+                   uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of the chunked form for T tokens (0 when T < 64). */
+size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_dim);
 
 /* The GDN gates of T tokens (engine.c:788-793), in place like the engine:
  * beta[t][h] <- 1/(1+exp(-beta[t][h])), gate[t][h] <- log1p(exp(alpha[t][h]

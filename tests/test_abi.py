@@ -123,13 +123,14 @@ def test_synth_normal_is_splitmix_box_muller(hiplib, golden):
 def test_gdn_rejects_bad_args(hiplib):
     F = ctypes.c_float
     # head_dim outside {64, 128}
-    rc = hiplib.yhip_gdn_chunk(P, P, 4096, P, P, 4096, P, 4096, P, P, 8, 16, 16, 256, F(1e-6), None)
+    rc = hiplib.yhip_gdn_chunk(P, P, 4096, P, P, 4096, P, 4096, P, P, 8, 16, 16, 256, F(1e-6), None, 0, None)
     assert rc == -22 and "head_dim" in _err(hiplib)
     # strides that do not cover the heads
-    rc = hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 1024, P, 2048, P, P, 8, 16, 16, 128, F(1e-6), None)
+    rc = hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 1024, P, 2048, P, P, 8, 16, 16, 128, F(1e-6), None, 0, None)
     assert rc == -22 and "strides" in _err(hiplib)
     # misaligned q
-    rc = hiplib.yhip_gdn_chunk(P, P, 2048, ctypes.c_void_p(0x1004), P, 2048, P, 2048, P, P, 8, 16, 16, 128, F(1e-6), None)
+    rc = hiplib.yhip_gdn_chunk(P, P, 2048, ctypes.c_void_p(0x1004), P, 2048, P, 2048, P, P, 8, 16, 16, 128, F(1e-6),
+                               None, 0, None)
     assert rc == -22 and "aligned" in _err(hiplib)
     # null pointers
     rc = hiplib.yhip_gdn_step(None, P, P, P, P, P, P, 16, 16, 128, F(1e-6), None)
@@ -137,5 +138,10 @@ def test_gdn_rejects_bad_args(hiplib):
     rc = hiplib.yhip_gdn_gates(P, None, P, P, P, 4, 16, None)
     assert rc == -22 and "null" in _err(hiplib)
     # no tokens is a no-op
-    assert hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 2048, P, 2048, P, P, 0, 16, 16, 128, F(1e-6), None) == 0
+    assert hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 2048, P, 2048, P, P, 0, 16, 16, 128, F(1e-6), None, 0, None) == 0
+    # a workspace that is too small for the chunked form
+    rc = hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 2048, P, 2048, P, P, 128, 16, 16, 128, F(1e-6), P, 4096, None)
+    assert rc == -28 and "workspace" in _err(hiplib)
+    assert hiplib.yhip_gdn_chunk_workspace(63, 16, 128) == 0
+    assert hiplib.yhip_gdn_chunk_workspace(4096, 16, 128) == 64 * 16 * (3 * 64 * 128 + 64 * 64 + 64 * 128 + 4) * 4
     assert hiplib.yhip_gdn_gates(P, P, P, P, P, 0, 16, None) == 0

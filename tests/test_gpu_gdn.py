@@ -77,59 +77,68 @@ def test_gdn_step_matches_oracle(cuda, oracle, n_k, n_v, d):
     assert e_o <= TOL and e_s <= TOL
 
 
-@pytest.mark.parametrize("T,n_k,n_v,d", [(1, 16, 16, 128), (31, 16, 16, 128), (33, 4, 8, 128), (100, 2, 4, 64),
-                                         (300, 16, 16, 128)])
-def test_gdn_chunk_matches_oracle(cuda, oracle, T, n_k, n_v, d):
+@pytest.mark.parametrize("chunked", [False, True], ids=["tokenwise", "chunked"])
+@pytest.mark.parametrize("T,n_k,n_v,d", [(1, 16, 16, 128), (31, 16, 16, 128), (33, 4, 8, 128), (64, 16, 16, 128),
+                                         (65, 2, 4, 64), (100, 2, 4, 64), (130, 4, 2, 128), (300, 16, 16, 128)])
+def test_gdn_chunk_matches_oracle(cuda, oracle, T, n_k, n_v, d, chunked):
     from yllm_amd.gdn import gdn_chunk
 
     q, k, v, alpha, beta_raw, S0 = inputs(200 + T, T, n_k, n_v, d, s0_scale=0.02)
     beta, gate = oracle_gates(oracle, alpha, beta_raw, np.zeros(n_v, np.float32), -np.ones(n_v, np.float32))
     S_want, o_want, _, _ = oracle.gdn_sequence(S0.ravel(), q, k, v, gate, beta, T, n_k, d, n_v, d, EPS)
     S, qd, kd, vd, gd, bd = to_dev(cuda, S0, q, k, v, gate, beta)
-    out = gdn_chunk(S, qd, kd, vd, gd, bd, n_k, EPS).cpu().numpy()
+    out = gdn_chunk(S, qd, kd, vd, gd, bd, n_k, EPS, chunked=chunked).cpu().numpy()
     e_o, e_s = rel_l2(out, o_want), rel_l2(S.cpu().numpy().ravel(), S_want)
     rows = max(rel_l2(out[t], o_want[t]) for t in range(T))
-    print(f"gdn chunk T={T} {n_k}/{n_v} d={d}: out {e_o:.3e} (worst row {rows:.3e}) state {e_s:.3e}")
+    print(f"gdn chunk T={T} {n_k}/{n_v} d={d} chunked={chunked}: out {e_o:.3e} (worst row {rows:.3e}) "
+          f"state {e_s:.3e}")
     assert e_o <= TOL and e_s <= TOL and rows <= 3 * TOL
 
 
-def test_gdn_chunk_interleaved_layout_and_prenormalised(cuda, oracle):
+@pytest.mark.parametrize("chunked", [False, True], ids=["tokenwise", "chunked"])
+def test_gdn_chunk_interleaved_layout_and_prenormalised(cuda, oracle, chunked):
     """q, k, v as slices of one [T, conv_channels] row (the engine's qkv
     buffer, engine.c:820-823) and q/k normalised by the caller (eps <= 0)."""
     from yllm_amd.gdn import gdn_chunk
 
-    T, n_k, n_v, d = 45, 2, 4, 128
+    T, n_k, n_v, d = 145, 2, 4, 128
     q, k, v, alpha, beta_raw, S0 = inputs(301, T, n_k, n_v, d)
     beta, gate = oracle_gates(oracle, alpha, beta_raw, np.zeros(n_v, np.float32), -np.ones(n_v, np.float32))
     S_want, o_want, qn, kn = oracle.gdn_sequence(S0.ravel(), q, k, v, gate, beta, T, n_k, d, n_v, d, EPS)
     qkv = np.concatenate([qn, kn, v], axis=1)
     (qkv_d, S, gd, bd) = to_dev(cuda, qkv, S0, gate, beta)
     kd0 = n_k * d
-    out = gdn_chunk(S, qkv_d[:, :kd0], qkv_d[:, kd0:2 * kd0], qkv_d[:, 2 * kd0:], gd, bd, n_k, eps=0.0)
+    out = gdn_chunk(S, qkv_d[:, :kd0], qkv_d[:, kd0:2 * kd0], qkv_d[:, 2 * kd0:], gd, bd, n_k, eps=0.0,
+                    chunked=chunked)
     assert rel_l2(out.cpu().numpy(), o_want) <= TOL
     assert rel_l2(S.cpu().numpy().ravel(), S_want) <= TOL
 
 
-def test_gdn_chunk_split_is_exact(cuda):
+@pytest.mark.parametrize("chunked,cut", [(False, 37), (True, 64)], ids=["tokenwise", "chunked"])
+def test_gdn_chunk_split_is_exact(cuda, chunked, cut):
     """Running T tokens in one call or as two calls (state carried in S) gives
-    identical bits: the per-token arithmetic does not depend on how tokens
-    are staged."""
+    identical bits: token by token the arithmetic does not depend on how
+    tokens are staged, and in the chunked form a cut on a chunk boundary
+    leaves every chunk's computation unchanged."""
     from yllm_amd.gdn import gdn_chunk
 
-    T, n_k, n_v, d, cut = 100, 16, 16, 128, 37
+    T, n_k, n_v, d = 200, 16, 16, 128
     q, k, v, alpha, beta_raw, S0 = inputs(400, T, n_k, n_v, d, s0_scale=0.02)
     gate = -np.log1p(np.exp(alpha)).astype(np.float32)
     beta = (1 / (1 + np.exp(-beta_raw))).astype(np.float32)
     Sa, qd, kd, vd, gd, bd = to_dev(cuda, S0, q, k, v, gate, beta)
     Sb = Sa.clone()
-    full = gdn_chunk(Sa, qd, kd, vd, gd, bd, n_k)
-    first = gdn_chunk(Sb, qd[:cut], kd[:cut], vd[:cut], gd[:cut].contiguous(), bd[:cut].contiguous(), n_k)
-    second = gdn_chunk(Sb, qd[cut:], kd[cut:], vd[cut:], gd[cut:].contiguous(), bd[cut:].contiguous(), n_k)
+    full = gdn_chunk(Sa, qd, kd, vd, gd, bd, n_k, chunked=chunked)
+    first = gdn_chunk(Sb, qd[:cut], kd[:cut], vd[:cut], gd[:cut].contiguous(), bd[:cut].contiguous(), n_k,
+                      chunked=chunked)
+    second = gdn_chunk(Sb, qd[cut:], kd[cut:], vd[cut:], gd[cut:].contiguous(), bd[cut:].contiguous(), n_k,
+                       chunked=chunked)
     assert torch.equal(full, torch.cat([first, second]))
     assert torch.equal(Sa, Sb)
 
 
-def test_gdn_full_size_prefill(cuda, oracle):
+@pytest.mark.parametrize("chunked", [False, True], ids=["tokenwise", "chunked"])
+def test_gdn_full_size_prefill(cuda, oracle, chunked):
     """The fifth configuration's GDN layer: 4096 tokens, 16 heads, d = 128."""
     from yllm_amd.gdn import gdn_chunk, gdn_gates
 
@@ -139,7 +148,7 @@ def test_gdn_full_size_prefill(cuda, oracle):
     S_want, o_want, _, _ = oracle.gdn_sequence(S0.ravel(), q, k, v, gate, beta, T, n_k, d, n_v, d, EPS)
     S, qd, kd, vd, al, be = to_dev(cuda, S0, q, k, v, alpha, beta_raw)
     gd = gdn_gates(al, be, *to_dev(cuda, np.zeros(n_v), -np.ones(n_v)))
-    out = gdn_chunk(S, qd, kd, vd, gd, be, n_k).cpu().numpy()
+    out = gdn_chunk(S, qd, kd, vd, gd, be, n_k, chunked=chunked).cpu().numpy()
     e_o, e_s = rel_l2(out, o_want), rel_l2(S.cpu().numpy().ravel(), S_want)
-    print(f"gdn full T={T}: out {e_o:.3e} state {e_s:.3e}")
+    print(f"gdn full T={T} chunked={chunked}: out {e_o:.3e} state {e_s:.3e}")
     assert e_o <= TOL and e_s <= TOL

@@ -233,7 +233,8 @@ int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, co
 
 static int gdn_common(const char* fn, float* S, float* out, uint32_t out_stride, const float* q, const float* k,
                       uint32_t qk_stride, const float* v, uint32_t v_stride, const float* gate, const float* beta,
-                      uint32_t T, uint32_t n_k, uint32_t n_v, uint32_t head_dim, float eps, void* stream)
+                      uint32_t T, uint32_t n_k, uint32_t n_v, uint32_t head_dim, float eps, void* workspace,
+                      size_t workspace_bytes, void* stream)
 {
     if (!S || !out || !q || !k || !v || !gate || !beta) return fail(YHIP_EINVAL, "%s: null pointer", fn);
     if (head_dim != 64 && head_dim != 128) return fail(YHIP_EINVAL, "%s: head_dim %u not in {64,128}", fn, head_dim);
@@ -260,6 +261,15 @@ static int gdn_common(const char* fn, float* S, float* out, uint32_t out_stride,
     a.v_stride = v_stride;
     a.out_stride = out_stride;
     a.eps = eps;
+    // the chunked form runs when a workspace is given and the sequence fills a chunk
+    if (workspace && T >= yhip::gdn_chunk_tokens()) {
+        const size_t need = yhip::gdn_chunk_workspace(T, n_v, head_dim);
+        if (workspace_bytes < need)
+            return fail(YHIP_ENOSPC, "%s: workspace of %zu bytes, need %zu", fn, workspace_bytes, need);
+        if ((uintptr_t)workspace & 15) return fail(YHIP_EINVAL, "%s: workspace must be 16-byte aligned", fn);
+        a.ws = reinterpret_cast<float*>(workspace);
+        a.n_chunks = (T + yhip::gdn_chunk_tokens() - 1) / yhip::gdn_chunk_tokens();
+    }
     return done(yhip::launch_gdn(a, (hipStream_t)stream), fn);
 }
 
@@ -268,15 +278,23 @@ int yhip_gdn_step(float* S, float* out, const float* q, const float* k, const fl
                   void* stream)
 {
     return gdn_common("yhip_gdn_step", S, out, n_v_heads * head_dim, q, k, n_k_heads * head_dim, v,
-                      n_v_heads * head_dim, gate, beta, 1, n_k_heads, n_v_heads, head_dim, l2_eps, stream);
+                      n_v_heads * head_dim, gate, beta, 1, n_k_heads, n_v_heads, head_dim, l2_eps, nullptr, 0,
+                      stream);
 }
 
 int yhip_gdn_chunk(float* S, float* out, uint32_t out_stride, const float* q, const float* k, uint32_t qk_stride,
                    const float* v, uint32_t v_stride, const float* gate, const float* beta, uint32_t T,
-                   uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps, void* stream)
+                   uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps, void* workspace,
+                   size_t workspace_bytes, void* stream)
 {
     return gdn_common("yhip_gdn_chunk", S, out, out_stride, q, k, qk_stride, v, v_stride, gate, beta, T, n_k_heads,
-                      n_v_heads, head_dim, l2_eps, stream);
+                      n_v_heads, head_dim, l2_eps, workspace, workspace_bytes, stream);
+}
+
+size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_dim)
+{
+    if ((head_dim != 64 && head_dim != 128) || T < yhip::gdn_chunk_tokens()) return 0;
+    return yhip::gdn_chunk_workspace(T, n_v_heads, head_dim);
 }
 
 int yhip_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt_bias, const float* ssm_a,

@@ -12,7 +12,11 @@
 // Columns never interact, so the state parallelises over (head, column)
 // without communication; only the time dimension is sequential.
 //
-// Decomposition.  A workgroup (4 waves) owns 64 columns of one head for the
+// Two forms.  The token-by-token kernel (gdn_kernel) serves decode steps,
+// short sequences and callers without a workspace; the chunked form below
+// (gdn_prep_kernel + gdn_scan_kernel) serves prefill.
+//
+// Token by token.  A workgroup (4 waves) owns 64 columns of one head for the
 // whole sequence; lane l holds column j0+l and wave w the d_k slice
 // [w*D/4, (w+1)*D/4) of it, in registers (32 floats at D = 128).  Inputs are
 // staged through LDS in chunks of 32 tokens, double buffered (the next
@@ -203,6 +207,344 @@ __global__ __launch_bounds__(256, 1) void gdn_kernel(GdnArgs a)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Chunked form.  For a chunk of kC tokens t = 0..kC-1 starting from the
+// state M0 (M[j][i] = S[h][j][i], d_v x d_k), with cumulative log-decays
+// G_t = sum_{s<=t} gate_s, gamma_t = exp(G_t) and e_t = exp(G_last - G_t),
+// the per-token recurrence unrolls to
+//     (I + A) Delta = diag(beta) V - diag(beta*gamma) K M0^T
+//     A[t][s] = beta_t exp(G_t - G_s) (k_t . k_s)            s < t
+//     O       = diag(gamma) Q M0^T + P Delta,  P[t][s] = exp(G_t - G_s) (q_t . k_s), s <= t
+//     M_last  = gamma_last M0 + Delta^T diag(e) K
+// (rows of Delta, V, K, Q, O are tokens).  With T = (I + A)^-1, U = T
+// diag(beta) V and W = T diag(beta*gamma) K, Delta = U - W M0^T.
+// gdn_prep_kernel computes, for every (v-head, chunk) at once, W, Q~ =
+// diag(gamma) Q, K~ = diag(e) K, P, U and gamma_last; gdn_scan_kernel then
+// walks the chunks in order with the state slice of 16 rows in LDS:
+// R = W M^T and Q~ M^T (one MFMA pass over [W; Q~]), Delta = U - R,
+// O = Q~ M^T + P Delta, M <- gamma_last M + Delta^T K~.  All products are
+// fp32 MFMA (v_mfma_f32_16x16x4_f32) with fp32 accumulation.
+constexpr int kC = 64;  // tokens per chunk of the chunked form
+
+__device__ inline f32x4 mfma_f32(float a, float b, const f32x4& c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int D>
+struct ChunkWs {
+    // per (v-head, chunk): [W; Q~] [2kC][D], K~ [kC][D], P [kC][kC], U [kC][D], gamma_last (+3 pad)
+    static constexpr size_t floats = (size_t)2 * kC * D + (size_t)kC * D + (size_t)kC * kC + (size_t)kC * D + 4;
+    float* WQ;
+    float* Kt;
+    float* P;
+    float* U;
+    float* gl;
+    __device__ ChunkWs(float* ws, uint32_t h, uint32_t c, uint32_t n_chunks)
+    {
+        WQ = ws + ((size_t)h * n_chunks + c) * floats;
+        Kt = WQ + 2 * kC * D;
+        P = Kt + kC * D;
+        U = P + kC * kC;
+        gl = U + kC * D;
+    }
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs a)
+{
+    constexpr int KP = D + 4;  // LDS row stride of the q / k rows (16-byte rows, staggered banks)
+    constexpr int AP = kC + 4;
+    constexpr int KQ = D / 4;  // contraction indices per lane group in the Gram MFMAs
+    __shared__ float Kn[kC][KP];
+    __shared__ float Qn[kC][KP];
+    __shared__ float Am[kC][AP];
+    __shared__ float sg[kC], sb[kC], sgam[kC], see[kC];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const uint32_t c = blockIdx.x, h = blockIdx.y, kh = h % a.n_k;
+    const uint32_t t0 = c * kC;
+    const int nt = (int)min((uint32_t)kC, a.T - t0);
+    ChunkWs<D> w(a.ws, h, c, a.n_chunks);
+
+    // q and k rows of the chunk (zero past the last token): all loads issued
+    // before any LDS store
+    {
+        constexpr int NE = kC * D / 4 / 256;
+        f32x4 kv[NE], qv[NE];
+#pragma unroll
+        for (int u = 0; u < NE; ++u) {
+            const int e = tid + 256 * u, t = e / (D / 4), i = (e % (D / 4)) * 4;
+            const size_t off = (size_t)(t0 + min(t, nt - 1)) * a.qk_stride + (size_t)kh * D + i;
+            kv[u] = *reinterpret_cast<const f32x4*>(a.k + off);
+            qv[u] = *reinterpret_cast<const f32x4*>(a.q + off);
+        }
+#pragma unroll
+        for (int u = 0; u < NE; ++u) {
+            const int e = tid + 256 * u, t = e / (D / 4), i = (e % (D / 4)) * 4;
+            const float keep = t < nt ? 1.0f : 0.0f;
+            *reinterpret_cast<f32x4*>(&Kn[t][i]) = kv[u] * keep;
+            *reinterpret_cast<f32x4*>(&Qn[t][i]) = qv[u] * keep;
+        }
+    }
+    // gates: inclusive prefix sum of the log-decays over the chunk
+    if (wave == 0) {
+        float gv = lane < nt ? a.gate[(size_t)(t0 + lane) * a.n_v + h] : 0.0f;
+        const float bv = lane < nt ? a.beta[(size_t)(t0 + lane) * a.n_v + h] : 0.0f;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float x = __shfl_up(gv, o, 64);
+            if (lane >= o) gv += x;
+        }
+        const float glast = __shfl(gv, 63, 64);
+        sg[lane] = gv;
+        sb[lane] = bv;
+        sgam[lane] = expf(gv);
+        see[lane] = expf(glast - gv);
+        if (lane == 0) w.gl[0] = expf(glast);
+    }
+    __syncthreads();
+    if (a.eps > 0.0f) {
+        for (int row = wave; row < 2 * kC; row += 4) {
+            float* p = row < kC ? Kn[row] : Qn[row - kC];
+            float x[D / 64], ss = 0.0f;
+#pragma unroll
+            for (int u = 0; u < D / 64; ++u) {
+                x[u] = p[lane + 64 * u];
+                ss += x[u] * x[u];
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+            const float rs = 1.0f / fmaxf(sqrtf(ss), a.eps);
+#pragma unroll
+            for (int u = 0; u < D / 64; ++u) p[lane + 64 * u] = x[u] * rs;
+        }
+        __syncthreads();
+    }
+
+    // Gram matrices K K^T and Q K^T; wave w owns token rows 16w..16w+15.
+    // Lane group g contracts over d_k indices g*KQ .. g*KQ+KQ-1.
+    {
+        float ak[KQ], aq[KQ];
+#pragma unroll
+        for (int kb = 0; kb < KQ; kb += 4) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(&Kn[16 * wave + r][g * KQ + kb]);
+            const f32x4 y = *reinterpret_cast<const f32x4*>(&Qn[16 * wave + r][g * KQ + kb]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                ak[kb + e] = x[e];
+                aq[kb + e] = y[e];
+            }
+        }
+        for (int cb = 0; cb < kC / 16; ++cb) {
+            // four independent accumulators per product keep the MFMA pipe full
+            f32x4 skk[4], sqk[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) skk[e] = sqk[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < KQ; kb += 4) {
+                const f32x4 b = *reinterpret_cast<const f32x4*>(&Kn[16 * cb + r][g * KQ + kb]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    skk[e] = mfma_f32(ak[kb + e], b[e], skk[e]);
+                    sqk[e] = mfma_f32(aq[kb + e], b[e], sqk[e]);
+                }
+            }
+            const f32x4 skk_all = (skk[0] + skk[1]) + (skk[2] + skk[3]);
+            const f32x4 sqk_all = (sqk[0] + sqk[1]) + (sqk[2] + sqk[3]);
+            const int s = 16 * cb + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * wave + 4 * g + i;
+                const float dec = s <= t ? expf(sg[t] - sg[s]) : 0.0f;
+                Am[t][s] = s < t ? sb[t] * dec * skk_all[i] : 0.0f;
+                w.P[t * kC + s] = dec * sqk_all[i];
+            }
+        }
+    }
+    __syncthreads();
+
+    // forward substitution (I + A) X = [diag(beta) V | diag(beta*gamma) K],
+    // one right-hand-side column per thread, X kept in registers
+    if (tid < 2 * D) {
+        const int col = tid;
+        float X[kC];
+        // rows past the last token have beta = 0, so their (clamped, valid)
+        // V rows contribute nothing
+        if (col < D) {
+            const float* vp = a.v + (size_t)h * D + col;
+#pragma unroll
+            for (int t = 0; t < kC; ++t) X[t] = vp[(size_t)(t0 + min(t, nt - 1)) * a.v_stride];
+#pragma unroll
+            for (int t = 0; t < kC; ++t) X[t] *= sb[t];
+        } else {
+#pragma unroll
+            for (int t = 0; t < kC; ++t) X[t] = sb[t] * sgam[t] * Kn[t][col - D];
+        }
+        // row t of A is read (broadcast) one row ahead of its use
+        f32x4 cur[kC / 4], nxt[kC / 4];
+#pragma unroll
+        for (int s4 = 0; s4 < kC / 4; ++s4) cur[s4] = *reinterpret_cast<const f32x4*>(&Am[1][4 * s4]);
+#pragma unroll
+        for (int t = 1; t < kC; ++t) {
+            if (t + 1 < kC) {
+#pragma unroll
+                for (int s4 = 0; s4 < kC / 4; ++s4)
+                    if (4 * s4 < t + 1) nxt[s4] = *reinterpret_cast<const f32x4*>(&Am[t + 1][4 * s4]);
+            }
+            float acc[4] = {X[t], 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < t; ++s) acc[s & 3] = fmaf(-cur[s >> 2][s & 3], X[s], acc[s & 3]);
+            X[t] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+            for (int s4 = 0; s4 < kC / 4; ++s4) cur[s4] = nxt[s4];
+        }
+        float* dst = col < D ? w.U + col : w.WQ + (col - D);
+#pragma unroll
+        for (int t = 0; t < kC; ++t) dst[(size_t)t * D] = X[t];
+    }
+
+    // Q~ = diag(gamma) Q (rows kC..2kC-1 of [W; Q~]) and K~ = diag(e) K
+    for (int e = tid; e < kC * D / 4; e += 256) {
+        const int t = e / (D / 4), i = (e % (D / 4)) * 4;
+        const f32x4 q = *reinterpret_cast<const f32x4*>(&Qn[t][i]);
+        const f32x4 k = *reinterpret_cast<const f32x4*>(&Kn[t][i]);
+        *reinterpret_cast<f32x4*>(w.WQ + (size_t)(kC + t) * D + i) = q * sgam[t];
+        *reinterpret_cast<f32x4*>(w.Kt + (size_t)t * D + i) = k * see[t];
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(512) void gdn_scan_kernel(GdnArgs a)
+{
+    constexpr int J = 16;       // state rows (d_v indices) per workgroup
+    constexpr int KQ = D / 4;   // d_k indices per lane group in the [W; Q~] M^T pass
+    constexpr int NCB = D / 16; // 16-wide d_k blocks of the state update (<= 8 waves)
+    constexpr int MP = D + 4;
+    __shared__ float Ml[J][MP];
+    __shared__ float Ol[kC][J + 1], Dl[kC][J + 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;  // 8 waves
+    const int r = lane & 15, g = lane >> 4;
+    constexpr uint32_t nblk = D / J;
+    // workgroup b = slice * n_v + h: consecutive workgroups go to different
+    // XCDs, so the slices of one head (b mod 8 fixed when n_v is a multiple
+    // of 8) share an L2 and read the head's chunk data once
+    const uint32_t h = blockIdx.x % a.n_v, j0 = (blockIdx.x / a.n_v) * J;
+    const float scale = 1.0f / sqrtf((float)D);
+    float* S = a.S + ((size_t)h * D + j0) * D;
+
+    for (int e = tid; e < J * D / 4; e += 512) {
+        const int j = e / (D / 4), i = (e % (D / 4)) * 4;
+        *reinterpret_cast<f32x4*>(&Ml[j][i]) = *reinterpret_cast<const f32x4*>(S + (size_t)j * D + i);
+    }
+
+    // operands of one chunk held in registers; the next chunk's are loaded
+    // while the current one is computed.  Wave w: row block w of [W; Q~]
+    // (phase 1), row block w of P and of U (waves 0-3), d_k block w of K~
+    // (phase 3, waves < NCB).
+    struct Ops {
+        f32x4 wq[KQ / 4];
+        f32x4 p[4];
+        float kt[16];
+        float u[4];
+        float gl;
+    };
+    auto load_ops = [&](Ops& o, uint32_t c) {
+        ChunkWs<D> w(a.ws, h, c, a.n_chunks);
+        const float* arow = w.WQ + (size_t)(16 * wave + r) * D + g * KQ;
+#pragma unroll
+        for (int i = 0; i < KQ / 4; ++i) o.wq[i] = *reinterpret_cast<const f32x4*>(arow + 4 * i);
+        if (wave < 4) {
+            const float* prow = w.P + (size_t)(16 * wave + r) * kC + 16 * g;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o.p[i] = *reinterpret_cast<const f32x4*>(prow + 4 * i);
+        }
+        if (wave < NCB) {
+#pragma unroll
+            for (int kb = 0; kb < 16; ++kb) o.kt[kb] = w.Kt[(size_t)(16 * g + kb) * D + 16 * wave + r];
+        }
+        if (wave < 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o.u[i] = w.U[(size_t)(16 * wave + 4 * g + i) * D + j0 + r];
+        }
+        o.gl = w.gl[0];
+    };
+    Ops cur, nxt;
+    load_ops(cur, 0);
+    __syncthreads();
+
+    for (uint32_t c = 0; c < a.n_chunks; ++c) {
+        const uint32_t t0 = c * kC;
+        const int nt = (int)min((uint32_t)kC, a.T - t0);
+        if (c + 1 < a.n_chunks) load_ops(nxt, c + 1);
+
+        // phase 1: row block `wave` of [W; Q~] times M^T (lane (g, r) supplies
+        // M[j0 + r][g*KQ .. g*KQ+KQ-1] as the B operand); waves 0-3 hold rows
+        // of W M^T and form Delta = U - W M^T directly, waves 4-7 rows of Q~ M^T
+        {
+            f32x4 acc[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < KQ / 4; ++i) {
+                const f32x4 mb = *reinterpret_cast<const f32x4*>(&Ml[r][g * KQ + 4 * i]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = mfma_f32(cur.wq[i][e], mb[e], acc[e]);
+            }
+            const f32x4 x = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * wave + 4 * g + i;
+                if (wave < 4)
+                    Dl[row][r] = cur.u[i] - x[i];
+                else
+                    Ol[row - kC][r] = x[i];
+            }
+        }
+        __syncthreads();
+        // phase 2 (waves 0-3): O = Q~ M^T + P Delta for token rows 16w..16w+15
+        if (wave < 4) {
+            f32x4 acc[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[0][i] = Ol[16 * wave + 4 * g + i][r];
+            acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[e & 1] = mfma_f32(cur.p[i][e], Dl[16 * g + 4 * i + e][r], acc[e & 1]);
+            const f32x4 o = acc[0] + acc[1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * wave + 4 * g + i;
+                if (t < nt) a.out[(size_t)(t0 + t) * a.out_stride + (size_t)h * D + j0 + r] = o[i] * scale;
+            }
+        }
+        // phase 3: M <- gamma_last M + Delta^T K~ for d_k block `wave`; a wave
+        // reads and writes only its own columns of Ml
+        if (wave < NCB) {
+            f32x4 acc[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[0][i] = cur.gl * Ml[4 * g + i][16 * wave + r];
+            acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < 16; ++kb) acc[kb & 1] = mfma_f32(Dl[16 * g + kb][r], cur.kt[kb], acc[kb & 1]);
+            const f32x4 nm = acc[0] + acc[1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Ml[4 * g + i][16 * wave + r] = nm[i];
+        }
+        __syncthreads();
+        if (c + 1 < a.n_chunks) cur = nxt;
+    }
+
+    for (int e = tid; e < J * D / 4; e += 512) {
+        const int j = e / (D / 4), i = (e % (D / 4)) * 4;
+        *reinterpret_cast<f32x4*>(S + (size_t)j * D + i) = *reinterpret_cast<const f32x4*>(&Ml[j][i]);
+    }
+}
+
 // engine.c:788-793: beta <- sigmoid(beta), gate <- softplus(alpha + dt) * a,
 // softplus as log1p(exp(.)) like the reference
 __global__ void gdn_gates_kernel(float* beta, float* gate, const float* alpha, const float* dt,
@@ -218,7 +560,12 @@ __global__ void gdn_gates_kernel(float* beta, float* gate, const float* alpha, c
 template <int D>
 hipError_t launch_gdn_d(const GdnArgs& a, hipStream_t st)
 {
-    hipLaunchKernelGGL(gdn_kernel<D>, dim3(a.n_v * (D / kCols)), dim3(256), 0, st, a);
+    if (a.ws) {
+        hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(a.n_chunks, a.n_v), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(a.n_v * (D / 16)), dim3(512), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(gdn_kernel<D>, dim3(a.n_v * (D / kCols)), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
@@ -232,6 +579,15 @@ hipError_t launch_gdn(const GdnArgs& a, hipStream_t st)
     default: return hipErrorInvalidValue;
     }
 }
+
+size_t gdn_chunk_workspace(uint32_t T, uint32_t n_v, uint32_t D)
+{
+    const size_t n_chunks = (T + kC - 1) / kC;
+    const size_t per = D == 64 ? ChunkWs<64>::floats : ChunkWs<128>::floats;
+    return n_chunks * n_v * per * sizeof(float);
+}
+
+uint32_t gdn_chunk_tokens() { return kC; }
 
 hipError_t launch_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt, const float* ssm_a,
                             uint32_t T, uint32_t n_v, hipStream_t st)

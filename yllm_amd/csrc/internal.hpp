@@ -72,8 +72,13 @@ struct GdnArgs {
     uint32_t T, n_k, n_v, D;
     uint32_t qk_stride, v_stride, out_stride;
     float eps;                       // <= 0: q, k are already normalised
+    float* ws;                       // chunked form: per (v-head, chunk) intermediates, or null
+    uint32_t n_chunks;
 };
 hipError_t launch_gdn(const GdnArgs& a, hipStream_t st);
+// bytes of the chunked form's workspace, and its chunk length in tokens
+size_t gdn_chunk_workspace(uint32_t T, uint32_t n_v, uint32_t D);
+uint32_t gdn_chunk_tokens();
 hipError_t launch_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt, const float* ssm_a,
                             uint32_t T, uint32_t n_v, hipStream_t st);
 

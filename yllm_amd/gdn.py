@@ -61,11 +61,18 @@ def gdn_gates(alpha: torch.Tensor, beta: torch.Tensor, dt_bias: torch.Tensor, ss
     return gate
 
 
+def gdn_chunk_workspace_bytes(T: int, n_v: int, d: int) -> int:
+    return int(lib().yhip_gdn_chunk_workspace(T, n_v, d))
+
+
 def gdn_chunk(S: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor,
-              beta: torch.Tensor, n_k: int, eps: float = L2_EPS, out: torch.Tensor | None = None) -> torch.Tensor:
+              beta: torch.Tensor, n_k: int, eps: float = L2_EPS, out: torch.Tensor | None = None,
+              workspace: torch.Tensor | None = None, chunked: bool = True) -> torch.Tensor:
     """T tokens in order.  q, k: [T, >= n_k*d]; v: [T, >= n_v*d]; gate, beta:
     [T, n_v].  Returns out [T, n_v*d]; S is left at the state after the last
-    token.  eps <= 0 skips the q/k normalisation."""
+    token.  eps <= 0 skips the q/k normalisation.  chunked=True uses the
+    chunked form (with `workspace`, allocated here when not given);
+    chunked=False runs the token-by-token recurrence."""
     _f32_gpu(S, q, k, v, gate, beta)
     if S.dim() != 3 or S.shape[1] != S.shape[2] or not S.is_contiguous():
         raise YhipError(-22, "gdn: S must be contiguous [n_v, d, d]")
@@ -83,8 +90,13 @@ def gdn_chunk(S: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     To, os_ = _rows(out)
     if To != T:
         raise YhipError(-22, "gdn: out must have T rows")
+    ws_bytes = gdn_chunk_workspace_bytes(T, n_v, d) if chunked else 0
+    if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
+        workspace = torch.empty(ws_bytes // 4, dtype=torch.float32, device=S.device)
+    ws_ptr = workspace.data_ptr() if ws_bytes else None
     check(lib().yhip_gdn_chunk(S.data_ptr(), out.data_ptr(), os_, q.data_ptr(), k.data_ptr(), qs, v.data_ptr(), vs,
-                               gate.data_ptr(), beta.data_ptr(), T, n_k, n_v, d, float(eps), _stream()))
+                               gate.data_ptr(), beta.data_ptr(), T, n_k, n_v, d, float(eps), ws_ptr, ws_bytes,
+                               _stream()))
     return out
 
 
