@@ -19,6 +19,9 @@ batch of synthetic input, with all inputs resident in HBM:
   gdn4k       one Gated DeltaNet layer over a 4096-token prompt, 16 heads,
               d_k = d_v = 128, fp32 (the fifth configuration's GDN layer):
               yhip_gdn_gates + yhip_gdn_chunk from a zero state.
+  hybrid      the fifth configuration end to end: 3 GDN layers + 1 gated
+              attention layer (16 / 2 heads, d 256, bf16), 4096-token
+              prefill then 256 decode steps; tokens/s over the whole pass.
 
 The default line reports prefill2k as `value`, decode32k and gdn4k under
 "secondary".  The CPU baseline is the oracle restatement of the reference's
@@ -313,6 +316,77 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
     return res
 
 
+def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
+    """The fifth configuration: one group of 3 Gated-DeltaNet layers and 1
+    gated GQA attention layer, a 4096-token prefill then n_dec decode steps."""
+    import torch
+
+    from yllm_amd.attention import (LayerKV, attn_decode, attn_prefill, decode_workspace, decode_workspace_bytes,
+                                    kv_store)
+    from yllm_amd.gdn import gdn_chunk, gdn_chunk_workspace_bytes, gdn_gates, gdn_step
+
+    dev = torch.device("cuda:0")
+    seed = SEED + 5
+    T, n_gdn, hg, dg = 4096, 3, 16, 128          # GDN: 16 heads, d_k = d_v = 128
+    nh, nkv, da = 16, 2, 256                     # gated attention: 16 / 2 heads, d = 256
+    L = T + n_dec
+    first = [0]
+
+    def draw(n, bf16=False):
+        x = synth_raw(seed, n, first[0])
+        first[0] += n
+        t = torch.from_numpy(x).to(dev)
+        return t.to(torch.bfloat16) if bf16 else t
+
+    gd = [dict(q=draw(L * hg * dg).view(L, -1), k=draw(L * hg * dg).view(L, -1), v=draw(L * hg * dg).view(L, -1),
+               alpha=draw(L * hg).view(L, hg), beta_raw=draw(L * hg).view(L, hg)) for _ in range(n_gdn)]
+    at = dict(q=draw(L * nh * da, True).view(L, -1), gate=draw(L * nh * da).view(L, -1),
+              k=draw(L * nkv * da, True).view(L, -1), v=draw(L * nkv * da, True).view(L, -1))
+    dt = torch.zeros(hg, device=dev)
+    a = -torch.ones(hg, device=dev)
+    S = [torch.zeros((hg, dg, dg), device=dev) for _ in range(n_gdn)]
+    beta = [torch.empty((L, hg), device=dev) for _ in range(n_gdn)]
+    gate = [torch.empty((L, hg), device=dev) for _ in range(n_gdn)]
+    gout = torch.empty((L, hg * dg), device=dev)
+    ws = torch.empty(gdn_chunk_workspace_bytes(T, hg, dg) // 4, device=dev)
+    cache = LayerKV.empty(nkv, da, L, device=dev)
+    aout = torch.empty((L, nh * da), dtype=torch.bfloat16, device=dev)
+    dout = torch.empty(nh * da, device=dev)
+    dws = decode_workspace(decode_workspace_bytes(1, L, L, nh, nkv, da), dev)
+    q_dec = at["q"][T:].float()  # decode queries are fp32 (engine hb2)
+
+    def step(i):
+        for li in range(n_gdn):
+            S[li].zero_()
+            beta[li].copy_(gd[li]["beta_raw"])
+            gdn_gates(gd[li]["alpha"], beta[li], dt, a, gate=gate[li])
+        # prefill
+        for li in range(n_gdn):
+            g = gd[li]
+            gdn_chunk(S[li], g["q"][:T], g["k"][:T], g["v"][:T], gate[li][:T], beta[li][:T], hg,
+                      out=gout[:T], workspace=ws)
+        kv_store(cache, at["k"][:T], at["v"][:T], 0)
+        attn_prefill(at["q"][:T], cache, 0, nh, gate=at["gate"][:T], out=aout[:T])
+        # decode
+        for t in range(T, L):
+            for li in range(n_gdn):
+                g = gd[li]
+                gdn_step(S[li], g["q"][t], g["k"][t], g["v"][t], gate[li][t], beta[li][t], hg, out=gout[t])
+            kv_store(cache, at["k"][t:t + 1], at["v"][t:t + 1], t)
+            attn_decode(q_dec[t - T], cache, t, nh, gate=at["gate"][t], out=dout, workspace=dws)
+
+    ms, _ = time_steps(step, steps, warmup, dout)
+    return {
+        "value": L / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": L / (ms * 1e-3),
+        "config": {"workload": f"qwen35 hybrid group: {n_gdn} Gated-DeltaNet layers ({hg} heads, d {dg}, fp32) + "
+                               f"1 gated attention layer ({nh}/{nkv} heads, d {da}, bf16 q/k/v, sigmoid gate); "
+                               f"{T}-token prefill (chunked GDN, MFMA attention) then {n_dec} decode steps "
+                               f"(GDN steps, KV store, split-K decode) per step; N(0,1)*0.5 seed {hex(seed)}",
+                   "prefill_tokens": T, "decode_steps": n_dec},
+        "roofline": None,
+    }
+
+
 # ---------------------------------------------------------------- CPU leg
 
 def _oracle():
@@ -421,7 +495,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="prefill2k",
-                    choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch", "gdn4k"])
+                    choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch", "gdn4k",
+                             "hybrid"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k / gdn4k secondary lines")
     ap.add_argument("--gdn-tokenwise", action="store_true",
@@ -459,9 +534,12 @@ def main() -> int:
         res = run_decode(131072, 32, 8, 128, 4, 2, args.steps, args.warmup, cpu, "decode128k")
     elif w == "gdn4k":
         res = run_gdn(4096, 16, 128, args.steps, args.warmup, cpu)
+    elif w == "hybrid":
+        res = run_hybrid(args.steps, args.warmup)
     else:
         res = run_decode_batch(32, 8, 128, 64, args.steps, args.warmup)
-    dtype = "f32" if w == "gdn4k" else "f16 MFMA, f32 accumulate/softmax"
+    dtype = {"gdn4k": "f32", "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}.get(
+        w, "f16 MFMA, f32 accumulate/softmax")
 
     line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",

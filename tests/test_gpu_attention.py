@@ -79,6 +79,26 @@ def test_kv_store_bits_match_reference_rounding(cuda, oracle, golden, src):
     assert not Kb[:, rows:].any() and not Vb[:, :, rows:].any()
 
 
+@pytest.mark.parametrize("src", [torch.float32, torch.bfloat16])
+def test_kv_store_few_rows_matches_bulk(cuda, src):
+    """Appending 1-3 rows at a time (the one-launch path) writes the same bits
+    as one bulk store of all rows."""
+    from yllm_amd.attention import LayerKV, kv_store
+
+    n_kv, hd, rows = 2, 128, 70
+    K, V = gen(61, (rows, n_kv * hd), f16=False), gen(62, (rows, n_kv * hd), f16=False)
+    kt, vt = torch.from_numpy(K).to(cuda).to(src), torch.from_numpy(V).to(cuda).to(src)
+    bulk, step = LayerKV.empty(n_kv, hd, rows, device=cuda), LayerKV.empty(n_kv, hd, rows, device=cuda)
+    kv_store(bulk, kt, vt, 0)
+    p, n = 0, 1
+    while p < rows:
+        m = min(n, rows - p)
+        kv_store(step, kt[p:p + m], vt[p:p + m], p)
+        p, n = p + m, n % 3 + 1
+    torch.cuda.synchronize()
+    assert torch.equal(bulk.k, step.k) and torch.equal(bulk.v, step.v)
+
+
 def test_kv_engine_layout_round_trip(cuda, oracle):
     from yllm_amd.attention import LayerKV, kv_from_engine, kv_to_engine
 

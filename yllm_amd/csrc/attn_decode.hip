@@ -371,11 +371,14 @@ size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_
 {
     // A single sequence splits evenly: about one workgroup per CU (256), each
     // streaming an equal run, is fastest (measured at 32k and 128k keys).  A
-    // ragged batch needs finer splits to balance: about 2048 workgroups
-    // (measured 4.7 -> 5.9 TB/s on 64 sequences of 1k..32k keys).  Splits
-    // stay at least 1024 keys long; shorter ones cost more in start-up and
-    // partials than they gain.  YHIP_DECODE_WG / YHIP_DECODE_MINSK override
-    // the workgroup target and the minimum for tuning sweeps.
+    // ragged batch needs finer splits: its workgroups have unequal work and
+    // their count is quantised by the resident slots (512 at d <= 128), so a
+    // split size that leaves a nearly empty last round costs a whole round
+    // (64 sequences of 1k..32k keys: 4.5 TB/s at 2048 workgroups, 5.9 at
+    // 3072).  A split is a multiple of 128 keys (one 32-key block per wave);
+    // short contexts with few kv heads get splits down to 128 keys so they
+    // still spread over many CUs.  YHIP_DECODE_WG / YHIP_DECODE_MINSK
+    // override the workgroup target and the minimum split for tuning sweeps.
     static const long env_wg = [] {
         const char* e = getenv("YHIP_DECODE_WG");
         return e ? atol(e) : 0L;
@@ -383,15 +386,14 @@ size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_
     static const uint64_t min_sk = [] {
         const char* e = getenv("YHIP_DECODE_MINSK");
         const long v = e ? atol(e) : 0;
-        return (uint64_t)(v > 0 ? v : 1024);
+        return (uint64_t)(v > 0 ? v : 128);
     }();
-    const uint64_t target_wg = env_wg > 0 ? (uint64_t)env_wg : (n_seq == 1 ? 256 : 2048);
+    const uint64_t target_wg = env_wg > 0 ? (uint64_t)env_wg : (n_seq == 1 ? 256 : 3072);
     const uint64_t work = total_len * (uint64_t)n_kv;
     uint64_t sk = (work + target_wg - 1) / target_wg;
     if (sk < min_sk) sk = min_sk;
-    sk = (sk + 255) / 256 * 256;  // whole 32-key blocks for each of up to 8 waves
     if (sk < (max_len + kMaxSplits - 1) / kMaxSplits) sk = ((uint64_t)max_len + kMaxSplits - 1) / kMaxSplits;
-    sk = (sk + 255) / 256 * 256;
+    sk = (sk + 127) / 128 * 128;
     uint32_t ns;
     if (sk >= max_len) {
         sk = ((uint64_t)max_len + 31) / 32 * 32;

@@ -12,9 +12,10 @@
 // Columns never interact, so the state parallelises over (head, column)
 // without communication; only the time dimension is sequential.
 //
-// Two forms.  The token-by-token kernel (gdn_kernel) serves decode steps,
-// short sequences and callers without a workspace; the chunked form below
-// (gdn_prep_kernel + gdn_scan_kernel) serves prefill.
+// Three kernels.  A single token (a decode step) runs gdn_step_kernel; the
+// token-by-token kernel (gdn_kernel) serves short sequences and callers
+// without a workspace; the chunked form below (gdn_prep_kernel +
+// gdn_scan_kernel) serves prefill.
 //
 // Token by token.  A workgroup (4 waves) owns 64 columns of one head for the
 // whole sequence; lane l holds column j0+l and wave w the d_k slice
@@ -545,6 +546,81 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(GdnArgs a)
     }
 }
 
+// One token (a decode step).  A workgroup of 256 threads owns 16 columns of
+// one head; the 16 lanes of a column hold D/16 elements each, so both dot
+// products over d_k are a 16-lane butterfly and nothing goes through LDS.
+// All of a lane's loads (state slice, q/k slices, v, gates) are issued
+// together: one memory round trip, then the update, then the stores.
+template <int D>
+__global__ __launch_bounds__(256) void gdn_step_kernel(GdnArgs a)
+{
+    constexpr int SL = D / 16;
+    const int tid = threadIdx.x, part = tid & 15, col = tid >> 4;
+    constexpr uint32_t nblk = D / 16;
+    const uint32_t h = blockIdx.x / nblk, j = (blockIdx.x % nblk) * 16 + col;
+    const uint32_t kh = h % a.n_k;
+    const float scale = 1.0f / sqrtf((float)D);
+    float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
+    const float* kp = a.k + (size_t)kh * D + part * SL;
+    const float* qp = a.q + (size_t)kh * D + part * SL;
+    float s[SL], k[SL], q[SL];
+#pragma unroll
+    for (int i = 0; i < SL; i += 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(Sp + i);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(kp + i);
+        const f32x4 z = *reinterpret_cast<const f32x4*>(qp + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            s[i + e] = x[e];
+            k[i + e] = y[e];
+            q[i + e] = z[e];
+        }
+    }
+    const float vj = a.v[(size_t)h * D + j];
+    const float g = expf(a.gate[h]), bt = a.beta[h];
+    auto sum16 = [](float x) {
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+        return x;
+    };
+    if (a.eps > 0.0f) {
+        float kk = 0.0f, qq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < SL; ++i) {
+            kk += k[i] * k[i];
+            qq += q[i] * q[i];
+        }
+        const float rk = 1.0f / fmaxf(sqrtf(sum16(kk)), a.eps), rq = 1.0f / fmaxf(sqrtf(sum16(qq)), a.eps);
+#pragma unroll
+        for (int i = 0; i < SL; ++i) {
+            k[i] *= rk;
+            q[i] *= rq;
+        }
+    }
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+        s[i] *= g;
+        p = fmaf(s[i], k[i], p);
+    }
+    const float delta = (vj - sum16(p)) * bt;
+    float p2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+        s[i] = fmaf(k[i], delta, s[i]);
+        p2 = fmaf(s[i], q[i], p2);
+    }
+    const float o = sum16(p2) * scale;
+#pragma unroll
+    for (int i = 0; i < SL; i += 4) {
+        f32x4 x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = s[i + e];
+        *reinterpret_cast<f32x4*>(Sp + i) = x;
+    }
+    if (part == 0) a.out[(size_t)h * D + j] = o;
+}
+
 // engine.c:788-793: beta <- sigmoid(beta), gate <- softplus(alpha + dt) * a,
 // softplus as log1p(exp(.)) like the reference
 __global__ void gdn_gates_kernel(float* beta, float* gate, const float* alpha, const float* dt,
@@ -560,7 +636,9 @@ __global__ void gdn_gates_kernel(float* beta, float* gate, const float* alpha, c
 template <int D>
 hipError_t launch_gdn_d(const GdnArgs& a, hipStream_t st)
 {
-    if (a.ws) {
+    if (a.T == 1) {
+        hipLaunchKernelGGL(gdn_step_kernel<D>, dim3(a.n_v * (D / 16)), dim3(256), 0, st, a);
+    } else if (a.ws) {
         hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(a.n_chunks, a.n_v), dim3(256), 0, st, a);
         hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(a.n_v * (D / 16)), dim3(512), 0, st, a);
     } else {

@@ -60,6 +60,23 @@ __global__ __launch_bounds__(256) void v_store_kernel(uint16_t* __restrict__ vc,
     }
 }
 
+// A few rows (decode appends one per step): K and V elements in one launch,
+// one thread per (row, element); the V writes are 2-byte scatters into the
+// tiles, which is cheap at this size and saves the second launch.
+__global__ __launch_bounds__(256) void kv_rows_kernel(uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                      const void* __restrict__ k, const void* __restrict__ v,
+                                                      uint32_t dt, uint32_t pos_start, uint32_t B, uint32_t n_kv,
+                                                      uint32_t D, uint32_t kv_stride)
+{
+    const uint32_t kv_dim = n_kv * D;
+    const uint64_t idx = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (idx >= (uint64_t)B * kv_dim) return;
+    const uint32_t b = (uint32_t)(idx / kv_dim), j = (uint32_t)(idx - (uint64_t)b * kv_dim);
+    const uint32_t h = j / D, d = j - h * D;
+    kc[k_index(h, pos_start + b, d, D, kv_stride)] = to_cache_bits(k, (size_t)b * kv_dim + j, dt);
+    vc[v_index(h, pos_start + b, d, D, kv_stride)] = to_cache_bits(v, (size_t)b * kv_dim + j, dt);
+}
+
 // V tiles -> engine V rows (bits copied)
 __global__ __launch_bounds__(256) void v_to_engine_kernel(uint16_t* __restrict__ ev,
                                                           const uint16_t* __restrict__ vc,
@@ -109,6 +126,10 @@ hipError_t launch_kv_store(uint16_t* kc, uint16_t* vc, const void* k, const void
 {
     const uint32_t kv_dim = n_kv * D;
     dim3 gk((uint32_t)(((uint64_t)B * kv_dim + 255u) / 256u));
+    if (B <= 4) {
+        hipLaunchKernelGGL(kv_rows_kernel, gk, dim3(256), 0, st, kc, vc, k, v, dt, pos_start, B, n_kv, D, kv_stride);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_store_kernel, gk, dim3(256), 0, st, kc, k, dt, pos_start, B, n_kv, D,
                        kv_stride);
     dim3 gv((kv_dim + 63u) / 64u, (B + 63u) / 64u);
