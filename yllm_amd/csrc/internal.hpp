@@ -57,6 +57,7 @@ struct PrefillArgs {
     uint32_t gate_stride;
     uint32_t pos_start, B, n_heads, n_kv, D;
     float c;
+    uint32_t xcd_map;  // set by the launcher: workgroup -> (query block, head) grouped by kv head per XCD
 };
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
 
