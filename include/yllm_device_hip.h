@@ -2,9 +2,10 @@
  *
  * The engine-side half of the boundary: a Device (inference/include/device.h:
  * 37-50) whose load_weights installs per-layer forward functions that run the
- * attention of each block (KV store, decode, causal prefill) on the GPU
- * through libyllm_hip.so and keep the rest of the block on the engine's own
- * CPU operators.  Built inside the reference tree (device_hip.c includes
+ * attention of each block (KV store, decode, causal prefill; for qwen35 also
+ * the Gated-DeltaNet recurrence and the gated attention) on the GPU through
+ * libyllm_hip.so and keep the rest of the block on the engine's own CPU
+ * operators.  Built inside the reference tree (device_hip.c includes
  * yllm.h / device.h / llf.h / matvec.h) and linked with libyllm_hip.so and
  * libamdhip64.
  *
@@ -30,10 +31,12 @@ struct Device;
  * engine.c:360-364) or NULL with a message in err when no usable gfx950
  * device `device_id` exists.  load_weights (bound by engine_bind_device,
  * engine.c:354-384) allocates the HBM KV cache for the engine's layer range
- * and installs fwd_block / fwd_block_batch (yllm.h:115-116); it fails with
- * -1 and a message for shapes the kernels do not take (head_dim not 64, 128
- * or 256; more than 16 query heads per kv head) and for ARCH_QWEN35, so the
- * caller can rebind the CPU device. */
+ * (attention layers) and the HBM recurrent state (qwen35 GDN layers) and
+ * installs fwd_block / fwd_block_batch (yllm.h:115-116); it fails with -1 and
+ * a message for shapes the kernels do not take (head_dim not 64, 128 or 256;
+ * more than 16 query heads per kv head; GDN head dim not 64 or 128), so the
+ * caller can rebind the CPU device.  The GDN state is copied back to
+ * e->ssm_state after every GPU update, so the host state is always current. */
 struct Device* device_create_hip(int device_id, char* err, size_t errlen);
 
 /* KV-cache interface (device.h:58-63 cuda_after_prefill; cache.c:174-247).
@@ -41,8 +44,10 @@ struct Device* device_create_hip(int device_id, char* err, size_t errlen);
  * so host KV is always current after a forward; these two move rows
  * 0..n_pos-1 of every layer of the engine's range between e->kv (engine
  * layout) and the head-major HBM cache.  Call device_hip_kv_from_host after
- * KV was written on the host (sess_kv_load), device_hip_kv_to_host only to
- * rebuild a host copy from HBM.  Return 0 or -1. */
+ * KV was written on the host (sess_kv_load); it also marks every HBM GDN
+ * state stale, so each is re-sent from e->ssm_state by its layer's next
+ * call.  device_hip_kv_to_host only rebuilds a host KV copy from HBM.
+ * Return 0 or -1. */
 int device_hip_kv_from_host(struct Engine* e, uint32_t n_pos);
 int device_hip_kv_to_host(struct Engine* e, uint32_t n_pos);
 

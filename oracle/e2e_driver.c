@@ -19,7 +19,10 @@
  * gets the same routing by running each decode step with device_mode set
  * to DEV_MODE_VULKAN: in a build without Vulkan every Vulkan hook is the
  * CPU stub of device_cpu.c:175-202 (returns -1 or does nothing), so the step
- * is the CPU step except that blocks go through e->fwd_block.  Batched
+ * is the CPU step except that blocks go through e->fwd_block.  The CPU run
+ * takes the same route: for llama / qwen its fwd_block is the CPU block
+ * (engine_fwd_block_at), and for qwen35 it is fwd_block_qwen35, which the
+ * unpatched CPU branch never reaches (it calls the llama block).  Batched
  * prefill already goes through e->fwd_block_batch in DEV_MODE_CPU
  * (engine.c:652).
  */
@@ -51,6 +54,105 @@ static void fill(float* w, size_t n, float a, uint64_t seed)
     }
 }
 
+/* The tensors of a synthetic model on their way to llf_emit. */
+typedef struct {
+    ConvItem* items;
+    void** bufs;
+    int n, cap;
+    uint32_t seed;
+} Items;
+
+/* one tensor of ROWS x COLS (COLS 0 or 1: a vector), uniform in
+ * center +- amp, stored f16 or f32 */
+static int add(Items* t, uint32_t layer, uint32_t slot, const char* name, uint32_t rows, uint32_t cols, int f16,
+               float amp, float center)
+{
+    size_t n = (size_t)rows * (cols > 1 ? cols : 1), j;
+    float* w;
+    ConvItem* it;
+    if (t->n >= t->cap) return -1;
+    w = (float*)malloc(n * 4);
+    if (!w) return -1;
+    it = &t->items[t->n];
+    fill(w, n, amp, (uint64_t)t->seed * 1000003u + (uint64_t)t->n * 7919u);
+    if (center != 0.0f)
+        for (j = 0; j < n; j++) w[j] += center;
+    it->layer = layer;
+    it->slot = slot;
+    it->ndim = cols > 1 ? 2 : 1;
+    it->shape[0] = rows;
+    it->shape[1] = cols > 1 ? cols : 0;
+    snprintf(it->name, sizeof it->name, "%s", name);
+    if (f16) {
+        uint16_t* h = (uint16_t*)malloc(n * 2);
+        if (!h) {
+            free(w);
+            return -1;
+        }
+        f32_to_f16_buf(w, h, n);
+        free(w);
+        t->bufs[t->n] = h;
+        it->dtype = DT_F16;
+        it->nbytes = n * 2;
+    } else {
+        t->bufs[t->n] = w;
+        it->dtype = DT_F32;
+        it->nbytes = n * 4;
+    }
+    it->src = (const uint8_t*)t->bufs[t->n];
+    t->n++;
+    return 0;
+}
+
+static int items_open(Items* t, int cap, uint32_t seed, char* err, size_t errlen)
+{
+    t->items = (ConvItem*)calloc((size_t)cap, sizeof(ConvItem));
+    t->bufs = (void**)calloc((size_t)cap, sizeof(void*));
+    t->n = 0;
+    t->cap = cap;
+    t->seed = seed;
+    if (t->items && t->bufs) return 0;
+    free(t->items);
+    free(t->bufs);
+    snprintf(err, errlen, "out of memory");
+    return -1;
+}
+
+static int items_emit(Items* t, const char* path, const LlfHeader* h, int add_failed, char* err, size_t errlen)
+{
+    int rc, i;
+    if (add_failed) {
+        snprintf(err, errlen, "out of memory building the model");
+        rc = -1;
+    } else {
+        rc = llf_emit(path, h, t->items, t->n, err, errlen);
+    }
+    for (i = 0; i < t->n; i++) free(t->bufs[i]);
+    free(t->bufs);
+    free(t->items);
+    return rc;
+}
+
+static void header(LlfHeader* h, uint32_t arch, uint32_t blocks, uint32_t hidden, uint32_t heads, uint32_t kv_heads,
+                   uint32_t head_dim, uint32_t vocab, uint32_t seq)
+{
+    float eps = 1e-5f, theta = 10000.0f;
+    memset(h, 0, sizeof *h);
+    memcpy(h->magic, YLLM_MAGIC, 8);
+    h->version = YLLM_VERSION;
+    h->arch = arch;
+    h->n_blocks = blocks;
+    h->vocab = vocab;
+    h->hidden = hidden;
+    h->n_heads = heads;
+    h->n_kv_heads = kv_heads;
+    h->head_dim = head_dim;
+    h->max_seq = seq;
+    h->dtype = DT_F16;
+    memcpy(&h->norm_eps_bits, &eps, 4);
+    memcpy(&h->rope_theta_bits, &theta, 4);
+}
+
 /* A synthetic model in the LLF format, written by the reference's own
  * llf_emit (convert.c:31-140) as its converters do: layer 0 the f16
  * embedding, layers 1..blocks the nine block tensors (f32 norms near 1, f16
@@ -62,92 +164,85 @@ int ye_make_model(const char* path, uint32_t arch, uint32_t blocks, uint32_t hid
 {
     const uint32_t hd = hidden / heads, kv_dim = kv_heads * hd;
     const uint32_t inter = ((hidden * 8 / 3 + 63) / 64) * 64;
-    const uint32_t per_block = arch == ARCH_QWEN ? 12 : 9;
-    const int n_items = 1 + (int)(blocks * per_block) + 2;
-    ConvItem* items = (ConvItem*)calloc((size_t)n_items, sizeof(ConvItem));
-    void** bufs = (void**)calloc((size_t)n_items, sizeof(void*));
+    Items t;
     LlfHeader h;
-    int k = 0, rc, i;
     uint32_t b;
-    float eps = 1e-5f, theta = 10000.0f;
-    if (!items || !bufs) {
-        free(items);
-        free(bufs);
-        snprintf(err, errlen, "out of memory");
-        return -1;
-    }
-    memset(&h, 0, sizeof h);
-    memcpy(h.magic, YLLM_MAGIC, 8);
-    h.version = YLLM_VERSION;
-    h.arch = arch;
-    h.n_blocks = blocks;
-    h.vocab = vocab;
-    h.hidden = hidden;
-    h.n_heads = heads;
-    h.n_kv_heads = kv_heads;
-    h.head_dim = hd;
-    h.max_seq = seq;
-    h.dtype = DT_F16;
-    memcpy(&h.norm_eps_bits, &eps, 4);
-    memcpy(&h.rope_theta_bits, &theta, 4);
-
-#define ADD(LAYER, SLOT, NAME, ROWS, COLS, F16, AMP, CENTER)                                         \
-    do {                                                                                          \
-        size_t n_ = (size_t)(ROWS) * (COLS);                                                      \
-        float* w_ = (float*)malloc(n_ * 4);                                                       \
-        ConvItem* it_ = &items[k];                                                                \
-        fill(w_, n_, (AMP), (uint64_t)seed * 1000003u + (uint64_t)k * 7919u);                     \
-        if ((CENTER) != 0.0f) {                                                                   \
-            size_t j_;                                                                            \
-            for (j_ = 0; j_ < n_; j_++) w_[j_] += (CENTER);                                       \
-        }                                                                                         \
-        it_->layer = (LAYER);                                                                     \
-        it_->slot = (SLOT);                                                                       \
-        it_->ndim = (COLS) > 1 ? 2 : 1;                                                           \
-        it_->shape[0] = (ROWS);                                                                   \
-        it_->shape[1] = (COLS) > 1 ? (COLS) : 0;                                                  \
-        snprintf(it_->name, sizeof it_->name, "%s", (NAME));                                      \
-        if (F16) {                                                                                \
-            uint16_t* h_ = (uint16_t*)malloc(n_ * 2);                                             \
-            f32_to_f16_buf(w_, h_, n_);                                                           \
-            free(w_);                                                                             \
-            bufs[k] = h_;                                                                         \
-            it_->dtype = DT_F16;                                                                  \
-            it_->nbytes = n_ * 2;                                                                 \
-        } else {                                                                                  \
-            bufs[k] = w_;                                                                         \
-            it_->dtype = DT_F32;                                                                  \
-            it_->nbytes = n_ * 4;                                                                 \
-        }                                                                                         \
-        it_->src = (const uint8_t*)bufs[k];                                                       \
-        k++;                                                                                      \
-    } while (0)
-
-    ADD(0, SLOT_EMBED, "embed", vocab, hidden, 1, 1.0f, 0.0f);
+    int bad = 0;
+    if (items_open(&t, 3 + (int)blocks * 12, seed, err, errlen) != 0) return -1;
+    header(&h, arch, blocks, hidden, heads, kv_heads, hd, vocab, seq);
+    bad |= add(&t, 0, SLOT_EMBED, "embed", vocab, hidden, 1, 1.0f, 0.0f);
     for (b = 1; b <= blocks; b++) {
-        ADD(b, SLOT_NORM1, "norm1", hidden, 1, 0, 0.1f, 1.0f);
-        ADD(b, SLOT_Q, "q", hidden, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
-        ADD(b, SLOT_K, "k", kv_dim, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
-        ADD(b, SLOT_V, "v", kv_dim, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
-        ADD(b, SLOT_O, "o", hidden, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
-        ADD(b, SLOT_NORM2, "norm2", hidden, 1, 0, 0.1f, 1.0f);
-        ADD(b, SLOT_GATE, "gate", inter, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
-        ADD(b, SLOT_UP, "up", inter, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
-        ADD(b, SLOT_DOWN, "down", hidden, inter, 1, sqrtf(3.0f / inter), 0.0f);
+        bad |= add(&t, b, SLOT_NORM1, "norm1", hidden, 1, 0, 0.1f, 1.0f);
+        bad |= add(&t, b, SLOT_Q, "q", hidden, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+        bad |= add(&t, b, SLOT_K, "k", kv_dim, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+        bad |= add(&t, b, SLOT_V, "v", kv_dim, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+        bad |= add(&t, b, SLOT_O, "o", hidden, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+        bad |= add(&t, b, SLOT_NORM2, "norm2", hidden, 1, 0, 0.1f, 1.0f);
+        bad |= add(&t, b, SLOT_GATE, "gate", inter, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+        bad |= add(&t, b, SLOT_UP, "up", inter, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+        bad |= add(&t, b, SLOT_DOWN, "down", hidden, inter, 1, sqrtf(3.0f / inter), 0.0f);
         if (arch == ARCH_QWEN) {
-            ADD(b, SLOT_QBIAS, "q_bias", hidden, 1, 0, 0.5f, 0.0f);
-            ADD(b, SLOT_KBIAS, "k_bias", kv_dim, 1, 0, 0.5f, 0.0f);
-            ADD(b, SLOT_VBIAS, "v_bias", kv_dim, 1, 0, 0.5f, 0.0f);
+            bad |= add(&t, b, SLOT_QBIAS, "q_bias", hidden, 1, 0, 0.5f, 0.0f);
+            bad |= add(&t, b, SLOT_KBIAS, "k_bias", kv_dim, 1, 0, 0.5f, 0.0f);
+            bad |= add(&t, b, SLOT_VBIAS, "v_bias", kv_dim, 1, 0, 0.5f, 0.0f);
         }
     }
-    ADD(blocks + 1, 0, "final_norm", hidden, 1, 0, 0.1f, 1.0f);
-    ADD(blocks + 2, 0, "output", vocab, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
-#undef ADD
-    rc = llf_emit(path, &h, items, k, err, errlen);
-    for (i = 0; i < k; i++) free(bufs[i]);
-    free(bufs);
-    free(items);
-    return rc;
+    bad |= add(&t, blocks + 1, 0, "final_norm", hidden, 1, 0, 0.1f, 1.0f);
+    bad |= add(&t, blocks + 2, 0, "output", vocab, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+    return items_emit(&t, path, &h, bad, err, errlen);
+}
+
+/* A synthetic qwen35 hybrid model (ARCH_QWEN35), in the tensor slots
+ * fwd_block_qwen35 reads (engine.c:736-982): block b is a gated attention
+ * layer when b % 4 == 0 (heads x head_dim query and gate projections,
+ * kv_heads x head_dim K/V, per-head QK-norm) and a Gated-DeltaNet layer
+ * otherwise (qkv projection of 2*n_k*hvd + n_v*hvd conv channels, z gate,
+ * f32 conv1d of width 4, ssm_a in [-1.5, -0.5], dt bias, alpha / beta
+ * projections, gated-norm weight and ssm_out).  Every block has the SwiGLU
+ * FFN.  Returns 0 or -1 with err set. */
+int ye_make_model_q35(const char* path, uint32_t blocks, uint32_t hidden, uint32_t heads, uint32_t kv_heads,
+                      uint32_t head_dim, uint32_t n_k, uint32_t n_v, uint32_t hvd, uint32_t vocab, uint32_t seq,
+                      uint32_t seed, char* err, size_t errlen)
+{
+    const uint32_t qdim = heads * head_dim, kv_dim = kv_heads * head_dim;
+    const uint32_t vdim = n_v * hvd, conv = 2 * n_k * hvd + vdim, kwidth = 4;
+    const uint32_t inter = ((hidden * 8 / 3 + 63) / 64) * 64;
+    Items t;
+    LlfHeader h;
+    uint32_t b;
+    int bad = 0;
+    if (items_open(&t, 3 + (int)blocks * 16, seed, err, errlen) != 0) return -1;
+    header(&h, ARCH_QWEN35, blocks, hidden, heads, kv_heads, head_dim, vocab, seq);
+    bad |= add(&t, 0, SLOT_EMBED, "embed", vocab, hidden, 1, 1.0f, 0.0f);
+    for (b = 1; b <= blocks; b++) {
+        bad |= add(&t, b, SLOT_NORM1, "norm1", hidden, 1, 0, 0.1f, 1.0f);
+        if (b % 4 == 0) {
+            bad |= add(&t, b, SLOT_Q, "q", qdim, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+            bad |= add(&t, b, SLOT_QGATE, "q_gate", qdim, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+            bad |= add(&t, b, SLOT_K, "k", kv_dim, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+            bad |= add(&t, b, SLOT_V, "v", kv_dim, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+            bad |= add(&t, b, SLOT_O, "o", hidden, qdim, 1, sqrtf(3.0f / qdim), 0.0f);
+            bad |= add(&t, b, SLOT_QNORM, "q_norm", head_dim, 1, 0, 0.1f, 1.0f);
+            bad |= add(&t, b, SLOT_KNORM, "k_norm", head_dim, 1, 0, 0.1f, 1.0f);
+        } else {
+            bad |= add(&t, b, SLOT_QKV, "qkv", conv, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+            bad |= add(&t, b, SLOT_GATE_ATTN, "z", vdim, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+            bad |= add(&t, b, SLOT_SSM_CONV1D, "conv1d", kwidth, conv, 0, sqrtf(3.0f / kwidth), 0.0f);
+            bad |= add(&t, b, SLOT_SSM_A, "ssm_a", n_v, 1, 0, 0.5f, -1.0f);
+            bad |= add(&t, b, SLOT_SSM_DT, "ssm_dt", n_v, 1, 0, 0.5f, 0.0f);
+            bad |= add(&t, b, SLOT_SSM_ALPHA, "alpha", n_v, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+            bad |= add(&t, b, SLOT_SSM_BETA, "beta", n_v, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+            bad |= add(&t, b, SLOT_SSM_NORM, "ssm_norm", hvd, 1, 0, 0.1f, 1.0f);
+            bad |= add(&t, b, SLOT_SSM_OUT, "ssm_out", hidden, vdim, 1, sqrtf(3.0f / vdim), 0.0f);
+        }
+        bad |= add(&t, b, SLOT_NORM2, "norm2", hidden, 1, 0, 0.1f, 1.0f);
+        bad |= add(&t, b, SLOT_GATE, "gate", inter, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+        bad |= add(&t, b, SLOT_UP, "up", inter, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+        bad |= add(&t, b, SLOT_DOWN, "down", hidden, inter, 1, sqrtf(3.0f / inter), 0.0f);
+    }
+    bad |= add(&t, blocks + 1, 0, "final_norm", hidden, 1, 0, 0.1f, 1.0f);
+    bad |= add(&t, blocks + 2, 0, "output", vocab, hidden, 1, sqrtf(3.0f / hidden), 0.0f);
+    return items_emit(&t, path, &h, bad, err, errlen);
 }
 
 /* engine_bind_device (engine.c:354-384) with the HIP factory in place of
@@ -222,13 +317,12 @@ int ye_run(const char* path, int use_hip, int device_id, int fail_after, const u
     for (i = 0; i < n_decode; i++, pos++) {
         uint32_t tok = argmax(logits + (size_t)i * vocab, vocab);
         tokens[i] = tok;
-        if (use_hip && status[0] == 0) {
+        {
+            /* both runs: see the file comment */
             DeviceMode saved = e.device_mode;
-            e.device_mode = DEV_MODE_VULKAN;  /* see the file comment */
+            e.device_mode = DEV_MODE_VULKAN;
             engine_forward(&e, tok, pos);
             e.device_mode = saved;
-        } else {
-            engine_forward(&e, tok, pos);
         }
         memcpy(logits + (size_t)(i + 1) * vocab, e.logits, (size_t)vocab * 4);
     }
@@ -252,7 +346,9 @@ int ye_run(const char* path, int use_hip, int device_id, int fail_after, const u
             return -1;
         }
         for (l = 1; l <= nb; l++) {
+            const LlfTensorMeta* mt = &e.ws.model.metas[e.ws.model.base_idx[l]];
             size_t r;
+            if (e.ws.model.h.arch == ARCH_QWEN35 && mt[SLOT_SSM_CONV1D].size > 0) continue; /* no KV */
             for (r = 0; r < (size_t)pos; r++) {
                 if (memcmp(e.kv + l * slot + r * e.kv_dim, keep + l * slot + r * e.kv_dim, e.kv_dim * 2)) diff++;
                 if (memcmp(e.kv + (nb + l) * slot + r * e.kv_dim, keep + (nb + l) * slot + r * e.kv_dim,

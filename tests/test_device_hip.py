@@ -3,8 +3,9 @@
 The engine is the reference's own C (inference/core, device_cpu.c) compiled
 from its sources with yllm_amd/device/device_hip.c and a driver
 (oracle/e2e_driver.c) into oracle/_ref/libyref_e2e.so.  A synthetic model
-(llama, or qwen with q/k/v biases) is written with the reference's LLF
-writer (llf_emit, convert.c:31).
+(llama, qwen with q/k/v biases, or the qwen35 hybrid of Gated-DeltaNet and
+gated attention layers) is written with the reference's LLF writer
+(llf_emit, convert.c:31).
 Each case runs the same prompt (batched prefill, engine.c:590-709) and greedy
 decode steps (engine_forward, engine.c:1248) on the engine bound to the CPU
 device and bound to the HIP backend, and compares logits (max relative L2
@@ -34,6 +35,8 @@ def e2e():
     lib = ctypes.CDLL(str(E2E_LIB))
     lib.ye_make_model.restype = c_int
     lib.ye_make_model.argtypes = [c_char_p] + [c_uint32] * 8 + [c_char_p, c_size_t]
+    lib.ye_make_model_q35.restype = c_int
+    lib.ye_make_model_q35.argtypes = [c_char_p] + [c_uint32] * 11 + [c_char_p, c_size_t]
     lib.ye_run.restype = c_int
     lib.ye_run.argtypes = [c_char_p, c_int, c_int, c_int, POINTER(c_uint32), c_int, c_int, POINTER(c_float),
                            POINTER(c_uint32), POINTER(c_int), c_char_p, c_size_t]
@@ -46,6 +49,15 @@ ARCH_LLAMA, ARCH_QWEN = 0, 1  # llf.h:22-23
 def make_model(lib, path, blocks, hidden, heads, kv_heads, vocab=512, seq=256, seed=7, arch=ARCH_LLAMA):
     err = ctypes.create_string_buffer(256)
     rc = lib.ye_make_model(str(path).encode(), arch, blocks, hidden, heads, kv_heads, vocab, seq, seed, err, 256)
+    assert rc == 0, err.value.decode()
+    return path
+
+
+def make_q35(lib, path, blocks, hidden, heads, kv_heads, head_dim, n_k, n_v, hvd, vocab=512, seq=256, seed=11):
+    """Block b is gated attention when b % 4 == 0, a GDN layer otherwise."""
+    err = ctypes.create_string_buffer(256)
+    rc = lib.ye_make_model_q35(str(path).encode(), blocks, hidden, heads, kv_heads, head_dim, n_k, n_v, hvd, vocab,
+                               seq, seed, err, 256)
     assert rc == 0, err.value.decode()
     return path
 
@@ -98,6 +110,25 @@ def test_bind_without_usable_gpu_falls_back_to_cpu(e2e, tmp_path):
     assert np.array_equal(got, want) and np.array_equal(gt, wt)
 
 
+def test_qwen35_model_runs_on_the_cpu_engine(e2e, tmp_path):
+    """The synthetic qwen35 model is one the reference engine runs: batched
+    prefill (chunks of >= 16 tokens: smaller ones take the engine's
+    per-token DEV_MODE_CPU branch, which calls the llama block) and decode
+    through fwd_block_qwen35.  Without a GPU the HIP bind falls back and
+    gives the same bits."""
+    import torch
+
+    path = make_q35(e2e, tmp_path / "q.llf", 4, 256, 4, 2, 256, 2, 4, 64)
+    prompt = prompt_of(40)
+    want, wt, _, _ = run(e2e, path, prompt, 3, use_hip=False)
+    assert np.isfinite(want).all() and np.std(want[-1]) > 0.1
+    if torch.cuda.is_available():
+        return
+    got, gt, status, msg = run(e2e, path, prompt, 3, use_hip=True)
+    assert status[0] == -1 and msg.startswith("hip:"), (status, msg)
+    assert np.array_equal(got, want) and np.array_equal(gt, wt)
+
+
 # ------------------------------------------------------------------------ GPU
 
 @pytest.mark.gpu
@@ -145,3 +176,50 @@ def test_engine_failure_hook_mid_run_stays_within_tolerance(e2e, cuda, tmp_path)
     assert status[0] == 0, msg
     assert max(rel_l2(got[i], want[i]) for i in range(7)) <= TOL
     assert np.array_equal(gt, wt)
+
+
+Q35_CASES = [
+    # blocks, hidden, heads, kv, head_dim, n_k, n_v, hvd, prompt
+    (4, 256, 4, 2, 256, 2, 4, 64, 83),     # d 256 gated attention; GDN d 64; prefill 64 (chunked) + 19
+    (8, 512, 8, 2, 128, 4, 8, 128, 40),    # two groups; GDN d 128, 8 v heads on 4 k heads
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("blocks,hidden,heads,kv_heads,head_dim,n_k,n_v,hvd,n_prompt", Q35_CASES)
+def test_qwen35_end_to_end_matches_cpu(e2e, cuda, tmp_path, blocks, hidden, heads, kv_heads, head_dim, n_k, n_v,
+                                       hvd, n_prompt):
+    """qwen35 hybrid blocks on the backend: GDN state in HBM (chunked prefill,
+    one-token steps), gated attention with the fused gate, against the
+    engine's own fwd_block_qwen35 on the CPU."""
+    path = make_q35(e2e, tmp_path / "q.llf", blocks, hidden, heads, kv_heads, head_dim, n_k, n_v, hvd)
+    prompt = prompt_of(n_prompt)
+    n_dec = 8
+    want, wt, _, _ = run(e2e, path, prompt, n_dec, use_hip=False)
+    got, gt, status, msg = run(e2e, path, prompt, n_dec, use_hip=True)
+    assert status[0] == 0, msg
+    errs = [rel_l2(got[i], want[i]) for i in range(n_dec + 1)]
+    print(f"e2e qwen35 blocks={blocks} hidden={hidden} attn {heads}/{kv_heads}x{head_dim} gdn {n_k}/{n_v}x{hvd} "
+          f"prompt={n_prompt}: max rel_l2 {max(errs):.3e}, tokens {gt.tolist()}")
+    assert max(errs) <= TOL
+    assert np.array_equal(np.argmax(got, axis=1), np.argmax(want, axis=1))
+    assert np.array_equal(gt, wt)
+    assert status[1] == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fail_after", [0, 5])
+def test_qwen35_failure_hook(e2e, cuda, tmp_path, fail_after):
+    """fail_after 0: every block on the CPU, bit for bit.  fail_after 5: the
+    prefill's 4 blocks and one decode block on the GPU, then the CPU, which
+    continues from the GDN state and KV the backend mirrored to the host."""
+    path = make_q35(e2e, tmp_path / "q.llf", 4, 256, 4, 2, 256, 2, 4, 64)
+    prompt = prompt_of(40)
+    want, wt, _, _ = run(e2e, path, prompt, 4, use_hip=False)
+    got, gt, status, msg = run(e2e, path, prompt, 4, use_hip=True, fail_after=fail_after)
+    assert status[0] == 0, msg
+    if fail_after == 0:
+        assert np.array_equal(got, want) and np.array_equal(gt, wt)
+    else:
+        assert max(rel_l2(got[i], want[i]) for i in range(5)) <= TOL
+        assert np.array_equal(gt, wt)

@@ -21,6 +21,17 @@
  * host array e->kv, so host KV is always current: a CPU fallback, session
  * save (cache.c:174-247) and the CPU path of any layer stay valid.
  *
+ * ARCH_QWEN35 (fwd_block_qwen35, engine.c:736-982) is covered too.  Its
+ * Gated-DeltaNet layers keep their recurrent state in HBM (yhip_gdn_chunk:
+ * l2norm + state update, one token or a whole batch, chunked); the
+ * projections, gates, conv1d delay line, gated RMSNorm and FFN stay on the
+ * engine's operators.  After every GPU update the state is copied back to
+ * e->ssm_state, so the host copy is always current as the KV is.  Its gated
+ * attention layers (d = 256, QK-norm, M-RoPE on 64 dims, sigmoid gate) use
+ * the same KV store and decode / prefill entry points with the gate fused.
+ * The reference's batch forward for qwen35 runs token by token
+ * (engine.c:723-734); here a batch is one GPU call per layer.
+ *
  * Failure handling: any HIP error in a block marks the backend failed; that
  * block is recomputed with the saved CPU forward (e->x is untouched until
  * the attention output is back) and -1 is returned; every later block runs
@@ -60,6 +71,10 @@ _Static_assert(offsetof(Engine, pb) == 384, "Engine.pb");
 _Static_assert(offsetof(Engine, pb2) == 392, "Engine.pb2");
 _Static_assert(offsetof(Engine, pbq) == 400, "Engine.pbq");
 _Static_assert(offsetof(Engine, pb_cap) == 448, "Engine.pb_cap");
+_Static_assert(offsetof(Engine, ssm_state) == 360, "Engine.ssm_state");
+_Static_assert(offsetof(Engine, ssm_conv) == 368, "Engine.ssm_conv");
+_Static_assert(offsetof(Engine, pbg) == 424, "Engine.pbg");
+_Static_assert(offsetof(Engine, pbu) == 432, "Engine.pbu");
 _Static_assert(offsetof(Engine, dev) == 528, "Engine.dev");
 _Static_assert(offsetof(Engine, d_kv) == 536, "Engine.d_kv");
 _Static_assert(offsetof(Engine, w_dev) == 544, "Engine.w_dev");
@@ -79,19 +94,36 @@ typedef int (*FwdBatchFn)(Engine*, uint32_t, uint32_t, uint32_t);
 typedef struct {
     int device_id;
     hipStream_t stream;
-    /* model shape */
-    uint32_t arch, hidden, n_heads, n_kv, head_dim, kv_dim, n_blocks, max_seq;
-    /* HBM KV: block layers first..last, K then V per layer */
-    uint32_t first, last, kv_stride;
+    /* model shape; qdim = n_heads * head_dim (== hidden except for qwen35) */
+    uint32_t arch, hidden, n_heads, n_kv, head_dim, qdim, kv_dim, n_blocks, max_seq;
+    /* HBM KV: one slot per attention layer of first..last, K then V */
+    uint32_t first, last, kv_stride, n_kv_slots;
     uint64_t layer_elems;
     uint16_t* d_cache;
-    uint32_t* dev_len;  /* per resident layer: rows 0..dev_len-1 are in HBM */
-    /* staging for one call: q / attention out [cap][hidden], k / v [cap][kv_dim] */
-    uint32_t cap;
-    float *d_q, *d_k, *d_v, *d_out;
+    int32_t* kv_slot;   /* per layer first..last: its KV slot, -1 for a GDN layer */
+    uint32_t* dev_len;  /* per KV slot: rows 0..dev_len-1 are in HBM */
+    /* Gated-DeltaNet layers (qwen35): per layer first..last its state slot
+     * (-1 for an attention layer) and its index among the model's GDN layers
+     * (gdn_index_of, engine.c:711-720: the slot of e->ssm_state / ssm_conv) */
+    int32_t* gdn_slot;
+    uint32_t* gdn_ord;
+    uint8_t* state_ok;  /* per state slot: the HBM state equals the host state */
+    uint32_t n_gdn_slots, conv_chan, kwidth, n_v, n_k, hvd, value_dim;
+    float* d_state;
+    float* d_gb;        /* gate [cap][n_v], then beta [cap][n_v] */
+    void* d_gws;        /* chunked-form workspace for cap tokens */
+    size_t gws_bytes;
+    float* h_state;     /* one layer's state on its way back to host */
+    float* h_conv;      /* one layer's conv delay line, kept to undo a failed block */
+    /* staging for one call: q (or a GDN qkv row), k, v, gate, output */
+    uint32_t cap, q_w, o_w;
+    float *d_q, *d_k, *d_v, *d_g, *d_out;
     uint16_t* d_rows;  /* host f16 rows on their way into HBM (catch-up) */
     void* d_ws;
     size_t ws_bytes;
+    /* host rows of a qwen35 block: normed input, q or qkv, gate or z,
+     * k, v, alpha / beta / gate, GPU output, projection output */
+    float *h_n, *h_q, *h_z, *h_k, *h_v, *h_ab, *h_o, *h_x;
     /* fallback */
     FwdFn cpu_fwd;
     FwdBatchFn cpu_fwd_batch;
@@ -117,7 +149,7 @@ static int hip_ok(hipError_t rc, char* err, size_t errlen, const char* what)
 
 static uint16_t* layer_k(const HipCtx* c, uint32_t layer)
 {
-    return c->d_cache + (size_t)(layer - c->first) * 2 * c->layer_elems;
+    return c->d_cache + (size_t)c->kv_slot[layer - c->first] * 2 * c->layer_elems;
 }
 
 static uint16_t* layer_v(const HipCtx* c, uint32_t layer)
@@ -125,18 +157,52 @@ static uint16_t* layer_v(const HipCtx* c, uint32_t layer)
     return layer_k(c, layer) + c->layer_elems;
 }
 
+static void dfree(void* p)
+{
+    if (p) hipFree(p);
+}
+
+static void free_staging(HipCtx* c)
+{
+    dfree(c->d_q);
+    dfree(c->d_k);
+    dfree(c->d_v);
+    dfree(c->d_g);
+    dfree(c->d_out);
+    dfree(c->d_rows);
+    dfree(c->d_gb);
+    dfree(c->d_gws);
+    free(c->h_n);
+    free(c->h_q);
+    free(c->h_z);
+    free(c->h_k);
+    free(c->h_v);
+    free(c->h_ab);
+    free(c->h_o);
+    free(c->h_x);
+    c->d_q = c->d_k = c->d_v = c->d_g = c->d_out = c->d_gb = NULL;
+    c->d_rows = NULL;
+    c->d_gws = NULL;
+    c->h_n = c->h_q = c->h_z = c->h_k = c->h_v = c->h_ab = c->h_o = c->h_x = NULL;
+    c->gws_bytes = 0;
+    c->cap = 0;
+}
+
 static void release(HipCtx* c)
 {
     if (!c) return;
-    if (c->d_cache) hipFree(c->d_cache);
-    if (c->d_q) hipFree(c->d_q);
-    if (c->d_k) hipFree(c->d_k);
-    if (c->d_v) hipFree(c->d_v);
-    if (c->d_out) hipFree(c->d_out);
-    if (c->d_rows) hipFree(c->d_rows);
-    if (c->d_ws) hipFree(c->d_ws);
+    free_staging(c);
+    dfree(c->d_cache);
+    dfree(c->d_state);
+    dfree(c->d_ws);
     if (c->stream) hipStreamDestroy(c->stream);
     free(c->dev_len);
+    free(c->kv_slot);
+    free(c->gdn_slot);
+    free(c->gdn_ord);
+    free(c->state_ok);
+    free(c->h_state);
+    free(c->h_conv);
     {
         int id = c->device_id;
         memset(c, 0, sizeof(*c));
@@ -148,21 +214,33 @@ static void release(HipCtx* c)
 /* staging for up to `rows` tokens of one call */
 static int ensure_cap(HipCtx* c, uint32_t rows)
 {
+    int q35 = c->arch == ARCH_QWEN35;
     if (rows <= c->cap) return 0;
-    if (c->d_q) hipFree(c->d_q);
-    if (c->d_k) hipFree(c->d_k);
-    if (c->d_v) hipFree(c->d_v);
-    if (c->d_out) hipFree(c->d_out);
-    if (c->d_rows) hipFree(c->d_rows);
-    c->d_q = c->d_k = c->d_v = c->d_out = NULL;
-    c->d_rows = NULL;
-    c->cap = 0;
-    if (hipMalloc((void**)&c->d_q, (size_t)rows * c->hidden * 4) != hipSuccess ||
-        hipMalloc((void**)&c->d_out, (size_t)rows * c->hidden * 4) != hipSuccess ||
+    free_staging(c);
+    if (hipMalloc((void**)&c->d_q, (size_t)rows * c->q_w * 4) != hipSuccess ||
+        hipMalloc((void**)&c->d_out, (size_t)rows * c->o_w * 4) != hipSuccess ||
         hipMalloc((void**)&c->d_k, (size_t)rows * c->kv_dim * 4) != hipSuccess ||
         hipMalloc((void**)&c->d_v, (size_t)rows * c->kv_dim * 4) != hipSuccess ||
         hipMalloc((void**)&c->d_rows, (size_t)rows * c->kv_dim * 2 * 2) != hipSuccess)
         return -1;
+    if (q35) {
+        size_t wide = c->q_w > c->o_w ? c->q_w : c->o_w;
+        if (hipMalloc((void**)&c->d_g, (size_t)rows * c->qdim * 4) != hipSuccess) return -1;
+        c->h_n = (float*)malloc((size_t)rows * c->hidden * 4);
+        c->h_q = (float*)malloc((size_t)rows * c->q_w * 4);
+        c->h_z = (float*)malloc((size_t)rows * wide * 4);
+        c->h_k = (float*)malloc((size_t)rows * c->kv_dim * 4);
+        c->h_v = (float*)malloc((size_t)rows * c->kv_dim * 4);
+        c->h_o = (float*)malloc((size_t)rows * c->o_w * 4);
+        c->h_x = (float*)malloc((size_t)rows * c->hidden * 4);
+        if (!c->h_n || !c->h_q || !c->h_z || !c->h_k || !c->h_v || !c->h_o || !c->h_x) return -1;
+        if (c->n_gdn_slots) {
+            c->h_ab = (float*)malloc((size_t)rows * 3 * c->n_v * 4);
+            if (!c->h_ab || hipMalloc((void**)&c->d_gb, (size_t)rows * 2 * c->n_v * 4) != hipSuccess) return -1;
+            c->gws_bytes = yhip_gdn_chunk_workspace(rows, c->n_v, c->hvd);
+            if (c->gws_bytes && hipMalloc(&c->d_gws, c->gws_bytes) != hipSuccess) return -1;
+        }
+    }
     c->cap = rows;
     return 0;
 }
@@ -173,7 +251,7 @@ static int ensure_cap(HipCtx* c, uint32_t rows)
  * f16 sources bit for bit. */
 static int catch_up(HipCtx* c, Engine* e, uint32_t layer, uint32_t upto)
 {
-    uint32_t* have = &c->dev_len[layer - c->first];
+    uint32_t* have = &c->dev_len[c->kv_slot[layer - c->first]];
     const uint16_t* hk = e->kv + (size_t)layer * e->max_seq * c->kv_dim;
     const uint16_t* hv = e->kv + (size_t)(c->n_blocks + layer) * e->max_seq * c->kv_dim;
     while (*have < upto) {
@@ -282,12 +360,216 @@ static int gpu_decode(HipCtx* c, Engine* e, uint32_t layer, uint32_t pos, const 
     if (yhip_kv_store(kc, vc, c->d_k, c->d_v, YHIP_F32, pos, 1, c->n_kv, c->head_dim, c->kv_stride,
                       c->stream) != YHIP_OK)
         return -1;
-    c->dev_len[layer - c->first] = pos + 1;
+    c->dev_len[c->kv_slot[layer - c->first]] = pos + 1;
     if (yhip_attn_decode(c->d_out, c->d_q, kc, vc, pos, c->n_heads, c->n_kv, c->head_dim, c->kv_stride, NULL,
                          c->d_ws, c->ws_bytes, c->stream) != YHIP_OK)
         return -1;
     if (hipMemcpyAsync(att_out, c->d_out, nq * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return -1;
     return hipStreamSynchronize(c->stream) == hipSuccess ? 0 : -1;
+}
+
+/* ---- ARCH_QWEN35 blocks (fwd_block_qwen35, engine.c:736-982) ---------- */
+
+/* y[B][out] = x[B][in] . W^T: the engine's matmul for one row (as its
+ * per-token forward), matmul_batch for a batch */
+static void proj(float* y, const float* x, const uint8_t* base, const LlfTensorMeta* t, uint32_t out, uint32_t in,
+                 uint32_t B)
+{
+    if (B == 1)
+        matmul(y, x, base + t->offset, out, in, t->dtype);
+    else
+        matmul_batch(y, x, base + t->offset, out, in, t->dtype, B);
+}
+
+static float sigmoidf_(float x)
+{
+    return 1.0f / (1.0f + expf(-x));
+}
+
+/* GDN layer, engine.c:764-850 up to the output projection: c->h_n (normed
+ * rows) -> c->h_x (ssm_out rows).  The conv delay line advances on the host;
+ * the recurrence (l2norm of q/k, decay, delta rule, output) runs on the HBM
+ * state.  On failure the delay line is restored and -1 returned. */
+static int q35_gdn(Engine* e, HipCtx* c, uint32_t layer, uint32_t B, const uint8_t* base, const LlfTensorMeta* mt,
+                   float eps)
+{
+    const uint32_t hidden = c->hidden, cc = c->conv_chan, vd = c->value_dim, nv = c->n_v, hvd = c->hvd;
+    const uint32_t kd = c->n_k * hvd, li = layer - c->first;
+    const size_t state_n = (size_t)nv * hvd * hvd;
+    const int32_t slot = c->gdn_slot[li];
+    float* conv_state = e->ssm_conv + (size_t)c->gdn_ord[li] * c->kwidth * cc;
+    float* host_S = e->ssm_state + (size_t)c->gdn_ord[li] * state_n;
+    float* dS = c->d_state + (size_t)slot * state_n;
+    const float* dt = (const float*)(base + mt[SLOT_SSM_DT].offset);
+    const float* a = (const float*)(base + mt[SLOT_SSM_A].offset);
+    float *qkv = c->h_q, *z = c->h_z, *alpha = c->h_ab, *beta = alpha + (size_t)B * nv, *gate = beta + (size_t)B * nv;
+    uint32_t b, h, ch;
+    int ok;
+
+    proj(qkv, c->h_n, base, &mt[SLOT_QKV], cc, hidden, B);
+    proj(z, c->h_n, base, &mt[SLOT_GATE_ATTN], vd, hidden, B);
+    proj(alpha, c->h_n, base, &mt[SLOT_SSM_ALPHA], nv, hidden, B);
+    proj(beta, c->h_n, base, &mt[SLOT_SSM_BETA], nv, hidden, B);
+    for (b = 0; b < B; b++) {
+        float* bb = beta + (size_t)b * nv;
+        const float* ab = alpha + (size_t)b * nv;
+        float* gb = gate + (size_t)b * nv;
+        for (h = 0; h < nv; h++) {
+            bb[h] = sigmoidf_(bb[h]);
+            gb[h] = log1pf(expf(ab[h] + dt[h])) * a[h];
+        }
+    }
+    memcpy(c->h_conv, conv_state, (size_t)c->kwidth * cc * 4);
+    for (b = 0; b < B; b++) {
+        float* row = qkv + (size_t)b * cc;
+        conv1d_update(conv_state, row, base + mt[SLOT_SSM_CONV1D].offset, cc, c->kwidth);
+        for (ch = 0; ch < cc; ch++) row[ch] = row[ch] * sigmoidf_(row[ch]);
+    }
+
+    ok = (c->state_ok[slot] ||
+          hipMemcpyAsync(dS, host_S, state_n * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess) &&
+         hipMemcpyAsync(c->d_q, qkv, (size_t)B * cc * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+         hipMemcpyAsync(c->d_gb, gate, (size_t)B * nv * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+         hipMemcpyAsync(c->d_gb + (size_t)B * nv, beta, (size_t)B * nv * 4, hipMemcpyHostToDevice, c->stream) ==
+             hipSuccess;
+    c->state_ok[slot] = 0;
+    ok = ok &&
+         yhip_gdn_chunk(dS, c->d_out, vd, c->d_q, c->d_q + kd, cc, c->d_q + 2 * kd, cc, c->d_gb,
+                        c->d_gb + (size_t)B * nv, B, c->n_k, nv, hvd, eps, c->d_gws, c->gws_bytes,
+                        c->stream) == YHIP_OK &&
+         hipMemcpyAsync(c->h_o, c->d_out, (size_t)B * vd * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
+         hipMemcpyAsync(c->h_state, dS, state_n * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
+         hipStreamSynchronize(c->stream) == hipSuccess;
+    if (!ok) {
+        memcpy(conv_state, c->h_conv, (size_t)c->kwidth * cc * 4);
+        return -1;
+    }
+    memcpy(host_S, c->h_state, state_n * 4);
+    c->state_ok[slot] = 1;
+
+    /* gated RMSNorm per v head (engine.c:840-850), then ssm_out */
+    for (b = 0; b < B; b++)
+        for (h = 0; h < nv; h++) {
+            float* o = c->h_o + (size_t)b * vd + (size_t)h * hvd;
+            rmsnorm_gated(o, o, base + mt[SLOT_SSM_NORM].offset, z + (size_t)b * vd + (size_t)h * hvd, hvd, eps,
+                          mt[SLOT_SSM_NORM].dtype);
+        }
+    proj(c->h_x, c->h_o, base, &mt[SLOT_SSM_OUT], hidden, vd, B);
+    return 0;
+}
+
+/* gated attention layer, engine.c:886-966 up to o_proj: c->h_n -> c->h_x */
+static int q35_attn(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_t B, const uint8_t* base,
+                    const LlfTensorMeta* mt, float eps, float theta)
+{
+    const uint32_t hidden = c->hidden, qd = c->qdim, kvd = c->kv_dim, hd = c->head_dim;
+    uint16_t *kc = layer_k(c, layer), *vc = layer_v(c, layer);
+    uint32_t b, h, j;
+    int ok;
+
+    proj(c->h_q, c->h_n, base, &mt[SLOT_Q], qd, hidden, B);
+    proj(c->h_z, c->h_n, base, &mt[SLOT_QGATE], qd, hidden, B);
+    proj(c->h_k, c->h_n, base, &mt[SLOT_K], kvd, hidden, B);
+    proj(c->h_v, c->h_n, base, &mt[SLOT_V], kvd, hidden, B);
+    for (b = 0; b < B; b++) {
+        float* q = c->h_q + (size_t)b * qd;
+        float* k = c->h_k + (size_t)b * kvd;
+        const float* v = c->h_v + (size_t)b * kvd;
+        uint32_t pos = pos0 + b;
+        uint16_t* hk = e->kv + (size_t)layer * e->max_seq * kvd + (size_t)pos * kvd;
+        uint16_t* hv = e->kv + (size_t)(c->n_blocks + layer) * e->max_seq * kvd + (size_t)pos * kvd;
+        head_norm(q, &mt[SLOT_QNORM], base, c->n_heads, hd, eps);
+        head_norm(k, &mt[SLOT_KNORM], base, c->n_kv, hd, eps);
+        for (h = 0; h < c->n_heads; h++) rope_inplace_mrope(q + (size_t)h * hd, hd, 64, pos, theta);
+        for (h = 0; h < c->n_kv; h++) rope_inplace_mrope(k + (size_t)h * hd, hd, 64, pos, theta);
+        for (j = 0; j < kvd; j++) {
+            hk[j] = f32_to_f16(k[j]);
+            hv[j] = f32_to_f16(v[j]);
+        }
+    }
+
+    ok = catch_up(c, e, layer, pos0) == 0 &&
+         hipMemcpyAsync(c->d_q, c->h_q, (size_t)B * qd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+         hipMemcpyAsync(c->d_g, c->h_z, (size_t)B * qd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+         hipMemcpyAsync(c->d_k, c->h_k, (size_t)B * kvd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+         hipMemcpyAsync(c->d_v, c->h_v, (size_t)B * kvd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+         yhip_kv_store(kc, vc, c->d_k, c->d_v, YHIP_F32, pos0, B, c->n_kv, hd, c->kv_stride, c->stream) == YHIP_OK;
+    if (!ok) return -1;
+    c->dev_len[c->kv_slot[layer - c->first]] = pos0 + B;
+    if (B == 1)
+        ok = yhip_attn_decode(c->d_out, c->d_q, kc, vc, pos0, c->n_heads, c->n_kv, hd, c->kv_stride, c->d_g, c->d_ws,
+                              c->ws_bytes, c->stream) == YHIP_OK;
+    else
+        ok = yhip_attn_prefill(c->d_out, YHIP_F32, qd, c->d_q, YHIP_F32, qd, kc, vc, pos0, B, c->n_heads, c->n_kv, hd,
+                               c->kv_stride, c->d_g, qd, c->stream) == YHIP_OK;
+    ok = ok &&
+         hipMemcpyAsync(c->h_o, c->d_out, (size_t)B * qd * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
+         hipStreamSynchronize(c->stream) == hipSuccess;
+    if (!ok) return -1;
+    proj(c->h_x, c->h_o, base, &mt[SLOT_O], hidden, qd, B);
+    return 0;
+}
+
+/* One qwen35 block over B rows X[B][hidden] at positions pos0..pos0+B-1:
+ * norm1, the layer's mixer (GDN or gated attention), residual, norm2,
+ * SwiGLU FFN, residual.  X is written only after the GPU part succeeded. */
+static int q35_block(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_t B, float* X)
+{
+    const uint8_t* base = layer_base(e, layer);
+    const LlfTensorMeta* mt = &e->ws.model.metas[e->ws.model.base_idx[layer]];
+    const uint32_t hidden = c->hidden;
+    const uint32_t inter = mt[SLOT_GATE].shape[0] * mt[SLOT_GATE].shape[1] / hidden;
+    float eps, theta, *fg, *fu;
+    uint32_t b, j;
+    int rc;
+    scalars(e, &eps, &theta);
+    for (b = 0; b < B; b++)
+        rmsnorm(c->h_n + (size_t)b * hidden, X + (size_t)b * hidden, base + mt[SLOT_NORM1].offset, hidden, eps,
+                mt[SLOT_NORM1].dtype);
+    if (c->gdn_slot[layer - c->first] >= 0)
+        rc = q35_gdn(e, c, layer, B, base, mt, eps);
+    else
+        rc = q35_attn(e, c, layer, pos0, B, base, mt, eps, theta);
+    if (rc != 0) return -1;
+
+    for (b = 0; b < B; b++) {
+        float* xb = X + (size_t)b * hidden;
+        const float* ob = c->h_x + (size_t)b * hidden;
+        for (j = 0; j < hidden; j++) xb[j] += ob[j];
+        rmsnorm(c->h_n + (size_t)b * hidden, xb, base + mt[SLOT_NORM2].offset, hidden, eps, mt[SLOT_NORM2].dtype);
+    }
+    fg = B == 1 ? e->ffn : e->pbg;
+    fu = B == 1 ? e->ffn + inter : e->pbu;
+    proj(fg, c->h_n, base, &mt[SLOT_GATE], inter, hidden, B);
+    proj(fu, c->h_n, base, &mt[SLOT_UP], inter, hidden, B);
+    for (b = 0; b < B; b++)
+        swiglu(fg + (size_t)b * inter, fg + (size_t)b * inter, fu + (size_t)b * inter, inter);
+    proj(c->h_x, fg, base, &mt[SLOT_DOWN], hidden, inter, B);
+    for (b = 0; b < B; b++) {
+        float* xb = X + (size_t)b * hidden;
+        const float* db = c->h_x + (size_t)b * hidden;
+        for (j = 0; j < hidden; j++) xb[j] += db[j];
+    }
+    return 0;
+}
+
+/* fwd_block / fwd_block_batch for qwen35.  A CPU-computed GDN block leaves
+ * the HBM state stale; it is re-sent before the layer's next GPU call. */
+static int q35_fwd(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_t B, int batch)
+{
+    int turn = B > c->cap ? 0 : gpu_turn(c, layer, pos0 + B);
+    if (turn > 0 && q35_block(e, c, layer, pos0, B, batch ? e->pb : e->x) == 0) return 0;
+    if (turn > 0) {
+        c->failed = 1;
+        turn = -1;
+    }
+    if (layer >= c->first && layer <= c->last && c->gdn_slot[layer - c->first] >= 0)
+        c->state_ok[c->gdn_slot[layer - c->first]] = 0;
+    if (batch)
+        c->cpu_fwd_batch(e, layer, pos0, B);
+    else
+        c->cpu_fwd(e, layer, pos0);
+    return turn;
 }
 
 /* fwd_block: engine_fwd_block_at (engine.c:992-1109) with the attention
@@ -301,6 +583,7 @@ static int hip_fwd_block(Engine* e, uint32_t layer, uint32_t pos)
     uint32_t hidden, kv_dim, inter, j;
     int turn;
     if (!c) return -1;
+    if (c->arch == ARCH_QWEN35) return q35_fwd(e, c, layer, pos, 1, 0);
     turn = gpu_turn(c, layer, pos + 1);
     if (turn <= 0) {
         c->cpu_fwd(e, layer, pos);
@@ -361,7 +644,7 @@ static int gpu_prefill(HipCtx* c, Engine* e, uint32_t layer, uint32_t pos_start,
     if (yhip_kv_store(kc, vc, c->d_k, c->d_v, YHIP_F32, pos_start, B, c->n_kv, c->head_dim, c->kv_stride,
                       c->stream) != YHIP_OK)
         return -1;
-    c->dev_len[layer - c->first] = pos_start + B;
+    c->dev_len[c->kv_slot[layer - c->first]] = pos_start + B;
     if (yhip_attn_prefill(c->d_out, YHIP_F32, c->hidden, c->d_q, YHIP_F32, c->hidden, kc, vc, pos_start, B,
                           c->n_heads, c->n_kv, c->head_dim, c->kv_stride, NULL, 0, c->stream) != YHIP_OK)
         return -1;
@@ -381,6 +664,7 @@ static int hip_fwd_block_batch(Engine* e, uint32_t layer, uint32_t pos_start, ui
     int turn;
     if (!c) return -1;
     if (B == 0) return 0;
+    if (c->arch == ARCH_QWEN35) return q35_fwd(e, c, layer, pos_start, B, 1);
     turn = gpu_turn(c, layer, pos_start + B);
     if (turn <= 0) {
         c->cpu_fwd_batch(e, layer, pos_start, B);
@@ -430,17 +714,63 @@ static int hip_fwd_block_batch(Engine* e, uint32_t layer, uint32_t pos_start, ui
     return 0;
 }
 
+/* Layer map of [first, last]: KV slots for attention layers, state slots
+ * and GDN ordinals for qwen35's Gated-DeltaNet layers (a layer is GDN when
+ * it has a conv1d tensor, as engine_init and gdn_index_of decide,
+ * engine.c:283-305, 711-720), and the GDN shape of fwd_block_qwen35
+ * (engine.c:766-772).  Returns 0 or -1 with err set. */
+static int plan_layers(Engine* e, HipCtx* c, char* err, size_t errlen)
+{
+    const LlModel* m = &e->ws.model;
+    uint32_t nl = c->last - c->first + 1, l, ord = 0;
+    c->kv_slot = (int32_t*)calloc(nl, sizeof(int32_t));
+    c->gdn_slot = (int32_t*)calloc(nl, sizeof(int32_t));
+    c->gdn_ord = (uint32_t*)calloc(nl, sizeof(uint32_t));
+    if (!c->kv_slot || !c->gdn_slot || !c->gdn_ord) return say(err, errlen, "out of host memory", NULL);
+    for (l = 1; l <= c->last; l++) {
+        const LlfTensorMeta* mt = &m->metas[m->base_idx[l]];
+        int gdn = c->arch == ARCH_QWEN35 && mt[SLOT_SSM_CONV1D].size > 0;
+        if (gdn) {
+            uint32_t cc = mt[SLOT_SSM_CONV1D].shape[1], kw = mt[SLOT_SSM_CONV1D].shape[0];
+            uint32_t nv = mt[SLOT_SSM_A].shape[0], hvd = mt[SLOT_SSM_NORM].shape[0];
+            if (c->conv_chan == 0) {
+                if (hvd != 64 && hvd != 128) return say(err, errlen, "GDN head dim must be 64 or 128", NULL);
+                if (nv == 0 || kw == 0 || cc <= nv * hvd || (cc - nv * hvd) % (2 * hvd))
+                    return say(err, errlen, "GDN conv channels do not split into q, k, v heads", NULL);
+                if (mt[SLOT_SSM_CONV1D].dtype != DT_F32 || mt[SLOT_SSM_A].dtype != DT_F32 ||
+                    mt[SLOT_SSM_DT].dtype != DT_F32)
+                    return say(err, errlen, "GDN conv1d, ssm_a and ssm_dt must be f32", NULL);
+                if (!e->ssm_state || !e->ssm_conv) return say(err, errlen, "engine has no GDN state", NULL);
+                c->conv_chan = cc;
+                c->kwidth = kw;
+                c->n_v = nv;
+                c->hvd = hvd;
+                c->value_dim = nv * hvd;
+                c->n_k = (cc - nv * hvd) / (2 * hvd);
+            } else if (cc != c->conv_chan || kw != c->kwidth || nv != c->n_v || hvd != c->hvd) {
+                return say(err, errlen, "GDN layers differ in shape", NULL);
+            }
+        }
+        if (l >= c->first) {
+            c->kv_slot[l - c->first] = gdn ? -1 : (int32_t)c->n_kv_slots++;
+            c->gdn_slot[l - c->first] = gdn ? (int32_t)c->n_gdn_slots++ : -1;
+            c->gdn_ord[l - c->first] = gdn ? ord : 0;
+        }
+        if (gdn) ord++;
+    }
+    return 0;
+}
+
 static int hip_load_weights(Engine* e, char* err, size_t errlen)
 {
     HipCtx* c = ctx_of(e);
     const LlfHeader* h;
-    uint32_t first, last, nl;
-    size_t cache_bytes;
+    uint32_t first, last;
+    size_t cache_bytes, state_bytes;
     if (!c) return say(err, errlen, "no backend state", NULL);
     h = &e->ws.model.h;
     release(c);
-    if (h->arch == ARCH_QWEN35) return say(err, errlen, "ARCH_QWEN35 blocks are not offloaded by this backend", NULL);
-    if (h->n_heads * h->head_dim != h->hidden)
+    if (h->arch != ARCH_QWEN35 && h->n_heads * h->head_dim != h->hidden)
         return say(err, errlen, "n_heads*head_dim != hidden is not supported", NULL);
     if (h->head_dim != 64 && h->head_dim != 128 && h->head_dim != 256)
         return say(err, errlen, "head_dim must be 64, 128 or 256", NULL);
@@ -452,29 +782,44 @@ static int hip_load_weights(Engine* e, char* err, size_t errlen)
     first = e->layer_begin > 1 ? e->layer_begin : 1;
     last = e->layer_end > 0 && e->layer_end - 1 < h->n_blocks ? e->layer_end - 1 : h->n_blocks;
     if (first > last) first = last = 1;
-    nl = last - first + 1;
 
-    if (hip_ok(hipSetDevice(c->device_id), err, errlen, "hipSetDevice") ||
-        hip_ok(hipStreamCreate(&c->stream), err, errlen, "hipStreamCreate"))
-        return -1;
     c->arch = h->arch;
     c->hidden = h->hidden;
     c->n_heads = h->n_heads;
     c->n_kv = h->n_kv_heads;
     c->head_dim = h->head_dim;
+    c->qdim = h->n_heads * h->head_dim;
     c->kv_dim = e->kv_dim;
     c->n_blocks = h->n_blocks;
     c->max_seq = e->max_seq;
     c->first = first;
     c->last = last;
+    if (plan_layers(e, c, err, errlen) != 0) return -1;
+    c->q_w = c->qdim > c->conv_chan ? c->qdim : c->conv_chan;
+    c->o_w = c->qdim > c->value_dim ? c->qdim : c->value_dim;
+
+    if (hip_ok(hipSetDevice(c->device_id), err, errlen, "hipSetDevice") ||
+        hip_ok(hipStreamCreate(&c->stream), err, errlen, "hipStreamCreate"))
+        return -1;
     c->kv_stride = (e->max_seq + 63) / 64 * 64;
     c->layer_elems = yhip_kv_layer_elems(c->n_kv, c->head_dim, c->kv_stride);
-    cache_bytes = (size_t)nl * 2 * c->layer_elems * 2;
-    if (hip_ok(hipMalloc((void**)&c->d_cache, cache_bytes), err, errlen, "KV cache allocation") ||
-        hip_ok(hipMemsetAsync(c->d_cache, 0, cache_bytes, c->stream), err, errlen, "KV cache clear"))
+    cache_bytes = (size_t)c->n_kv_slots * 2 * c->layer_elems * 2;
+    if (cache_bytes &&
+        (hip_ok(hipMalloc((void**)&c->d_cache, cache_bytes), err, errlen, "KV cache allocation") ||
+         hip_ok(hipMemsetAsync(c->d_cache, 0, cache_bytes, c->stream), err, errlen, "KV cache clear")))
         return -1;
-    c->dev_len = (uint32_t*)calloc(nl, sizeof(uint32_t));
+    c->dev_len = (uint32_t*)calloc(c->n_kv_slots + 1, sizeof(uint32_t));
     if (!c->dev_len) return say(err, errlen, "out of host memory", NULL);
+    if (c->n_gdn_slots) {
+        /* the HBM state is loaded from e->ssm_state by each layer's first call */
+        state_bytes = (size_t)c->n_v * c->hvd * c->hvd * 4;
+        c->state_ok = (uint8_t*)calloc(c->n_gdn_slots, 1);
+        c->h_state = (float*)malloc(state_bytes);
+        c->h_conv = (float*)malloc((size_t)c->kwidth * c->conv_chan * 4);
+        if (!c->state_ok || !c->h_state || !c->h_conv) return say(err, errlen, "out of host memory", NULL);
+        if (hip_ok(hipMalloc((void**)&c->d_state, state_bytes * c->n_gdn_slots), err, errlen, "GDN state allocation"))
+            return -1;
+    }
     if (ensure_cap(c, e->pb_cap > 0 ? e->pb_cap : 64) != 0) return say(err, errlen, "staging allocation", NULL);
     c->ws_bytes = yhip_attn_decode_workspace(1, c->max_seq, c->max_seq, c->n_heads, c->n_kv, c->head_dim);
     if (c->ws_bytes && hip_ok(hipMalloc(&c->d_ws, c->ws_bytes), err, errlen, "decode workspace")) return -1;
@@ -552,11 +897,13 @@ static int move_kv(Engine* e, uint32_t n_pos, int to_host)
 {
     HipCtx* c = ctx_of(e);
     uint32_t l;
-    if (!c || !c->d_cache || c->failed) return -1;
+    if (!c || !c->stream || c->failed) return -1;
     if (n_pos > c->max_seq) n_pos = c->max_seq;
+    if (!to_host && c->state_ok) memset(c->state_ok, 0, c->n_gdn_slots);
     for (l = c->first; l <= c->last && n_pos > 0; l++) {
         uint16_t* hk = e->kv + (size_t)l * e->max_seq * c->kv_dim;
         uint16_t* hv = e->kv + (size_t)(c->n_blocks + l) * e->max_seq * c->kv_dim;
+        if (c->kv_slot[l - c->first] < 0) continue;
         if (to_host) {
             uint16_t *dk, *dv;
             size_t bytes = (size_t)n_pos * c->kv_dim * 2;
@@ -572,7 +919,7 @@ static int move_kv(Engine* e, uint32_t n_pos, int to_host)
             }
             hipFree(dk);
         } else {
-            c->dev_len[l - c->first] = 0;
+            c->dev_len[c->kv_slot[l - c->first]] = 0;
             if (catch_up(c, e, l, n_pos) != 0) return -1;
         }
     }
