@@ -50,6 +50,7 @@ P = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     (128, 2, 4, 128, "n_kv_heads"),
     (128, 34, 2, 128, "16 query heads"),
     (128, 8, 2, 100, "multiple of 64"),
+    (256, 8, 2, 1 << 22, "under 2 GiB"),   # 4M positions x 256 dims x 2 B = 2 GiB per kv head
 ])
 def test_decode_rejects_bad_shapes(hiplib, hd, nh, nkv, stride, msg):
     rc = hiplib.yhip_attn_decode(P, P, P, P, 3, nh, nkv, hd, stride, None, None, 0, None)

@@ -41,6 +41,11 @@ int check_heads(const char* fn, uint32_t n_heads, uint32_t n_kv, uint32_t head_d
         return fail(YHIP_EINVAL, "%s: more than 16 query heads per kv head (%u/%u)", fn, n_heads, n_kv);
     if (kv_stride == 0 || kv_stride % 64 != 0)
         return fail(YHIP_EINVAL, "%s: kv_stride %u must be a positive multiple of 64", fn, kv_stride);
+    // the kernels address one kv head's K rows or V tiles with 32-bit buffer
+    // offsets and use offsets from 2 GiB up as "past the end"
+    if ((uint64_t)kv_stride * head_dim * 2 >= 0x80000000ull)
+        return fail(YHIP_EINVAL, "%s: one kv head's cache (kv_stride %u x head_dim %u) must stay under 2 GiB", fn,
+                    kv_stride, head_dim);
     return 0;
 }
 

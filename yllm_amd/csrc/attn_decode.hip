@@ -102,29 +102,44 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
 
     const int krow = 8 * (n >> 2) + (n & 3);  // + 4t for half t
 
-    auto load = [&](Frag<D>& f, uint32_t key0) {
-        const uint16_t* kp = K + (size_t)(key0 + krow) * D + g * 8;
+    // Block loads go through buffer resources over this kv head's K rows and
+    // V tiles, and every prefetch is issued, valid or not: with a fixed
+    // number of loads per block the compiler waits for exactly the block a
+    // step reads (a conditional prefetch makes it wait for all loads,
+    // including the one just issued for the next block).  A block past the
+    // split gets an offset beyond the resource; the hardware returns zeros
+    // for it without a memory access.
+    const uint32_t nblk = (kend - kbeg + kKeysPerBlock - 1) / kKeysPerBlock;
+    const uint32_t head_bytes = a.kv_stride * D * 2;
+    const __amdgpu_buffer_rsrc_t rK =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(K), 0, head_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rV =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(Vt), 0, head_bytes, 0x00020000);
+    const uint32_t k_lane = (krow * D + g * 8) * 2;      // bytes within a block's K rows
+    const uint32_t v_lane = (n * kVTile + g * 8) * 2;    // row d = n (+16b), positions 8g..8g+7
+    auto load = [&](Frag<D>& f, uint32_t blk) {
+        const uint32_t key0 = kbeg + blk * kKeysPerBlock;
+        const bool ok = blk < nblk;
+        const uint32_t kb = ok ? key0 * D * 2 + k_lane : 0x80000000u;
+        const uint32_t vb = ok ? (key0 / kVTile) * D * kVTile * 2 + v_lane : 0x80000000u;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int c = 0; c < NC; ++c)
-                f.k[t][c] = *reinterpret_cast<const f16x8*>(kp + (size_t)4 * t * D + c * 32);
-        // the tile holding key0..key0+31, row d = b*16+n, positions 8g..8g+7
-        const uint16_t* vp = Vt + (size_t)(key0 / kVTile) * D * kVTile + n * kVTile + g * 8;
+                f.k[t][c] = __builtin_bit_cast(
+                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rK, kb + (4 * t * D + c * 32) * 2, 0, 0));
 #pragma unroll
-        for (int b = 0; b < NB; ++b) f.v[b] = *reinterpret_cast<const f16x8*>(vp + b * 16 * kVTile);
+        for (int b = 0; b < NB; ++b)
+            f.v[b] = __builtin_bit_cast(f16x8,
+                                        __builtin_amdgcn_raw_buffer_load_b128(rV, vb + b * 16 * kVTile * 2, 0, 0));
     };
 
-    // Up to NBUF blocks of this wave in flight: the first ones are issued
-    // before q is read so the two latencies overlap.
+    // NBUF blocks of this wave in flight: the first ones are issued before q
+    // is read so the two latencies overlap.
     constexpr int NBUF = nbuf_of<D>();
     Frag<D> f[NBUF];
-    const uint32_t nblk = (kend - kbeg + kKeysPerBlock - 1) / kKeysPerBlock;
 #pragma unroll
-    for (int i = 0; i < NBUF; ++i) {
-        const uint32_t b = wave + i * kWaves;
-        if (b < nblk) load(f[i], kbeg + b * kKeysPerBlock);
-    }
+    for (int i = 0; i < NBUF; ++i) load(f[i], wave + i * kWaves);
 
     // B operand of the score MFMA: head slot n, dims c*32 + 8g .. +7
     f16x8 qhi[NC], qlo[NC];
@@ -212,8 +227,7 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
                 break;
             }
             compute(f[i], kbeg + b * kKeysPerBlock);
-            const uint32_t nb = b + NBUF * kWaves;
-            if (nb < nblk) load(f[i], kbeg + nb * kKeysPerBlock);
+            load(f[i], b + NBUF * kWaves);
         }
         if (stop) break;
     }

@@ -172,6 +172,12 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         const size_t base = (size_t)my_q * a.q_stride + (size_t)h * D + hh * 8;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, base + kk * 16, a.q_dtype);
+        // Complete the query loads here.  Their first reader is the first
+        // score MFMA inside the key loop, whose tile loads are conditional;
+        // left pending, the wait the compiler places before that MFMA cannot
+        // count the tile loads and becomes a full vmcnt(0) on every step,
+        // exposing the next tile's global latency each time.
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     }
 
     // Buffer resources over this kv head's K rows and V tiles (reads past the
