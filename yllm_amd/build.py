@@ -73,6 +73,14 @@ def build(verbose: bool = True) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
+    # A kernel whose body the host pass could not instantiate leaves its
+    # launch stub undefined without any compiler error; the library would
+    # then fail to load.  Refuse it here.
+    nm = subprocess.run(["nm", "-D", "--undefined-only", str(tmp)], capture_output=True, text=True)
+    stubs = [l.split()[-1] for l in nm.stdout.splitlines() if "__device_stub__" in l]
+    if stubs:
+        tmp.unlink()
+        raise RuntimeError("kernel launch stubs missing from the host objects: " + ", ".join(stubs))
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources for {ARCH}")

@@ -8,9 +8,9 @@
 // Tiling.  A workgroup owns 128 consecutive queries of one query head; each
 // of its 4-wave key groups (one or two, see prefill_groups) gives wave w 32
 // of them.  Keys stream through LDS in tiles of 64 (K rows [64][D] and V^T
-// [D][64], straight from the cache layout), loaded with buffer
-// instructions into registers -- K two tiles ahead, V one -- and stored to
-// padded LDS rows.  With two groups, group g takes tiles g, g+2, ... and
+// [D][64], straight from the cache layout), loaded from HBM directly into
+// LDS -- K two tiles ahead, V one -- as unpadded rows with XOR-swizzled
+// 16-byte chunks.  With two groups, group g takes tiles g, g+2, ... and
 // the partial (max, sum, O) of the groups merge through LDS at the end.
 // Workgroups are issued heaviest (latest queries) first so the causal
 // triangle drains evenly.
@@ -31,6 +31,7 @@
 
 #include <math.h>
 #include <stdlib.h>
+
 
 namespace yhip {
 namespace {
@@ -104,27 +105,57 @@ __device__ inline void store_out4(void* out, size_t off, uint32_t dt, f32x4 v)
     }
 }
 
+// One 16-byte HBM -> LDS load per lane: lane i writes at lds + 16 i.  A
+// __device__ function, not a lambda: lambdas in a kernel are host-device, and
+// the host compilation pass silently drops a kernel whose lambdas call this
+// gfx950-only builtin.
+__device__ inline void lds_load16(__amdgpu_buffer_rsrc_t r, _Float16* lds, int voff, uint32_t soff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+// 16-byte chunk swizzle of an LDS tile row (XOR into the chunk index).  For
+// rows of 8 chunks (128 B) the swizzle is (r & 7) ^ bit 3 of r: 8 consecutive
+// rows then hit 8 distinct chunk columns (32-bank LDS, b128 reads in groups
+// of 8 lanes) and 16 consecutive rows give each half of a 256-byte bank
+// window 8 distinct columns (64 banks, groups of 16 lanes).  Rows of 16 or
+// more chunks (256 B and up) use r & 15.  Both depend on bits 0..3 of the
+// row only, so rows 32 apart share the swizzle.
+template <int NCH>
+__device__ inline int chunk_swz(int r)
+{
+    return NCH >= 16 ? (r & 15) : ((r & 7) ^ ((r >> 3) & 1));
+}
+
 template <int D, int NG>
 __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefill_kernel(PrefillArgs a)
 {
-    constexpr int KS = D + 8;     // K tile row stride (halfs), 16 B pad
-    constexpr int VS = BN + 8;    // V tile row stride (halfs)
+    static_assert(NG == 1 || NG == 2, "one or two key groups");
     constexpr int NKK = D / 16;   // k-chunks of the score MFMA
     constexpr int NDB = D / 32;   // d-blocks of the output MFMA
     constexpr int CH = D / 32;    // 16-byte chunks per thread per tile (K and V each)
     constexpr int KCH = D / 8;    // 16-byte chunks per K row
+    constexpr int VCH = BN / 8;   // 16-byte chunks per V row
     constexpr float kSlack = 8.0f;
     // NG key groups of 4 waves share the workgroup's 128 queries: group g
     // walks key tiles g, g+NG, g+2NG, ... with its own LDS buffers, and the
     // groups' partial results are merged at the end, so the longest chain
-    // of dependent tiles a wave walks is 1/NG of the causal row.  Within a
-    // group K is staged two of its tiles ahead (the score MFMAs of its next
-    // tile run during the softmax of the current one) and V one tile ahead,
-    // each double buffered; every buffer is rewritten only after the
-    // barrier that ends its last reader's step, so one barrier per step
-    // suffices (plus one in the first step, after the prologue's scores).
-    __shared__ _Float16 Kl[2][NG][BN * KS];
-    __shared__ _Float16 Vl[2][NG][D * VS];
+    // of dependent tiles a wave walks is 1/NG of the causal row.
+    //
+    // Tiles go from HBM straight into LDS (buffer loads with the LDS
+    // destination; lane i of a load writes 16 bytes at base + 16 i), K rows
+    // [64][D] and V^T rows [D][64], unpadded with swizzled 16-byte chunks.
+    // Within a group K is loaded two of its tiles ahead (the score MFMAs of
+    // its next tile run during the softmax of the current one) and V one
+    // tile ahead, each double buffered.  Buffers of parity 0 and 1 are
+    // separate variables, so the compiler can see that a step's loads in
+    // flight (into one parity) never alias its LDS reads (of the other) and
+    // does not wait for them; each thread waits for its own loads before the
+    // barrier that ends the step.
+    __shared__ __attribute__((aligned(16))) _Float16 Kl0[NG][BN * D];
+    __shared__ __attribute__((aligned(16))) _Float16 Kl1[NG][BN * D];
+    __shared__ __attribute__((aligned(16))) _Float16 Vl0[NG][D * BN];
+    __shared__ __attribute__((aligned(16))) _Float16 Vl1[NG][D * BN];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int grp = tid >> 8, gtid = tid & 255, wave = gtid >> 6;
@@ -175,65 +206,69 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // Complete the query loads here.  Their first reader is the first
         // score MFMA inside the key loop, whose tile loads are conditional;
         // left pending, the wait the compiler places before that MFMA cannot
-        // count the tile loads and becomes a full vmcnt(0) on every step,
-        // exposing the next tile's global latency each time.
+        // count the tile loads and becomes a full vmcnt(0) on every step.
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     }
 
-    // Buffer resources over this kv head's K rows and V tiles (reads past the
-    // cache return zeros).  Per-thread offsets are fixed; a tile adds the
-    // scalar kt*BN*D*2 bytes (the same for K rows and 32-position V tiles).
+    // Buffer resources over this kv head's K rows and V tiles.  A tile adds
+    // the scalar offset kt*BN*D*2 bytes (the same for K rows and two
+    // 32-position V tiles); every tile lies inside the cache (kv_stride is a
+    // multiple of 64 above kmax).
     const uint32_t head_bytes = a.kv_stride * D * 2;
     const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.kc + k_index(kvh, 0, 0, D, a.kv_stride)), 0, head_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.vc + v_index(kvh, 0, 0, D, a.kv_stride)), 0, head_bytes, 0x00020000);
-    int kgo[CH], klo[CH], vlo[CH], vkey[CH];
+    // Chunk L = 256 i + gtid of a tile is the 16 bytes this thread loads with
+    // its i-th instruction.  K: LDS row R = L / KCH holds key row
+    // lds_row_of_key(R) (an involution), column chunk (L % KCH) ^ swz(R).
+    // V: LDS row d = L / VCH holds positions 8c..8c+7 in chunk
+    // (L % VCH) ^ swz(d), from 32-position tile c / 4.
+    int kgo[CH], vgo[CH];
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
-        const int c = gtid + 256 * i;
-        const int row = c / KCH, col = c % KCH;
-        kgo[i] = (row * D + col * 8) * 2;
-        klo[i] = lds_row_of_key(row) * KS + col * 8;
-        // V chunk c: 32-position tile c/(4D), row d, 8 positions
-        const int t = c / (4 * D), r = c % (4 * D);
-        vkey[i] = t * (int)kVTile + (r & 3) * 8;  // key of the chunk within the 64-key tile
-        vlo[i] = (r >> 2) * VS + vkey[i];
+        const int L = gtid + 256 * i;
+        const int R = L / KCH, kc = (L % KCH) ^ chunk_swz<KCH>(R);
+        kgo[i] = (lds_row_of_key(R) * D + kc * 8) * 2;
+        const int d = L / VCH, vc = (L % VCH) ^ chunk_swz<VCH>(d);
+        vgo[i] = (vc >> 2) * (D * (int)kVTile * 2) + d * (int)kVTile * 2 + (vc & 3) * 16;
     }
-    u32x4 kreg[CH], vreg[CH];
-    auto load_k = [&](uint32_t st) {
+    // buffers by parity (a constant at every call after inlining)
+    auto kbuf = [&](int par) { return par ? &Kl1[grp][0] : &Kl0[grp][0]; };
+    auto vbuf = [&](int par) { return par ? &Vl1[grp][0] : &Vl0[grp][0]; };
+    auto dma_k = [&](int par, uint32_t st) {
         const uint32_t off = tile_of(st) * BN * D * 2;
-#pragma unroll
-        for (int i = 0; i < CH; ++i)
-            kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rK, kgo[i], off, 0));
-    };
-    auto load_v = [&](uint32_t st) {
-        const uint32_t off = tile_of(st) * BN * D * 2;
-#pragma unroll
-        for (int i = 0; i < CH; ++i)
-            vreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rV, gtid * 16 + i * 4096, off, 0));
-    };
-    auto store_k = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < CH; ++i) *reinterpret_cast<u32x4*>(&Kl[buf][grp][klo[i]]) = kreg[i];
-    };
-    auto store_v = [&](int buf, uint32_t st) {
-        const uint32_t k0 = tile_of(st) * BN;
-        const bool tail = k0 + BN - 1 > kmax;
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-            u32x4 v = vreg[i];
-            if (tail) {
-                // keys past kmax were never stored: their P is 0, their V must be finite
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t key = k0 + vkey[i] + 2 * e;
-                    if (key > kmax) v[e] = 0u;
-                    else if (key + 1 > kmax) v[e] &= 0xffffu;
-                }
-            }
-            *reinterpret_cast<u32x4*>(&Vl[buf][grp][vlo[i]]) = v;
+            lds_load16(rK, kbuf(par) + (256 * i + 64 * wave) * 8, kgo[i], off);
         }
+    };
+    auto dma_v = [&](int par, uint32_t st) {
+        const uint32_t off = tile_of(st) * BN * D * 2;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            lds_load16(rV, vbuf(par) + (256 * i + 64 * wave) * 8, vgo[i], off);
+        }
+    };
+    auto dma_done = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };  // vmcnt(0): this thread's tile loads landed
+
+    // MFMA operands from LDS.  K fragment (j, kk): key row r32 + 32 j, dims
+    // 16 kk + 8 hh .. +7 = chunk 2 kk + hh.  V fragment (b, kc): row
+    // d = 32 b + r32, positions 16 kc + 8 hh .. +7 = chunk 2 kc + hh.
+    const int ksw = chunk_swz<KCH>(r32), vsw = chunk_swz<VCH>(r32);
+    auto read_k = [&](int par, int j, int kk) {
+        return *reinterpret_cast<const f16x8*>(kbuf(par) + (r32 + 32 * j) * D + (((2 * kk + hh) ^ ksw) << 3));
+    };
+    auto read_v = [&](int par, int b, int kc, uint32_t k0) {
+        f16x8 v = *reinterpret_cast<const f16x8*>(vbuf(par) + (32 * b + r32) * BN + (((2 * kc + hh) ^ vsw) << 3));
+        if (k0 + BN - 1 > kmax) {
+            // keys past kmax were never stored and may hold any bits: their P
+            // is 0, their V must be finite
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (k0 + 16 * kc + 8 * hh + e > kmax) v[e] = (_Float16)0.0f;
+        }
+        return v;
     };
 
     // running max (log2 domain): finite so that a tile whose keys are all in
@@ -246,14 +281,13 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
 
-    // scores of step st's tile into S (both 32-key halves)
-    auto qk = [&](f32x16 (&S)[2], uint32_t st) {
-        const _Float16* kr = &Kl[st & 1][grp][r32 * KS + hh * 8];
+    // scores of the tile in K buffer P into S (both 32-key halves)
+    auto qk = [&](f32x16 (&S)[2], int par) {
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const f16x8 kf = *reinterpret_cast<const f16x8*>(kr + 32 * j * KS + kk * 16);
+                const f16x8 kf = read_k(par, j, kk);
                 S[j] = kk == 0 ? mfma32(kf, qf[0], f32x16{}) : mfma32(kf, qf[kk], S[j]);
             }
     };
@@ -283,32 +317,35 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
             pf[i >> 3][i & 7] = (_Float16)p;
         }
     };
-    auto pv = [&](const f16x8 (&pf)[4], uint32_t st) {
-        const _Float16* vr = &Vl[st & 1][grp][r32 * VS + hh * 8];
+    // O^T += V^T P^T over the tile in V buffer P; fragments are read two
+    // MFMAs ahead (three in a ring)
+    auto pv = [&](const f16x8 (&pf)[4], int par, uint32_t st) {
+        constexpr int NM = 4 * NDB;  // MFMA n: kc = n / NDB, b = n % NDB
+        const uint32_t k0 = tile_of(st) * BN;
+        f16x8 vf[3];
+        vf[0] = read_v(par, 0, 0, k0);
+        vf[1] = read_v(par, 1 % NDB, 1 / NDB, k0);
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc)
-#pragma unroll
-            for (int b = 0; b < NDB; ++b)  // independent accumulators back to back
-                o[b] = mfma32(*reinterpret_cast<const f16x8*>(vr + b * 32 * VS + kc * 16), pf[kc], o[b]);
+        for (int n = 0; n < NM; ++n) {
+            if (n + 2 < NM) vf[(n + 2) % 3] = read_v(par, (n + 2) % NDB, (n + 2) / NDB, k0);
+            o[n % NDB] = mfma32(vf[n % 3], pf[n / NDB], o[n % NDB]);
+        }
     };
-    // scores of step st's tile into Snext while the probabilities of Scur are
-    // formed: each score MFMA is followed by the exp2 work it can hide
-    auto qk_probs = [&](f32x16 (&Snext)[2], uint32_t st, const f32x16 (&Scur)[2], f16x8 (&pf)[4]) {
+    // scores of the tile in K buffer P into Snext while the probabilities of
+    // Scur are formed: each score MFMA is followed by the exp2 work it can
+    // hide, and K fragments are read two MFMAs ahead
+    auto qk_probs = [&](f32x16 (&Snext)[2], int par, const f32x16 (&Scur)[2], f16x8 (&pf)[4]) {
         constexpr int PPM = 32 / (2 * NKK);  // probabilities per MFMA
-        const _Float16* kr = &Kl[st & 1][grp][r32 * KS + hh * 8];
+        constexpr int NM = 2 * NKK;          // MFMA n: kk = n / 2, half j = n % 2
         const float nm = -m;
-        // MFMA n = kk*2 + j (halves alternate, so neighbours are independent);
-        // its K fragment is read one MFMA ahead
-        f16x8 kf = *reinterpret_cast<const f16x8*>(kr);
+        f16x8 kf[3];
+        kf[0] = read_k(par, 0, 0);
+        kf[1] = read_k(par, 1, 0);
 #pragma unroll
-        for (int n = 0; n < 2 * NKK; ++n) {
+        for (int n = 0; n < NM; ++n) {
             const int kk = n >> 1, j = n & 1;
-            f16x8 kn = kf;
-            if (n + 1 < 2 * NKK) {
-                const int kk1 = (n + 1) >> 1, j1 = (n + 1) & 1;
-                kn = *reinterpret_cast<const f16x8*>(kr + 32 * j1 * KS + kk1 * 16);
-            }
-            Snext[j] = kk == 0 ? mfma32(kf, qf[0], f32x16{}) : mfma32(kf, qf[kk], Snext[j]);
+            if (n + 2 < NM) kf[(n + 2) % 3] = read_k(par, (n + 2) & 1, (n + 2) >> 1);
+            Snext[j] = kk == 0 ? mfma32(kf[n % 3], qf[0], f32x16{}) : mfma32(kf[n % 3], qf[kk], Snext[j]);
 #pragma unroll
             for (int u = 0; u < PPM; ++u) {
                 const int i = n * PPM + u;
@@ -316,8 +353,7 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
                 l += p;
                 pf[i >> 3][i & 7] = (_Float16)p;
             }
-            kf = kn;
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // next fragment's LDS read
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // a fragment read two ahead
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // this MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, 4 * PPM, 0);  // softmax work it hides
         }
@@ -337,81 +373,77 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
 
     // prologue: the group's first K, V and second K in LDS; scores of step 0
     if (gsteps > 0) {
-        load_k(0);
-        load_v(0);
-        store_k(0);
-        store_v(0, 0);
+        dma_k(0, 0);
+        dma_v(0, 0);
     }
-    if (gsteps > 1) {
-        load_k(1);
-        store_k(1);
-    }
+    if (gsteps > 1) dma_k(1, 1);
+    dma_done();
     __syncthreads();
     f32x16 Sa[2], Sb[2];
     if (wsteps > 0) qk(Sa, 0);
+    // step 0 loads K(2) over K(0), whose last readers are the scores above
+    __syncthreads();
 
-    // step st: loads K(st+2), V(st+1); scores of st+1 overlap the softmax of
-    // st; P.V of st; stores K(st+2) over K(st) and V(st+1) over V(st-1); one
-    // barrier.  With pos_start not a multiple of 32 a wave's queries straddle
-    // a tile boundary, so a tile with a successor may still need the mask.
-    auto step = [&](uint32_t st, f32x16 (&Scur)[2], f32x16 (&Snext)[2]) {
-        if (st + 2 < gsteps) load_k(st + 2);
-        if (st + 1 < gsteps) load_v(st + 1);
+    // step st (parity p = st % 2): loads K(st+2) into K buffer p (it held
+    // K(st), last read by the previous step's scores) and V(st+1) into V
+    // buffer 1-p (it held V(st-1)); scores of st+1 (K buffer 1-p) overlap the
+    // softmax of st; P.V of st (V buffer p); one barrier.  With pos_start
+    // not a multiple of 32 a wave's queries straddle a tile boundary, so a
+    // tile with a successor may still need the mask.
+    auto step = [&](int p, uint32_t st, f32x16 (&Scur)[2], f32x16 (&Snext)[2]) {
+        if (st + 2 < gsteps) dma_k(p, st + 2);
+        if (st + 1 < gsteps) dma_v(1 - p, st + 1);
         if (st + 1 < wsteps) {
             mask(Scur, st);
             update_max(Scur);
             f16x8 pf[4];
-            qk_probs(Snext, st + 1, Scur, pf);
-            pv(pf, st);
+            qk_probs(Snext, 1 - p, Scur, pf);
+            pv(pf, p, st);
         } else if (st < wsteps) {
             mask(Scur, st);
             update_max(Scur);
             f16x8 pf[4];
             probs(Scur, pf);
-            pv(pf, st);
+            pv(pf, p, st);
         }
-        // K(0)'s last reader is the prologue's score pass, which no barrier
-        // separates from the first store over it
-        if (st == 0) __syncthreads();
-        if (st + 2 < gsteps) store_k(st & 1);
-        if (st + 1 < gsteps) store_v((st + 1) & 1, st + 1);
+        dma_done();
         __syncthreads();
     };
     for (uint32_t st = 0; st < nsteps; st += 2) {
-        step(st, Sa, Sb);
-        if (st + 1 < nsteps) step(st + 1, Sb, Sa);
+        step(0, st, Sa, Sb);
+        if (st + 1 < nsteps) step(1, st + 1, Sb, Sa);
     }
 
     l += __shfl_xor(l, 32, 64);
-    if (NG > 1) {
-        // groups 1..NG-1 hand (m, l, O) to group 0 through LDS; the tile
-        // buffers are free after the last step's barrier
-        constexpr int NV = NDB * 16 + 2;  // floats per lane
-        static_assert(NV * 256 * 4 * (NG - 1) <= (int)sizeof(Kl), "merge area");
-        float* xo = reinterpret_cast<float*>(&Kl[0][0][0]) + (size_t)(grp > 0 ? grp - 1 : 0) * NV * 256;
-        if (grp > 0) {
-            xo[gtid] = m;
-            xo[256 + gtid] = l;
+    if constexpr (NG > 1) {
+        // group 1 hands (m, l, O) to group 0 through LDS, free after the last
+        // step's barrier: m, l in V buffer 0, O blocks 0..NDB/2-1 in K buffer
+        // 0 and the rest in K buffer 1 (16 floats x 256 lanes per block)
+        static_assert(NDB / 2 * 16 * 256 * 4 <= (int)sizeof(Kl0) && 2 * 256 * 4 <= (int)sizeof(Vl0), "merge area");
+        float* ml = reinterpret_cast<float*>(&Vl0[0][0]);
+        auto oarea = [&](int b) {
+            return b < NDB / 2 ? reinterpret_cast<float*>(&Kl0[0][0]) + b * 16 * 256
+                               : reinterpret_cast<float*>(&Kl1[0][0]) + (b - NDB / 2) * 16 * 256;
+        };
+        if (grp == 1) {
+            ml[gtid] = m;
+            ml[256 + gtid] = l;
 #pragma unroll
             for (int b = 0; b < NDB; ++b)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) xo[(2 + b * 16 + i) * 256 + gtid] = o[b][i];
+                for (int i = 0; i < 16; ++i) oarea(b)[i * 256 + gtid] = o[b][i];
         }
         __syncthreads();
-        if (grp > 0) return;
+        if (grp == 1) return;
+        const float m1 = ml[gtid], l1 = ml[256 + gtid];
+        const float mg = fmaxf(m, m1);
+        const float a0 = fast_exp2(m - mg), a1 = fast_exp2(m1 - mg);
+        m = mg;
+        l = l * a0 + l1 * a1;
 #pragma unroll
-        for (int g = 1; g < NG; ++g) {
-            const float* xi = reinterpret_cast<const float*>(&Kl[0][0][0]) + (size_t)(g - 1) * NV * 256;
-            const float m1 = xi[gtid], l1 = xi[256 + gtid];
-            const float mg = fmaxf(m, m1);
-            const float a0 = fast_exp2(m - mg), a1 = fast_exp2(m1 - mg);
-            m = mg;
-            l = l * a0 + l1 * a1;
+        for (int b = 0; b < NDB; ++b)
 #pragma unroll
-            for (int b = 0; b < NDB; ++b)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[b][i] = o[b][i] * a0 + xi[(2 + b * 16 + i) * 256 + gtid] * a1;
-        }
+            for (int i = 0; i < 16; ++i) o[b][i] = o[b][i] * a0 + oarea(b)[i * 256 + gtid] * a1;
     }
     if (!wave_active) return;
     const uint32_t qi = wq0 + r32;
