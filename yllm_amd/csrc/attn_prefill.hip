@@ -127,6 +127,44 @@ __device__ inline int chunk_swz(int r)
     return NCH >= 16 ? (r & 15) : ((r & 7) ^ ((r >> 3) & 1));
 }
 
+// Schedule of one key step's MFMAs: NQ score MFMAs of the next tile and NPV
+// P.V MFMAs of this tile (k-slot kc = n / NDB uses the probabilities
+// 8 kc .. 8 kc + 7), with the tile's 32 probabilities spread over them.
+// The exp2 of a probability is quarter rate (about as long as half a
+// 32x32x16 MFMA with its fma, add and convert), so one to two per MFMA hide
+// under the matrix pipe, where 32 under the score MFMAs alone or under the
+// PV MFMAs alone would not.  Slot order: the first NQ/2 score MFMAs under
+// k-slot 0's probabilities; then for kc = 0..3 k-slot kc's PV MFMAs
+// interleaved with the next score MFMAs under k-slot kc+1's probabilities.
+struct FSlot {
+    int8_t pv;  // 0: score MFMA n, 1: PV MFMA n
+    int8_t n;
+    int8_t p0;  // probabilities p0 .. p0+np-1 formed after this MFMA
+    int8_t np;
+};
+template <int NQ, int NPV, int NDB>
+struct FusedSchedule {
+    static constexpr int N = NQ + NPV;
+    FSlot s[N];
+    constexpr FusedSchedule() : s{}
+    {
+        const int QA = NQ / 2, QB = (NQ - QA + 2) / 3;
+        int k = 0, q = 0, v = 0;
+        for (int t = 0; t < QA; ++t)
+            s[k++] = FSlot{0, (int8_t)q++, (int8_t)(t * 8 / QA), (int8_t)((t + 1) * 8 / QA - t * 8 / QA)};
+        for (int kc = 0; kc < 4; ++kc) {
+            const int nq = kc < 3 ? (QB < NQ - q ? QB : NQ - q) : NQ - q;
+            const int tot = NDB + nq;
+            for (int t = 0; t < tot; ++t) {
+                const bool is_pv = (t + 1) * NDB / tot > t * NDB / tot;
+                const int p0 = kc < 3 ? 8 * (kc + 1) + t * 8 / tot : 0;
+                const int np = kc < 3 ? (t + 1) * 8 / tot - t * 8 / tot : 0;
+                s[k++] = FSlot{(int8_t)is_pv, (int8_t)(is_pv ? v++ : q++), (int8_t)p0, (int8_t)np};
+            }
+        }
+    }
+};
+
 template <int D, int NG>
 __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefill_kernel(PrefillArgs a)
 {
@@ -259,16 +297,26 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
     auto read_k = [&](int par, int j, int kk) {
         return *reinterpret_cast<const f16x8*>(kbuf(par) + (r32 + 32 * j) * D + (((2 * kk + hh) ^ ksw) << 3));
     };
-    auto read_v = [&](int par, int b, int kc, uint32_t k0) {
-        f16x8 v = *reinterpret_cast<const f16x8*>(vbuf(par) + (32 * b + r32) * BN + (((2 * kc + hh) ^ vsw) << 3));
-        if (k0 + BN - 1 > kmax) {
-            // keys past kmax were never stored and may hold any bits: their P
-            // is 0, their V must be finite
+    auto read_v = [&](int par, int b, int kc) {
+        return *reinterpret_cast<const f16x8*>(vbuf(par) + (32 * b + r32) * BN + (((2 * kc + hh) ^ vsw) << 3));
+    };
+    // Keys past kmax in the workgroup's last tile were never stored and may
+    // hold any bits: their P is 0, but their V must be finite.  The group
+    // that owns that tile zeroes them in LDS once, in the step that reads it.
+    auto zero_v_tail = [&](int par, uint32_t st) {
+        const uint32_t k0 = tile_of(st) * BN;
+        const uint32_t valid = kmax - k0 + 1;  // keys 0..valid-1 of the tile are stored
+        _Float16* vb = vbuf(par);
+        for (int idx = gtid; idx < D * VCH; idx += 256) {
+            const int d = idx / VCH, c = idx % VCH;  // logical chunk c: keys 8c..8c+7
+            if ((uint32_t)(8 * c + 7) < valid) continue;
+            f16x8* ch = reinterpret_cast<f16x8*>(vb + d * BN + ((c ^ chunk_swz<VCH>(d)) << 3));
+            f16x8 v = *ch;
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                if (k0 + 16 * kc + 8 * hh + e > kmax) v[e] = (_Float16)0.0f;
+                if ((uint32_t)(8 * c + e) >= valid) v[e] = (_Float16)0.0f;
+            *ch = v;
         }
-        return v;
     };
 
     // running max (log2 domain): finite so that a tile whose keys are all in
@@ -319,43 +367,50 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
     };
     // O^T += V^T P^T over the tile in V buffer P; fragments are read two
     // MFMAs ahead (three in a ring)
-    auto pv = [&](const f16x8 (&pf)[4], int par, uint32_t st) {
+    auto pv = [&](const f16x8 (&pf)[4], int par) {
         constexpr int NM = 4 * NDB;  // MFMA n: kc = n / NDB, b = n % NDB
-        const uint32_t k0 = tile_of(st) * BN;
         f16x8 vf[3];
-        vf[0] = read_v(par, 0, 0, k0);
-        vf[1] = read_v(par, 1 % NDB, 1 / NDB, k0);
+        vf[0] = read_v(par, 0, 0);
+        vf[1] = read_v(par, 1 % NDB, 1 / NDB);
 #pragma unroll
         for (int n = 0; n < NM; ++n) {
-            if (n + 2 < NM) vf[(n + 2) % 3] = read_v(par, (n + 2) % NDB, (n + 2) / NDB, k0);
+            if (n + 2 < NM) vf[(n + 2) % 3] = read_v(par, (n + 2) % NDB, (n + 2) / NDB);
             o[n % NDB] = mfma32(vf[n % 3], pf[n / NDB], o[n % NDB]);
         }
     };
-    // scores of the tile in K buffer P into Snext while the probabilities of
-    // Scur are formed: each score MFMA is followed by the exp2 work it can
-    // hide, and K fragments are read two MFMAs ahead
-    auto qk_probs = [&](f32x16 (&Snext)[2], int par, const f32x16 (&Scur)[2], f16x8 (&pf)[4]) {
-        constexpr int PPM = 32 / (2 * NKK);  // probabilities per MFMA
-        constexpr int NM = 2 * NKK;          // MFMA n: kk = n / 2, half j = n % 2
+    // Scores of the next tile (K buffer kpar) into Snext and P.V of this tile
+    // (V buffer vpar), with this tile's probabilities (from Scur) formed
+    // between them per FusedSchedule; K and V fragments are read two MFMAs
+    // ahead in their own streams.
+    auto qk_pv = [&](f32x16 (&Snext)[2], int kpar, const f32x16 (&Scur)[2], int vpar) {
+        constexpr int NQ = 2 * NKK, NPV = 4 * NDB;
+        constexpr FusedSchedule<NQ, NPV, NDB> sch{};
+        constexpr int MAXP = 8;
         const float nm = -m;
-        f16x8 kf[3];
-        kf[0] = read_k(par, 0, 0);
-        kf[1] = read_k(par, 1, 0);
+        f16x8 pf[4], kf[3], vf[3];
+        kf[0] = read_k(kpar, 0, 0);
+        kf[1] = read_k(kpar, 1, 0);
+        vf[0] = read_v(vpar, 0, 0);
+        vf[1] = read_v(vpar, 1 % NDB, 1 / NDB);
 #pragma unroll
-        for (int n = 0; n < NM; ++n) {
-            const int kk = n >> 1, j = n & 1;
-            if (n + 2 < NM) kf[(n + 2) % 3] = read_k(par, (n + 2) & 1, (n + 2) >> 1);
-            Snext[j] = kk == 0 ? mfma32(kf[n % 3], qf[0], f32x16{}) : mfma32(kf[n % 3], qf[kk], Snext[j]);
-#pragma unroll
-            for (int u = 0; u < PPM; ++u) {
-                const int i = n * PPM + u;
-                const float p = fast_exp2(fmaf(Scur[i >> 4][i & 15], a.c, nm));
-                l += p;
-                pf[i >> 3][i & 7] = (_Float16)p;
+        for (int t = 0; t < sch.N; ++t) {
+            const int n = sch.s[t].n;
+            if (sch.s[t].pv) {
+                if (n + 2 < NPV) vf[(n + 2) % 3] = read_v(vpar, (n + 2) % NDB, (n + 2) / NDB);
+                o[n % NDB] = mfma32(vf[n % 3], pf[n / NDB], o[n % NDB]);
+            } else {
+                if (n + 2 < NQ) kf[(n + 2) % 3] = read_k(kpar, (n + 2) & 1, (n + 2) >> 1);
+                Snext[n & 1] = n < 2 ? mfma32(kf[n % 3], qf[0], f32x16{}) : mfma32(kf[n % 3], qf[n >> 1], Snext[n & 1]);
             }
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // a fragment read two ahead
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // this MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 4 * PPM, 0);  // softmax work it hides
+#pragma unroll
+            for (int u = 0; u < MAXP; ++u) {
+                if (u < sch.s[t].np) {
+                    const int i = sch.s[t].p0 + u;
+                    const float p = fast_exp2(fmaf(Scur[i >> 4][i & 15], a.c, nm));
+                    l += p;
+                    pf[i >> 3][i & 7] = (_Float16)p;
+                }
+            }
         }
     };
     // a tile that reaches past the wave's first query: keys beyond the
@@ -390,21 +445,25 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
     // softmax of st; P.V of st (V buffer p); one barrier.  With pos_start
     // not a multiple of 32 a wave's queries straddle a tile boundary, so a
     // tile with a successor may still need the mask.
+    const uint32_t tail_step = (ntiles - 1) / NG;  // the step that reads the last tile
+    const int tail_grp = (int)((ntiles - 1) % NG);  // in this group's buffers
     auto step = [&](int p, uint32_t st, f32x16 (&Scur)[2], f32x16 (&Snext)[2]) {
         if (st + 2 < gsteps) dma_k(p, st + 2);
         if (st + 1 < gsteps) dma_v(1 - p, st + 1);
+        if (st == tail_step && (kmax + 1) % BN != 0) {  // workgroup-uniform
+            if (grp == tail_grp) zero_v_tail(p, st);
+            __syncthreads();
+        }
         if (st + 1 < wsteps) {
             mask(Scur, st);
             update_max(Scur);
-            f16x8 pf[4];
-            qk_probs(Snext, 1 - p, Scur, pf);
-            pv(pf, p, st);
+            qk_pv(Snext, 1 - p, Scur, p);
         } else if (st < wsteps) {
             mask(Scur, st);
             update_max(Scur);
             f16x8 pf[4];
             probs(Scur, pf);
-            pv(pf, p, st);
+            pv(pf, p);
         }
         dma_done();
         __syncthreads();
