@@ -48,6 +48,7 @@ HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
 MFMA_F16_PEAK = 2.5e15   # FLOP/s, dense f16/bf16 MFMA
 METRIC = "attn decode GB/s (% HBM peak); prefill attn TFLOP/s (% MFMA peak)"
 SEED = 0x5EED0000
+ROTATE_BYTES = 300 << 20  # rotating input sets exceed the 256 MB MALL (Infinity Cache)
 EAGER = False  # --eager: launch each step from the host (for counter collection)
 CHUNKED_GDN = True  # --gdn-tokenwise: time the token-by-token GDN kernel instead
 
@@ -141,10 +142,22 @@ def run_prefill(L: int, nh: int, nkv: int, hd: int, cfg: int, steps: int, warmup
     q = torch.from_numpy(synth(seed, nq).reshape(L, nh * hd)).to(dev).half()
     k = torch.from_numpy(synth(seed, nk, nq).reshape(L, nkv * hd)).to(dev).half()
     v = torch.from_numpy(synth(seed, nk, nq + nk).reshape(L, nkv * hd)).to(dev).half()
-    cache = LayerKV.empty(nkv, hd, L, device=dev)
-    kv_store(cache, k, v, 0)
-    out = torch.empty((L, nh * hd), dtype=torch.float32, device=dev)
-    ms, kern_ms = time_steps(lambda i: attn_prefill(q, cache, 0, nh, out=out), steps, warmup, out)
+    # Consecutive steps rotate over copies of (q, cache, out) whose total
+    # exceeds the 256 MB MALL, so every step reads its inputs from HBM.
+    set_bytes = nq * 2 + 2 * nk * 2 + L * nh * hd * 4
+    n_sets = max(1, -(-ROTATE_BYTES // set_bytes))
+    qs, caches, outs = [], [], []
+    for _ in range(n_sets):
+        c = LayerKV.empty(nkv, hd, L, device=dev)
+        kv_store(c, k, v, 0)
+        qs.append(q.clone())
+        caches.append(c)
+        outs.append(torch.empty((L, nh * hd), dtype=torch.float32, device=dev))
+    del q
+    last = (warmup + steps - 1) % n_sets
+    ms, kern_ms = time_steps(lambda i: attn_prefill(qs[i % n_sets], caches[i % n_sets], 0, nh, out=outs[i % n_sets]),
+                             steps, warmup, outs[last])
+    q, out = qs[last], outs[last]
     flops = prefill_flops(L, nh, hd)
     achieved = flops / (kern_ms * 1e-3)
     res = {
@@ -153,7 +166,8 @@ def run_prefill(L: int, nh: int, nkv: int, hd: int, cfg: int, steps: int, warmup
         "ms_per_step": ms,
         "tokens_per_s": L / (ms * 1e-3),
         "config": {"workload": f"causal GQA prefill attention, {L} tokens, {nh} query / {nkv} KV heads, "
-                               f"head_dim {hd}, f16 Q/K/V N(0,1)*0.5 seed {hex(seed)}, f32 out",
+                               f"head_dim {hd}, f16 Q/K/V N(0,1)*0.5 seed {hex(seed)}, f32 out; "
+                               f"{n_sets} rotating input sets (> 256 MB MALL)",
                    "tokens": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd},
         "roofline": {"bound": "mfma", "kernel": "prefill_kernel<%d>" % hd, "achieved": achieved / 1e12,
                      "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s", "frac": achieved / MFMA_F16_PEAK,
@@ -284,23 +298,30 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
     S = torch.zeros((n_h, d, d), device=dev)
     beta = torch.empty_like(beta_raw)
     gate = torch.empty_like(alpha)
-    out = torch.empty((T, n_h * d), device=dev)
     ws = torch.empty(max(gdn_chunk_workspace_bytes(T, n_h, d) // 4, 1), device=dev)
+    # rotating copies of the inputs and output beyond the 256 MB MALL
+    set_bytes = 4 * (4 * n + 2 * T * n_h)
+    n_sets = max(1, -(-ROTATE_BYTES // set_bytes))
+    sets = [(q.clone(), k.clone(), v.clone(), alpha.clone(), beta_raw.clone(), torch.empty((T, n_h * d), device=dev))
+            for _ in range(n_sets)]
 
     def step(i):
+        qi, ki, vi, ai, bi, oi = sets[i % n_sets]
         S.zero_()
-        beta.copy_(beta_raw)
-        gdn_gates(alpha, beta, dt, a, gate=gate)
-        gdn_chunk(S, q, k, v, gate, beta, n_h, out=out, workspace=ws, chunked=CHUNKED_GDN)
+        beta.copy_(bi)
+        gdn_gates(ai, beta, dt, a, gate=gate)
+        gdn_chunk(S, qi, ki, vi, gate, beta, n_h, out=oi, workspace=ws, chunked=CHUNKED_GDN)
 
-    ms, kern_ms = time_steps(step, steps, warmup, out)
+    ms, kern_ms = time_steps(step, steps, warmup, sets[(warmup + steps - 1) % n_sets][5])
+    out = sets[(warmup + steps - 1) % n_sets][5]
     nbytes, flops = gdn_bytes(T, n_h, n_h, d), gdn_flops(T, n_h, d)
     t_roof = max(nbytes / HBM_PEAK, flops / MFMA_F16_PEAK)
     res = {
         "value": T / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
         "config": {"workload": f"Gated DeltaNet layer prefill, {T} tokens, {n_h} heads, d_k = d_v = {d}, fp32, "
                                f"q/k/v/alpha/beta N(0,1)*0.5 seed {hex(seed)}, dt_bias 0, ssm_a -1, "
-                               f"gates + l2norm + recurrence ({'chunked' if CHUNKED_GDN else 'token by token'})",
+                               f"gates + l2norm + recurrence ({'chunked' if CHUNKED_GDN else 'token by token'}); "
+                               f"{n_sets} rotating input sets (> 256 MB MALL)",
                    "tokens": T, "heads": n_h, "head_dim": d},
         "roofline": {"bound": "hbm",
                      "kernel": ("gdn_prep_kernel<%d> + gdn_scan_kernel<%d>" % (d, d) if CHUNKED_GDN else
