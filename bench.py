@@ -339,35 +339,45 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
 
 def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
     """The fifth configuration: one group of 3 Gated-DeltaNet layers and 1
-    gated GQA attention layer, a 4096-token prefill then n_dec decode steps."""
+    gated GQA attention layer, a 4096-token prefill then n_dec decode steps.
+    A GDN layer's GPU part is conv1d + silu over its qkv rows, the gates, the
+    l2norm + recurrence, and the gated RMSNorm (the projections are not on
+    this path)."""
     import torch
 
     from yllm_amd.attention import (LayerKV, attn_decode, attn_prefill, decode_workspace, decode_workspace_bytes,
                                     kv_store)
-    from yllm_amd.gdn import gdn_chunk, gdn_chunk_workspace_bytes, gdn_gates, gdn_step
+    from yllm_amd.gdn import gdn_chunk, gdn_chunk_workspace_bytes, gdn_conv, gdn_gated_norm, gdn_gates, gdn_step
 
     dev = torch.device("cuda:0")
     seed = SEED + 5
-    T, n_gdn, hg, dg = 4096, 3, 16, 128          # GDN: 16 heads, d_k = d_v = 128
+    T, n_gdn, hg, dg, kw = 4096, 3, 16, 128, 4   # GDN: 16 heads, d_k = d_v = 128, conv width 4
     nh, nkv, da = 16, 2, 256                     # gated attention: 16 / 2 heads, d = 256
     L = T + n_dec
+    kd, conv = hg * dg, 3 * hg * dg              # q, k: kd channels each; v: hg*dg
     first = [0]
 
-    def draw(n, bf16=False):
+    def draw(n, bf16=False, scale=None):
         x = synth_raw(seed, n, first[0])
         first[0] += n
         t = torch.from_numpy(x).to(dev)
+        if scale is not None:
+            t = t * scale
         return t.to(torch.bfloat16) if bf16 else t
 
-    gd = [dict(q=draw(L * hg * dg).view(L, -1), k=draw(L * hg * dg).view(L, -1), v=draw(L * hg * dg).view(L, -1),
-               alpha=draw(L * hg).view(L, hg), beta_raw=draw(L * hg).view(L, hg)) for _ in range(n_gdn)]
+    gd = [dict(qkv=draw(L * conv).view(L, conv), z=draw(L * hg * dg).view(L, -1),
+               alpha=draw(L * hg).view(L, hg), beta_raw=draw(L * hg).view(L, hg),
+               conv_w=draw(conv * kw, scale=0.5).view(conv, kw), norm_w=draw(dg, scale=0.1) + 1.0)
+          for _ in range(n_gdn)]
     at = dict(q=draw(L * nh * da, True).view(L, -1), gate=draw(L * nh * da).view(L, -1),
               k=draw(L * nkv * da, True).view(L, -1), v=draw(L * nkv * da, True).view(L, -1))
     dt = torch.zeros(hg, device=dev)
     a = -torch.ones(hg, device=dev)
     S = [torch.zeros((hg, dg, dg), device=dev) for _ in range(n_gdn)]
+    cst = [torch.zeros((kw, conv), device=dev) for _ in range(n_gdn)]
     beta = [torch.empty((L, hg), device=dev) for _ in range(n_gdn)]
     gate = [torch.empty((L, hg), device=dev) for _ in range(n_gdn)]
+    xc = torch.empty((L, conv), device=dev)           # conv + silu rows: q | k | v
     gout = torch.empty((L, hg * dg), device=dev)
     ws = torch.empty(gdn_chunk_workspace_bytes(T, hg, dg) // 4, device=dev)
     cache = LayerKV.empty(nkv, da, L, device=dev)
@@ -376,30 +386,42 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
     dws = decode_workspace(decode_workspace_bytes(1, L, L, nh, nkv, da), dev)
     q_dec = at["q"][T:].float()  # decode queries are fp32 (engine hb2)
 
+    def gdn_layer_prefill(li):
+        g = gd[li]
+        gdn_conv(g["qkv"][:T], cst[li], g["conv_w"], out=xc[:T])
+        gdn_chunk(S[li], xc[:T, :kd], xc[:T, kd:2 * kd], xc[:T, 2 * kd:], gate[li][:T], beta[li][:T], hg,
+                  out=gout[:T], workspace=ws)
+        gdn_gated_norm(gout[:T], g["z"][:T], g["norm_w"], hg, out=gout[:T])
+
+    def gdn_layer_step(li, t):
+        g = gd[li]
+        gdn_conv(g["qkv"][t:t + 1], cst[li], g["conv_w"], out=xc[t:t + 1])
+        gdn_step(S[li], xc[t, :kd], xc[t, kd:2 * kd], xc[t, 2 * kd:], gate[li][t], beta[li][t], hg, out=gout[t])
+        gdn_gated_norm(gout[t:t + 1], g["z"][t:t + 1], g["norm_w"], hg, out=gout[t:t + 1])
+
     def step(i):
         for li in range(n_gdn):
             S[li].zero_()
+            cst[li].zero_()
             beta[li].copy_(gd[li]["beta_raw"])
             gdn_gates(gd[li]["alpha"], beta[li], dt, a, gate=gate[li])
         # prefill
         for li in range(n_gdn):
-            g = gd[li]
-            gdn_chunk(S[li], g["q"][:T], g["k"][:T], g["v"][:T], gate[li][:T], beta[li][:T], hg,
-                      out=gout[:T], workspace=ws)
+            gdn_layer_prefill(li)
         kv_store(cache, at["k"][:T], at["v"][:T], 0)
         attn_prefill(at["q"][:T], cache, 0, nh, gate=at["gate"][:T], out=aout[:T])
         # decode
         for t in range(T, L):
             for li in range(n_gdn):
-                g = gd[li]
-                gdn_step(S[li], g["q"][t], g["k"][t], g["v"][t], gate[li][t], beta[li][t], hg, out=gout[t])
+                gdn_layer_step(li, t)
             kv_store(cache, at["k"][t:t + 1], at["v"][t:t + 1], t)
             attn_decode(q_dec[t - T], cache, t, nh, gate=at["gate"][t], out=dout, workspace=dws)
 
     ms, _ = time_steps(step, steps, warmup, dout)
     return {
         "value": L / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": L / (ms * 1e-3),
-        "config": {"workload": f"qwen35 hybrid group: {n_gdn} Gated-DeltaNet layers ({hg} heads, d {dg}, fp32) + "
+        "config": {"workload": f"qwen35 hybrid group: {n_gdn} Gated-DeltaNet layers ({hg} heads, d {dg}, fp32: "
+                               f"conv1d width {kw} + silu, gates, l2norm + recurrence, gated RMSNorm) + "
                                f"1 gated attention layer ({nh}/{nkv} heads, d {da}, bf16 q/k/v, sigmoid gate); "
                                f"{T}-token prefill (chunked GDN, MFMA attention) then {n_dec} decode steps "
                                f"(GDN steps, KV store, split-K decode) per step; N(0,1)*0.5 seed {hex(seed)}",

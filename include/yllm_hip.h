@@ -177,6 +177,29 @@ size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_di
 int yhip_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt_bias, const float* ssm_a,
                    uint32_t T, uint32_t n_v_heads, void* stream);
 
+/* The causal conv1d + silu ahead of the recurrence for T tokens in order:
+ * conv1d_update (matvec.c:956-968) then silu (engine.c:809-812) per token.
+ * conv_state: the delay line, fp32 [kwidth][dim] (row kwidth-1 newest, the
+ * engine's e->ssm_conv slot, engine.c:802), updated in place; conv_w: fp32
+ * [dim][kwidth] (the gguf layout the reference reads, w[ch*kwidth + i]).
+ * x: T rows of dim channels x_stride floats apart (the qkv projection
+ * rows); out: T rows out_stride apart, not overlapping x (a token's
+ * window reads the kwidth-1 inputs before it).  silu = 0 stores the
+ * conv values themselves (bit for bit the reference's; with silu the
+ * device expf adds its own rounding).  kwidth 1..8. */
+int yhip_gdn_conv(float* out, uint32_t out_stride, const float* x, uint32_t x_stride, float* conv_state,
+                  const float* conv_w, uint32_t T, uint32_t dim, uint32_t kwidth, int silu, void* stream);
+
+/* Gated RMSNorm after the recurrence (rmsnorm_gated, matvec.c:1007-1021,
+ * applied per v-head at engine.c:845-847): for token t and head h,
+ * y = x * w * (1/sqrtf(mean(x^2) + eps)) * (z / (1 + expf(-z))) over the
+ * head's head_dim values.  x, z, y: T rows of n_heads*head_dim with their
+ * own strides (y may alias x); w: [head_dim] fp32 (w_dtype YHIP_F32) or f16
+ * bits (YHIP_F16).  head_dim a multiple of 64, at most 256. */
+int yhip_gdn_gated_norm(float* y, uint32_t y_stride, const float* x, uint32_t x_stride, const float* z,
+                        uint32_t z_stride, const void* w, uint32_t w_dtype, uint32_t T, uint32_t n_heads,
+                        uint32_t head_dim, float eps, void* stream);
+
 /* ---- Synthetic inputs (host) ----------------------------------------------
  * Seeded generator shared by the tests and the benchmark so that the CPU
  * oracle and the GPU see identical bits: splitmix64 as the reference's yrng

@@ -211,3 +211,44 @@ void yo_gdn_sequence(float* S, float* out, float* q, float* k, const float* v,
                             num_k_heads, hk, n_vheads, hv);
     }
 }
+
+/* matvec.c:956-968.  Products and sums are separate roundings (the reference
+ * is compiled in ISO C mode without FMA contraction). */
+void yo_conv1d_update(float* state, float* x, const float* w, uint32_t dim, uint32_t kwidth)
+{
+    uint32_t ch, i;
+    memmove(state, state + dim, (size_t)(kwidth - 1) * dim * sizeof(float));
+    memcpy(state + (size_t)(kwidth - 1) * dim, x, (size_t)dim * sizeof(float));
+    for (ch = 0; ch < dim; ch++) {
+        float acc = 0.0f;
+        for (i = 0; i < kwidth; i++) acc += state[(size_t)i * dim + ch] * w[(size_t)ch * kwidth + i];
+        x[ch] = acc;
+    }
+}
+
+/* engine.c:809-812 */
+void yo_conv_silu_sequence(float* state, float* x, const float* w, uint32_t T, uint32_t dim, uint32_t kwidth)
+{
+    uint32_t t, ch;
+    for (t = 0; t < T; t++) {
+        float* row = x + (size_t)t * dim;
+        yo_conv1d_update(state, row, w, dim, kwidth);
+        for (ch = 0; ch < dim; ch++) row[ch] = row[ch] / (1.0f + expf(-row[ch]));
+    }
+}
+
+/* matvec.c:1007-1021 */
+void yo_rmsnorm_gated(float* y, const float* x, const void* w, int w_f16, const float* z, uint32_t n, float eps)
+{
+    float s = 0.0f;
+    uint32_t i;
+    for (i = 0; i < n; i++) s += x[i] * x[i];
+    {
+        const float inv = 1.0f / sqrtf(s / (float)n + eps);
+        for (i = 0; i < n; i++) {
+            const float wgt = w_f16 ? yo_f16_to_f32(((const uint16_t*)w)[i]) : ((const float*)w)[i];
+            const float zg = z[i];
+            y[i] = x[i] * wgt * inv * (zg / (1.0f + expf(-zg)));
+        }
+    }
+}

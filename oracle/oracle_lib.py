@@ -52,6 +52,9 @@ class Oracle:
                                       c_uint32]
         L.yo_gate_sigmoid.argtypes = [FP, FP, c_uint32]
         L.yo_gdn_gates.argtypes = [FP, FP, FP, FP, FP, c_uint32]
+        L.yo_conv1d_update.argtypes = [FP, FP, FP, c_uint32, c_uint32]
+        L.yo_conv_silu_sequence.argtypes = [FP, FP, FP, c_uint32, c_uint32, c_uint32]
+        L.yo_rmsnorm_gated.argtypes = [FP, FP, ctypes.c_void_p, ctypes.c_int, FP, c_uint32, c_float]
         L.yo_gdn_state_update.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32]
         L.yo_gdn_sequence.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32,
                                       c_uint32, c_float]
@@ -123,6 +126,46 @@ class Oracle:
         return S, out, q, k
 
 
+def _conv_args(state, x, w):
+    return (np.array(state, dtype=np.float32, order="C", copy=True), np.array(x, dtype=np.float32, order="C", copy=True),
+            np.ascontiguousarray(w, dtype=np.float32))
+
+
+def _oracle_conv(self, state, x, w, kwidth):
+    """matvec.c:956-968 over the rows of x: returns (new state, conv rows)."""
+    st, xr, wc = _conv_args(state, x, w)
+    dim = xr.shape[-1]
+    for row in xr.reshape(-1, dim):
+        self.L.yo_conv1d_update(fp(st), fp(row), fp(wc), dim, kwidth)
+    return st, xr
+
+
+def _oracle_conv_silu(self, state, x, w, kwidth):
+    """engine.c:809-812 over T rows: conv then silu; returns (state, rows)."""
+    st, xr, wc = _conv_args(state, x, w)
+    T, dim = xr.shape
+    self.L.yo_conv_silu_sequence(fp(st), fp(xr), fp(wc), T, dim, kwidth)
+    return st, xr
+
+
+def _oracle_rmsnorm_gated(self, x, w, z, eps):
+    """matvec.c:1007-1021 per row of x (w f32, or f16 bits as uint16)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    z = np.ascontiguousarray(z, dtype=np.float32)
+    y = np.empty_like(x)
+    n = x.shape[-1]
+    w_f16 = int(w.dtype == np.uint16)
+    w = np.ascontiguousarray(w)
+    for yr, xr, zr in zip(y.reshape(-1, n), x.reshape(-1, n), z.reshape(-1, n)):
+        self.L.yo_rmsnorm_gated(fp(yr), fp(xr), w.ctypes.data_as(ctypes.c_void_p), w_f16, fp(zr), n, eps)
+    return y
+
+
+Oracle.conv = _oracle_conv
+Oracle.conv_silu = _oracle_conv_silu
+Oracle.rmsnorm_gated = _oracle_rmsnorm_gated
+
+
 class Ref:
     """The reference compiled from its own sources (oracle/_ref)."""
 
@@ -138,6 +181,8 @@ class Ref:
         L.softmax.argtypes = [FP, c_uint32]
         L.l2norm_inplace.argtypes = [FP, c_uint32, c_float]
         L.gdn_state_update.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32]
+        L.conv1d_update.argtypes = [FP, FP, ctypes.c_void_p, c_uint32, c_uint32]
+        L.rmsnorm_gated.argtypes = [FP, FP, ctypes.c_void_p, FP, c_uint32, c_float, c_uint32]
         L.yrng.restype = c_uint64
         L.yrng.argtypes = [POINTER(c_uint64)]
         L.ysrand.restype = c_uint64
@@ -155,6 +200,26 @@ class Ref:
         L.yr_gdn.argtypes = [c_uint32, c_uint32, c_uint32, FP, FP, FP, FP, FP, c_float, FP, FP, FP, FP, FP, FP,
                              FP, FP]
         self.L = L
+
+    def conv(self, state, x, w, kwidth):
+        """The reference's conv1d_update (matvec.c:956) over the rows of x."""
+        st, xr, wc = _conv_args(state, x, w)
+        dim = xr.shape[-1]
+        for row in xr.reshape(-1, dim):
+            self.L.conv1d_update(fp(st), fp(row), wc.ctypes.data_as(ctypes.c_void_p), dim, kwidth)
+        return st, xr
+
+    def rmsnorm_gated(self, x, w, z, eps):
+        """The reference's rmsnorm_gated (matvec.c:1007) per row (w f32 or f16 bits)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        z = np.ascontiguousarray(z, dtype=np.float32)
+        y = np.empty_like(x)
+        n = x.shape[-1]
+        dtype = 0 if w.dtype == np.uint16 else 1  # DT_F16 = 0, DT_F32 = 1 (llf.h:14-15)
+        w = np.ascontiguousarray(w)
+        for yr, xr, zr in zip(y.reshape(-1, n), x.reshape(-1, n), z.reshape(-1, n)):
+            self.L.rmsnorm_gated(fp(yr), fp(xr), w.ctypes.data_as(ctypes.c_void_p), fp(zr), n, eps, dtype)
+        return y
 
     def f32_to_f16(self, x):
         x = np.ascontiguousarray(x, dtype=np.float32)

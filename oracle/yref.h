@@ -93,4 +93,18 @@ void yo_gdn_sequence(float* S, float* out, float* q, float* k, const float* v,
                      const float* gate, const float* beta, uint32_t T, uint32_t num_k_heads,
                      uint32_t hk, uint32_t n_vheads, uint32_t hv, float eps);
 
+/* matvec.c:956-968 (conv1d_update): the delay line state [kwidth][dim]
+ * shifts up one row, x becomes its last row, and
+ * x[ch] = sum_i state[i][ch] * w[ch*kwidth + i] (in i order), in place. */
+void yo_conv1d_update(float* state, float* x, const float* w, uint32_t dim, uint32_t kwidth);
+
+/* engine.c:809-812 for T consecutive tokens: conv1d_update then silu
+ * x / (1 + expf(-x)) per channel.  x: [T][dim] in place. */
+void yo_conv_silu_sequence(float* state, float* x, const float* w, uint32_t T, uint32_t dim, uint32_t kwidth);
+
+/* matvec.c:1007-1021 (rmsnorm_gated): inv = 1/sqrtf(sum x^2 / n + eps);
+ * y[i] = x[i] * w[i] * inv * (z[i] / (1 + expf(-z[i]))); w f32 (w_f16 == 0)
+ * or f16 bits. */
+void yo_rmsnorm_gated(float* y, const float* x, const void* w, int w_f16, const float* z, uint32_t n, float eps);
+
 #endif

@@ -160,6 +160,26 @@ def main() -> None:
         for k in ("q", "k", "v", "alpha_raw", "beta_raw", "beta", "gate", "S"):
             fx[f"{name}_{k}"] = r[k]
 
+    # ---- GDN neighbours: conv1d_update matvec.c:956-968, rmsnorm_gated 1007-1021 ----
+    dim, kw, T = 96, 4, 7
+    seeds = np.array([5001, 5002, 5003], np.int64)
+    st0 = uniform_pm1(int(seeds[0]), kw * dim).reshape(kw, dim)
+    x = uniform_pm1(int(seeds[1]), T * dim, 2.0).reshape(T, dim)
+    w = uniform_pm1(int(seeds[2]), dim * kw, 0.7)
+    st, rows = ref.conv(st0, x, w, kw)
+    fx["conv1d_meta"] = np.array([dim, kw, T], np.int64)
+    fx["conv1d_seeds"] = seeds
+    fx["conv1d_state"] = st
+    fx["conv1d_rows"] = rows
+    n = 128
+    seeds = np.array([5011, 5012, 5013], np.int64)
+    xx = uniform_pm1(int(seeds[0]), 3 * n).reshape(3, n)
+    zz = uniform_pm1(int(seeds[1]), 3 * n, 3.0).reshape(3, n)
+    wf = (uniform_pm1(int(seeds[2]), n, 0.5) + np.float32(1.0)).astype(np.float32)
+    fx["rmsg_seeds"] = seeds
+    fx["rmsg_f32"] = ref.rmsnorm_gated(xx, wf, zz, np.float32(1e-6))
+    fx["rmsg_f16"] = ref.rmsnorm_gated(xx, ref.f32_to_f16(wf), zz, np.float32(1e-6))
+
     np.savez_compressed(OUT, **fx)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(fx)} arrays)")
 

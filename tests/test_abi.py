@@ -146,3 +146,28 @@ def test_gdn_rejects_bad_args(hiplib):
     assert hiplib.yhip_gdn_chunk_workspace(63, 16, 128) == 0
     assert hiplib.yhip_gdn_chunk_workspace(4096, 16, 128) == 64 * 16 * (3 * 64 * 128 + 64 * 64 + 64 * 128 + 4) * 4
     assert hiplib.yhip_gdn_gates(P, P, P, P, P, 0, 16, None) == 0
+
+
+def test_gdn_neighbours_reject_bad_args(hiplib):
+    F = ctypes.c_float
+    X, O = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x900000)  # never dereferenced
+    # conv: kwidth outside 1..8, strides, overlap of out and x, nulls; T = 0 is a no-op
+    rc = hiplib.yhip_gdn_conv(O, 512, X, 512, P, P, 4, 512, 9, 1, None)
+    assert rc == -22 and "kwidth" in _err(hiplib)
+    rc = hiplib.yhip_gdn_conv(O, 512, X, 256, P, P, 4, 512, 4, 1, None)
+    assert rc == -22 and "strides" in _err(hiplib)
+    rc = hiplib.yhip_gdn_conv(X, 512, X, 512, P, P, 4, 512, 4, 1, None)
+    assert rc == -22 and "overlap" in _err(hiplib)
+    rc = hiplib.yhip_gdn_conv(O, 512, X, 512, None, P, 4, 512, 4, 1, None)
+    assert rc == -22 and "null" in _err(hiplib)
+    assert hiplib.yhip_gdn_conv(O, 512, X, 512, P, P, 0, 512, 4, 1, None) == 0
+    # gated norm: head_dim not a multiple of 64 or above 256, weight dtype, strides
+    rc = hiplib.yhip_gdn_gated_norm(P, 2048, P, 2048, P, 2048, P, 1, 4, 16, 100, F(1e-6), None)
+    assert rc == -22 and "head_dim" in _err(hiplib)
+    rc = hiplib.yhip_gdn_gated_norm(P, 4096, P, 4096, P, 4096, P, 1, 4, 16, 512, F(1e-6), None)
+    assert rc == -22 and "head_dim" in _err(hiplib)
+    rc = hiplib.yhip_gdn_gated_norm(P, 2048, P, 2048, P, 2048, P, 2, 4, 16, 128, F(1e-6), None)
+    assert rc == -22 and "w_dtype" in _err(hiplib)
+    rc = hiplib.yhip_gdn_gated_norm(P, 2048, P, 1024, P, 2048, P, 1, 4, 16, 128, F(1e-6), None)
+    assert rc == -22 and "strides" in _err(hiplib)
+    assert hiplib.yhip_gdn_gated_norm(P, 2048, P, 2048, P, 2048, P, 1, 0, 16, 128, F(1e-6), None) == 0

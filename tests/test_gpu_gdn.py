@@ -152,3 +152,80 @@ def test_gdn_full_size_prefill(cuda, oracle, chunked):
     e_o, e_s = rel_l2(out, o_want), rel_l2(S.cpu().numpy().ravel(), S_want)
     print(f"gdn full T={T} chunked={chunked}: out {e_o:.3e} state {e_s:.3e}")
     assert e_o <= TOL and e_s <= TOL
+
+
+# ---------------------------------------------------------------- neighbours
+
+def conv_inputs(seed, T, dim, kw, stride=None):
+    stride = stride or dim
+    x = gen(seed, T * stride, 1.0).reshape(T, stride)
+    st = gen(seed + 1, kw * dim, 1.0).reshape(kw, dim)
+    w = gen(seed + 2, dim * kw, 0.5).reshape(dim, kw)
+    return x, st, w
+
+
+@pytest.mark.parametrize("T,dim,kw", [(1, 96, 4), (2, 96, 4), (7, 40, 3), (8, 256, 4), (37, 300, 4), (129, 1024, 2),
+                                      (64, 64, 1), (33, 130, 8)])
+def test_gdn_conv_bits_match_oracle(cuda, oracle, T, dim, kw):
+    """Without silu the conv outputs and the new delay line are the
+    reference's bits (conv1d_update order, no contraction)."""
+    from yllm_amd.gdn import gdn_conv
+
+    x, st, w = conv_inputs(500 + T + dim, T, dim, kw)
+    st_want, rows_want = oracle.conv(st, x, w, kw)
+    xd, sd, wd = to_dev(cuda, x, st, w)
+    out = gdn_conv(xd, sd, wd, silu=False).cpu().numpy()
+    assert np.array_equal(out.view(np.uint32), rows_want.view(np.uint32))
+    assert np.array_equal(sd.cpu().numpy().view(np.uint32), st_want.view(np.uint32))
+
+
+def test_gdn_conv_silu_strided_and_split(cuda, oracle):
+    """conv + silu on qkv rows with extra columns (row stride > dim), against
+    the oracle to 2e-6; and 200 tokens in one call or as 3 + 197 (the delay
+    line carries the state) give the same bits."""
+    from yllm_amd.gdn import gdn_conv
+
+    T, dim, kw, stride = 200, 192, 4, 256
+    x, st, w = conv_inputs(601, T, dim, kw, stride)
+    st_want, rows_want = oracle.conv_silu(st, x[:, :dim], w, kw)
+    xd, sd, wd = to_dev(cuda, x, st, w)
+    sd2 = sd.clone()
+    out = gdn_conv(xd, sd, wd)
+    assert rel_l2(out.cpu().numpy(), rows_want) <= 2e-7
+    assert np.allclose(out.cpu().numpy(), rows_want, rtol=2e-6, atol=1e-7)
+    assert np.array_equal(sd.cpu().numpy(), st_want)
+    parts = torch.cat([gdn_conv(xd[:3], sd2, wd), gdn_conv(xd[3:], sd2, wd)])
+    assert torch.equal(parts, out) and torch.equal(sd2, sd)
+
+
+def test_gdn_conv_full_size(cuda, oracle):
+    """The fifth configuration's layer: 4096 tokens, 2*16*128 + 16*128 = 6144
+    channels, kernel width 4."""
+    from yllm_amd.gdn import gdn_conv
+
+    T, dim, kw = 4096, 6144, 4
+    x, st, w = conv_inputs(0x5EED0105, T, dim, kw)
+    st_want, rows_want = oracle.conv(st, x, w, kw)
+    xd, sd, wd = to_dev(cuda, x, st, w)
+    out = gdn_conv(xd, sd, wd, silu=False).cpu().numpy()
+    assert np.array_equal(out.view(np.uint32), rows_want.view(np.uint32))
+    assert np.array_equal(sd.cpu().numpy().view(np.uint32), st_want.view(np.uint32))
+
+
+@pytest.mark.parametrize("w_f16", [False, True], ids=["w_f32", "w_f16"])
+@pytest.mark.parametrize("T,n_heads,hd", [(1, 16, 128), (37, 4, 64), (5, 3, 256), (130, 16, 128)])
+def test_gdn_gated_norm_matches_oracle(cuda, oracle, T, n_heads, hd, w_f16):
+    from yllm_amd.gdn import gdn_gated_norm
+
+    x = gen(700 + T, T * n_heads * hd, 0.7).reshape(T, n_heads * hd)
+    z = gen(701 + T, T * n_heads * hd, 2.0).reshape(T, n_heads * hd)
+    w = (gen(702, hd, 0.2) + np.float32(1.0)).astype(np.float32)
+    wo = oracle.f32_to_f16(w) if w_f16 else w
+    want = oracle.rmsnorm_gated(x.reshape(-1, hd), wo, z.reshape(-1, hd), np.float32(EPS)).reshape(T, -1)
+    xd, zd = to_dev(cuda, x, z)
+    wd = torch.from_numpy(wo.view(np.float16) if w_f16 else w).to(cuda)
+    got = gdn_gated_norm(xd, zd, wd, n_heads).cpu().numpy()
+    assert np.allclose(got, want, rtol=3e-6, atol=1e-7), float(np.abs(got - want).max())
+    # in place, as the engine applies it
+    gdn_gated_norm(xd, zd, wd, n_heads, out=xd)
+    assert np.allclose(xd.cpu().numpy(), want, rtol=3e-6, atol=1e-7)

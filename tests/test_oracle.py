@@ -322,3 +322,70 @@ def test_gdn_vs_reference_live(oracle, ref):
     assert np.array_equal(bits(beta), bits(r["beta"])) and np.array_equal(bits(gate), bits(r["gate"]))
     S1, _ = oracle.gdn_step(S, r["q"], r["k"], r["v"], gate, beta, nk, hd, nv, hd)
     assert np.array_equal(bits(S1), bits(r["S"]))
+
+
+# ---------------------------------------------------------------- GDN neighbours
+
+def _conv_inputs(golden):
+    dim, kw, T = (int(v) for v in golden["conv1d_meta"])
+    s = [int(v) for v in golden["conv1d_seeds"]]
+    return (uniform_pm1(s[0], kw * dim).reshape(kw, dim), uniform_pm1(s[1], T * dim, 2.0).reshape(T, dim),
+            uniform_pm1(s[2], dim * kw, 0.7), kw)
+
+
+def test_conv1d_golden(oracle, golden):
+    """matvec.c:956-968 over 7 tokens: state and outputs bit for bit."""
+    st0, x, w, kw = _conv_inputs(golden)
+    st, rows = oracle.conv(st0, x, w, kw)
+    assert np.array_equal(bits(st), bits(golden["conv1d_state"]))
+    assert np.array_equal(bits(rows), bits(golden["conv1d_rows"]))
+
+
+def test_conv1d_vs_reference_live(oracle, ref):
+    st0 = uniform_pm1(61, 3 * 40).reshape(3, 40)
+    x = uniform_pm1(62, 9 * 40, 3.0).reshape(9, 40)
+    w = uniform_pm1(63, 40 * 3)
+    a, b = oracle.conv(st0, x, w, 3), ref.conv(st0, x, w, 3)
+    assert np.array_equal(bits(a[0]), bits(b[0])) and np.array_equal(bits(a[1]), bits(b[1]))
+
+
+def test_conv1d_closed_forms(oracle):
+    """A single tap on the newest input is the identity; a single tap on the
+    oldest reads the input kwidth-1 tokens back; silu(x) = x * sigmoid(x)."""
+    dim, kw, T = 24, 4, 10
+    x = uniform_pm1(71, T * dim, 3.0).reshape(T, dim)
+    st0 = np.zeros((kw, dim), np.float32)
+    w_new = np.zeros((dim, kw), np.float32)
+    w_new[:, kw - 1] = 1.0
+    st, rows = oracle.conv(st0, x, w_new, kw)
+    assert np.array_equal(rows, x) and np.array_equal(st, x[-kw:])
+    w_old = np.zeros((dim, kw), np.float32)
+    w_old[:, 0] = 1.0
+    _, rows = oracle.conv(st0, x, w_old, kw)
+    assert np.array_equal(rows[kw - 1:], x[:T - kw + 1]) and not rows[:kw - 1].any()
+    _, rows = oracle.conv_silu(st0, x, w_new, kw)
+    x64 = x.astype(np.float64)
+    assert np.allclose(rows, x64 / (1 + np.exp(-x64)), rtol=2e-7, atol=1e-7)
+
+
+def test_rmsnorm_gated_golden(oracle, golden):
+    s = [int(v) for v in golden["rmsg_seeds"]]
+    n = 128
+    x = uniform_pm1(s[0], 3 * n).reshape(3, n)
+    z = uniform_pm1(s[1], 3 * n, 3.0).reshape(3, n)
+    wf = (uniform_pm1(s[2], n, 0.5) + np.float32(1.0)).astype(np.float32)
+    assert np.array_equal(bits(oracle.rmsnorm_gated(x, wf, z, np.float32(1e-6))), bits(golden["rmsg_f32"]))
+    wh = oracle.f32_to_f16(wf)
+    assert np.array_equal(bits(oracle.rmsnorm_gated(x, wh, z, np.float32(1e-6))), bits(golden["rmsg_f16"]))
+
+
+def test_rmsnorm_gated_fp64(oracle):
+    """Against the fp64 formula: y = x w / sqrt(mean(x^2) + eps) * z sigmoid(z)."""
+    n = 128
+    x = uniform_pm1(81, 5 * n, 2.0).reshape(5, n)
+    z = uniform_pm1(82, 5 * n, 4.0).reshape(5, n)
+    w = uniform_pm1(83, n, 0.3) + np.float32(1.0)
+    y = oracle.rmsnorm_gated(x, w.astype(np.float32), z, np.float32(1e-6))
+    x64, z64 = x.astype(np.float64), z.astype(np.float64)
+    want = x64 * w / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * z64 / (1 + np.exp(-z64))
+    assert np.allclose(y, want, rtol=3e-6, atol=1e-6)

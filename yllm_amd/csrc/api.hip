@@ -302,6 +302,66 @@ size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_di
     return yhip::gdn_chunk_workspace(T, n_v_heads, head_dim);
 }
 
+int yhip_gdn_conv(float* out, uint32_t out_stride, const float* x, uint32_t x_stride, float* conv_state,
+                  const float* conv_w, uint32_t T, uint32_t dim, uint32_t kwidth, int silu, void* stream)
+{
+    const char* fn = "yhip_gdn_conv";
+    if (!out || !x || !conv_state || !conv_w) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    if (dim == 0 || kwidth == 0 || kwidth > 8) return fail(YHIP_EINVAL, "%s: need dim >= 1 and kwidth in 1..8", fn);
+    if (x_stride < dim || out_stride < dim) return fail(YHIP_EINVAL, "%s: strides must cover dim channels", fn);
+    if ((uint64_t)T * (x_stride > out_stride ? x_stride : out_stride) > 0xffffffffull)
+        return fail(YHIP_EINVAL, "%s: too many elements", fn);
+    if (T == 0) return done(hipSuccess, "");
+    {
+        const uintptr_t o0 = (uintptr_t)out, o1 = o0 + ((size_t)(T - 1) * out_stride + dim) * sizeof(float);
+        const uintptr_t x0 = (uintptr_t)x, x1 = x0 + ((size_t)(T - 1) * x_stride + dim) * sizeof(float);
+        if (o0 < x1 && x0 < o1) return fail(YHIP_EINVAL, "%s: out must not overlap x", fn);
+    }
+    yhip::GdnConvArgs a = {};
+    a.out = out;
+    a.x = x;
+    a.state = conv_state;
+    a.w = conv_w;
+    a.out_stride = out_stride;
+    a.x_stride = x_stride;
+    a.T = T;
+    a.dim = dim;
+    a.kwidth = kwidth;
+    a.silu = silu != 0;
+    return done(yhip::launch_gdn_conv(a, (hipStream_t)stream), fn);
+}
+
+int yhip_gdn_gated_norm(float* y, uint32_t y_stride, const float* x, uint32_t x_stride, const float* z,
+                        uint32_t z_stride, const void* w, uint32_t w_dtype, uint32_t T, uint32_t n_heads,
+                        uint32_t head_dim, float eps, void* stream)
+{
+    const char* fn = "yhip_gdn_gated_norm";
+    if (!y || !x || !z || !w) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    if (head_dim == 0 || head_dim % 64 || head_dim > 256)
+        return fail(YHIP_EINVAL, "%s: head_dim %u must be 64, 128, 192 or 256", fn, head_dim);
+    if (w_dtype != YHIP_F32 && w_dtype != YHIP_F16) return fail(YHIP_EINVAL, "%s: w_dtype must be F32 or F16", fn);
+    if (n_heads == 0) return fail(YHIP_EINVAL, "%s: n_heads must be >= 1", fn);
+    const uint64_t row = (uint64_t)n_heads * head_dim;
+    if (x_stride < row || z_stride < row || y_stride < row)
+        return fail(YHIP_EINVAL, "%s: strides must cover n_heads*head_dim", fn);
+    if ((uint64_t)T * n_heads > 0x7fffffffull) return fail(YHIP_EINVAL, "%s: too many rows", fn);
+    if (T == 0) return done(hipSuccess, "");
+    yhip::GdnNormArgs a = {};
+    a.y = y;
+    a.x = x;
+    a.z = z;
+    a.w = w;
+    a.y_stride = y_stride;
+    a.x_stride = x_stride;
+    a.z_stride = z_stride;
+    a.T = T;
+    a.n_heads = n_heads;
+    a.head_dim = head_dim;
+    a.w_f16 = w_dtype == YHIP_F16;
+    a.eps = eps;
+    return done(yhip::launch_gdn_gated_norm(a, (hipStream_t)stream), fn);
+}
+
 int yhip_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt_bias, const float* ssm_a,
                    uint32_t T, uint32_t n_v_heads, void* stream)
 {

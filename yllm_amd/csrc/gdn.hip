@@ -428,7 +428,6 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(GdnArgs a)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;  // 8 waves
     const int r = lane & 15, g = lane >> 4;
-    constexpr uint32_t nblk = D / J;
     // workgroup b = slice * n_v + h: consecutive workgroups go to different
     // XCDs, so the slices of one head (b mod 8 fixed when n_v is a multiple
     // of 8) share an L2 and read the head's chunk data once

@@ -61,6 +61,26 @@ struct PrefillArgs {
 };
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
 
+// ---- gdn_conv.hip ----
+struct GdnConvArgs {
+    float* out;             // [T] rows out_stride apart (not overlapping x)
+    const float* x;         // [T] rows x_stride apart
+    float* state;           // delay line [kwidth][dim], updated in place
+    const float* w;         // [dim][kwidth]
+    uint32_t out_stride, x_stride, T, dim, kwidth;
+    int silu;
+};
+hipError_t launch_gdn_conv(const GdnConvArgs& a, hipStream_t st);
+struct GdnNormArgs {
+    float* y;               // may alias x
+    const float* x;
+    const float* z;
+    const void* w;          // [head_dim] f32, or f16 when w_f16
+    uint32_t y_stride, x_stride, z_stride, T, n_heads, head_dim, w_f16;
+    float eps;
+};
+hipError_t launch_gdn_gated_norm(const GdnNormArgs& a, hipStream_t st);
+
 // ---- gdn.hip ----
 struct GdnArgs {
     float* S;                        // [n_v][D][D] state, S[h][j][i]

@@ -7,6 +7,9 @@ inference/core/engine.c):
     gdn_step(S, q, k, v, gate, beta, n_k)       l2norm (engine.c:826-827) +
                                                 gdn_state_update (matvec.c:975-1004)
     gdn_chunk(S, q, k, v, gate, beta, n_k)      the same over T tokens in order
+    gdn_conv(x, conv_state, conv_w)             conv1d_update + silu (matvec.c:956-968,
+                                                engine.c:809-812) over T tokens
+    gdn_gated_norm(x, z, w, n_heads)            rmsnorm_gated per v-head (matvec.c:1007-1021)
 
 S is the fp32 state [n_v, d, d] (S[h, j, :] is column j, the reference's
 transposed storage), updated in place.  Tensors are torch fp32 tensors on the
@@ -17,7 +20,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import YhipError, check, lib
+from ._lib import F16, F32, YhipError, check, lib
 
 L2_EPS = 1e-6  # the qwen35 GDN l2norm epsilon (engine.c:826-827 passes the model's norm eps)
 
@@ -114,4 +117,54 @@ def gdn_step(S: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         out = torch.empty(n_v * d, dtype=torch.float32, device=S.device)
     check(lib().yhip_gdn_step(S.data_ptr(), out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                               gate.data_ptr(), beta.data_ptr(), n_k, n_v, d, float(eps), _stream()))
+    return out
+
+
+def gdn_conv(x: torch.Tensor, conv_state: torch.Tensor, conv_w: torch.Tensor, silu: bool = True,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """x: [T, dim] rows (row stride free); conv_state: fp32 [kwidth, dim]
+    delay line, updated in place; conv_w: fp32 [dim, kwidth].  Returns
+    silu(conv) rows [T, dim] (a new tensor unless `out` is given; out must
+    not overlap x)."""
+    _f32_gpu(x, conv_state, conv_w)
+    T, xs = _rows(x)
+    if conv_state.dim() != 2 or not conv_state.is_contiguous():
+        raise YhipError(-22, "gdn_conv: conv_state must be contiguous [kwidth, dim]")
+    kwidth, dim = conv_state.shape
+    if conv_w.shape != (dim, kwidth) or not conv_w.is_contiguous():
+        raise YhipError(-22, "gdn_conv: conv_w must be contiguous [dim, kwidth]")
+    if x.shape[1] < dim:
+        raise YhipError(-22, "gdn_conv: x rows must hold dim channels")
+    if out is None:
+        out = torch.empty((T, dim), dtype=torch.float32, device=x.device)
+    _f32_gpu(out)
+    To, os_ = _rows(out)
+    if To != T:
+        raise YhipError(-22, "gdn_conv: out must have T rows")
+    check(lib().yhip_gdn_conv(out.data_ptr(), os_, x.data_ptr(), xs, conv_state.data_ptr(), conv_w.data_ptr(), T,
+                              dim, kwidth, int(silu), _stream()))
+    return out
+
+
+def gdn_gated_norm(x: torch.Tensor, z: torch.Tensor, w: torch.Tensor, n_heads: int, eps: float = L2_EPS,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """x, z: [T, n_heads*head_dim] rows; w: [head_dim] fp32 or f16.  Returns
+    rmsnorm(x, w) * silu(z) per head (into `out`, which may be x)."""
+    _f32_gpu(x, z)
+    T, xs = _rows(x)
+    Tz, zs = _rows(z)
+    head_dim = w.numel()
+    if Tz != T or x.shape[1] < n_heads * head_dim or z.shape[1] < n_heads * head_dim:
+        raise YhipError(-22, "gdn_gated_norm: x and z must be [T, n_heads*head_dim]")
+    if not w.is_cuda or w.dtype not in (torch.float32, torch.float16) or not w.is_contiguous():
+        raise YhipError(-22, "gdn_gated_norm: w must be a contiguous fp32 or f16 GPU tensor")
+    if out is None:
+        out = torch.empty((T, n_heads * head_dim), dtype=torch.float32, device=x.device)
+    _f32_gpu(out)
+    Ty, ys = _rows(out)
+    if Ty != T:
+        raise YhipError(-22, "gdn_gated_norm: out must have T rows")
+    check(lib().yhip_gdn_gated_norm(out.data_ptr(), ys, x.data_ptr(), xs, z.data_ptr(), zs, w.data_ptr(),
+                                    F16 if w.dtype == torch.float16 else F32, T, n_heads, head_dim,
+                                    float(eps), _stream()))
     return out
