@@ -19,6 +19,9 @@ batch of synthetic input, with all inputs resident in HBM:
   gdn4k       one Gated DeltaNet layer over a 4096-token prompt, 16 heads,
               d_k = d_v = 128, fp32 (the fifth configuration's GDN layer):
               yhip_gdn_gates + yhip_gdn_chunk from a zero state.
+  rope8k      fused RoPE + KV store ahead of attention: 8192 tokens,
+              32 / 8 heads of 128 (llama pairs, theta 5e5), f32 q/k/v
+              slices of one projection row -> f16 q, f16 K/V cache.
   hybrid      the fifth configuration end to end: 3 GDN layers + 1 gated
               attention layer (16 / 2 heads, d 256, bf16), 4096-token
               prefill then 256 decode steps; tokens/s over the whole pass.
@@ -337,6 +340,53 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
     return res
 
 
+def rope_bytes(L: int, nh: int, nkv: int, hd: int) -> float:
+    """Algorithmic HBM bytes of one fused RoPE + KV store over L tokens: read
+    q, k, v (f32), write q (f16) and the K and V cache rows (f16)."""
+    return float(L) * hd * ((4 + 2) * nh + 2 * (4 + 2) * nkv)
+
+
+def run_rope(L: int, nh: int, nkv: int, hd: int, theta: float, steps: int, warmup: int, cpu: bool):
+    import torch
+
+    from yllm_amd.attention import ROPE_PAIRS, LayerKV, rope_kv_store
+
+    dev = torch.device("cuda:0")
+    seed = SEED + 6
+    qd, kvd = nh * hd, nkv * hd
+    width = qd + 2 * kvd
+    x = torch.from_numpy(synth_raw(seed, L * width).reshape(L, width)).to(dev)
+    # rotating copies of (projection rows, q out, cache) beyond the 256 MB MALL
+    set_bytes = rope_bytes(L, nh, nkv, hd)
+    n_sets = max(1, int(-(-ROTATE_BYTES // set_bytes)))
+    sets = [(x.clone(), torch.empty((L, qd), dtype=torch.float16, device=dev),
+             LayerKV.empty(nkv, hd, L, device=dev)) for _ in range(n_sets)]
+    del x
+
+    def step(i):
+        xi, qo, c = sets[i % n_sets]
+        rope_kv_store(c, xi[:, :qd], xi[:, qd:qd + kvd], xi[:, qd + kvd:], 0, nh, ROPE_PAIRS, theta, q_out=qo)
+
+    last = sets[(warmup + steps - 1) % n_sets]
+    ms, kern_ms = time_steps(step, steps, warmup, last[1])
+    nbytes = rope_bytes(L, nh, nkv, hd)
+    achieved = nbytes / (kern_ms * 1e-3)
+    res = {
+        "value": L / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": L / (ms * 1e-3),
+        "config": {"workload": f"fused RoPE (llama pairs, theta {theta:g}) + KV store, {L} tokens at positions "
+                               f"0..{L - 1}, {nh} query / {nkv} KV heads, head_dim {hd}; f32 q/k/v slices of one "
+                               f"projection row N(0,1) seed {hex(seed)}, f16 q out, f16 K/V cache; "
+                               f"{n_sets} rotating input sets (> 256 MB MALL)",
+                   "tokens": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd},
+        "roofline": {"bound": "hbm", "kernel": "rope_kv_kernel<%d,%d>" % (ROPE_PAIRS, hd), "achieved": achieved / 1e9,
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": achieved / HBM_PEAK,
+                     "bytes_per_launch": nbytes, "launch_ms": kern_ms, "traffic": traffic_of(f"rope{L}")},
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_rope(last, L, nh, nkv, hd, theta)
+    return res
+
+
 def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
     """The fifth configuration: one group of 3 Gated-DeltaNet layers and 1
     gated GQA attention layer, a 4096-token prefill then n_dec decode steps.
@@ -345,8 +395,8 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
     this path)."""
     import torch
 
-    from yllm_amd.attention import (LayerKV, attn_decode, attn_prefill, decode_workspace, decode_workspace_bytes,
-                                    kv_store)
+    from yllm_amd.attention import (ROPE_MROPE, LayerKV, attn_decode, attn_prefill, decode_workspace,
+                                    decode_workspace_bytes, rope_kv_store)
     from yllm_amd.gdn import gdn_chunk, gdn_chunk_workspace_bytes, gdn_conv, gdn_gated_norm, gdn_gates, gdn_step
 
     dev = torch.device("cuda:0")
@@ -369,8 +419,8 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
                alpha=draw(L * hg).view(L, hg), beta_raw=draw(L * hg).view(L, hg),
                conv_w=draw(conv * kw, scale=0.5).view(conv, kw), norm_w=draw(dg, scale=0.1) + 1.0)
           for _ in range(n_gdn)]
-    at = dict(q=draw(L * nh * da, True).view(L, -1), gate=draw(L * nh * da).view(L, -1),
-              k=draw(L * nkv * da, True).view(L, -1), v=draw(L * nkv * da, True).view(L, -1))
+    qd, kvd = nh * da, nkv * da
+    at = dict(qkv=draw(L * (qd + 2 * kvd)).view(L, -1), gate=draw(L * qd).view(L, -1))
     dt = torch.zeros(hg, device=dev)
     a = -torch.ones(hg, device=dev)
     S = [torch.zeros((hg, dg, dg), device=dev) for _ in range(n_gdn)]
@@ -384,7 +434,13 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
     aout = torch.empty((L, nh * da), dtype=torch.bfloat16, device=dev)
     dout = torch.empty(nh * da, device=dev)
     dws = decode_workspace(decode_workspace_bytes(1, L, L, nh, nkv, da), dev)
-    q_dec = at["q"][T:].float()  # decode queries are fp32 (engine hb2)
+    q_pre = torch.empty((T, qd), dtype=torch.bfloat16, device=dev)  # rotated prefill queries
+    q_dec = torch.empty((1, qd), device=dev)                          # rotated decode query (fp32, engine hb2)
+    qkv = at["qkv"]
+
+    def rope_store(t0, t1, q_out):
+        rope_kv_store(cache, qkv[t0:t1, :qd], qkv[t0:t1, qd:qd + kvd], qkv[t0:t1, qd + kvd:], t0, nh, ROPE_MROPE,
+                      1e7, n_rot=64, q_out=q_out)
 
     def gdn_layer_prefill(li):
         g = gd[li]
@@ -408,23 +464,25 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
         # prefill
         for li in range(n_gdn):
             gdn_layer_prefill(li)
-        kv_store(cache, at["k"][:T], at["v"][:T], 0)
-        attn_prefill(at["q"][:T], cache, 0, nh, gate=at["gate"][:T], out=aout[:T])
+        rope_store(0, T, q_pre)
+        attn_prefill(q_pre, cache, 0, nh, gate=at["gate"][:T], out=aout[:T])
         # decode
         for t in range(T, L):
             for li in range(n_gdn):
                 gdn_layer_step(li, t)
-            kv_store(cache, at["k"][t:t + 1], at["v"][t:t + 1], t)
-            attn_decode(q_dec[t - T], cache, t, nh, gate=at["gate"][t], out=dout, workspace=dws)
+            rope_store(t, t + 1, q_dec)
+            attn_decode(q_dec[0], cache, t, nh, gate=at["gate"][t], out=dout, workspace=dws)
 
     ms, _ = time_steps(step, steps, warmup, dout)
     return {
         "value": L / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": L / (ms * 1e-3),
         "config": {"workload": f"qwen35 hybrid group: {n_gdn} Gated-DeltaNet layers ({hg} heads, d {dg}, fp32: "
                                f"conv1d width {kw} + silu, gates, l2norm + recurrence, gated RMSNorm) + "
-                               f"1 gated attention layer ({nh}/{nkv} heads, d {da}, bf16 q/k/v, sigmoid gate); "
+                               f"1 gated attention layer ({nh}/{nkv} heads, d {da}: M-RoPE over 64 dims + KV "
+                               f"store from fp32 q/k/v rows, bf16 prefill queries, sigmoid gate); "
                                f"{T}-token prefill (chunked GDN, MFMA attention) then {n_dec} decode steps "
-                               f"(GDN steps, KV store, split-K decode) per step; N(0,1)*0.5 seed {hex(seed)}",
+                               f"(GDN steps, RoPE + KV store, split-K decode) per step; N(0,1)*0.5 seed "
+                               f"{hex(seed)}",
                    "prefill_tokens": T, "decode_steps": n_dec},
         "roofline": None,
     }
@@ -468,6 +526,48 @@ def cpu_prefill(q, k, v, out, L, nh, nkv, hd):
             "sample": f"the whole workload ({L} tokens, all heads), one pass, {dt:.2f} s; effective "
                       f"parallelism <= {nh} heads; {model}",
             "seconds": dt, "parity_rel_l2": rel_l2(out.cpu().numpy(), want)}
+
+
+def cpu_rope(rope_set, L, nh, nkv, hd, theta):
+    """The oracle's per-token loop (the reference's engine.c:1054-1072 is
+    single-threaded) over a sample of tokens spread over the positions; the
+    same rows of the GPU's q and caches are checked against it."""
+    O = _oracle()
+    x, qo, cache = rope_set
+    qd, kvd = nh * hd, nkv * hd
+    rows = np.unique(np.linspace(0, L - 1, min(L, 2048)).astype(np.int64))
+    xs = x[rows].cpu().numpy()
+    t0 = time.perf_counter()
+    n = 0
+    while True:  # whole passes over the sample until ~2 s of CPU work
+        for r, row in zip(rows, xs):
+            q, kc, vc = O.rope_kv_store(row[None, :qd], row[None, qd:qd + kvd], row[None, qd + kvd:], int(r), nh,
+                                        nkv, hd, np.float32(theta), 1)
+        n += len(rows)
+        dt = time.perf_counter() - t0
+        if dt > 2.0:
+            break
+    # parity of the sampled rows (the last pass left the last row's results; redo the sample for the check)
+    qs, ks, vs = [], [], []
+    for r, row in zip(rows, xs):
+        q, kc, vc = O.rope_kv_store(row[None, :qd], row[None, qd:qd + kvd], row[None, qd + kvd:], int(r), nh,
+                                    nkv, hd, np.float32(theta), 1)
+        qs.append(q[0])
+        ks.append(kc[0])
+        vs.append(vc[0])
+    torch = sys.modules["torch"]
+    torch.cuda.synchronize()
+    got_q = qo[rows].float().cpu().numpy()
+    want_q = np.float16(np.stack(qs)).astype(np.float32)
+    K = cache.k.view(torch.int16).cpu().numpy().view(np.uint16)[:, rows, :].transpose(1, 0, 2).reshape(len(rows), kvd)
+    k_equal = float((K == np.stack(ks)).mean())
+    cores = 1
+    _, model = _host_desc(O)
+    return {"value": n / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{len(rows)} tokens spread over positions 0..{L - 1}, passes until 2 s "
+                      f"({n} tokens in {dt:.2f} s), one thread (the reference loop is serial); {model}",
+            "seconds": dt, "q_max_abs_err_f16": float(np.abs(got_q - want_q).max()),
+            "k_bits_equal_frac": k_equal}
 
 
 def cpu_gdn(q, k, v, alpha, beta_raw, out, T, n_h, d):
@@ -539,7 +639,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="prefill2k",
                     choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch", "gdn4k",
-                             "hybrid"])
+                             "rope8k", "hybrid"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k / gdn4k secondary lines")
     ap.add_argument("--gdn-tokenwise", action="store_true",
@@ -577,11 +677,13 @@ def main() -> int:
         res = run_decode(131072, 32, 8, 128, 4, 2, args.steps, args.warmup, cpu, "decode128k")
     elif w == "gdn4k":
         res = run_gdn(4096, 16, 128, args.steps, args.warmup, cpu)
+    elif w == "rope8k":
+        res = run_rope(8192, 32, 8, 128, 500000.0, args.steps, args.warmup, cpu)
     elif w == "hybrid":
         res = run_hybrid(args.steps, args.warmup)
     else:
         res = run_decode_batch(32, 8, 128, 64, args.steps, args.warmup)
-    dtype = {"gdn4k": "f32", "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}.get(
+    dtype = {"gdn4k": "f32", "rope8k": "f32 rotation, f16 stores", "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}.get(
         w, "f16 MFMA, f32 accumulate/softmax")
 
     line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,

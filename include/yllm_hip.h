@@ -134,6 +134,35 @@ int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, co
                       uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
                       const float* gate, uint32_t gate_stride, void* stream);
 
+/* ---- RoPE + KV store (the step before attention) ---------------------------
+ * rope: YHIP_ROPE_PAIRS = rope_inplace, (v[2j], v[2j+1]) (matvec.c:890-904,
+ * llama); YHIP_ROPE_HALF = rope_inplace_qwen, (v[j], v[j+d/2]) (907-921,
+ * qwen); YHIP_ROPE_MROPE = rope_inplace_mrope, (v[j], v[j+n_rot/2]) over the
+ * first n_rot dims only (924-939, qwen35 with n_rot = 64); YHIP_ROPE_NONE
+ * leaves q and k as they are.  freq = powf(theta, -2j/dn) (dn = head_dim, or
+ * n_rot), angle = freq * pos, in float like the reference (the device
+ * powf/cosf/sinf differ from the host library by an ulp or two). */
+#define YHIP_ROPE_NONE 0u
+#define YHIP_ROPE_PAIRS 1u
+#define YHIP_ROPE_HALF 2u
+#define YHIP_ROPE_MROPE 3u
+
+/* Fused RoPE + KV store for B tokens at positions pos_start.. (engine.c:
+ * 1054-1072; qwen35 910-934): q and k fp32 rows (post-projection, post
+ * QK-norm) are rotated; q goes to q_out (YHIP_F32 / F16 / BF16, rows
+ * q_out_stride apart; q_out may be q itself with F32 and the same stride;
+ * q_out NULL skips q); k is stored into the head-major K cache and v (fp32
+ * rows v_stride apart) into the V tiles, both with the reference f32->f16
+ * rounding, as yhip_kv_store does.  Strides are in elements, so q, k, v may
+ * be slices of one fused projection row; q, k, v (and an f32 q_out) must be
+ * 8-byte aligned, an f16/bf16 q_out 4-byte aligned, every stride even.
+ * One launch. */
+int yhip_rope_kv_store(void* q_out, uint32_t q_out_dtype, uint32_t q_out_stride, const float* q, uint32_t q_stride,
+                       const float* k, uint32_t k_stride, const float* v, uint32_t v_stride, uint16_t* kcache,
+                       uint16_t* vcache, uint32_t pos_start, uint32_t B, uint32_t n_heads, uint32_t n_kv_heads,
+                       uint32_t head_dim, uint32_t kv_stride, uint32_t rope, uint32_t n_rot, float theta,
+                       void* stream);
+
 /* ---- Gated DeltaNet (qwen35 linear attention) ------------------------------
  * State S: fp32 [n_v_heads][head_dim][head_dim], S[h][j][i] = column j of
  * v-head h (the reference's transposed storage, matvec.c:972-973); v-head h

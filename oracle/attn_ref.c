@@ -252,3 +252,48 @@ void yo_rmsnorm_gated(float* y, const float* x, const void* w, int w_f16, const 
         }
     }
 }
+
+/* matvec.c:890-939: rope_inplace (kind 1, pairs (2j, 2j+1)), rope_inplace_qwen
+ * (kind 2, pairs (j, j+d/2)) and rope_inplace_mrope (kind 3, pairs
+ * (j, j+n_rot/2) for j < n_rot/2, other dims unchanged); kind 0 leaves v.
+ * Products and differences are separate roundings. */
+void yo_rope(float* v, uint32_t d, uint32_t pos, float theta, int kind, uint32_t n_rot)
+{
+    uint32_t n_pairs, span, j;
+    if (kind == 0) return;
+    span = kind == 3 ? n_rot : d;
+    n_pairs = span / 2;
+    for (j = 0; j < n_pairs; j++) {
+        const uint32_t i0 = kind == 1 ? 2 * j : j;
+        const uint32_t i1 = kind == 1 ? 2 * j + 1 : j + n_pairs;
+        const float freq = powf(theta, -2.0f * (float)j / (float)span);
+        const float ang = freq * (float)pos;
+        const float c = cosf(ang), s = sinf(ang);
+        const float a = v[i0], b = v[i1];
+        v[i0] = a * c - b * s;
+        v[i1] = a * s + b * c;
+    }
+}
+
+/* engine.c:1054-1072 (and 532-550 batched): per token, RoPE on every q and
+ * k head, then k and v rounded into the engine-layout caches at row pos. */
+void yo_rope_kv_store(float* q, float* k, const float* v, uint16_t* kcache, uint16_t* vcache, uint32_t pos_start,
+                      uint32_t B, uint32_t n_heads, uint32_t n_kv, uint32_t d, int kind, uint32_t n_rot,
+                      float theta)
+{
+    const size_t qd = (size_t)n_heads * d, kvd = (size_t)n_kv * d;
+    uint32_t b, h;
+    size_t j;
+    for (b = 0; b < B; b++) {
+        const uint32_t pos = pos_start + b;
+        float* qb = q + b * qd;
+        float* kb = k + b * kvd;
+        const float* vb = v + b * kvd;
+        for (h = 0; h < n_heads; h++) yo_rope(qb + (size_t)h * d, d, pos, theta, kind, n_rot);
+        for (h = 0; h < n_kv; h++) yo_rope(kb + (size_t)h * d, d, pos, theta, kind, n_rot);
+        for (j = 0; j < kvd; j++) {
+            kcache[(size_t)pos * kvd + j] = yo_f32_to_f16(kb[j]);
+            vcache[(size_t)pos * kvd + j] = yo_f32_to_f16(vb[j]);
+        }
+    }
+}

@@ -55,6 +55,9 @@ class Oracle:
         L.yo_conv1d_update.argtypes = [FP, FP, FP, c_uint32, c_uint32]
         L.yo_conv_silu_sequence.argtypes = [FP, FP, FP, c_uint32, c_uint32, c_uint32]
         L.yo_rmsnorm_gated.argtypes = [FP, FP, ctypes.c_void_p, ctypes.c_int, FP, c_uint32, c_float]
+        L.yo_rope.argtypes = [FP, c_uint32, c_uint32, c_float, c_int, c_uint32]
+        L.yo_rope_kv_store.argtypes = [FP, FP, FP, HP, HP, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, c_int,
+                                       c_uint32, c_float]
         L.yo_gdn_state_update.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32]
         L.yo_gdn_sequence.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32,
                                       c_uint32, c_float]
@@ -161,6 +164,40 @@ def _oracle_rmsnorm_gated(self, x, w, z, eps):
     return y
 
 
+def _rope_rows(fn, x, pos, d):
+    """Apply fn(head, pos) to every head of d floats of x [B][..., n*d]; row b at pos[b]."""
+    y = np.array(x, dtype=np.float32, order="C", copy=True)
+    rows = y.reshape(y.shape[0], -1, d)
+    for b in range(rows.shape[0]):
+        for h in range(rows.shape[1]):
+            head = np.ascontiguousarray(rows[b, h])
+            fn(head, int(pos[b]))
+            rows[b, h] = head
+    return y
+
+
+def _oracle_rope(self, x, pos, d, theta, kind, n_rot=0):
+    """yo_rope over every head of every row of x [B][n*d] (row b at position pos[b])."""
+    return _rope_rows(lambda h, p: self.L.yo_rope(fp(h), d, p, theta, kind, n_rot), x, pos, d)
+
+
+def _oracle_rope_kv_store(self, q, k, v, pos_start, n_heads, n_kv, d, theta, kind, n_rot=0):
+    """yo_rope_kv_store on B rows: returns (rotated q, K rows, V rows) with
+    the caches as engine rows pos_start..pos_start+B-1 [B][n_kv*d] (u16)."""
+    q = np.array(q, np.float32, order="C", copy=True)
+    k = np.array(k, np.float32, order="C", copy=True)
+    v = np.ascontiguousarray(v, np.float32)
+    B = q.shape[0]
+    kvd = n_kv * d
+    kc = np.zeros((pos_start + B, kvd), np.uint16)
+    vc = np.zeros_like(kc)
+    self.L.yo_rope_kv_store(fp(q), fp(k), fp(v), hp(kc), hp(vc), pos_start, B, n_heads, n_kv, d, kind, n_rot,
+                            theta)
+    return q, kc[pos_start:], vc[pos_start:]
+
+
+Oracle.rope = _oracle_rope
+Oracle.rope_kv_store = _oracle_rope_kv_store
 Oracle.conv = _oracle_conv
 Oracle.conv_silu = _oracle_conv_silu
 Oracle.rmsnorm_gated = _oracle_rmsnorm_gated
@@ -183,6 +220,9 @@ class Ref:
         L.gdn_state_update.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32]
         L.conv1d_update.argtypes = [FP, FP, ctypes.c_void_p, c_uint32, c_uint32]
         L.rmsnorm_gated.argtypes = [FP, FP, ctypes.c_void_p, FP, c_uint32, c_float, c_uint32]
+        L.rope_inplace.argtypes = [FP, c_uint32, c_uint32, c_float]
+        L.rope_inplace_qwen.argtypes = [FP, c_uint32, c_uint32, c_float]
+        L.rope_inplace_mrope.argtypes = [FP, c_uint32, c_uint32, c_uint32, c_float]
         L.yrng.restype = c_uint64
         L.yrng.argtypes = [POINTER(c_uint64)]
         L.ysrand.restype = c_uint64
@@ -220,6 +260,16 @@ class Ref:
         for yr, xr, zr in zip(y.reshape(-1, n), x.reshape(-1, n), z.reshape(-1, n)):
             self.L.rmsnorm_gated(fp(yr), fp(xr), w.ctypes.data_as(ctypes.c_void_p), fp(zr), n, eps, dtype)
         return y
+
+    def rope(self, x, pos, d, theta, kind, n_rot=0):
+        """The reference's rope_inplace (kind 1), rope_inplace_qwen (2) or
+        rope_inplace_mrope (3) (matvec.c:890-939) on every head of x."""
+        L = self.L
+        fns = {0: lambda h, p: None,
+               1: lambda h, p: L.rope_inplace(fp(h), d, p, theta),
+               2: lambda h, p: L.rope_inplace_qwen(fp(h), d, p, theta),
+               3: lambda h, p: L.rope_inplace_mrope(fp(h), d, n_rot, p, theta)}
+        return _rope_rows(fns[kind], x, pos, d)
 
     def f32_to_f16(self, x):
         x = np.ascontiguousarray(x, dtype=np.float32)

@@ -107,4 +107,19 @@ void yo_conv_silu_sequence(float* state, float* x, const float* w, uint32_t T, u
  * or f16 bits. */
 void yo_rmsnorm_gated(float* y, const float* x, const void* w, int w_f16, const float* z, uint32_t n, float eps);
 
+/* matvec.c:890-939 (rope_inplace / rope_inplace_qwen / rope_inplace_mrope):
+ * kind 1 rotates pairs (2j, 2j+1), kind 2 pairs (j, j+d/2), kind 3 pairs
+ * (j, j+n_rot/2) of the first n_rot dims only, kind 0 nothing; freq =
+ * powf(theta, -2j/span) with span = d (n_rot for kind 3), angle = freq*pos,
+ * (a, b) -> (a cos - b sin, a sin + b cos).  One head of d floats, in place. */
+void yo_rope(float* v, uint32_t d, uint32_t pos, float theta, int kind, uint32_t n_rot);
+
+/* engine.c:1054-1072: for each of B tokens at pos_start.., yo_rope on the
+ * n_heads q heads and n_kv k heads (q [B][n_heads*d], k [B][n_kv*d] in
+ * place), then k and v [B][n_kv*d] rounded (yo_f32_to_f16) into the
+ * engine-layout caches at row pos (kcache, vcache [rows][n_kv*d]). */
+void yo_rope_kv_store(float* q, float* k, const float* v, uint16_t* kcache, uint16_t* vcache, uint32_t pos_start,
+                      uint32_t B, uint32_t n_heads, uint32_t n_kv, uint32_t d, int kind, uint32_t n_rot,
+                      float theta);
+
 #endif

@@ -3,7 +3,7 @@ sources (oracle/_ref/libyref.so, `make -C oracle ref`).
 
 Every expected value in the fixture is produced by the reference's compiled
 code: its f32/f16/bf16 conversions (platform.c), softmax / l2norm /
-gdn_state_update (matvec.c), yrng (platform.c), and the attention loops that
+gdn_state_update / rope_inplace* (matvec.c), yrng (platform.c), and the attention loops that
 are inline in its per-layer forward (engine.c:1074-1096 decode, 532-563
 batched prefill, 935-960 gated attention, 788-793 GDN gates), which
 oracle/ref_driver.c runs on a synthetic one-block model.  Inputs that are
@@ -47,6 +47,12 @@ GATED = [
 ]
 # (name, n_k, n_v, hd): qwen35 GDN step
 GDN = [("gdn_2_4", 2, 4, 16), ("gdn_4_2", 4, 2, 32), ("gdn_3_3", 3, 3, 64)]
+# (name, kind, head_dim, n_rot, theta): RoPE of 3 heads at 8 positions
+ROPE = [
+    ("rope_pairs", 1, 64, 0, 10000.0),        # llama rope_inplace
+    ("rope_half", 2, 128, 0, 1000000.0),      # qwen rope_inplace_qwen
+    ("rope_mrope", 3, 256, 64, 10000000.0),   # qwen35 rope_inplace_mrope
+]
 
 
 def prev_rows(ref: Ref, seed: int, n: int, kvd: int) -> np.ndarray:
@@ -179,6 +185,16 @@ def main() -> None:
     fx["rmsg_seeds"] = seeds
     fx["rmsg_f32"] = ref.rmsnorm_gated(xx, wf, zz, np.float32(1e-6))
     fx["rmsg_f16"] = ref.rmsnorm_gated(xx, ref.f32_to_f16(wf), zz, np.float32(1e-6))
+
+    # ---- RoPE: rope_inplace / rope_inplace_qwen / rope_inplace_mrope, matvec.c:890-939 ----
+    pos = np.array([0, 1, 2, 17, 511, 4095, 32767, 131071], np.int64)
+    for ri, (name, kind, d, n_rot, theta) in enumerate(ROPE):
+        seed = 6001 + ri
+        x = uniform_pm1(seed, len(pos) * 3 * d, 2.0).reshape(len(pos), 3 * d)
+        fx[f"{name}_meta"] = np.array([kind, d, n_rot, seed], np.int64)
+        fx[f"{name}_theta"] = np.float32([theta])
+        fx[f"{name}_pos"] = pos
+        fx[f"{name}_out"] = ref.rope(x, pos, d, np.float32(theta), kind, n_rot)
 
     np.savez_compressed(OUT, **fx)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(fx)} arrays)")

@@ -171,3 +171,31 @@ def test_gdn_neighbours_reject_bad_args(hiplib):
     rc = hiplib.yhip_gdn_gated_norm(P, 2048, P, 1024, P, 2048, P, 1, 4, 16, 128, F(1e-6), None)
     assert rc == -22 and "strides" in _err(hiplib)
     assert hiplib.yhip_gdn_gated_norm(P, 2048, P, 2048, P, 2048, P, 1, 0, 16, 128, F(1e-6), None) == 0
+
+
+def test_rope_kv_store_rejects_bad_args(hiplib):
+    F = ctypes.c_float
+
+    def call(q_out=P, qdt=1, qos=1024, q=P, qs=1024, ks=256, vs=256, pos=0, B=4, nh=8, nkv=2, d=128, kvs=64,
+             rope=2, n_rot=0, k=P):
+        return hiplib.yhip_rope_kv_store(q_out, qdt, qos, q, qs, k, ks, P, vs, P, P, pos, B, nh, nkv, d, kvs,
+                                         rope, n_rot, F(1e6), None)
+
+    assert call(rope=4) == -22 and "rope kind" in _err(hiplib)
+    assert call(rope=3, n_rot=0) == -22 and "n_rot" in _err(hiplib)
+    assert call(rope=3, n_rot=33) == -22 and "n_rot" in _err(hiplib)
+    assert call(rope=3, n_rot=256) == -22 and "n_rot" in _err(hiplib)
+    assert call(d=96) == -22 and "head_dim" in _err(hiplib)
+    assert call(nh=40, qs=5120, qos=5120) == -22 and "16 query heads" in _err(hiplib)
+    assert call(qdt=3) == -22 and "dtype" in _err(hiplib)
+    assert call(ks=255) == -22 and "strides" in _err(hiplib)
+    assert call(qs=1000) == -22 and "strides" in _err(hiplib)
+    assert call(pos=61, B=4) == -22 and "kv_stride" in _err(hiplib)
+    assert call(ks=257) == -22 and "aligned" in _err(hiplib)
+    assert call(q=ctypes.c_void_p(0x1004)) == -22 and "aligned" in _err(hiplib)
+    assert call(q_out=ctypes.c_void_p(0x1002), qdt=0) == -22 and "aligned" in _err(hiplib)
+    assert call(k=None) == -22 and "null" in _err(hiplib)
+    assert call(q=None) == -22 and "null" in _err(hiplib)
+    # no q (q_out NULL) skips the q checks; B = 0 is a no-op
+    assert call(q_out=None, q=None, qs=0, qos=0, B=0) == 0
+    assert call(B=0, rope=3, n_rot=64) == 0

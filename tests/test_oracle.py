@@ -389,3 +389,112 @@ def test_rmsnorm_gated_fp64(oracle):
     x64, z64 = x.astype(np.float64), z.astype(np.float64)
     want = x64 * w / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * z64 / (1 + np.exp(-z64))
     assert np.allclose(y, want, rtol=3e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------- RoPE
+
+ROPE_NAMES = ["rope_pairs", "rope_half", "rope_mrope"]
+
+
+def _rope_case(golden, name):
+    kind, d, n_rot, seed = (int(v) for v in golden[f"{name}_meta"])
+    pos = golden[f"{name}_pos"]
+    x = uniform_pm1(seed, len(pos) * 3 * d, 2.0).reshape(len(pos), 3 * d)
+    return kind, d, n_rot, golden[f"{name}_theta"][0], pos, x
+
+
+@pytest.mark.parametrize("name", ROPE_NAMES)
+def test_rope_golden(oracle, golden, name):
+    kind, d, n_rot, theta, pos, x = _rope_case(golden, name)
+    got = oracle.rope(x, pos, d, theta, kind, n_rot)
+    assert np.array_equal(bits(got), bits(golden[f"{name}_out"]))
+
+
+@pytest.mark.parametrize("kind,d,n_rot,theta", [(1, 128, 0, 500000.0), (2, 64, 0, 10000.0),
+                                                (3, 128, 32, 1e6), (3, 64, 64, 10000.0)])
+def test_rope_vs_reference_live(oracle, ref, kind, d, n_rot, theta):
+    pos = np.array([3, 99, 1000, 65535, 200000], np.int64)
+    x = uniform_pm1(121 + kind, len(pos) * 5 * d, 3.0).reshape(len(pos), 5 * d)
+    want = ref.rope(x, pos, d, np.float32(theta), kind, n_rot)
+    assert np.array_equal(bits(oracle.rope(x, pos, d, np.float32(theta), kind, n_rot)), bits(want))
+
+
+def _rope_f64(x, pos, d, theta, kind, n_rot):
+    """Textbook rotation in fp64, pairs chosen per kind (matvec.c:890-939)."""
+    y = np.array(x, np.float64).reshape(len(pos), -1, d)
+    span = n_rot if kind == 3 else d
+    j = np.arange(span // 2)
+    i0 = 2 * j if kind == 1 else j
+    i1 = 2 * j + 1 if kind == 1 else j + span // 2
+    freq = np.float64(theta) ** (-2.0 * j / span)
+    for b, p in enumerate(pos):
+        c, s = np.cos(freq * p), np.sin(freq * p)
+        a0, a1 = y[b][:, i0].copy(), y[b][:, i1].copy()
+        y[b][:, i0] = a0 * c - a1 * s
+        y[b][:, i1] = a0 * s + a1 * c
+    return y.reshape(len(pos), -1)
+
+
+@pytest.mark.parametrize("kind,d,n_rot", [(1, 64, 0), (2, 128, 0), (3, 256, 64)])
+def test_rope_fp64_rotation(oracle, kind, d, n_rot):
+    # small positions: the float angle's error (pos * ulp(freq)) stays below 1e-5
+    pos = np.arange(0, 64, 7)
+    x = uniform_pm1(131, len(pos) * 2 * d).reshape(len(pos), 2 * d)
+    got = oracle.rope(x, pos, d, np.float32(10000.0), kind, n_rot)
+    assert np.abs(got - _rope_f64(x, pos, d, 10000.0, kind, n_rot)).max() < 2e-5
+
+
+def test_rope_closed_forms(oracle):
+    d = 64
+    x = uniform_pm1(141, 4 * d).reshape(2, 2 * d)
+    # position 0: cos 0 = 1, sin 0 = 0 exactly, every kind is the identity
+    for kind, n_rot in ((0, 0), (1, 0), (2, 0), (3, 32)):
+        assert np.array_equal(bits(oracle.rope(x, [0, 0], d, np.float32(1e4), kind, n_rot)), bits(x))
+    # kind 0 (no rope) leaves every position alone
+    assert np.array_equal(bits(oracle.rope(x, [5, 77], d, np.float32(1e4), 0, 0)), bits(x))
+    # MROPE over all d dims is the qwen pairing with span d, bit for bit
+    y3 = oracle.rope(x, [9, 1234], d, np.float32(1e6), 3, d)
+    y2 = oracle.rope(x, [9, 1234], d, np.float32(1e6), 2, 0)
+    assert np.array_equal(bits(y3), bits(y2))
+    # MROPE leaves dims n_rot.. untouched
+    y = oracle.rope(x, [9, 1234], d, np.float32(1e6), 3, 16).reshape(2, 2, d)
+    assert np.array_equal(bits(y[:, :, 16:]), bits(x.reshape(2, 2, d)[:, :, 16:]))
+    # the llama and qwen pairings are one permutation apart: interleave the
+    # halves, rotate pairs (2j, 2j+1), de-interleave == rotate (j, j+d/2)
+    perm = np.empty(d, np.int64)
+    perm[0::2], perm[1::2] = np.arange(d // 2), np.arange(d // 2, d)
+    xi = x.reshape(2, 2, d)[:, :, perm].reshape(2, 2 * d)
+    yp = oracle.rope(xi, [3, 4000], d, np.float32(1e4), 1, 0).reshape(2, 2, d)
+    yq = oracle.rope(x, [3, 4000], d, np.float32(1e4), 2, 0).reshape(2, 2, d)
+    assert np.array_equal(bits(yp), bits(yq[:, :, perm]))
+    # each rotation keeps the pair's length
+    y = oracle.rope(x, [31, 31], d, np.float32(1e4), 1, 0).reshape(-1, 2)
+    xr = x.reshape(-1, 2).astype(np.float64)
+    assert np.allclose(np.hypot(y[:, 0], y[:, 1]), np.hypot(xr[:, 0], xr[:, 1]), rtol=1e-6)
+
+
+@pytest.mark.parametrize("name", ROPE_NAMES)
+def test_rope_kv_store_loop_golden(oracle, golden, name):
+    # the per-token loop (engine.c:1054-1072) on rows [q | k | v] of one head
+    # each: q and k are the golden rotations, the caches their f16 rounding
+    kind, d, n_rot, theta, pos, x = _rope_case(golden, name)
+    out = golden[f"{name}_out"]
+    for b in (0, 3, 5, 7):
+        q, kc, vc = oracle.rope_kv_store(x[b:b + 1, :d], x[b:b + 1, d:2 * d], x[b:b + 1, 2 * d:], int(pos[b]), 1, 1,
+                                         d, theta, kind, n_rot)
+        assert np.array_equal(bits(q[0]), bits(out[b, :d]))
+        assert np.array_equal(kc[0], oracle.f32_to_f16(out[b, d:2 * d]))
+        assert np.array_equal(vc[0], oracle.f32_to_f16(x[b, 2 * d:]))
+
+
+def test_rope_kv_store_loop_gqa_rows(oracle):
+    # several heads and consecutive rows: each head rotated on its own at its row's position
+    nh, nkv, d, ps, B = 6, 2, 64, 30, 5
+    q = uniform_pm1(151, B * nh * d).reshape(B, nh * d)
+    k = uniform_pm1(152, B * nkv * d).reshape(B, nkv * d)
+    v = uniform_pm1(153, B * nkv * d).reshape(B, nkv * d)
+    qr, kc, vc = oracle.rope_kv_store(q, k, v, ps, nh, nkv, d, np.float32(1e4), 2)
+    pos = np.arange(ps, ps + B)
+    assert np.array_equal(bits(qr), bits(oracle.rope(q, pos, d, np.float32(1e4), 2)))
+    assert np.array_equal(kc, oracle.f32_to_f16(oracle.rope(k, pos, d, np.float32(1e4), 2)))
+    assert np.array_equal(vc, oracle.f32_to_f16(v))

@@ -42,6 +42,9 @@ SIGNATURES = {
                                c_size_t, c_void_p]),
     "yhip_gdn_chunk_workspace": (c_size_t, [c_uint32, c_uint32, c_uint32]),
     "yhip_gdn_gates": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_void_p]),
+    "yhip_rope_kv_store": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p,
+                                   c_uint32, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
+                                   c_uint32, c_uint32, c_uint32, c_float, c_void_p]),
     "yhip_gdn_conv": (c_int, [c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_void_p, c_uint32, c_uint32,
                               c_uint32, c_int, c_void_p]),
     "yhip_gdn_gated_norm": (c_int, [c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32,

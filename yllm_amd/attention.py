@@ -99,6 +99,56 @@ def kv_store(cache: LayerKV, k: torch.Tensor, v: torch.Tensor, pos_start: int) -
                               k.shape[0], cache.n_kv, cache.head_dim, cache.kv_stride, _stream()))
 
 
+ROPE_NONE, ROPE_PAIRS, ROPE_HALF, ROPE_MROPE = 0, 1, 2, 3
+
+
+def _rows(t: torch.Tensor, width: int, name: str) -> tuple[torch.Tensor, int]:
+    """A [B, >=width] fp32 matrix with unit column stride; returns (t, row stride)."""
+    if t.dim() == 1:
+        t = t.unsqueeze(0)
+    if t.dim() != 2 or t.dtype != torch.float32 or t.stride(1) != 1 or t.shape[1] < width:
+        raise YhipError(-22, f"rope_kv_store: {name} must be fp32 [B, >={width}] with unit column stride")
+    return t, (t.stride(0) if t.shape[0] > 1 else t.shape[1])
+
+
+def rope_kv_store(cache: LayerKV, q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor, pos_start: int,
+                  n_heads: int, rope: int, theta: float, n_rot: int = 0, q_out: torch.Tensor | None = None,
+                  q_out_dtype: torch.dtype = torch.float32) -> torch.Tensor | None:
+    """RoPE on q and k for rows at positions pos_start.. (engine.c:1054-1072,
+    qwen35 engine.c:910-934), k and v stored into the cache like kv_store.
+
+    q [B, n_heads*head_dim], k and v [B, n_kv*head_dim], fp32, rows may be
+    strided slices of one projection output.  rope: ROPE_PAIRS (llama),
+    ROPE_HALF (qwen), ROPE_MROPE (qwen35, first n_rot dims) or ROPE_NONE.
+    Returns the rotated q (q_out, allocated in q_out_dtype if not given;
+    q_out may be q itself), or None when q is None."""
+    for t in (q, k, v, q_out):
+        if t is not None and not t.is_cuda:
+            raise YhipError(-22, "tensor must be on the GPU")
+    d = cache.head_dim
+    k, ks = _rows(k, cache.n_kv * d, "k")
+    v, vs = _rows(v, cache.n_kv * d, "v")
+    B = k.shape[0]
+    qs = qos = 0
+    qdt = F32
+    if q is not None:
+        q, qs = _rows(q, n_heads * d, "q")
+        if q_out is None:
+            q_out = torch.empty((B, n_heads * d), dtype=q_out_dtype, device=q.device)
+        if q_out.dim() != 2 or q_out.stride(1) != 1 or q_out.shape[0] != B or q_out.shape[1] < n_heads * d:
+            raise YhipError(-22, "rope_kv_store: q_out must be [B, >=n_heads*head_dim] with unit column stride")
+        qos = q_out.stride(0) if B > 1 else q_out.shape[1]
+        qdt = _dtype_code(q_out)
+        if q.shape[0] != B:
+            raise YhipError(-22, "rope_kv_store: q, k, v row counts differ")
+    if v.shape[0] != B:
+        raise YhipError(-22, "rope_kv_store: q, k, v row counts differ")
+    check(lib().yhip_rope_kv_store(_ptr(q_out) if q is not None else None, qdt, qos, _ptr(q), qs, _ptr(k), ks,
+                                   _ptr(v), vs, _ptr(cache.k), _ptr(cache.v), pos_start, B, n_heads, cache.n_kv,
+                                   d, cache.kv_stride, rope, n_rot, theta, _stream()))
+    return q_out if q is not None else None
+
+
 def kv_from_engine(cache: LayerKV, eng_k: torch.Tensor, eng_v: torch.Tensor) -> None:
     """Fill rows 0..n-1 from engine-layout f16 rows [n, n_kv*head_dim] (yllm.h:109)."""
     _need_gpu(eng_k, eng_v)

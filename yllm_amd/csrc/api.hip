@@ -7,6 +7,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
 
 namespace {
 
@@ -300,6 +301,68 @@ size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_di
 {
     if ((head_dim != 64 && head_dim != 128) || T < yhip::gdn_chunk_tokens()) return 0;
     return yhip::gdn_chunk_workspace(T, n_v_heads, head_dim);
+}
+
+int yhip_rope_kv_store(void* q_out, uint32_t q_out_dtype, uint32_t q_out_stride, const float* q, uint32_t q_stride,
+                       const float* k, uint32_t k_stride, const float* v, uint32_t v_stride, uint16_t* kcache,
+                       uint16_t* vcache, uint32_t pos_start, uint32_t B, uint32_t n_heads, uint32_t n_kv_heads,
+                       uint32_t head_dim, uint32_t kv_stride, uint32_t rope, uint32_t n_rot, float theta,
+                       void* stream)
+{
+    const char* fn = "yhip_rope_kv_store";
+    int rc = check_heads(fn, n_heads, n_kv_heads, head_dim, kv_stride);
+    if (rc) return rc;
+    if (!k || !v || !kcache || !vcache || (q_out && !q)) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    if (rope > YHIP_ROPE_MROPE) return fail(YHIP_EINVAL, "%s: unknown rope kind %u", fn, rope);
+    if (rope == YHIP_ROPE_MROPE && (n_rot == 0 || n_rot % 2 || n_rot > head_dim))
+        return fail(YHIP_EINVAL, "%s: n_rot %u must be even and at most head_dim", fn, n_rot);
+    if (q_out && !valid_dtype(q_out_dtype)) return fail(YHIP_EINVAL, "%s: bad q_out dtype", fn);
+    const uint64_t kv_dim = (uint64_t)n_kv_heads * head_dim, qd = (uint64_t)n_heads * head_dim;
+    if (k_stride < kv_dim || v_stride < kv_dim || (q_out && (q_stride < qd || q_out_stride < qd)))
+        return fail(YHIP_EINVAL, "%s: strides must cover the heads", fn);
+    if ((uint64_t)pos_start + B > kv_stride)
+        return fail(YHIP_EINVAL, "%s: rows %u..%u exceed kv_stride %u", fn, pos_start, pos_start + B, kv_stride);
+    // pairs of adjacent elements move as one 8-byte (f32) or 4-byte (f16/bf16) access
+    const uint32_t qo_align = q_out_dtype == YHIP_F32 ? 8u : 4u;
+    if ((uintptr_t)k % 8 || (uintptr_t)v % 8 || (uintptr_t)kcache % 4 || k_stride % 2 || v_stride % 2 ||
+        (q_out && ((uintptr_t)q % 8 || (uintptr_t)q_out % qo_align || q_stride % 2 || q_out_stride % 2)))
+        return fail(YHIP_EINVAL, "%s: q/k/v must be 8-byte aligned with even strides", fn);
+    if (B == 0) return done(hipSuccess, "");
+    yhip::RopeArgs a = {};
+    a.q_out = q_out;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.kc = kcache;
+    a.vc = vcache;
+    a.q_out_dtype = q_out_dtype;
+    a.q_out_stride = q_out_stride;
+    a.q_stride = q_stride;
+    a.k_stride = k_stride;
+    a.v_stride = v_stride;
+    a.pos_start = pos_start;
+    a.B = B;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.D = head_dim;
+    a.kv_stride = kv_stride;
+    a.kind = rope;
+    a.n_rot = rope == YHIP_ROPE_MROPE ? n_rot : head_dim;
+    {
+        // the reference's frequency formula (matvec.c:895), host powf;
+        // the last table is kept per thread
+        thread_local float t_theta = 0.0f;
+        thread_local uint32_t t_span = 0;
+        thread_local float t_freq[128];
+        const uint32_t span = a.n_rot;
+        if (rope != YHIP_ROPE_NONE && (t_span != span || !(t_theta == theta))) {
+            for (uint32_t j = 0; j < span / 2; ++j) t_freq[j] = powf(theta, -2.0f * (float)j / (float)span);
+            t_span = span;
+            t_theta = theta;
+        }
+        if (rope != YHIP_ROPE_NONE) memcpy(a.freq, t_freq, sizeof(float) * (span / 2));
+    }
+    return done(yhip::launch_rope_kv(a, (hipStream_t)stream), fn);
 }
 
 int yhip_gdn_conv(float* out, uint32_t out_stride, const float* x, uint32_t x_stride, float* conv_state,

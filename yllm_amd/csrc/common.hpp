@@ -12,6 +12,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kF16 = 0, kF32 = 1, kBF16 = 2;
+// RoPE kinds (the public YHIP_ROPE_* values)
+constexpr uint32_t kRopeNone = 0, kRopePairs = 1, kRopeHalf = 2, kRopeMrope = 3;
 
 // KV cache geometry (per sequence, per layer):
 //   K: [n_kv][kv_stride][D]                  row = position

@@ -61,6 +61,24 @@ struct PrefillArgs {
 };
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
 
+// ---- rope.hip ----
+struct RopeArgs {
+    void* q_out;            // rows q_out_stride apart, dtype q_out_dtype (null: no q)
+    const float* q;         // rows q_stride apart
+    const float* k;         // rows k_stride apart
+    const float* v;         // rows v_stride apart
+    uint16_t* kc;           // head-major K cache
+    uint16_t* vc;           // V tiles
+    uint32_t q_out_dtype, q_out_stride, q_stride, k_stride, v_stride;
+    uint32_t pos_start, B, n_heads, n_kv, D, kv_stride, kind, n_rot;
+    // set by the launcher: waves per token, heads per wave, workgroups of each role
+    uint32_t groups, heads_per_wave, rope_blocks, v_blocks;
+    // freq[j] = powf(theta, -2j/span) for the rotated pairs j < span/2,
+    // computed on the host with the C library's powf, as the reference does
+    float freq[128];
+};
+hipError_t launch_rope_kv(RopeArgs a, hipStream_t st);
+
 // ---- gdn_conv.hip ----
 struct GdnConvArgs {
     float* out;             // [T] rows out_stride apart (not overlapping x)

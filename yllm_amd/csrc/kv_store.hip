@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void k_store_kernel(uint16_t* __restrict__ kc,
 // that reads walk source rows and writes walk positions inside a tile.
 __global__ __launch_bounds__(256) void v_store_kernel(uint16_t* __restrict__ vc,
                                                       const void* __restrict__ v, uint32_t dt,
-                                                      uint32_t pos_start, uint32_t B,
+                                                      uint32_t v_stride, uint32_t pos_start, uint32_t B,
                                                       uint32_t n_kv, uint32_t D,
                                                       uint32_t kv_stride)
 {
@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void v_store_kernel(uint16_t* __restrict__ vc,
     const uint32_t tx = threadIdx.x & 63u, ty = threadIdx.x >> 6;
     for (uint32_t r = ty; r < 64u; r += 4u) {
         const uint32_t b = b0 + r, j = j0 + tx;
-        if (b < B && j < kv_dim) tile[r][tx] = to_cache_bits(v, (size_t)b * kv_dim + j, dt);
+        if (b < B && j < kv_dim) tile[r][tx] = to_cache_bits(v, (size_t)b * v_stride + j, dt);
     }
     __syncthreads();
     for (uint32_t r = ty; r < 64u; r += 4u) {
@@ -133,7 +133,7 @@ hipError_t launch_kv_store(uint16_t* kc, uint16_t* vc, const void* k, const void
     hipLaunchKernelGGL(k_store_kernel, gk, dim3(256), 0, st, kc, k, dt, pos_start, B, n_kv, D,
                        kv_stride);
     dim3 gv((kv_dim + 63u) / 64u, (B + 63u) / 64u);
-    hipLaunchKernelGGL(v_store_kernel, gv, dim3(256), 0, st, vc, v, dt, pos_start, B, n_kv, D,
+    hipLaunchKernelGGL(v_store_kernel, gv, dim3(256), 0, st, vc, v, dt, kv_dim, pos_start, B, n_kv, D,
                        kv_stride);
     return hipGetLastError();
 }
@@ -148,7 +148,7 @@ hipError_t launch_kv_from_engine(uint16_t* kc, uint16_t* vc, const uint16_t* ek,
                        D, kv_stride, 0);
     // f16 bits through the same tiler as the store (f16 sources are copied)
     dim3 gv((kv_dim + 63u) / 64u, (rows + 63u) / 64u);
-    hipLaunchKernelGGL(v_store_kernel, gv, dim3(256), 0, st, vc, (const void*)ev, kF16, 0u, rows, n_kv,
+    hipLaunchKernelGGL(v_store_kernel, gv, dim3(256), 0, st, vc, (const void*)ev, kF16, kv_dim, 0u, rows, n_kv,
                        D, kv_stride);
     return hipGetLastError();
 }
