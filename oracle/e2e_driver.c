@@ -33,6 +33,7 @@
 
 #include <math.h>
 
+#include "cache.h"
 #include "convert.h"
 #include "yllm.h"
 #include "yllm_device_hip.h"
@@ -358,6 +359,102 @@ int ye_run(const char* path, int use_hip, int device_id, int fail_after, const u
         }
         status[1] = diff;
         free(keep);
+    }
+    engine_free(&e);
+    return 0;
+}
+
+/* One greedy decode step through e->fwd_block (see the file comment). */
+static void decode_step(Engine* e, uint32_t tok, uint32_t pos)
+{
+    DeviceMode saved = e->device_mode;
+    e->device_mode = DEV_MODE_VULKAN;
+    engine_forward(e, tok, pos);
+    e->device_mode = saved;
+}
+
+static int open_bound(Engine* e, const char* path, int use_hip, int device_id, int* bound, char* err,
+                      size_t errlen)
+{
+    memset(e, 0, sizeof *e);
+    *bound = -1;
+    if (engine_init(e, path, 0, 0, err, errlen) != 0) return -1;
+    if (use_hip) {
+        *bound = bind_hip(e, device_id, err, errlen);
+        if (*bound == -2) {
+            engine_free(e);
+            return -1;
+        }
+    }
+    return 0;
+}
+
+/* Session save and resume through the reference's YLLMSKV01 format
+ * (sess_kv_save / sess_kv_load, cache.c:174-247).  Engine A runs the prompt
+ * as a batched prefill and n_before greedy decode steps, then saves its KV
+ * (pos = n_prompt + n_before rows) to sess_path and is freed.  Engine B, a
+ * fresh engine bound the same way, loads the file and, for the HIP backend,
+ * sends the loaded rows to HBM with device_hip_kv_from_host; it then decodes
+ * n_after steps from A's next greedy token.  logits: [n_after][vocab] of B's
+ * steps; tokens: [n_before + n_after] all chosen tokens.  status[0] = bind
+ * result of B (0 HIP, -1 CPU), status[1] = the position sess_kv_load gave.
+ * Returns 0 or -1 with err set. */
+int ye_resume(const char* path, int use_hip, int device_id, const uint32_t* prompt, int n_prompt, int n_before,
+              int n_after, const char* sess_path, float* logits, uint32_t* tokens, int* status, char* err,
+              size_t errlen)
+{
+    Engine e;
+    uint32_t vocab, pos, next, loaded = 0;
+    int i, bound;
+    float* last;
+    status[0] = status[1] = -1;
+    if (open_bound(&e, path, use_hip, device_id, &bound, err, errlen) != 0) return -1;
+    vocab = e.ws.model.h.vocab;
+    if (engine_forward_prefill(&e, prompt, n_prompt, 0) != 0) {
+        snprintf(err, errlen, "prefill failed");
+        engine_free(&e);
+        return -1;
+    }
+    last = (float*)malloc((size_t)vocab * 4);
+    if (!last) {
+        engine_free(&e);
+        return -1;
+    }
+    memcpy(last, e.logits, (size_t)vocab * 4);
+    pos = (uint32_t)n_prompt;
+    for (i = 0; i < n_before; i++, pos++) {
+        tokens[i] = argmax(last, vocab);
+        decode_step(&e, tokens[i], pos);
+        memcpy(last, e.logits, (size_t)vocab * 4);
+    }
+    next = argmax(last, vocab);
+    free(last);
+    if (sess_kv_save(&e, pos, sess_path) != 0) {
+        snprintf(err, errlen, "sess_kv_save failed");
+        engine_free(&e);
+        return -1;
+    }
+    engine_free(&e);
+
+    if (open_bound(&e, path, use_hip, device_id, &bound, err, errlen) != 0) return -1;
+    status[0] = bound;
+    if (sess_kv_load(&e, sess_path, &loaded) != 0) {
+        snprintf(err, errlen, "sess_kv_load failed");
+        engine_free(&e);
+        return -1;
+    }
+    status[1] = (int)loaded;
+    if (bound == 0 && device_hip_kv_from_host(&e, loaded) != 0) {
+        snprintf(err, errlen, "device_hip_kv_from_host failed");
+        engine_free(&e);
+        return -1;
+    }
+    pos = loaded;
+    for (i = 0; i < n_after; i++, pos++) {
+        tokens[n_before + i] = next;
+        decode_step(&e, next, pos);
+        memcpy(logits + (size_t)i * vocab, e.logits, (size_t)vocab * 4);
+        next = argmax(e.logits, vocab);
     }
     engine_free(&e);
     return 0;

@@ -37,6 +37,9 @@ def e2e():
     lib.ye_make_model.argtypes = [c_char_p] + [c_uint32] * 8 + [c_char_p, c_size_t]
     lib.ye_make_model_q35.restype = c_int
     lib.ye_make_model_q35.argtypes = [c_char_p] + [c_uint32] * 11 + [c_char_p, c_size_t]
+    lib.ye_resume.restype = c_int
+    lib.ye_resume.argtypes = [c_char_p, c_int, c_int, POINTER(c_uint32), c_int, c_int, c_int, c_char_p,
+                              POINTER(c_float), POINTER(c_uint32), POINTER(c_int), c_char_p, c_size_t]
     lib.ye_run.restype = c_int
     lib.ye_run.argtypes = [c_char_p, c_int, c_int, c_int, POINTER(c_uint32), c_int, c_int, POINTER(c_float),
                            POINTER(c_uint32), POINTER(c_int), c_char_p, c_size_t]
@@ -76,6 +79,33 @@ def run(lib, path, prompt, n_decode, use_hip, fail_after=-1, vocab=512):
     return logits, tokens[:n_decode], status, err.value.decode()
 
 
+def resume(lib, path, prompt, n_before, n_after, use_hip, sess_path, vocab=512):
+    """Save after n_before decode steps (sess_kv_save), resume in a fresh
+    engine (sess_kv_load [+ device_hip_kv_from_host]) for n_after steps."""
+    prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+    logits = np.zeros((n_after, vocab), dtype=np.float32)
+    tokens = np.zeros(n_before + n_after, dtype=np.uint32)
+    status = np.zeros(2, dtype=np.int32)
+    err = ctypes.create_string_buffer(256)
+    rc = lib.ye_resume(str(path).encode(), int(use_hip), 0, prompt.ctypes.data_as(POINTER(c_uint32)), len(prompt),
+                       n_before, n_after, str(sess_path).encode(), logits.ctypes.data_as(POINTER(c_float)),
+                       tokens.ctypes.data_as(POINTER(c_uint32)), status.ctypes.data_as(POINTER(c_int)), err, 256)
+    assert rc == 0, err.value.decode()
+    return logits, tokens, status, err.value.decode()
+
+
+def read_session(path):
+    """A YLLMSKV01 file (cache.c:174-196): 8 magic bytes, n_blocks, kv_dim,
+    max_seq, pos (u32), then per layer 1..n_blocks K rows 0..pos-1 and V rows
+    0..pos-1 (f16 bits)."""
+    raw = Path(path).read_bytes()
+    assert raw[:8] == b"YLLMSKV0"
+    nb, kvd, max_seq, pos = np.frombuffer(raw[8:24], dtype=np.uint32)
+    rows = np.frombuffer(raw[24:], dtype=np.uint16)
+    assert rows.size == nb * 2 * pos * kvd
+    return (int(nb), int(kvd), int(max_seq), int(pos)), rows.reshape(nb, 2, pos, kvd)
+
+
 def rel_l2(a, b):
     return float(np.linalg.norm((a - b).ravel()) / max(np.linalg.norm(b.ravel()), 1e-30))
 
@@ -85,6 +115,21 @@ def prompt_of(n, vocab=512, seed=3):
 
 
 # ------------------------------------------------------------------ CPU only
+
+def test_session_resume_on_the_cpu_engine_is_exact(e2e, tmp_path):
+    """The driver's save / resume on the CPU engine continues exactly as an
+    uninterrupted run (the file holds every KV row the decode reads)."""
+    path = make_model(e2e, tmp_path / "m.llf", 2, 512, 8, 2)
+    prompt = prompt_of(37)
+    nb, na = 3, 4
+    want, wt, _, _ = run(e2e, path, prompt, nb + na, use_hip=False)
+    got, gt, status, _ = resume(e2e, path, prompt, nb, na, False, tmp_path / "s.kv")
+    assert status[1] == len(prompt) + nb
+    assert np.array_equal(gt, wt)
+    assert np.array_equal(got.view(np.uint32), want[nb + 1:].view(np.uint32))
+    (n_blocks, kvd, max_seq, pos), rows = read_session(tmp_path / "s.kv")
+    assert (n_blocks, kvd, pos) == (2, 128, len(prompt) + nb)
+
 
 def test_plugin_exports_every_declared_symbol(e2e):
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
@@ -223,3 +268,32 @@ def test_qwen35_failure_hook(e2e, cuda, tmp_path, fail_after):
     else:
         assert max(rel_l2(got[i], want[i]) for i in range(5)) <= TOL
         assert np.array_equal(gt, wt)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("arch,hidden,heads,kv_heads", [(ARCH_LLAMA, 512, 8, 2), (ARCH_QWEN, 1024, 8, 2)])
+def test_session_save_resume_with_hbm_cache(e2e, cuda, tmp_path, arch, hidden, heads, kv_heads):
+    """KV persistence (YLLMSKV01, cache.c:174-247) with an HBM-resident cache:
+    a HIP-bound engine saves its session; a fresh HIP-bound engine loads it,
+    sends the rows to HBM (device_hip_kv_from_host) and continues exactly as
+    the uninterrupted HIP run, bit for bit.  The file carries the same rows
+    as the CPU engine's file (first layer bit-equal, later layers within the
+    attention tolerance of the residual stream they come from)."""
+    path = make_model(e2e, tmp_path / "m.llf", 3, hidden, heads, kv_heads, arch=arch)
+    prompt = prompt_of(70)
+    nb, na = 3, 5
+    want, wt, st_u, msg = run(e2e, path, prompt, nb + na, use_hip=True)
+    assert st_u[0] == 0, msg
+    got, gt, status, msg = resume(e2e, path, prompt, nb, na, True, tmp_path / "hip.kv")
+    assert status[0] == 0, msg
+    assert status[1] == len(prompt) + nb
+    assert np.array_equal(gt, wt)
+    assert np.array_equal(got.view(np.uint32), want[nb + 1:].view(np.uint32))
+    _, _, _, _ = resume(e2e, path, prompt, nb, 1, False, tmp_path / "cpu.kv")
+    h_hip, rows_hip = read_session(tmp_path / "hip.kv")
+    h_cpu, rows_cpu = read_session(tmp_path / "cpu.kv")
+    assert h_hip == h_cpu
+    assert np.array_equal(rows_hip[0], rows_cpu[0])
+    f16 = lambda r: r.view(np.float16).astype(np.float32)
+    for layer in range(1, h_hip[0]):
+        assert rel_l2(f16(rows_hip[layer]), f16(rows_cpu[layer])) <= TOL
