@@ -22,6 +22,9 @@ batch of synthetic input, with all inputs resident in HBM:
   rope8k      fused RoPE + KV store ahead of attention: 8192 tokens,
               32 / 8 heads of 128 (llama pairs, theta 5e5), f32 q/k/v
               slices of one projection row -> f16 q, f16 K/V cache.
+  oproj8k     o_proj after prefill attention: x += W_o . att, 8192 tokens,
+              W_o 4096 x 4096 f16, f16 att (one hipBLASLt GEMM).
+  oproj1      the same for one decode token (the GEMV kernel, HBM-bound).
   hybrid      the fifth configuration end to end: 3 GDN layers + 1 gated
               attention layer (16 / 2 heads, d 256, bf16), 4096-token
               prefill then 256 decode steps; tokens/s over the whole pass.
@@ -74,7 +77,7 @@ def prefill_flops(L: int, nh: int, hd: int, pos_start: int = 0) -> float:
     return 4.0 * nh * hd * keys
 
 
-def time_steps(fn, steps: int, warmup: int, out=None):
+def time_steps(fn, steps: int, warmup: int, out=None, eager: bool = False):
     """Run fn(i) `warmup` times eagerly, capture steps warmup..warmup+steps-1
     in one HIP graph and time its replay with HIP events on the replay stream,
     so host launch overhead is not part of the measurement.  The output of
@@ -85,7 +88,7 @@ def time_steps(fn, steps: int, warmup: int, out=None):
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    if EAGER:
+    if EAGER or eager:
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for i in range(steps):
@@ -387,6 +390,67 @@ def run_rope(L: int, nh: int, nkv: int, hd: int, theta: float, steps: int, warmu
     return res
 
 
+def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool):
+    """o_proj x += W_o . att over B tokens, f16 weights; att f32 for one
+    decode token (the engine's att_out), f16 for a prefill batch (the prefill
+    kernel's f16 output)."""
+    import torch
+
+    from yllm_amd.attention import o_proj, o_proj_workspace_bytes
+
+    dev = torch.device("cuda:0")
+    seed = SEED + 7
+    w = (torch.from_numpy(synth_raw(seed, hidden * qdim).reshape(hidden, qdim)).to(dev) / np.sqrt(qdim)).half()
+    att = torch.from_numpy(synth_raw(seed, B * qdim, hidden * qdim).reshape(B, qdim)).to(dev) * 0.5
+    gemv = B <= 8
+    if not gemv:
+        att = att.half()
+    x = torch.from_numpy(synth_raw(seed, B * hidden, hidden * qdim + B * qdim).reshape(B, hidden)).to(dev)
+    # rotating (weights, att, x) sets beyond the 256 MB MALL
+    att_dt, att_size = att.dtype, att.element_size()
+    set_bytes = hidden * qdim * 2 + B * (qdim * att_size + hidden * 4)
+    n_sets = max(1, int(-(-ROTATE_BYTES // set_bytes)))
+    sets = [(w.clone(), att.clone(), x.clone()) for _ in range(n_sets)]
+    x_ref = x.clone()
+    del w, att, x
+    ws = torch.empty(max(o_proj_workspace_bytes(B, qdim, torch.float16, att_dt), 256), dtype=torch.uint8,
+                     device=dev)
+
+    def step(i):
+        wi, ai, xi = sets[i % n_sets]
+        o_proj(xi, ai, wi, workspace=ws)
+
+    last = sets[(warmup + steps - 1) % n_sets]
+    # x accumulates from step to step, so no replay-vs-eager output check; the
+    # GEMM path (hipBLASLt) is launched eagerly, outside any graph capture
+    ms, kern_ms = time_steps(step, steps, warmup, None, eager=not gemv)
+    flops = 2.0 * B * hidden * qdim
+    nbytes = hidden * qdim * 2.0 + B * qdim * att_size + 2.0 * B * hidden * 4.0
+    if gemv:
+        roof = {"bound": "hbm", "kernel": "oproj_gemv_kernel<1,%d>" % (1 if B == 1 else 8),
+                "achieved": nbytes / (kern_ms * 1e-3) / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": nbytes / (kern_ms * 1e-3) / HBM_PEAK, "bytes_per_launch": nbytes, "launch_ms": kern_ms,
+                "traffic": traffic_of(f"oproj{B}")}
+        value, unit = nbytes / (ms * 1e-3) / 1e9, "GB/s"
+    else:
+        roof = {"bound": "mfma", "kernel": "hipBLASLt f16 GEMM (f32 C/D, beta 1)",
+                "achieved": flops / (kern_ms * 1e-3) / 1e12, "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
+                "frac": flops / (kern_ms * 1e-3) / MFMA_F16_PEAK, "flops_per_launch": flops, "launch_ms": kern_ms,
+                "traffic": traffic_of(f"oproj{B}")}
+        value, unit = flops / (ms * 1e-3) / 1e12, "TFLOP/s"
+    res = {
+        "value": value, "unit": unit, "ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3),
+        "config": {"workload": f"o_proj x += W_o . att, {B} token(s), W_o {hidden} x {qdim} f16, "
+                               f"{'f32' if gemv else 'f16'} att, f32 residual, N(0,1) seed {hex(seed)}; "
+                               f"{n_sets} rotating sets (> 256 MB MALL)",
+                   "tokens": B, "hidden": hidden, "qdim": qdim},
+        "roofline": roof,
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_oproj(last, x_ref, B, hidden, qdim)
+    return res
+
+
 def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
     """The fifth configuration: one group of 3 Gated-DeltaNet layers and 1
     gated GQA attention layer, a 4096-token prefill then n_dec decode steps.
@@ -570,6 +634,41 @@ def cpu_rope(rope_set, L, nh, nkv, hd, theta):
             "k_bits_equal_frac": k_equal}
 
 
+def cpu_oproj(oproj_set, x_before, B, hidden, qdim):
+    """The oracle's matmul_f16 rows (the reference runs them with OpenMP over
+    output rows) on a sample of tokens; those rows of the GPU result are
+    checked against it.  x_before is the set's residual before the timed
+    steps; the GPU applied o_proj to it (warmup + steps) / n_sets times, so
+    the check uses one fresh GPU call on a copy."""
+    import torch
+
+    from yllm_amd.attention import o_proj
+
+    O = _oracle()
+    from oracle_lib import rel_l2
+
+    w, att, _ = oproj_set
+    rows = np.unique(np.linspace(0, B - 1, min(B, 8)).astype(np.int64))
+    xg = x_before.clone()
+    o_proj(xg, att, w)
+    torch.cuda.synchronize()
+    wn = w.view(torch.int16).cpu().numpy().view(np.uint16)
+    an = att[rows].float().cpu().numpy()
+    xn = x_before[rows].cpu().numpy()
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        want = O.o_proj(xn, an, wn)
+        n += len(rows)
+        dt = time.perf_counter() - t0
+        if dt > 2.0:
+            break
+    _, model = _host_desc(O)
+    return {"value": n / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{len(rows)} tokens, passes until 2 s ({n} tokens in {dt:.2f} s), one thread; {model}",
+            "seconds": dt, "parity_rel_l2": rel_l2(xg[rows].cpu().numpy(), want)}
+
+
 def cpu_gdn(q, k, v, alpha, beta_raw, out, T, n_h, d):
     """The oracle's single-threaded recurrence (the reference's gdn_state_update
     has no OpenMP) over the whole sequence."""
@@ -639,7 +738,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="prefill2k",
                     choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch", "gdn4k",
-                             "rope8k", "hybrid"])
+                             "rope8k", "oproj8k", "oproj1", "hybrid"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k / gdn4k secondary lines")
     ap.add_argument("--gdn-tokenwise", action="store_true",
@@ -679,18 +778,23 @@ def main() -> int:
         res = run_gdn(4096, 16, 128, args.steps, args.warmup, cpu)
     elif w == "rope8k":
         res = run_rope(8192, 32, 8, 128, 500000.0, args.steps, args.warmup, cpu)
+    elif w == "oproj8k":
+        res = run_oproj(8192, 4096, 4096, args.steps, args.warmup, cpu)
+    elif w == "oproj1":
+        res = run_oproj(1, 4096, 4096, args.steps, args.warmup, cpu)
     elif w == "hybrid":
         res = run_hybrid(args.steps, args.warmup)
     else:
         res = run_decode_batch(32, 8, 128, 64, args.steps, args.warmup)
-    dtype = {"gdn4k": "f32", "rope8k": "f32 rotation, f16 stores", "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}.get(
+    dtype = {"gdn4k": "f32", "rope8k": "f32 rotation, f16 stores", "oproj8k": "f16 MFMA, f32 accumulate",
+             "oproj1": "f16 weights, f32 activations and accumulate", "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}.get(
         w, "f16 MFMA, f32 accumulate/softmax")
 
     line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": dtype, "data": "synthetic",
             "config": res["config"], "tokens_per_s": res["tokens_per_s"], "roofline": res["roofline"],
-            "timing": ("K eager launches" if EAGER else "K steps captured in one HIP graph") +
+            "timing": ("K eager launches" if EAGER or w == "oproj8k" else "K steps captured in one HIP graph") +
                       ", timed with HIP events on the launch stream",
             "measured_copy_GBps": copy_ceiling_gbps()}
     if "cpu_baseline" in res:

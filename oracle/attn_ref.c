@@ -297,3 +297,35 @@ void yo_rope_kv_store(float* q, float* k, const float* v, uint16_t* kcache, uint
         }
     }
 }
+
+/* matvec.c:98-122 (matmul_f32 / matmul_f16): y[o] = sum_i x[i] * w[o*in + i]
+ * in i order from 0, w f32 (w_f16 == 0) or f16 bits. */
+void yo_matmul(float* y, const float* x, const void* w, int w_f16, uint32_t out, uint32_t in)
+{
+    uint32_t o, i;
+    for (o = 0; o < out; o++) {
+        float acc = 0.0f;
+        if (w_f16) {
+            const uint16_t* wr = (const uint16_t*)w + (size_t)o * in;
+            for (i = 0; i < in; i++) acc += x[i] * yo_f16_to_f32(wr[i]);
+        } else {
+            const float* wr = (const float*)w + (size_t)o * in;
+            for (i = 0; i < in; i++) acc += x[i] * wr[i];
+        }
+        y[o] = acc;
+    }
+}
+
+/* engine.c:969-973 per token: y = matmul(att_out, W_o), then x += y.
+ * x [B][hidden], att [B][qdim], in place on x. */
+void yo_o_proj(float* x, const float* att, const void* w, int w_f16, uint32_t B, uint32_t hidden, uint32_t qdim)
+{
+    float* y = (float*)malloc((size_t)hidden * sizeof(float));
+    uint32_t b, j;
+    if (!y) return;
+    for (b = 0; b < B; b++) {
+        yo_matmul(y, att + (size_t)b * qdim, w, w_f16, hidden, qdim);
+        for (j = 0; j < hidden; j++) x[(size_t)b * hidden + j] += y[j];
+    }
+    free(y);
+}

@@ -56,6 +56,8 @@ class Oracle:
         L.yo_conv_silu_sequence.argtypes = [FP, FP, FP, c_uint32, c_uint32, c_uint32]
         L.yo_rmsnorm_gated.argtypes = [FP, FP, ctypes.c_void_p, ctypes.c_int, FP, c_uint32, c_float]
         L.yo_rope.argtypes = [FP, c_uint32, c_uint32, c_float, c_int, c_uint32]
+        L.yo_matmul.argtypes = [FP, FP, ctypes.c_void_p, c_int, c_uint32, c_uint32]
+        L.yo_o_proj.argtypes = [FP, FP, ctypes.c_void_p, c_int, c_uint32, c_uint32, c_uint32]
         L.yo_rope_kv_store.argtypes = [FP, FP, FP, HP, HP, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, c_int,
                                        c_uint32, c_float]
         L.yo_gdn_state_update.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32]
@@ -196,6 +198,28 @@ def _oracle_rope_kv_store(self, q, k, v, pos_start, n_heads, n_kv, d, theta, kin
     return q, kc[pos_start:], vc[pos_start:]
 
 
+def _oracle_matmul(self, x, w):
+    """yo_matmul of one row x [in] with w [out][in] (f32, or f16 bits as uint16)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w)
+    y = np.empty(w.shape[0], np.float32)
+    self.L.yo_matmul(fp(y), fp(x), w.ctypes.data_as(ctypes.c_void_p), int(w.dtype == np.uint16), w.shape[0],
+                     w.shape[1])
+    return y
+
+
+def _oracle_o_proj(self, x, att, w):
+    """yo_o_proj: x [B][hidden] + matmul(att [B][qdim], w [hidden][qdim]) per row (new array)."""
+    x = np.array(x, np.float32, order="C", copy=True)
+    att = np.ascontiguousarray(att, np.float32)
+    w = np.ascontiguousarray(w)
+    self.L.yo_o_proj(fp(x), fp(att), w.ctypes.data_as(ctypes.c_void_p), int(w.dtype == np.uint16), x.shape[0],
+                     w.shape[0], w.shape[1])
+    return x
+
+
+Oracle.matmul = _oracle_matmul
+Oracle.o_proj = _oracle_o_proj
 Oracle.rope = _oracle_rope
 Oracle.rope_kv_store = _oracle_rope_kv_store
 Oracle.conv = _oracle_conv
@@ -220,6 +244,7 @@ class Ref:
         L.gdn_state_update.argtypes = [FP, FP, FP, FP, FP, FP, FP, c_uint32, c_uint32, c_uint32, c_uint32]
         L.conv1d_update.argtypes = [FP, FP, ctypes.c_void_p, c_uint32, c_uint32]
         L.rmsnorm_gated.argtypes = [FP, FP, ctypes.c_void_p, FP, c_uint32, c_float, c_uint32]
+        L.matmul.argtypes = [FP, FP, ctypes.c_void_p, c_uint32, c_uint32, c_uint32]
         L.rope_inplace.argtypes = [FP, c_uint32, c_uint32, c_float]
         L.rope_inplace_qwen.argtypes = [FP, c_uint32, c_uint32, c_float]
         L.rope_inplace_mrope.argtypes = [FP, c_uint32, c_uint32, c_uint32, c_float]
@@ -270,6 +295,15 @@ class Ref:
                2: lambda h, p: L.rope_inplace_qwen(fp(h), d, p, theta),
                3: lambda h, p: L.rope_inplace_mrope(fp(h), d, n_rot, p, theta)}
         return _rope_rows(fns[kind], x, pos, d)
+
+    def matmul(self, x, w):
+        """The reference's matmul (matvec.c:785): DT_F32 for f32 w, DT_F16 for f16 bits."""
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w)
+        y = np.empty(w.shape[0], np.float32)
+        self.L.matmul(fp(y), fp(x), w.ctypes.data_as(ctypes.c_void_p), w.shape[0], w.shape[1],
+                      0 if w.dtype == np.uint16 else 1)  # DT_F16 = 0, DT_F32 = 1 (llf.h:14-15)
+        return y
 
     def f32_to_f16(self, x):
         x = np.ascontiguousarray(x, dtype=np.float32)

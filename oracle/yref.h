@@ -118,6 +118,14 @@ void yo_rope(float* v, uint32_t d, uint32_t pos, float theta, int kind, uint32_t
  * n_heads q heads and n_kv k heads (q [B][n_heads*d], k [B][n_kv*d] in
  * place), then k and v [B][n_kv*d] rounded (yo_f32_to_f16) into the
  * engine-layout caches at row pos (kcache, vcache [rows][n_kv*d]). */
+/* matvec.c:98-122 (matmul_f32 / matmul_f16): y[o] = sum_i x[i] * w[o*in + i],
+ * summed in i order from 0; w f32 (w_f16 == 0) or f16 bits, rows of `in`. */
+void yo_matmul(float* y, const float* x, const void* w, int w_f16, uint32_t out, uint32_t in);
+
+/* engine.c:969-973 for B tokens: x[b] += matmul(att[b], W_o) (hidden outputs
+ * of qdim inputs); x [B][hidden] updated in place. */
+void yo_o_proj(float* x, const float* att, const void* w, int w_f16, uint32_t B, uint32_t hidden, uint32_t qdim);
+
 void yo_rope_kv_store(float* q, float* k, const float* v, uint16_t* kcache, uint16_t* vcache, uint32_t pos_start,
                       uint32_t B, uint32_t n_heads, uint32_t n_kv, uint32_t d, int kind, uint32_t n_rot,
                       float theta);

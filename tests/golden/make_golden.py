@@ -3,7 +3,7 @@ sources (oracle/_ref/libyref.so, `make -C oracle ref`).
 
 Every expected value in the fixture is produced by the reference's compiled
 code: its f32/f16/bf16 conversions (platform.c), softmax / l2norm /
-gdn_state_update / rope_inplace* (matvec.c), yrng (platform.c), and the attention loops that
+gdn_state_update / rope_inplace* / matmul (matvec.c), yrng (platform.c), and the attention loops that
 are inline in its per-layer forward (engine.c:1074-1096 decode, 532-563
 batched prefill, 935-960 gated attention, 788-793 GDN gates), which
 oracle/ref_driver.c runs on a synthetic one-block model.  Inputs that are
@@ -195,6 +195,15 @@ def main() -> None:
         fx[f"{name}_theta"] = np.float32([theta])
         fx[f"{name}_pos"] = pos
         fx[f"{name}_out"] = ref.rope(x, pos, d, np.float32(theta), kind, n_rot)
+
+    # ---- o_proj matmul: matmul_f16 / matmul_f32, matvec.c:98-122 (dispatch 785-795) ----
+    for name, out, inn, f16, seed in (("mm_f16", 96, 256, True, 7001), ("mm_f32", 40, 128, False, 7002)):
+        x = uniform_pm1(seed, 3 * inn, 2.0).reshape(3, inn)
+        w = uniform_pm1(seed + 100, out * inn, 0.5).reshape(out, inn)
+        if f16:
+            w = ref.f32_to_f16(w)
+        fx[f"{name}_meta"] = np.array([out, inn, int(f16), seed], np.int64)
+        fx[f"{name}_y"] = np.stack([ref.matmul(row, w) for row in x])
 
     np.savez_compressed(OUT, **fx)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(fx)} arrays)")

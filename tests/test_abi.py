@@ -199,3 +199,25 @@ def test_rope_kv_store_rejects_bad_args(hiplib):
     # no q (q_out NULL) skips the q checks; B = 0 is a no-op
     assert call(q_out=None, q=None, qs=0, qos=0, B=0) == 0
     assert call(B=0, rope=3, n_rot=64) == 0
+
+
+def test_o_proj_rejects_bad_args(hiplib):
+    def call(x=P, xs=4096, att=P, adt=1, ats=4096, w=P, wdt=0, B=1, hidden=4096, qdim=4096, ws=None, wsb=0):
+        return hiplib.yhip_o_proj(x, xs, att, adt, ats, w, wdt, B, hidden, qdim, ws, wsb, None)
+
+    assert call(wdt=2) == -22 and "w_dtype" in _err(hiplib)      # bf16 slots: the reference reads them as f16
+    assert call(adt=0, wdt=1) == -22 and "att_dtype" in _err(hiplib)  # f16 att needs f16 weights
+    assert call(adt=2) == -22 and "att_dtype" in _err(hiplib)
+    assert call(qdim=900) == -22 and "multiple of 8" in _err(hiplib)
+    assert call(xs=4000) == -22 and "strides" in _err(hiplib)
+    assert call(ats=4100) == -22 and "strides" in _err(hiplib)
+    assert call(w=ctypes.c_void_p(0x1008)) == -22 and "aligned" in _err(hiplib)
+    assert call(att=None) == -22 and "null" in _err(hiplib)
+    # up to 8 tokens need no workspace; more need the hipBLASLt workspace (+ f16 hi/lo rows)
+    assert hiplib.yhip_o_proj_workspace(8, 4096, 0, 1) == 0
+    need16 = hiplib.yhip_o_proj_workspace(64, 4096, 0, 1)
+    need32 = hiplib.yhip_o_proj_workspace(64, 4096, 1, 1)
+    assert need16 == need32 + 2 * 64 * 4096 * 2 and need32 >= 1 << 20
+    assert hiplib.yhip_o_proj_workspace(64, 4096, 0, 0) == need32  # f16 att: one GEMM, no hi/lo rows
+    assert call(B=64, ws=P, wsb=need16 - 1) == -28 and "workspace" in _err(hiplib)
+    assert call(B=0) == 0

@@ -498,3 +498,53 @@ def test_rope_kv_store_loop_gqa_rows(oracle):
     assert np.array_equal(bits(qr), bits(oracle.rope(q, pos, d, np.float32(1e4), 2)))
     assert np.array_equal(kc, oracle.f32_to_f16(oracle.rope(k, pos, d, np.float32(1e4), 2)))
     assert np.array_equal(vc, oracle.f32_to_f16(v))
+
+
+# ---------------------------------------------------------------- o_proj
+
+def _mm_case(golden, name):
+    out, inn, f16, seed = (int(v) for v in golden[f"{name}_meta"])
+    x = uniform_pm1(seed, 3 * inn, 2.0).reshape(3, inn)
+    w = uniform_pm1(seed + 100, out * inn, 0.5).reshape(out, inn)
+    return x, w, bool(f16)
+
+
+@pytest.mark.parametrize("name", ["mm_f16", "mm_f32"])
+def test_matmul_golden(oracle, golden, name):
+    x, w, f16 = _mm_case(golden, name)
+    if f16:
+        w = oracle.f32_to_f16(w)
+    got = np.stack([oracle.matmul(row, w) for row in x])
+    assert np.array_equal(bits(got), bits(golden[f"{name}_y"]))
+
+
+@pytest.mark.parametrize("out,inn,f16", [(64, 896, True), (33, 4096, False), (128, 128, True)])
+def test_matmul_vs_reference_live(oracle, ref, out, inn, f16):
+    x = uniform_pm1(161, inn, 3.0)
+    w = uniform_pm1(162, out * inn).reshape(out, inn)
+    if f16:
+        w = oracle.f32_to_f16(w)
+    assert np.array_equal(bits(oracle.matmul(x, w)), bits(ref.matmul(x, w)))
+
+
+def test_matmul_and_o_proj_closed_forms(oracle):
+    n = 64
+    x = uniform_pm1(171, 2 * n).reshape(2, n)
+    # identity weights give x back exactly, f32 or f16 (1.0 is exact in f16)
+    eye = np.eye(n, dtype=np.float32)
+    for w in (eye, oracle.f32_to_f16(eye)):
+        assert np.array_equal(bits(oracle.matmul(x[0], w)), bits(x[0]))
+    # a permutation matrix permutes; a row of twos doubles one element exactly
+    perm = np.random.default_rng(5).permutation(n)
+    assert np.array_equal(bits(oracle.matmul(x[0], eye[perm])), bits(x[0][perm]))
+    # fp64 against a textbook product, f16 weights decoded exactly
+    w16 = oracle.f32_to_f16(uniform_pm1(172, 48 * n).reshape(48, n))
+    wd = w16.view(np.float16).astype(np.float64)
+    y = oracle.matmul(x[1], w16)
+    assert np.allclose(y, wd @ x[1].astype(np.float64), rtol=1e-5, atol=1e-5)
+    # o_proj = residual + matmul per token, rows independent
+    res = uniform_pm1(173, 2 * 48).reshape(2, 48)
+    got = oracle.o_proj(res, x, w16)
+    want = res.astype(np.float64) + x.astype(np.float64) @ wd.T
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-5)
+    assert np.array_equal(bits(got[1]), bits((res[1] + oracle.matmul(x[1], w16)).astype(np.float32)))

@@ -149,6 +149,36 @@ def rope_kv_store(cache: LayerKV, q: torch.Tensor | None, k: torch.Tensor, v: to
     return q_out if q is not None else None
 
 
+def o_proj_workspace_bytes(B: int, qdim: int, w_dtype: torch.dtype, att_dtype: torch.dtype = torch.float32) -> int:
+    return int(lib().yhip_o_proj_workspace(B, qdim, _DT[w_dtype], _DT[att_dtype]))
+
+
+def o_proj(x: torch.Tensor, att: torch.Tensor, w: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """x[b] += w . att[b] in place (engine.c:969-973: matmul(att_out, SLOT_O) and
+    the residual add).  x [B, hidden] f32, att [B, qdim] f32, w [hidden, qdim]
+    f16 or f32 (att f16 with f16 weights); rows of x and att may be strided.
+    Returns x."""
+    for t in (x, att, w):
+        if not t.is_cuda:
+            raise YhipError(-22, "tensor must be on the GPU")
+    if x.dim() == 1:
+        x, att = x.unsqueeze(0), att.unsqueeze(0)
+    if x.dtype != torch.float32 or att.dtype not in (torch.float32, torch.float16) or x.stride(1) != 1 \
+            or att.stride(1) != 1:
+        raise YhipError(-22, "o_proj: x (f32) and att (f32 / f16) must be rows with unit column stride")
+    if not w.is_contiguous() or w.dim() != 2 or w.shape[1] != att.shape[1] or w.shape[0] != x.shape[1]:
+        raise YhipError(-22, f"o_proj: w {tuple(w.shape)} does not match att {tuple(att.shape)} / x {tuple(x.shape)}")
+    B, hidden, qdim = x.shape[0], w.shape[0], w.shape[1]
+    need = o_proj_workspace_bytes(B, qdim, w.dtype, att.dtype)
+    ws = _workspace(need, x.device, workspace)
+    xs = x.stride(0) if B > 1 else hidden
+    ats = att.stride(0) if B > 1 else qdim
+    check(lib().yhip_o_proj(_ptr(x), xs, _ptr(att), _dtype_code(att), ats, _ptr(w), _dtype_code(w), B, hidden,
+                            qdim, _ptr(ws),
+                            ws.numel() * ws.element_size() if ws is not None else 0, _stream()))
+    return x
+
+
 def kv_from_engine(cache: LayerKV, eng_k: torch.Tensor, eng_v: torch.Tensor) -> None:
     """Fill rows 0..n-1 from engine-layout f16 rows [n, n_kv*head_dim] (yllm.h:109)."""
     _need_gpu(eng_k, eng_v)

@@ -365,6 +365,52 @@ int yhip_rope_kv_store(void* q_out, uint32_t q_out_dtype, uint32_t q_out_stride,
     return done(yhip::launch_rope_kv(a, (hipStream_t)stream), fn);
 }
 
+size_t yhip_o_proj_workspace(uint32_t B, uint32_t qdim, uint32_t w_dtype, uint32_t att_dtype)
+{
+    return yhip::oproj_workspace(B, qdim, w_dtype == YHIP_F16, att_dtype == YHIP_F16);
+}
+
+int yhip_o_proj(float* x, uint32_t x_stride, const void* att, uint32_t att_dtype, uint32_t att_stride,
+                const void* w, uint32_t w_dtype, uint32_t B, uint32_t hidden, uint32_t qdim, void* workspace,
+                size_t workspace_bytes, void* stream)
+{
+    const char* fn = "yhip_o_proj";
+    if (!x || !att || !w) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    if (w_dtype != YHIP_F16 && w_dtype != YHIP_F32)
+        return fail(YHIP_EINVAL, "%s: w_dtype must be YHIP_F16 or YHIP_F32", fn);
+    if (att_dtype != YHIP_F32 && !(att_dtype == YHIP_F16 && w_dtype == YHIP_F16))
+        return fail(YHIP_EINVAL, "%s: att_dtype must be YHIP_F32, or YHIP_F16 with f16 weights", fn);
+    if (hidden == 0 || qdim == 0 || qdim % 8) return fail(YHIP_EINVAL, "%s: qdim %u must be a positive multiple of 8", fn, qdim);
+    if (x_stride < hidden || att_stride < qdim || att_stride % 8)
+        return fail(YHIP_EINVAL, "%s: strides must cover the rows (att_stride a multiple of 8)", fn);
+    if ((uintptr_t)w % 16 || (uintptr_t)att % 16 || (uintptr_t)x % 4)
+        return fail(YHIP_EINVAL, "%s: w and att must be 16-byte aligned", fn);
+    if ((uint64_t)B * qdim > 0x7fffffffull || (uint64_t)hidden * qdim > 0xffffffffull)
+        return fail(YHIP_EINVAL, "%s: too many elements", fn);
+    if (B == 0) return done(hipSuccess, "");
+    const size_t need = yhip::oproj_workspace(B, qdim, w_dtype == YHIP_F16, att_dtype == YHIP_F16);
+    if (need && (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256))
+        return fail(YHIP_ENOSPC, "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", fn, need,
+                    workspace_bytes);
+    if (need && ((const char*)workspace < (const char*)x + (size_t)B * x_stride * 4 &&
+                 (const char*)x < (const char*)workspace + need))
+        return fail(YHIP_EINVAL, "%s: workspace overlaps x", fn);
+    yhip::OProjArgs a = {};
+    a.x = x;
+    a.att = att;
+    a.w = w;
+    a.x_stride = x_stride;
+    a.att_stride = att_stride;
+    a.B = B;
+    a.hidden = hidden;
+    a.qdim = qdim;
+    a.w_f16 = w_dtype == YHIP_F16;
+    a.att_f16 = att_dtype == YHIP_F16;
+    const char* msg = yhip::launch_oproj(a, workspace, workspace_bytes, (hipStream_t)stream);
+    if (msg) return fail(YHIP_EDEVICE, "%s: %s", fn, msg);
+    return done(hipSuccess, "");
+}
+
 int yhip_gdn_conv(float* out, uint32_t out_stride, const float* x, uint32_t x_stride, float* conv_state,
                   const float* conv_w, uint32_t T, uint32_t dim, uint32_t kwidth, int silu, void* stream)
 {
