@@ -461,7 +461,7 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
 
     from yllm_amd.attention import (ROPE_MROPE, LayerKV, attn_decode, attn_prefill, decode_workspace,
                                     decode_workspace_bytes, rope_kv_store)
-    from yllm_amd.gdn import gdn_chunk, gdn_chunk_workspace_bytes, gdn_conv, gdn_gated_norm, gdn_gates, gdn_step
+    from yllm_amd.gdn import gdn_chunk, gdn_chunk_workspace_bytes, gdn_conv, gdn_decode, gdn_gated_norm, gdn_gates
 
     dev = torch.device("cuda:0")
     seed = SEED + 5
@@ -489,6 +489,7 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
     a = -torch.ones(hg, device=dev)
     S = [torch.zeros((hg, dg, dg), device=dev) for _ in range(n_gdn)]
     cst = [torch.zeros((kw, conv), device=dev) for _ in range(n_gdn)]
+    cst2 = [torch.zeros((kw, conv), device=dev) for _ in range(n_gdn)]
     beta = [torch.empty((L, hg), device=dev) for _ in range(n_gdn)]
     gate = [torch.empty((L, hg), device=dev) for _ in range(n_gdn)]
     xc = torch.empty((L, conv), device=dev)           # conv + silu rows: q | k | v
@@ -514,17 +515,19 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
         gdn_gated_norm(gout[:T], g["z"][:T], g["norm_w"], hg, out=gout[:T])
 
     def gdn_layer_step(li, t):
+        # two launches per layer and token; the delay line alternates between
+        # cst and cst2 (an even number of decode tokens ends back in cst)
         g = gd[li]
-        gdn_conv(g["qkv"][t:t + 1], cst[li], g["conv_w"], out=xc[t:t + 1])
-        gdn_step(S[li], xc[t, :kd], xc[t, kd:2 * kd], xc[t, 2 * kd:], gate[li][t], beta[li][t], hg, out=gout[t])
-        gdn_gated_norm(gout[t:t + 1], g["z"][t:t + 1], g["norm_w"], hg, out=gout[t:t + 1])
+        c_in, c_out = (cst[li], cst2[li]) if (t - T) % 2 == 0 else (cst2[li], cst[li])
+        gdn_decode(S[li], c_in, c_out, g["qkv"][t], g["z"][t], g["alpha"][t], g["beta_raw"][t], g["conv_w"], dt, a,
+                   g["norm_w"], hg, y=gout[t])
 
     def step(i):
         for li in range(n_gdn):
             S[li].zero_()
             cst[li].zero_()
-            beta[li].copy_(gd[li]["beta_raw"])
-            gdn_gates(gd[li]["alpha"], beta[li], dt, a, gate=gate[li])
+            beta[li][:T].copy_(gd[li]["beta_raw"][:T])
+            gdn_gates(gd[li]["alpha"][:T], beta[li][:T], dt, a, gate=gate[li][:T])
         # prefill
         for li in range(n_gdn):
             gdn_layer_prefill(li)
@@ -545,7 +548,7 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
                                f"1 gated attention layer ({nh}/{nkv} heads, d {da}: M-RoPE over 64 dims + KV "
                                f"store from fp32 q/k/v rows, bf16 prefill queries, sigmoid gate); "
                                f"{T}-token prefill (chunked GDN, MFMA attention) then {n_dec} decode steps "
-                               f"(GDN steps, RoPE + KV store, split-K decode) per step; N(0,1)*0.5 seed "
+                               f"(fused GDN token per layer (2 launches), RoPE + KV store, split-K decode) per step; N(0,1)*0.5 seed "
                                f"{hex(seed)}",
                    "prefill_tokens": T, "decode_steps": n_dec},
         "roofline": None,

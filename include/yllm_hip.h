@@ -220,6 +220,25 @@ int yhip_gdn_chunk(float* S, float* out, uint32_t out_stride, const float* q, co
 /* Workspace bytes of the chunked form for T tokens (0 when T < 64). */
 size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_dim);
 
+/* One decode token of a Gated DeltaNet layer in two launches (engine.c:786-847
+ * after the projections): the gates of alpha / beta_raw (788-793),
+ * conv1d_update + silu of the projected row qkv (805-812, the conv bit for bit
+ * the reference's), l2norm of q and k with l2_eps (826-827), the state update
+ * (gdn_state_update, matvec.c:975-1004) and rmsnorm_gated of each v head with
+ * z, norm_w and norm_eps (845-847) into y.  qkv is [2*n_k*head_dim +
+ * n_v*head_dim] (q | k | v), z and y [n_v*head_dim], alpha, beta_raw,
+ * dt_bias, ssm_a [n_v]; conv_w [conv_dim][kwidth] f32; norm_w [head_dim]
+ * YHIP_F32 or YHIP_F16.  The delay line [kwidth][conv_dim] (row kwidth-1 the
+ * newest input, as yhip_gdn_conv keeps it) is read from conv_in and written
+ * to conv_out, which must not overlap it: swap the two every token.  S as
+ * for yhip_gdn_step (updated in place, 16-byte aligned).  head_dim 64 or 128,
+ * n_v_heads >= n_k_heads, kwidth 1..8. */
+int yhip_gdn_decode(float* S, const float* conv_in, float* conv_out, float* y, const float* qkv, const float* z,
+                    const float* alpha, const float* beta_raw, const float* conv_w, const float* dt_bias,
+                    const float* ssm_a, const void* norm_w, uint32_t norm_w_dtype, uint32_t n_k_heads,
+                    uint32_t n_v_heads, uint32_t head_dim, uint32_t kwidth, float l2_eps, float norm_eps,
+                    void* stream);
+
 /* The GDN gates of T tokens (engine.c:788-793), in place like the engine:
  * beta[t][h] <- 1/(1+exp(-beta[t][h])), gate[t][h] <- log1p(exp(alpha[t][h]
  * + dt_bias[h])) * ssm_a[h]. */

@@ -221,3 +221,20 @@ def test_o_proj_rejects_bad_args(hiplib):
     assert hiplib.yhip_o_proj_workspace(64, 4096, 0, 0) == need32  # f16 att: one GEMM, no hi/lo rows
     assert call(B=64, ws=P, wsb=need16 - 1) == -28 and "workspace" in _err(hiplib)
     assert call(B=0) == 0
+
+
+def test_gdn_decode_rejects_bad_args(hiplib):
+    F = ctypes.c_float
+    A, B = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x900000)  # delay lines, never dereferenced
+
+    def call(S=P, cin=A, cout=B, nk=16, nv=16, d=128, kw=4, ndt=1):
+        return hiplib.yhip_gdn_decode(S, cin, cout, P, P, P, P, P, P, P, P, P, ndt, nk, nv, d, kw, F(1e-6), F(1e-6),
+                                      None)
+
+    assert call(d=256) == -22 and "head_dim" in _err(hiplib)
+    assert call(nk=4, nv=2) == -22 and "n_k_heads" in _err(hiplib)
+    assert call(kw=9) == -22 and "kwidth" in _err(hiplib)
+    assert call(ndt=2) == -22 and "dtype" in _err(hiplib)
+    assert call(S=ctypes.c_void_p(0x1004)) == -22 and "aligned" in _err(hiplib)
+    assert call(cout=ctypes.c_void_p(0x100000 + 64)) == -22 and "overlaps" in _err(hiplib)
+    assert call(cin=None) == -22 and "null" in _err(hiplib)

@@ -229,3 +229,100 @@ def test_gdn_gated_norm_matches_oracle(cuda, oracle, T, n_heads, hd, w_f16):
     # in place, as the engine applies it
     gdn_gated_norm(xd, zd, wd, n_heads, out=xd)
     assert np.allclose(xd.cpu().numpy(), want, rtol=3e-6, atol=1e-7)
+
+
+# ------------------------------------------------------- fused decode token
+
+def _layer_inputs(seed, T, n_k, n_v, d, kw, w_f16, oracle):
+    conv_dim = (2 * n_k + n_v) * d
+    qkv = gen(seed, T * conv_dim, 1.0).reshape(T, conv_dim)
+    z = gen(seed + 1, T * n_v * d, 1.0).reshape(T, n_v * d)
+    alpha = gen(seed + 2, T * n_v, 1.0).reshape(T, n_v)
+    beta_raw = gen(seed + 3, T * n_v, 1.0).reshape(T, n_v)
+    conv_w = gen(seed + 4, conv_dim * kw, 0.5).reshape(conv_dim, kw)
+    dt = gen(seed + 5, n_v, 0.5)
+    a = -np.abs(gen(seed + 6, n_v, 1.0)) - 0.1
+    norm_w = (gen(seed + 7, d, 0.1) + 1.0).astype(np.float32)
+    if w_f16:
+        norm_w = oracle.f32_to_f16(norm_w)
+    st0 = gen(seed + 8, kw * conv_dim, 1.0).reshape(kw, conv_dim)
+    S0 = gen(seed + 9, n_v * d * d, 0.05).reshape(n_v, d, d)
+    return qkv, z, alpha, beta_raw, conv_w, dt, a, norm_w, st0, S0
+
+
+def _oracle_layer(oracle, S, st, qkv, z, alpha, beta_raw, conv_w, dt, a, norm_w, n_k, n_v, d, kw):
+    """engine.c:786-847 token by token from the pinned oracle pieces."""
+    ys = []
+    for t in range(qkv.shape[0]):
+        st, rows = oracle.conv_silu(st, qkv[t][None], conv_w, kw)
+        beta, gate = oracle.gdn_gates(alpha[t], beta_raw[t], dt, a)
+        r = rows[0]
+        S, out, _, _ = oracle.gdn_sequence(S, r[:n_k * d], r[n_k * d:2 * n_k * d], r[2 * n_k * d:], gate, beta, 1,
+                                           n_k, d, n_v, d, EPS)
+        ys.append(oracle.rmsnorm_gated(out.reshape(n_v, d), norm_w, z[t].reshape(n_v, d), np.float32(EPS)).ravel())
+    return S, st, np.stack(ys)
+
+
+@pytest.mark.parametrize("n_k,n_v,d,kw,w_f16", [
+    (16, 16, 128, 4, False),  # the fifth configuration's GDN layer
+    (2, 4, 64, 4, True),
+    (4, 8, 128, 3, False),
+    (1, 3, 64, 1, False),
+])
+def test_gdn_decode_matches_oracle(cuda, oracle, n_k, n_v, d, kw, w_f16):
+    from yllm_amd.gdn import gdn_decode
+
+    T = 5
+    qkv, z, alpha, beta_raw, conv_w, dt, a, norm_w, st0, S0 = _layer_inputs(3100 + d + kw, T, n_k, n_v, d, kw,
+                                                                             w_f16, oracle)
+    S_want, st_want, y_want = _oracle_layer(oracle, S0, st0, qkv, z, alpha, beta_raw, conv_w, dt, a, norm_w, n_k,
+                                            n_v, d, kw)
+    S, st_a, st_b, qkv_t, z_t, al, br, cw, dtt, at = to_dev(cuda, S0, st0, np.zeros_like(st0), qkv, z, alpha,
+                                                             beta_raw, conv_w, dt, a)
+    nw = torch.from_numpy(norm_w).to(cuda)
+    nw = nw.view(torch.float16) if w_f16 else nw
+    ys = []
+    for t in range(T):
+        ys.append(gdn_decode(S, st_a, st_b, qkv_t[t], z_t[t], al[t], br[t], cw, dtt, at, nw, n_k).cpu().numpy())
+        st_a, st_b = st_b, st_a
+    y = np.stack(ys)
+    err_y = max(rel_l2(y[t], y_want[t]) for t in range(T))
+    err_s = rel_l2(S.cpu().numpy(), S_want)
+    print(f"gdn_decode n_k={n_k} n_v={n_v} d={d} kw={kw}: y max rel_l2 {err_y:.2e}, state {err_s:.2e}")
+    assert err_y <= 1e-5 and err_s <= 1e-5
+    # the delay line holds the inputs themselves: bit for bit
+    assert np.array_equal(st_a.cpu().numpy().view(np.uint32), st_want.view(np.uint32))
+
+
+def test_gdn_prefill_then_decode_tokens(cuda, oracle):
+    """A 70-token prefill through gdn_conv + gdn_gates + gdn_chunk (chunked) +
+    gdn_gated_norm, then 4 decode tokens through gdn_decode: the delay line
+    and the state hand over between the two paths (the oracle runs all 74
+    tokens one by one)."""
+    from yllm_amd.gdn import (gdn_chunk, gdn_chunk_workspace_bytes, gdn_conv, gdn_decode, gdn_gated_norm,
+                              gdn_gates)
+
+    n_k, n_v, d, kw, T0, T1 = 4, 8, 128, 4, 70, 4
+    T = T0 + T1
+    qkv, z, alpha, beta_raw, conv_w, dt, a, norm_w, st0, S0 = _layer_inputs(3300, T, n_k, n_v, d, kw, False, oracle)
+    S_want, _, y_want = _oracle_layer(oracle, S0, st0, qkv, z, alpha, beta_raw, conv_w, dt, a, norm_w, n_k, n_v, d,
+                                      kw)
+    S, st_a, st_b, qkv_t, z_t, al, br, cw, dtt, at, nw = to_dev(cuda, S0, st0, np.zeros_like(st0), qkv, z, alpha,
+                                                                 beta_raw, conv_w, dt, a, norm_w)
+    kd = n_k * d
+    xc = gdn_conv(qkv_t[:T0], st_a, cw)
+    beta = br[:T0].clone()
+    gate = torch.empty_like(beta)
+    gdn_gates(al[:T0], beta, dtt, at, gate=gate)
+    ws = torch.empty(gdn_chunk_workspace_bytes(T0, n_v, d) // 4, device=cuda)
+    out = gdn_chunk(S, xc[:, :kd], xc[:, kd:2 * kd], xc[:, 2 * kd:], gate, beta, n_k, workspace=ws)
+    y_pre = gdn_gated_norm(out, z_t[:T0], nw, n_v).cpu().numpy()
+    ys = []
+    for t in range(T0, T):
+        ys.append(gdn_decode(S, st_a, st_b, qkv_t[t], z_t[t], al[t], br[t], cw, dtt, at, nw, n_k).cpu().numpy())
+        st_a, st_b = st_b, st_a
+    err_pre = rel_l2(y_pre, y_want[:T0])
+    err_dec = max(rel_l2(ys[i], y_want[T0 + i]) for i in range(T1))
+    err_s = rel_l2(S.cpu().numpy(), S_want)
+    print(f"prefill {T0} + decode {T1}: prefill y {err_pre:.2e}, decode y {err_dec:.2e}, state {err_s:.2e}")
+    assert err_pre <= TOL and err_dec <= TOL and err_s <= TOL

@@ -411,6 +411,51 @@ int yhip_o_proj(float* x, uint32_t x_stride, const void* att, uint32_t att_dtype
     return done(hipSuccess, "");
 }
 
+int yhip_gdn_decode(float* S, const float* conv_in, float* conv_out, float* y, const float* qkv, const float* z,
+                    const float* alpha, const float* beta_raw, const float* conv_w, const float* dt_bias,
+                    const float* ssm_a, const void* norm_w, uint32_t norm_w_dtype, uint32_t n_k_heads,
+                    uint32_t n_v_heads, uint32_t head_dim, uint32_t kwidth, float l2_eps, float norm_eps,
+                    void* stream)
+{
+    const char* fn = "yhip_gdn_decode";
+    if (!S || !conv_in || !conv_out || !y || !qkv || !z || !alpha || !beta_raw || !conv_w || !dt_bias || !ssm_a ||
+        !norm_w)
+        return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    if (head_dim != 64 && head_dim != 128) return fail(YHIP_EINVAL, "%s: head_dim %u not 64 or 128", fn, head_dim);
+    if (n_k_heads == 0 || n_v_heads < n_k_heads)
+        return fail(YHIP_EINVAL, "%s: need 1 <= n_k_heads (%u) <= n_v_heads (%u)", fn, n_k_heads, n_v_heads);
+    if (kwidth < 1 || kwidth > 8) return fail(YHIP_EINVAL, "%s: kwidth %u not in 1..8", fn, kwidth);
+    if (norm_w_dtype != YHIP_F32 && norm_w_dtype != YHIP_F16) return fail(YHIP_EINVAL, "%s: bad norm_w dtype", fn);
+    if ((uintptr_t)S % 16) return fail(YHIP_EINVAL, "%s: S must be 16-byte aligned", fn);
+    const uint64_t conv_dim = (uint64_t)(2 * n_k_heads + n_v_heads) * head_dim;
+    if (conv_dim * kwidth > 0x7fffffffull) return fail(YHIP_EINVAL, "%s: too many channels", fn);
+    const size_t line = (size_t)conv_dim * kwidth * sizeof(float);
+    if ((const char*)conv_out < (const char*)conv_in + line && (const char*)conv_in < (const char*)conv_out + line)
+        return fail(YHIP_EINVAL, "%s: conv_out overlaps conv_in", fn);
+    yhip::GdnDecodeArgs a = {};
+    a.S = S;
+    a.conv_in = conv_in;
+    a.conv_out = conv_out;
+    a.qkv = qkv;
+    a.z = z;
+    a.alpha = alpha;
+    a.beta_raw = beta_raw;
+    a.conv_w = conv_w;
+    a.dt_bias = dt_bias;
+    a.ssm_a = ssm_a;
+    a.norm_w = norm_w;
+    a.y = y;
+    a.n_k = n_k_heads;
+    a.n_v = n_v_heads;
+    a.D = head_dim;
+    a.kwidth = kwidth;
+    a.conv_dim = (uint32_t)conv_dim;
+    a.norm_w_f16 = norm_w_dtype == YHIP_F16;
+    a.l2_eps = l2_eps;
+    a.norm_eps = norm_eps;
+    return done(yhip::launch_gdn_decode(a, (hipStream_t)stream), fn);
+}
+
 int yhip_gdn_conv(float* out, uint32_t out_stride, const float* x, uint32_t x_stride, float* conv_state,
                   const float* conv_w, uint32_t T, uint32_t dim, uint32_t kwidth, int silu, void* stream)
 {

@@ -1,0 +1,204 @@
+// gdn_decode.hip -- one decode token of a Gated DeltaNet layer in two launches
+// (engine.c:786-847 for a single token): the gates (788-793), conv1d +
+// silu over the projected qkv row (805-812, conv1d_update matvec.c:956-968),
+// l2norm of q and k per k head (826-827, matvec.c:942-949), the state update
+// and output (gdn_state_update, matvec.c:975-1004) and the gated RMSNorm of
+// each v head (845-847, rmsnorm_gated matvec.c:1007-1021).
+//
+// Two launches.  gdn_decode_kernel: a workgroup (256 threads) owns 16 state
+// columns of v head h (D/16 workgroups per head, as gdn_step_kernel), which
+// reads k head kh = h % n_k:
+//  1. every thread issues its loads at once: its slice of the state, one q
+//     and one k channel of head kh (conv weights and delay line), and for 16
+//     threads one of the workgroup's v channels;
+//  2. conv + silu of those channels (products and sums rounded separately
+//     in the reference's order, so the conv is bit for bit the
+//     reference's), the gates, the l2norm of q and k through LDS (every
+//     workgroup of the head computes the whole q and k head, 2 D channels);
+//  3. the state update of its 16 columns by 16 threads each (decay, delta
+//     rule, output) and the raw outputs into y.
+// Then the gated RMSNorm kernel (gdn_conv.hip) normalises each head of y in
+// place: its sum over the head's D outputs spans the head's workgroups.
+// The delay line is read from conv_in and written to conv_out (separate
+// buffers, swapped by the caller every token), so no workgroup can read a
+// row that another one has already replaced.  q/k channels of head kh are
+// written by the workgroups of v head kh (n_v >= n_k, so it exists), 16 per
+// workgroup; v channels by the workgroup that owns them.
+#include "common.hpp"
+#include "internal.hpp"
+
+#include <math.h>
+
+namespace yhip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kCols = 16;  // state columns per workgroup
+constexpr int kMaxKw = 8;
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void gdn_decode_kernel(GdnDecodeArgs a)
+{
+    // separate product and sum roundings in the conv, as the reference
+#pragma clang fp contract(off)
+    constexpr int TPC = kThreads / kCols;  // threads per state column (16)
+    constexpr int SL = D / TPC;            // state elements per thread
+    constexpr uint32_t nblk = D / kCols;   // workgroups per head
+    __shared__ float qs[D], ks[D], vs[kCols];
+    __shared__ float red[2];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t h = blockIdx.x / nblk, blk = blockIdx.x % nblk;
+    const uint32_t kh = h % a.n_k;
+    const uint32_t key_dim = a.n_k * D;
+    const uint32_t col = tid / TPC, part = tid % TPC, j = blk * kCols + col;
+
+    // 1. loads: state slice, then this thread's conv channels
+    float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
+    float s[SL];
+#pragma unroll
+    for (int i = 0; i < SL; i += 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(Sp + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[i + e] = x[e];
+    }
+    // channel c of the 2 D q/k channels (q: c < D, k: c >= D) and, for
+    // tid < kCols, v channel j0 + tid
+    struct Chan {
+        float X[kMaxKw], w[kMaxKw];
+        uint32_t ch;
+    };
+    auto load = [&](Chan& c, uint32_t ch) {
+        c.ch = ch;
+#pragma unroll
+        for (int r = 0; r < kMaxKw; ++r) {
+            if (r >= (int)a.kwidth) break;
+            c.w[r] = a.conv_w[(size_t)ch * a.kwidth + r];
+            c.X[r] = r + 1 < (int)a.kwidth ? a.conv_in[(size_t)(r + 1) * a.conv_dim + ch] : a.qkv[ch];
+        }
+    };
+    auto conv = [&](const Chan& c) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kMaxKw; ++r) {
+            if (r >= (int)a.kwidth) break;
+            acc = acc + c.X[r] * c.w[r];
+        }
+        return acc / (1.0f + expf(-acc));
+    };
+    auto store_line = [&](const Chan& c) {
+#pragma unroll
+        for (int r = 0; r < kMaxKw; ++r) {
+            if (r >= (int)a.kwidth) break;
+            a.conv_out[(size_t)r * a.conv_dim + c.ch] = c.X[r];
+        }
+    };
+    constexpr int QK_PER = 2 * D / kThreads;  // q/k channels per thread (1 at D = 128)
+    Chan cq[QK_PER > 0 ? QK_PER : 1];
+    const bool qk_thread = QK_PER > 0 || tid < 2 * D;
+#pragma unroll
+    for (int u = 0; u < (QK_PER > 0 ? QK_PER : 1); ++u) {
+        const uint32_t c = tid + u * kThreads;  // 0 .. 2D-1
+        if (qk_thread) load(cq[u], c < (uint32_t)D ? kh * D + c : key_dim + kh * D + (c - D));
+    }
+    Chan cv;
+    const bool v_thread = tid < kCols;
+    if (v_thread) load(cv, 2 * key_dim + h * D + blk * kCols + tid);
+
+    // 2. conv + silu; the new delay line row r is X[r]
+#pragma unroll
+    for (int u = 0; u < (QK_PER > 0 ? QK_PER : 1); ++u) {
+        if (!qk_thread) break;
+        const uint32_t c = tid + u * kThreads;
+        const float y = conv(cq[u]);
+        if (c < (uint32_t)D) qs[c] = y;
+        else ks[c - D] = y;
+        // head kh's q/k channels: 16 of them per workgroup of v head kh
+        if (h == kh && (c % D) / kCols == blk) store_line(cq[u]);
+    }
+    if (v_thread) {
+        vs[tid] = conv(cv);
+        store_line(cv);
+    }
+    __syncthreads();
+    // l2 norms: wave 0 sums q^2, wave 1 sums k^2 (the reference sums in order;
+    // this is a tree, equal to rounding)
+    if (wave < 2) {
+        const float* src = wave == 0 ? qs : ks;
+        float ss = 0.0f;
+        for (int i = lane; i < D; i += 64) ss += src[i] * src[i];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        if (lane == 0) red[wave] = 1.0f / fmaxf(sqrtf(ss), a.l2_eps);
+    }
+    __syncthreads();
+    const float rq = red[0], rk = red[1];
+    // gates (engine.c:788-793)
+    const float bt = 1.0f / (1.0f + expf(-a.beta_raw[h]));
+    const float g = expf(log1pf(expf(a.alpha[h] + a.dt_bias[h])) * a.ssm_a[h]);
+
+    // 3. state update of column j (matvec.c:975-1004, as gdn_step_kernel)
+    float k[SL], q[SL];
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+        k[i] = ks[part * SL + i] * rk;
+        q[i] = qs[part * SL + i] * rq;
+    }
+    auto sum_tpc = [](float x) {
+#pragma unroll
+        for (int m = TPC / 2; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+        return x;
+    };
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+        s[i] *= g;
+        p = fmaf(s[i], k[i], p);
+    }
+    const float delta = (vs[col] - sum_tpc(p)) * bt;
+    float p2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+        s[i] = fmaf(k[i], delta, s[i]);
+        p2 = fmaf(s[i], q[i], p2);
+    }
+    const float o = sum_tpc(p2) * (1.0f / sqrtf((float)D));
+#pragma unroll
+    for (int i = 0; i < SL; i += 4) {
+        f32x4 x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = s[i + e];
+        *reinterpret_cast<f32x4*>(Sp + i) = x;
+    }
+    if (part == 0) a.y[(size_t)h * D + j] = o;
+}
+
+}  // namespace
+
+hipError_t launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t st)
+{
+    switch (a.D) {
+    case 64: hipLaunchKernelGGL(gdn_decode_kernel<64>, dim3(a.n_v * (64 / kCols)), dim3(kThreads), 0, st, a); break;
+    case 128:
+        hipLaunchKernelGGL(gdn_decode_kernel<128>, dim3(a.n_v * (128 / kCols)), dim3(kThreads), 0, st, a);
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // gated RMSNorm of each head, in place on y
+    GdnNormArgs n = {};
+    n.y = a.y;
+    n.x = a.y;
+    n.z = a.z;
+    n.w = a.norm_w;
+    n.y_stride = n.x_stride = n.z_stride = a.n_v * a.D;
+    n.T = 1;
+    n.n_heads = a.n_v;
+    n.head_dim = a.D;
+    n.w_f16 = a.norm_w_f16;
+    n.eps = a.norm_eps;
+    return launch_gdn_gated_norm(n, st);
+}
+
+}  // namespace yhip

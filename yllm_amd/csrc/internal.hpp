@@ -112,6 +112,25 @@ struct GdnNormArgs {
 };
 hipError_t launch_gdn_gated_norm(const GdnNormArgs& a, hipStream_t st);
 
+// ---- gdn_decode.hip ----
+struct GdnDecodeArgs {
+    float* S;               // [n_v][D][D] state, updated in place
+    const float* conv_in;   // delay line [kwidth][conv_dim] before the token
+    float* conv_out;        // delay line after the token (not overlapping conv_in)
+    const float* qkv;       // [conv_dim] projected row: q | k | v
+    const float* z;         // [n_v * D]
+    const float* alpha;     // [n_v]
+    const float* beta_raw;  // [n_v]
+    const float* conv_w;    // [conv_dim][kwidth]
+    const float* dt_bias;   // [n_v]
+    const float* ssm_a;     // [n_v]
+    const void* norm_w;     // [D] f32, or f16 when norm_w_f16
+    float* y;               // [n_v * D]
+    uint32_t n_k, n_v, D, kwidth, conv_dim, norm_w_f16;
+    float l2_eps, norm_eps;
+};
+hipError_t launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t st);
+
 // ---- gdn.hip ----
 struct GdnArgs {
     float* S;                        // [n_v][D][D] state, S[h][j][i]

@@ -10,6 +10,8 @@ inference/core/engine.c):
     gdn_conv(x, conv_state, conv_w)             conv1d_update + silu (matvec.c:956-968,
                                                 engine.c:809-812) over T tokens
     gdn_gated_norm(x, z, w, n_heads)            rmsnorm_gated per v-head (matvec.c:1007-1021)
+    gdn_decode(S, conv_in, conv_out, qkv, ...)  one decode token of the layer, all of the above
+                                                in two launches (engine.c:786-847)
 
 S is the fp32 state [n_v, d, d] (S[h, j, :] is column j, the reference's
 transposed storage), updated in place.  Tensors are torch fp32 tensors on the
@@ -168,3 +170,40 @@ def gdn_gated_norm(x: torch.Tensor, z: torch.Tensor, w: torch.Tensor, n_heads: i
                                     F16 if w.dtype == torch.float16 else F32, T, n_heads, head_dim,
                                     float(eps), _stream()))
     return out
+
+
+def gdn_decode(S: torch.Tensor, conv_in: torch.Tensor, conv_out: torch.Tensor, qkv: torch.Tensor, z: torch.Tensor,
+               alpha: torch.Tensor, beta_raw: torch.Tensor, conv_w: torch.Tensor, dt_bias: torch.Tensor,
+               ssm_a: torch.Tensor, norm_w: torch.Tensor, n_k: int, l2_eps: float = L2_EPS,
+               norm_eps: float = L2_EPS, y: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode token of a GDN layer (engine.c:786-847 after the
+    projections): gates, conv1d + silu, l2norm, state update, gated RMSNorm.
+    S [n_v, d, d] updated in place; conv_in -> conv_out the delay line
+    [kwidth, conv_dim] before / after the token (two buffers, swap them each
+    token); qkv [conv_dim] = q | k | v; z [n_v*d]; alpha, beta_raw, dt_bias,
+    ssm_a [n_v]; conv_w [conv_dim, kwidth]; norm_w [d] fp32 or f16.
+    Returns y [n_v*d]."""
+    _f32_gpu(S, conv_in, conv_out, qkv, z, alpha, beta_raw, conv_w, dt_bias, ssm_a)
+    n_v, d = S.shape[0], S.shape[1]
+    kwidth, conv_dim = conv_in.shape
+    if S.shape != (n_v, d, d) or not S.is_contiguous() or conv_out.shape != conv_in.shape:
+        raise YhipError(-22, "gdn_decode: S must be contiguous [n_v, d, d]; conv_in / conv_out [kwidth, conv_dim]")
+    if conv_dim != (2 * n_k + n_v) * d or conv_w.shape != (conv_dim, kwidth):
+        raise YhipError(-22, "gdn_decode: conv_dim must be (2*n_k + n_v)*d and conv_w [conv_dim, kwidth]")
+    for t in (conv_in, conv_out, qkv, z, alpha, beta_raw, conv_w, dt_bias, ssm_a, norm_w):
+        if not t.is_contiguous():
+            raise YhipError(-22, "gdn_decode: tensors must be contiguous")
+    if qkv.numel() < conv_dim or z.numel() < n_v * d or min(alpha.numel(), beta_raw.numel(), dt_bias.numel(),
+                                                            ssm_a.numel()) < n_v or norm_w.numel() != d:
+        raise YhipError(-22, "gdn_decode: input sizes do not match the heads")
+    if not norm_w.is_cuda or norm_w.dtype not in (torch.float32, torch.float16):
+        raise YhipError(-22, "gdn_decode: norm_w must be fp32 or f16 on the GPU")
+    if y is None:
+        y = torch.empty(n_v * d, dtype=torch.float32, device=S.device)
+    _f32_gpu(y)
+    check(lib().yhip_gdn_decode(S.data_ptr(), conv_in.data_ptr(), conv_out.data_ptr(), y.data_ptr(), qkv.data_ptr(),
+                                z.data_ptr(), alpha.data_ptr(), beta_raw.data_ptr(), conv_w.data_ptr(),
+                                dt_bias.data_ptr(), ssm_a.data_ptr(), norm_w.data_ptr(),
+                                F16 if norm_w.dtype == torch.float16 else F32, n_k, n_v, d, kwidth, float(l2_eps),
+                                float(norm_eps), _stream()))
+    return y
