@@ -114,6 +114,21 @@ __device__ inline void lds_load16(__amdgpu_buffer_rsrc_t r, _Float16* lds, int v
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
+// Workgroup barrier for LDS traffic only: it waits for this thread's LDS
+// accesses (lgkmcnt(0)) and nothing else.  __syncthreads(), and a fence on
+// LDS alone, also wait for every outstanding buffer load into LDS
+// (vmcnt(0)), which would stall on the next item's tile loads; tile loads
+// are instead waited for explicitly before the barrier that publishes them.
+// The empty asm statements keep the compiler from moving memory accesses
+// across the barrier.
+__device__ inline void lds_barrier()
+{
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt at their maxima (no wait)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // 16-byte chunk swizzle of an LDS tile row (XOR into the chunk index).  For
 // rows of 8 chunks (128 B) the swizzle is (r & 7) ^ bit 3 of r: 8 consecutive
 // rows then hit 8 distinct chunk columns (32-bank LDS, b128 reads in groups
@@ -194,336 +209,453 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
     __shared__ __attribute__((aligned(16))) _Float16 Kl1[NG][BN * D];
     __shared__ __attribute__((aligned(16))) _Float16 Vl0[NG][D * BN];
     __shared__ __attribute__((aligned(16))) _Float16 Vl1[NG][D * BN];
+    // (max, sum) of group 1's queries for the two-group merge
+    __shared__ float s_ml[NG > 1 ? 512 : 1];
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int grp = tid >> 8, gtid = tid & 255, wave = gtid >> 6;
-    const int r32 = lane & 31, hh = lane >> 5;
-
+    // Items (query block, head) in heaviest-first order are dealt to the
+    // resident workgroups in snake order (item slot it*W + j on even rounds,
+    // it*W + W-1-j on odd ones), which balances the causal triangle's
+    // linearly decreasing costs; the grid is one item per workgroup when
+    // there are no more items than resident slots.
     const uint32_t nqb = (a.B + BM - 1) / BM;
+    // item `it` of this workgroup -> (query block, head); false past the last
+    auto item_of = [&](uint32_t it, uint32_t& qb, uint32_t& h) -> bool {
+        if (a.xcd_map) {
+            // Consecutive workgroups go to the 8 XCDs in turn.  XCD x serves
+            // kv head x % n_kv, so the query heads that read one kv head
+            // share an L2 and its K/V tiles are fetched from HBM once per XCD
+            // group, not once per XCD; the XCD's own workgroups take its items.
+            const uint32_t x = blockIdx.x % 8u, j = blockIdx.x / 8u, W = gridDim.x / 8u;
+            const uint32_t slot = it * W + ((it & 1u) ? W - 1u - j : j);
+            if (slot >= nqb * a.n_heads / 8u) return false;
+            const uint32_t per = 8u / a.n_kv, G = a.n_heads / a.n_kv;
+            const uint32_t g = x % a.n_kv, i = slot * per + x / a.n_kv;
+            qb = nqb - 1 - i / G;
+            h = g * G + i % G;
+        } else {
+            const uint32_t W = gridDim.x;
+            const uint32_t slot = it * W + ((it & 1u) ? W - 1u - blockIdx.x : blockIdx.x);
+            if (slot >= nqb * a.n_heads) return false;
+            qb = nqb - 1 - slot / a.n_heads;
+            h = slot % a.n_heads;
+        }
+        return true;
+    };
+    // An item's first loads are issued during the previous item: its
+    // group's first K, V and second K tiles in the previous item's last key
+    // step, into buffers that step no longer reads (the V tile only after
+    // the step when that step reads V buffer 0), and, for f16 queries, the
+    // query fragments after the key loop (registers the key loop reads
+    // cannot be loaded inside it without the compiler waiting for them
+    // there).  Their latency hides under that step, the merge and the output
+    // stores.  With a gate the epilogue loads the gate values, which would
+    // then wait behind these loads; such items issue their loads at their
+    // own start.
+    const bool early = a.gate == nullptr;
     uint32_t qb, h;
-    if (a.xcd_map) {
-        // Consecutive workgroups go to the 8 XCDs in turn.  XCD x serves kv
-        // head x % n_kv, so the query heads that read one kv head share an
-        // L2 and its K/V tiles are fetched from HBM once per XCD group, not
-        // once per XCD; within an XCD the order stays heaviest first.
-        const uint32_t x = blockIdx.x % 8u, slot = blockIdx.x / 8u;
-        const uint32_t per = 8u / a.n_kv, G = a.n_heads / a.n_kv;
-        const uint32_t g = x % a.n_kv, i = slot * per + x / a.n_kv;
-        qb = nqb - 1 - i / G;
-        h = g * G + i % G;
-    } else {
-        qb = nqb - 1 - blockIdx.x / a.n_heads;
-        h = blockIdx.x % a.n_heads;
-    }
-    const uint32_t kvh = h * a.n_kv / a.n_heads;  // engine.c:537
+    if (!item_of(0, qb, h)) return;  // uniform over the workgroup
+    for (uint32_t it = 0;; ++it) {
+        // Thread indices pass through an opaque move each item so that nothing
+        // derived from them is hoisted out of the item loop: the key loop's
+        // register budget stays that of a single item.
+        int tid;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+        const int lane = tid & 63;
+        const int grp = tid >> 8, gtid = tid & 255, wave = gtid >> 6;
+        const int r32 = lane & 31, hh = lane >> 5;
+        uint32_t qb_next = 0, h_next = 0;
+        const bool has_next = item_of(it + 1, qb_next, h_next);
 
-    const uint32_t qi0 = qb * BM;
-    const uint32_t qlast = min(a.B, qi0 + BM) - 1;
-    const uint32_t kmax = a.pos_start + qlast;  // last key any query here reads
-    const uint32_t ntiles = kmax / BN + 1;
-    const uint32_t nsteps = (ntiles + NG - 1) / NG;  // loop steps (workgroup-uniform)
-    // this group's tiles: kt = grp + NG*st for st < gsteps
-    const uint32_t gsteps = ntiles > (uint32_t)grp ? (ntiles - grp + NG - 1) / NG : 0;
-
-    const uint32_t wq0 = qi0 + wave * 32;
-    const bool wave_active = wq0 < a.B;
-    const uint32_t wpos_first = a.pos_start + wq0;
-    const uint32_t wpos_last = a.pos_start + min(wq0 + 31, a.B - 1);
-    const uint32_t my_pos = a.pos_start + wq0 + r32;
-    const uint32_t my_q = min(wq0 + r32, a.B - 1);
-    // tiles this wave computes: 0 .. wtiles-1, of which this group's are st < wsteps
-    const uint32_t wtiles = wave_active ? wpos_last / BN + 1 : 0;
-    const uint32_t wsteps = wtiles > (uint32_t)grp ? (wtiles - grp + NG - 1) / NG : 0;
-    auto tile_of = [&](uint32_t st) { return (uint32_t)grp + NG * st; };
-
-    f16x8 qf[NKK];
-    {
-        const size_t base = (size_t)my_q * a.q_stride + (size_t)h * D + hh * 8;
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, base + kk * 16, a.q_dtype);
-        // Complete the query loads here.  Their first reader is the first
-        // score MFMA inside the key loop, whose tile loads are conditional;
-        // left pending, the wait the compiler places before that MFMA cannot
-        // count the tile loads and becomes a full vmcnt(0) on every step.
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    }
-
-    // Buffer resources over this kv head's K rows and V tiles.  A tile adds
-    // the scalar offset kt*BN*D*2 bytes (the same for K rows and two
-    // 32-position V tiles); every tile lies inside the cache (kv_stride is a
-    // multiple of 64 above kmax).
-    const uint32_t head_bytes = a.kv_stride * D * 2;
-    const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(a.kc + k_index(kvh, 0, 0, D, a.kv_stride)), 0, head_bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(a.vc + v_index(kvh, 0, 0, D, a.kv_stride)), 0, head_bytes, 0x00020000);
-    // Chunk L = 256 i + gtid of a tile is the 16 bytes this thread loads with
-    // its i-th instruction.  K: LDS row R = L / KCH holds key row
-    // lds_row_of_key(R) (an involution), column chunk (L % KCH) ^ swz(R).
-    // V: LDS row d = L / VCH holds positions 8c..8c+7 in chunk
-    // (L % VCH) ^ swz(d), from 32-position tile c / 4.
-    int kgo[CH], vgo[CH];
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-        const int L = gtid + 256 * i;
-        const int R = L / KCH, kc = (L % KCH) ^ chunk_swz<KCH>(R);
-        kgo[i] = (lds_row_of_key(R) * D + kc * 8) * 2;
-        const int d = L / VCH, vc = (L % VCH) ^ chunk_swz<VCH>(d);
-        vgo[i] = (vc >> 2) * (D * (int)kVTile * 2) + d * (int)kVTile * 2 + (vc & 3) * 16;
-    }
-    // buffers by parity (a constant at every call after inlining)
-    auto kbuf = [&](int par) { return par ? &Kl1[grp][0] : &Kl0[grp][0]; };
-    auto vbuf = [&](int par) { return par ? &Vl1[grp][0] : &Vl0[grp][0]; };
-    auto dma_k = [&](int par, uint32_t st) {
-        const uint32_t off = tile_of(st) * BN * D * 2;
+        // Chunk L = 256 i + gtid of a tile is the 16 bytes this thread loads
+        // with its i-th instruction.  K: LDS row R = L / KCH holds key row
+        // lds_row_of_key(R) (an involution), column chunk (L % KCH) ^ swz(R).
+        // V: LDS row d = L / VCH holds positions 8c..8c+7 in chunk
+        // (L % VCH) ^ swz(d), from 32-position tile c / 4.
+        int kgo[CH], vgo[CH];
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-            lds_load16(rK, kbuf(par) + (256 * i + 64 * wave) * 8, kgo[i], off);
+            const int L = gtid + 256 * i;
+            const int R = L / KCH, kc = (L % KCH) ^ chunk_swz<KCH>(R);
+            kgo[i] = (lds_row_of_key(R) * D + kc * 8) * 2;
+            const int d = L / VCH, vc = (L % VCH) ^ chunk_swz<VCH>(d);
+            vgo[i] = (vc >> 2) * (D * (int)kVTile * 2) + d * (int)kVTile * 2 + (vc & 3) * 16;
         }
-    };
-    auto dma_v = [&](int par, uint32_t st) {
-        const uint32_t off = tile_of(st) * BN * D * 2;
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            lds_load16(rV, vbuf(par) + (256 * i + 64 * wave) * 8, vgo[i], off);
-        }
-    };
-    auto dma_done = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };  // vmcnt(0): this thread's tile loads landed
-
-    // MFMA operands from LDS.  K fragment (j, kk): key row r32 + 32 j, dims
-    // 16 kk + 8 hh .. +7 = chunk 2 kk + hh.  V fragment (b, kc): row
-    // d = 32 b + r32, positions 16 kc + 8 hh .. +7 = chunk 2 kc + hh.
-    const int ksw = chunk_swz<KCH>(r32), vsw = chunk_swz<VCH>(r32);
-    auto read_k = [&](int par, int j, int kk) {
-        return *reinterpret_cast<const f16x8*>(kbuf(par) + (r32 + 32 * j) * D + (((2 * kk + hh) ^ ksw) << 3));
-    };
-    auto read_v = [&](int par, int b, int kc) {
-        return *reinterpret_cast<const f16x8*>(vbuf(par) + (32 * b + r32) * BN + (((2 * kc + hh) ^ vsw) << 3));
-    };
-    // Keys past kmax in the workgroup's last tile were never stored and may
-    // hold any bits: their P is 0, but their V must be finite.  The group
-    // that owns that tile zeroes them in LDS once, in the step that reads it.
-    auto zero_v_tail = [&](int par, uint32_t st) {
-        const uint32_t k0 = tile_of(st) * BN;
-        const uint32_t valid = kmax - k0 + 1;  // keys 0..valid-1 of the tile are stored
-        _Float16* vb = vbuf(par);
-        for (int idx = gtid; idx < D * VCH; idx += 256) {
-            const int d = idx / VCH, c = idx % VCH;  // logical chunk c: keys 8c..8c+7
-            if ((uint32_t)(8 * c + 7) < valid) continue;
-            f16x8* ch = reinterpret_cast<f16x8*>(vb + d * BN + ((c ^ chunk_swz<VCH>(d)) << 3));
-            f16x8 v = *ch;
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if ((uint32_t)(8 * c + e) >= valid) v[e] = (_Float16)0.0f;
-            *ch = v;
-        }
-    };
-
-    // running max (log2 domain): finite so that a tile whose keys are all in
-    // the lane's future (possible as a group's first tile) leaves l and O at
-    // zero instead of forming -inf - -inf
-    float m = -1e30f, l = 0.0f;
-    f32x16 o[NDB];
-#pragma unroll
-    for (int b = 0; b < NDB; ++b)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
-
-    // scores of the tile in K buffer P into S (both 32-key halves)
-    auto qk = [&](f32x16 (&S)[2], int par) {
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const f16x8 kf = read_k(par, j, kk);
-                S[j] = kk == 0 ? mfma32(kf, qf[0], f32x16{}) : mfma32(kf, qf[kk], S[j]);
-            }
-    };
-    // running max update of the lane's query from tile scores S (raw, masked)
-    auto update_max = [&](const f32x16 (&S)[2]) {
-        float mx = S[0][0];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, S[j][i]);
-        mx = wave_max_xor(mx, 32) * a.c;
-        if (__ballot(mx > m + kSlack)) {  // wave-uniform: some query's max moved
-            const float mn = mx > m + kSlack ? mx : m;
-            const float alpha = fast_exp2(m - mn);
-            m = mn;
-            l *= alpha;
-#pragma unroll
-            for (int b = 0; b < NDB; ++b) o[b] *= alpha;
-        }
-    };
-    auto probs = [&](const f32x16 (&S)[2], f16x8 (&pf)[4]) {
-        const float nm = -m;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const float p = fast_exp2(fmaf(S[i >> 4][i & 15], a.c, nm));
-            l += p;
-            pf[i >> 3][i & 7] = (_Float16)p;
-        }
-    };
-    // O^T += V^T P^T over the tile in V buffer P; fragments are read two
-    // MFMAs ahead (three in a ring)
-    auto pv = [&](const f16x8 (&pf)[4], int par) {
-        constexpr int NM = 4 * NDB;  // MFMA n: kc = n / NDB, b = n % NDB
-        f16x8 vf[3];
-        vf[0] = read_v(par, 0, 0);
-        vf[1] = read_v(par, 1 % NDB, 1 / NDB);
-#pragma unroll
-        for (int n = 0; n < NM; ++n) {
-            if (n + 2 < NM) vf[(n + 2) % 3] = read_v(par, (n + 2) % NDB, (n + 2) / NDB);
-            o[n % NDB] = mfma32(vf[n % 3], pf[n / NDB], o[n % NDB]);
-        }
-    };
-    // Scores of the next tile (K buffer kpar) into Snext and P.V of this tile
-    // (V buffer vpar), with this tile's probabilities (from Scur) formed
-    // between them per FusedSchedule; K and V fragments are read two MFMAs
-    // ahead in their own streams.
-    auto qk_pv = [&](f32x16 (&Snext)[2], int kpar, const f32x16 (&Scur)[2], int vpar) {
-        constexpr int NQ = 2 * NKK, NPV = 4 * NDB;
-        constexpr FusedSchedule<NQ, NPV, NDB> sch{};
-        constexpr int MAXP = 8;
-        const float nm = -m;
-        f16x8 pf[4], kf[3], vf[3];
-        kf[0] = read_k(kpar, 0, 0);
-        kf[1] = read_k(kpar, 1, 0);
-        vf[0] = read_v(vpar, 0, 0);
-        vf[1] = read_v(vpar, 1 % NDB, 1 / NDB);
-#pragma unroll
-        for (int t = 0; t < sch.N; ++t) {
-            const int n = sch.s[t].n;
-            if (sch.s[t].pv) {
-                if (n + 2 < NPV) vf[(n + 2) % 3] = read_v(vpar, (n + 2) % NDB, (n + 2) / NDB);
-                o[n % NDB] = mfma32(vf[n % 3], pf[n / NDB], o[n % NDB]);
-            } else {
-                if (n + 2 < NQ) kf[(n + 2) % 3] = read_k(kpar, (n + 2) & 1, (n + 2) >> 1);
-                Snext[n & 1] = n < 2 ? mfma32(kf[n % 3], qf[0], f32x16{}) : mfma32(kf[n % 3], qf[n >> 1], Snext[n & 1]);
-            }
-#pragma unroll
-            for (int u = 0; u < MAXP; ++u) {
-                if (u < sch.s[t].np) {
-                    const int i = sch.s[t].p0 + u;
-                    const float p = fast_exp2(fmaf(Scur[i >> 4][i & 15], a.c, nm));
-                    l += p;
-                    pf[i >> 3][i & 7] = (_Float16)p;
-                }
-            }
-        }
-    };
-    // a tile that reaches past the wave's first query: keys beyond the
-    // lane's position get -inf
-    auto mask = [&](f32x16 (&S)[2], uint32_t st) {
-        const uint32_t k0 = tile_of(st) * BN;
-        if (k0 + BN - 1 > wpos_first) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (k0 + 32 * j + key_of_acc(i, hh) > my_pos) S[j][i] = -INFINITY;
-        }
-    };
-
-    // prologue: the group's first K, V and second K in LDS; scores of step 0
-    if (gsteps > 0) {
-        dma_k(0, 0);
-        dma_v(0, 0);
-    }
-    if (gsteps > 1) dma_k(1, 1);
-    dma_done();
-    __syncthreads();
-    f32x16 Sa[2], Sb[2];
-    if (wsteps > 0) qk(Sa, 0);
-    // step 0 loads K(2) over K(0), whose last readers are the scores above
-    __syncthreads();
-
-    // step st (parity p = st % 2): loads K(st+2) into K buffer p (it held
-    // K(st), last read by the previous step's scores) and V(st+1) into V
-    // buffer 1-p (it held V(st-1)); scores of st+1 (K buffer 1-p) overlap the
-    // softmax of st; P.V of st (V buffer p); one barrier.  With pos_start
-    // not a multiple of 32 a wave's queries straddle a tile boundary, so a
-    // tile with a successor may still need the mask.
-    const uint32_t tail_step = (ntiles - 1) / NG;  // the step that reads the last tile
-    const int tail_grp = (int)((ntiles - 1) % NG);  // in this group's buffers
-    auto step = [&](int p, uint32_t st, f32x16 (&Scur)[2], f32x16 (&Snext)[2]) {
-        if (st + 2 < gsteps) dma_k(p, st + 2);
-        if (st + 1 < gsteps) dma_v(1 - p, st + 1);
-        if (st == tail_step && (kmax + 1) % BN != 0) {  // workgroup-uniform
-            if (grp == tail_grp) zero_v_tail(p, st);
-            __syncthreads();
-        }
-        if (st + 1 < wsteps) {
-            mask(Scur, st);
-            update_max(Scur);
-            qk_pv(Snext, 1 - p, Scur, p);
-        } else if (st < wsteps) {
-            mask(Scur, st);
-            update_max(Scur);
-            f16x8 pf[4];
-            probs(Scur, pf);
-            pv(pf, p);
-        }
-        dma_done();
-        __syncthreads();
-    };
-    for (uint32_t st = 0; st < nsteps; st += 2) {
-        step(0, st, Sa, Sb);
-        if (st + 1 < nsteps) step(1, st + 1, Sb, Sa);
-    }
-
-    l += __shfl_xor(l, 32, 64);
-    if constexpr (NG > 1) {
-        // group 1 hands (m, l, O) to group 0 through LDS, free after the last
-        // step's barrier: m, l in V buffer 0, O blocks 0..NDB/2-1 in K buffer
-        // 0 and the rest in K buffer 1 (16 floats x 256 lanes per block)
-        static_assert(NDB / 2 * 16 * 256 * 4 <= (int)sizeof(Kl0) && 2 * 256 * 4 <= (int)sizeof(Vl0), "merge area");
-        float* ml = reinterpret_cast<float*>(&Vl0[0][0]);
-        auto oarea = [&](int b) {
-            return b < NDB / 2 ? reinterpret_cast<float*>(&Kl0[0][0]) + b * 16 * 256
-                               : reinterpret_cast<float*>(&Kl1[0][0]) + (b - NDB / 2) * 16 * 256;
+        const int ksw = chunk_swz<KCH>(r32), vsw = chunk_swz<VCH>(r32);
+        // buffers by parity (a constant at every call after inlining)
+        auto kbuf = [&](int par) { return par ? &Kl1[grp][0] : &Kl0[grp][0]; };
+        auto vbuf = [&](int par) { return par ? &Vl1[grp][0] : &Vl0[grp][0]; };
+        // Buffer resources over a kv head's K rows and V tiles.  A tile adds
+        // the scalar offset kt*BN*D*2 bytes (the same for K rows and two
+        // 32-position V tiles); every tile lies inside the cache (kv_stride is a
+        // multiple of 64 above kmax).
+        const uint32_t head_bytes = a.kv_stride * D * 2;
+        auto rsrc_k = [&](uint32_t kv) {
+            return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.kc + k_index(kv, 0, 0, D, a.kv_stride)), 0,
+                                                     head_bytes, 0x00020000);
         };
-        if (grp == 1) {
-            ml[gtid] = m;
-            ml[256 + gtid] = l;
+        auto rsrc_v = [&](uint32_t kv) {
+            return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.vc + v_index(kv, 0, 0, D, a.kv_stride)), 0,
+                                                     head_bytes, 0x00020000);
+        };
+        // tile kt of a K (V) resource into K (V) buffer par
+        auto dma_k_of = [&](__amdgpu_buffer_rsrc_t r, int par, uint32_t kt) {
 #pragma unroll
-            for (int b = 0; b < NDB; ++b)
+            for (int i = 0; i < CH; ++i) lds_load16(r, kbuf(par) + (256 * i + 64 * wave) * 8, kgo[i], kt * BN * D * 2);
+        };
+        auto dma_v_of = [&](__amdgpu_buffer_rsrc_t r, int par, uint32_t kt) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) oarea(b)[i * 256 + gtid] = o[b][i];
+            for (int i = 0; i < CH; ++i) lds_load16(r, vbuf(par) + (256 * i + 64 * wave) * 8, vgo[i], kt * BN * D * 2);
+        };
+        auto dma_done = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };  // vmcnt(0): this thread's loads landed
+        f16x8 qf[NKK];
+        // the first loads of item (iqb, ih), see above: the K tiles, the first V
+        // tile and the queries
+        auto item_tiles = [&](uint32_t iqb) {
+            const uint32_t intiles = (a.pos_start + min(a.B, iqb * BM + BM) - 1) / BN + 1;
+            return intiles > (uint32_t)grp ? (intiles - grp + NG - 1) / NG : 0u;  // this group's
+        };
+        auto issue_item_k = [&](uint32_t iqb, uint32_t ih) {
+            const uint32_t igsteps = item_tiles(iqb);
+            const __amdgpu_buffer_rsrc_t rk = rsrc_k(ih * a.n_kv / a.n_heads);
+            if (igsteps > 0) dma_k_of(rk, 0, grp);
+            if (igsteps > 1) dma_k_of(rk, 1, grp + NG);
+        };
+        auto issue_item_q = [&](uint32_t iqb, uint32_t ih) {
+            if (a.q_dtype == kF16) {
+                const uint32_t iq = min(iqb * BM + wave * 32 + r32, a.B - 1);
+                const uint16_t* qp =
+                    reinterpret_cast<const uint16_t*>(a.q) + (size_t)iq * a.q_stride + (size_t)ih * D + hh * 8;
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk) qf[kk] = *reinterpret_cast<const f16x8*>(qp + kk * 16);
+            }
+        };
+        auto issue_item_v = [&](uint32_t iqb, uint32_t ih) {
+            if (item_tiles(iqb) > 0) dma_v_of(rsrc_v(ih * a.n_kv / a.n_heads), 0, grp);
+        };
+        if (it == 0 || !early) {
+            if (it > 0) __syncthreads();  // the previous item's epilogue read LDS these loads overwrite
+            issue_item_k(qb, h);
+            issue_item_v(qb, h);
+            issue_item_q(qb, h);
         }
-        __syncthreads();
-        if (grp == 1) return;
-        const float m1 = ml[gtid], l1 = ml[256 + gtid];
-        const float mg = fmaxf(m, m1);
-        const float a0 = fast_exp2(m - mg), a1 = fast_exp2(m1 - mg);
-        m = mg;
-        l = l * a0 + l1 * a1;
+
+        const uint32_t kvh = h * a.n_kv / a.n_heads;  // engine.c:537
+        const uint32_t qi0 = qb * BM;
+        const uint32_t qlast = min(a.B, qi0 + BM) - 1;
+        const uint32_t kmax = a.pos_start + qlast;  // last key any query here reads
+        const uint32_t ntiles = kmax / BN + 1;
+        const uint32_t nsteps = (ntiles + NG - 1) / NG;  // loop steps (workgroup-uniform)
+        // this group's tiles: kt = grp + NG*st for st < gsteps
+        const uint32_t gsteps = ntiles > (uint32_t)grp ? (ntiles - grp + NG - 1) / NG : 0;
+
+        const uint32_t wq0 = qi0 + wave * 32;
+        const bool wave_active = wq0 < a.B;
+        const uint32_t wpos_first = a.pos_start + wq0;
+        const uint32_t wpos_last = a.pos_start + min(wq0 + 31, a.B - 1);
+        const uint32_t my_pos = a.pos_start + wq0 + r32;
+        const uint32_t my_q = min(wq0 + r32, a.B - 1);
+        // tiles this wave computes: 0 .. wtiles-1, of which this group's are st < wsteps
+        const uint32_t wtiles = wave_active ? wpos_last / BN + 1 : 0;
+        const uint32_t wsteps = wtiles > (uint32_t)grp ? (wtiles - grp + NG - 1) / NG : 0;
+        auto tile_of = [&](uint32_t st) { return (uint32_t)grp + NG * st; };
+
+        const __amdgpu_buffer_rsrc_t rK = rsrc_k(kvh), rV = rsrc_v(kvh);
+        auto dma_k = [&](int par, uint32_t st) { dma_k_of(rK, par, tile_of(st)); };
+        auto dma_v = [&](int par, uint32_t st) { dma_v_of(rV, par, tile_of(st)); };
+
+        // MFMA operands from LDS.  K fragment (j, kk): key row r32 + 32 j, dims
+        // 16 kk + 8 hh .. +7 = chunk 2 kk + hh.  V fragment (b, kc): row
+        // d = 32 b + r32, positions 16 kc + 8 hh .. +7 = chunk 2 kc + hh.
+        auto read_k = [&](int par, int j, int kk) {
+            return *reinterpret_cast<const f16x8*>(kbuf(par) + (r32 + 32 * j) * D + (((2 * kk + hh) ^ ksw) << 3));
+        };
+        auto read_v = [&](int par, int b, int kc) {
+            return *reinterpret_cast<const f16x8*>(vbuf(par) + (32 * b + r32) * BN + (((2 * kc + hh) ^ vsw) << 3));
+        };
+        // Keys past kmax in the workgroup's last tile were never stored and may
+        // hold any bits: their P is 0, but their V must be finite.  The group
+        // that owns that tile zeroes them in LDS once, in the step that reads it.
+        auto zero_v_tail = [&](int par, uint32_t st) {
+            const uint32_t k0 = tile_of(st) * BN;
+            const uint32_t valid = kmax - k0 + 1;  // keys 0..valid-1 of the tile are stored
+            _Float16* vb = vbuf(par);
+            for (int idx = gtid; idx < D * VCH; idx += 256) {
+                const int d = idx / VCH, c = idx % VCH;  // logical chunk c: keys 8c..8c+7
+                if ((uint32_t)(8 * c + 7) < valid) continue;
+                f16x8* ch = reinterpret_cast<f16x8*>(vb + d * BN + ((c ^ chunk_swz<VCH>(d)) << 3));
+                f16x8 v = *ch;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if ((uint32_t)(8 * c + e) >= valid) v[e] = (_Float16)0.0f;
+                *ch = v;
+            }
+        };
+
+        // running max (log2 domain): finite so that a tile whose keys are all in
+        // the lane's future (possible as a group's first tile) leaves l and O at
+        // zero instead of forming -inf - -inf
+        float m = -1e30f, l = 0.0f;
+        f32x16 o[NDB];
 #pragma unroll
         for (int b = 0; b < NDB; ++b)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[b][i] = o[b][i] * a0 + oarea(b)[i * 256 + gtid] * a1;
-    }
-    if (!wave_active) return;
-    const uint32_t qi = wq0 + r32;
-    if (qi >= a.B) return;
-    const float inv = 1.0f / l;
+            for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
+
+        // scores of the tile in K buffer P into S (both 32-key halves)
+        auto qk = [&](f32x16 (&S)[2], int par) {
 #pragma unroll
-    for (int b = 0; b < NDB; ++b) {
+            for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-            const uint32_t d = b * 32 + 8 * i4 + 4 * hh;
-            f32x4 v;
+                for (int j = 0; j < 2; ++j) {
+                    const f16x8 kf = read_k(par, j, kk);
+                    S[j] = kk == 0 ? mfma32(kf, qf[0], f32x16{}) : mfma32(kf, qf[kk], S[j]);
+                }
+        };
+        // running max update of the lane's query from tile scores S (raw, masked)
+        auto update_max = [&](const f32x16 (&S)[2]) {
+            float mx = S[0][0];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = o[b][4 * i4 + e] * inv;
-            if (a.gate) {
-                const float* gp = a.gate + (size_t)qi * a.gate_stride + (size_t)h * D + d;
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] *= sigmoid_ref(gp[e]);
+                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, S[j][i]);
+            // the lane pair (l, l+32) holds one query: exchange the halves
+            const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx),
+                                                             __builtin_bit_cast(uint32_t, mx), false, false);
+            mx = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1])) * a.c;
+            if (__ballot(mx > m + kSlack)) {  // wave-uniform: some query's max moved
+                const float mn = mx > m + kSlack ? mx : m;
+                const float alpha = fast_exp2(m - mn);
+                m = mn;
+                l *= alpha;
+#pragma unroll
+                for (int b = 0; b < NDB; ++b) o[b] *= alpha;
             }
-            store_out4(a.out, (size_t)qi * a.out_stride + (size_t)h * D + d, a.out_dtype, v);
+        };
+        auto probs = [&](const f32x16 (&S)[2], f16x8 (&pf)[4]) {
+            const float nm = -m;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const float p = fast_exp2(fmaf(S[i >> 4][i & 15], a.c, nm));
+                l += p;
+                pf[i >> 3][i & 7] = (_Float16)p;
+            }
+        };
+        // O^T += V^T P^T over the tile in V buffer P; fragments are read two
+        // MFMAs ahead (three in a ring)
+        auto pv = [&](const f16x8 (&pf)[4], int par) {
+            constexpr int NM = 4 * NDB;  // MFMA n: kc = n / NDB, b = n % NDB
+            f16x8 vf[3];
+            vf[0] = read_v(par, 0, 0);
+            vf[1] = read_v(par, 1 % NDB, 1 / NDB);
+#pragma unroll
+            for (int n = 0; n < NM; ++n) {
+                if (n + 2 < NM) vf[(n + 2) % 3] = read_v(par, (n + 2) % NDB, (n + 2) / NDB);
+                o[n % NDB] = mfma32(vf[n % 3], pf[n / NDB], o[n % NDB]);
+            }
+        };
+        // Scores of the next tile (K buffer kpar) into Snext and P.V of this tile
+        // (V buffer vpar), with this tile's probabilities (from Scur) formed
+        // between them per FusedSchedule; K and V fragments are read two MFMAs
+        // ahead in their own streams.
+        auto qk_pv = [&](f32x16 (&Snext)[2], int kpar, const f32x16 (&Scur)[2], int vpar) {
+            constexpr int NQ = 2 * NKK, NPV = 4 * NDB;
+            constexpr FusedSchedule<NQ, NPV, NDB> sch{};
+            constexpr int MAXP = 8;
+            const float nm = -m;
+            f16x8 pf[4], kf[3], vf[3];
+            kf[0] = read_k(kpar, 0, 0);
+            kf[1] = read_k(kpar, 1, 0);
+            vf[0] = read_v(vpar, 0, 0);
+            vf[1] = read_v(vpar, 1 % NDB, 1 / NDB);
+#pragma unroll
+            for (int t = 0; t < sch.N; ++t) {
+                const int n = sch.s[t].n;
+                if (sch.s[t].pv) {
+                    if (n + 2 < NPV) vf[(n + 2) % 3] = read_v(vpar, (n + 2) % NDB, (n + 2) / NDB);
+                    o[n % NDB] = mfma32(vf[n % 3], pf[n / NDB], o[n % NDB]);
+                } else {
+                    if (n + 2 < NQ) kf[(n + 2) % 3] = read_k(kpar, (n + 2) & 1, (n + 2) >> 1);
+                    Snext[n & 1] = n < 2 ? mfma32(kf[n % 3], qf[0], f32x16{})
+                                         : mfma32(kf[n % 3], qf[n >> 1], Snext[n & 1]);
+                }
+#pragma unroll
+                for (int u = 0; u < MAXP; ++u) {
+                    if (u < sch.s[t].np) {
+                        const int i = sch.s[t].p0 + u;
+                        const float p = fast_exp2(fmaf(Scur[i >> 4][i & 15], a.c, nm));
+                        l += p;
+                        pf[i >> 3][i & 7] = (_Float16)p;
+                    }
+                }
+            }
+        };
+        // a tile that reaches past the wave's first query: keys beyond the
+        // lane's position get -inf
+        auto mask = [&](f32x16 (&S)[2], uint32_t st) {
+            const uint32_t k0 = tile_of(st) * BN;
+            if (k0 + BN - 1 > wpos_first) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (k0 + 32 * j + key_of_acc(i, hh) > my_pos) S[j][i] = -INFINITY;
+            }
+        };
+
+        // prologue: this item's first loads are in flight (issued above or at the
+        // end of the previous item); f32 and bf16 queries are loaded and
+        // converted here.  All loads are complete before the key loop, whose
+        // waits then count only tile loads.
+        dma_done();
+        if (a.q_dtype != kF16) {
+            const size_t qbase = (size_t)my_q * a.q_stride + (size_t)h * D + hh * 8;
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, qbase + kk * 16, a.q_dtype);
+            dma_done();
         }
-    }
+        __syncthreads();
+        f32x16 Sa[2], Sb[2];
+        if (wsteps > 0) qk(Sa, 0);
+        // step 0 loads K(2) over K(0), whose last readers are the scores above
+        __syncthreads();
+
+        // step st (parity p = st % 2): loads K(st+2) into K buffer p (it held
+        // K(st), last read by the previous step's scores) and V(st+1) into V
+        // buffer 1-p (it held V(st-1)); scores of st+1 (K buffer 1-p) overlap the
+        // softmax of st; P.V of st (V buffer p); one barrier.  With pos_start
+        // not a multiple of 32 a wave's queries straddle a tile boundary, so a
+        // tile with a successor may still need the mask.
+        const uint32_t tail_step = (ntiles - 1) / NG;  // the step that reads the last tile
+        const int tail_grp = (int)((ntiles - 1) % NG);  // in this group's buffers
+        const bool prefetch = has_next && early;
+        // the group's last step (or, for a group without tiles, the first) issues
+        // the next item's loads
+        const uint32_t last_st = gsteps > 0 ? gsteps - 1 : 0;
+        auto step = [&](int p, uint32_t st, f32x16 (&Scur)[2], f32x16 (&Snext)[2]) {
+            if (st + 2 < gsteps) dma_k(p, st + 2);
+            if (st + 1 < gsteps) dma_v(1 - p, st + 1);
+            if (prefetch && st == last_st) {
+                // K buffers are free (no scores follow), V buffer 1-p too
+                issue_item_k(qb_next, h_next);
+                if (p == 1 || gsteps == 0) issue_item_v(qb_next, h_next);
+            }
+            if (st == tail_step && (kmax + 1) % BN != 0) {  // workgroup-uniform
+                if (grp == tail_grp) zero_v_tail(p, st);
+                lds_barrier();
+            }
+            if (st + 1 < wsteps) {
+                mask(Scur, st);
+                update_max(Scur);
+                qk_pv(Snext, 1 - p, Scur, p);
+            } else if (st < wsteps) {
+                mask(Scur, st);
+                update_max(Scur);
+                f16x8 pf[4];
+                probs(Scur, pf);
+                pv(pf, p);
+            }
+            // this step's own loads (none from the group's last step on, whose
+            // next-item loads are waited for by the next item)
+            if (!(prefetch && st >= last_st)) dma_done();
+            lds_barrier();
+        };
+        for (uint32_t st = 0; st < nsteps; st += 2) {
+            step(0, st, Sa, Sb);
+            if (st + 1 < nsteps) step(1, st + 1, Sb, Sa);
+        }
+
+        // the next item's first V tile when the last step still read V buffer 0,
+        // and its queries
+        if (prefetch) {
+            if (gsteps > 0 && (last_st & 1u) == 0) issue_item_v(qb_next, h_next);
+            issue_item_q(qb_next, h_next);
+        }
+        {
+            // the lane pair (l, l+32) holds one query: add the halves
+            const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, l),
+                                                             __builtin_bit_cast(uint32_t, l), false, false);
+            l = __builtin_bit_cast(float, (uint32_t)sw[0]) + __builtin_bit_cast(float, (uint32_t)sw[1]);
+        }
+        // Thread indices for the epilogue from a fresh opaque read, so that the
+        // ones of the item's start need not stay live through the key loop.
+        int tid_e;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(tid_e) : "v"((int)threadIdx.x));
+        const int gtid_e = tid_e & 255, lane_e = tid_e & 63;
+        if constexpr (NG > 1) {
+            // Group 1 hands (m, l, O) to group 0 through LDS: m, l in s_ml and O
+            // through V buffer 1 of both groups (the one buffer the next item's
+            // first loads leave free; 32 KB at d = 128), half the blocks at a time.
+            constexpr int HB = NDB / 2;  // O blocks per round
+            static_assert(HB * 16 * 256 * 4 <= (int)sizeof(Vl1), "merge area");
+            float* oarea = reinterpret_cast<float*>(&Vl1[0][0]);
+            if (grp == 1) {
+                s_ml[gtid_e] = m;
+                s_ml[256 + gtid_e] = l;
+            }
+            float a0 = 1.0f, a1 = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                if (grp == 1) {
+#pragma unroll
+                    for (int b = 0; b < HB; ++b)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) oarea[(b * 16 + i) * 256 + gtid_e] = o[r * HB + b][i];
+                }
+                lds_barrier();
+                if (grp == 0) {
+                    if (r == 0) {
+                        const float m1 = s_ml[gtid_e], l1 = s_ml[256 + gtid_e];
+                        const float mg = fmaxf(m, m1);
+                        a0 = fast_exp2(m - mg);
+                        a1 = fast_exp2(m1 - mg);
+                        m = mg;
+                        l = l * a0 + l1 * a1;
+                    }
+#pragma unroll
+                    for (int b = 0; b < HB; ++b)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                            o[r * HB + b][i] = o[r * HB + b][i] * a0 + oarea[(b * 16 + i) * 256 + gtid_e] * a1;
+                }
+                if (r == 0) lds_barrier();  // round 0 read before round 1 overwrites
+            }
+        }
+        const uint32_t qi = qi0 + (gtid_e >> 6) * 32 + (lane_e & 31);
+        if ((tid_e >> 8) == 0 && qi < a.B) {  // group 1 handed its part over
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int b = 0; b < NDB; ++b) {
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const uint32_t d = b * 32 + 8 * i4 + 4 * (lane_e >> 5);
+                f32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = o[b][4 * i4 + e] * inv;
+                if (a.gate) {
+                    const float* gp = a.gate + (size_t)qi * a.gate_stride + (size_t)h * D + d;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] *= sigmoid_ref(gp[e]);
+                }
+                store_out4(a.out, (size_t)qi * a.out_stride + (size_t)h * D + d, a.out_dtype, v);
+            }
+        }
+        }
+        if (!has_next) break;
+        qb = qb_next;
+        h = h_next;
+    }  // items
+}
+
+int n_cus()
+{
+    static const int n_cu = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    return n_cu;
 }
 
 template <int D, int NG>
@@ -538,8 +670,32 @@ hipError_t launch_prefill_d(PrefillArgs a, hipStream_t st)
     const uint32_t nqb0 = (a.B + BM - 1) / BM;
     a.xcd_map = env != 0 && a.n_kv <= 8 && 8 % a.n_kv == 0 && a.n_heads % a.n_kv == 0 &&
                 ((uint64_t)nqb0 * (a.n_heads / a.n_kv)) % (8 / a.n_kv) == 0;
-    const uint32_t nqb = (a.B + BM - 1) / BM;
-    hipLaunchKernelGGL((prefill_kernel<D, NG>), dim3(nqb * a.n_heads), dim3(256 * NG), 0, st, a);
+    const uint32_t items = nqb0 * a.n_heads;
+    // resident workgroups: one round of the grid fills every slot once
+    static const int per_cu = [] {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<D, NG>, 256 * NG, 0) != hipSuccess || n < 1)
+            n = 1;
+        return n;
+    }();
+    // Resident workgroups walking the item list pay off with one 8-wave
+    // workgroup per CU (two key groups), where nothing else on the CU covers
+    // a workgroup's start and end (2048 tokens x 28 heads: 57.1 -> 55.7 us);
+    // with two 4-wave workgroups per CU the hardware's own dispatch of the
+    // next workgroup already overlaps them and is about 1 % faster (8192
+    // tokens).  YHIP_PREFILL_PERSIST=0/1 forces the choice for comparisons.
+    static const int persist = [] {
+        const char* e = getenv("YHIP_PREFILL_PERSIST");
+        return e ? atoi(e) : -1;
+    }();
+    uint32_t grid = items;
+    if (persist > 0 || (persist < 0 && NG > 1)) {
+        const uint64_t slots = (uint64_t)per_cu * (uint64_t)n_cus();
+        if (slots < grid) grid = (uint32_t)slots;
+        if (a.xcd_map) grid = grid / 8u * 8u;  // whole XCD groups (items are a multiple of 8)
+        if (grid == 0) grid = items;
+    }
+    hipLaunchKernelGGL((prefill_kernel<D, NG>), dim3(grid), dim3(256 * NG), 0, st, a);
     return hipGetLastError();
 }
 
@@ -556,13 +712,7 @@ int prefill_groups(const PrefillArgs& a)
         const char* e = getenv("YHIP_PREFILL_NG");
         return e ? atoi(e) : 0;
     }();
-    static const int n_cu = [] {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            n = 256;
-        return n;
-    }();
+    const int n_cu = n_cus();
     if (a.D > 128) return 1;
     if (env == 1 || env == 2) return env;
     const uint64_t wgs = (uint64_t)((a.B + BM - 1) / BM) * a.n_heads;

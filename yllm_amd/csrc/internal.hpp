@@ -57,7 +57,10 @@ struct PrefillArgs {
     uint32_t gate_stride;
     uint32_t pos_start, B, n_heads, n_kv, D;
     float c;
-    uint32_t xcd_map;  // set by the launcher: workgroup -> (query block, head) grouped by kv head per XCD
+    // set by the launcher: the (query block, head) items are grouped by kv
+    // head per XCD (xcd_map) and dealt to gridDim.x resident workgroups in
+    // snake order, heaviest first
+    uint32_t xcd_map;
 };
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
 
