@@ -283,6 +283,40 @@ def test_prefill_gated_parity(cuda, oracle):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("nh,nkv,hd,ps,B,qdt,odt,gated", [
+    # more (query block, head) items than resident 8-wave workgroups: each
+    # workgroup walks several items, the next item's tiles load during the
+    # previous one's last key step (f32 queries load at the item's start)
+    (28, 4, 128, 0, 2048, torch.float32, torch.float32, False),
+    # gated: every item issues its own loads; 3 kv heads: items are not
+    # grouped per XCD; unaligned start and a partial last query block
+    (24, 3, 128, 37, 2000, torch.float16, torch.float32, True),
+    (32, 8, 64, 0, 2048, torch.bfloat16, torch.float16, False),
+])
+def test_prefill_resident_workgroups_sampled_rows(cuda, oracle, nh, nkv, hd, ps, B, qdt, odt, gated):
+    from yllm_amd.attention import attn_prefill, round_bf16
+
+    kvd = nkv * hd
+    L = ps + B
+    K, V = gen(1700 + L, (L, kvd)), gen(1800 + L, (L, kvd))
+    q = gen(1900 + L, (B, nh * hd))
+    if qdt == torch.bfloat16:
+        q = round_bf16(q.ravel().copy()).reshape(B, nh * hd)
+    gate = gen(2000 + L, (B, nh * hd), 1.0, f16=False) if gated else None
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    got = attn_prefill(torch.from_numpy(q).to(cuda).to(qdt), cache, ps, nh, out_dtype=odt,
+                       gate=torch.from_numpy(gate).to(cuda) if gated else None).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    tol = TOL + (2.0 ** -10 if odt == torch.float16 else 0.0)
+    for b in (0, 1, 127, 128, 255, 640, 1023, 1024, 1500, B - 129, B - 2, B - 1):
+        t = ps + b
+        want = oracle.decode(q[b], kc[: t + 1], vc[: t + 1], t, nh, nkv, hd)
+        if gated:
+            want = oracle.gate_sigmoid(want.ravel(), gate[b].ravel())
+        err = rel_l2(got[b].ravel(), want.ravel())
+        assert err <= tol, f"row {b}: rel_l2={err:.3e}"
+
+
 @pytest.mark.parametrize("nh,nkv,hd,L", [(28, 4, 128, 2048), (32, 8, 128, 8192)])
 def test_prefill_full_size_sampled_rows(cuda, oracle, nh, nkv, hd, L):
     """Configs 2 and 4-prefill at full size: sampled rows against the oracle at their position,
