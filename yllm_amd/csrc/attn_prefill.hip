@@ -114,21 +114,6 @@ __device__ inline void lds_load16(__amdgpu_buffer_rsrc_t r, _Float16* lds, int v
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
-// Workgroup barrier for LDS traffic only: it waits for this thread's LDS
-// accesses (lgkmcnt(0)) and nothing else.  __syncthreads(), and a fence on
-// LDS alone, also wait for every outstanding buffer load into LDS
-// (vmcnt(0)), which would stall on the next item's tile loads; tile loads
-// are instead waited for explicitly before the barrier that publishes them.
-// The empty asm statements keep the compiler from moving memory accesses
-// across the barrier.
-__device__ inline void lds_barrier()
-{
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt at their maxima (no wait)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
 // 16-byte chunk swizzle of an LDS tile row (XOR into the chunk index).  For
 // rows of 8 chunks (128 B) the swizzle is (r & 7) ^ bit 3 of r: 8 consecutive
 // rows then hit 8 distinct chunk columns (32-bank LDS, b128 reads in groups

@@ -83,6 +83,21 @@ __device__ inline float load_as_f32(const void* p, size_t i, uint32_t dt)
     return dt == kBF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
 }
 
+// Workgroup barrier for LDS traffic only: it waits for this thread's LDS
+// accesses (lgkmcnt(0)) and nothing else.  __syncthreads(), and a fence on
+// LDS alone, also wait for every outstanding global or buffer load of the
+// thread (vmcnt(0)), which stalls on loads issued ahead for later use;
+// loads whose data another thread reads through LDS must be waited for
+// explicitly before the barrier that publishes them.  The empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ inline void lds_barrier()
+{
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt at their maxima (no wait)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ inline float wave_max_xor(float v, int mask)
