@@ -25,6 +25,12 @@ batch of synthetic input, with all inputs resident in HBM:
   oproj8k     o_proj after prefill attention: x += W_o . att, 8192 tokens,
               W_o 4096 x 4096 f16, f16 att (one hipBLASLt GEMM).
   oproj1      the same for one decode token (the GEMV kernel, HBM-bound).
+  kvstore8k   the KV store on its own: 8192 rows of K and V, 8 KV heads of
+              128, f32 -> f16 with the reference rounding into the
+              head-major cache (K rows, V 32-position tiles).
+  gated4k     the qwen35 gated attention prefill of the fifth configuration:
+              4096 tokens, 16 / 2 heads, head_dim 256, bf16 queries, f32
+              sigmoid gate fused in the epilogue, bf16 out.
   hybrid      the fifth configuration end to end: 3 GDN layers + 1 gated
               attention layer (16 / 2 heads, d 256, bf16), 4096-token
               prefill then 256 decode steps; tokens/s over the whole pass.
@@ -413,6 +419,93 @@ def run_rope(L: int, nh: int, nkv: int, hd: int, theta: float, steps: int, warmu
     return res
 
 
+def kvstore_bytes(L: int, nkv: int, hd: int) -> float:
+    return float(L) * nkv * hd * 2 * (4 + 2)  # K and V: f32 read, f16 written
+
+
+def run_kvstore(L: int, nkv: int, hd: int, steps: int, warmup: int, cpu: bool):
+    import torch
+
+    from yllm_amd.attention import LayerKV, kv_store
+
+    dev = torch.device("cuda:0")
+    seed = SEED + 7
+    kvd = nkv * hd
+    k = torch.from_numpy(synth_raw(seed, L * kvd).reshape(L, kvd)).to(dev)
+    v = torch.from_numpy(synth_raw(seed, L * kvd, L * kvd).reshape(L, kvd)).to(dev)
+    # rotating copies of (k, v rows, cache) beyond the 256 MB MALL
+    n_sets = max(1, int(-(-ROTATE_BYTES // kvstore_bytes(L, nkv, hd))))
+    sets = [(k.clone(), v.clone(), LayerKV.empty(nkv, hd, L, device=dev, zero=False)) for _ in range(n_sets)]
+    del k, v
+
+    def step(i):
+        ki, vi, c = sets[i % n_sets]
+        kv_store(c, ki, vi, 0)
+
+    last = sets[(warmup + steps - 1) % n_sets]
+    ms, kern_ms = time_steps(step, steps, warmup, last[2].k)
+    nbytes = kvstore_bytes(L, nkv, hd)
+    achieved = nbytes / (kern_ms * 1e-3)
+    res = {
+        "value": achieved / 1e9, "unit": "GB/s", "ms_per_step": ms, "tokens_per_s": L / (ms * 1e-3),
+        "config": {"workload": f"KV store: {L} rows at positions 0..{L - 1}, {nkv} KV heads, head_dim {hd}; "
+                               f"f32 K/V rows N(0,1) seed {hex(seed)} -> f16 (the reference's round-half-up) "
+                               f"into the head-major cache; {n_sets} rotating input sets (> 256 MB MALL)",
+                   "tokens": L, "n_kv_heads": nkv, "head_dim": hd},
+        "roofline": {"bound": "hbm", "kernel": "kv_block_kernel", "achieved": achieved / 1e9,
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": achieved / HBM_PEAK,
+                     "bytes_per_launch": nbytes, "launch_ms": kern_ms, "traffic": traffic_of(f"kvstore{L}")},
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_kvstore(last, L, nkv, hd)
+    return res
+
+
+def run_gated_prefill(L: int, nh: int, nkv: int, hd: int, steps: int, warmup: int, cpu: bool):
+    import torch
+
+    from yllm_amd.attention import LayerKV, attn_prefill, kv_store
+
+    dev = torch.device("cuda:0")
+    seed = SEED + 5
+    nq, nk = L * nh * hd, L * nkv * hd
+    q = torch.from_numpy(synth(seed, nq).reshape(L, nh * hd)).to(dev).to(torch.bfloat16)
+    k = torch.from_numpy(synth(seed, nk, nq).reshape(L, nkv * hd)).to(dev).half()
+    v = torch.from_numpy(synth(seed, nk, nq + nk).reshape(L, nkv * hd)).to(dev).half()
+    gate = torch.from_numpy(synth_raw(seed, nq, nq + 2 * nk).reshape(L, nh * hd)).to(dev)
+    set_bytes = nq * 2 + 2 * nk * 2 + nq * 4 + nq * 2
+    n_sets = max(1, -(-ROTATE_BYTES // set_bytes))
+    sets = []
+    for _ in range(n_sets):
+        c = LayerKV.empty(nkv, hd, L, device=dev)
+        kv_store(c, k, v, 0)
+        sets.append((q.clone(), c, gate.clone(), torch.empty((L, nh * hd), dtype=torch.bfloat16, device=dev)))
+    del q, gate
+
+    def step(i):
+        qi, c, gi, oi = sets[i % n_sets]
+        attn_prefill(qi, c, 0, nh, gate=gi, out=oi)
+
+    last = sets[(warmup + steps - 1) % n_sets]
+    ms, kern_ms = time_steps(step, steps, warmup, last[3])
+    flops = prefill_flops(L, nh, hd)
+    achieved = flops / (kern_ms * 1e-3)
+    res = {
+        "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms, "tokens_per_s": L / (ms * 1e-3),
+        "config": {"workload": f"qwen35 gated attention prefill: causal GQA over {L} tokens, {nh} query / {nkv} KV "
+                               f"heads, head_dim {hd}; bf16 queries, f16 K/V, f32 sigmoid gate fused in the "
+                               f"epilogue, bf16 out; N(0,1)*0.5 seed {hex(seed)}; {n_sets} rotating input sets "
+                               f"(> 256 MB MALL)",
+                   "tokens": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd},
+        "roofline": {"bound": "mfma", "kernel": "prefill_kernel<%d>" % hd, "achieved": achieved / 1e12,
+                     "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s", "frac": achieved / MFMA_F16_PEAK,
+                     "flops_per_launch": flops, "launch_ms": kern_ms, "traffic": traffic_of(f"gated{L}")},
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_gated_prefill(last, k, v, L, nh, nkv, hd)
+    return res
+
+
 def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool):
     """o_proj x += W_o . att over B tokens, f16 weights; att f32 for one
     decode token (the engine's att_out), f16 for a prefill batch (the prefill
@@ -619,6 +712,70 @@ def cpu_prefill(q, k, v, out, L, nh, nkv, hd):
             "seconds": dt, "parity_rel_l2": rel_l2(out.cpu().numpy(), want)}
 
 
+def cpu_kvstore(kv_set, L, nkv, hd):
+    """The reference's store is the scalar f32_to_f16 per element
+    (engine.c:1068-1072, platform.c:340-379); the oracle's restatement runs
+    over all rows until ~2 s of CPU work.  The GPU cache's K rows and V tiles
+    are compared bit for bit with it."""
+    O = _oracle()
+    torch = sys.modules["torch"]
+    k, v, cache = kv_set
+    kn, vn = k.cpu().numpy(), v.cpu().numpy()
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        kc = O.f32_to_f16(kn)
+        vc = O.f32_to_f16(vn)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt > 2.0:
+            break
+    torch.cuda.synchronize()
+    kvd = nkv * hd
+    gk = cache.k.view(torch.int16).cpu().numpy().view(np.uint16)[:, :L, :].transpose(1, 0, 2).reshape(L, kvd)
+    gv = (cache.v.view(torch.int16).cpu().numpy().view(np.uint16)  # [nkv][L/32][hd][32]
+          .transpose(1, 3, 0, 2).reshape(-1, nkv, hd)[:L].reshape(L, kvd))
+    same = bool(np.array_equal(gk, kc.reshape(L, kvd)) and np.array_equal(gv, vc.reshape(L, kvd)))
+    cores, model = _host_desc(O)
+    return {"value": kvstore_bytes(L, nkv, hd) * n / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"the whole workload ({L} rows, K and V), {n} passes, {dt:.2f} s, single thread as the "
+                      f"reference's loop; {model}", "seconds": dt, "parity_bit_exact": same}
+
+
+def cpu_gated_prefill(gset, k, v, L, nh, nkv, hd):
+    """The oracle (OpenMP over heads, as the reference) on the last 64 query
+    rows (the longest key ranges), the sigmoid gate applied as engine.c:959-960;
+    FLOP/s from the sample's own causal work."""
+    O = _oracle()
+    from oracle_lib import rel_l2
+
+    torch = sys.modules["torch"]
+    q, _, gate, out = gset
+    S = 64
+    p0 = L - S
+    qn = q[p0:].float().cpu().numpy()
+    kc = O.f32_to_f16(k.float().cpu().numpy())
+    vc = O.f32_to_f16(v.float().cpu().numpy())
+    t0 = time.perf_counter()
+    want = O.prefill(qn, kc, vc, p0, S, nh, nkv, hd)
+    want = O.gate_sigmoid(want.ravel(), gate[p0:].cpu().numpy().ravel())
+    dt = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    got = out[p0:].float().cpu().numpy().ravel()
+    from yllm_amd.attention import round_bf16
+
+    cores, model = _host_desc(O)
+    flops = prefill_flops(S, nh, hd, p0)
+    # the output is bf16: against the f32 oracle the error includes bf16's own
+    # rounding (2^-9 relative); against the oracle rounded to bf16 it is the
+    # kernel's
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"query rows {p0}..{L - 1} (the last {S}, all heads, keys 0..row), one pass, {dt:.2f} s; "
+                      f"effective parallelism <= {nh} heads; {model}",
+            "seconds": dt, "parity_rel_l2": rel_l2(got, want),
+            "parity_rel_l2_vs_bf16_rounded": rel_l2(got, round_bf16(np.array(want, np.float32, copy=True)))}
+
+
 def cpu_rope(rope_set, L, nh, nkv, hd, theta):
     """The oracle's per-token loop (the reference's engine.c:1054-1072 is
     single-threaded) over a sample of tokens spread over the positions; the
@@ -765,7 +922,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="prefill2k",
                     choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch", "gdn4k",
-                             "rope8k", "oproj8k", "oproj1", "hybrid"])
+                             "rope8k", "oproj8k", "oproj1", "kvstore8k", "gated4k", "hybrid"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k / gdn4k secondary lines")
     ap.add_argument("--gdn-tokenwise", action="store_true",
@@ -809,12 +966,18 @@ def main() -> int:
         res = run_oproj(8192, 4096, 4096, args.steps, args.warmup, cpu)
     elif w == "oproj1":
         res = run_oproj(1, 4096, 4096, args.steps, args.warmup, cpu)
+    elif w == "kvstore8k":
+        res = run_kvstore(8192, 8, 128, args.steps, args.warmup, cpu)
+    elif w == "gated4k":
+        res = run_gated_prefill(4096, 16, 2, 256, args.steps, args.warmup, cpu)
     elif w == "hybrid":
         res = run_hybrid(args.steps, args.warmup)
     else:
         res = run_decode_batch(32, 8, 128, 64, args.steps, args.warmup)
     dtype = {"gdn4k": "f32", "rope8k": "f32 rotation, f16 stores", "oproj8k": "f16 MFMA, f32 accumulate",
-             "oproj1": "f16 weights, f32 activations and accumulate", "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}.get(
+             "oproj1": "f16 weights, f32 activations and accumulate",
+             "kvstore8k": "f32 -> f16 (reference rounding)",
+             "gated4k": "bf16 q, f16 K/V MFMA, f32 accumulate/softmax, bf16 out", "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}.get(
         w, "f16 MFMA, f32 accumulate/softmax")
 
     line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,

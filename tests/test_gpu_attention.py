@@ -79,6 +79,40 @@ def test_kv_store_bits_match_reference_rounding(cuda, oracle, golden, src):
     assert not Kb[:, rows:].any() and not Vb[:, :, rows:].any()
 
 
+@pytest.mark.parametrize("src", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("ps,B", [(37, 100), (64, 64), (5, 250)])
+def test_kv_store_block_kernel_matches_element_path(cuda, oracle, src, ps, B):
+    """The bulk store over 64-position blocks (16-byte aligned sources) and
+    the element-wise path (a source one element off 16-byte alignment) write
+    the same bits, those of the reference rounding, and nothing outside
+    positions ps..ps+B-1."""
+    from yllm_amd.attention import LayerKV, kv_store
+
+    n_kv, hd = 2, 128
+    kvd = n_kv * hd
+    K, V = gen(71 + B, (B, kvd), 2.0, f16=False), gen(72 + B, (B, kvd), 2.0, f16=False)
+    kt, vt = torch.from_numpy(K).to(cuda).to(src), torch.from_numpy(V).to(cuda).to(src)
+    # the same rows at a data pointer 2 or 4 bytes past a 16-byte boundary
+    kb = torch.empty(B * kvd + 1, dtype=src, device=cuda)
+    vb = torch.empty(B * kvd + 1, dtype=src, device=cuda)
+    kb[1:].copy_(kt.reshape(-1))
+    vb[1:].copy_(vt.reshape(-1))
+    km, vm = kb[1:].view(B, kvd), vb[1:].view(B, kvd)
+    assert km.data_ptr() % 16 != 0
+    blk, elt = LayerKV.empty(n_kv, hd, ps + B + 30, device=cuda), LayerKV.empty(n_kv, hd, ps + B + 30, device=cuda)
+    kv_store(blk, kt, vt, ps)
+    kv_store(elt, km, vm, ps)
+    torch.cuda.synchronize()
+    assert torch.equal(blk.k, elt.k) and torch.equal(blk.v, elt.v)
+    Kb, Vb = cache_bits(blk)
+    Kx, Vx = kt.float().cpu().numpy(), vt.float().cpu().numpy()
+    Kw, Vw = engine_to_headmajor(oracle.f32_to_f16(Kx), oracle.f32_to_f16(Vx), n_kv, hd, -(-B // 64) * 64)
+    assert np.array_equal(Kb[:, ps:ps + B], Kw[:, :B])
+    assert np.array_equal(untile_v(Vb)[:, :, ps:ps + B], untile_v(Vw)[:, :, :B])
+    assert not Kb[:, :ps].any() and not Kb[:, ps + B:].any()
+    assert not untile_v(Vb)[:, :, :ps].any() and not untile_v(Vb)[:, :, ps + B:].any()
+
+
 @pytest.mark.parametrize("src", [torch.float32, torch.bfloat16])
 def test_kv_store_few_rows_matches_bulk(cuda, src):
     """Appending 1-3 rows at a time (the one-launch path) writes the same bits

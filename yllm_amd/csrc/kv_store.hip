@@ -60,6 +60,79 @@ __global__ __launch_bounds__(256) void v_store_kernel(uint16_t* __restrict__ vc,
     }
 }
 
+// Bulk store, K and V in one launch.  A workgroup owns 64 destination
+// positions (aligned to 64, so a V group of 8 positions never straddles a
+// 32-position tile) times 64 dimensions of one kv head.  Each thread takes
+// groups of 8 consecutive dimensions of a row: two 16-byte f32 loads (or
+// one f16 / bf16 load), the reference rounding, one 16-byte K store; the V
+// group goes through LDS, from which groups of 8 consecutive positions of
+// one dimension are read back and stored as 16 bytes into the tile.
+// Positions outside [pos_start, pos_start + B) are neither read nor
+// written.  Sources are 16-byte aligned rows of n_kv * D elements.
+template <uint32_t DT>
+__global__ __launch_bounds__(256) void kv_block_kernel(uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                       const void* __restrict__ k, const void* __restrict__ v,
+                                                       uint32_t pos_start, uint32_t B, uint32_t n_kv, uint32_t D,
+                                                       uint32_t kv_stride)
+{
+    __shared__ uint16_t tv[64][72];  // [position][dimension], rows 144 bytes apart
+    const uint32_t kv_dim = n_kv * D;
+    const uint32_t j0 = blockIdx.x * 64u;                          // first dimension (one kv head)
+    const uint32_t p0 = (pos_start & ~63u) + blockIdx.y * 64u;     // first destination position
+    const uint32_t h = j0 / D, d0 = j0 - h * D;
+    typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+    auto load8 = [&](const void* src, size_t off, u16x8& out) {
+        if constexpr (DT == kF32) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(src) + off);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(src) + off + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                out[e] = f32_to_f16_ref(a[e]);
+                out[e + 4] = f32_to_f16_ref(b[e]);
+            }
+        } else {
+            const u16x8 w = *reinterpret_cast<const u16x8*>(reinterpret_cast<const uint16_t*>(src) + off);
+            if constexpr (DT == kF16) {
+                out = w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) out[e] = f32_to_f16_ref(bf16_bits_to_f32(w[e]));
+            }
+        }
+    };
+#pragma unroll
+    for (uint32_t it = 0; it < 2; ++it) {
+        const uint32_t g = threadIdx.x + 256u * it;  // row g / 8, dimensions 8 (g % 8) ..
+        const uint32_t r = g >> 3, c = (g & 7u) * 8u;
+        const uint32_t pos = p0 + r;
+        if (pos < pos_start || pos >= pos_start + B) continue;
+        const size_t off = (size_t)(pos - pos_start) * kv_dim + j0 + c;
+        u16x8 kb, vb;
+        load8(k, off, kb);
+        load8(v, off, vb);
+        *reinterpret_cast<u16x8*>(kc + k_index(h, pos, d0 + c, D, kv_stride)) = kb;
+        *reinterpret_cast<u16x8*>(&tv[r][c]) = vb;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t it = 0; it < 2; ++it) {
+        const uint32_t g = threadIdx.x + 256u * it;  // dimension g / 8, positions 8 (g % 8) ..
+        const uint32_t dl = g >> 3, r0 = (g & 7u) * 8u;
+        const uint32_t pos0 = p0 + r0;
+        u16x8 w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = tv[r0 + e][dl];
+        uint16_t* dst = vc + v_index(h, pos0, d0 + dl, D, kv_stride);
+        if (pos0 >= pos_start && pos0 + 8u <= pos_start + B) {
+            *reinterpret_cast<u16x8*>(dst) = w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (pos0 + e >= pos_start && pos0 + e < pos_start + B) dst[e] = w[e];
+        }
+    }
+}
+
 // A few rows (decode appends one per step): K and V elements in one launch,
 // one thread per (row, element); the V writes are 2-byte scatters into the
 // tiles, which is cheap at this size and saves the second launch.
@@ -128,6 +201,21 @@ hipError_t launch_kv_store(uint16_t* kc, uint16_t* vc, const void* k, const void
     dim3 gk((uint32_t)(((uint64_t)B * kv_dim + 255u) / 256u));
     if (B <= 4) {
         hipLaunchKernelGGL(kv_rows_kernel, gk, dim3(256), 0, st, kc, vc, k, v, dt, pos_start, B, n_kv, D, kv_stride);
+        return hipGetLastError();
+    }
+    const bool aligned = ((uintptr_t)k % 16u) == 0 && ((uintptr_t)v % 16u) == 0 && ((uintptr_t)kc % 16u) == 0 &&
+                         ((uintptr_t)vc % 16u) == 0;
+    if (aligned && D % 64u == 0) {
+        // K and V in one launch, 64 aligned destination positions x 64 dimensions per workgroup
+        const dim3 gb(kv_dim / 64u, ((pos_start & 63u) + B + 63u) / 64u);
+        switch (dt) {
+        case kF32: hipLaunchKernelGGL(kv_block_kernel<kF32>, gb, dim3(256), 0, st, kc, vc, k, v, pos_start, B, n_kv,
+                                      D, kv_stride); break;
+        case kF16: hipLaunchKernelGGL(kv_block_kernel<kF16>, gb, dim3(256), 0, st, kc, vc, k, v, pos_start, B, n_kv,
+                                      D, kv_stride); break;
+        default: hipLaunchKernelGGL(kv_block_kernel<kBF16>, gb, dim3(256), 0, st, kc, vc, k, v, pos_start, B, n_kv,
+                                    D, kv_stride); break;
+        }
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_store_kernel, gk, dim3(256), 0, st, kc, k, dt, pos_start, B, n_kv, D,
