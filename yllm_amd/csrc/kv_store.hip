@@ -230,15 +230,8 @@ hipError_t launch_kv_from_engine(uint16_t* kc, uint16_t* vc, const uint16_t* ek,
                                  uint32_t rows, uint32_t n_kv, uint32_t D, uint32_t kv_stride,
                                  hipStream_t st)
 {
-    const uint32_t kv_dim = n_kv * D;
-    dim3 gk((uint32_t)(((uint64_t)rows * kv_dim + 255u) / 256u));
-    hipLaunchKernelGGL(k_copy_kernel, gk, dim3(256), 0, st, kc, const_cast<uint16_t*>(ek), rows, n_kv,
-                       D, kv_stride, 0);
-    // f16 bits through the same tiler as the store (f16 sources are copied)
-    dim3 gv((kv_dim + 63u) / 64u, (rows + 63u) / 64u);
-    hipLaunchKernelGGL(v_store_kernel, gv, dim3(256), 0, st, vc, (const void*)ev, kF16, kv_dim, 0u, rows, n_kv,
-                       D, kv_stride);
-    return hipGetLastError();
+    // f16 engine rows are a store of f16 sources (their bits are copied)
+    return launch_kv_store(kc, vc, ek, ev, kF16, 0u, rows, n_kv, D, kv_stride, st);
 }
 
 hipError_t launch_kv_to_engine(uint16_t* ek, uint16_t* ev, const uint16_t* kc, const uint16_t* vc,
