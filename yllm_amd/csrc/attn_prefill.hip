@@ -5,15 +5,17 @@
 // keys 0..pos_start+b; scores scaled by 1/sqrt(d); softmax; weighted V),
 // with the optional qwen35 sigmoid gate (engine.c:959-960).
 //
-// Tiling.  A workgroup owns 128 consecutive queries of one query head; each
-// of its 4-wave key groups (one or two, see prefill_groups) gives wave w 32
-// of them.  Keys stream through LDS in tiles of 64 (K rows [64][D] and V^T
-// [D][64], straight from the cache layout), loaded from HBM directly into
-// LDS -- K two tiles ahead, V one -- as unpadded rows with XOR-swizzled
-// 16-byte chunks.  With two groups, group g takes tiles g, g+2, ... and
-// the partial (max, sum, O) of the groups merge through LDS at the end.
-// Workgroups are issued heaviest (latest queries) first so the causal
-// triangle drains evenly.
+// Tiling.  A work item is 128 consecutive queries of one query head; each
+// of the workgroup's 4-wave key groups (one or two, see prefill_groups)
+// gives wave w 32 of them.  Keys stream through LDS in tiles of 64 (K rows
+// [64][D] and V^T [D][64], straight from the cache layout), loaded from HBM
+// directly into LDS -- K two tiles ahead, V one -- as unpadded rows with
+// XOR-swizzled 16-byte chunks.  With two groups, group g takes tiles g,
+// g+2, ... and the partial (max, sum, O) of the groups merge through LDS at
+// the end.  Items are taken heaviest (latest queries) first so the causal
+// triangle drains evenly; with one 8-wave workgroup per CU the grid is the
+// resident workgroups, each walking its items in snake order with the next
+// item's first loads issued during the current item's last key step.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_f16), everything transposed so that a
 // lane owns one query for the whole kernel:
