@@ -137,6 +137,62 @@ def test_gdn_chunk_split_is_exact(cuda, chunked, cut):
     assert torch.equal(Sa, Sb)
 
 
+def test_gdn_chunk_long_ragged_split_is_exact(cuda, oracle):
+    """2100 tokens (33 chunks, the last one of 52 tokens) in one chunked call
+    give the bits of two calls of 1024 and 1076 tokens (a cut on a chunk
+    boundary), and match the oracle."""
+    from yllm_amd.gdn import gdn_chunk
+
+    T, cut, n_k, n_v, d = 2100, 1024, 4, 8, 64
+    q, k, v, alpha, beta_raw, S0 = inputs(0x91ECE, T, n_k, n_v, d, s0_scale=0.02)
+    beta, gate = oracle_gates(oracle, alpha, beta_raw, np.zeros(n_v, np.float32), -np.ones(n_v, np.float32))
+    S_want, o_want, _, _ = oracle.gdn_sequence(S0.ravel(), q, k, v, gate, beta, T, n_k, d, n_v, d, EPS)
+    Sa, qd, kd, vd, gd, bd = to_dev(cuda, S0, q, k, v, gate, beta)
+    Sb = Sa.clone()
+    full = gdn_chunk(Sa, qd, kd, vd, gd, bd, n_k, EPS)
+    first = gdn_chunk(Sb, qd[:cut], kd[:cut], vd[:cut], gd[:cut].contiguous(), bd[:cut].contiguous(), n_k, EPS)
+    second = gdn_chunk(Sb, qd[cut:], kd[cut:], vd[cut:], gd[cut:].contiguous(), bd[cut:].contiguous(), n_k, EPS)
+    assert torch.equal(full, torch.cat([first, second]))
+    assert torch.equal(Sa, Sb)
+    assert rel_l2(full.cpu().numpy(), o_want) <= TOL
+    assert rel_l2(Sa.cpu().numpy().ravel(), S_want) <= TOL
+
+
+def test_gdn_chunk_graph_replays(cuda):
+    """The chunked form (gates in, workspace allocated inside the capture)
+    captured in a graph: every replay, with eager work and synchronisations
+    between them, gives the eager bits."""
+    from yllm_amd.gdn import gdn_chunk
+
+    T, n_k, n_v, d = 2304, 16, 16, 128
+    q, k, v, alpha, beta_raw, S0 = inputs(0x6A4F, T, n_k, n_v, d, s0_scale=0.02)
+    gate = -np.log1p(np.exp(alpha)).astype(np.float32)
+    beta = (1 / (1 + np.exp(-beta_raw))).astype(np.float32)
+    S_init, qd, kd, vd, gd, bd = to_dev(cuda, S0, q, k, v, gate, beta)
+    S = S_init.clone()
+    want = gdn_chunk(S, qd, kd, vd, gd, bd, n_k, EPS)
+    S_want = S.clone()
+    S.copy_(S_init)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        gdn_chunk(S, qd, kd, vd, gd, bd, n_k, EPS)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        got = gdn_chunk(S, qd, kd, vd, gd, bd, n_k, EPS)
+    for i in range(3):
+        S.copy_(S_init)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i}"
+        assert torch.equal(S, S_want), f"replay {i}"
+        junk = torch.randn(1 << 20, device=S.device)
+        torch.cuda.synchronize()
+        del junk
+
+
 @pytest.mark.parametrize("chunked", [False, True], ids=["tokenwise", "chunked"])
 def test_gdn_full_size_prefill(cuda, oracle, chunked):
     """The fifth configuration's GDN layer: 4096 tokens, 16 heads, d = 128."""

@@ -252,15 +252,20 @@ struct ChunkWs {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs a)
+__global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
 {
     constexpr int KP = D + 4;  // LDS row stride of the q / k rows (16-byte rows, staggered banks)
     constexpr int AP = kC + 4;
     constexpr int KQ = D / 4;  // contraction indices per lane group in the Gram MFMAs
+    // A shares its LDS with the q rows: once Q~ is written out and each wave
+    // holds its Gram rows of Q in registers, Qn is dead.  84 -> 68 KiB, two
+    // workgroups per CU.
+    static_assert(kC * AP <= kC * KP, "A must fit in the q rows");
     __shared__ float Kn[kC][KP];
-    __shared__ float Qn[kC][KP];
-    __shared__ float Am[kC][AP];
+    __shared__ float QA[kC * KP];
     __shared__ float sg[kC], sb[kC], sgam[kC], see[kC];
+    float(*Qn)[KP] = reinterpret_cast<float(*)[KP]>(QA);
+    float(*Am)[AP] = reinterpret_cast<float(*)[AP]>(QA);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -324,6 +329,15 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs a)
         __syncthreads();
     }
 
+    // Q~ = diag(gamma) Q (rows kC..2kC-1 of [W; Q~]) and K~ = diag(e) K
+    for (int e = tid; e < kC * D / 4; e += 256) {
+        const int t = e / (D / 4), i = (e % (D / 4)) * 4;
+        const f32x4 q = *reinterpret_cast<const f32x4*>(&Qn[t][i]);
+        const f32x4 k = *reinterpret_cast<const f32x4*>(&Kn[t][i]);
+        *reinterpret_cast<f32x4*>(w.WQ + (size_t)(kC + t) * D + i) = q * sgam[t];
+        *reinterpret_cast<f32x4*>(w.Kt + (size_t)t * D + i) = k * see[t];
+    }
+
     // Gram matrices K K^T and Q K^T; wave w owns token rows 16w..16w+15.
     // Lane group g contracts over d_k indices g*KQ .. g*KQ+KQ-1.
     {
@@ -338,6 +352,7 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs a)
                 aq[kb + e] = y[e];
             }
         }
+        __syncthreads();  // every read of Qn is done: A may overwrite it
         for (int cb = 0; cb < kC / 16; ++cb) {
             // four independent accumulators per product keep the MFMA pipe full
             f32x4 skk[4], sqk[4];
@@ -404,15 +419,6 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs a)
         float* dst = col < D ? w.U + col : w.WQ + (col - D);
 #pragma unroll
         for (int t = 0; t < kC; ++t) dst[(size_t)t * D] = X[t];
-    }
-
-    // Q~ = diag(gamma) Q (rows kC..2kC-1 of [W; Q~]) and K~ = diag(e) K
-    for (int e = tid; e < kC * D / 4; e += 256) {
-        const int t = e / (D / 4), i = (e % (D / 4)) * 4;
-        const f32x4 q = *reinterpret_cast<const f32x4*>(&Qn[t][i]);
-        const f32x4 k = *reinterpret_cast<const f32x4*>(&Kn[t][i]);
-        *reinterpret_cast<f32x4*>(w.WQ + (size_t)(kC + t) * D + i) = q * sgam[t];
-        *reinterpret_cast<f32x4*>(w.Kt + (size_t)t * D + i) = k * see[t];
     }
 }
 
