@@ -479,6 +479,12 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(GdnArgs a)
     };
     Ops cur, nxt;
     load_ops(cur, 0);
+    // The first chunk's operands are complete before the loop.  Otherwise the
+    // compiler's wait insertion, merging the loop entry with the back edge,
+    // puts a wait for them into phase 1 of every iteration, where it also
+    // waits for the next chunk's operands issued just before (one memory
+    // latency per chunk).
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
 
     for (uint32_t c = 0; c < a.n_chunks; ++c) {
