@@ -98,7 +98,8 @@ int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
  * multi-sequence form of the same computation.
  *   kcaches/vcaches: device arrays [n_seq] of device pointers, each one
  *                    sequence's layer cache in the layout above;
- *   lens:            device [n_seq], keys per sequence (>= 1);
+ *   lens:            device [n_seq], keys per sequence (a sequence with 0
+ *                    keys gets a zero output row);
  *   max_len, total_len: host values, the maximum and the sum of lens (they
  *                    size the split; max_len must bound every lens[i]);
  *   q/att_out rows:  q_stride / out_stride floats apart per sequence;
@@ -111,11 +112,16 @@ int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
                            uint32_t kv_stride, const float* gate, uint32_t gate_stride,
                            void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes the two decode entry points need for these shapes (0 when
- * the context is short enough for one split).  It holds the per-split
- * partial results; no initialisation is needed, and one workspace can serve
- * calls of any shape that fits, provided they do not run concurrently (e.g.
- * on two streams). */
+/* Workspace bytes for the decode entry points (0 when the context is short
+ * enough for one split).  It holds the per-split partial results and needs
+ * no initialisation.  For n_seq = 1 the size serves yhip_attn_decode at
+ * every pos < max_len (and the batch form with one sequence of at most
+ * max_len keys), so one workspace sized for the engine's max_seq lasts a
+ * whole generation.  For n_seq > 1 it is what a batch call with exactly
+ * these n_seq, max_len and total_len needs (the split plan depends on all
+ * three; a call checks its own need and returns YHIP_ENOSPC when the
+ * workspace is short).  Calls that share a workspace must not run
+ * concurrently (e.g. on two streams). */
 size_t yhip_attn_decode_workspace(uint32_t n_seq, uint32_t max_len, uint64_t total_len,
                                   uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
 

@@ -66,10 +66,23 @@ def test_decode_rejects_null_and_range(hiplib):
 def test_decode_workspace_is_checked(hiplib):
     need = hiplib.yhip_attn_decode_workspace(1, 100000, 100000, 32, 8, 128)
     assert need > 0
-    rc = hiplib.yhip_attn_decode(P, P, P, P, 99999, 32, 8, 128, 131072, None, P, need - 1, None)
+    rc = hiplib.yhip_attn_decode(P, P, P, P, 99999, 32, 8, 128, 131072, None, P, 4096, None)
     assert rc == -28 and "workspace" in _err(hiplib)
     # a short context needs no split and no workspace
     assert hiplib.yhip_attn_decode_workspace(1, 64, 64, 32, 8, 128) == 0
+
+
+@pytest.mark.parametrize("nh,nkv,hd,max_len", [(32, 8, 128, 4352), (28, 4, 128, 10000), (16, 2, 256, 4352),
+                                               (14, 2, 64, 512), (32, 8, 128, 131072)])
+def test_decode_workspace_serves_every_shorter_position(hiplib, nh, nkv, hd, max_len):
+    """A single-sequence workspace sized for max_len serves every shorter call:
+    the size never shrinks as max_len grows, although the split count is not
+    monotone in the length (4352 keys at 32/8 split 17 ways, 4096 keys 32
+    ways).  The engine sizes one workspace for max_seq."""
+    ws = hiplib.yhip_attn_decode_workspace
+    sizes = np.array([ws(1, L, L, nh, nkv, hd) for L in range(1, max_len + 1, 1 if max_len <= 20000 else 61)])
+    assert (np.diff(sizes.astype(np.int64)) >= 0).all()
+    assert sizes[-1] == ws(1, max_len, max_len, nh, nkv, hd)
 
 
 def test_prefill_rejects_bad_args(hiplib):

@@ -243,6 +243,64 @@ def test_decode_workspace_reuse_across_calls(cuda, oracle):
         assert err <= TOL
 
 
+def test_decode_workspace_for_max_len_serves_every_position(cuda, oracle):
+    """The engine sizes one decode workspace for max_seq and decodes at every
+    position below it.  The split count is not monotone in the length (at
+    32/8 heads, 4352 keys split 17 ways and 4096 keys 32 ways), so a
+    workspace of yhip_attn_decode_workspace(1, 4352, ...) must serve every
+    shorter call: each C call below gets exactly that many bytes."""
+    from yllm_amd._lib import check, lib
+    from yllm_amd.attention import decode_workspace, decode_workspace_bytes
+
+    nh, nkv, hd, L = 32, 8, 128, 4352
+    kvd = nkv * hd
+    K, V = gen(41, (L, kvd)), gen(42, (L, kvd))
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    nbytes = decode_workspace_bytes(1, L, L, nh, nkv, hd)
+    ws = decode_workspace(nbytes, cuda)
+    q = gen(43, (nh * hd,), f16=False)
+    qt = torch.from_numpy(q).to(cuda)
+    out = torch.empty(nh * hd, dtype=torch.float32, device=cuda)
+    stream = torch.cuda.current_stream().cuda_stream
+    for n in range(2900, L + 1):
+        check(lib().yhip_attn_decode(out.data_ptr(), qt.data_ptr(), cache.k.data_ptr(), cache.v.data_ptr(), n - 1, nh,
+                                     nkv, hd, cache.kv_stride, None, ws.data_ptr(), nbytes, stream))
+        if n in (2900, 3000, 4096, 4097, 4224, L):
+            want = oracle.decode(q, kc[:n], vc[:n], n - 1, nh, nkv, hd)
+            err = rel_l2(out.cpu().numpy(), want)
+            assert err <= TOL, f"{n} keys: rel_l2 {err:.3e}"
+
+
+@pytest.mark.parametrize("max_len", [100, 5000])
+def test_decode_batch_empty_sequence_gives_zeros(cuda, oracle, max_len):
+    """A sequence with no keys gets a zero output row, with one split
+    (max_len 100) as with several (5000), gated or not."""
+    from yllm_amd.attention import DecodeBatch, LayerKV, attn_decode_batch, kv_store
+
+    nh, nkv, hd = 8, 2, 128
+    kvd = nkv * hd
+    lens = [max_len, 0, 37]
+    caches, wants, qs = [], [], []
+    gate = gen(49, (3, nh * hd), 1.0, f16=False)
+    for i, L in enumerate(lens):
+        K, V = gen(450 + i, (max(L, 1), kvd)), gen(550 + i, (max(L, 1), kvd))
+        q = gen(650 + i, (nh * hd,), f16=False)
+        c = LayerKV.empty(nkv, hd, max_len, device=cuda)
+        kv_store(c, torch.from_numpy(K).to(cuda), torch.from_numpy(V).to(cuda), 0)
+        caches.append(c)
+        qs.append(q)
+        wants.append(None if L == 0 else
+                     oracle.decode(q, oracle.f32_to_f16(K[:L]), oracle.f32_to_f16(V[:L]), L - 1, nh, nkv, hd))
+    for g in (None, torch.from_numpy(gate).to(cuda)):
+        out = torch.full((3, nh * hd), float("nan"), device=cuda)
+        attn_decode_batch(torch.from_numpy(np.stack(qs)).to(cuda), DecodeBatch(caches), lens, nh, gate=g, out=out)
+        got = out.cpu().numpy()
+        assert (got[1] == 0).all()
+        for i in (0, 2):
+            want = wants[i] if g is None else oracle.gate_sigmoid(wants[i], gate[i])
+            assert rel_l2(got[i], want) <= TOL
+
+
 def test_decode_long_context_full_size(cuda, oracle):
     """Config 4 decode at its full size: 131072 keys, 32q/8kv, d=128 (split-K + LSE merge)."""
     from yllm_amd.attention import attn_decode

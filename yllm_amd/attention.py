@@ -251,7 +251,7 @@ def attn_decode_batch(q: torch.Tensor, batch: DecodeBatch, lens: list[int] | np.
                       gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
                       workspace: torch.Tensor | None = None,
                       lens_dev: torch.Tensor | None = None) -> torch.Tensor:
-    """q: f32 [n_seq, n_heads*head_dim]; lens[i] keys for sequence i (>= 1)."""
+    """q: f32 [n_seq, n_heads*head_dim]; lens[i] keys for sequence i (0: a zero output row)."""
     _need_gpu(q, gate)
     n_seq = len(batch.caches)
     d = batch.head_dim

@@ -111,20 +111,21 @@ int yhip_kv_to_engine(uint16_t* eng_k, uint16_t* eng_v, const uint16_t* kcache,
 size_t yhip_attn_decode_workspace(uint32_t n_seq, uint32_t max_len, uint64_t total_len,
                                   uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim)
 {
-    uint32_t sk, ns;
     if (n_kv_heads == 0) return 0;
-    return yhip::decode_plan(n_seq, max_len, total_len, n_heads, n_kv_heads, head_dim, &sk, &ns);
+    return yhip::decode_workspace_bound(n_seq, max_len, total_len, n_heads, n_kv_heads, head_dim);
 }
 
-int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
-                           uint32_t q_stride, const uint16_t* const* kcaches,
-                           const uint16_t* const* vcaches, const uint32_t* lens,
-                           uint32_t n_seq, uint32_t max_len, uint64_t total_len,
-                           uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                           uint32_t kv_stride, const float* gate, uint32_t gate_stride,
-                           void* workspace, size_t workspace_bytes, void* stream)
+}  // extern "C"
+
+namespace yhip {
+
+int decode_batch_common(const char* fn, float* att_out, uint32_t out_stride, const float* q, uint32_t q_stride,
+                        const uint16_t* const* kcaches, const uint16_t* const* vcaches, const uint32_t* lens,
+                        uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
+                        uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride, const float* gate,
+                        uint32_t gate_stride, void* workspace, size_t workspace_bytes, const char* ws_name,
+                        void* stream)
 {
-    const char* fn = "yhip_attn_decode_batch";
     if (!att_out || !q || !kcaches || !vcaches || !lens) return fail(YHIP_EINVAL, "%s: null pointer", fn);
     int rc = check_heads(fn, n_heads, n_kv_heads, head_dim, kv_stride);
     if (rc) return rc;
@@ -140,7 +141,8 @@ int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
     const size_t need = yhip::decode_plan(n_seq, max_len, total_len, n_heads, n_kv_heads, head_dim,
                                           &a.split_keys, &a.n_splits);
     if (need > 0 && (!workspace || workspace_bytes < need))
-        return fail(YHIP_ENOSPC, "%s: workspace %zu < %zu bytes", fn, workspace_bytes, need);
+        return fail(YHIP_ENOSPC, "%s: these shapes need %zu bytes of split partials, the %s holds %zu", fn, need,
+                    ws_name, workspace_bytes);
     a.q = q;
     a.kptrs = kcaches;
     a.vptrs = vcaches;
@@ -159,6 +161,26 @@ int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
     yhip::decode_bind_workspace(a, workspace);
     return done(yhip::launch_decode(a, (hipStream_t)stream), fn);
 }
+
+int api_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+
+}  // namespace yhip
+
+extern "C" {
+
+int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
+                           uint32_t q_stride, const uint16_t* const* kcaches,
+                           const uint16_t* const* vcaches, const uint32_t* lens,
+                           uint32_t n_seq, uint32_t max_len, uint64_t total_len,
+                           uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                           uint32_t kv_stride, const float* gate, uint32_t gate_stride,
+                           void* workspace, size_t workspace_bytes, void* stream)
+{
+    return yhip::decode_batch_common("yhip_attn_decode_batch", att_out, out_stride, q, q_stride, kcaches, vcaches, lens,
+                               n_seq, max_len, total_len, n_heads, n_kv_heads, head_dim, kv_stride, gate,
+                               gate_stride, workspace, workspace_bytes, "workspace", stream);
+}
+
 
 int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
                      const uint16_t* vcache, uint32_t pos, uint32_t n_heads,

@@ -82,12 +82,23 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     // a length beyond the planned maximum is clamped, never read past
     const uint32_t len = min(min(a.lens ? a.lens[seq] : a.len0, a.kv_stride), a.split_keys * a.n_splits);
     const uint32_t kbeg = split * a.split_keys;
-    if (kbeg >= len) return;  // uniform over the workgroup
-    const uint32_t kend = min(len, kbeg + a.split_keys);
     // query heads h with h*n_kv/n_heads == kvh form [h0, h1) (engine.c:1079)
     const uint32_t h0 = (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
     const uint32_t h1 = ((kvh + 1) * a.n_heads + a.n_kv - 1) / a.n_kv;
     const uint32_t G = h1 - h0;
+    if (kbeg >= len) {  // uniform over the workgroup
+        // a sequence without keys gets zeros (times the gate), as the merge
+        // kernel writes them when there are several splits
+        if (len == 0 && a.n_splits == 1)
+            for (uint32_t idx = threadIdx.x; idx < G * D; idx += kThreads) {
+                const uint32_t h = h0 + idx / D, d = idx % D;
+                float r = 0.0f;
+                if (a.gate) r *= sigmoid_ref(a.gate[(size_t)seq * a.gate_stride + (size_t)h * D + d]);
+                a.out[(size_t)seq * a.out_stride + (size_t)h * D + d] = r;
+            }
+        return;
+    }
+    const uint32_t kend = min(len, kbeg + a.split_keys);
 
     const uint16_t* K = (a.kptrs ? a.kptrs[seq] : a.k0) + k_index(kvh, 0, 0, D, a.kv_stride);
     const uint16_t* Vt = (a.vptrs ? a.vptrs[seq] : a.v0) + v_index(kvh, 0, 0, D, a.kv_stride);
@@ -380,6 +391,40 @@ size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 }  // namespace
 
+namespace {
+
+// The plan's two tunables: the workgroup target of a launch and the smallest
+// split (a multiple of 128 keys).  YHIP_DECODE_WG / YHIP_DECODE_MINSK
+// override them for tuning sweeps.
+uint64_t plan_target_wg(uint32_t n_seq)
+{
+    static const long env_wg = [] {
+        const char* e = getenv("YHIP_DECODE_WG");
+        return e ? atol(e) : 0L;
+    }();
+    return env_wg > 0 ? (uint64_t)env_wg : (n_seq == 1 ? 256 : 3072);
+}
+
+uint64_t plan_min_split()
+{
+    static const uint64_t min_sk = [] {
+        const char* e = getenv("YHIP_DECODE_MINSK");
+        const long v = e ? atol(e) : 0;
+        return (uint64_t)(v > 0 ? v : 128);
+    }();
+    return min_sk;
+}
+
+size_t partial_bytes(uint32_t n_seq, uint32_t n_splits, uint32_t n_heads, uint32_t n_kv, uint32_t D)
+{
+    if (n_splits <= 1) return 0;
+    const size_t gmax = (n_heads + n_kv - 1) / n_kv;
+    const size_t groups = (size_t)n_seq * n_kv;
+    return align256(groups * n_splits * gmax * 2 * sizeof(float)) + groups * n_splits * gmax * D * sizeof(float);
+}
+
+}  // namespace
+
 size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
                    uint32_t n_kv, uint32_t D, uint32_t* split_keys, uint32_t* n_splits)
 {
@@ -391,18 +436,8 @@ size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_
     // (64 sequences of 1k..32k keys: 4.5 TB/s at 2048 workgroups, 5.9 at
     // 3072).  A split is a multiple of 128 keys (one 32-key block per wave);
     // short contexts with few kv heads get splits down to 128 keys so they
-    // still spread over many CUs.  YHIP_DECODE_WG / YHIP_DECODE_MINSK
-    // override the workgroup target and the minimum split for tuning sweeps.
-    static const long env_wg = [] {
-        const char* e = getenv("YHIP_DECODE_WG");
-        return e ? atol(e) : 0L;
-    }();
-    static const uint64_t min_sk = [] {
-        const char* e = getenv("YHIP_DECODE_MINSK");
-        const long v = e ? atol(e) : 0;
-        return (uint64_t)(v > 0 ? v : 128);
-    }();
-    const uint64_t target_wg = env_wg > 0 ? (uint64_t)env_wg : (n_seq == 1 ? 256 : 3072);
+    // still spread over many CUs.
+    const uint64_t target_wg = plan_target_wg(n_seq), min_sk = plan_min_split();
     const uint64_t work = total_len * (uint64_t)n_kv;
     uint64_t sk = (work + target_wg - 1) / target_wg;
     if (sk < min_sk) sk = min_sk;
@@ -418,10 +453,29 @@ size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_
     }
     *split_keys = (uint32_t)sk;
     *n_splits = ns;
-    if (ns == 1) return 0;
-    const size_t gmax = (n_heads + n_kv - 1) / n_kv;
-    const size_t groups = (size_t)n_seq * n_kv;
-    return align256(groups * ns * gmax * 2 * sizeof(float)) + groups * ns * gmax * D * sizeof(float);
+    return partial_bytes(n_seq, ns, n_heads, n_kv, D);
+}
+
+size_t decode_workspace_bound(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
+                              uint32_t n_kv, uint32_t D)
+{
+    uint32_t sk, ns;
+    const size_t exact = decode_plan(n_seq, max_len, total_len, n_heads, n_kv, D, &sk, &ns);
+    if (n_seq != 1) return exact;
+    // Every single-sequence call with len <= max_len: the split size is at
+    // least len*n_kv/target, at least the minimum split and at least
+    // len/kMaxSplits, so the split count is at most the smallest of
+    // target/n_kv, max_len/min split and kMaxSplits (rounded up).  The count
+    // itself is not monotone in len (the split size is rounded up to 128
+    // keys), so a workspace sized for max_len alone can be too small for a
+    // shorter call.
+    const uint64_t target_wg = plan_target_wg(1), min_sk = plan_min_split();
+    uint64_t nsb = (target_wg + n_kv - 1) / n_kv;
+    const uint64_t by_len = ((uint64_t)max_len + min_sk - 1) / min_sk;
+    if (by_len < nsb) nsb = by_len;
+    if (nsb > kMaxSplits) nsb = kMaxSplits;
+    const size_t bound = partial_bytes(1, (uint32_t)nsb, n_heads, n_kv, D);
+    return bound > exact ? bound : exact;
 }
 
 void decode_bind_workspace(DecodeArgs& a, void* workspace)

@@ -40,9 +40,26 @@ constexpr uint32_t kMaxSplits = 256;
 // Split plan for the shapes; returns the workspace bytes (0 without splits).
 size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
                    uint32_t n_kv, uint32_t D, uint32_t* split_keys, uint32_t* n_splits);
+// Workspace bytes that serve the shapes: for one sequence, every call with
+// len <= max_len (the split count is not monotone in len); for a batch, the
+// call's own plan.
+size_t decode_workspace_bound(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
+                              uint32_t n_kv, uint32_t D);
 // carve the workspace into part_ml / part_o for a plan
 void decode_bind_workspace(DecodeArgs& a, void* workspace);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
+
+// ---- api.hip ----
+// The checks, plan and launches of yhip_attn_decode_batch with the partials
+// in `workspace` of workspace_bytes (ws_name names it in the error message).
+int decode_batch_common(const char* fn, float* att_out, uint32_t out_stride, const float* q, uint32_t q_stride,
+                        const uint16_t* const* kcaches, const uint16_t* const* vcaches, const uint32_t* lens,
+                        uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_t n_heads,
+                        uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride, const float* gate,
+                        uint32_t gate_stride, void* workspace, size_t workspace_bytes, const char* ws_name,
+                        void* stream);
+// sets the per-thread message of yhip_last_error and returns code
+int api_fail(int code, const char* msg);
 
 // ---- attn_prefill.hip ----
 struct PrefillArgs {
