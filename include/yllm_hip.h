@@ -112,6 +112,24 @@ int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
                            uint32_t kv_stride, const float* gate, uint32_t gate_stride,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* yhip_attn_decode_batch without a workspace: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops that forbid hipMalloc): the split-K partials
+ * go to a fixed scratch array of YHIP_DECODE_SCRATCH_BYTES that the library
+ * holds on each GPU it runs on until the process ends, and the call itself
+ * allocates nothing.  Arguments, checks and results are those of
+ * yhip_attn_decode_batch; shapes whose partials exceed the scratch return
+ * YHIP_ENOSPC (use yhip_attn_decode_batch with a workspace for them).  All
+ * calls on one GPU share its scratch: calls that overlap on one GPU (two
+ * streams, two host threads) race; serialise them.  The first call on each
+ * device resolves the scratch's address there. */
+#define YHIP_DECODE_SCRATCH_BYTES (16u << 20)
+int yhip_attn_decode_batch_noalloc(float* att_out, uint32_t out_stride, const float* q, uint32_t q_stride,
+                                   const uint16_t* const* kcaches, const uint16_t* const* vcaches,
+                                   const uint32_t* lens, uint32_t n_seq, uint32_t max_len, uint64_t total_len,
+                                   uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
+                                   const float* gate, uint32_t gate_stride, void* stream);
+
 /* Workspace bytes for the decode entry points (0 when the context is short
  * enough for one split).  It holds the per-split partial results and needs
  * no initialisation.  For n_seq = 1 the size serves yhip_attn_decode at
