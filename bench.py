@@ -58,9 +58,11 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
 MFMA_F16_PEAK = 2.5e15   # FLOP/s, dense f16/bf16 MFMA
+MFMA_F32_PEAK = 157.3e12  # FLOP/s, dense fp32 MFMA
 METRIC = "attn decode GB/s (% HBM peak); prefill attn TFLOP/s (% MFMA peak)"
 SEED = 0x5EED0000
 ROTATE_BYTES = 300 << 20  # rotating input sets exceed the 256 MB MALL (Infinity Cache)
+GDN_CHUNKED_KERNELS = "gdn_prep_kernel<%d> + gdn_scan_kernel<%d>"
 EAGER = False  # --eager: launch each step from the host (for counter collection)
 CHUNKED_GDN = True  # --gdn-tokenwise: time the token-by-token GDN kernel instead
 
@@ -260,7 +262,7 @@ def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, step
     return res
 
 
-def run_decode_batch(nh: int, nkv: int, hd: int, n_seq: int, steps: int, warmup: int):
+def run_decode_batch(nh: int, nkv: int, hd: int, n_seq: int, steps: int, warmup: int, cpu: bool):
     import torch
 
     from yllm_amd.attention import (DecodeBatch, LayerKV, attn_decode_batch, decode_workspace,
@@ -293,7 +295,7 @@ def run_decode_batch(nh: int, nkv: int, hd: int, n_seq: int, steps: int, warmup:
                                                          lens_dev=lens_dev), steps, warmup, out)
     nbytes = float(lens.sum()) * kvd * 2 * 2 + 2.0 * n_seq * nh * hd * 4
     achieved = nbytes / (kern_ms * 1e-3)
-    return {
+    res = {
         "value": nbytes / (ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms,
         "tokens_per_s": n_seq / (ms * 1e-3),
         "config": {"workload": f"batched decode, {n_seq} sequences, lengths U[1024,32768] (sum {int(lens.sum())}), "
@@ -304,6 +306,9 @@ def run_decode_batch(nh: int, nkv: int, hd: int, n_seq: int, steps: int, warmup:
                      "frac": achieved / HBM_PEAK, "bytes_per_launch": nbytes, "launch_ms": kern_ms,
                      "traffic": traffic_of("decode_batch")},
     }
+    if cpu:
+        res["cpu_baseline"] = cpu_decode_batch(q, caches, lens, out, nh, nkv, hd)
+    return res
 
 
 def gdn_bytes(T: int, n_k: int, n_v: int, d: int) -> float:
@@ -350,7 +355,11 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
     ms, kern_ms = time_steps(step, steps, warmup, sets[(warmup + steps - 1) % n_sets][5])
     out = sets[(warmup + steps - 1) % n_sets][5]
     nbytes, flops = gdn_bytes(T, n_h, n_h, d), gdn_flops(T, n_h, d)
-    t_roof = max(nbytes / HBM_PEAK, flops / MFMA_F16_PEAK)
+    # the arithmetic is fp32 (the reference's type): bound by the fp32 MFMA
+    # peak or by HBM, whichever takes longer
+    t_mfma, t_hbm = flops / MFMA_F32_PEAK, nbytes / HBM_PEAK
+    t_roof = max(t_mfma, t_hbm)
+    kern_s = kern_ms * 1e-3
     res = {
         "value": T / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
         "config": {"workload": f"Gated DeltaNet layer prefill, {T} tokens, {n_h} heads, d_k = d_v = {d}, fp32, "
@@ -358,13 +367,16 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
                                f"gates + l2norm + recurrence ({'chunked' if CHUNKED_GDN else 'token by token'}); "
                                f"{n_sets} rotating input sets (> 256 MB MALL)",
                    "tokens": T, "heads": n_h, "head_dim": d},
-        "roofline": {"bound": "hbm",
-                     "kernel": ("gdn_prep_kernel<%d> + gdn_scan_kernel<%d>" % (d, d) if CHUNKED_GDN else
+        "roofline": {"bound": "mfma" if t_mfma >= t_hbm else "hbm",
+                     "kernel": (GDN_CHUNKED_KERNELS % (d, d) if CHUNKED_GDN else
                                 "gdn_kernel<%d>" % d) + " (+ gdn_gates_kernel)",
-                     "achieved": nbytes / (kern_ms * 1e-3) / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": t_roof / (kern_ms * 1e-3), "bytes_per_launch": nbytes, "flops_per_launch": flops,
+                     **({"achieved": flops / kern_s / 1e12, "peak": MFMA_F32_PEAK / 1e12, "unit": "TFLOP/s"}
+                        if t_mfma >= t_hbm else
+                        {"achieved": nbytes / kern_s / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s"}),
+                     "frac": t_roof / kern_s, "bytes_per_launch": nbytes, "flops_per_launch": flops,
                      "launch_ms": kern_ms, "traffic": traffic_of(f"gdn{T}"),
-                     "note": "frac = max(bytes/HBM peak, flops/MFMA peak) / measured time"},
+                     "note": "fp32 arithmetic: frac = max(bytes / 8 TB/s, flops / 157.3 TFLOP/s fp32 MFMA) / "
+                             "measured time; flops are the sequential form's 7*d^2 per head and token"},
         "gflops": flops / (ms * 1e-3) / 1e9,
     }
     if cpu:
@@ -567,7 +579,7 @@ def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool
     return res
 
 
-def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
+def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
     """The fifth configuration: one group of 3 Gated-DeltaNet layers and 1
     gated GQA attention layer, a 4096-token prefill then n_dec decode steps.
     A GDN layer's GPU part is conv1d + silu over its qkv rows, the gates, the
@@ -658,7 +670,7 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
 
     # one step is ~1300 launches: its graph is captured once and replayed
     ms, _ = time_steps(step, steps, warmup, dout, graph_per_step=True)
-    return {
+    res = {
         "value": L / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": L / (ms * 1e-3),
         "config": {"workload": f"qwen35 hybrid group: {n_gdn} Gated-DeltaNet layers ({hg} heads, d {dg}, fp32: "
                                f"conv1d width {kw} + silu, gates, l2norm + recurrence, gated RMSNorm) + "
@@ -670,6 +682,14 @@ def run_hybrid(steps: int, warmup: int, n_dec: int = 256):
                    "prefill_tokens": T, "decode_steps": n_dec},
         "roofline": None,
     }
+    if cpu:
+        torch.cuda.synchronize()
+        li = n_gdn - 1  # the shared output rows hold the last GDN layer's results
+        res["cpu_baseline"] = cpu_hybrid(
+            {k2: v2.cpu().numpy() for k2, v2 in gd[li].items()}, S[li].cpu().numpy(), gout.cpu().numpy(),
+            qkv.cpu().numpy(), at["gate"].cpu().numpy(), aout.float().cpu().numpy(), dout.cpu().numpy(),
+            T, n_dec, n_gdn, hg, dg, kw, nh, nkv, da)
+    return res
 
 
 # ---------------------------------------------------------------- CPU leg
@@ -695,21 +715,26 @@ def _host_desc(O) -> tuple[int, str]:
 
 
 def cpu_prefill(q, k, v, out, L, nh, nkv, hd):
-    """Full workload on the CPU oracle (OpenMP over heads, as the reference)."""
+    """The CPU oracle (OpenMP over heads, as the reference): the whole
+    workload up to 2048 tokens; beyond, the last 64 query rows (the longest
+    key ranges, ~10 s of the whole 8k pass's ~40 s would be too long for the
+    default run), FLOP/s from the sample's own causal work."""
     O = _oracle()
     from oracle_lib import rel_l2
 
-    qn = q.float().cpu().numpy()
+    p0 = 0 if L <= 2048 else L - 64
+    qn = q[p0:].float().cpu().numpy()
     kc = O.f32_to_f16(k.float().cpu().numpy())
     vc = O.f32_to_f16(v.float().cpu().numpy())
     t0 = time.perf_counter()
-    want = O.prefill(qn, kc, vc, 0, L, nh, nkv, hd)
+    want = O.prefill(qn, kc, vc, p0, L - p0, nh, nkv, hd)
     dt = time.perf_counter() - t0
     cores, model = _host_desc(O)
-    return {"value": prefill_flops(L, nh, hd) / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"the whole workload ({L} tokens, all heads), one pass, {dt:.2f} s; effective "
-                      f"parallelism <= {nh} heads; {model}",
-            "seconds": dt, "parity_rel_l2": rel_l2(out.cpu().numpy(), want)}
+    what = (f"the whole workload ({L} tokens, all heads)" if p0 == 0 else
+            f"query rows {p0}..{L - 1} (the last {L - p0}, all heads, keys 0..row)")
+    return {"value": prefill_flops(L - p0, nh, hd, p0) / dt / 1e12, "unit": "TFLOP/s", "cores": cores,
+            "kind": "port", "sample": f"{what}, one pass, {dt:.2f} s; effective parallelism <= {nh} heads; {model}",
+            "seconds": dt, "parity_rel_l2": rel_l2(out[p0:].cpu().numpy(), want)}
 
 
 def cpu_kvstore(kv_set, L, nkv, hd):
@@ -901,6 +926,102 @@ def cpu_decode(q, cache, out, L, nh, nkv, hd):
             "seconds": dt, "parity_rel_l2": rel_l2(out.cpu().numpy(), want)}
 
 
+def cpu_hybrid(g, S_gpu, gout, qkv, gate, aout, dout, T, n_dec, n_gdn, hg, dg, kw, nh, nkv, da):
+    """The oracle's restatement of the qwen35 group, token by token as the
+    reference runs it (engine.c:723-734 batch -> per token; 786-847 GDN;
+    910-960 gated attention), on a bounded sample:
+      - one GDN layer over all T + n_dec tokens (conv + silu, gates, l2norm
+        + state update, gated RMSNorm; single thread, as gdn_state_update);
+        the group has n_gdn such layers, counted n_gdn times;
+      - the attention layer's RoPE + KV store of every row, the prefill's
+        last 64 query rows (scaled to the whole causal prefill by FLOPs) and
+        the last 16 decode steps (scaled to n_dec).
+    Parity: that GDN layer's prefill and decode output rows and final state,
+    the sampled prefill rows (bf16 output) and the last decode step."""
+    O = _oracle()
+    from oracle_lib import rel_l2
+    from yllm_amd.attention import round_bf16
+
+    L = T + n_dec
+    conv = 3 * hg * dg
+    kd = hg * dg
+    eps = np.float32(1e-6)
+    dt0, a0 = np.zeros(hg, np.float32), -np.ones(hg, np.float32)
+    # GDN layer, token by token
+    t0 = time.perf_counter()
+    st = np.zeros((kw, conv), np.float32)
+    Sc = np.zeros(hg * dg * dg, np.float32)
+    ys = np.empty((L, kd), np.float32)
+    for t in range(L):
+        st, rows = O.conv_silu(st, g["qkv"][t][None], g["conv_w"], kw)
+        beta, gt = O.gdn_gates(g["alpha"][t], g["beta_raw"][t], dt0, a0)
+        r = rows[0]
+        Sc, o, _, _ = O.gdn_sequence(Sc, r[:kd], r[kd:2 * kd], r[2 * kd:], gt, beta, 1, hg, dg, hg, dg, eps)
+        ys[t] = O.rmsnorm_gated(o.reshape(hg, dg), g["norm_w"], g["z"][t].reshape(hg, dg), eps).ravel()
+    t_gdn = time.perf_counter() - t0
+    # attention: RoPE + store of every row (one pass), then the samples
+    qd, kvd = nh * da, nkv * da
+    t0 = time.perf_counter()
+    q_rot, kc, vc = O.rope_kv_store(qkv[:, :qd], qkv[:, qd:qd + kvd], qkv[:, qd + kvd:], 0, nh, nkv, da,
+                                    np.float32(1e7), 3, 64)
+    t_rope = time.perf_counter() - t0
+    S_pre = 64
+    p0 = T - S_pre
+    q_bf = round_bf16(np.ascontiguousarray(q_rot[p0:T], np.float32).copy())
+    t0 = time.perf_counter()
+    want_pre = O.prefill(q_bf, kc, vc, p0, S_pre, nh, nkv, da)
+    want_pre = O.gate_sigmoid(want_pre.ravel(), gate[p0:T].ravel()).reshape(S_pre, qd)
+    t_pre = (time.perf_counter() - t0) * prefill_flops(T, nh, da) / prefill_flops(S_pre, nh, da, p0)
+    n_s = 16
+    t0 = time.perf_counter()
+    for t in range(L - n_s, L):
+        want_dec = O.gate_sigmoid(O.decode(q_rot[t], kc[:t + 1], vc[:t + 1], t, nh, nkv, da).ravel(), gate[t])
+    t_dec = (time.perf_counter() - t0) * n_dec / n_s
+    total = n_gdn * t_gdn + t_rope + t_pre + t_dec
+    cores, model = _host_desc(O)
+    err_gdn = max(rel_l2(gout[:T], ys[:T]), max(rel_l2(gout[t], ys[t]) for t in range(T, L)))
+    return {"value": L / total, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"one GDN layer over all {L} tokens ({t_gdn:.2f} s, single thread, counted {n_gdn}x), the "
+                      f"attention layer's RoPE + store of {L} rows ({t_rope:.2f} s), its last {S_pre} prefill rows "
+                      f"(scaled by FLOPs to {t_pre:.2f} s) and last {n_s} decode steps (scaled to {n_dec}: "
+                      f"{t_dec:.2f} s); OpenMP over heads for attention as the reference; {model}",
+            "seconds": total, "parity_rel_l2": max(err_gdn, rel_l2(aout[p0:T], want_pre), rel_l2(dout, want_dec)),
+            "parity_detail": {"gdn_out": err_gdn, "gdn_state": rel_l2(S_gpu.ravel(), Sc),
+                              "attn_prefill_rows_bf16": rel_l2(aout[p0:T], want_pre),
+                              "attn_last_decode": rel_l2(dout, want_dec)}}
+
+
+def cpu_decode_batch(q, caches, lens, out, nh, nkv, hd):
+    """The oracle's decode (the reference runs one engine per sequence,
+    OpenMP over heads) on four of the batch's sequences: the shortest, the
+    longest and two between; GB/s from their KV bytes, parity per sequence."""
+    from yllm_amd.attention import kv_to_engine
+
+    O = _oracle()
+    from oracle_lib import rel_l2
+
+    torch = sys.modules["torch"]
+    order = np.argsort(lens)
+    pick = [int(order[0]), int(order[len(order) // 3]), int(order[2 * len(order) // 3]), int(order[-1])]
+    qn, got = q.cpu().numpy(), out.cpu().numpy()
+    errs, secs, nbytes = [], 0.0, 0.0
+    for i in pick:
+        L = int(lens[i])
+        ek, ev = kv_to_engine(caches[i], L)
+        kc = ek.view(torch.int16).cpu().numpy().view(np.uint16)
+        vc = ev.view(torch.int16).cpu().numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        want = O.decode(qn[i], kc, vc, L - 1, nh, nkv, hd)
+        secs += time.perf_counter() - t0
+        nbytes += decode_bytes(L, nkv, nh, hd)
+        errs.append(rel_l2(got[i], want))
+    cores, model = _host_desc(O)
+    return {"value": nbytes / secs / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"sequences {pick} ({', '.join(str(int(lens[i])) for i in pick)} keys), one decode step "
+                      f"each, {secs:.2f} s; {model}",
+            "seconds": secs, "parity_rel_l2": max(errs)}
+
+
 # -------------------------------------------------------------- traffic
 
 def traffic_of(label: str):
@@ -915,6 +1036,54 @@ def traffic_of(label: str):
         return None
 
 
+# the other configurations' lines in the default run, with their own step counts
+SECONDARY = ["decode32k", "prefill8k", "decode128k", "decode_batch", "gated4k", "gdn4k", "hybrid"]
+SECONDARY_STEPS = {"decode32k": (200, 20), "prefill8k": (20, 3), "decode128k": (50, 5), "decode_batch": (20, 3),
+                   "gated4k": (20, 3), "gdn4k": (10, 2), "hybrid": (3, 1)}
+SECONDARY_METRIC = {"decode32k": "attn decode GB/s", "prefill8k": "prefill attn TFLOP/s",
+                    "decode128k": "attn decode GB/s", "decode_batch": "attn decode GB/s",
+                    "gated4k": "prefill attn TFLOP/s", "gdn4k": "GDN prefill tokens/s", "hybrid": "hybrid tokens/s"}
+DTYPES = {"gdn4k": "f32", "rope8k": "f32 rotation, f16 stores", "oproj8k": "f16 MFMA, f32 accumulate",
+          "oproj1": "f16 weights, f32 activations and accumulate", "kvstore8k": "f32 -> f16 (reference rounding)",
+          "gated4k": "bf16 q, f16 K/V MFMA, f32 accumulate/softmax, bf16 out",
+          "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}
+
+
+def timing_of(w: str, steps: int) -> str:
+    how = ("K eager launches" if EAGER or w == "oproj8k" else
+           "one step captured in a HIP graph, replayed K times" if w == "hybrid" else
+           "K steps captured in one HIP graph")
+    return how + ", timed with HIP events on the launch stream"
+
+
+def run_workload(w: str, steps: int, warmup: int, cpu: bool):
+    if w == "prefill2k":
+        return run_prefill(2048, 28, 4, 128, 2, steps, warmup, cpu)
+    if w == "prefill8k":
+        return run_prefill(8192, 32, 8, 128, 4, steps, warmup, cpu)
+    if w == "decode32k":
+        return run_decode(32768, 32, 8, 128, 4, 6, steps, warmup, cpu, "decode32k")
+    if w == "decode128k":
+        return run_decode(131072, 32, 8, 128, 4, 2, steps, warmup, cpu, "decode128k")
+    if w == "decode_batch":
+        return run_decode_batch(32, 8, 128, 64, steps, warmup, cpu)
+    if w == "gdn4k":
+        return run_gdn(4096, 16, 128, steps, warmup, cpu)
+    if w == "rope8k":
+        return run_rope(8192, 32, 8, 128, 500000.0, steps, warmup, cpu)
+    if w == "oproj8k":
+        return run_oproj(8192, 4096, 4096, steps, warmup, cpu)
+    if w == "oproj1":
+        return run_oproj(1, 4096, 4096, steps, warmup, cpu)
+    if w == "kvstore8k":
+        return run_kvstore(8192, 8, 128, steps, warmup, cpu)
+    if w == "gated4k":
+        return run_gated_prefill(4096, 16, 2, 256, steps, warmup, cpu)
+    if w == "hybrid":
+        return run_hybrid(steps, warmup, cpu)
+    raise ValueError(w)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -924,7 +1093,8 @@ def main() -> int:
                     choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch", "gdn4k",
                              "rope8k", "oproj8k", "oproj1", "kvstore8k", "gated4k", "hybrid"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-secondary", action="store_true", help="skip the decode32k / gdn4k secondary lines")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other configurations' secondary lines (" + ", ".join(SECONDARY) + ")")
     ap.add_argument("--gdn-tokenwise", action="store_true",
                     help="gdn4k: time the token-by-token recurrence instead of the chunked form")
     ap.add_argument("--eager", action="store_true",
@@ -950,51 +1120,29 @@ def main() -> int:
     lib()  # fails loudly when the HIP library is missing
     cpu = not args.no_cpu
     w = args.workload
-    if w == "prefill2k":
-        res = run_prefill(2048, 28, 4, 128, 2, args.steps, args.warmup, cpu)
-    elif w == "prefill8k":
-        res = run_prefill(8192, 32, 8, 128, 4, args.steps, args.warmup, cpu)
-    elif w == "decode32k":
-        res = run_decode(32768, 32, 8, 128, 4, 6, args.steps, args.warmup, cpu, "decode32k")
-    elif w == "decode128k":
-        res = run_decode(131072, 32, 8, 128, 4, 2, args.steps, args.warmup, cpu, "decode128k")
-    elif w == "gdn4k":
-        res = run_gdn(4096, 16, 128, args.steps, args.warmup, cpu)
-    elif w == "rope8k":
-        res = run_rope(8192, 32, 8, 128, 500000.0, args.steps, args.warmup, cpu)
-    elif w == "oproj8k":
-        res = run_oproj(8192, 4096, 4096, args.steps, args.warmup, cpu)
-    elif w == "oproj1":
-        res = run_oproj(1, 4096, 4096, args.steps, args.warmup, cpu)
-    elif w == "kvstore8k":
-        res = run_kvstore(8192, 8, 128, args.steps, args.warmup, cpu)
-    elif w == "gated4k":
-        res = run_gated_prefill(4096, 16, 2, 256, args.steps, args.warmup, cpu)
-    elif w == "hybrid":
-        res = run_hybrid(args.steps, args.warmup)
-    else:
-        res = run_decode_batch(32, 8, 128, 64, args.steps, args.warmup)
-    dtype = {"gdn4k": "f32", "rope8k": "f32 rotation, f16 stores", "oproj8k": "f16 MFMA, f32 accumulate",
-             "oproj1": "f16 weights, f32 activations and accumulate",
-             "kvstore8k": "f32 -> f16 (reference rounding)",
-             "gated4k": "bf16 q, f16 K/V MFMA, f32 accumulate/softmax, bf16 out", "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}.get(
-        w, "f16 MFMA, f32 accumulate/softmax")
-
+    t0 = time.perf_counter()
+    res = run_workload(w, args.steps, args.warmup, cpu)
+    print(f"bench: {w} {res['value']:.4g} {res['unit']} ({time.perf_counter() - t0:.1f} s)", file=sys.stderr,
+          flush=True)
     line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": dtype, "data": "synthetic",
+            "vs_baseline": None, "dtype": DTYPES.get(w, "f16 MFMA, f32 accumulate/softmax"), "data": "synthetic",
             "config": res["config"], "tokens_per_s": res["tokens_per_s"], "roofline": res["roofline"],
-            "timing": ("K eager launches" if EAGER or w == "oproj8k" else
-                       "one step captured in a HIP graph, replayed K times" if w == "hybrid" else
-                       "K steps captured in one HIP graph") + ", timed with HIP events on the launch stream",
-            "measured_copy_GBps": copy_ceiling_gbps()}
+            "timing": timing_of(w, args.steps), "measured_copy_GBps": copy_ceiling_gbps()}
     if "cpu_baseline" in res:
         line["cpu_baseline"] = res["cpu_baseline"]
     if w == "prefill2k" and not args.no_secondary:
-        sec = run_decode(32768, 32, 8, 128, 4, 6, 200, 20, cpu, "decode32k")
-        gdn = run_gdn(4096, 16, 128, 10, 2, cpu)
-        line["secondary"] = [{"metric": "attn decode GB/s", **sec},
-                             {"metric": "GDN prefill tokens/s", "dtype": "f32", **gdn}]
+        sec = []
+        for name in SECONDARY:
+            steps, warmup = SECONDARY_STEPS.get(name, (args.steps, args.warmup))
+            t0 = time.perf_counter()
+            r = run_workload(name, steps, warmup, cpu)
+            print(f"bench: {name} {r['value']:.4g} {r['unit']} ({time.perf_counter() - t0:.1f} s)", file=sys.stderr,
+                  flush=True)
+            sec.append({"workload": name, "metric": SECONDARY_METRIC[name],
+                        "dtype": DTYPES.get(name, "f16 MFMA, f32 accumulate/softmax"), "steps": steps,
+                        "warmup": warmup, "timing": timing_of(name, steps), **r})
+        line["secondary"] = sec
     print(json.dumps(line), flush=True)
     return 0
 
