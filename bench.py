@@ -215,6 +215,61 @@ def run_prefill(L: int, nh: int, nkv: int, hd: int, cfg: int, steps: int, warmup
     return res
 
 
+def run_prefill_chunked(L: int, nh: int, nkv: int, hd: int, chunk: int, cfg: int, steps: int, warmup: int,
+                        cpu: bool):
+    """The prompt as the engine issues it: engine_forward_prefill hands the
+    block at most 64 tokens per call (pb_cap, engine.c:270-272, 622-653), so
+    an L-token prompt is L / chunk attention launches at positions 0, chunk,
+    2 chunk, ...; a step is all of them (the K/V rows already stored)."""
+    import torch
+
+    from yllm_amd.attention import LayerKV, attn_prefill, kv_store, prefill_workspace, prefill_workspace_bytes
+
+    dev = torch.device("cuda:0")
+    seed = SEED + cfg
+    nq, nk = L * nh * hd, L * nkv * hd
+    q = torch.from_numpy(synth(seed, nq).reshape(L, nh * hd)).to(dev).half()
+    k = torch.from_numpy(synth(seed, nk, nq).reshape(L, nkv * hd)).to(dev).half()
+    v = torch.from_numpy(synth(seed, nk, nq + nk).reshape(L, nkv * hd)).to(dev).half()
+    set_bytes = nq * 2 + 2 * nk * 2 + L * nh * hd * 4
+    n_sets = max(1, -(-ROTATE_BYTES // set_bytes))
+    qs, caches, outs = [], [], []
+    for _ in range(n_sets):
+        c = LayerKV.empty(nkv, hd, L, device=dev)
+        kv_store(c, k, v, 0)
+        qs.append(q.clone())
+        caches.append(c)
+        outs.append(torch.empty((L, nh * hd), dtype=torch.float32, device=dev))
+    del q
+    ws = prefill_workspace(prefill_workspace_bytes(chunk, L, nh, nkv, hd), dev)
+
+    def step(i):
+        qi, ci, oi = qs[i % n_sets], caches[i % n_sets], outs[i % n_sets]
+        for p0 in range(0, L, chunk):
+            attn_prefill(qi[p0:p0 + chunk], ci, p0, nh, out=oi[p0:p0 + chunk], workspace=ws)
+
+    last = (warmup + steps - 1) % n_sets
+    ms, kern_ms = time_steps(step, steps, warmup, outs[last])
+    q, out = qs[last], outs[last]
+    flops = prefill_flops(L, nh, hd)
+    achieved = flops / (kern_ms * 1e-3)
+    res = {
+        "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms, "tokens_per_s": L / (ms * 1e-3),
+        "config": {"workload": f"causal GQA prefill attention of a {L}-token prompt issued as the engine does, "
+                               f"{L // chunk} calls of {chunk} tokens at positions 0, {chunk}, ...; {nh} query / "
+                               f"{nkv} KV heads, head_dim {hd}, f16 Q/K/V N(0,1)*0.5 seed {hex(seed)}, f32 out; "
+                               f"{n_sets} rotating input sets (> 256 MB MALL)",
+                   "tokens": L, "chunk": chunk, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd},
+        "roofline": {"bound": "mfma", "kernel": "prefill_kernel<%d> (+ prefill_merge_kernel<%d>), %d launches"
+                     % (hd, hd, L // chunk), "achieved": achieved / 1e12, "peak": MFMA_F16_PEAK / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved / MFMA_F16_PEAK, "flops_per_launch": flops,
+                     "launch_ms": kern_ms, "traffic": traffic_of(f"prefill{L}c{chunk}")},
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_prefill(q, k, v, out, L, nh, nkv, hd)
+    return res
+
+
 def decode_bytes(L: int, nkv: int, nh: int, hd: int) -> float:
     return float(L) * nkv * hd * 2 * 2 + 2.0 * nh * hd * 4  # K,V once (GQA-aware) + q in + out
 
@@ -1037,10 +1092,11 @@ def traffic_of(label: str):
 
 
 # the other configurations' lines in the default run, with their own step counts
-SECONDARY = ["decode32k", "prefill8k", "decode128k", "decode_batch", "gated4k", "gdn4k", "hybrid"]
-SECONDARY_STEPS = {"decode32k": (200, 20), "prefill8k": (20, 3), "decode128k": (50, 5), "decode_batch": (20, 3),
+SECONDARY = ["decode32k", "prefill8k", "prefill2k_chunked", "decode128k", "decode_batch", "gated4k", "gdn4k", "hybrid"]
+SECONDARY_STEPS = {"decode32k": (200, 20), "prefill8k": (20, 3), "prefill2k_chunked": (10, 2), "decode128k": (50, 5), "decode_batch": (20, 3),
                    "gated4k": (20, 3), "gdn4k": (10, 2), "hybrid": (3, 1)}
 SECONDARY_METRIC = {"decode32k": "attn decode GB/s", "prefill8k": "prefill attn TFLOP/s",
+                    "prefill2k_chunked": "prefill attn TFLOP/s",
                     "decode128k": "attn decode GB/s", "decode_batch": "attn decode GB/s",
                     "gated4k": "prefill attn TFLOP/s", "gdn4k": "GDN prefill tokens/s", "hybrid": "hybrid tokens/s"}
 DTYPES = {"gdn4k": "f32", "rope8k": "f32 rotation, f16 stores", "oproj8k": "f16 MFMA, f32 accumulate",
@@ -1061,6 +1117,10 @@ def run_workload(w: str, steps: int, warmup: int, cpu: bool):
         return run_prefill(2048, 28, 4, 128, 2, steps, warmup, cpu)
     if w == "prefill8k":
         return run_prefill(8192, 32, 8, 128, 4, steps, warmup, cpu)
+    if w == "prefill2k_chunked":
+        return run_prefill_chunked(2048, 28, 4, 128, 64, 2, steps, warmup, cpu)
+    if w == "prefill8k_chunked":
+        return run_prefill_chunked(8192, 32, 8, 128, 64, 4, steps, warmup, cpu)
     if w == "decode32k":
         return run_decode(32768, 32, 8, 128, 4, 6, steps, warmup, cpu, "decode32k")
     if w == "decode128k":
@@ -1090,7 +1150,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="prefill2k",
-                    choices=["prefill2k", "prefill8k", "decode32k", "decode128k", "decode_batch", "gdn4k",
+                    choices=["prefill2k", "prefill8k", "prefill2k_chunked", "prefill8k_chunked", "decode32k", "decode128k", "decode_batch", "gdn4k",
                              "rope8k", "oproj8k", "oproj1", "kvstore8k", "gated4k", "hybrid"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true",

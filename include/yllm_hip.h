@@ -151,12 +151,27 @@ size_t yhip_attn_decode_workspace(uint32_t n_seq, uint32_t max_len, uint64_t tot
  * apart (head h at h*head_dim), out rows out_stride elements of out_dtype;
  * dtypes YHIP_F32 / YHIP_F16 / YHIP_BF16.  gate: NULL or fp32 rows
  * gate_stride apart.  Computes QK^T and PV on f16 MFMA with fp32
- * accumulation and an fp32 online softmax. */
+ * accumulation and an fp32 online softmax.
+ *
+ * A launch with fewer (128-query block, head) items than CUs -- the
+ * engine's prefill issues at most 64 tokens per call (engine.c:270-272,
+ * 622-653) -- packs each kv head's query heads into full blocks and splits
+ * the keys over workgroups so the GPU fills; the splits' partial results
+ * need yhip_attn_prefill_workspace bytes of workspace (16-byte aligned, no
+ * initialisation; 0 when the launch does not split).  With workspace NULL
+ * such a launch runs unsplit (correct, slower for long prefixes). */
 int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, const void* q,
                       uint32_t q_dtype, uint32_t q_stride, const uint16_t* kcache,
                       const uint16_t* vcache, uint32_t pos_start, uint32_t B, uint32_t n_heads,
                       uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
-                      const float* gate, uint32_t gate_stride, void* stream);
+                      const float* gate, uint32_t gate_stride, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* Workspace bytes that serve every yhip_attn_prefill call of B tokens with
+ * pos_start + B <= max_end (an engine sizes one for its chunk size and
+ * max_seq).  Calls sharing a workspace must not run concurrently. */
+size_t yhip_attn_prefill_workspace(uint32_t B, uint32_t max_end, uint32_t n_heads, uint32_t n_kv_heads,
+                                   uint32_t head_dim);
 
 /* ---- RoPE + KV store (the step before attention) ---------------------------
  * rope: YHIP_ROPE_PAIRS = rope_inplace, (v[2j], v[2j+1]) (matvec.c:890-904,

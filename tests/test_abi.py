@@ -87,16 +87,16 @@ def test_decode_workspace_serves_every_shorter_position(hiplib, nh, nkv, hd, max
 
 def test_prefill_rejects_bad_args(hiplib):
     # positions past the cache
-    rc = hiplib.yhip_attn_prefill(P, 1, 1024, P, 1, 1024, P, P, 100, 64, 8, 2, 128, 128, None, 0, None)
+    rc = hiplib.yhip_attn_prefill(P, 1, 1024, P, 1, 1024, P, P, 100, 64, 8, 2, 128, 128, None, 0, None, 0, None)
     assert rc == -22 and "exceed" in _err(hiplib)
     # dtype
-    rc = hiplib.yhip_attn_prefill(P, 7, 1024, P, 1, 1024, P, P, 0, 64, 8, 2, 128, 128, None, 0, None)
+    rc = hiplib.yhip_attn_prefill(P, 7, 1024, P, 1, 1024, P, P, 0, 64, 8, 2, 128, 128, None, 0, None, 0, None)
     assert rc == -22 and "dtype" in _err(hiplib)
     # stride
-    rc = hiplib.yhip_attn_prefill(P, 1, 1000, P, 1, 1024, P, P, 0, 64, 8, 2, 128, 128, None, 0, None)
+    rc = hiplib.yhip_attn_prefill(P, 1, 1000, P, 1, 1024, P, P, 0, 64, 8, 2, 128, 128, None, 0, None, 0, None)
     assert rc == -22 and "stride" in _err(hiplib)
     # empty batch is a no-op
-    assert hiplib.yhip_attn_prefill(P, 1, 1024, P, 1, 1024, P, P, 0, 0, 8, 2, 128, 128, None, 0, None) == 0
+    assert hiplib.yhip_attn_prefill(P, 1, 1024, P, 1, 1024, P, P, 0, 0, 8, 2, 128, 128, None, 0, None, 0, None) == 0
 
 
 def test_kv_store_rejects_overflow(hiplib):

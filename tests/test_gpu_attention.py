@@ -427,3 +427,85 @@ def test_prefill_full_size_sampled_rows(cuda, oracle, nh, nkv, hd, L):
         dec = attn_decode(torch.from_numpy(q[t]).to(cuda), cache, t, nh).cpu().numpy()
         assert err <= TOL, f"row {t}: rel_l2={err:.3e}"
         assert rel_l2(got[t], dec) <= TOL
+
+
+# ------------------------------------------------------ prefill: engine chunks
+
+@pytest.mark.parametrize("nh,nkv,hd,ps,B,qdt,odt,gated", [
+    # the engine's 64-token chunks (engine.c:270-272, 622-653) at the start,
+    # middle and end of an 8k prompt: packed rows, split keys
+    (28, 4, 128, 0, 64, torch.float32, torch.float32, False),
+    (28, 4, 128, 1984, 64, torch.float32, torch.float32, False),
+    (32, 8, 128, 8128, 64, torch.float16, torch.float32, False),
+    (16, 2, 256, 4032, 64, torch.bfloat16, torch.bfloat16, True),
+    (14, 2, 64, 2000, 64, torch.float32, torch.float16, False),
+    # a wave's rows straddle two heads (B not a multiple of 32); uneven groups
+    (28, 4, 128, 3001, 37, torch.float32, torch.float32, False),
+    (6, 4, 64, 777, 50, torch.float32, torch.float32, True),
+    (32, 8, 128, 5000, 1, torch.float32, torch.float32, False),
+    # plain rows (B >= 128) with split keys: few (query block, head) items
+    (8, 2, 128, 3000, 200, torch.float16, torch.float32, False),
+])
+def test_prefill_engine_chunk_parity(cuda, oracle, nh, nkv, hd, ps, B, qdt, odt, gated):
+    from yllm_amd.attention import attn_prefill, prefill_workspace_bytes, round_bf16
+
+    kvd = nkv * hd
+    L = ps + B
+    K, V = gen(2700 + L, (L, kvd)), gen(2800 + L, (L, kvd))
+    q = gen(2900 + L, (B, nh * hd), f16=(qdt == torch.float16))
+    if qdt == torch.bfloat16:
+        q = round_bf16(q.ravel().copy()).reshape(B, nh * hd)
+    gate = gen(3000 + L, (B, nh * hd), 1.0, f16=False) if gated else None
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    want = oracle.prefill(q, kc, vc, ps, B, nh, nkv, hd)
+    if gated:
+        want = oracle.gate_sigmoid(want.ravel(), gate.ravel()).reshape(B, nh * hd)
+    qt = torch.from_numpy(q).to(cuda).to(qdt)
+    gt = torch.from_numpy(gate).to(cuda) if gated else None
+    tol = TOL + (2.0 ** -8 if odt == torch.bfloat16 else 2.0 ** -10 if odt == torch.float16 else 0.0)
+    need = prefill_workspace_bytes(B, L, nh, nkv, hd)
+    # with the key-split workspace (the mirror allocates it), then through the
+    # C ABI without one: the same packing, unsplit
+    from yllm_amd._lib import check, lib
+
+    for split in (True, False):
+        if split:
+            out = attn_prefill(qt, cache, ps, nh, out_dtype=odt, gate=gt)
+        else:
+            out = torch.empty((B, nh * hd), dtype=odt, device=cuda)
+            code = {torch.float32: 1, torch.float16: 0, torch.bfloat16: 2}
+            check(lib().yhip_attn_prefill(out.data_ptr(), code[odt], nh * hd, qt.data_ptr(), code[qdt], nh * hd,
+                                          cache.k.data_ptr(), cache.v.data_ptr(), ps, B, nh, nkv, hd, cache.kv_stride,
+                                          gt.data_ptr() if gated else None, nh * hd if gated else 0, None, 0,
+                                          torch.cuda.current_stream().cuda_stream))
+        got = out.float().cpu().numpy()
+        err = rel_l2(got, want)
+        rows = max(rel_l2(got[i], want[i]) for i in range(B))
+        print(f"chunk {nh}/{nkv} d={hd} ps={ps} B={B} {'split' if split else 'unsplit'} ({need} B): "
+              f"rel_l2={err:.3e} worst row {rows:.3e}")
+        assert np.isfinite(got).all()
+        assert err <= tol and rows <= 3 * tol
+
+
+def test_prefill_chunked_prompt_equals_single_launch(cuda, oracle):
+    """A 2048-token prompt issued as 32 calls of 64 tokens (the engine's
+    chunking, every call a split launch) gives the single launch's result to
+    rounding, and both match the oracle's rows."""
+    from yllm_amd.attention import attn_prefill, prefill_workspace, prefill_workspace_bytes
+
+    nh, nkv, hd, L, C = 28, 4, 128, 2048, 64
+    kvd = nkv * hd
+    K, V = gen(0x5EED0002 + 7, (L, kvd)), gen(0x5EED0102 + 7, (L, kvd))
+    q = gen(0x5EED0202 + 7, (L, nh * hd), f16=False)
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    qt = torch.from_numpy(q).to(cuda)
+    whole = attn_prefill(qt, cache, 0, nh).cpu().numpy()
+    out = torch.empty((L, nh * hd), device=cuda)
+    ws = prefill_workspace(prefill_workspace_bytes(C, L, nh, nkv, hd), cuda)
+    for p0 in range(0, L, C):
+        attn_prefill(qt[p0:p0 + C], cache, p0, nh, out=out[p0:p0 + C], workspace=ws)
+    chunked = out.cpu().numpy()
+    assert rel_l2(chunked, whole) <= 2e-4
+    for t in (0, 63, 64, 1000, 1983, 1984, 2047):
+        want = oracle.decode(q[t], kc[: t + 1], vc[: t + 1], t, nh, nkv, hd)
+        assert rel_l2(chunked[t], want) <= TOL

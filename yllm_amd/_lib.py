@@ -37,7 +37,8 @@ SIGNATURES = {
     "yhip_attn_decode_workspace": (c_size_t, [c_uint32, c_uint32, c_uint64, c_uint32, c_uint32, c_uint32]),
     "yhip_attn_prefill": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, c_uint32, c_void_p,
                                   c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
-                                  c_void_p, c_uint32, c_void_p]),
+                                  c_void_p, c_uint32, c_void_p, c_size_t, c_void_p]),
+    "yhip_attn_prefill_workspace": (c_size_t, [c_uint32, c_uint32, c_uint32, c_uint32, c_uint32]),
     "yhip_gdn_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
                               c_uint32, c_uint32, c_float, c_void_p]),
     "yhip_gdn_chunk": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32,

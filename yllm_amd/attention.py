@@ -273,22 +273,42 @@ def attn_decode_batch(q: torch.Tensor, batch: DecodeBatch, lens: list[int] | np.
     return out
 
 
+def prefill_workspace_bytes(B: int, max_end: int, n_heads: int, n_kv: int, head_dim: int) -> int:
+    """Workspace of every attn_prefill of B tokens ending at or before max_end."""
+    return int(lib().yhip_attn_prefill_workspace(B, max_end, n_heads, n_kv, head_dim))
+
+
+def prefill_workspace(nbytes: int, device: torch.device | str = "cuda") -> torch.Tensor:
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
 def attn_prefill(q: torch.Tensor, cache: LayerKV, pos_start: int, n_heads: int,
                  out_dtype: torch.dtype = torch.float32, gate: torch.Tensor | None = None,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
-    """B prompt tokens at positions pos_start.. ; q: [B, n_heads*head_dim] (f32/f16/bf16)."""
-    _need_gpu(q, gate)
+                 out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """B prompt tokens at positions pos_start.. ; q: [B, n_heads*head_dim] (f32/f16/bf16).
+    q, out and gate may be row slices of larger matrices (unit column stride).
+    A launch with few work items splits the keys over a workspace (allocated
+    here unless given; see prefill_workspace_bytes)."""
+    for t in (q, gate, out):
+        if t is not None and (not t.is_cuda or t.dim() != 2 or t.stride(1) != 1):
+            raise YhipError(-22, "attn_prefill: q, out and gate must be GPU rows with unit column stride")
     d = cache.head_dim
-    if q.dim() != 2 or q.shape[1] != n_heads * d:
+    if q.shape[1] != n_heads * d:
         raise YhipError(-22, "attn_prefill: q must be [B, n_heads*head_dim]")
     B = q.shape[0]
     if out is None:
         out = torch.empty((B, n_heads * d), dtype=out_dtype, device=q.device)
-    _need_gpu(out)
-    gstride = gate.shape[-1] if gate is not None else 0
-    check(lib().yhip_attn_prefill(_ptr(out), _dtype_code(out), out.shape[1], _ptr(q), _dtype_code(q),
-                                  q.shape[1], _ptr(cache.k), _ptr(cache.v), pos_start, B, n_heads, cache.n_kv,
-                                  d, cache.kv_stride, _ptr(gate), gstride, _stream()))
+    if out.shape[0] != B or out.shape[1] != n_heads * d:
+        raise YhipError(-22, "attn_prefill: out must be [B, n_heads*head_dim]")
+    nbytes = prefill_workspace_bytes(B, pos_start + B, n_heads, cache.n_kv, d)
+    ws = _workspace(nbytes, q.device, workspace)
+    qs = q.stride(0) if B > 1 else q.shape[1]
+    os_ = out.stride(0) if B > 1 else out.shape[1]
+    gs = (gate.stride(0) if B > 1 else gate.shape[1]) if gate is not None else 0
+    check(lib().yhip_attn_prefill(_ptr(out), _dtype_code(out), os_, _ptr(q), _dtype_code(q), qs, _ptr(cache.k),
+                                  _ptr(cache.v), pos_start, B, n_heads, cache.n_kv, d, cache.kv_stride, _ptr(gate),
+                                  gs, _ptr(ws), ws.numel() * ws.element_size() if ws is not None else 0,
+                                  _stream()))
     return out
 
 

@@ -217,11 +217,19 @@ int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
     return done(yhip::launch_decode(a, (hipStream_t)stream), fn);
 }
 
+size_t yhip_attn_prefill_workspace(uint32_t B, uint32_t max_end, uint32_t n_heads, uint32_t n_kv_heads,
+                                   uint32_t head_dim)
+{
+    if (n_kv_heads == 0 || !valid_head_dim(head_dim)) return 0;
+    return yhip::prefill_workspace_bound(B, max_end, n_heads, n_kv_heads, head_dim);
+}
+
 int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, const void* q,
                       uint32_t q_dtype, uint32_t q_stride, const uint16_t* kcache,
                       const uint16_t* vcache, uint32_t pos_start, uint32_t B, uint32_t n_heads,
                       uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
-                      const float* gate, uint32_t gate_stride, void* stream)
+                      const float* gate, uint32_t gate_stride, void* workspace, size_t workspace_bytes,
+                      void* stream)
 {
     const char* fn = "yhip_attn_prefill";
     if (!att_out || !q || !kcache || !vcache) return fail(YHIP_EINVAL, "%s: null pointer", fn);
@@ -256,6 +264,18 @@ int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, co
     a.n_kv = n_kv_heads;
     a.D = head_dim;
     a.c = (float)(1.4426950408889634 / sqrt((double)head_dim));
+    // a launch with few work items splits the keys when a workspace is given
+    // for the partials; without one it runs unsplit
+    size_t need = yhip::prefill_plan(a);
+    if (need > 0 && !workspace) {
+        a.n_split = 1;
+        a.split_tiles = (pos_start + B - 1) / 64 + 1;
+        need = 0;
+    }
+    if (need > 0 && (workspace_bytes < need || (uintptr_t)workspace % 16))
+        return fail(YHIP_ENOSPC, "%s: the key split needs %zu bytes of workspace (16-byte aligned), %zu given", fn,
+                    need, workspace_bytes);
+    yhip::prefill_bind_workspace(a, workspace);
     return done(yhip::launch_prefill(a, (hipStream_t)stream), fn);
 }
 

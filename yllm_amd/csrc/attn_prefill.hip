@@ -167,10 +167,81 @@ struct FusedSchedule {
     }
 };
 
-template <int D, int NG>
+// first query head of kv head g: heads h with h*n_kv/n_heads == g are
+// [head0(g), head0(g+1)) (engine.c:537)
+__device__ inline uint32_t head0(const PrefillArgs& a, uint32_t g) { return (g * a.n_heads + a.n_kv - 1) / a.n_kv; }
+
+// A work item: query block qb (plain rows) or row block qb (packed rows) of
+// kv head kvh, key split `split`; h is the query head of plain rows.
+struct PItem {
+    uint32_t qb, h, kvh, split;
+};
+
+// Row r (0..127) of an item -> query index b and head; valid is false for
+// rows past the item's end (their loads are clamped to the last row).
+struct PRow {
+    uint32_t b, h;
+    bool valid;
+};
+template <bool SPLIT>
+__device__ inline PRow row_of(const PrefillArgs& a, const PItem& I, uint32_t r)
+{
+    if (!(SPLIT && a.pack)) {
+        const uint32_t q = I.qb * BM + r;
+        return PRow{min(q, a.B - 1), I.h, q < a.B};
+    }
+    const uint32_t h0 = head0(a, I.kvh), nrows = (head0(a, I.kvh + 1) - h0) * a.B;
+    const uint32_t rr = I.qb * BM + r, rc = min(rr, nrows - 1);
+    return PRow{rc % a.B, h0 + rc / a.B, rr < nrows};
+}
+
+// The query indices a wave's 32 rows span (wave-uniform): [first, last].
+template <bool SPLIT>
+__device__ inline bool wave_span(const PrefillArgs& a, const PItem& I, int wave, uint32_t& first, uint32_t& last)
+{
+    if (!(SPLIT && a.pack)) {
+        const uint32_t q0 = I.qb * BM + wave * 32;
+        first = q0;
+        last = min(q0 + 31, a.B - 1);
+        return q0 < a.B;
+    }
+    const uint32_t nrows = (head0(a, I.kvh + 1) - head0(a, I.kvh)) * a.B;
+    const uint32_t r0 = I.qb * BM + wave * 32, rl = min(r0 + 31, nrows - 1);
+    if (r0 / a.B == rl / a.B) {
+        first = r0 % a.B;
+        last = rl % a.B;
+    } else {  // the rows cross into the next head: its first queries, the previous head's last
+        first = 0;
+        last = a.B - 1;
+    }
+    return r0 < nrows;
+}
+
+// Key tiles of an item: [t0, t0 + nt).  The item's last key is kmax (its
+// last query's position; with packed rows (B < 128) every item holds some
+// head's query B-1).
+template <bool SPLIT>
+__device__ inline void item_keys(const PrefillArgs& a, const PItem& I, uint32_t& kmax, uint32_t& t0, uint32_t& nt)
+{
+    kmax = a.pos_start + ((SPLIT && a.pack) ? a.B - 1 : min(a.B, I.qb * BM + BM) - 1);
+    const uint32_t all = kmax / BN + 1;
+    if (SPLIT) {
+        t0 = I.split * a.split_tiles;
+        const uint32_t t1 = min(all, t0 + a.split_tiles);
+        nt = t1 > t0 ? t1 - t0 : 0;
+    } else {
+        t0 = 0;
+        nt = all;
+    }
+}
+
+// SPLIT: the split mode (one item per workgroup, packed rows, a key range
+// per split); a separate instantiation keeps the plain mode's registers.
+template <int D, int NG, bool SPLIT>
 __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefill_kernel(PrefillArgs a)
 {
     static_assert(NG == 1 || NG == 2, "one or two key groups");
+    static_assert(!SPLIT || NG == 1, "the split mode runs one key group");
     constexpr int NKK = D / 16;   // k-chunks of the score MFMA
     constexpr int NDB = D / 32;   // d-blocks of the output MFMA
     constexpr int CH = D / 32;    // 16-byte chunks per thread per tile (K and V each)
@@ -205,8 +276,31 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
     // linearly decreasing costs; the grid is one item per workgroup when
     // there are no more items than resident slots.
     const uint32_t nqb = (a.B + BM - 1) / BM;
-    // item `it` of this workgroup -> (query block, head); false past the last
-    auto item_of = [&](uint32_t it, uint32_t& qb, uint32_t& h) -> bool {
+    // item `it` of this workgroup; false past the last
+    auto item_of = [&](uint32_t it, PItem& I) -> bool {
+        if (SPLIT) {
+            // one item per workgroup.  The items of a (kv head, split) tile
+            // group read the same K/V tiles: XCD x serves tile groups x, x+8,
+            // ... (consecutive workgroups go to the 8 XCDs in turn), so they
+            // share its L2.
+            if (it > 0) return false;
+            const uint32_t x = blockIdx.x % 8u, j = blockIdx.x / 8u;
+            const uint32_t ipg = a.n_rb * (a.pack ? 1u : a.gmax);
+            const uint32_t tg = (j / ipg) * 8u + x, w = j % ipg;
+            if (tg >= a.n_kv * a.n_split) return false;
+            I.kvh = tg % a.n_kv;
+            I.split = tg / a.n_kv;
+            const uint32_t h0 = head0(a, I.kvh), h1 = head0(a, I.kvh + 1);
+            if (a.pack) {
+                I.qb = w;
+                I.h = h0;
+                return w * BM < (h1 - h0) * a.B;
+            }
+            I.qb = a.n_rb - 1 - w / a.gmax;  // heaviest first
+            I.h = h0 + w % a.gmax;
+            return I.h < h1;
+        }
+        I.split = 0;
         if (a.xcd_map) {
             // Consecutive workgroups go to the 8 XCDs in turn.  XCD x serves
             // kv head x % n_kv, so the query heads that read one kv head
@@ -217,15 +311,16 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
             if (slot >= nqb * a.n_heads / 8u) return false;
             const uint32_t per = 8u / a.n_kv, G = a.n_heads / a.n_kv;
             const uint32_t g = x % a.n_kv, i = slot * per + x / a.n_kv;
-            qb = nqb - 1 - i / G;
-            h = g * G + i % G;
+            I.qb = nqb - 1 - i / G;
+            I.h = g * G + i % G;
         } else {
             const uint32_t W = gridDim.x;
             const uint32_t slot = it * W + ((it & 1u) ? W - 1u - blockIdx.x : blockIdx.x);
             if (slot >= nqb * a.n_heads) return false;
-            qb = nqb - 1 - slot / a.n_heads;
-            h = slot % a.n_heads;
+            I.qb = nqb - 1 - slot / a.n_heads;
+            I.h = slot % a.n_heads;
         }
+        I.kvh = I.h * a.n_kv / a.n_heads;  // engine.c:537
         return true;
     };
     // An item's first loads are issued during the previous item: its
@@ -239,8 +334,8 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
     // then wait behind these loads; such items issue their loads at their
     // own start.
     const bool early = a.gate == nullptr;
-    uint32_t qb, h;
-    if (!item_of(0, qb, h)) return;  // uniform over the workgroup
+    PItem cur;
+    if (!item_of(0, cur)) return;  // uniform over the workgroup
     for (uint32_t it = 0;; ++it) {
         // Thread indices pass through an opaque move each item so that nothing
         // derived from them is hoisted out of the item loop: the key loop's
@@ -250,8 +345,8 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         const int lane = tid & 63;
         const int grp = tid >> 8, gtid = tid & 255, wave = gtid >> 6;
         const int r32 = lane & 31, hh = lane >> 5;
-        uint32_t qb_next = 0, h_next = 0;
-        const bool has_next = item_of(it + 1, qb_next, h_next);
+        PItem nxt{};
+        const bool has_next = item_of(it + 1, nxt);
 
         // Chunk L = 256 i + gtid of a tile is the 16 bytes this thread loads
         // with its i-th instruction.  K: LDS row R = L / KCH holds key row
@@ -295,56 +390,58 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         };
         auto dma_done = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };  // vmcnt(0): this thread's loads landed
         f16x8 qf[NKK];
-        // the first loads of item (iqb, ih), see above: the K tiles, the first V
+        // the first loads of an item, see above: the K tiles, the first V
         // tile and the queries
-        auto item_tiles = [&](uint32_t iqb) {
-            const uint32_t intiles = (a.pos_start + min(a.B, iqb * BM + BM) - 1) / BN + 1;
-            return intiles > (uint32_t)grp ? (intiles - grp + NG - 1) / NG : 0u;  // this group's
+        auto item_steps = [&](const PItem& I, uint32_t& t0) {
+            uint32_t km, nt;
+            item_keys<SPLIT>(a, I, km, t0, nt);
+            return nt > (uint32_t)grp ? (nt - grp + NG - 1) / NG : 0u;  // this group's tiles
         };
-        auto issue_item_k = [&](uint32_t iqb, uint32_t ih) {
-            const uint32_t igsteps = item_tiles(iqb);
-            const __amdgpu_buffer_rsrc_t rk = rsrc_k(ih * a.n_kv / a.n_heads);
-            if (igsteps > 0) dma_k_of(rk, 0, grp);
-            if (igsteps > 1) dma_k_of(rk, 1, grp + NG);
+        auto issue_item_k = [&](const PItem& I) {
+            uint32_t t0;
+            const uint32_t igsteps = item_steps(I, t0);
+            const __amdgpu_buffer_rsrc_t rk = rsrc_k(I.kvh);
+            if (igsteps > 0) dma_k_of(rk, 0, t0 + grp);
+            if (igsteps > 1) dma_k_of(rk, 1, t0 + grp + NG);
         };
-        auto issue_item_q = [&](uint32_t iqb, uint32_t ih) {
+        auto issue_item_q = [&](const PItem& I) {
             if (a.q_dtype == kF16) {
-                const uint32_t iq = min(iqb * BM + wave * 32 + r32, a.B - 1);
+                const PRow rw = row_of<SPLIT>(a, I, wave * 32 + r32);
                 const uint16_t* qp =
-                    reinterpret_cast<const uint16_t*>(a.q) + (size_t)iq * a.q_stride + (size_t)ih * D + hh * 8;
+                    reinterpret_cast<const uint16_t*>(a.q) + (size_t)rw.b * a.q_stride + (size_t)rw.h * D + hh * 8;
 #pragma unroll
                 for (int kk = 0; kk < NKK; ++kk) qf[kk] = *reinterpret_cast<const f16x8*>(qp + kk * 16);
             }
         };
-        auto issue_item_v = [&](uint32_t iqb, uint32_t ih) {
-            if (item_tiles(iqb) > 0) dma_v_of(rsrc_v(ih * a.n_kv / a.n_heads), 0, grp);
+        auto issue_item_v = [&](const PItem& I) {
+            uint32_t t0;
+            if (item_steps(I, t0) > 0) dma_v_of(rsrc_v(I.kvh), 0, t0 + grp);
         };
         if (it == 0 || !early) {
             if (it > 0) __syncthreads();  // the previous item's epilogue read LDS these loads overwrite
-            issue_item_k(qb, h);
-            issue_item_v(qb, h);
-            issue_item_q(qb, h);
+            issue_item_k(cur);
+            issue_item_v(cur);
+            issue_item_q(cur);
         }
 
-        const uint32_t kvh = h * a.n_kv / a.n_heads;  // engine.c:537
-        const uint32_t qi0 = qb * BM;
-        const uint32_t qlast = min(a.B, qi0 + BM) - 1;
-        const uint32_t kmax = a.pos_start + qlast;  // last key any query here reads
-        const uint32_t ntiles = kmax / BN + 1;
+        const uint32_t kvh = cur.kvh;
+        uint32_t kmax, t0, ntiles;  // this item's keys end at kmax; its tiles are t0 .. t0+ntiles-1
+        item_keys<SPLIT>(a, cur, kmax, t0, ntiles);
         const uint32_t nsteps = (ntiles + NG - 1) / NG;  // loop steps (workgroup-uniform)
-        // this group's tiles: kt = grp + NG*st for st < gsteps
+        // this group's tiles: kt = t0 + grp + NG*st for st < gsteps
         const uint32_t gsteps = ntiles > (uint32_t)grp ? (ntiles - grp + NG - 1) / NG : 0;
 
-        const uint32_t wq0 = qi0 + wave * 32;
-        const bool wave_active = wq0 < a.B;
-        const uint32_t wpos_first = a.pos_start + wq0;
-        const uint32_t wpos_last = a.pos_start + min(wq0 + 31, a.B - 1);
-        const uint32_t my_pos = a.pos_start + wq0 + r32;
-        const uint32_t my_q = min(wq0 + r32, a.B - 1);
-        // tiles this wave computes: 0 .. wtiles-1, of which this group's are st < wsteps
-        const uint32_t wtiles = wave_active ? wpos_last / BN + 1 : 0;
+        uint32_t wfirst, wlast;
+        const bool wave_active = wave_span<SPLIT>(a, cur, wave, wfirst, wlast);
+        const uint32_t wpos_first = a.pos_start + wfirst;
+        const uint32_t wpos_last = a.pos_start + wlast;
+        const PRow myrow = row_of<SPLIT>(a, cur, wave * 32 + r32);
+        const uint32_t my_pos = a.pos_start + myrow.b;
+        // tiles this wave computes: t0 .. t0+wtiles-1, of which this group's are st < wsteps
+        const uint32_t wend = wave_active ? wpos_last / BN + 1 : 0;  // one past the wave's last tile
+        const uint32_t wtiles = wend > t0 ? min(wend - t0, ntiles) : 0;
         const uint32_t wsteps = wtiles > (uint32_t)grp ? (wtiles - grp + NG - 1) / NG : 0;
-        auto tile_of = [&](uint32_t st) { return (uint32_t)grp + NG * st; };
+        auto tile_of = [&](uint32_t st) { return t0 + (uint32_t)grp + NG * st; };
 
         const __amdgpu_buffer_rsrc_t rK = rsrc_k(kvh), rV = rsrc_v(kvh);
         auto dma_k = [&](int par, uint32_t st) { dma_k_of(rK, par, tile_of(st)); };
@@ -495,7 +592,7 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // waits then count only tile loads.
         dma_done();
         if (a.q_dtype != kF16) {
-            const size_t qbase = (size_t)my_q * a.q_stride + (size_t)h * D + hh * 8;
+            const size_t qbase = (size_t)myrow.b * a.q_stride + (size_t)myrow.h * D + hh * 8;
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, qbase + kk * 16, a.q_dtype);
             dma_done();
@@ -512,8 +609,11 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // softmax of st; P.V of st (V buffer p); one barrier.  With pos_start
         // not a multiple of 32 a wave's queries straddle a tile boundary, so a
         // tile with a successor may still need the mask.
-        const uint32_t tail_step = (ntiles - 1) / NG;  // the step that reads the last tile
-        const int tail_grp = (int)((ntiles - 1) % NG);  // in this group's buffers
+        // the step that reads the tile holding kmax (the item's last tile, unless
+        // a later split owns it), in this group's buffers
+        const bool has_tail = ntiles > 0 && t0 + ntiles == kmax / BN + 1 && (kmax + 1) % BN != 0;
+        const uint32_t tail_step = (ntiles - 1) / NG;
+        const int tail_grp = (int)((ntiles - 1) % NG);
         const bool prefetch = has_next && early;
         // the group's last step (or, for a group without tiles, the first) issues
         // the next item's loads
@@ -523,10 +623,10 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
             if (st + 1 < gsteps) dma_v(1 - p, st + 1);
             if (prefetch && st == last_st) {
                 // K buffers are free (no scores follow), V buffer 1-p too
-                issue_item_k(qb_next, h_next);
-                if (p == 1 || gsteps == 0) issue_item_v(qb_next, h_next);
+                issue_item_k(nxt);
+                if (p == 1 || gsteps == 0) issue_item_v(nxt);
             }
-            if (st == tail_step && (kmax + 1) % BN != 0) {  // workgroup-uniform
+            if (has_tail && st == tail_step) {  // workgroup-uniform
                 if (grp == tail_grp) zero_v_tail(p, st);
                 lds_barrier();
             }
@@ -554,8 +654,8 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // the next item's first V tile when the last step still read V buffer 0,
         // and its queries
         if (prefetch) {
-            if (gsteps > 0 && (last_st & 1u) == 0) issue_item_v(qb_next, h_next);
-            issue_item_q(qb_next, h_next);
+            if (gsteps > 0 && (last_st & 1u) == 0) issue_item_v(nxt);
+            issue_item_q(nxt);
         }
         {
             // the lane pair (l, l+32) holds one query: add the halves
@@ -607,30 +707,107 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
                 if (r == 0) lds_barrier();  // round 0 read before round 1 overwrites
             }
         }
-        const uint32_t qi = qi0 + (gtid_e >> 6) * 32 + (lane_e & 31);
-        if ((tid_e >> 8) == 0 && qi < a.B) {  // group 1 handed its part over
-        const float inv = 1.0f / l;
-#pragma unroll
-        for (int b = 0; b < NDB; ++b) {
-#pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {
-                const uint32_t d = b * 32 + 8 * i4 + 4 * (lane_e >> 5);
-                f32x4 v;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = o[b][4 * i4 + e] * inv;
-                if (a.gate) {
-                    const float* gp = a.gate + (size_t)qi * a.gate_stride + (size_t)h * D + d;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] *= sigmoid_ref(gp[e]);
+        const PRow rw = row_of<SPLIT>(a, cur, (gtid_e >> 6) * 32 + (lane_e & 31));
+        if ((tid_e >> 8) == 0 && rw.valid) {  // group 1 handed its part over
+            if (SPLIT && a.n_split > 1) {
+                // split partials: (max, sum) and the unnormalised O of this
+                // row over this split's keys
+                const size_t pr = ((size_t)cur.split * a.n_heads + rw.h) * a.B + rw.b;
+                if ((lane_e >> 5) == 0) {
+                    typedef float f32x2 __attribute__((ext_vector_type(2)));
+                    *reinterpret_cast<f32x2*>(a.part_ml + 2 * pr) = f32x2{m, l};
                 }
-                store_out4(a.out, (size_t)qi * a.out_stride + (size_t)h * D + d, a.out_dtype, v);
+#pragma unroll
+                for (int b = 0; b < NDB; ++b)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4) {
+                        const uint32_t d = b * 32 + 8 * i4 + 4 * (lane_e >> 5);
+                        f32x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = o[b][4 * i4 + e];
+                        *reinterpret_cast<f32x4*>(a.part_o + pr * D + d) = v;
+                    }
+            } else {
+                const float inv = 1.0f / l;
+#pragma unroll
+                for (int b = 0; b < NDB; ++b) {
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4) {
+                        const uint32_t d = b * 32 + 8 * i4 + 4 * (lane_e >> 5);
+                        f32x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = o[b][4 * i4 + e] * inv;
+                        if (a.gate) {
+                            const float* gp = a.gate + (size_t)rw.b * a.gate_stride + (size_t)rw.h * D + d;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] *= sigmoid_ref(gp[e]);
+                        }
+                        store_out4(a.out, (size_t)rw.b * a.out_stride + (size_t)rw.h * D + d, a.out_dtype, v);
+                    }
+                }
             }
         }
-        }
         if (!has_next) break;
-        qb = qb_next;
-        h = h_next;
+        cur = nxt;
     }  // items
+}
+
+// One thread per (row, 4 output dimensions) of the split mode: the splits'
+// (max, sum, O) partials of query b of head h are combined in the log2
+// domain, then normalised, gated and stored.  Rows are b * n_heads + h, so a
+// workgroup's output stores are contiguous; each round of 8 splits issues
+// its loads together.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a)
+{
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    constexpr uint32_t C4 = D / 4;
+    constexpr uint32_t kRound = 8;
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t row = idx / C4, c4 = idx % C4;
+    if (row >= a.B * a.n_heads) return;
+    const uint32_t b = row / a.n_heads, h = row % a.n_heads;
+    const size_t split_stride = (size_t)a.n_heads * a.B;
+    const size_t p0 = (size_t)h * a.B + b;
+    float M = -1e30f, L = 0.0f;
+    f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s0 = 0; s0 < a.n_split; s0 += kRound) {
+        f32x2 ml[kRound];
+        f32x4 os[kRound];
+#pragma unroll
+        for (uint32_t r = 0; r < kRound; ++r) {
+            if (s0 + r < a.n_split) {
+                const size_t p = (s0 + r) * split_stride + p0;
+                ml[r] = *reinterpret_cast<const f32x2*>(a.part_ml + 2 * p);
+                os[r] = *reinterpret_cast<const f32x4*>(a.part_o + p * D + 4 * c4);
+            } else {
+                ml[r] = f32x2{-1e30f, 0.0f};
+                os[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        float mr = M;
+#pragma unroll
+        for (uint32_t r = 0; r < kRound; ++r) mr = fmaxf(mr, ml[r][0]);
+        const float co = fast_exp2(M - mr);
+        L *= co;
+        O *= co;
+#pragma unroll
+        for (uint32_t r = 0; r < kRound; ++r) {
+            const float c = fast_exp2(ml[r][0] - mr);
+            L += ml[r][1] * c;
+            O += os[r] * c;
+        }
+        M = mr;
+    }
+    // every query has key 0 in split 0, so L > 0
+    f32x4 v = O * (1.0f / L);
+    const uint32_t d = 4 * c4;
+    if (a.gate) {
+        const float* gp = a.gate + (size_t)b * a.gate_stride + (size_t)h * D + d;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] *= sigmoid_ref(gp[e]);
+    }
+    store_out4(a.out, (size_t)b * a.out_stride + (size_t)h * D + d, a.out_dtype, v);
 }
 
 int n_cus()
@@ -661,7 +838,8 @@ hipError_t launch_prefill_d(PrefillArgs a, hipStream_t st)
     // resident workgroups: one round of the grid fills every slot once
     static const int per_cu = [] {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<D, NG>, 256 * NG, 0) != hipSuccess || n < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<D, NG, false>, 256 * NG, 0) != hipSuccess ||
+            n < 1)
             n = 1;
         return n;
     }();
@@ -682,7 +860,21 @@ hipError_t launch_prefill_d(PrefillArgs a, hipStream_t st)
         if (a.xcd_map) grid = grid / 8u * 8u;  // whole XCD groups (items are a multiple of 8)
         if (grid == 0) grid = items;
     }
-    hipLaunchKernelGGL((prefill_kernel<D, NG>), dim3(grid), dim3(256 * NG), 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<D, NG, false>), dim3(grid), dim3(256 * NG), 0, st, a);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_prefill_split_d(const PrefillArgs& a, hipStream_t st)
+{
+    const uint32_t ipg = a.n_rb * (a.pack ? 1u : a.gmax);
+    const uint32_t groups = a.n_kv * a.n_split;
+    const uint32_t grid = (groups + 7u) / 8u * 8u * ipg;
+    hipLaunchKernelGGL((prefill_kernel<D, 1, true>), dim3(grid), dim3(256), 0, st, a);
+    if (a.n_split > 1) {
+        const uint64_t threads = (uint64_t)a.B * a.n_heads * (D / 4);
+        hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
@@ -708,8 +900,117 @@ int prefill_groups(const PrefillArgs& a)
 
 }  // namespace
 
+namespace {
+
+size_t align256p(size_t x) { return (x + 255) / 256 * 256; }
+
+// Split-mode tunables (YHIP_PREFILL_SPLIT=0 turns the mode off; the others
+// bound the split count and the tiles per split, for sweeps).
+struct SplitTune {
+    int on;
+    uint32_t max_split, min_tiles;
+};
+const SplitTune& split_tune()
+{
+    static const SplitTune t = [] {
+        SplitTune r{1, 16, 4};
+        if (const char* e = getenv("YHIP_PREFILL_SPLIT")) r.on = atoi(e) != 0;
+        if (const char* e = getenv("YHIP_PREFILL_MAXSPLIT")) r.max_split = (uint32_t)(atoi(e) > 0 ? atoi(e) : 1);
+        if (const char* e = getenv("YHIP_PREFILL_MINTILES")) r.min_tiles = (uint32_t)(atoi(e) > 0 ? atoi(e) : 1);
+        return r;
+    }();
+    return t;
+}
+
+size_t split_bytes(uint32_t n_split, uint32_t B, uint32_t n_heads, uint32_t D)
+{
+    if (n_split <= 1) return 0;
+    const size_t rows = (size_t)n_split * n_heads * B;
+    return align256p(rows * 2 * sizeof(float)) + rows * D * sizeof(float);
+}
+
+// Items of a split-mode launch before splitting, and the workgroups that
+// fill the GPU once.
+void split_shape(uint32_t B, uint32_t n_heads, uint32_t n_kv, uint32_t D, uint32_t& pack, uint32_t& n_rb,
+                 uint32_t& gmax, uint64_t& base, uint64_t& target)
+{
+    gmax = (n_heads + n_kv - 1) / n_kv;
+    pack = B < (uint32_t)BM;
+    n_rb = pack ? (gmax * B + BM - 1) / BM : (B + BM - 1) / BM;
+    base = (uint64_t)n_kv * n_rb * (pack ? 1u : gmax);
+    target = (uint64_t)(D <= 128 ? 2 : 1) * (uint64_t)n_cus();
+}
+
+}  // namespace
+
+size_t prefill_plan(PrefillArgs& a)
+{
+    a.split_mode = a.pack = 0;
+    a.n_split = 1;
+    a.split_tiles = 0;
+    a.n_rb = 0;
+    a.gmax = 0;
+    const SplitTune& t = split_tune();
+    // The plain mode, (query block, head) items, fills the GPU when there
+    // are at least as many items as CUs (prompts of a few hundred tokens and
+    // up).  Fewer items -- the engine's 64-token chunks over a long prefix
+    // -- would leave most CUs idle while each walks the whole prefix: the
+    // split mode packs a kv head's query heads into full 128-row items and
+    // splits the keys so that the launch fills the GPU.
+    if (!t.on || (uint64_t)((a.B + BM - 1) / BM) * a.n_heads >= (uint64_t)n_cus()) return 0;
+    uint64_t base, target;
+    split_shape(a.B, a.n_heads, a.n_kv, a.D, a.pack, a.n_rb, a.gmax, base, target);
+    a.split_mode = 1;
+    const uint32_t ntiles = (a.pos_start + a.B - 1) / BN + 1;
+    uint64_t S = target / base;
+    if (S > t.max_split) S = t.max_split;
+    const uint32_t by_tiles = (ntiles + t.min_tiles - 1) / t.min_tiles;
+    if (S > by_tiles) S = by_tiles;
+    if (S < 1) S = 1;
+    a.split_tiles = (ntiles + (uint32_t)S - 1) / (uint32_t)S;
+    a.n_split = (ntiles + a.split_tiles - 1) / a.split_tiles;
+    return split_bytes(a.n_split, a.B, a.n_heads, a.D);
+}
+
+size_t prefill_workspace_bound(uint32_t B, uint32_t max_end, uint32_t n_heads, uint32_t n_kv, uint32_t D)
+{
+    // the plan for any pos_start <= max_end - B: its split count is at most
+    // min(target/base, max_split, ceil(tiles/min_tiles)) with the most tiles
+    const SplitTune& t = split_tune();
+    if (!t.on || B == 0 || n_kv == 0 || max_end < B || (uint64_t)((B + BM - 1) / BM) * n_heads >= (uint64_t)n_cus())
+        return 0;
+    uint32_t pack, n_rb, gmax;
+    uint64_t base, target;
+    split_shape(B, n_heads, n_kv, D, pack, n_rb, gmax, base, target);
+    const uint32_t ntiles = (max_end - 1) / BN + 1;
+    uint64_t S = target / base;
+    if (S > t.max_split) S = t.max_split;
+    const uint32_t by_tiles = (ntiles + t.min_tiles - 1) / t.min_tiles;
+    if (S > by_tiles) S = by_tiles;
+    return split_bytes((uint32_t)(S < 1 ? 1 : S), B, n_heads, D);
+}
+
+void prefill_bind_workspace(PrefillArgs& a, void* workspace)
+{
+    if (a.n_split <= 1 || !workspace) {
+        a.part_ml = a.part_o = nullptr;
+        return;
+    }
+    char* p = reinterpret_cast<char*>(workspace);
+    a.part_ml = reinterpret_cast<float*>(p);
+    a.part_o = reinterpret_cast<float*>(p + align256p((size_t)a.n_split * a.n_heads * a.B * 2 * sizeof(float)));
+}
+
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st)
 {
+    if (a.split_mode) {
+        switch (a.D) {
+        case 64: return launch_prefill_split_d<64>(a, st);
+        case 128: return launch_prefill_split_d<128>(a, st);
+        case 256: return launch_prefill_split_d<256>(a, st);
+        default: return hipErrorInvalidValue;
+        }
+    }
     const int ng = prefill_groups(a);
     switch (a.D) {
     case 64: return ng == 2 ? launch_prefill_d<64, 2>(a, st) : launch_prefill_d<64, 1>(a, st);

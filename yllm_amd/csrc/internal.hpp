@@ -78,7 +78,25 @@ struct PrefillArgs {
     // head per XCD (xcd_map) and dealt to gridDim.x resident workgroups in
     // snake order, heaviest first
     uint32_t xcd_map;
+    // Split mode (set by prefill_plan for launches with fewer work items
+    // than CUs, e.g. the engine's 64-token chunks over a long prefix): an
+    // item is (row block, kv head, key split).  With pack, the rows of a kv
+    // head are its query heads' B queries each (head-major, G*B rows), so
+    // 128 rows fill a workgroup even when B < 128; otherwise rows are the B
+    // queries of one head.  Split s covers key tiles [s*split_tiles,
+    // (s+1)*split_tiles); with n_split > 1 the workgroups write (max, sum,
+    // unnormalised O) partials and a merge kernel forms the output.
+    uint32_t split_mode, pack, n_split, split_tiles, n_rb, gmax;
+    float* part_ml;  // [n_split][n_heads][B][2]
+    float* part_o;   // [n_split][n_heads][B][D]
 };
+// Work plan of a prefill launch: fills the split-mode fields of a and
+// returns the workspace bytes it needs (0 without partials).
+size_t prefill_plan(PrefillArgs& a);
+// Workspace bytes that serve every launch of B query tokens with pos_start +
+// B <= max_end (the split count does not grow with pos_start beyond a bound).
+size_t prefill_workspace_bound(uint32_t B, uint32_t max_end, uint32_t n_heads, uint32_t n_kv, uint32_t D);
+void prefill_bind_workspace(PrefillArgs& a, void* workspace);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
 
 // ---- rope.hip ----

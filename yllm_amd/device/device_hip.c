@@ -121,6 +121,8 @@ typedef struct {
     uint16_t* d_rows;  /* host f16 rows on their way into HBM (catch-up) */
     void* d_ws;
     size_t ws_bytes;
+    void* d_pws;        /* prefill key-split partials for up to cap tokens per call */
+    size_t pws_bytes;
     /* host rows of a qwen35 block: normed input, q or qkv, gate or z,
      * k, v, alpha / beta / gate, GPU output, projection output */
     float *h_n, *h_q, *h_z, *h_k, *h_v, *h_ab, *h_o, *h_x;
@@ -164,6 +166,9 @@ static void dfree(void* p)
 
 static void free_staging(HipCtx* c)
 {
+    dfree(c->d_pws);
+    c->d_pws = NULL;
+    c->pws_bytes = 0;
     dfree(c->d_q);
     dfree(c->d_k);
     dfree(c->d_v);
@@ -241,6 +246,13 @@ static int ensure_cap(HipCtx* c, uint32_t rows)
             if (c->gws_bytes && hipMalloc(&c->d_gws, c->gws_bytes) != hipSuccess) return -1;
         }
     }
+    /* the prefill's key-split partials, for every call of up to `rows`
+     * tokens ending at or before max_seq */
+    for (uint32_t b = 1; b <= rows; ++b) {
+        size_t n = yhip_attn_prefill_workspace(b, c->max_seq, c->n_heads, c->n_kv, c->head_dim);
+        if (n > c->pws_bytes) c->pws_bytes = n;
+    }
+    if (c->pws_bytes && hipMalloc(&c->d_pws, c->pws_bytes) != hipSuccess) return -1;
     c->cap = rows;
     return 0;
 }
@@ -501,7 +513,7 @@ static int q35_attn(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_
                               c->ws_bytes, c->stream) == YHIP_OK;
     else
         ok = yhip_attn_prefill(c->d_out, YHIP_F32, qd, c->d_q, YHIP_F32, qd, kc, vc, pos0, B, c->n_heads, c->n_kv, hd,
-                               c->kv_stride, c->d_g, qd, c->stream) == YHIP_OK;
+                               c->kv_stride, c->d_g, qd, c->d_pws, c->pws_bytes, c->stream) == YHIP_OK;
     ok = ok &&
          hipMemcpyAsync(c->h_o, c->d_out, (size_t)B * qd * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
          hipStreamSynchronize(c->stream) == hipSuccess;
@@ -646,7 +658,8 @@ static int gpu_prefill(HipCtx* c, Engine* e, uint32_t layer, uint32_t pos_start,
         return -1;
     c->dev_len[c->kv_slot[layer - c->first]] = pos_start + B;
     if (yhip_attn_prefill(c->d_out, YHIP_F32, c->hidden, c->d_q, YHIP_F32, c->hidden, kc, vc, pos_start, B,
-                          c->n_heads, c->n_kv, c->head_dim, c->kv_stride, NULL, 0, c->stream) != YHIP_OK)
+                          c->n_heads, c->n_kv, c->head_dim, c->kv_stride, NULL, 0, c->d_pws, c->pws_bytes,
+                          c->stream) != YHIP_OK)
         return -1;
     if (hipMemcpyAsync(e->pb2, c->d_out, nq * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return -1;
     return hipStreamSynchronize(c->stream) == hipSuccess ? 0 : -1;
