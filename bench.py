@@ -23,7 +23,8 @@ batch of synthetic input, with all inputs resident in HBM:
               32 / 8 heads of 128 (llama pairs, theta 5e5), f32 q/k/v
               slices of one projection row -> f16 q, f16 K/V cache.
   oproj8k     o_proj after prefill attention: x += W_o . att, 8192 tokens,
-              W_o 4096 x 4096 f16, f16 att (one hipBLASLt GEMM).
+              W_o 4096 x 4096 f16, f16 att (the MFMA GEMM, residual fused).
+  oproj64     the same for the engine's 64-token prefill chunk, f32 att.
   oproj1      the same for one decode token (the GEMV kernel, HBM-bound).
   kvstore8k   the KV store on its own: 8192 rows of K and V, 8 KV heads of
               128, f32 -> f16 with the reference rounding into the
@@ -586,7 +587,7 @@ def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool
     w = (torch.from_numpy(synth_raw(seed, hidden * qdim).reshape(hidden, qdim)).to(dev) / np.sqrt(qdim)).half()
     att = torch.from_numpy(synth_raw(seed, B * qdim, hidden * qdim).reshape(B, qdim)).to(dev) * 0.5
     gemv = B <= 8
-    if not gemv:
+    if B > 64:  # a prefill-sized batch: the attention kernel's f16 output
         att = att.half()
     x = torch.from_numpy(synth_raw(seed, B * hidden, hidden * qdim + B * qdim).reshape(B, hidden)).to(dev)
     # rotating (weights, att, x) sets beyond the 256 MB MALL
@@ -596,7 +597,7 @@ def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool
     sets = [(w.clone(), att.clone(), x.clone()) for _ in range(n_sets)]
     x_ref = x.clone()
     del w, att, x
-    ws = torch.empty(max(o_proj_workspace_bytes(B, qdim, torch.float16, att_dt), 256), dtype=torch.uint8,
+    ws = torch.empty(max(o_proj_workspace_bytes(B, hidden, qdim, torch.float16, att_dt), 256), dtype=torch.uint8,
                      device=dev)
 
     def step(i):
@@ -604,9 +605,8 @@ def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool
         o_proj(xi, ai, wi, workspace=ws)
 
     last = sets[(warmup + steps - 1) % n_sets]
-    # x accumulates from step to step, so no replay-vs-eager output check; the
-    # GEMM path (hipBLASLt) is launched eagerly, outside any graph capture
-    ms, kern_ms = time_steps(step, steps, warmup, None, eager=not gemv)
+    # x accumulates from step to step, so no replay-vs-eager output check
+    ms, kern_ms = time_steps(step, steps, warmup, None)
     flops = 2.0 * B * hidden * qdim
     nbytes = hidden * qdim * 2.0 + B * qdim * att_size + 2.0 * B * hidden * 4.0
     if gemv:
@@ -616,7 +616,8 @@ def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool
                 "traffic": traffic_of(f"oproj{B}")}
         value, unit = nbytes / (ms * 1e-3) / 1e9, "GB/s"
     else:
-        roof = {"bound": "mfma", "kernel": "hipBLASLt f16 GEMM (f32 C/D, beta 1)",
+        roof = {"bound": "mfma", "kernel": ("oproj_gemm_kernel<%d,%d>" % ((4, 4) if B > 128 else (1, 1))) +
+                ("" if att_dt == torch.float16 else " (+ oproj_split_kernel)"),
                 "achieved": flops / (kern_ms * 1e-3) / 1e12, "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                 "frac": flops / (kern_ms * 1e-3) / MFMA_F16_PEAK, "flops_per_launch": flops, "launch_ms": kern_ms,
                 "traffic": traffic_of(f"oproj{B}")}
@@ -624,7 +625,7 @@ def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool
     res = {
         "value": value, "unit": unit, "ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3),
         "config": {"workload": f"o_proj x += W_o . att, {B} token(s), W_o {hidden} x {qdim} f16, "
-                               f"{'f32' if gemv else 'f16'} att, f32 residual, N(0,1) seed {hex(seed)}; "
+                               f"{'f32' if att_dt == torch.float32 else 'f16'} att, f32 residual, N(0,1) seed {hex(seed)}; "
                                f"{n_sets} rotating sets (> 256 MB MALL)",
                    "tokens": B, "hidden": hidden, "qdim": qdim},
         "roofline": roof,
@@ -1106,7 +1107,7 @@ DTYPES = {"gdn4k": "f32", "rope8k": "f32 rotation, f16 stores", "oproj8k": "f16 
 
 
 def timing_of(w: str, steps: int) -> str:
-    how = ("K eager launches" if EAGER or w == "oproj8k" else
+    how = ("K eager launches" if EAGER else
            "one step captured in a HIP graph, replayed K times" if w == "hybrid" else
            "K steps captured in one HIP graph")
     return how + ", timed with HIP events on the launch stream"
@@ -1135,6 +1136,8 @@ def run_workload(w: str, steps: int, warmup: int, cpu: bool):
         return run_oproj(8192, 4096, 4096, steps, warmup, cpu)
     if w == "oproj1":
         return run_oproj(1, 4096, 4096, steps, warmup, cpu)
+    if w == "oproj64":
+        return run_oproj(64, 4096, 4096, steps, warmup, cpu)
     if w == "kvstore8k":
         return run_kvstore(8192, 8, 128, steps, warmup, cpu)
     if w == "gated4k":
@@ -1151,7 +1154,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="prefill2k",
                     choices=["prefill2k", "prefill8k", "prefill2k_chunked", "prefill8k_chunked", "decode32k", "decode128k", "decode_batch", "gdn4k",
-                             "rope8k", "oproj8k", "oproj1", "kvstore8k", "gated4k", "hybrid"])
+                             "rope8k", "oproj8k", "oproj64", "oproj1", "kvstore8k", "gated4k", "hybrid"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the other configurations' secondary lines (" + ", ".join(SECONDARY) + ")")

@@ -205,19 +205,22 @@ int yhip_rope_kv_store(void* q_out, uint32_t q_out_dtype, uint32_t q_out_stride,
 /* ---- o_proj (the step after attention) -------------------------------------
  * x[b] += W_o . att[b] for B tokens: matmul(att_out, x2, SLOT_O) then the
  * residual add (engine.c:969-973; qwen35 after its gate, 958-973), with
- * matmul_f16 / matmul_f32 (matvec.c:98-122, dispatch 785-795).  w: W_o
- * [hidden][qdim] row-major, YHIP_F16 or YHIP_F32 (the reference's matmul
- * reads DT_BF16 slots as f16 bits, matvec.c:793, so BF16 is refused; the
- * quantised slot types stay on the engine's CPU matmul).  att [B][qdim] is
- * YHIP_F32 (the engine's att_out) or YHIP_F16 (an attention output written
- * as f16; needs f16 weights); x [B][hidden] f32; rows att_stride /
- * x_stride elements apart; x is updated in place.  Up to 8 tokens: one pass
- * over the weights, products and sums in f32 (no workspace).  More:
- * hipBLASLt GEMMs with f32 accumulation (f16 weights with f32 att take att
- * as f16 hi + lo parts, two GEMMs); workspace of yhip_o_proj_workspace
- * bytes.  qdim must be a multiple of 8; w and att 16-byte aligned with
- * att_stride a multiple of 8 elements. */
-size_t yhip_o_proj_workspace(uint32_t B, uint32_t qdim, uint32_t w_dtype, uint32_t att_dtype);
+ * matmul_f16 / matmul_f32 (matvec.c:98-122, dispatch 785-795); replaces the
+ * reference CUDA backend's cublasGemmEx call for this product
+ * (cuda_kernels.cu:104-112).  w: W_o [hidden][qdim] row-major, YHIP_F16 or
+ * YHIP_F32 (the reference's matmul reads DT_BF16 slots as f16 bits,
+ * matvec.c:793, so BF16 is refused; the quantised slot types stay on the
+ * engine's CPU matmul).  att [B][qdim] is YHIP_F32 (the engine's att_out) or
+ * YHIP_F16 (an attention output written as f16; needs f16 weights); x
+ * [B][hidden] f32; rows att_stride / x_stride elements apart; x is updated
+ * in place.  Up to 8 tokens: one pass over the weights, products and sums in
+ * f32 (no workspace).  More: an f16 MFMA GEMM with f32 accumulation and the
+ * residual add fused (f32 att, and f32 weights, enter as f16 hi + lo parts
+ * whose products accumulate together: about 22 bits of each operand); the
+ * parts take yhip_o_proj_workspace bytes (0 for f16 att).  qdim must be a
+ * multiple of 8; w and att 16-byte aligned with att_stride a multiple of 8
+ * elements; hidden * qdim below 2^30. */
+size_t yhip_o_proj_workspace(uint32_t B, uint32_t hidden, uint32_t qdim, uint32_t w_dtype, uint32_t att_dtype);
 int yhip_o_proj(float* x, uint32_t x_stride, const void* att, uint32_t att_dtype, uint32_t att_stride,
                 const void* w, uint32_t w_dtype, uint32_t B, uint32_t hidden, uint32_t qdim, void* workspace,
                 size_t workspace_bytes, void* stream);

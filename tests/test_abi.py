@@ -226,13 +226,15 @@ def test_o_proj_rejects_bad_args(hiplib):
     assert call(ats=4100) == -22 and "strides" in _err(hiplib)
     assert call(w=ctypes.c_void_p(0x1008)) == -22 and "aligned" in _err(hiplib)
     assert call(att=None) == -22 and "null" in _err(hiplib)
-    # up to 8 tokens need no workspace; more need the hipBLASLt workspace (+ f16 hi/lo rows)
-    assert hiplib.yhip_o_proj_workspace(8, 4096, 0, 1) == 0
-    need16 = hiplib.yhip_o_proj_workspace(64, 4096, 0, 1)
-    need32 = hiplib.yhip_o_proj_workspace(64, 4096, 1, 1)
-    assert need16 == need32 + 2 * 64 * 4096 * 2 and need32 >= 1 << 20
-    assert hiplib.yhip_o_proj_workspace(64, 4096, 0, 0) == need32  # f16 att: one GEMM, no hi/lo rows
+    # up to 8 tokens need no workspace; more need the f16 hi/lo parts of f32 att (and of f32 weights)
+    assert hiplib.yhip_o_proj_workspace(8, 4096, 4096, 0, 1) == 0
+    need16 = hiplib.yhip_o_proj_workspace(64, 4096, 4096, 0, 1)
+    need32 = hiplib.yhip_o_proj_workspace(64, 4096, 4096, 1, 1)
+    assert need16 == 2 * 64 * 4096 * 2
+    assert need32 == need16 + 2 * 4096 * 4096 * 2
+    assert hiplib.yhip_o_proj_workspace(64, 4096, 4096, 0, 0) == 0  # f16 att: one product, no parts
     assert call(B=64, ws=P, wsb=need16 - 1) == -28 and "workspace" in _err(hiplib)
+    assert call(hidden=32768, qdim=32768) == -22  # the weights' byte offsets must fit 32 bits
     assert call(B=0) == 0
 
 

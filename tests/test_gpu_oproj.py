@@ -2,9 +2,9 @@
 
 x[b] += W_o . att[b].  Up to 8 tokens the GEMV kernel keeps every product
 and sum in f32 (the reference's arithmetic in another order); more tokens go
-through hipBLASLt with f16 weights times the f16 hi + lo parts of f32 att
+through the MFMA GEMM with f16 weights times the f16 hi + lo parts of f32 att
 (about 22 bits of each activation), f16 weights times f16 att (the attention
-kernel's f16 output, one GEMM) or f32 weights times f32 att.  Either way the
+kernel's f16 output) or, for f32 weights, the hi + lo parts of both.  Either way the
 result must be within relative L2 1e-5 of the f32 oracle (the stated bar is
 1e-3), on the updated x and on the product alone.
 """
@@ -45,6 +45,10 @@ def to_dev(cuda, w):
     (64, 4096, 4096, True),
     (300, 2048, 4096, True),
     (77, 1024, 2048, False),  # f32 GEMM
+    (200, 4096, 4096, True),  # 256 x 256 tiles, a partial token tile
+    (200, 1000, 904, False),  # f32 weights; hidden and qdim no multiples of the tiles or of 64
+    (130, 520, 1032, True),   # the smallest 256-token tile config, ragged edges
+    (64, 333, 904, True),     # the engine's 64-token chunk, ragged edges
 ])
 def test_o_proj_matches_oracle(cuda, oracle, B, hidden, qdim, f16):
     from yllm_amd.attention import o_proj
@@ -89,7 +93,7 @@ def test_o_proj_strided_rows_and_repeat(cuda, oracle):
     hidden, qdim = 1024, 2048
     w = weights(oracle, 2101, hidden, qdim, True)
     wt = to_dev(cuda, w)
-    ws = torch.empty(o_proj_workspace_bytes(40, qdim, torch.float16), dtype=torch.uint8, device=cuda)
+    ws = torch.empty(o_proj_workspace_bytes(40, hidden, qdim, torch.float16), dtype=torch.uint8, device=cuda)
     for B in (40, 12, 5):
         x0 = gen(2102 + B, (B, hidden + 64))
         att = gen(2103 + B, (B, qdim + 32), 0.5)

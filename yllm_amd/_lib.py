@@ -49,7 +49,7 @@ SIGNATURES = {
     "yhip_rope_kv_store": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p,
                                    c_uint32, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                                    c_uint32, c_uint32, c_uint32, c_float, c_void_p]),
-    "yhip_o_proj_workspace": (c_size_t, [c_uint32, c_uint32, c_uint32, c_uint32]),
+    "yhip_o_proj_workspace": (c_size_t, [c_uint32, c_uint32, c_uint32, c_uint32, c_uint32]),
     "yhip_o_proj": (c_int, [c_void_p, c_uint32, c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, c_uint32, c_uint32,
                             c_uint32, c_void_p, c_size_t, c_void_p]),
     "yhip_gdn_decode": (c_int, [c_void_p] * 12 + [c_uint32] * 5 + [c_float, c_float, c_void_p]),

@@ -149,8 +149,9 @@ def rope_kv_store(cache: LayerKV, q: torch.Tensor | None, k: torch.Tensor, v: to
     return q_out if q is not None else None
 
 
-def o_proj_workspace_bytes(B: int, qdim: int, w_dtype: torch.dtype, att_dtype: torch.dtype = torch.float32) -> int:
-    return int(lib().yhip_o_proj_workspace(B, qdim, _DT[w_dtype], _DT[att_dtype]))
+def o_proj_workspace_bytes(B: int, hidden: int, qdim: int, w_dtype: torch.dtype,
+                           att_dtype: torch.dtype = torch.float32) -> int:
+    return int(lib().yhip_o_proj_workspace(B, hidden, qdim, _DT[w_dtype], _DT[att_dtype]))
 
 
 def o_proj(x: torch.Tensor, att: torch.Tensor, w: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
@@ -169,7 +170,7 @@ def o_proj(x: torch.Tensor, att: torch.Tensor, w: torch.Tensor, workspace: torch
     if not w.is_contiguous() or w.dim() != 2 or w.shape[1] != att.shape[1] or w.shape[0] != x.shape[1]:
         raise YhipError(-22, f"o_proj: w {tuple(w.shape)} does not match att {tuple(att.shape)} / x {tuple(x.shape)}")
     B, hidden, qdim = x.shape[0], w.shape[0], w.shape[1]
-    need = o_proj_workspace_bytes(B, qdim, w.dtype, att.dtype)
+    need = o_proj_workspace_bytes(B, hidden, qdim, w.dtype, att.dtype)
     ws = _workspace(need, x.device, workspace)
     xs = x.stride(0) if B > 1 else hidden
     ats = att.stride(0) if B > 1 else qdim

@@ -1,8 +1,7 @@
 """Build the gfx950 attention library in-tree: yllm_amd/libyllm_hip.so.
 
 Every source under yllm_amd/csrc is compiled with hipcc for gfx950 and
-linked into one shared library with a plain C ABI (include/yllm_hip.h),
-against hipBLASLt (the o_proj GEMMs).
+linked into one shared library with a plain C ABI (include/yllm_hip.h).
 Packed-fp32 instruction selection is switched off for device code
 (-Xclang -target-feature -Xclang -packed-fp32-ops).
 
@@ -72,7 +71,7 @@ def build(verbose: bool = True) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     rocm_lib = Path(hipcc).resolve().parent.parent / "lib"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-           f"-L{rocm_lib}", "-lhipblaslt", f"-Wl,-rpath,{rocm_lib}"]
+           f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

@@ -407,9 +407,9 @@ int yhip_rope_kv_store(void* q_out, uint32_t q_out_dtype, uint32_t q_out_stride,
     return done(yhip::launch_rope_kv(a, (hipStream_t)stream), fn);
 }
 
-size_t yhip_o_proj_workspace(uint32_t B, uint32_t qdim, uint32_t w_dtype, uint32_t att_dtype)
+size_t yhip_o_proj_workspace(uint32_t B, uint32_t hidden, uint32_t qdim, uint32_t w_dtype, uint32_t att_dtype)
 {
-    return yhip::oproj_workspace(B, qdim, w_dtype == YHIP_F16, att_dtype == YHIP_F16);
+    return yhip::oproj_workspace(B, qdim, w_dtype == YHIP_F16, att_dtype == YHIP_F16, hidden);
 }
 
 int yhip_o_proj(float* x, uint32_t x_stride, const void* att, uint32_t att_dtype, uint32_t att_stride,
@@ -423,14 +423,15 @@ int yhip_o_proj(float* x, uint32_t x_stride, const void* att, uint32_t att_dtype
     if (att_dtype != YHIP_F32 && !(att_dtype == YHIP_F16 && w_dtype == YHIP_F16))
         return fail(YHIP_EINVAL, "%s: att_dtype must be YHIP_F32, or YHIP_F16 with f16 weights", fn);
     if (hidden == 0 || qdim == 0 || qdim % 8) return fail(YHIP_EINVAL, "%s: qdim %u must be a positive multiple of 8", fn, qdim);
-    if (x_stride < hidden || att_stride < qdim || att_stride % 8)
-        return fail(YHIP_EINVAL, "%s: strides must cover the rows (att_stride a multiple of 8)", fn);
+    if (x_stride < hidden || att_stride < qdim || att_stride % 8 || x_stride >= (1u << 27))
+        return fail(YHIP_EINVAL, "%s: strides must cover the rows (att_stride a multiple of 8, x_stride < 2^27)", fn);
     if ((uintptr_t)w % 16 || (uintptr_t)att % 16 || (uintptr_t)x % 4)
         return fail(YHIP_EINVAL, "%s: w and att must be 16-byte aligned", fn);
-    if ((uint64_t)B * qdim > 0x7fffffffull || (uint64_t)hidden * qdim > 0xffffffffull)
+    // the GEMM addresses the weights with 32-bit byte offsets (f16 parts)
+    if ((uint64_t)B * qdim > 0x7fffffffull || (uint64_t)hidden * qdim >= (1ull << 30))
         return fail(YHIP_EINVAL, "%s: too many elements", fn);
     if (B == 0) return done(hipSuccess, "");
-    const size_t need = yhip::oproj_workspace(B, qdim, w_dtype == YHIP_F16, att_dtype == YHIP_F16);
+    const size_t need = yhip::oproj_workspace(B, qdim, w_dtype == YHIP_F16, att_dtype == YHIP_F16, hidden);
     if (need && (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256))
         return fail(YHIP_ENOSPC, "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", fn, need,
                     workspace_bytes);

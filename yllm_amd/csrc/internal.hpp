@@ -124,9 +124,8 @@ struct OProjArgs {
     const void* w;          // [hidden][qdim], f16 when w_f16 else f32
     uint32_t x_stride, att_stride, B, hidden, qdim, w_f16, att_f16;
 };
-constexpr uint32_t kGemvRows = 8;                 // up to this many tokens: one pass over the weights
-constexpr size_t kGemmWorkspace = (size_t)32 << 20;  // hipBLASLt workspace
-size_t oproj_workspace(uint32_t B, uint32_t qdim, uint32_t w_f16, uint32_t att_f16);
+constexpr uint32_t kGemvRows = 8;  // up to this many tokens: one pass over the weights
+size_t oproj_workspace(uint32_t B, uint32_t qdim, uint32_t w_f16, uint32_t att_f16, uint32_t hidden);
 // null on success, else a message
 const char* launch_oproj(const OProjArgs& a, void* ws, size_t ws_bytes, hipStream_t st);
 
