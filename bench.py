@@ -1126,6 +1126,8 @@ def run_workload(w: str, steps: int, warmup: int, cpu: bool):
         return run_decode(32768, 32, 8, 128, 4, 6, steps, warmup, cpu, "decode32k")
     if w == "decode128k":
         return run_decode(131072, 32, 8, 128, 4, 2, steps, warmup, cpu, "decode128k")
+    if w == "decode4k_d256":  # the hybrid group's gated-attention decode step at the end of its 256 steps
+        return run_decode(4352, 16, 2, 256, 5, 64, steps, warmup, cpu, "decode4k_d256")
     if w == "decode_batch":
         return run_decode_batch(32, 8, 128, 64, steps, warmup, cpu)
     if w == "gdn4k":
@@ -1153,7 +1155,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="prefill2k",
-                    choices=["prefill2k", "prefill8k", "prefill2k_chunked", "prefill8k_chunked", "decode32k", "decode128k", "decode_batch", "gdn4k",
+                    choices=["prefill2k", "prefill8k", "prefill2k_chunked", "prefill8k_chunked", "decode32k", "decode4k_d256", "decode128k", "decode_batch", "gdn4k",
                              "rope8k", "oproj8k", "oproj64", "oproj1", "kvstore8k", "gated4k", "hybrid"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true",

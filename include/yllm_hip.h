@@ -262,7 +262,7 @@ int yhip_gdn_chunk(float* S, float* out, uint32_t out_stride, const float* q, co
 /* Workspace bytes of the chunked form for T tokens (0 when T < 64). */
 size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_dim);
 
-/* One decode token of a Gated DeltaNet layer in two launches (engine.c:786-847
+/* One decode token of a Gated DeltaNet layer in one launch (engine.c:786-847
  * after the projections): the gates of alpha / beta_raw (788-793),
  * conv1d_update + silu of the projected row qkv (805-812, the conv bit for bit
  * the reference's), l2norm of q and k with l2_eps (826-827), the state update

@@ -1,11 +1,13 @@
-// gdn_decode.hip -- one decode token of a Gated DeltaNet layer in two launches
+// gdn_decode.hip -- one decode token of a Gated DeltaNet layer
 // (engine.c:786-847 for a single token): the gates (788-793), conv1d +
 // silu over the projected qkv row (805-812, conv1d_update matvec.c:956-968),
 // l2norm of q and k per k head (826-827, matvec.c:942-949), the state update
 // and output (gdn_state_update, matvec.c:975-1004) and the gated RMSNorm of
 // each v head (845-847, rmsnorm_gated matvec.c:1007-1021).
 //
-// Two launches.  gdn_decode_kernel: a workgroup (256 threads) owns 16 state
+// The default is one launch, gdn_decode_head_kernel (below): a 1024-thread
+// workgroup per v head with the gated RMSNorm fused.  The two-launch form
+// (YHIP_GDN_DECODE2=1): gdn_decode_kernel, a workgroup (256 threads) owns 16 state
 // columns of v head h (D/16 workgroups per head, as gdn_step_kernel), which
 // reads k head kh = h % n_k:
 //  1. every thread issues its loads at once: its slice of the state, one q
@@ -28,6 +30,7 @@
 #include "internal.hpp"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace yhip {
 namespace {
@@ -173,10 +176,157 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(GdnDecodeArgs a)
     if (part == 0) a.y[(size_t)h * D + j] = o;
 }
 
+// One launch for the whole token: a workgroup of 1024 threads owns a whole
+// v head (TPC = 1024 / D threads per state column, SL = D / TPC elements
+// each), so the gated RMSNorm's sum over the head's D outputs stays in the
+// workgroup.  Every thread issues its loads at once (state slice, one conv
+// channel: threads 0..2D-1 the q/k channels of k head kh, 2D..3D-1 the v
+// channels of head h), then conv + silu, l2 norms, gates, the state update
+// and the normalised, gated outputs.  The head's 64 KiB of state (D = 128)
+// moves through one CU; with a 16-column workgroup per 256 threads the state
+// is spread over 8 CUs, but the RMSNorm then needs a second launch.
+template <int D>
+__global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
+{
+#pragma clang fp contract(off)
+    constexpr int NT = 1024;
+    constexpr int TPC = NT / D;   // threads per state column
+    constexpr int SL = D / TPC;   // state elements per thread
+    static_assert(3 * D <= NT, "one conv channel per thread");
+    __shared__ float qs[D], ks[D], vs[D];
+    __shared__ float red[2];
+    __shared__ float ssq[NT / 64];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t h = blockIdx.x, kh = h % a.n_k;
+    const uint32_t key_dim = a.n_k * D;
+    const uint32_t j = tid / TPC, part = tid % TPC;
+
+    float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
+    float s[SL];
+#pragma unroll
+    for (int i = 0; i < SL; i += 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(Sp + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[i + e] = x[e];
+    }
+    // this thread's conv channel: q (tid < D), k (< 2D) of head kh, v (< 3D) of head h
+    const bool has_ch = tid < 3 * D;
+    const uint32_t ch = tid < D ? kh * D + tid
+                        : tid < 2 * D ? key_dim + kh * D + (tid - D)
+                                      : 2 * key_dim + h * D + (tid - 2 * D);
+    float X[kMaxKw], w[kMaxKw];
+    if (has_ch) {
+#pragma unroll
+        for (int r = 0; r < kMaxKw; ++r) {
+            if (r >= (int)a.kwidth) break;
+            w[r] = a.conv_w[(size_t)ch * a.kwidth + r];
+            X[r] = r + 1 < (int)a.kwidth ? a.conv_in[(size_t)(r + 1) * a.conv_dim + ch] : a.qkv[ch];
+        }
+    }
+    const float zv = part == 0 ? a.z[(size_t)h * D + j] : 0.0f;
+    const float wv = part == 0 ? (a.norm_w_f16 ? (float)reinterpret_cast<const _Float16*>(a.norm_w)[j]
+                                               : reinterpret_cast<const float*>(a.norm_w)[j])
+                               : 0.0f;
+    if (has_ch) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kMaxKw; ++r) {
+            if (r >= (int)a.kwidth) break;
+            acc = acc + X[r] * w[r];
+        }
+        const float y = acc / (1.0f + expf(-acc));
+        if (tid < D) qs[tid] = y;
+        else if (tid < 2 * D) ks[tid - D] = y;
+        else vs[tid - 2 * D] = y;
+        // the delay line: head kh's q/k channels by the workgroup of v head
+        // kh (n_v >= n_k), v channels by their own head's
+        if (tid >= 2 * D || h == kh) {
+#pragma unroll
+            for (int r = 0; r < kMaxKw; ++r) {
+                if (r >= (int)a.kwidth) break;
+                a.conv_out[(size_t)r * a.conv_dim + ch] = X[r];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave < 2) {
+        const float* src = wave == 0 ? qs : ks;
+        float ss = 0.0f;
+        for (int i = lane; i < D; i += 64) ss += src[i] * src[i];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        if (lane == 0) red[wave] = 1.0f / fmaxf(sqrtf(ss), a.l2_eps);
+    }
+    __syncthreads();
+    const float rq = red[0], rk = red[1];
+    const float bt = 1.0f / (1.0f + expf(-a.beta_raw[h]));
+    const float g = expf(log1pf(expf(a.alpha[h] + a.dt_bias[h])) * a.ssm_a[h]);
+
+    float k[SL], q[SL];
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+        k[i] = ks[part * SL + i] * rk;
+        q[i] = qs[part * SL + i] * rq;
+    }
+    auto sum_tpc = [](float x) {
+#pragma unroll
+        for (int m = TPC / 2; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+        return x;
+    };
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+        s[i] *= g;
+        p = fmaf(s[i], k[i], p);
+    }
+    const float delta = (vs[j] - sum_tpc(p)) * bt;
+    float p2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+        s[i] = fmaf(k[i], delta, s[i]);
+        p2 = fmaf(s[i], q[i], p2);
+    }
+    const float o = sum_tpc(p2) * (1.0f / sqrtf((float)D));
+#pragma unroll
+    for (int i = 0; i < SL; i += 4) {
+        f32x4 x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = s[i + e];
+        *reinterpret_cast<f32x4*>(Sp + i) = x;
+    }
+    // rmsnorm_gated over the head's D outputs (matvec.c:1007-1021), as
+    // gdn_gated_norm_kernel computes it
+    float sq = part == 0 ? o * o : 0.0f;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) sq += __shfl_xor(sq, m, 64);
+    if (lane == 0) ssq[wave] = sq;
+    __syncthreads();
+    float ss = 0.0f;
+#pragma unroll
+    for (int wv2 = 0; wv2 < NT / 64; ++wv2) ss += ssq[wv2];
+    const float inv = 1.0f / sqrtf(ss / (float)D + a.norm_eps);
+    if (part == 0) a.y[(size_t)h * D + j] = o * wv * inv * (zv / (1.0f + expf(-zv)));
+}
+
 }  // namespace
 
 hipError_t launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t st)
 {
+    // one workgroup per v head, the norm fused (one launch); YHIP_GDN_DECODE2=1
+    // selects the two-launch form (16-column workgroups + the norm kernel)
+    static const int two = [] {
+        const char* e = getenv("YHIP_GDN_DECODE2");
+        return e ? atoi(e) : 0;
+    }();
+    if (!two) {
+        switch (a.D) {
+        case 64: hipLaunchKernelGGL(gdn_decode_head_kernel<64>, dim3(a.n_v), dim3(1024), 0, st, a); break;
+        case 128: hipLaunchKernelGGL(gdn_decode_head_kernel<128>, dim3(a.n_v), dim3(1024), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (a.D) {
     case 64: hipLaunchKernelGGL(gdn_decode_kernel<64>, dim3(a.n_v * (64 / kCols)), dim3(kThreads), 0, st, a); break;
     case 128:
