@@ -35,8 +35,12 @@ struct Device;
  * installs fwd_block / fwd_block_batch (yllm.h:115-116); it fails with -1 and
  * a message for shapes the kernels do not take (head_dim not 64, 128 or 256;
  * more than 16 query heads per kv head; GDN head dim not 64 or 128), so the
- * caller can rebind the CPU device.  The GDN state is copied back to
- * e->ssm_state after every GPU update, so the host state is always current. */
+ * caller can rebind the CPU device.  The GDN state stays in HBM between
+ * calls: e->ssm_state is brought up to date when the host needs it -- before
+ * a GDN block runs on the CPU (fallback), in device_hip_kv_to_host and in
+ * free_dev -- not after every update (1 MiB per layer and token at the
+ * fifth configuration's shape).  After a GPU failure, a layer updated on the
+ * GPU since its last copy keeps its last host state when that copy fails. */
 struct Device* device_create_hip(int device_id, char* err, size_t errlen);
 
 /* KV-cache interface (device.h:58-63 cuda_after_prefill; cache.c:174-247).
@@ -46,8 +50,9 @@ struct Device* device_create_hip(int device_id, char* err, size_t errlen);
  * layout) and the head-major HBM cache.  Call device_hip_kv_from_host after
  * KV was written on the host (sess_kv_load); it also marks every HBM GDN
  * state stale, so each is re-sent from e->ssm_state by its layer's next
- * call.  device_hip_kv_to_host only rebuilds a host KV copy from HBM.
- * Return 0 or -1. */
+ * call.  device_hip_kv_to_host rebuilds a host KV copy from HBM and brings
+ * e->ssm_state up to date (call it before reading the host state, e.g. for
+ * a session save).  Return 0 or -1. */
 int device_hip_kv_from_host(struct Engine* e, uint32_t n_pos);
 int device_hip_kv_to_host(struct Engine* e, uint32_t n_pos);
 

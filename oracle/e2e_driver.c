@@ -14,17 +14,13 @@
  * Routing of decode blocks.  The reference engine sends a decode block to
  * e->fwd_block only in its accelerator modes (forward_layer, engine.c:1155-1158);
  * in DEV_MODE_CPU it calls engine_fwd_block_at directly (1159-1165).  The
- * integration adds one line that makes the CPU branch call e->fwd_block
- * (which is engine_fwd_block_at for the CPU device).  This unmodified build
- * gets the same routing by running each decode step with device_mode set
- * to DEV_MODE_VULKAN: in a build without Vulkan every Vulkan hook is the
- * CPU stub of device_cpu.c:175-202 (returns -1 or does nothing), so the step
- * is the CPU step except that blocks go through e->fwd_block.  The CPU run
- * takes the same route: for llama / qwen its fwd_block is the CPU block
- * (engine_fwd_block_at), and for qwen35 it is fwd_block_qwen35, which the
- * unpatched CPU branch never reaches (it calls the llama block).  Batched
- * prefill already goes through e->fwd_block_batch in DEV_MODE_CPU
- * (engine.c:652).
+ * integration changes that one line so the CPU branch calls e->fwd_block
+ * (INTEGRATION.md); this library is built with that change (oracle/Makefile,
+ * target e2e, rewrites engine.c:1164 on its way into the compiler), so
+ * decode steps here are plain engine_forward calls in DEV_MODE_CPU.  For the
+ * CPU device e->fwd_block is the engine's own block (engine_fwd_block_at for
+ * llama / qwen, fwd_block_qwen35 for qwen35); batched prefill goes through
+ * e->fwd_block_batch in DEV_MODE_CPU without any change (engine.c:652).
  */
 #include <stddef.h>
 #include <stdio.h>
@@ -161,10 +157,13 @@ static void header(LlfHeader* h, uint32_t arch, uint32_t blocks, uint32_t hidden
  * plus q/k/v biases for ARCH_QWEN, then the final norm and the f16 output
  * matrix.  Returns 0 or -1 with err set. */
 int ye_make_model(const char* path, uint32_t arch, uint32_t blocks, uint32_t hidden, uint32_t heads,
-                  uint32_t kv_heads, uint32_t vocab, uint32_t seq, uint32_t seed, char* err, size_t errlen)
+                  uint32_t kv_heads, uint32_t vocab, uint32_t seq, uint32_t seed, uint32_t ffn, char* err,
+                  size_t errlen)
 {
+    /* ffn: the FFN width, 0 for the usual 8/3 hidden (a narrow FFN keeps the
+     * CPU side of long-prompt runs short; the FFN is not on the path) */
     const uint32_t hd = hidden / heads, kv_dim = kv_heads * hd;
-    const uint32_t inter = ((hidden * 8 / 3 + 63) / 64) * 64;
+    const uint32_t inter = ffn ? ffn : ((hidden * 8 / 3 + 63) / 64) * 64;
     Items t;
     LlfHeader h;
     uint32_t b;
@@ -318,13 +317,7 @@ int ye_run(const char* path, int use_hip, int device_id, int fail_after, const u
     for (i = 0; i < n_decode; i++, pos++) {
         uint32_t tok = argmax(logits + (size_t)i * vocab, vocab);
         tokens[i] = tok;
-        {
-            /* both runs: see the file comment */
-            DeviceMode saved = e.device_mode;
-            e.device_mode = DEV_MODE_VULKAN;
-            engine_forward(&e, tok, pos);
-            e.device_mode = saved;
-        }
+        engine_forward(&e, tok, pos);
         memcpy(logits + (size_t)(i + 1) * vocab, e.logits, (size_t)vocab * 4);
     }
     if (use_hip && status[0] == 0 && fail_after < 0) {
@@ -364,13 +357,10 @@ int ye_run(const char* path, int use_hip, int device_id, int fail_after, const u
     return 0;
 }
 
-/* One greedy decode step through e->fwd_block (see the file comment). */
+/* One greedy decode step (through e->fwd_block, see the file comment). */
 static void decode_step(Engine* e, uint32_t tok, uint32_t pos)
 {
-    DeviceMode saved = e->device_mode;
-    e->device_mode = DEV_MODE_VULKAN;
     engine_forward(e, tok, pos);
-    e->device_mode = saved;
 }
 
 static int open_bound(Engine* e, const char* path, int use_hip, int device_id, int* bound, char* err,

@@ -34,7 +34,7 @@ def e2e():
         pytest.skip("oracle/_ref/libyref_e2e.so is not built (needs the reference sources: make -C oracle e2e)")
     lib = ctypes.CDLL(str(E2E_LIB))
     lib.ye_make_model.restype = c_int
-    lib.ye_make_model.argtypes = [c_char_p] + [c_uint32] * 8 + [c_char_p, c_size_t]
+    lib.ye_make_model.argtypes = [c_char_p] + [c_uint32] * 9 + [c_char_p, c_size_t]
     lib.ye_make_model_q35.restype = c_int
     lib.ye_make_model_q35.argtypes = [c_char_p] + [c_uint32] * 11 + [c_char_p, c_size_t]
     lib.ye_resume.restype = c_int
@@ -49,9 +49,10 @@ def e2e():
 ARCH_LLAMA, ARCH_QWEN = 0, 1  # llf.h:22-23
 
 
-def make_model(lib, path, blocks, hidden, heads, kv_heads, vocab=512, seq=256, seed=7, arch=ARCH_LLAMA):
+def make_model(lib, path, blocks, hidden, heads, kv_heads, vocab=512, seq=256, seed=7, arch=ARCH_LLAMA, ffn=0):
     err = ctypes.create_string_buffer(256)
-    rc = lib.ye_make_model(str(path).encode(), arch, blocks, hidden, heads, kv_heads, vocab, seq, seed, err, 256)
+    rc = lib.ye_make_model(str(path).encode(), arch, blocks, hidden, heads, kv_heads, vocab, seq, seed, ffn, err,
+                           256)
     assert rc == 0, err.value.decode()
     return path
 
@@ -198,6 +199,32 @@ def test_engine_end_to_end_matches_cpu(e2e, cuda, tmp_path, arch, hidden, heads,
     assert np.array_equal(gt, wt)
     # the HBM cache holds exactly the engine's KV rows
     assert status[1] == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hidden,heads,kv_heads,max_seq,n_prompt,n_dec", [
+    # the second configuration's head shape (28 / 4, head_dim 128) with a
+    # prompt of several of the engine's 64-token prefill chunks
+    (3584, 28, 4, 1024, 600, 6),
+    # a decode workspace sized for max_seq 4352 at 8 kv heads serves the
+    # shorter positions too (4352 keys split 17 ways, 2241 keys 18 ways);
+    # a short workspace would make the backend fall back to the CPU, and
+    # device_hip_kv_to_host at the end of the run would then fail
+    (2048, 16, 8, 4352, 2240, 4),
+])
+def test_engine_end_to_end_real_head_shapes(e2e, cuda, tmp_path, hidden, heads, kv_heads, max_seq, n_prompt, n_dec):
+    path = make_model(e2e, tmp_path / "m.llf", 1, hidden, heads, kv_heads, seq=max_seq, ffn=64)
+    prompt = prompt_of(n_prompt)
+    want, wt, _, _ = run(e2e, path, prompt, n_dec, use_hip=False)
+    got, gt, status, msg = run(e2e, path, prompt, n_dec, use_hip=True)
+    assert status[0] == 0, msg
+    errs = [rel_l2(got[i], want[i]) for i in range(n_dec + 1)]
+    print(f"e2e {heads}/{kv_heads} d={hidden // heads} prompt {n_prompt} max_seq {max_seq}: max rel_l2 "
+          f"{max(errs):.3e}, tokens {gt.tolist()}")
+    assert max(errs) <= TOL
+    assert np.array_equal(np.argmax(got, axis=1), np.argmax(want, axis=1))
+    assert np.array_equal(gt, wt)
+    assert status[1] == 0  # still bound at the end: the HBM cache equals the host KV
 
 
 @pytest.mark.gpu

@@ -107,13 +107,17 @@ typedef struct {
      * (gdn_index_of, engine.c:711-720: the slot of e->ssm_state / ssm_conv) */
     int32_t* gdn_slot;
     uint32_t* gdn_ord;
-    uint8_t* state_ok;  /* per state slot: the HBM state equals the host state */
+    /* per state slot, where the current GDN state is: STATE_HOST (e->ssm_state;
+     * HBM stale), STATE_BOTH, STATE_DEV (HBM; e->ssm_state stale until
+     * sync_state_to_host) */
+    uint8_t* state_loc;
     uint32_t n_gdn_slots, conv_chan, kwidth, n_v, n_k, hvd, value_dim;
     float* d_state;
     float* d_gb;        /* gate [cap][n_v], then beta [cap][n_v] */
     void* d_gws;        /* chunked-form workspace for cap tokens */
     size_t gws_bytes;
-    float* h_state;     /* one layer's state on its way back to host */
+    uint16_t* d_kvstage; /* engine-layout rows on their way to the host (kv_to_host) */
+    uint32_t kvstage_rows;
     float* h_conv;      /* one layer's conv delay line, kept to undo a failed block */
     /* staging for one call: q (or a GDN qkv row), k, v, gate, output */
     uint32_t cap, q_w, o_w;
@@ -136,6 +140,37 @@ typedef struct {
 static HipCtx* ctx_of(const Engine* e)
 {
     return e && e->dev ? (HipCtx*)e->dev->handle : NULL;
+}
+
+enum { STATE_HOST = 0, STATE_BOTH = 1, STATE_DEV = 2 };
+
+/* Make e->ssm_state of GDN layer `layer` current when HBM holds its state:
+ * one synchronous copy.  Returns 0, or -1 when the copy fails (after a GPU
+ * failure the layers updated on the GPU since their last copy keep a stale
+ * host state). */
+static int sync_state_to_host(Engine* e, HipCtx* c, uint32_t layer)
+{
+    const uint32_t li = layer - c->first;
+    const int32_t slot = c->gdn_slot[li];
+    const size_t state_n = (size_t)c->n_v * c->hvd * c->hvd;
+    if (slot < 0 || c->state_loc[slot] != STATE_DEV) return 0;
+    if (hipMemcpyAsync(e->ssm_state + (size_t)c->gdn_ord[li] * state_n, c->d_state + (size_t)slot * state_n,
+                       state_n * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        return -1;
+    c->state_loc[slot] = STATE_BOTH;
+    return 0;
+}
+
+static int sync_states_to_host(Engine* e, HipCtx* c)
+{
+    uint32_t l;
+    int rc = 0;
+    if (!c->state_loc || !c->gdn_slot) return 0;
+    if (c->stream && hipStreamSynchronize(c->stream) != hipSuccess) rc = -1;
+    for (l = c->first; l <= c->last; l++)
+        if (sync_state_to_host(e, c, l) != 0) rc = -1;
+    return rc;
 }
 
 static int say(char* err, size_t errlen, const char* what, const char* detail)
@@ -205,8 +240,8 @@ static void release(HipCtx* c)
     free(c->kv_slot);
     free(c->gdn_slot);
     free(c->gdn_ord);
-    free(c->state_ok);
-    free(c->h_state);
+    free(c->state_loc);
+    dfree(c->d_kvstage);
     free(c->h_conv);
     {
         int id = c->device_id;
@@ -438,26 +473,26 @@ static int q35_gdn(Engine* e, HipCtx* c, uint32_t layer, uint32_t B, const uint8
         for (ch = 0; ch < cc; ch++) row[ch] = row[ch] * sigmoidf_(row[ch]);
     }
 
-    ok = (c->state_ok[slot] ||
+    /* the state lives in HBM between calls: it is sent only when the host
+     * holds the current one (first call, after a CPU block or a restore) and
+     * comes back only when the host needs it (sync_state_to_host) */
+    ok = (c->state_loc[slot] != STATE_HOST ||
           hipMemcpyAsync(dS, host_S, state_n * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess) &&
          hipMemcpyAsync(c->d_q, qkv, (size_t)B * cc * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
          hipMemcpyAsync(c->d_gb, gate, (size_t)B * nv * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
          hipMemcpyAsync(c->d_gb + (size_t)B * nv, beta, (size_t)B * nv * 4, hipMemcpyHostToDevice, c->stream) ==
              hipSuccess;
-    c->state_ok[slot] = 0;
     ok = ok &&
          yhip_gdn_chunk(dS, c->d_out, vd, c->d_q, c->d_q + kd, cc, c->d_q + 2 * kd, cc, c->d_gb,
                         c->d_gb + (size_t)B * nv, B, c->n_k, nv, hvd, eps, c->d_gws, c->gws_bytes,
                         c->stream) == YHIP_OK &&
          hipMemcpyAsync(c->h_o, c->d_out, (size_t)B * vd * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
-         hipMemcpyAsync(c->h_state, dS, state_n * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
          hipStreamSynchronize(c->stream) == hipSuccess;
     if (!ok) {
         memcpy(conv_state, c->h_conv, (size_t)c->kwidth * cc * 4);
         return -1;
     }
-    memcpy(host_S, c->h_state, state_n * 4);
-    c->state_ok[slot] = 1;
+    c->state_loc[slot] = STATE_DEV;
 
     /* gated RMSNorm per v head (engine.c:840-850), then ssm_out */
     for (b = 0; b < B; b++)
@@ -565,8 +600,9 @@ static int q35_block(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32
     return 0;
 }
 
-/* fwd_block / fwd_block_batch for qwen35.  A CPU-computed GDN block leaves
- * the HBM state stale; it is re-sent before the layer's next GPU call. */
+/* fwd_block / fwd_block_batch for qwen35.  A GDN block computed on the CPU
+ * first takes the current state from HBM (when HBM holds it), and leaves the
+ * HBM state stale; it is re-sent before the layer's next GPU call. */
 static int q35_fwd(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_t B, int batch)
 {
     int turn = B > c->cap ? 0 : gpu_turn(c, layer, pos0 + B);
@@ -575,8 +611,10 @@ static int q35_fwd(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_t
         c->failed = 1;
         turn = -1;
     }
-    if (layer >= c->first && layer <= c->last && c->gdn_slot[layer - c->first] >= 0)
-        c->state_ok[c->gdn_slot[layer - c->first]] = 0;
+    if (layer >= c->first && layer <= c->last && c->gdn_slot[layer - c->first] >= 0) {
+        sync_state_to_host(e, c, layer);
+        c->state_loc[c->gdn_slot[layer - c->first]] = STATE_HOST;
+    }
     if (batch)
         c->cpu_fwd_batch(e, layer, pos0, B);
     else
@@ -826,10 +864,9 @@ static int hip_load_weights(Engine* e, char* err, size_t errlen)
     if (c->n_gdn_slots) {
         /* the HBM state is loaded from e->ssm_state by each layer's first call */
         state_bytes = (size_t)c->n_v * c->hvd * c->hvd * 4;
-        c->state_ok = (uint8_t*)calloc(c->n_gdn_slots, 1);
-        c->h_state = (float*)malloc(state_bytes);
+        c->state_loc = (uint8_t*)calloc(c->n_gdn_slots, 1); /* STATE_HOST */
         c->h_conv = (float*)malloc((size_t)c->kwidth * c->conv_chan * 4);
-        if (!c->state_ok || !c->h_state || !c->h_conv) return say(err, errlen, "out of host memory", NULL);
+        if (!c->state_loc || !c->h_conv) return say(err, errlen, "out of host memory", NULL);
         if (hip_ok(hipMalloc((void**)&c->d_state, state_bytes * c->n_gdn_slots), err, errlen, "GDN state allocation"))
             return -1;
     }
@@ -859,6 +896,8 @@ static void hip_free_dev(Engine* e)
     HipCtx* c = ctx_of(e);
     if (c) {
         if (c->stream) hipStreamSynchronize(c->stream);
+        /* the engine continues on the CPU with e->ssm_state */
+        sync_states_to_host(e, c);
         release(c);
     }
     if (e->fwd_block == hip_fwd_block) engine_attach_cpu_fwd(e);
@@ -912,25 +951,38 @@ static int move_kv(Engine* e, uint32_t n_pos, int to_host)
     uint32_t l;
     if (!c || !c->stream || c->failed) return -1;
     if (n_pos > c->max_seq) n_pos = c->max_seq;
-    if (!to_host && c->state_ok) memset(c->state_ok, 0, c->n_gdn_slots);
+    if (!to_host && c->state_loc) memset(c->state_loc, STATE_HOST, c->n_gdn_slots);
+    if (to_host && sync_states_to_host(e, c) != 0) return -1;
     for (l = c->first; l <= c->last && n_pos > 0; l++) {
         uint16_t* hk = e->kv + (size_t)l * e->max_seq * c->kv_dim;
         uint16_t* hv = e->kv + (size_t)(c->n_blocks + l) * e->max_seq * c->kv_dim;
         if (c->kv_slot[l - c->first] < 0) continue;
         if (to_host) {
-            uint16_t *dk, *dv;
-            size_t bytes = (size_t)n_pos * c->kv_dim * 2;
-            if (hipMalloc((void**)&dk, 2 * bytes) != hipSuccess) return -1;
-            dv = dk + (size_t)n_pos * c->kv_dim;
-            if (yhip_kv_to_engine(dk, dv, layer_k(c, l), layer_v(c, l), n_pos, c->n_kv, c->head_dim, c->kv_stride,
-                                  c->stream) != YHIP_OK ||
-                hipMemcpyAsync(hk, dk, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
-                hipMemcpyAsync(hv, dv, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
-                hipStreamSynchronize(c->stream) != hipSuccess) {
-                hipFree(dk);
-                return -1;
+            /* rows p0.. of the head-major cache, converted in pieces through one
+             * staging buffer (allocated at the first call and kept): the K rows
+             * of piece p0 start p0 rows into every head, its V tiles p0/32
+             * tiles in (p0 is a multiple of 64) */
+            uint32_t p0;
+            if (!c->d_kvstage) {
+                c->kvstage_rows = c->max_seq < 4096 ? (c->max_seq + 63) / 64 * 64 : 4096;
+                if (hipMalloc((void**)&c->d_kvstage, (size_t)c->kvstage_rows * c->kv_dim * 2 * 2) != hipSuccess) {
+                    c->d_kvstage = NULL;
+                    return -1;
+                }
             }
-            hipFree(dk);
+            for (p0 = 0; p0 < n_pos; p0 += c->kvstage_rows) {
+                const uint32_t n = n_pos - p0 < c->kvstage_rows ? n_pos - p0 : c->kvstage_rows;
+                const size_t bytes = (size_t)n * c->kv_dim * 2, off = (size_t)p0 * c->kv_dim;
+                uint16_t* dk = c->d_kvstage;
+                uint16_t* dv = dk + (size_t)c->kvstage_rows * c->kv_dim;
+                if (yhip_kv_to_engine(dk, dv, layer_k(c, l) + (size_t)p0 * c->head_dim,
+                                      layer_v(c, l) + (size_t)(p0 / 32) * c->head_dim * 32, n, c->n_kv, c->head_dim,
+                                      c->kv_stride, c->stream) != YHIP_OK ||
+                    hipMemcpyAsync(hk + off, dk, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+                    hipMemcpyAsync(hv + off, dv, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+                    hipStreamSynchronize(c->stream) != hipSuccess)
+                    return -1;
+            }
         } else {
             c->dev_len[c->kv_slot[l - c->first]] = 0;
             if (catch_up(c, e, l, n_pos) != 0) return -1;
