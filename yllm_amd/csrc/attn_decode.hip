@@ -74,9 +74,10 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     constexpr int kThreads = 64 * kWaves;
     constexpr int NC = D / 32;  // 32-wide d chunks of the QK contraction
     constexpr int NB = D / 16;  // 16-row d blocks of the PV output
-    __shared__ float s_o[kWaves][16][D + 4];
+    __shared__ __attribute__((aligned(16))) float s_o[kWaves][16][D + 4];
     __shared__ float s_m[kWaves][16];
     __shared__ float s_l[kWaves][16];
+    __shared__ float s_hm[16], s_hl[16];  // per head: max and sum over the waves
 
     const uint32_t seq = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
     // a length beyond the planned maximum is clamped, never read past
@@ -145,30 +146,56 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
                                         __builtin_amdgcn_raw_buffer_load_b128(rV, vb + b * 16 * kVTile * 2, 0, 0));
     };
 
-    // NBUF blocks of this wave in flight: the first ones are issued before q
-    // is read so the two latencies overlap.
+    // q is read once per workgroup: each thread loads float4s of the G heads'
+    // rows (issued before the first blocks, so waiting for q does not wait
+    // for K/V), splits them into f16 hi + lo parts and stages both in LDS
+    // (rows padded by 16 bytes against bank conflicts; zeros for the padded
+    // head slots).  The staging area is the one the wave combine uses after
+    // the key loop.
+    constexpr int D4 = D / 4;
+    constexpr int QROW = D + 8;                                 // halves per staged row
+    constexpr int QPT = (16 * D4 + kThreads - 1) / kThreads;   // float4s per thread
+    static_assert(sizeof(s_o) >= 2 * 16 * QROW * sizeof(_Float16), "q staging fits the combine area");
+    _Float16* s_q = reinterpret_cast<_Float16*>(&s_o[0][0][0]);  // [2][16][QROW]: hi, lo
+    f32x4 qv[QPT];
+    {
+        const float* qbase = a.q + (size_t)seq * a.q_stride + (size_t)h0 * D;
+#pragma unroll
+        for (int r = 0; r < QPT; ++r) {
+            const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4;
+            qv[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (idx < 16 * D4 && hn < G) qv[r] = *reinterpret_cast<const f32x4*>(qbase + (size_t)idx * 4);
+        }
+    }
+
+    // NBUF blocks of this wave in flight
     constexpr int NBUF = nbuf_of<D>();
     Frag<D> f[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF; ++i) load(f[i], wave + i * kWaves);
 
+#pragma unroll
+    for (int r = 0; r < QPT; ++r) {
+        const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
+        if (idx < 16 * D4) {
+            f16x4 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const _Float16 h = (_Float16)qv[r][e];
+                hi[e] = h;
+                lo[e] = (_Float16)(qv[r][e] - (float)h);
+            }
+            *reinterpret_cast<f16x4*>(s_q + hn * QROW + d) = hi;
+            *reinterpret_cast<f16x4*>(s_q + (16 + hn) * QROW + d) = lo;
+        }
+    }
+    lds_barrier();
     // B operand of the score MFMA: head slot n, dims c*32 + 8g .. +7
     f16x8 qhi[NC], qlo[NC];
-    {
-        const bool valid = (uint32_t)n < G;
-        const float* qrow = a.q + (size_t)seq * a.q_stride + (size_t)(h0 + (valid ? n : 0)) * D;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const f32x4 lo4 = *reinterpret_cast<const f32x4*>(qrow + c * 32 + g * 8);
-            const f32x4 hi4 = *reinterpret_cast<const f32x4*>(qrow + c * 32 + g * 8 + 4);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float x = valid ? (j < 4 ? lo4[j] : hi4[j - 4]) : 0.0f;
-                const _Float16 h = (_Float16)x;
-                qhi[c][j] = h;
-                qlo[c][j] = (_Float16)(x - (float)h);
-            }
-        }
+    for (int c = 0; c < NC; ++c) {
+        qhi[c] = *reinterpret_cast<const f16x8*>(s_q + n * QROW + c * 32 + g * 8);
+        qlo[c] = *reinterpret_cast<const f16x8*>(s_q + (16 + n) * QROW + c * 32 + g * 8);
     }
 
     auto compute = [&](Frag<D>& f, uint32_t key0) {
@@ -226,22 +253,25 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         for (int b = 0; b < NB; ++b) o[b] = mfma16(f.v[b], pf, o[b]);
     };
 
-    // ring of NBUF fragment sets: compute slot i, then refill it with the
-    // block NBUF*kWaves ahead
-    for (uint32_t base = 0;; base += NBUF) {
-        bool stop = false;
+    // Ring of NBUF fragment sets over this wave's blocks (wave, wave+W, ...):
+    // while a block NBUF ahead exists, compute slot i and refill it; the last
+    // NBUF blocks are computed without refills.  (Refills past the split are
+    // not free even though they read nothing: the buffer unit still takes
+    // each lane's 16 bytes through its pipeline, ~1.4 us for one d = 256
+    // block, which dominates a launch of one block per wave.)
+    const uint32_t nbw = nblk > (uint32_t)wave ? (nblk - wave + kWaves - 1) / kWaves : 0;
+    uint32_t j = 0;
+    for (; j + NBUF < nbw; j += NBUF) {
 #pragma unroll
         for (int i = 0; i < NBUF; ++i) {
-            const uint32_t b = wave + (base + i) * kWaves;
-            if (b >= nblk) {
-                stop = true;
-                break;
-            }
+            const uint32_t b = wave + (j + i) * kWaves;
             compute(f[i], kbeg + b * kKeysPerBlock);
             load(f[i], b + NBUF * kWaves);
         }
-        if (stop) break;
     }
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i)
+        if (j + i < nbw) compute(f[i], kbeg + (wave + (j + i) * kWaves) * kKeysPerBlock);
 
     // per-lane partial sums -> per head (the four lane groups hold one head)
     l += __shfl_xor(l, 16, 64);
@@ -250,68 +280,90 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         s_m[wave][n] = m;
         s_l[wave][n] = l;
     }
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s_o[wave][n][b * 16 + 4 * g + i] = o[b][i];
     __syncthreads();
 
-    // combine the four waves; a single split writes the result directly
-    const size_t grp = (size_t)seq * a.n_kv + kvh;  // (sequence, kv head) group
-    for (uint32_t idx = threadIdx.x; idx < G * D; idx += kThreads) {
-        const uint32_t hn = idx / D, d = idx - hn * D;
+    // Combine the four waves: every lane rescales its own accumulators to the
+    // head's maximum over the waves before staging them, so the sum below is
+    // four float4 reads per output float4.
+    {
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hn]);
-        float L = 0.0f, O = 0.0f;
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][n]);
+        const float sc = m == -INFINITY ? 0.0f : fast_exp2(m - M);
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float mw = s_m[w][hn];
-            if (mw != -INFINITY) {
-                const float sc = fast_exp2(mw - M);
-                L += s_l[w][hn] * sc;
-                O += s_o[w][hn][d] * sc;
-            }
+        for (int b = 0; b < NB; ++b)
+            *reinterpret_cast<f32x4*>(&s_o[wave][n][b * 16 + 4 * g]) = o[b] * sc;
+        if (wave == 0 && g == 0) {
+            float L = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w)
+                if (s_m[w][n] != -INFINITY) L += s_l[w][n] * fast_exp2(s_m[w][n] - M);
+            s_hm[n] = M;
+            s_hl[n] = L;
         }
+    }
+    __syncthreads();
+
+    // a single split writes the result directly, otherwise a partial
+    const size_t grp = (size_t)seq * a.n_kv + kvh;  // (sequence, kv head) group
+    for (uint32_t idx = threadIdx.x; idx < G * D4; idx += kThreads) {
+        const uint32_t hn = idx / D4, d = (idx - hn * D4) * 4;
+        f32x4 O = *reinterpret_cast<const f32x4*>(&s_o[0][hn][d]);
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) O += *reinterpret_cast<const f32x4*>(&s_o[w][hn][d]);
         if (a.n_splits == 1) {
             const uint32_t h = h0 + hn;
-            float r = O / L;
-            if (a.gate) r *= sigmoid_ref(a.gate[(size_t)seq * a.gate_stride + (size_t)h * D + d]);
-            a.out[(size_t)seq * a.out_stride + (size_t)h * D + d] = r;
+            f32x4 r = O / s_hl[hn];
+            if (a.gate) {
+                const float* gp = a.gate + (size_t)seq * a.gate_stride + (size_t)h * D + d;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) r[e] *= sigmoid_ref(gp[e]);
+            }
+            *reinterpret_cast<f32x4*>(a.out + (size_t)seq * a.out_stride + (size_t)h * D + d) = r;
         } else {
             const size_t slot = (grp * a.n_splits + split) * a.gmax + hn;
-            a.part_o[slot * D + d] = O;
+            *reinterpret_cast<f32x4*>(a.part_o + slot * D + d) = O;
             if (d == 0) {
-                a.part_ml[slot * 2] = M;
-                a.part_ml[slot * 2 + 1] = L;
+                a.part_ml[slot * 2] = s_hm[hn];
+                a.part_ml[slot * 2 + 1] = s_hl[hn];
             }
         }
     }
 }
 
-// One workgroup per (query head, sequence).  Thread t owns 4 output
-// dimensions and a strided subset of the splits; it loads the subset's
-// (max, sum) pairs and partial outputs together (one memory round trip),
-// combines them against its own running max, and the subsets are then
-// combined in LDS with one more rescale.
+// One workgroup per (query head, 64-dimension slice, sequence): 16 float4
+// columns x 16 split subsets.  Thread t owns 4 output dimensions and the
+// splits sg, sg+16, ...; it loads their (max, sum) pairs and partial outputs
+// together (one memory round trip for up to 16 * kRound splits), combines
+// them against its own running max, and the 16 subsets are then combined in
+// LDS with one more rescale.  The gate is loaded first, beside the partials.
+constexpr uint32_t kMergeSlice = 64;
+
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
 {
-    constexpr uint32_t E4 = D / 4;       // float4 columns of one head
-    constexpr uint32_t NG = 256 / E4;    // split subsets combined in parallel
+    constexpr uint32_t SL = D < kMergeSlice ? D : kMergeSlice;  // dimensions per workgroup
+    constexpr uint32_t E4 = SL / 4;     // float4 columns of the slice
+    constexpr uint32_t NG = 256 / E4;   // split subsets combined in parallel
+    constexpr uint32_t NS = D / SL;     // slices per head
     __shared__ f32x4 s_o[256];
     __shared__ float s_m[256], s_l[256];
-    const uint32_t h = blockIdx.x, seq = blockIdx.y, t = threadIdx.x;
+    const uint32_t h = blockIdx.x / NS, d0 = (blockIdx.x % NS) * SL, seq = blockIdx.y, t = threadIdx.x;
     const uint32_t kvh = h * a.n_kv / a.n_heads;
     const uint32_t hn = h - (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
     const uint32_t len = min(min(a.lens ? a.lens[seq] : a.len0, a.kv_stride), a.split_keys * a.n_splits);
     const uint32_t ns = (len + a.split_keys - 1) / a.split_keys;
     const size_t sbase = ((size_t)seq * a.n_kv + kvh) * a.n_splits;
     const uint32_t e4 = t % E4, sg = t / E4;
+    const uint32_t d = d0 + 4 * e4;
 
-    // A thread combines the splits sg, sg+NG, ...: all loads of a round of
-    // up to kRound splits are issued before any of them is used, so the
-    // merge costs one memory round trip per round instead of one per split.
+    f32x4 gt = f32x4{1.f, 1.f, 1.f, 1.f};
+    if (a.gate && sg == 0) {  // gate rows need not be 16-byte aligned
+        const float* gp = a.gate + (size_t)seq * a.gate_stride + (size_t)h * D + d;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gt[e] = gp[e];
+    }
+
     constexpr uint32_t kRound = 8;
     float M = -INFINITY, L = 0.0f;
     f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -325,7 +377,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
                 const size_t slot = (sbase + s) * a.gmax + hn;
                 ms[r] = a.part_ml[slot * 2];
                 ls[r] = a.part_ml[slot * 2 + 1];
-                os[r] = *reinterpret_cast<const f32x4*>(a.part_o + slot * D + 4 * e4);
+                os[r] = *reinterpret_cast<const f32x4*>(a.part_o + slot * D + d);
             } else {
                 ms[r] = -INFINITY;
                 ls[r] = 0.0f;
@@ -368,11 +420,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
             }
         }
         f32x4 r = ns ? Ot / Lt : f32x4{0.f, 0.f, 0.f, 0.f};
-        const uint32_t d = 4 * t;
         if (a.gate) {
-            const float* gp = a.gate + (size_t)seq * a.gate_stride + (size_t)h * D + d;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) r[e] *= sigmoid_ref(gp[e]);
+            for (int e = 0; e < 4; ++e) r[e] *= sigmoid_ref(gt[e]);
         }
         *reinterpret_cast<f32x4*>(a.out + (size_t)seq * a.out_stride + (size_t)h * D + d) = r;
     }
@@ -383,7 +433,9 @@ hipError_t launch_decode_d(const DecodeArgs& a, hipStream_t st)
 {
     dim3 grid(a.n_splits, a.n_kv, a.n_seq);
     hipLaunchKernelGGL(decode_split_kernel<D>, grid, dim3(64 * waves_of<D>()), 0, st, a);
-    if (a.n_splits > 1) hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.n_heads, a.n_seq), dim3(256), 0, st, a);
+    constexpr uint32_t slices = D < kMergeSlice ? 1 : D / kMergeSlice;
+    if (a.n_splits > 1)
+        hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.n_heads * slices, a.n_seq), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
