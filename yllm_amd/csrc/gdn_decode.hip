@@ -107,6 +107,10 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(GdnDecodeArgs a)
     Chan cv;
     const bool v_thread = tid < kCols;
     if (v_thread) load(cv, 2 * key_dim + h * D + blk * kCols + tid);
+    // gates (engine.c:788-793), read with the other loads: after a barrier
+    // their loads would add a memory round trip to the token's chain
+    const float bt = 1.0f / (1.0f + expf(-a.beta_raw[h]));
+    const float g = expf(log1pf(expf(a.alpha[h] + a.dt_bias[h])) * a.ssm_a[h]);
 
     // 2. conv + silu; the new delay line row r is X[r]
 #pragma unroll
@@ -136,9 +140,6 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(GdnDecodeArgs a)
     }
     __syncthreads();
     const float rq = red[0], rk = red[1];
-    // gates (engine.c:788-793)
-    const float bt = 1.0f / (1.0f + expf(-a.beta_raw[h]));
-    const float g = expf(log1pf(expf(a.alpha[h] + a.dt_bias[h])) * a.ssm_a[h]);
 
     // 3. state update of column j (matvec.c:975-1004, as gdn_step_kernel)
     float k[SL], q[SL];
@@ -194,7 +195,7 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     constexpr int SL = D / TPC;   // state elements per thread
     static_assert(3 * D <= NT, "one conv channel per thread");
     __shared__ float qs[D], ks[D], vs[D];
-    __shared__ float red[2];
+    __shared__ float l2p[2 * D / 64];  // per wave: sum of squares of its q or k channels
     __shared__ float ssq[NT / 64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -228,6 +229,11 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     const float wv = part == 0 ? (a.norm_w_f16 ? (float)reinterpret_cast<const _Float16*>(a.norm_w)[j]
                                                : reinterpret_cast<const float*>(a.norm_w)[j])
                                : 0.0f;
+    // gates (engine.c:788-793), read with the other loads: after a barrier
+    // their loads would add a memory round trip to the token's chain
+    const float bt = 1.0f / (1.0f + expf(-a.beta_raw[h]));
+    const float g = expf(log1pf(expf(a.alpha[h] + a.dt_bias[h])) * a.ssm_a[h]);
+    float y = 0.0f;
     if (has_ch) {
         float acc = 0.0f;
 #pragma unroll
@@ -235,7 +241,7 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
             if (r >= (int)a.kwidth) break;
             acc = acc + X[r] * w[r];
         }
-        const float y = acc / (1.0f + expf(-acc));
+        y = acc / (1.0f + expf(-acc));
         if (tid < D) qs[tid] = y;
         else if (tid < 2 * D) ks[tid - D] = y;
         else vs[tid - 2 * D] = y;
@@ -249,19 +255,21 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
             }
         }
     }
-    __syncthreads();
-    if (wave < 2) {
-        const float* src = wave == 0 ? qs : ks;
-        float ss = 0.0f;
-        for (int i = lane; i < D; i += 64) ss += src[i] * src[i];
+    // l2 norms: the q channels are waves 0 .. D/64-1, the k channels the next
+    // D/64 waves; each wave sums its squares, one barrier publishes them
+    // (the reference sums in order; this is a tree, equal to rounding)
+    float y2 = tid < 2 * D ? y * y : 0.0f;
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-        if (lane == 0) red[wave] = 1.0f / fmaxf(sqrtf(ss), a.l2_eps);
-    }
+    for (int m = 32; m >= 1; m >>= 1) y2 += __shfl_xor(y2, m, 64);
+    if (lane == 0 && wave < 2 * D / 64) l2p[wave] = y2;
     __syncthreads();
-    const float rq = red[0], rk = red[1];
-    const float bt = 1.0f / (1.0f + expf(-a.beta_raw[h]));
-    const float g = expf(log1pf(expf(a.alpha[h] + a.dt_bias[h])) * a.ssm_a[h]);
+    float qq = 0.0f, kk = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < D / 64; ++w2) {
+        qq += l2p[w2];
+        kk += l2p[D / 64 + w2];
+    }
+    const float rq = 1.0f / fmaxf(sqrtf(qq), a.l2_eps), rk = 1.0f / fmaxf(sqrtf(kk), a.l2_eps);
 
     float k[SL], q[SL];
 #pragma unroll
