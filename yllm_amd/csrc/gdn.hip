@@ -14,8 +14,8 @@
 //
 // Three kernels.  A single token (a decode step) runs gdn_step_kernel; the
 // token-by-token kernel (gdn_kernel) serves short sequences and callers
-// without a workspace; the chunked form below (gdn_prep_kernel +
-// gdn_scan_kernel) serves prefill.
+// without a workspace; the chunked form below (gdn_prep_kernel,
+// gdn_chain_kernel, gdn_out_kernel) serves prefill.
 //
 // Token by token.  A workgroup (4 waves) owns 64 columns of one head for the
 // whole sequence; lane l holds column j0+l and wave w the d_k slice
@@ -219,11 +219,13 @@ __global__ __launch_bounds__(256, 1) void gdn_kernel(GdnArgs a)
 //     M_last  = gamma_last M0 + Delta^T diag(e) K
 // (rows of Delta, V, K, Q, O are tokens).  With T = (I + A)^-1, U = T
 // diag(beta) V and W = T diag(beta*gamma) K, Delta = U - W M0^T.
-// gdn_prep_kernel computes, for every (v-head, chunk) at once, W, Q~ =
-// diag(gamma) Q, K~ = diag(e) K, P, U and gamma_last; gdn_scan_kernel then
-// walks the chunks in order with the state slice of 16 rows in LDS:
-// R = W M^T and Q~ M^T (one MFMA pass over [W; Q~]), Delta = U - R,
-// O = Q~ M^T + P Delta, M <- gamma_last M + Delta^T K~.  All products are
+// Three launches: gdn_prep_kernel computes, for every (v-head, chunk) at
+// once, W, Q~ = diag(gamma) Q, K~ = diag(e) K, P, U and gamma_last;
+// gdn_chain_kernel walks the chunks in order, state only (Delta = U - W M^T,
+// M <- gamma_last M + Delta^T K~), recording each chunk's starting state and
+// Delta; gdn_out_kernel then forms O = Q~ Mc^T + P Delta for every chunk at
+// once.  Only the chain is sequential, and it carries 256 of the 448 MFMAs
+// per chunk and slice that a single walking kernel did.  All products are
 // fp32 MFMA (v_mfma_f32_16x16x4_f32) with fp32 accumulation.
 constexpr int kC = 64;  // tokens per chunk of the chunked form
 
@@ -234,13 +236,17 @@ __device__ inline f32x4 mfma_f32(float a, float b, const f32x4& c)
 
 template <int D>
 struct ChunkWs {
-    // per (v-head, chunk): [W; Q~] [2kC][D], K~ [kC][D], P [kC][kC], U [kC][D], gamma_last (+3 pad)
-    static constexpr size_t floats = (size_t)2 * kC * D + (size_t)kC * D + (size_t)kC * kC + (size_t)kC * D + 4;
+    // per (v-head, chunk): [W; Q~] [2kC][D] (token rows), K~^T [D][kC], P [kC][kC],
+    // U^T [D][kC] (the chain kernel overwrites it with Delta^T), gamma_last (+3 pad),
+    // Mc [D][D] (the state at the chunk's start, rows j)
+    static constexpr size_t floats =
+        (size_t)2 * kC * D + (size_t)kC * D + (size_t)kC * kC + (size_t)kC * D + 4 + (size_t)D * D;
     float* WQ;
     float* Kt;
     float* P;
     float* U;
     float* gl;
+    float* Mc;
     __device__ ChunkWs(float* ws, uint32_t h, uint32_t c, uint32_t n_chunks)
     {
         WQ = ws + ((size_t)h * n_chunks + c) * floats;
@@ -248,6 +254,7 @@ struct ChunkWs {
         P = Kt + kC * D;
         U = P + kC * kC;
         gl = U + kC * D;
+        Mc = gl + 4;
     }
 };
 
@@ -329,13 +336,18 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
         __syncthreads();
     }
 
-    // Q~ = diag(gamma) Q (rows kC..2kC-1 of [W; Q~]) and K~ = diag(e) K
+    // Q~ = diag(gamma) Q (rows kC..2kC-1 of [W; Q~]) and K~^T = (diag(e) K)^T
+    // (d_k rows of kC tokens: the chain kernel's operand loads are then 16
+    // contiguous bytes per lane)
     for (int e = tid; e < kC * D / 4; e += 256) {
         const int t = e / (D / 4), i = (e % (D / 4)) * 4;
         const f32x4 q = *reinterpret_cast<const f32x4*>(&Qn[t][i]);
-        const f32x4 k = *reinterpret_cast<const f32x4*>(&Kn[t][i]);
         *reinterpret_cast<f32x4*>(w.WQ + (size_t)(kC + t) * D + i) = q * sgam[t];
-        *reinterpret_cast<f32x4*>(w.Kt + (size_t)t * D + i) = k * see[t];
+        const int ik = e / (kC / 4), t4 = (e % (kC / 4)) * 4;
+        f32x4 kt;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) kt[u] = Kn[t4 + u][ik] * see[t4 + u];
+        *reinterpret_cast<f32x4*>(w.Kt + (size_t)ik * kC + t4) = kt;
     }
 
     // Gram matrices K K^T and Q K^T; wave w owns token rows 16w..16w+15.
@@ -416,144 +428,277 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
 #pragma unroll
             for (int s4 = 0; s4 < kC / 4; ++s4) cur[s4] = nxt[s4];
         }
-        float* dst = col < D ? w.U + col : w.WQ + (col - D);
+        if (col < D) {
+            // U^T row col: kC contiguous floats
 #pragma unroll
-        for (int t = 0; t < kC; ++t) dst[(size_t)t * D] = X[t];
+            for (int t = 0; t < kC; t += 4)
+                *reinterpret_cast<f32x4*>(w.U + (size_t)col * kC + t) = f32x4{X[t], X[t + 1], X[t + 2], X[t + 3]};
+        } else {
+#pragma unroll
+            for (int t = 0; t < kC; ++t) w.WQ[(size_t)t * D + (col - D)] = X[t];
+        }
     }
 }
 
+// The recurrence across chunks, state only: per chunk, Delta = U - W M^T
+// and M <- gamma_last M + Delta^T K~ (the output is formed afterwards, all
+// chunks at once, by gdn_out_kernel).  A workgroup owns J = 16 state rows
+// (d_v indices j0..j0+15) of one head in LDS and walks the chunks in order;
+// it records each chunk's starting state (Mc) and Delta^T (in place of U^T)
+// for the output pass.
+//
+// Waves 0-3 compute, waves 4-7 stage every operand through LDS (the compute
+// waves issue no loads in the chunk loop): at the start of chunk c the
+// stagers write chunk c+1's W rows, K~^T rows, U^T slice and gamma_last
+// (~68 KB at d = 128, loaded into their registers during chunk c-1) into the
+// LDS buffer of parity c+1, record the chunk's starting state and issue half
+// of chunk c+2's loads, the other half after the first barrier.  Every
+// workgroup of a head needs the head's whole W and K~ for its 16 columns, so
+// a CU moves ~68 KB per chunk whatever the slice width, and a CU's memory
+// pipeline (~30-45 GB/s measured for such loads) rather than the MFMA sets
+// the pace: ~2.4 us per chunk.  (With every wave loading its own register
+// operands at the start of a chunk, phase A waited ~1.4 us for the loads to
+// issue: 3.2 us per chunk.)
+// Per chunk: phase A, compute wave w (row block w of W, d_k split over the
+// four lane groups) forms Delta rows 16w..16w+15; phase B, compute wave w
+// updates d_k blocks w, w+4 of the slice.  The barriers order LDS only (the
+// stagers' loads stay in flight across them).
 template <int D>
-__global__ __launch_bounds__(512) void gdn_scan_kernel(GdnArgs a)
+__global__ __launch_bounds__(512) void gdn_chain_kernel(GdnArgs a)
 {
     constexpr int J = 16;       // state rows (d_v indices) per workgroup
-    constexpr int KQ = D / 4;   // d_k indices per lane group in the [W; Q~] M^T pass
-    constexpr int NCB = D / 16; // 16-wide d_k blocks of the state update (<= 8 waves)
-    constexpr int MP = D + 4;
+    constexpr int KQ = D / 4;   // d_k indices per lane group in phase A
+    constexpr int NCB = D / 16; // 16-wide d_k blocks of phase B
+    constexpr int MP = D + 4, WP = D + 4, KP = kC + 4;
+    constexpr int NW4 = kC * D / 4 / 256;  // float4s of W (and of K~^T) per stager thread
+    static_assert(J * kC / 4 <= 256, "one U^T float4 per stager thread");
     __shared__ float Ml[J][MP];
-    __shared__ float Ol[kC][J + 1], Dl[kC][J + 1];
+    __shared__ float Dl[kC][J + 1];
+    __shared__ float Wl[2][kC][WP];
+    __shared__ float Kl[2][D][KP];
+    __shared__ float Ul[2][J][KP];
+    __shared__ float Gl[2];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;  // 8 waves
     const int r = lane & 15, g = lane >> 4;
+    const bool stager = wave >= 4;
+    const int st = tid - 256;  // stager thread index
     // workgroup b = slice * n_v + h: consecutive workgroups go to different
     // XCDs, so the slices of one head (b mod 8 fixed when n_v is a multiple
     // of 8) share an L2 and read the head's chunk data once
     const uint32_t h = blockIdx.x % a.n_v, j0 = (blockIdx.x / a.n_v) * J;
-    const float scale = 1.0f / sqrtf((float)D);
     float* S = a.S + ((size_t)h * D + j0) * D;
+    const uint32_t nlast = a.n_chunks - 1;
 
-    for (int e = tid; e < J * D / 4; e += 512) {
-        const int j = e / (D / 4), i = (e % (D / 4)) * 4;
-        *reinterpret_cast<f32x4*>(&Ml[j][i]) = *reinterpret_cast<const f32x4*>(S + (size_t)j * D + i);
-    }
-
-    // operands of one chunk held in registers; the next chunk's are loaded
-    // while the current one is computed.  Wave w: row block w of [W; Q~]
-    // (phase 1), row block w of P and of U (waves 0-3), d_k block w of K~
-    // (phase 3, waves < NCB).
-    struct Ops {
-        f32x4 wq[KQ / 4];
-        f32x4 p[4];
-        float kt[16];
-        float u[4];
+    struct Stage {
+        f32x4 w[NW4], k[NW4];  // a stager's share of one chunk's W and K~^T
+        f32x4 u;               // ... of its U^T slice
         float gl;
     };
-    auto load_ops = [&](Ops& o, uint32_t c) {
+    // the first half of a chunk's loads (W rows, U^T slice, gamma_last), then the second (K~^T rows)
+    auto stage_load0 = [&](Stage& sg, uint32_t c) {
         ChunkWs<D> w(a.ws, h, c, a.n_chunks);
-        const float* arow = w.WQ + (size_t)(16 * wave + r) * D + g * KQ;
 #pragma unroll
-        for (int i = 0; i < KQ / 4; ++i) o.wq[i] = *reinterpret_cast<const f32x4*>(arow + 4 * i);
-        if (wave < 4) {
-            const float* prow = w.P + (size_t)(16 * wave + r) * kC + 16 * g;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o.p[i] = *reinterpret_cast<const f32x4*>(prow + 4 * i);
-        }
-        if (wave < NCB) {
-#pragma unroll
-            for (int kb = 0; kb < 16; ++kb) o.kt[kb] = w.Kt[(size_t)(16 * g + kb) * D + 16 * wave + r];
-        }
-        if (wave < 4) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o.u[i] = w.U[(size_t)(16 * wave + 4 * g + i) * D + j0 + r];
-        }
-        o.gl = w.gl[0];
+        for (int u = 0; u < NW4; ++u)
+            sg.w[u] = *reinterpret_cast<const f32x4*>(w.WQ + (size_t)(st + 256 * u) * 4);  // kC x D
+        const int ju = st / (kC / 4), tu = (st % (kC / 4)) * 4;
+        if (st < J * kC / 4) sg.u = *reinterpret_cast<const f32x4*>(w.U + (size_t)(j0 + ju) * kC + tu);
+        sg.gl = w.gl[0];
     };
-    Ops cur, nxt;
-    load_ops(cur, 0);
-    // The first chunk's operands are complete before the loop.  Otherwise the
+    auto stage_load1 = [&](Stage& sg, uint32_t c) {
+        ChunkWs<D> w(a.ws, h, c, a.n_chunks);
+#pragma unroll
+        for (int u = 0; u < NW4; ++u)
+            sg.k[u] = *reinterpret_cast<const f32x4*>(w.Kt + (size_t)(st + 256 * u) * 4);  // D x kC
+    };
+    auto stage_store = [&](const Stage& sg, int p) {
+#pragma unroll
+        for (int u = 0; u < NW4; ++u) {
+            const int e = st + 256 * u;
+            const int tw = e / (D / 4), iw = (e % (D / 4)) * 4;
+            *reinterpret_cast<f32x4*>(&Wl[p][tw][iw]) = sg.w[u];
+            const int ik = e / (kC / 4), tk = (e % (kC / 4)) * 4;
+            *reinterpret_cast<f32x4*>(&Kl[p][ik][tk]) = sg.k[u];
+        }
+        const int ju = st / (kC / 4), tu = (st % (kC / 4)) * 4;
+        if (st < J * kC / 4) *reinterpret_cast<f32x4*>(&Ul[p][ju][tu]) = sg.u;
+        if (st == 0) Gl[p] = sg.gl;
+    };
+
+    for (int e = tid; e < J * D / 4; e += 512) {
+        const int jj = e / (D / 4), i = (e % (D / 4)) * 4;
+        *reinterpret_cast<f32x4*>(&Ml[jj][i]) = *reinterpret_cast<const f32x4*>(S + (size_t)jj * D + i);
+    }
+    Stage sa, sb;  // a stager's register sets of even and odd chunks
+    if (stager) {
+        stage_load0(sa, 0);
+        stage_load1(sa, 0);
+        stage_store(sa, 0);
+        stage_load0(sb, min(1u, nlast));
+        stage_load1(sb, min(1u, nlast));
+    }
+    // everything of chunks 0 and 1 is complete before the loop (otherwise the
     // compiler's wait insertion, merging the loop entry with the back edge,
-    // puts a wait for them into phase 1 of every iteration, where it also
-    // waits for the next chunk's operands issued just before (one memory
-    // latency per chunk).
+    // waits inside the loop for loads issued just before)
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
 
-    for (uint32_t c = 0; c < a.n_chunks; ++c) {
-        const uint32_t t0 = c * kC;
-        const int nt = (int)min((uint32_t)kC, a.T - t0);
-        if (c + 1 < a.n_chunks) load_ops(nxt, c + 1);
-
-        // phase 1: row block `wave` of [W; Q~] times M^T (lane (g, r) supplies
-        // M[j0 + r][g*KQ .. g*KQ+KQ-1] as the B operand); waves 0-3 hold rows
-        // of W M^T and form Delta = U - W M^T directly, waves 4-7 rows of Q~ M^T
-        {
+    // one chunk; `next` holds chunk c+1's operands, `fill` receives chunk c+2's
+    auto chunk = [&](uint32_t c, int p, const Stage& next, Stage& fill) {
+        ChunkWs<D> w(a.ws, h, c, a.n_chunks);
+        if (stager) {
+            stage_store(next, p ^ 1);
+            // the chunk's starting state, for the output pass (before phase B rewrites Ml)
+            for (int e = st; e < J * D / 4; e += 256) {
+                const int jj = e / (D / 4), i = (e % (D / 4)) * 4;
+                *reinterpret_cast<f32x4*>(w.Mc + (size_t)(j0 + jj) * D + i) =
+                    *reinterpret_cast<const f32x4*>(&Ml[jj][i]);
+            }
+            stage_load0(fill, min(c + 2, nlast));
+        } else {
+            // phase A: Delta rows 16w..16w+15 = U - W M^T (lane (g, r) supplies
+            // M[j0 + r][g*KQ .. g*KQ+KQ-1] as the B operand)
             f32x4 acc[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < KQ / 4; ++i) {
+                const f32x4 wa = *reinterpret_cast<const f32x4*>(&Wl[p][16 * wave + r][g * KQ + 4 * i]);
                 const f32x4 mb = *reinterpret_cast<const f32x4*>(&Ml[r][g * KQ + 4 * i]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[e] = mfma_f32(cur.wq[i][e], mb[e], acc[e]);
+                for (int e = 0; e < 4; ++e) acc[e] = mfma_f32(wa[e], mb[e], acc[e]);
             }
             const f32x4 x = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            const f32x4 u = *reinterpret_cast<const f32x4*>(&Ul[p][r][16 * wave + 4 * g]);
+            const f32x4 dl = u - x;  // Delta[16 wave + 4g + i][j0 + r]
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = 16 * wave + 4 * g + i;
-                if (wave < 4)
-                    Dl[row][r] = cur.u[i] - x[i];
-                else
-                    Ol[row - kC][r] = x[i];
+            for (int i = 0; i < 4; ++i) Dl[16 * wave + 4 * g + i][r] = dl[i];
+            *reinterpret_cast<f32x4*>(w.U + (size_t)(j0 + r) * kC + 16 * wave + 4 * g) = dl;
+        }
+        lds_barrier();
+        if (stager) {
+            stage_load1(fill, min(c + 2, nlast));
+        } else {
+            // phase B: M <- gamma_last M + Delta^T K~ for d_k blocks wave, wave+4, ...;
+            // a wave reads and writes only its own columns of Ml
+            const float gl = Gl[p];
+            constexpr int NB = NCB / 4;
+            f32x4 acc[NB][2];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int cb = wave + 4 * b;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[b][0][i] = gl * Ml[4 * g + i][16 * cb + r];
+                acc[b][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int k4 = 0; k4 < 4; ++k4) {
+                f32x4 kb4[NB];
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    kb4[b] = *reinterpret_cast<const f32x4*>(&Kl[p][16 * (wave + 4 * b) + r][16 * g + 4 * k4]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float da = Dl[16 * g + 4 * k4 + e][r];
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) acc[b][e & 1] = mfma_f32(da, kb4[b][e], acc[b][e & 1]);
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const f32x4 nm = acc[b][0] + acc[b][1];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Ml[4 * g + i][16 * (wave + 4 * b) + r] = nm[i];
             }
         }
-        __syncthreads();
-        // phase 2 (waves 0-3): O = Q~ M^T + P Delta for token rows 16w..16w+15
-        if (wave < 4) {
-            f32x4 acc[2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[0][i] = Ol[16 * wave + 4 * g + i][r];
-            acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc[e & 1] = mfma_f32(cur.p[i][e], Dl[16 * g + 4 * i + e][r], acc[e & 1]);
-            const f32x4 o = acc[0] + acc[1];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * wave + 4 * g + i;
-                if (t < nt) a.out[(size_t)(t0 + t) * a.out_stride + (size_t)h * D + j0 + r] = o[i] * scale;
-            }
-        }
-        // phase 3: M <- gamma_last M + Delta^T K~ for d_k block `wave`; a wave
-        // reads and writes only its own columns of Ml
-        if (wave < NCB) {
-            f32x4 acc[2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[0][i] = cur.gl * Ml[4 * g + i][16 * wave + r];
-            acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kb = 0; kb < 16; ++kb) acc[kb & 1] = mfma_f32(Dl[16 * g + kb][r], cur.kt[kb], acc[kb & 1]);
-            const f32x4 nm = acc[0] + acc[1];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) Ml[4 * g + i][16 * wave + r] = nm[i];
-        }
-        __syncthreads();
-        if (c + 1 < a.n_chunks) cur = nxt;
+        lds_barrier();
+    };
+    for (uint32_t c = 0;; c += 2) {
+        chunk(c, 0, sb, sa);
+        if (c + 1 > nlast) break;
+        chunk(c + 1, 1, sa, sb);
+        if (c + 2 > nlast) break;
     }
 
     for (int e = tid; e < J * D / 4; e += 512) {
-        const int j = e / (D / 4), i = (e % (D / 4)) * 4;
-        *reinterpret_cast<f32x4*>(S + (size_t)j * D + i) = *reinterpret_cast<const f32x4*>(&Ml[j][i]);
+        const int jj = e / (D / 4), i = (e % (D / 4)) * 4;
+        *reinterpret_cast<f32x4*>(S + (size_t)jj * D + i) = *reinterpret_cast<const f32x4*>(&Ml[jj][i]);
+    }
+}
+
+// The chunk outputs, all chunks at once: O = (Q~ Mc^T + P Delta) / sqrt(d)
+// for one (chunk, v head) per workgroup.  Q~ and P are staged in LDS; wave w
+// owns output columns (d_v) 16*(w % NJT).. and token row blocks of its
+// share, with its Mc rows and Delta^T rows as register operands (16-byte
+// loads).  fp32 MFMA, fp32 accumulation.
+template <int D>
+__global__ __launch_bounds__(512, 2) void gdn_out_kernel(GdnArgs a)
+{
+    constexpr int KQ = D / 4;      // d_k indices per lane group
+    constexpr int NJT = D / 16;    // 16-column output tiles
+    constexpr int WPT = 8 / NJT;   // waves per column tile (1 at D = 128, 2 at 64)
+    constexpr int RBW = 4 / WPT;   // 16-token row blocks per wave
+    constexpr int QP = D + 4, PP = kC + 4;
+    __shared__ float Ql[kC][QP];
+    __shared__ float Pl[kC][PP];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const uint32_t c = blockIdx.x, h = blockIdx.y;
+    const uint32_t t0 = c * kC;
+    const int nt = (int)min((uint32_t)kC, a.T - t0);
+    const int jt = wave % NJT, rb0 = (wave / NJT) * RBW;
+    ChunkWs<D> w(a.ws, h, c, a.n_chunks);
+
+    // register operands: Mc rows 16 jt + r (d_k range of lane group g) and
+    // Delta^T rows 16 jt + r (tokens 16g .. 16g+15); issued first
+    f32x4 mb[KQ / 4], db[4];
+    {
+        const float* mrow = w.Mc + (size_t)(16 * jt + r) * D + g * KQ;
+#pragma unroll
+        for (int i = 0; i < KQ / 4; ++i) mb[i] = *reinterpret_cast<const f32x4*>(mrow + 4 * i);
+        const float* drow = w.U + (size_t)(16 * jt + r) * kC + 16 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) db[i] = *reinterpret_cast<const f32x4*>(drow + 4 * i);
+    }
+    // Q~ (rows kC..2kC-1 of [W; Q~]) and P into LDS
+    for (int e = tid; e < kC * D / 4; e += 512) {
+        const int t = e / (D / 4), i = (e % (D / 4)) * 4;
+        *reinterpret_cast<f32x4*>(&Ql[t][i]) = *reinterpret_cast<const f32x4*>(w.WQ + (size_t)(kC + t) * D + i);
+    }
+    for (int e = tid; e < kC * kC / 4; e += 512) {
+        const int t = e / (kC / 4), i = (e % (kC / 4)) * 4;
+        *reinterpret_cast<f32x4*>(&Pl[t][i]) = *reinterpret_cast<const f32x4*>(w.P + (size_t)t * kC + i);
+    }
+    __syncthreads();
+
+    const float scale = 1.0f / sqrtf((float)D);
+#pragma unroll
+    for (int rr = 0; rr < RBW; ++rr) {
+        const int rb = rb0 + rr;
+        f32x4 acc[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // Q~ Mc^T: contraction over d_k, lane group g its KQ indices
+#pragma unroll
+        for (int i = 0; i < KQ / 4; ++i) {
+            const f32x4 qa = *reinterpret_cast<const f32x4*>(&Ql[16 * rb + r][g * KQ + 4 * i]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = mfma_f32(qa[e], mb[i][e], acc[e]);
+        }
+        // P Delta: contraction over the chunk's tokens, lane group g tokens 16g..16g+15
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 pa = *reinterpret_cast<const f32x4*>(&Pl[16 * rb + r][16 * g + 4 * i]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = mfma_f32(pa[e], db[i][e], acc[e]);
+        }
+        const f32x4 o = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * scale;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = 16 * rb + 4 * g + i;
+            if (t < nt) a.out[(size_t)(t0 + t) * a.out_stride + (size_t)h * D + 16 * jt + r] = o[i];
+        }
     }
 }
 
@@ -651,7 +796,8 @@ hipError_t launch_gdn_d(const GdnArgs& a, hipStream_t st)
         hipLaunchKernelGGL(gdn_step_kernel<D>, dim3(a.n_v * (D / 16)), dim3(256), 0, st, a);
     } else if (a.ws) {
         hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(a.n_chunks, a.n_v), dim3(256), 0, st, a);
-        hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(a.n_v * (D / 16)), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(gdn_chain_kernel<D>, dim3(a.n_v * (D / 16)), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(gdn_out_kernel<D>, dim3(a.n_chunks, a.n_v), dim3(512), 0, st, a);
     } else {
         hipLaunchKernelGGL(gdn_kernel<D>, dim3(a.n_v * (D / kCols)), dim3(256), 0, st, a);
     }
