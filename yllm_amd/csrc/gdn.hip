@@ -282,9 +282,11 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
     ChunkWs<D> w(a.ws, h, c, a.n_chunks);
 
     // q and k rows of the chunk (zero past the last token): all loads issued
-    // before any LDS store
+    // before any LDS store; the l2 norms are taken in registers (a row's D/4
+    // float4s sit in D/4 consecutive lanes)
     {
         constexpr int NE = kC * D / 4 / 256;
+        constexpr int RL = D / 4;
         f32x4 kv[NE], qv[NE];
 #pragma unroll
         for (int u = 0; u < NE; ++u) {
@@ -292,6 +294,24 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
             const size_t off = (size_t)(t0 + min(t, nt - 1)) * a.qk_stride + (size_t)kh * D + i;
             kv[u] = *reinterpret_cast<const f32x4*>(a.k + off);
             qv[u] = *reinterpret_cast<const f32x4*>(a.q + off);
+        }
+        if (a.eps > 0.0f) {
+#pragma unroll
+            for (int u = 0; u < NE; ++u) {
+                float kk = 0.0f, qq = 0.0f;
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                    kk += kv[u][x] * kv[u][x];
+                    qq += qv[u][x] * qv[u][x];
+                }
+#pragma unroll
+                for (int m = RL / 2; m >= 1; m >>= 1) {
+                    kk += __shfl_xor(kk, m, 64);
+                    qq += __shfl_xor(qq, m, 64);
+                }
+                kv[u] *= 1.0f / fmaxf(sqrtf(kk), a.eps);
+                qv[u] *= 1.0f / fmaxf(sqrtf(qq), a.eps);
+            }
         }
 #pragma unroll
         for (int u = 0; u < NE; ++u) {
@@ -318,23 +338,6 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
         if (lane == 0) w.gl[0] = expf(glast);
     }
     __syncthreads();
-    if (a.eps > 0.0f) {
-        for (int row = wave; row < 2 * kC; row += 4) {
-            float* p = row < kC ? Kn[row] : Qn[row - kC];
-            float x[D / 64], ss = 0.0f;
-#pragma unroll
-            for (int u = 0; u < D / 64; ++u) {
-                x[u] = p[lane + 64 * u];
-                ss += x[u] * x[u];
-            }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-            const float rs = 1.0f / fmaxf(sqrtf(ss), a.eps);
-#pragma unroll
-            for (int u = 0; u < D / 64; ++u) p[lane + 64 * u] = x[u] * rs;
-        }
-        __syncthreads();
-    }
 
     // Q~ = diag(gamma) Q (rows kC..2kC-1 of [W; Q~]) and K~^T = (diag(e) K)^T
     // (d_k rows of kC tokens: the chain kernel's operand loads are then 16
@@ -350,46 +353,59 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
         *reinterpret_cast<f32x4*>(w.Kt + (size_t)ik * kC + t4) = kt;
     }
 
-    // Gram matrices K K^T and Q K^T; wave w owns token rows 16w..16w+15.
-    // Lane group g contracts over d_k indices g*KQ .. g*KQ+KQ-1.
+    // Gram matrices K K^T and Q K^T over the ten 16x16 tiles (tb, sb) with
+    // sb <= tb (A needs s < t, P needs s <= t; P is zero above); wave w takes
+    // tiles w, w+4, w+8.  Lane group g contracts over d_k indices g*KQ ..
+    // g*KQ+KQ-1.  The sums stay in registers until every read of Qn is done,
+    // then A overwrites Qn.
     {
-        float ak[KQ], aq[KQ];
+        static_assert(kC == 64, "four 16-token blocks per chunk");
+        constexpr int NTL = 10, TPW = 3;
+        f32x4 gkk[TPW], gqk[TPW];
 #pragma unroll
-        for (int kb = 0; kb < KQ; kb += 4) {
-            const f32x4 x = *reinterpret_cast<const f32x4*>(&Kn[16 * wave + r][g * KQ + kb]);
-            const f32x4 y = *reinterpret_cast<const f32x4*>(&Qn[16 * wave + r][g * KQ + kb]);
+        for (int j = 0; j < TPW; ++j) {
+            const int ti = wave + 4 * j;
+            gkk[j] = gqk[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (ti < NTL) {  // uniform over the wave
+                const int tb = ti >= 6 ? 3 : ti >= 3 ? 2 : ti >= 1 ? 1 : 0, sbk = ti - tb * (tb + 1) / 2;
+                f32x4 skk[2], sqk[2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                ak[kb + e] = x[e];
-                aq[kb + e] = y[e];
+                for (int e = 0; e < 2; ++e) skk[e] = sqk[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kb = 0; kb < KQ; kb += 4) {
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(&Kn[16 * tb + r][g * KQ + kb]);
+                    const f32x4 y = *reinterpret_cast<const f32x4*>(&Qn[16 * tb + r][g * KQ + kb]);
+                    const f32x4 b = *reinterpret_cast<const f32x4*>(&Kn[16 * sbk + r][g * KQ + kb]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        skk[e & 1] = mfma_f32(x[e], b[e], skk[e & 1]);
+                        sqk[e & 1] = mfma_f32(y[e], b[e], sqk[e & 1]);
+                    }
+                }
+                gkk[j] = skk[0] + skk[1];
+                gqk[j] = sqk[0] + sqk[1];
             }
         }
         __syncthreads();  // every read of Qn is done: A may overwrite it
-        for (int cb = 0; cb < kC / 16; ++cb) {
-            // four independent accumulators per product keep the MFMA pipe full
-            f32x4 skk[4], sqk[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) skk[e] = sqk[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TPW; ++j) {
+            const int ti = wave + 4 * j;
+            if (ti < NTL) {
+                const int tb = ti >= 6 ? 3 : ti >= 3 ? 2 : ti >= 1 ? 1 : 0, sbk = ti - tb * (tb + 1) / 2;
+                const int s = 16 * sbk + r;
 #pragma unroll
-            for (int kb = 0; kb < KQ; kb += 4) {
-                const f32x4 b = *reinterpret_cast<const f32x4*>(&Kn[16 * cb + r][g * KQ + kb]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    skk[e] = mfma_f32(ak[kb + e], b[e], skk[e]);
-                    sqk[e] = mfma_f32(aq[kb + e], b[e], sqk[e]);
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * tb + 4 * g + i;
+                    const float dec = s <= t ? expf(sg[t] - sg[s]) : 0.0f;
+                    Am[t][s] = s < t ? sb[t] * dec * gkk[j][i] : 0.0f;
+                    w.P[t * kC + s] = dec * gqk[j][i];
                 }
             }
-            const f32x4 skk_all = (skk[0] + skk[1]) + (skk[2] + skk[3]);
-            const f32x4 sqk_all = (sqk[0] + sqk[1]) + (sqk[2] + sqk[3]);
-            const int s = 16 * cb + r;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * wave + 4 * g + i;
-                const float dec = s <= t ? expf(sg[t] - sg[s]) : 0.0f;
-                Am[t][s] = s < t ? sb[t] * dec * skk_all[i] : 0.0f;
-                w.P[t * kC + s] = dec * sqk_all[i];
-            }
         }
+        // P above the diagonal blocks: row block `wave`, column blocks wave+1 ..
+        for (int cb = wave + 1; cb < kC / 16; ++cb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w.P[(16 * wave + 4 * g + i) * kC + 16 * cb + r] = 0.0f;
     }
     __syncthreads();
 
