@@ -616,7 +616,7 @@ def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool
                 "traffic": traffic_of(f"oproj{B}")}
         value, unit = nbytes / (ms * 1e-3) / 1e9, "GB/s"
     else:
-        roof = {"bound": "mfma", "kernel": ("oproj_gemm_kernel<%d,%d>" % ((4, 4) if B > 128 else (1, 1))) +
+        roof = {"bound": "mfma", "kernel": ("oproj_gemm_kernel<%d,%d>" % ((2, 4) if B > 128 else (1, 1))) +
                 ("" if att_dt == torch.float16 else " (+ oproj_split_kernel)"),
                 "achieved": flops / (kern_ms * 1e-3) / 1e12, "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                 "frac": flops / (kern_ms * 1e-3) / MFMA_F16_PEAK, "flops_per_launch": flops, "launch_ms": kern_ms,

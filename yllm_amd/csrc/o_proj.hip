@@ -133,13 +133,14 @@ __global__ __launch_bounds__(256) void oproj_split_kernel(_Float16* hi, _Float16
 //
 // A workgroup (4 waves, 2 x 2) owns BT tokens x BO outputs; a wave owns
 // (TM x 32) x (TN x 32) of them in TM x TN v_mfma_f32_32x32x16_f16
-// accumulators.  K advances 64 at a time through LDS: both tiles go from HBM
+// accumulators.  K advances 32 at a time through LDS: both tiles go from HBM
 // straight into LDS (buffer loads with the LDS destination, 16 bytes per
-// lane), rows of 128 bytes with XOR-swizzled 16-byte chunks so the fragment
-// reads are free of bank conflicts, double buffered: the next step's tiles
-// load while this step's MFMAs run.  Output: lane l holds output o = l % 32
-// of its 32 x 32 block and 16 tokens, so 32 lanes store 128 contiguous bytes
-// of an x row; the residual add is fused there.
+// lane), rows of 64 bytes with XOR-swizzled 16-byte chunks so the fragment
+// reads are free of bank conflicts, in three stages: the tiles of the next
+// two steps load while this step's MFMAs run.  Output: lane l holds output
+// o = l % 32 of its 32 x 32 block and 16 tokens; the residual add is a float
+// atomic add per element at L2 (one add per element, so the result is the
+// load, add and store's), which keeps x's read off the kernel's tail.
 struct GemmArgs {
     const _Float16* t[3];  // token rows, ld t_ld (elements)
     const _Float16* o[3];  // output rows (W_o), ld K
@@ -148,7 +149,7 @@ struct GemmArgs {
 };
 
 constexpr int kBK = 32;     // K per step: rows of 4 chunks of 16 bytes
-constexpr int kStages = 4;  // LDS stages: the loads of 3 steps ahead are in flight
+constexpr int kStages = 3;  // LDS stages: the loads of 2 steps ahead are in flight
 
 // 16-byte chunk swizzle of a 64-byte LDS row: 8 consecutive rows hit 8
 // distinct bank groups (32 banks, b128 reads in groups of 8 lanes), and 16
@@ -175,7 +176,7 @@ __device__ inline void gemm_lds_load16(__amdgpu_buffer_rsrc_t r, _Float16* lds, 
 }
 
 template <int TM, int TN>
-__global__ __launch_bounds__(256, 1) void oproj_gemm_kernel(GemmArgs a)
+__global__ __launch_bounds__(256, 2) void oproj_gemm_kernel(GemmArgs a)
 {
     constexpr int BT = 2 * TM * 32, BO = 2 * TN * 32;  // workgroup tile
     constexpr int ROWS = BT + BO;                       // LDS rows per stage (128 B each)
@@ -292,71 +293,19 @@ __global__ __launch_bounds__(256, 1) void oproj_gemm_kernel(GemmArgs a)
     }
     wait_vm<0>();  // the loads past the end land before the workgroup ends
 
-    // x[t][o] += acc: lane l holds output o0 + .. + l % 32 and tokens
-    // 8 (i / 4) + 4 (l / 32) + i % 4 of each 32 x 32 block.  All loads of a
-    // row block of the tile are issued before its stores: stores through x
-    // may alias later loads as far as the compiler can tell, so a plain
-    // `x[...] += acc` would wait for every load in turn.
-    // x += acc through LDS: the stages are free once every wave has left the
-    // K loop.  A wave's (TM x 32) x (TN x 32) block goes out in row blocks of
-    // two 32-token groups at a time: it writes them to its own LDS region as
-    // rows of TN x 32 floats (lane l holds output l % 32 and tokens 8 (i / 4)
-    // + 4 (l / 32) + i % 4 of each 32 x 32 block), reads them back as 16-byte
-    // pieces of whole rows, and updates x with 16-byte loads and stores, all
-    // loads of a row block before its stores.
-    __syncthreads();
-    constexpr int RW = TN * 32;           // floats per LDS row (a wave's outputs)
-    constexpr int RB = 1;                 // 32-token groups per pass
-    constexpr int PAD = 4;                // floats of padding per row (bank spread)
-    static_assert(4 * RB * 32 * (RW + PAD) * 4 <= (int)sizeof(lds), "epilogue area");
-    float* ep = reinterpret_cast<float*>(lds) + wave * RB * 32 * (RW + PAD);
-    constexpr int C4 = RW / 4;            // 16-byte pieces per row
-    constexpr int ROWS_PER_LD = 64 / C4;  // rows one wave instruction covers
-    constexpr int NPIECE = RB * 32 / ROWS_PER_LD;
-#pragma unroll 1
-    for (int m0 = 0; m0 < TM; m0 += RB) {
+    // x[t][o] += acc with float atomics at L2 (each element receives one
+    // add: the result equals a load, add and store), no load of x on the way
 #pragma unroll
-        for (int mm = 0; mm < RB; ++mm)
+    for (int m = 0; m < TM; ++m)
 #pragma unroll
-            for (int n = 0; n < TN; ++n)
+        for (int n = 0; n < TN; ++n) {
+            const uint32_t o = o0 + (wo * TN + n) * 32 + r32;
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    ep[(mm * 32 + 8 * (i / 4) + 4 * hh + (i % 4)) * (RW + PAD) + n * 32 + r32] = acc[m0 + mm][n][i];
-        // (the wave reads only its own region: LDS operations of one wave are in order)
-        const uint32_t tw = t0 + (wt * TM + m0) * 32;  // the pass's first token
-        const uint32_t ow = o0 + wo * RW;              // the wave's first output
-        const int c4 = lane % C4, rsub = lane / C4;
-        f32x4 xv[NPIECE], av[NPIECE];
-#pragma unroll
-        for (int p = 0; p < NPIECE; ++p) {
-            const int row = p * ROWS_PER_LD + rsub;
-            av[p] = *reinterpret_cast<const f32x4*>(ep + row * (RW + PAD) + 4 * c4);
-            const uint32_t t = tw + row, o = ow + 4 * c4;
-            xv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (t < a.N) {
-                const float* xp = a.x + (size_t)t * a.x_stride + o;
-                if (o + 3 < a.M && ((uintptr_t)xp & 15) == 0)
-                    xv[p] = *reinterpret_cast<const f32x4*>(xp);
-                else
-                    for (int e = 0; e < 4; ++e)
-                        if (o + e < a.M) xv[p][e] = xp[e];
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t t = t0 + (wt * TM + m) * 32 + 8 * (i / 4) + 4 * hh + (i % 4);
+                if (t < a.N && o < a.M) unsafeAtomicAdd(a.x + (size_t)t * a.x_stride + o, acc[m][n][i]);
             }
         }
-#pragma unroll
-        for (int p = 0; p < NPIECE; ++p) {
-            const int row = p * ROWS_PER_LD + rsub;
-            const uint32_t t = tw + row, o = ow + 4 * c4;
-            if (t < a.N) {
-                float* xp = a.x + (size_t)t * a.x_stride + o;
-                const f32x4 v = xv[p] + av[p];
-                if (o + 3 < a.M && ((uintptr_t)xp & 15) == 0)
-                    *reinterpret_cast<f32x4*>(xp) = v;
-                else
-                    for (int e = 0; e < 4; ++e)
-                        if (o + e < a.M) xp[e] = v[e];
-            }
-        }
-    }
 }
 
 template <int TM, int TN>
@@ -368,11 +317,13 @@ hipError_t launch_gemm_tiles(const GemmArgs& a, hipStream_t st)
     return hipGetLastError();
 }
 
-// Tile choice: 256 x 256 workgroup tiles for large batches (MFMA-bound; a
-// wave's 128 x 128 block reads 512 bytes of LDS per MFMA); 64 x 64 for small
-// ones (the engine's chunks of up to 64 tokens: the weights are read once and
-// the launch is bandwidth-bound, so more, smaller workgroups stream them).
-// Token rows are launched in pieces whose byte offsets stay below 2 GiB.
+// Tile choice: 128 x 256 workgroup tiles for large batches, two workgroups
+// per CU (MFMA-bound; one workgroup's barrier wait is covered by the other's
+// MFMAs: 8192 x 4096 x 4096 ran 787 TFLOP/s against 771 for 256 x 256 tiles
+// at one workgroup per CU); 64 x 64 for small ones (the engine's chunks of
+// up to 64 tokens: the weights are read once and the launch is
+// bandwidth-bound, so more, smaller workgroups stream them).  Token rows are
+// launched in pieces whose byte offsets stay below 2 GiB.
 hipError_t launch_gemm(GemmArgs a, hipStream_t st)
 {
     const uint64_t row_bytes = (uint64_t)a.t_ld * 2;
@@ -384,7 +335,7 @@ hipError_t launch_gemm(GemmArgs a, hipStream_t st)
         b.N = (uint32_t)(N - n0 < per ? N - n0 : per);
         for (uint32_t s = 0; s < a.nseg; ++s) b.t[s] = a.t[s] + (size_t)n0 * a.t_ld;
         b.x = a.x + (size_t)n0 * a.x_stride;
-        const hipError_t e = b.N > 128 ? launch_gemm_tiles<4, 4>(b, st) : launch_gemm_tiles<1, 1>(b, st);
+        const hipError_t e = b.N > 128 ? launch_gemm_tiles<2, 4>(b, st) : launch_gemm_tiles<1, 1>(b, st);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
