@@ -223,10 +223,19 @@ __global__ __launch_bounds__(256, 2) void oproj_gemm_kernel(GemmArgs a)
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(p), 0, bytes, 0x00020000);
     };
     const uint32_t t_bytes = ((a.N - 1) * a.t_ld + a.K) * 2u, o_bytes = a.M * a.K * 2u;
+    // the segments' base addresses as offsets from segment 0's, read once
+    // (indexing a.t[seg] in the loop reads the kernel arguments from memory at
+    // every step and waits for them; a select chain over the pointers went
+    // through scratch memory)
+    const uint64_t tb0 = (uint64_t)a.t[0], ob0 = (uint64_t)a.o[0];
+    const uint64_t td1 = (uint64_t)a.t[1] - tb0, td2 = (uint64_t)a.t[2] - tb0;
+    const uint64_t od1 = (uint64_t)a.o[1] - ob0, od2 = (uint64_t)a.o[2] - ob0;
     auto issue = [&](_Float16* buf, uint32_t st) {
         const bool past = st >= nsteps;  // workgroup-uniform
         const uint32_t seg = past ? 0 : st / ksteps, k0 = past ? 0 : (st % ksteps) * kBK;
-        const __amdgpu_buffer_rsrc_t rt = rsrc(a.t[seg], t_bytes), ro = rsrc(a.o[seg], o_bytes);
+        const uint64_t s1 = seg == 1, s2 = seg == 2;
+        const __amdgpu_buffer_rsrc_t rt = rsrc((const _Float16*)(tb0 + s1 * td1 + s2 * td2), t_bytes);
+        const __amdgpu_buffer_rsrc_t ro = rsrc((const _Float16*)(ob0 + s1 * od1 + s2 * od2), o_bytes);
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
             // a chunk past K (the last step of a K that is no multiple of 64)
