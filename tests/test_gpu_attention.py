@@ -359,6 +359,29 @@ def test_prefill_parity(cuda, oracle, nh, nkv, hd, ps, B, qdt, odt):
     assert max(rows) <= 3 * tol
 
 
+@pytest.mark.parametrize("nh,nkv,hd,B,qsig", [(28, 4, 128, 192, 1.0), (28, 4, 128, 192, 4.0), (28, 4, 128, 192, 8.0),
+                                            (16, 2, 256, 130, 4.0), (8, 8, 64, 100, 8.0)])
+def test_prefill_f32_queries_large_scores(cuda, oracle, nh, nkv, hd, B, qsig):
+    """fp32 queries that f16 cannot represent, scaled up to scores of std
+    ~qsig/2 (|s| up to ~20 at qsig 8): the kernel's QK^T takes q rounded to
+    f16, an error of about |s| * 2^-11 per score, which stays within the
+    tolerance at these magnitudes (the peaked softmax of qsig 8 included)."""
+    from yllm_amd.attention import attn_prefill
+
+    kvd = nkv * hd
+    K, V = gen(1700 + hd, (B, kvd)), gen(1800 + hd, (B, kvd))
+    q = gen(1900 + hd, (B, nh * hd), qsig, f16=False)
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    want = oracle.prefill(q, kc, vc, 0, B, nh, nkv, hd)
+    s0 = q[:, :hd] @ K[:, :hd].T / np.sqrt(hd)  # head 0's scores (before the causal mask)
+    got = attn_prefill(torch.from_numpy(q).to(cuda), cache, 0, nh).cpu().numpy()
+    err = rel_l2(got, want)
+    rows = max(rel_l2(got[i], want[i]) for i in range(B))
+    print(f"prefill f32 q sigma {qsig} {nh}/{nkv} d={hd}: head-0 score std {s0.std():.2f} max {np.abs(s0).max():.1f}, "
+          f"rel_l2={err:.3e}, worst row {rows:.3e}")
+    assert err <= TOL and rows <= 3 * TOL
+
+
 def test_prefill_gated_parity(cuda, oracle):
     from yllm_amd.attention import attn_prefill
 
