@@ -643,7 +643,7 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
     this path)."""
     import torch
 
-    from yllm_amd.attention import (ROPE_MROPE, LayerKV, attn_decode, attn_prefill, decode_workspace,
+    from yllm_amd.attention import (ROPE_MROPE, LayerKV, attn_decode_rope, attn_prefill, decode_workspace,
                                     decode_workspace_bytes, rope_kv_store)
     from yllm_amd.gdn import gdn_chunk, gdn_chunk_workspace_bytes, gdn_conv, gdn_decode, gdn_gated_norm, gdn_gates
 
@@ -684,7 +684,6 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
     dout = torch.empty(nh * da, device=dev)
     dws = decode_workspace(decode_workspace_bytes(1, L, L, nh, nkv, da), dev)
     q_pre = torch.empty((T, qd), dtype=torch.bfloat16, device=dev)  # rotated prefill queries
-    q_dec = torch.empty((1, qd), device=dev)                          # rotated decode query (fp32, engine hb2)
     qkv = at["qkv"]
 
     def rope_store(t0, t1, q_out):
@@ -699,7 +698,7 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
         gdn_gated_norm(gout[:T], g["z"][:T], g["norm_w"], hg, out=gout[:T])
 
     def gdn_layer_step(li, t):
-        # two launches per layer and token; the delay line alternates between
+        # one launch per layer and token; the delay line alternates between
         # cst and cst2 (an even number of decode tokens ends back in cst)
         g = gd[li]
         c_in, c_out = (cst[li], cst2[li]) if (t - T) % 2 == 0 else (cst2[li], cst[li])
@@ -721,8 +720,9 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
         for t in range(T, L):
             for li in range(n_gdn):
                 gdn_layer_step(li, t)
-            rope_store(t, t + 1, q_dec)
-            attn_decode(q_dec[0], cache, t, nh, gate=at["gate"][t], out=dout, workspace=dws)
+            # RoPE + KV store of the token fused into the split-K decode
+            attn_decode_rope(qkv[t, :qd], qkv[t, qd:qd + kvd], qkv[t, qd + kvd:], cache, t, nh, ROPE_MROPE, 1e7,
+                             n_rot=64, gate=at["gate"][t], out=dout, workspace=dws)
 
     # one step is ~1300 launches: its graph is captured once and replayed
     ms, _ = time_steps(step, steps, warmup, dout, graph_per_step=True)
@@ -733,7 +733,7 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
                                f"1 gated attention layer ({nh}/{nkv} heads, d {da}: M-RoPE over 64 dims + KV "
                                f"store from fp32 q/k/v rows, bf16 prefill queries, sigmoid gate); "
                                f"{T}-token prefill (chunked GDN, MFMA attention) then {n_dec} decode steps "
-                               f"(fused GDN token per layer (2 launches), RoPE + KV store, split-K decode) per step; N(0,1)*0.5 seed "
+                               f"(fused GDN token per layer, one launch; RoPE + KV store fused into the split-K decode) per step; N(0,1)*0.5 seed "
                                f"{hex(seed)}",
                    "prefill_tokens": T, "decode_steps": n_dec},
         "roofline": None,

@@ -93,6 +93,25 @@ int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
                      uint32_t n_kv_heads, uint32_t head_dim, uint32_t kv_stride,
                      const float* gate, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The decode step with its RoPE and KV store fused into one launch: what
+ * yhip_rope_kv_store (one token at pos, q_out fp32) followed by
+ * yhip_attn_decode computes (engine.c:1054-1096; qwen35 910-960).  q, k, v are the token's raw
+ * (unrotated) fp32 rows, [n_heads*head_dim] and [n_kv_heads*head_dim]; q is
+ * not modified.  The key and value of position pos are rotated, rounded with
+ * the reference f32->f16 rounding and stored into kcache / vcache, which
+ * must not hold them yet.  rope, n_rot and theta as yhip_rope_kv_store
+ * (n_rot a multiple of 8); gate and workspace as yhip_attn_decode.  q and
+ * att_out 16-byte aligned.  The cosines and sines are the host's cosf / sinf
+ * of the reference's angles, so q and the stored key are rotated exactly as
+ * the reference rotates them (yhip_rope_kv_store uses the device's, an ulp
+ * or two apart).  It saves the separate RoPE launch of every decode token:
+ * the workgroup whose key range holds pos rotates the token's key and uses it
+ * directly, the others rotate only the query. */
+int yhip_attn_decode_rope(float* att_out, const float* q, const float* k, const float* v, uint16_t* kcache,
+                          uint16_t* vcache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                          uint32_t kv_stride, uint32_t rope, uint32_t n_rot, float theta, const float* gate,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* Ragged batch of independent sequences (one query token each).  No
  * reference counterpart beyond calling the decode once per engine; it is the
  * multi-sequence form of the same computation.

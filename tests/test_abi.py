@@ -255,3 +255,17 @@ def test_gdn_decode_rejects_bad_args(hiplib):
     assert call(S=ctypes.c_void_p(0x1004)) == -22 and "aligned" in _err(hiplib)
     assert call(cout=ctypes.c_void_p(0x100000 + 64)) == -22 and "overlaps" in _err(hiplib)
     assert call(cin=None) == -22 and "null" in _err(hiplib)
+
+
+def test_decode_rope_rejects_bad_args(hiplib):
+    F = ctypes.c_float
+    args = lambda **kw: [kw.get("out", P), P, P, P, P, P, kw.get("pos", 0), 8, 8, 64, 64, kw.get("rope", 1),
+                         kw.get("n_rot", 0), F(1e4), None, None, 0, None]
+    assert hiplib.yhip_attn_decode_rope(*args(out=None)) == -22 and "null" in _err(hiplib)
+    assert hiplib.yhip_attn_decode_rope(*args(pos=64)) == -22 and "kv_stride" in _err(hiplib)
+    assert hiplib.yhip_attn_decode_rope(*args(rope=9)) == -22 and "rope" in _err(hiplib)
+    assert hiplib.yhip_attn_decode_rope(*args(rope=3, n_rot=3)) == -22 and "n_rot" in _err(hiplib)
+    assert hiplib.yhip_attn_decode_rope(*args(out=ctypes.c_void_p(0x1004))) == -22 and "aligned" in _err(hiplib)
+    # 32k keys split: a workspace is needed
+    big = [P, P, P, P, P, P, 32767, 32, 8, 128, 32768, 1, 0, F(1e4), None, None, 0, None]
+    assert hiplib.yhip_attn_decode_rope(*big) == -28 and "workspace" in _err(hiplib)

@@ -141,9 +141,11 @@ def test_config5_gdn_layer_prefill_then_decode(cuda, oracle, li):
 def test_config5_gated_attention_prefill_then_decode(cuda, oracle):
     """The group's gated attention layer: M-RoPE (64 dims, theta 1e7) + KV
     store of 4096 prompt rows, causal prefill with bf16 queries and the
-    sigmoid gate, bf16 out; then 256 decode steps, each a one-row RoPE + store
-    and a gated decode over keys 0..t."""
-    from yllm_amd.attention import (ROPE_MROPE, LayerKV, attn_decode, attn_prefill, decode_workspace,
+    sigmoid gate, bf16 out; then 256 decode steps, each the token's RoPE +
+    store fused into a gated decode over keys 0..t (attn_decode_rope, the
+    bench's decode step; test_gpu_rope checks it against the two launches
+    bit for bit)."""
+    from yllm_amd.attention import (ROPE_MROPE, LayerKV, attn_decode_rope, attn_prefill, decode_workspace,
                                     decode_workspace_bytes, round_bf16, rope_kv_store)
 
     nh, nkv, hd, T0, T1, theta = 16, 2, 256, 4096, 256, np.float32(1e7)
@@ -164,9 +166,8 @@ def test_config5_gated_attention_prefill_then_decode(cuda, oracle):
     ws = decode_workspace(decode_workspace_bytes(1, T, T, nh, nkv, hd), cuda)
     dec = []
     for t in range(T0, T):
-        q_t = rope_kv_store(cache, xt[t:t + 1, :qd], xt[t:t + 1, qd:qd + kvd], xt[t:t + 1, qd + kvd:], t, nh,
-                            ROPE_MROPE, float(theta), n_rot=64)
-        dec.append(attn_decode(q_t[0], cache, t, nh, gate=gt[t], workspace=ws).cpu().numpy())
+        dec.append(attn_decode_rope(xt[t, :qd], xt[t, qd:qd + kvd], xt[t, qd + kvd:], cache, t, nh, ROPE_MROPE,
+                                    float(theta), n_rot=64, gate=gt[t], workspace=ws).cpu().numpy())
     # the stored K rows are the oracle's to an f16 ulp (device sin/cos), V bit for bit
     from yllm_amd.attention import kv_to_engine
 

@@ -20,6 +20,7 @@ from oracle_lib import rel_l2, untile_v
 
 pytestmark = pytest.mark.gpu
 SENTINEL = 0x7777  # cache fill that the store must leave alone outside its rows
+TOL_ATT = 1e-3    # attention outputs: max relative L2 error vs the fp32 CPU oracle
 
 
 def gen(seed, shape, sigma=1.0):
@@ -221,3 +222,68 @@ def test_rope_kv_store_full_size_sampled_rows(cuda, oracle):
     # dims past n_rot are copied unrotated: their K bits are exactly the rounding of k
     kk = K[:, :B, :].transpose(1, 0, 2).reshape(B, nkv, d)[:, :, 64:]
     assert np.array_equal(kk, oracle.f32_to_f16(np.ascontiguousarray(k.reshape(B, nkv, d)[:, :, 64:])))
+
+
+# ---------------------------------------------- RoPE + KV store + decode, fused
+
+@pytest.mark.parametrize("kind,nh,nkv,d,pos,n_rot,gated", [
+    ("pairs", 32, 8, 128, 4095, 0, False),
+    ("pairs", 32, 8, 128, 32767, 0, False),    # many splits; the token in the last
+    ("half", 14, 2, 64, 512, 0, False),
+    ("mrope", 16, 2, 256, 4351, 64, True),     # the hybrid group's gated layer
+    ("mrope", 16, 2, 256, 0, 64, True),        # the token is the only key
+    ("none", 28, 4, 128, 127, 0, False),       # the token ends a 128-key split
+    ("pairs", 8, 8, 64, 128, 0, False),        # the token starts a split
+])
+def test_decode_rope_matches_oracle_and_two_launches(cuda, oracle, kind, nh, nkv, d, pos, n_rot, gated):
+    """yhip_attn_decode_rope against the oracle (the reference's RoPE, store
+    and decode) and against yhip_rope_kv_store + yhip_attn_decode on a copy
+    of the same cache.  The fused path takes the host's cosf / sinf of the
+    reference's angles, the two-launch path the device's: q and the stored
+    key may differ by an fp32 / f16 ulp, the values and the earlier rows are
+    bit for bit the same."""
+    from yllm_amd.attention import (ROPE_HALF, ROPE_MROPE, ROPE_NONE, ROPE_PAIRS, LayerKV, attn_decode,
+                                    attn_decode_rope, kv_store, rope_kv_store)
+
+    rope = {"pairs": ROPE_PAIRS, "half": ROPE_HALF, "mrope": ROPE_MROPE, "none": ROPE_NONE}[kind]
+    theta = 1e7 if kind == "mrope" else 1e4
+    qd, kvd = nh * d, nkv * d
+    a = LayerKV.empty(nkv, d, pos + 41, device=cuda)
+    K0, V0 = gen(401 + d, (pos, kvd)), gen(402 + d, (pos, kvd))
+    if pos > 0:
+        kv_store(a, torch.from_numpy(K0).to(cuda), torch.from_numpy(V0).to(cuda), 0)
+    b = LayerKV(a.k.clone(), a.v.clone())
+    row, q, k, v = fused_rows(403 + d, 1, nh, nkv, d)
+    gate = gen(404 + d, (qd,)) if gated else None
+
+    # the oracle: the token's RoPE + store, then the decode over rows 0..pos
+    q_rot, kc_t, vc_t = oracle.rope_kv_store(q, k, v, pos, nh, nkv, d, np.float32(theta), rope, n_rot)
+    kc = np.concatenate([oracle.f32_to_f16(K0), kc_t]) if pos else kc_t
+    vc = np.concatenate([oracle.f32_to_f16(V0), vc_t]) if pos else vc_t
+    want = oracle.decode(q_rot[0], kc, vc, pos, nh, nkv, d)
+    if gated:
+        want = oracle.gate_sigmoid(want, gate)
+
+    rt = torch.from_numpy(row[0]).to(cuda)
+    qt, kt, vt = rt[:qd], rt[qd:qd + kvd], rt[qd + kvd:]
+    gt = torch.from_numpy(gate).to(cuda) if gated else None
+    q_before = qt.clone()
+    got = attn_decode_rope(qt, kt, vt, b, pos, nh, rope, theta, n_rot=n_rot, gate=gt).cpu().numpy()
+    assert torch.equal(qt, q_before)
+    q2 = rope_kv_store(a, qt.view(1, -1), kt.view(1, -1), vt.view(1, -1), pos, nh, rope, theta, n_rot=n_rot)
+    two = attn_decode(q2.view(-1), a, pos, nh, gate=gt).cpu().numpy()
+
+    err, err2 = rel_l2(got, want), rel_l2(got, two)
+    Ka, Va = cache_bits(a)
+    Kb, Vb = cache_bits(b)
+    kb_row = Kb[:, pos, :].reshape(-1)
+    k_ref = kc_t[0].reshape(nkv, d).reshape(-1)
+    ulps_ref = f16_ulps(kb_row, k_ref).max()
+    ulps_two = f16_ulps(kb_row, Ka[:, pos, :].reshape(-1)).max()
+    print(f"decode_rope {kind} {nh}/{nkv} d={d} pos={pos}: rel_l2 vs oracle {err:.2e}, vs two launches "
+          f"{err2:.2e}; token K row vs oracle <= {ulps_ref} ulp, vs two launches <= {ulps_two} ulp")
+    assert err <= TOL_ATT and err2 <= 1e-5
+    assert ulps_ref <= 1 and ulps_two <= 1
+    # everything but the token's K row is bit for bit the two-launch path's
+    Ka[:, pos, :] = Kb[:, pos, :]
+    assert np.array_equal(Ka, Kb) and np.array_equal(Va, Vb)

@@ -27,6 +27,9 @@ SIGNATURES = {
                                   c_uint32, c_uint32, c_void_p]),
     "yhip_attn_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32,
                                  c_uint32, c_uint32, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "yhip_attn_decode_rope": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32,
+                                      c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, c_float, c_void_p, c_void_p,
+                                      c_size_t, c_void_p]),
     "yhip_attn_decode_batch": (c_int, [c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_void_p,
                                        c_void_p, c_uint32, c_uint32, c_uint64, c_uint32, c_uint32,
                                        c_uint32, c_uint32, c_void_p, c_uint32, c_void_p, c_size_t,

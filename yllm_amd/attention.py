@@ -231,6 +231,28 @@ def attn_decode(q: torch.Tensor, cache: LayerKV, pos: int, n_heads: int, gate: t
     return out
 
 
+def attn_decode_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache: LayerKV, pos: int, n_heads: int,
+                     rope: int, theta: float, n_rot: int = 0, gate: torch.Tensor | None = None,
+                     out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """rope_kv_store of the token at pos followed by attn_decode, in one
+    launch (same result, same cache bits).  q [n_heads*head_dim], k and v
+    [n_kv*head_dim]: the token's raw fp32 rows (contiguous); q is not
+    modified; k and v are rotated / stored into the cache at pos."""
+    _need_gpu(q, k, v, gate)
+    d = cache.head_dim
+    if (q.dtype != torch.float32 or k.dtype != torch.float32 or v.dtype != torch.float32 or
+            q.numel() != n_heads * d or k.numel() != cache.n_kv * d or v.numel() != cache.n_kv * d):
+        raise YhipError(-22, "attn_decode_rope: q, k, v must be the token's f32 rows")
+    if out is None:
+        out = torch.empty(n_heads * d, dtype=torch.float32, device=q.device)
+    nbytes = decode_workspace_bytes(1, pos + 1, pos + 1, n_heads, cache.n_kv, d)
+    ws = _workspace(nbytes, q.device, workspace)
+    check(lib().yhip_attn_decode_rope(_ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(cache.k), _ptr(cache.v), pos,
+                                      n_heads, cache.n_kv, d, cache.kv_stride, rope, n_rot, theta, _ptr(gate),
+                                      _ptr(ws), nbytes, _stream()))
+    return out
+
+
 class DecodeBatch:
     """Device tables (K/V base pointers per sequence) for attn_decode_batch."""
 

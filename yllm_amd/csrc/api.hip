@@ -166,6 +166,26 @@ int api_fail(int code, const char* msg) { return fail(code, "%s", msg); }
 
 }  // namespace yhip
 
+namespace {
+
+// The reference's frequency formula (matvec.c:895) with the host powf, for
+// the rotated pairs j < span / 2; the last table is kept per thread.
+void rope_freqs(float* freq, uint32_t rope, uint32_t span, float theta)
+{
+    if (rope == YHIP_ROPE_NONE) return;
+    thread_local float t_theta = 0.0f;
+    thread_local uint32_t t_span = 0;
+    thread_local float t_freq[128];
+    if (t_span != span || !(t_theta == theta)) {
+        for (uint32_t j = 0; j < span / 2; ++j) t_freq[j] = powf(theta, -2.0f * (float)j / (float)span);
+        t_span = span;
+        t_theta = theta;
+    }
+    memcpy(freq, t_freq, sizeof(float) * (span / 2));
+}
+
+}  // namespace
+
 extern "C" {
 
 int yhip_attn_decode_batch(float* att_out, uint32_t out_stride, const float* q,
@@ -215,6 +235,64 @@ int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
     a.c = (float)(1.4426950408889634 / sqrt((double)head_dim));
     yhip::decode_bind_workspace(a, workspace);
     return done(yhip::launch_decode(a, (hipStream_t)stream), fn);
+}
+
+int yhip_attn_decode_rope(float* att_out, const float* q, const float* k, const float* v, uint16_t* kcache,
+                          uint16_t* vcache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                          uint32_t kv_stride, uint32_t rope, uint32_t n_rot, float theta, const float* gate,
+                          void* workspace, size_t workspace_bytes, void* stream)
+{
+    const char* fn = "yhip_attn_decode_rope";
+    if (!att_out || !q || !k || !v || !kcache || !vcache) return fail(YHIP_EINVAL, "%s: null pointer", fn);
+    int rc = check_heads(fn, n_heads, n_kv_heads, head_dim, kv_stride);
+    if (rc) return rc;
+    if (pos >= kv_stride) return fail(YHIP_EINVAL, "%s: pos %u >= kv_stride %u", fn, pos, kv_stride);
+    if (rope > YHIP_ROPE_MROPE) return fail(YHIP_EINVAL, "%s: unknown rope kind %u", fn, rope);
+    if (rope == YHIP_ROPE_MROPE && (n_rot == 0 || n_rot % 8 || n_rot > head_dim))
+        return fail(YHIP_EINVAL, "%s: n_rot %u must be a multiple of 8 and at most head_dim", fn, n_rot);
+    if ((uintptr_t)q % 16 || (uintptr_t)att_out % 16)
+        return fail(YHIP_EINVAL, "%s: q and att_out must be 16-byte aligned", fn);
+    yhip::DecodeArgs a = {};
+    const uint32_t len = pos + 1;
+    const size_t need = yhip::decode_plan(1, len, len, n_heads, n_kv_heads, head_dim, &a.split_keys,
+                                          &a.n_splits);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(YHIP_ENOSPC, "%s: workspace %zu < %zu bytes", fn, workspace_bytes, need);
+    a.q = q;
+    a.k0 = kcache;
+    a.v0 = vcache;
+    a.len0 = len;
+    a.out = att_out;
+    a.gate = gate;
+    a.n_seq = 1;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.D = head_dim;
+    a.kv_stride = kv_stride;
+    a.q_stride = n_heads * head_dim;
+    a.out_stride = n_heads * head_dim;
+    a.gate_stride = n_heads * head_dim;
+    a.c = (float)(1.4426950408889634 / sqrt((double)head_dim));
+    yhip::decode_bind_workspace(a, workspace);
+    yhip::DecodeRope r = {};
+    r.k = k;
+    r.v = v;
+    r.kc = kcache;
+    r.vc = vcache;
+    r.kind = rope;
+    r.n_rot = rope == YHIP_ROPE_MROPE ? n_rot : head_dim;
+    if (rope != YHIP_ROPE_NONE) {
+        // the angles and their cosines and sines as the reference forms them
+        // (matvec.c:895-898: host powf, float product, cosf, sinf)
+        float freq[128];
+        rope_freqs(freq, rope, r.n_rot, theta);
+        for (uint32_t j = 0; j < r.n_rot / 2; ++j) {
+            const float ang = freq[j] * (float)pos;
+            r.cs[0][j] = cosf(ang);
+            r.cs[1][j] = sinf(ang);
+        }
+    }
+    return done(yhip::launch_decode_rope(a, r, (hipStream_t)stream), fn);
 }
 
 size_t yhip_attn_prefill_workspace(uint32_t B, uint32_t max_end, uint32_t n_heads, uint32_t n_kv_heads,
@@ -390,20 +468,7 @@ int yhip_rope_kv_store(void* q_out, uint32_t q_out_dtype, uint32_t q_out_stride,
     a.kv_stride = kv_stride;
     a.kind = rope;
     a.n_rot = rope == YHIP_ROPE_MROPE ? n_rot : head_dim;
-    {
-        // the reference's frequency formula (matvec.c:895), host powf;
-        // the last table is kept per thread
-        thread_local float t_theta = 0.0f;
-        thread_local uint32_t t_span = 0;
-        thread_local float t_freq[128];
-        const uint32_t span = a.n_rot;
-        if (rope != YHIP_ROPE_NONE && (t_span != span || !(t_theta == theta))) {
-            for (uint32_t j = 0; j < span / 2; ++j) t_freq[j] = powf(theta, -2.0f * (float)j / (float)span);
-            t_span = span;
-            t_theta = theta;
-        }
-        if (rope != YHIP_ROPE_NONE) memcpy(a.freq, t_freq, sizeof(float) * (span / 2));
-    }
+    rope_freqs(a.freq, rope, a.n_rot, theta);
     return done(yhip::launch_rope_kv(a, (hipStream_t)stream), fn);
 }
 

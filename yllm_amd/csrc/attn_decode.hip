@@ -67,8 +67,15 @@ struct Frag {
     f16x8 v[D / 16];
 };
 
-template <int D>
-__global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_split_kernel(DecodeArgs a)
+// ROPE: the query arrives unrotated and the token at position len0 - 1 is
+// neither rotated nor stored yet (yhip_attn_decode_rope): every workgroup
+// rotates the query heads it stages (each thread loads its float4 and, for
+// pairs half a span apart, the partner float4), and the workgroup whose split
+// holds the token rotates the token's key, stores key and value into the
+// cache and substitutes them for the cache rows it loaded.  The cosines and
+// sines come from the host's cosf / sinf, as the reference computes them.
+template <int D, bool ROPE>
+__global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_split_kernel(DecodeArgs a, DecodeRope rp)
 {
     constexpr int kWaves = waves_of<D>();
     constexpr int kThreads = 64 * kWaves;
@@ -78,6 +85,7 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     __shared__ float s_m[kWaves][16];
     __shared__ float s_l[kWaves][16];
     __shared__ float s_hm[16], s_hl[16];  // per head: max and sum over the waves
+    __shared__ __attribute__((aligned(16))) uint16_t s_knew[ROPE ? D : 8], s_vnew[ROPE ? D : 8];  // the token's K, V bits
 
     const uint32_t seq = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
     // a length beyond the planned maximum is clamped, never read past
@@ -157,14 +165,56 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     constexpr int QPT = (16 * D4 + kThreads - 1) / kThreads;   // float4s per thread
     static_assert(sizeof(s_o) >= 2 * 16 * QROW * sizeof(_Float16), "q staging fits the combine area");
     _Float16* s_q = reinterpret_cast<_Float16*>(&s_o[0][0][0]);  // [2][16][QROW]: hi, lo
-    f32x4 qv[QPT];
+    // ROPE: pairs (d, d + half) of the first `span` dims for HALF / MROPE
+    // (half = span / 2), (d, d + 1) for PAIRS; a thread rotating a float4 of
+    // the first kind also loads its partner float4 at d +- half
+    const uint32_t rkind = ROPE ? rp.kind : kRopeNone;
+    const uint32_t span = (rkind == kRopeMrope) ? rp.n_rot : (uint32_t)D, half = span / 2;
+    const bool far_pairs = rkind == kRopeHalf || rkind == kRopeMrope;
+    // a rotated element's pair index (the cosine and sine it needs)
+    auto pair_of = [&](uint32_t d) -> uint32_t { return far_pairs ? (d < half ? d : d - half) : d >> 1; };
+    auto rotated = [&](uint32_t d) -> bool { return far_pairs ? d < span : rkind == kRopePairs; };
+    f32x4 qv[QPT], qp[ROPE ? QPT : 1], qc[ROPE ? QPT : 1], qs[ROPE ? QPT : 1];
     {
         const float* qbase = a.q + (size_t)seq * a.q_stride + (size_t)h0 * D;
 #pragma unroll
         for (int r = 0; r < QPT; ++r) {
-            const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4;
+            const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
             qv[r] = f32x4{0.f, 0.f, 0.f, 0.f};
             if (idx < 16 * D4 && hn < G) qv[r] = *reinterpret_cast<const f32x4*>(qbase + (size_t)idx * 4);
+            if constexpr (ROPE) {
+                qp[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (far_pairs && idx < 16 * D4 && hn < G && d < span)
+                    qp[r] = *reinterpret_cast<const f32x4*>(qbase + (size_t)hn * D + (d < half ? d + half : d - half));
+                // the cosines and sines (kernel arguments) are read with the
+                // other loads, each lane its elements' pairs
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    qc[r][e] = 1.0f;
+                    qs[r][e] = 0.0f;
+                    if (idx < 16 * D4 && hn < G && rotated(d + e)) {
+                        qc[r][e] = rp.cs[0][pair_of(d + e)];
+                        qs[r][e] = rp.cs[1][pair_of(d + e)];
+                    }
+                }
+            }
+        }
+    }
+    // ROPE: the new token (key len0 - 1) and, in the workgroup whose split
+    // holds it, its raw key element d and partner, and its value element
+    // (thread d < D)
+    const uint32_t tpos = len - 1;
+    const bool owns_tok = ROPE && kbeg <= tpos && tpos < kend;  // uniform over the workgroup
+    float kraw = 0.0f, kpart = 0.0f, vraw = 0.0f, kcos = 1.0f, ksin = 0.0f;
+    if (ROPE && owns_tok && threadIdx.x < (uint32_t)D) {
+        const uint32_t d = threadIdx.x;
+        const uint32_t pr = far_pairs ? (d < span ? (d < half ? d + half : d - half) : d) : (d ^ 1u);
+        kraw = rp.k[(size_t)kvh * D + d];
+        kpart = rp.k[(size_t)kvh * D + pr];
+        vraw = rp.v[(size_t)kvh * D + d];
+        if (rotated(d)) {
+            kcos = rp.cs[0][pair_of(d)];
+            ksin = rp.cs[1][pair_of(d)];
         }
     }
 
@@ -174,19 +224,60 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
 #pragma unroll
     for (int i = 0; i < NBUF; ++i) load(f[i], wave + i * kWaves);
 
+    if constexpr (ROPE) {
+        // element d with value x, partner value p and its pair's cosine c and
+        // sine sn: the reference's (a, b) -> (a c - b s, a s + b c), a the
+        // pair's first element (the unrotated elements carry c = 1, sn = 0 and
+        // pass through unchanged)
+        auto rotate = [&](uint32_t d, float x, float p, float c, float sn) {
+#pragma clang fp contract(off)
+            if (!rotated(d)) return x;
+            const bool first = far_pairs ? d < half : (d & 1u) == 0;
+            return first ? x * c - p * sn : p * sn + x * c;
+        };
 #pragma unroll
-    for (int r = 0; r < QPT; ++r) {
-        const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
-        if (idx < 16 * D4) {
-            f16x4 hi, lo;
+        for (int r = 0; r < QPT; ++r) {
+            const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
+            if (idx < 16 * D4) {
+                f16x4 hi, lo;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const _Float16 h = (_Float16)qv[r][e];
-                hi[e] = h;
-                lo[e] = (_Float16)(qv[r][e] - (float)h);
+                for (int e = 0; e < 4; ++e) {
+                    // partner: the same lane's float4 for PAIRS (element e ^ 1), else the loaded one
+                    const float p = far_pairs ? qp[r][e] : qv[r][e ^ 1];
+                    const float x = rotate(d + e, qv[r][e], p, qc[r][e], qs[r][e]);
+                    const _Float16 h = (_Float16)x;
+                    hi[e] = h;
+                    lo[e] = (_Float16)(x - (float)h);
+                }
+                *reinterpret_cast<f16x4*>(s_q + hn * QROW + d) = hi;
+                *reinterpret_cast<f16x4*>(s_q + (16 + hn) * QROW + d) = lo;
             }
-            *reinterpret_cast<f16x4*>(s_q + hn * QROW + d) = hi;
-            *reinterpret_cast<f16x4*>(s_q + (16 + hn) * QROW + d) = lo;
+        }
+        if (owns_tok && threadIdx.x < (uint32_t)D) {
+            // the token's key and value with the reference rounding, into the
+            // cache and, for the substitution below, into LDS
+            const uint32_t d = threadIdx.x;
+            const uint16_t kb = f32_to_f16_ref(rotate(d, kraw, kpart, kcos, ksin)), vb = f32_to_f16_ref(vraw);
+            rp.kc[k_index(kvh, tpos, d, D, a.kv_stride)] = kb;
+            rp.vc[v_index(kvh, tpos, d, D, a.kv_stride)] = vb;
+            s_knew[d] = kb;
+            s_vnew[d] = vb;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < QPT; ++r) {
+            const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
+            if (idx < 16 * D4) {
+                f16x4 hi, lo;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const _Float16 h = (_Float16)qv[r][e];
+                    hi[e] = h;
+                    lo[e] = (_Float16)(qv[r][e] - (float)h);
+                }
+                *reinterpret_cast<f16x4*>(s_q + hn * QROW + d) = hi;
+                *reinterpret_cast<f16x4*>(s_q + (16 + hn) * QROW + d) = lo;
+            }
         }
     }
     lds_barrier();
@@ -199,6 +290,32 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     }
 
     auto compute = [&](Frag<D>& f, uint32_t key0) {
+        if constexpr (ROPE) {
+            // the block holding the token: its row came from the cache before
+            // the token was stored; lanes holding it take the new bits.  K row
+            // rr sits in half t = (rr >> 2) & 1 of lane n = 4 (rr >> 3) + rr % 4;
+            // V position rr in element rr % 8 of lane group rr >> 3.
+            // (value selects only: a store into a fragment chosen at run time
+            // moved the fragment sets to scratch memory)
+            if (owns_tok && tpos >= key0 && tpos < key0 + kKeysPerBlock) {  // uniform over the wave
+                const uint32_t rr = tpos - key0;
+                const bool krow_here = (uint32_t)n == 4 * (rr >> 3) + (rr & 3u);
+                const bool k0 = krow_here && !(rr & 4u), k1 = krow_here && (rr & 4u);
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const f16x8 kn = *reinterpret_cast<const f16x8*>(&s_knew[c * 32 + g * 8]);
+                    f.k[0][c] = k0 ? kn : f.k[0][c];
+                    f.k[1][c] = k1 ? kn : f.k[1][c];
+                }
+                const bool vcol_here = (uint32_t)g == rr >> 3;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const _Float16 vn = __builtin_bit_cast(_Float16, s_vnew[b * 16 + n]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) f.v[b][e] = (vcol_here && (uint32_t)e == (rr & 7u)) ? vn : f.v[b][e];
+                }
+            }
+        }
         f32x4 s[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -428,11 +545,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
     }
 }
 
-template <int D>
-hipError_t launch_decode_d(const DecodeArgs& a, hipStream_t st)
+template <int D, bool ROPE>
+hipError_t launch_decode_d(const DecodeArgs& a, const DecodeRope& r, hipStream_t st)
 {
     dim3 grid(a.n_splits, a.n_kv, a.n_seq);
-    hipLaunchKernelGGL(decode_split_kernel<D>, grid, dim3(64 * waves_of<D>()), 0, st, a);
+    hipLaunchKernelGGL((decode_split_kernel<D, ROPE>), grid, dim3(64 * waves_of<D>()), 0, st, a, r);
     constexpr uint32_t slices = D < kMergeSlice ? 1 : D / kMergeSlice;
     if (a.n_splits > 1)
         hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.n_heads * slices, a.n_seq), dim3(256), 0, st, a);
@@ -546,10 +663,22 @@ void decode_bind_workspace(DecodeArgs& a, void* workspace)
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st)
 {
+    const DecodeRope none{};
     switch (a.D) {
-    case 64: return launch_decode_d<64>(a, st);
-    case 128: return launch_decode_d<128>(a, st);
-    case 256: return launch_decode_d<256>(a, st);
+    case 64: return launch_decode_d<64, false>(a, none, st);
+    case 128: return launch_decode_d<128, false>(a, none, st);
+    case 256: return launch_decode_d<256, false>(a, none, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_decode_rope(const DecodeArgs& a, const DecodeRope& r, hipStream_t st)
+{
+    if (a.n_seq != 1 || a.lens || a.len0 == 0) return hipErrorInvalidValue;
+    switch (a.D) {
+    case 64: return launch_decode_d<64, true>(a, r, st);
+    case 128: return launch_decode_d<128, true>(a, r, st);
+    case 256: return launch_decode_d<256, true>(a, r, st);
     default: return hipErrorInvalidValue;
     }
 }

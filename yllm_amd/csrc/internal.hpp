@@ -48,6 +48,18 @@ size_t decode_workspace_bound(uint32_t n_seq, uint32_t max_len, uint64_t total_l
 // carve the workspace into part_ml / part_o for a plan
 void decode_bind_workspace(DecodeArgs& a, void* workspace);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
+// RoPE and the KV store of the token at position len0 - 1 fused into a
+// single-sequence decode: q is the raw (unrotated) query row; k, v the raw
+// key and value rows of the token (fp32, n_kv * D each)
+struct DecodeRope {
+    const float* k;
+    const float* v;
+    uint16_t* kc;        // the K cache and V tiles the token is stored into
+    uint16_t* vc;
+    uint32_t kind, n_rot;
+    float cs[2][128];    // cos, sin of pair j's angle at the token's position, host cosf / sinf
+};
+hipError_t launch_decode_rope(const DecodeArgs& a, const DecodeRope& r, hipStream_t st);
 
 // ---- api.hip ----
 // The checks, plan and launches of yhip_attn_decode_batch with the partials
