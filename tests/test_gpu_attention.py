@@ -333,6 +333,10 @@ def test_decode_long_context_full_size(cuda, oracle):
     (2, 1, 256, 0, 129, torch.float32, torch.float32),
     (4, 1, 128, 0, 129, torch.float16, torch.float32),
     (2, 2, 64, 0, 193, torch.float32, torch.float32),
+    # head_dim 256 (32-key tiles, two waves per 32 queries): a start inside
+    # a tile, GQA 8:1, many items; and f16 queries into bf16 output
+    (8, 1, 256, 45, 300, torch.float16, torch.bfloat16),
+    (32, 4, 256, 0, 1100, torch.float16, torch.float32),
 ])
 def test_prefill_parity(cuda, oracle, nh, nkv, hd, ps, B, qdt, odt):
     from yllm_amd.attention import attn_prefill
@@ -461,6 +465,8 @@ def test_prefill_full_size_sampled_rows(cuda, oracle, nh, nkv, hd, L):
     (28, 4, 128, 1984, 64, torch.float32, torch.float32, False),
     (32, 8, 128, 8128, 64, torch.float16, torch.float32, False),
     (16, 2, 256, 4032, 64, torch.bfloat16, torch.bfloat16, True),
+    (16, 2, 256, 1001, 37, torch.float32, torch.float32, False),
+    (4, 4, 256, 100, 200, torch.float16, torch.float32, True),
     (14, 2, 64, 2000, 64, torch.float32, torch.float16, False),
     # a wave's rows straddle two heads (B not a multiple of 32); uneven groups
     (28, 4, 128, 3001, 37, torch.float32, torch.float32, False),

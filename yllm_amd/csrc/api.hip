@@ -347,7 +347,7 @@ int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, co
     size_t need = yhip::prefill_plan(a);
     if (need > 0 && !workspace) {
         a.n_split = 1;
-        a.split_tiles = (pos_start + B - 1) / 64 + 1;
+        a.split_tiles = (pos_start + B - 1) / yhip::prefill_tile_keys(head_dim) + 1;
         need = 0;
     }
     if (need > 0 && (workspace_bytes < need || (uintptr_t)workspace % 16))

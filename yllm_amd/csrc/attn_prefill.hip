@@ -39,7 +39,10 @@ namespace yhip {
 namespace {
 
 constexpr int BM = 128;  // queries per workgroup
-constexpr int BN = 64;   // keys per tile
+// Keys per tile: 64 up to head_dim 128; 32 at 256, so that a workgroup's
+// double-buffered K and V tiles take 64 KB of LDS and two workgroups (two
+// waves per SIMD) fit on a CU.
+__host__ __device__ constexpr int bn_of(int D) { return D > 128 ? 32 : 64; }
 
 __device__ inline f32x16 mfma32(const f16x8& a, const f16x8& b, const f32x16& c)
 {
@@ -120,23 +123,29 @@ __device__ inline void lds_load16(__amdgpu_buffer_rsrc_t r, _Float16* lds, int v
 // rows of 8 chunks (128 B) the swizzle is (r & 7) ^ bit 3 of r: 8 consecutive
 // rows then hit 8 distinct chunk columns (32-bank LDS, b128 reads in groups
 // of 8 lanes) and 16 consecutive rows give each half of a 256-byte bank
-// window 8 distinct columns (64 banks, groups of 16 lanes).  Rows of 16 or
-// more chunks (256 B and up) use r & 15.  Both depend on bits 0..3 of the
-// row only, so rows 32 apart share the swizzle.
+// window 8 distinct columns (64 banks, groups of 16 lanes).  Rows of 4
+// chunks (64 B, the V^T rows of 32-key tiles) take (bit 1 ^ bit 3, bit 2):
+// a bijection of bits 1, 2 for the four rows of one parity among 8 (32
+// banks) and of bits 2, 3 for the four rows r, r+4, r+8, r+12 that share a
+// 256-byte window (64 banks).  Rows of 16 or more chunks (256 B and up) use
+// r & 15.  All depend on bits 0..3 of the row only, so rows 32 apart share
+// the swizzle.
 template <int NCH>
 __device__ inline int chunk_swz(int r)
 {
-    return NCH >= 16 ? (r & 15) : ((r & 7) ^ ((r >> 3) & 1));
+    if constexpr (NCH >= 16) return r & 15;
+    else if constexpr (NCH == 8) return (r & 7) ^ ((r >> 3) & 1);
+    else return (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2);
 }
 
 // Schedule of one key step's MFMAs: NQ score MFMAs of the next tile and NPV
-// P.V MFMAs of this tile (k-slot kc = n / NDB uses the probabilities
-// 8 kc .. 8 kc + 7), with the tile's 32 probabilities spread over them.
+// P.V MFMAs of this tile (k-slot kc = n / NDB of NKC uses the probabilities
+// 8 kc .. 8 kc + 7), with the tile's 8 NKC probabilities spread over them.
 // The exp2 of a probability is quarter rate (about as long as half a
 // 32x32x16 MFMA with its fma, add and convert), so one to two per MFMA hide
 // under the matrix pipe, where 32 under the score MFMAs alone or under the
 // PV MFMAs alone would not.  Slot order: the first NQ/2 score MFMAs under
-// k-slot 0's probabilities; then for kc = 0..3 k-slot kc's PV MFMAs
+// k-slot 0's probabilities; then for kc = 0..NKC-1 k-slot kc's PV MFMAs
 // interleaved with the next score MFMAs under k-slot kc+1's probabilities.
 struct FSlot {
     int8_t pv;  // 0: score MFMA n, 1: PV MFMA n
@@ -144,23 +153,25 @@ struct FSlot {
     int8_t p0;  // probabilities p0 .. p0+np-1 formed after this MFMA
     int8_t np;
 };
-template <int NQ, int NPV, int NDB>
+template <int NQ, int NPV, int NDB, int NKC>
 struct FusedSchedule {
+    static_assert(NPV == NKC * NDB && NKC >= 2, "k-slots of 16 keys");
     static constexpr int N = NQ + NPV;
     FSlot s[N];
     constexpr FusedSchedule() : s{}
     {
-        const int QA = NQ / 2, QB = (NQ - QA + 2) / 3;
+        const int QA = NQ / 2, QB = (NQ - QA + NKC - 2) / (NKC - 1);
         int k = 0, q = 0, v = 0;
         for (int t = 0; t < QA; ++t)
             s[k++] = FSlot{0, (int8_t)q++, (int8_t)(t * 8 / QA), (int8_t)((t + 1) * 8 / QA - t * 8 / QA)};
-        for (int kc = 0; kc < 4; ++kc) {
-            const int nq = kc < 3 ? (QB < NQ - q ? QB : NQ - q) : NQ - q;
+        for (int kc = 0; kc < NKC; ++kc) {
+            const bool more = kc < NKC - 1;
+            const int nq = more ? (QB < NQ - q ? QB : NQ - q) : NQ - q;
             const int tot = NDB + nq;
             for (int t = 0; t < tot; ++t) {
                 const bool is_pv = (t + 1) * NDB / tot > t * NDB / tot;
-                const int p0 = kc < 3 ? 8 * (kc + 1) + t * 8 / tot : 0;
-                const int np = kc < 3 ? (t + 1) * 8 / tot - t * 8 / tot : 0;
+                const int p0 = more ? 8 * (kc + 1) + t * 8 / tot : 0;
+                const int np = more ? (t + 1) * 8 / tot - t * 8 / tot : 0;
                 s[k++] = FSlot{(int8_t)is_pv, (int8_t)(is_pv ? v++ : q++), (int8_t)p0, (int8_t)np};
             }
         }
@@ -220,7 +231,7 @@ __device__ inline bool wave_span(const PrefillArgs& a, const PItem& I, int wave,
 // Key tiles of an item: [t0, t0 + nt).  The item's last key is kmax (its
 // last query's position; with packed rows (B < 128) every item holds some
 // head's query B-1).
-template <bool SPLIT>
+template <int BN, bool SPLIT>
 __device__ inline void item_keys(const PrefillArgs& a, const PItem& I, uint32_t& kmax, uint32_t& t0, uint32_t& nt)
 {
     kmax = a.pos_start + ((SPLIT && a.pack) ? a.B - 1 : min(a.B, I.qb * BM + BM) - 1);
@@ -238,13 +249,29 @@ __device__ inline void item_keys(const PrefillArgs& a, const PItem& I, uint32_t&
 // SPLIT: the split mode (one item per workgroup, packed rows, a key range
 // per split); a separate instantiation keeps the plain mode's registers.
 template <int D, int NG, bool SPLIT>
-__global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefill_kernel(PrefillArgs a)
+__global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128) ? 2 : 1) void prefill_kernel(
+    PrefillArgs a)
 {
     static_assert(NG == 1 || NG == 2, "one or two key groups");
     static_assert(!SPLIT || NG == 1, "the split mode runs one key group");
-    constexpr int NKK = D / 16;   // k-chunks of the score MFMA
-    constexpr int NDB = D / 32;   // d-blocks of the output MFMA
-    constexpr int CH = D / 32;    // 16-byte chunks per thread per tile (K and V each)
+    // Pair mode (head_dim 256): a wave's 32 queries with all 256 dimensions
+    // need 64 registers of Q and 128 of O, which leaves one wave per SIMD.
+    // Instead two waves share 32 queries and each owns half the dimensions
+    // of Q and O; each forms the scores over its half, the halves meet
+    // through LDS at the step barrier (the sum is formed in the same order by
+    // both waves, so both hold the same scores, maximum and probabilities),
+    // and each accumulates its half of O.  The workgroup is 8 waves over the
+    // same 128 queries, one per CU, two waves per SIMD.
+    constexpr bool PAIR = D > 128;
+    static_assert(!PAIR || NG == 1, "pair mode runs one key group");
+    constexpr int LT = PAIR ? 512 : 256;  // threads of a key group (they share the tile loads)
+    constexpr int DQ = PAIR ? D / 2 : D;  // dimensions of Q and O a wave holds
+    constexpr int BN = bn_of(D);  // keys per tile
+    constexpr int NS = BN / 32;   // 32-key halves of a tile (score accumulators)
+    constexpr int NKC = BN / 16;  // k-slots of the output MFMA per tile
+    constexpr int NKK = DQ / 16;  // k-chunks of the score MFMA
+    constexpr int NDB = DQ / 32;  // d-blocks of the output MFMA
+    constexpr int CH = BN * D / (8 * LT);  // 16-byte chunks per thread per tile (K and V each)
     constexpr int KCH = D / 8;    // 16-byte chunks per K row
     constexpr int VCH = BN / 8;   // 16-byte chunks per V row
     constexpr float kSlack = 8.0f;
@@ -269,6 +296,9 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
     __shared__ __attribute__((aligned(16))) _Float16 Vl1[NG][D * BN];
     // (max, sum) of group 1's queries for the two-group merge
     __shared__ float s_ml[NG > 1 ? 512 : 1];
+    // pair mode: each wave's partial scores of a tile, by tile parity, as
+    // [parity][wave][float4 j][lane] (consecutive lanes, consecutive 16 bytes)
+    __shared__ f32x4 Xl[PAIR ? 2 * 8 * 4 * NS * 64 : 1];
 
     // Items (query block, head) in heaviest-first order are dealt to the
     // resident workgroups in snake order (item slot it*W + j on even rounds,
@@ -343,12 +373,14 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         int tid;
         asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
         const int lane = tid & 63;
-        const int grp = tid >> 8, gtid = tid & 255, wave = gtid >> 6;
+        const int grp = tid / LT, gtid = tid % LT, wave = gtid >> 6;
+        // the wave's 32 queries (qw) and, in pair mode, its half of the dimensions (hf)
+        const int qw = PAIR ? wave >> 1 : wave, hf = PAIR ? wave & 1 : 0;
         const int r32 = lane & 31, hh = lane >> 5;
         PItem nxt{};
         const bool has_next = item_of(it + 1, nxt);
 
-        // Chunk L = 256 i + gtid of a tile is the 16 bytes this thread loads
+        // Chunk L = LT i + gtid of a tile is the 16 bytes this thread loads
         // with its i-th instruction.  K: LDS row R = L / KCH holds key row
         // lds_row_of_key(R) (an involution), column chunk (L % KCH) ^ swz(R).
         // V: LDS row d = L / VCH holds positions 8c..8c+7 in chunk
@@ -356,7 +388,7 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         int kgo[CH], vgo[CH];
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-            const int L = gtid + 256 * i;
+            const int L = gtid + LT * i;
             const int R = L / KCH, kc = (L % KCH) ^ chunk_swz<KCH>(R);
             kgo[i] = (lds_row_of_key(R) * D + kc * 8) * 2;
             const int d = L / VCH, vc = (L % VCH) ^ chunk_swz<VCH>(d);
@@ -382,11 +414,11 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // tile kt of a K (V) resource into K (V) buffer par
         auto dma_k_of = [&](__amdgpu_buffer_rsrc_t r, int par, uint32_t kt) {
 #pragma unroll
-            for (int i = 0; i < CH; ++i) lds_load16(r, kbuf(par) + (256 * i + 64 * wave) * 8, kgo[i], kt * BN * D * 2);
+            for (int i = 0; i < CH; ++i) lds_load16(r, kbuf(par) + (LT * i + 64 * wave) * 8, kgo[i], kt * BN * D * 2);
         };
         auto dma_v_of = [&](__amdgpu_buffer_rsrc_t r, int par, uint32_t kt) {
 #pragma unroll
-            for (int i = 0; i < CH; ++i) lds_load16(r, vbuf(par) + (256 * i + 64 * wave) * 8, vgo[i], kt * BN * D * 2);
+            for (int i = 0; i < CH; ++i) lds_load16(r, vbuf(par) + (LT * i + 64 * wave) * 8, vgo[i], kt * BN * D * 2);
         };
         auto dma_done = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };  // vmcnt(0): this thread's loads landed
         f16x8 qf[NKK];
@@ -394,7 +426,7 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // tile and the queries
         auto item_steps = [&](const PItem& I, uint32_t& t0) {
             uint32_t km, nt;
-            item_keys<SPLIT>(a, I, km, t0, nt);
+            item_keys<BN, SPLIT>(a, I, km, t0, nt);
             return nt > (uint32_t)grp ? (nt - grp + NG - 1) / NG : 0u;  // this group's tiles
         };
         auto issue_item_k = [&](const PItem& I) {
@@ -406,9 +438,9 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         };
         auto issue_item_q = [&](const PItem& I) {
             if (a.q_dtype == kF16) {
-                const PRow rw = row_of<SPLIT>(a, I, wave * 32 + r32);
-                const uint16_t* qp =
-                    reinterpret_cast<const uint16_t*>(a.q) + (size_t)rw.b * a.q_stride + (size_t)rw.h * D + hh * 8;
+                const PRow rw = row_of<SPLIT>(a, I, qw * 32 + r32);
+                const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + (size_t)rw.b * a.q_stride +
+                                     (size_t)rw.h * D + hf * DQ + hh * 8;
 #pragma unroll
                 for (int kk = 0; kk < NKK; ++kk) qf[kk] = *reinterpret_cast<const f16x8*>(qp + kk * 16);
             }
@@ -426,16 +458,16 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
 
         const uint32_t kvh = cur.kvh;
         uint32_t kmax, t0, ntiles;  // this item's keys end at kmax; its tiles are t0 .. t0+ntiles-1
-        item_keys<SPLIT>(a, cur, kmax, t0, ntiles);
+        item_keys<BN, SPLIT>(a, cur, kmax, t0, ntiles);
         const uint32_t nsteps = (ntiles + NG - 1) / NG;  // loop steps (workgroup-uniform)
         // this group's tiles: kt = t0 + grp + NG*st for st < gsteps
         const uint32_t gsteps = ntiles > (uint32_t)grp ? (ntiles - grp + NG - 1) / NG : 0;
 
         uint32_t wfirst, wlast;
-        const bool wave_active = wave_span<SPLIT>(a, cur, wave, wfirst, wlast);
+        const bool wave_active = wave_span<SPLIT>(a, cur, qw, wfirst, wlast);
         const uint32_t wpos_first = a.pos_start + wfirst;
         const uint32_t wpos_last = a.pos_start + wlast;
-        const PRow myrow = row_of<SPLIT>(a, cur, wave * 32 + r32);
+        const PRow myrow = row_of<SPLIT>(a, cur, qw * 32 + r32);
         const uint32_t my_pos = a.pos_start + myrow.b;
         // tiles this wave computes: t0 .. t0+wtiles-1, of which this group's are st < wsteps
         const uint32_t wend = wave_active ? wpos_last / BN + 1 : 0;  // one past the wave's last tile
@@ -448,13 +480,40 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         auto dma_v = [&](int par, uint32_t st) { dma_v_of(rV, par, tile_of(st)); };
 
         // MFMA operands from LDS.  K fragment (j, kk): key row r32 + 32 j, dims
-        // 16 kk + 8 hh .. +7 = chunk 2 kk + hh.  V fragment (b, kc): row
-        // d = 32 b + r32, positions 16 kc + 8 hh .. +7 = chunk 2 kc + hh.
+        // DQ hf + 16 kk + 8 hh .. +7 = chunk 2 (kk + NKK hf) + hh.  V fragment
+        // (b, kc): row d = DQ hf + 32 b + r32, positions 16 kc + 8 hh .. +7 =
+        // chunk 2 kc + hh.
         auto read_k = [&](int par, int j, int kk) {
-            return *reinterpret_cast<const f16x8*>(kbuf(par) + (r32 + 32 * j) * D + (((2 * kk + hh) ^ ksw) << 3));
+            return *reinterpret_cast<const f16x8*>(kbuf(par) + (r32 + 32 * j) * D +
+                                                   (((2 * (kk + NKK * hf) + hh) ^ ksw) << 3));
         };
         auto read_v = [&](int par, int b, int kc) {
-            return *reinterpret_cast<const f16x8*>(vbuf(par) + (32 * b + r32) * BN + (((2 * kc + hh) ^ vsw) << 3));
+            return *reinterpret_cast<const f16x8*>(vbuf(par) + (DQ * hf + 32 * b + r32) * BN +
+                                                   (((2 * kc + hh) ^ vsw) << 3));
+        };
+        // pair mode: publish this wave's partial scores of a tile (before the
+        // step barrier), add the partner's (after it)
+        auto xwrite = [&](const f32x16 (&S)[NS], int par) {
+            if constexpr (PAIR) {
+#pragma unroll
+                for (int j = 0; j < NS; ++j)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4)
+                        Xl[((par * 8 + wave) * 4 * NS + 4 * j + q4) * 64 + lane] =
+                            f32x4{S[j][4 * q4], S[j][4 * q4 + 1], S[j][4 * q4 + 2], S[j][4 * q4 + 3]};
+            }
+        };
+        auto xadd = [&](f32x16 (&S)[NS], int par) {
+            if constexpr (PAIR) {
+#pragma unroll
+                for (int j = 0; j < NS; ++j)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        const f32x4 o4 = Xl[((par * 8 + (wave ^ 1)) * 4 * NS + 4 * j + q4) * 64 + lane];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) S[j][4 * q4 + e] += o4[e];
+                    }
+            }
         };
         // Keys past kmax in the workgroup's last tile were never stored and may
         // hold any bits: their P is 0, but their V must be finite.  The group
@@ -463,7 +522,7 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
             const uint32_t k0 = tile_of(st) * BN;
             const uint32_t valid = kmax - k0 + 1;  // keys 0..valid-1 of the tile are stored
             _Float16* vb = vbuf(par);
-            for (int idx = gtid; idx < D * VCH; idx += 256) {
+            for (int idx = gtid; idx < D * VCH; idx += LT) {
                 const int d = idx / VCH, c = idx % VCH;  // logical chunk c: keys 8c..8c+7
                 if ((uint32_t)(8 * c + 7) < valid) continue;
                 f16x8* ch = reinterpret_cast<f16x8*>(vb + d * BN + ((c ^ chunk_swz<VCH>(d)) << 3));
@@ -485,21 +544,21 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
 
-        // scores of the tile in K buffer P into S (both 32-key halves)
-        auto qk = [&](f32x16 (&S)[2], int par) {
+        // scores of the tile in K buffer P into S (its 32-key halves)
+        auto qk = [&](f32x16 (&S)[NS], int par) {
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < NS; ++j) {
                     const f16x8 kf = read_k(par, j, kk);
                     S[j] = kk == 0 ? mfma32(kf, qf[0], f32x16{}) : mfma32(kf, qf[kk], S[j]);
                 }
         };
         // running max update of the lane's query from tile scores S (raw, masked)
-        auto update_max = [&](const f32x16 (&S)[2]) {
+        auto update_max = [&](const f32x16 (&S)[NS]) {
             float mx = S[0][0];
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < NS; ++j)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) mx = fmaxf(mx, S[j][i]);
             // the lane pair (l, l+32) holds one query: exchange the halves
@@ -515,10 +574,10 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
                 for (int b = 0; b < NDB; ++b) o[b] *= alpha;
             }
         };
-        auto probs = [&](const f32x16 (&S)[2], f16x8 (&pf)[4]) {
+        auto probs = [&](const f32x16 (&S)[NS], f16x8 (&pf)[NKC]) {
             const float nm = -m;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) {
+            for (int i = 0; i < 16 * NS; ++i) {
                 const float p = fast_exp2(fmaf(S[i >> 4][i & 15], a.c, nm));
                 l += p;
                 pf[i >> 3][i & 7] = (_Float16)p;
@@ -526,8 +585,8 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         };
         // O^T += V^T P^T over the tile in V buffer P; fragments are read two
         // MFMAs ahead (three in a ring)
-        auto pv = [&](const f16x8 (&pf)[4], int par) {
-            constexpr int NM = 4 * NDB;  // MFMA n: kc = n / NDB, b = n % NDB
+        auto pv = [&](const f16x8 (&pf)[NKC], int par) {
+            constexpr int NM = NKC * NDB;  // MFMA n: kc = n / NDB, b = n % NDB
             f16x8 vf[3];
             vf[0] = read_v(par, 0, 0);
             vf[1] = read_v(par, 1 % NDB, 1 / NDB);
@@ -541,14 +600,14 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // (V buffer vpar), with this tile's probabilities (from Scur) formed
         // between them per FusedSchedule; K and V fragments are read two MFMAs
         // ahead in their own streams.
-        auto qk_pv = [&](f32x16 (&Snext)[2], int kpar, const f32x16 (&Scur)[2], int vpar) {
-            constexpr int NQ = 2 * NKK, NPV = 4 * NDB;
-            constexpr FusedSchedule<NQ, NPV, NDB> sch{};
+        auto qk_pv = [&](f32x16 (&Snext)[NS], int kpar, const f32x16 (&Scur)[NS], int vpar) {
+            constexpr int NQ = NS * NKK, NPV = NKC * NDB;  // score MFMA n: half n % NS, k-chunk n / NS
+            constexpr FusedSchedule<NQ, NPV, NDB, NKC> sch{};
             constexpr int MAXP = 8;
             const float nm = -m;
-            f16x8 pf[4], kf[3], vf[3];
+            f16x8 pf[NKC], kf[3], vf[3];
             kf[0] = read_k(kpar, 0, 0);
-            kf[1] = read_k(kpar, 1, 0);
+            kf[1] = read_k(kpar, 1 % NS, 1 / NS);
             vf[0] = read_v(vpar, 0, 0);
             vf[1] = read_v(vpar, 1 % NDB, 1 / NDB);
 #pragma unroll
@@ -558,9 +617,9 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
                     if (n + 2 < NPV) vf[(n + 2) % 3] = read_v(vpar, (n + 2) % NDB, (n + 2) / NDB);
                     o[n % NDB] = mfma32(vf[n % 3], pf[n / NDB], o[n % NDB]);
                 } else {
-                    if (n + 2 < NQ) kf[(n + 2) % 3] = read_k(kpar, (n + 2) & 1, (n + 2) >> 1);
-                    Snext[n & 1] = n < 2 ? mfma32(kf[n % 3], qf[0], f32x16{})
-                                         : mfma32(kf[n % 3], qf[n >> 1], Snext[n & 1]);
+                    if (n + 2 < NQ) kf[(n + 2) % 3] = read_k(kpar, (n + 2) % NS, (n + 2) / NS);
+                    Snext[n % NS] = n < NS ? mfma32(kf[n % 3], qf[0], f32x16{})
+                                           : mfma32(kf[n % 3], qf[n / NS], Snext[n % NS]);
                 }
 #pragma unroll
                 for (int u = 0; u < MAXP; ++u) {
@@ -575,11 +634,11 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         };
         // a tile that reaches past the wave's first query: keys beyond the
         // lane's position get -inf
-        auto mask = [&](f32x16 (&S)[2], uint32_t st) {
+        auto mask = [&](f32x16 (&S)[NS], uint32_t st) {
             const uint32_t k0 = tile_of(st) * BN;
             if (k0 + BN - 1 > wpos_first) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < NS; ++j)
 #pragma unroll
                     for (int i = 0; i < 16; ++i)
                         if (k0 + 32 * j + key_of_acc(i, hh) > my_pos) S[j][i] = -INFINITY;
@@ -592,14 +651,17 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // waits then count only tile loads.
         dma_done();
         if (a.q_dtype != kF16) {
-            const size_t qbase = (size_t)myrow.b * a.q_stride + (size_t)myrow.h * D + hh * 8;
+            const size_t qbase = (size_t)myrow.b * a.q_stride + (size_t)myrow.h * D + hf * DQ + hh * 8;
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, qbase + kk * 16, a.q_dtype);
             dma_done();
         }
         __syncthreads();
-        f32x16 Sa[2], Sb[2];
-        if (wsteps > 0) qk(Sa, 0);
+        f32x16 Sa[NS], Sb[NS];
+        if (wsteps > 0) {
+            qk(Sa, 0);
+            xwrite(Sa, 0);
+        }
         // step 0 loads K(2) over K(0), whose last readers are the scores above
         __syncthreads();
 
@@ -618,7 +680,7 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // the group's last step (or, for a group without tiles, the first) issues
         // the next item's loads
         const uint32_t last_st = gsteps > 0 ? gsteps - 1 : 0;
-        auto step = [&](int p, uint32_t st, f32x16 (&Scur)[2], f32x16 (&Snext)[2]) {
+        auto step = [&](int p, uint32_t st, f32x16 (&Scur)[NS], f32x16 (&Snext)[NS]) {
             if (st + 2 < gsteps) dma_k(p, st + 2);
             if (st + 1 < gsteps) dma_v(1 - p, st + 1);
             if (prefetch && st == last_st) {
@@ -631,13 +693,16 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
                 lds_barrier();
             }
             if (st + 1 < wsteps) {
+                xadd(Scur, p);
                 mask(Scur, st);
                 update_max(Scur);
                 qk_pv(Snext, 1 - p, Scur, p);
+                xwrite(Snext, 1 - p);
             } else if (st < wsteps) {
+                xadd(Scur, p);
                 mask(Scur, st);
                 update_max(Scur);
-                f16x8 pf[4];
+                f16x8 pf[NKC];
                 probs(Scur, pf);
                 pv(pf, p);
             }
@@ -667,7 +732,8 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
         // ones of the item's start need not stay live through the key loop.
         int tid_e;
         asm volatile("v_mov_b32 %0, %1" : "=v"(tid_e) : "v"((int)threadIdx.x));
-        const int gtid_e = tid_e & 255, lane_e = tid_e & 63;
+        const int gtid_e = tid_e % LT, lane_e = tid_e & 63;
+        const int qw_e = PAIR ? gtid_e >> 7 : gtid_e >> 6, hf_e = PAIR ? (gtid_e >> 6) & 1 : 0;
         if constexpr (NG > 1) {
             // Group 1 hands (m, l, O) to group 0 through LDS: m, l in s_ml and O
             // through V buffer 1 of both groups (the one buffer the next item's
@@ -707,13 +773,13 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
                 if (r == 0) lds_barrier();  // round 0 read before round 1 overwrites
             }
         }
-        const PRow rw = row_of<SPLIT>(a, cur, (gtid_e >> 6) * 32 + (lane_e & 31));
-        if ((tid_e >> 8) == 0 && rw.valid) {  // group 1 handed its part over
+        const PRow rw = row_of<SPLIT>(a, cur, qw_e * 32 + (lane_e & 31));
+        if (tid_e / LT == 0 && rw.valid) {  // group 1 handed its part over
             if (SPLIT && a.n_split > 1) {
                 // split partials: (max, sum) and the unnormalised O of this
                 // row over this split's keys
                 const size_t pr = ((size_t)cur.split * a.n_heads + rw.h) * a.B + rw.b;
-                if ((lane_e >> 5) == 0) {
+                if ((lane_e >> 5) == 0 && hf_e == 0) {
                     typedef float f32x2 __attribute__((ext_vector_type(2)));
                     *reinterpret_cast<f32x2*>(a.part_ml + 2 * pr) = f32x2{m, l};
                 }
@@ -721,7 +787,7 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
                 for (int b = 0; b < NDB; ++b)
 #pragma unroll
                     for (int i4 = 0; i4 < 4; ++i4) {
-                        const uint32_t d = b * 32 + 8 * i4 + 4 * (lane_e >> 5);
+                        const uint32_t d = hf_e * DQ + b * 32 + 8 * i4 + 4 * (lane_e >> 5);
                         f32x4 v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] = o[b][4 * i4 + e];
@@ -733,7 +799,7 @@ __global__ __launch_bounds__(256 * NG, (NG == 1 && D <= 128) ? 2 : 1) void prefi
                 for (int b = 0; b < NDB; ++b) {
 #pragma unroll
                     for (int i4 = 0; i4 < 4; ++i4) {
-                        const uint32_t d = b * 32 + 8 * i4 + 4 * (lane_e >> 5);
+                        const uint32_t d = hf_e * DQ + b * 32 + 8 * i4 + 4 * (lane_e >> 5);
                         f32x4 v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] = o[b][4 * i4 + e] * inv;
@@ -822,6 +888,9 @@ int n_cus()
     return n_cu;
 }
 
+// threads of a prefill workgroup: 4 waves per key group, 8 in pair mode
+constexpr int prefill_threads(int D, int NG) { return 256 * NG * (D > 128 ? 2 : 1); }
+
 template <int D, int NG>
 hipError_t launch_prefill_d(PrefillArgs a, hipStream_t st)
 {
@@ -838,7 +907,8 @@ hipError_t launch_prefill_d(PrefillArgs a, hipStream_t st)
     // resident workgroups: one round of the grid fills every slot once
     static const int per_cu = [] {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<D, NG, false>, 256 * NG, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<D, NG, false>, prefill_threads(D, NG), 0) !=
+                hipSuccess ||
             n < 1)
             n = 1;
         return n;
@@ -854,13 +924,13 @@ hipError_t launch_prefill_d(PrefillArgs a, hipStream_t st)
         return e ? atoi(e) : -1;
     }();
     uint32_t grid = items;
-    if (persist > 0 || (persist < 0 && NG > 1)) {
+    if (persist > 0 || (persist < 0 && prefill_threads(D, NG) > 256)) {
         const uint64_t slots = (uint64_t)per_cu * (uint64_t)n_cus();
         if (slots < grid) grid = (uint32_t)slots;
         if (a.xcd_map) grid = grid / 8u * 8u;  // whole XCD groups (items are a multiple of 8)
         if (grid == 0) grid = items;
     }
-    hipLaunchKernelGGL((prefill_kernel<D, NG, false>), dim3(grid), dim3(256 * NG), 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<D, NG, false>), dim3(grid), dim3(prefill_threads(D, NG)), 0, st, a);
     return hipGetLastError();
 }
 
@@ -870,7 +940,7 @@ hipError_t launch_prefill_split_d(const PrefillArgs& a, hipStream_t st)
     const uint32_t ipg = a.n_rb * (a.pack ? 1u : a.gmax);
     const uint32_t groups = a.n_kv * a.n_split;
     const uint32_t grid = (groups + 7u) / 8u * 8u * ipg;
-    hipLaunchKernelGGL((prefill_kernel<D, 1, true>), dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<D, 1, true>), dim3(grid), dim3(prefill_threads(D, 1)), 0, st, a);
     if (a.n_split > 1) {
         const uint64_t threads = (uint64_t)a.B * a.n_heads * (D / 4);
         hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, st, a);
@@ -938,7 +1008,7 @@ void split_shape(uint32_t B, uint32_t n_heads, uint32_t n_kv, uint32_t D, uint32
     pack = B < (uint32_t)BM;
     n_rb = pack ? (gmax * B + BM - 1) / BM : (B + BM - 1) / BM;
     base = (uint64_t)n_kv * n_rb * (pack ? 1u : gmax);
-    target = (uint64_t)(D <= 128 ? 2 : 1) * (uint64_t)n_cus();
+    target = (uint64_t)(D <= 128 ? 2 : 1) * (uint64_t)n_cus();  // resident workgroups per CU
 }
 
 }  // namespace
@@ -961,7 +1031,7 @@ size_t prefill_plan(PrefillArgs& a)
     uint64_t base, target;
     split_shape(a.B, a.n_heads, a.n_kv, a.D, a.pack, a.n_rb, a.gmax, base, target);
     a.split_mode = 1;
-    const uint32_t ntiles = (a.pos_start + a.B - 1) / BN + 1;
+    const uint32_t ntiles = (a.pos_start + a.B - 1) / bn_of((int)a.D) + 1;
     uint64_t S = target / base;
     if (S > t.max_split) S = t.max_split;
     const uint32_t by_tiles = (ntiles + t.min_tiles - 1) / t.min_tiles;
@@ -982,13 +1052,15 @@ size_t prefill_workspace_bound(uint32_t B, uint32_t max_end, uint32_t n_heads, u
     uint32_t pack, n_rb, gmax;
     uint64_t base, target;
     split_shape(B, n_heads, n_kv, D, pack, n_rb, gmax, base, target);
-    const uint32_t ntiles = (max_end - 1) / BN + 1;
+    const uint32_t ntiles = (max_end - 1) / bn_of((int)D) + 1;
     uint64_t S = target / base;
     if (S > t.max_split) S = t.max_split;
     const uint32_t by_tiles = (ntiles + t.min_tiles - 1) / t.min_tiles;
     if (S > by_tiles) S = by_tiles;
     return split_bytes((uint32_t)(S < 1 ? 1 : S), B, n_heads, D);
 }
+
+uint32_t prefill_tile_keys(uint32_t D) { return (uint32_t)bn_of((int)D); }
 
 void prefill_bind_workspace(PrefillArgs& a, void* workspace)
 {

@@ -109,6 +109,8 @@ size_t prefill_plan(PrefillArgs& a);
 // B <= max_end (the split count does not grow with pos_start beyond a bound).
 size_t prefill_workspace_bound(uint32_t B, uint32_t max_end, uint32_t n_heads, uint32_t n_kv, uint32_t D);
 void prefill_bind_workspace(PrefillArgs& a, void* workspace);
+// keys per tile of the prefill kernels at head_dim D (the unit of split_tiles)
+uint32_t prefill_tile_keys(uint32_t D);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st);
 
 // ---- rope.hip ----
