@@ -290,15 +290,23 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
     // flight (into one parity) never alias its LDS reads (of the other) and
     // does not wait for them; each thread waits for its own loads before the
     // barrier that ends the step.
+    //
+    // Pair mode keeps three buffers of each (K three tiles ahead, V two), so
+    // that every tile load has two steps to land: its steps are short (16
+    // MFMAs per wave) and all eight waves meet at each step's barrier.
+    constexpr int NB = PAIR ? 3 : 2;  // K buffers and V buffers
     __shared__ __attribute__((aligned(16))) _Float16 Kl0[NG][BN * D];
     __shared__ __attribute__((aligned(16))) _Float16 Kl1[NG][BN * D];
+    __shared__ __attribute__((aligned(16))) _Float16 Kl2[NB > 2 ? BN * D : 8];
     __shared__ __attribute__((aligned(16))) _Float16 Vl0[NG][D * BN];
     __shared__ __attribute__((aligned(16))) _Float16 Vl1[NG][D * BN];
-    // (max, sum) of group 1's queries for the two-group merge
-    __shared__ float s_ml[NG > 1 ? 512 : 1];
-    // pair mode: each wave's partial scores of a tile, by tile parity, as
-    // [parity][wave][float4 j][lane] (consecutive lanes, consecutive 16 bytes)
-    __shared__ f32x4 Xl[PAIR ? 2 * 8 * 4 * NS * 64 : 1];
+    __shared__ __attribute__((aligned(16))) _Float16 Vl2[NB > 2 ? D * BN : 8];
+    // Pair mode: each wave's partial scores of a tile, by tile parity, as
+    // [parity][wave][float4 j][lane] (consecutive lanes, consecutive 16
+    // bytes).  Two key groups: (max, sum) of group 1's queries for the merge.
+    // (One array: pair mode fills the 160 KB of LDS exactly.)
+    __shared__ f32x4 Xl[PAIR ? 2 * 8 * 4 * NS * 64 : NG > 1 ? 128 : 1];
+    float* const s_ml = reinterpret_cast<float*>(&Xl[0]);
 
     // Items (query block, head) in heaviest-first order are dealt to the
     // resident workgroups in snake order (item slot it*W + j on even rounds,
@@ -363,7 +371,7 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
     // stores.  With a gate the epilogue loads the gate values, which would
     // then wait behind these loads; such items issue their loads at their
     // own start.
-    const bool early = a.gate == nullptr;
+    const bool early = a.gate == nullptr && !PAIR;
     PItem cur;
     if (!item_of(0, cur)) return;  // uniform over the workgroup
     for (uint32_t it = 0;; ++it) {
@@ -373,7 +381,9 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
         int tid;
         asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
         const int lane = tid & 63;
-        const int grp = tid / LT, gtid = tid % LT, wave = gtid >> 6;
+        // with one key group the group is a constant, so the LDS tile bases are
+        // too and fold into the reads' offset fields
+        const int grp = NG > 1 ? tid / LT : 0, gtid = NG > 1 ? tid % LT : tid, wave = gtid >> 6;
         // the wave's 32 queries (qw) and, in pair mode, its half of the dimensions (hf)
         const int qw = PAIR ? wave >> 1 : wave, hf = PAIR ? wave & 1 : 0;
         const int r32 = lane & 31, hh = lane >> 5;
@@ -396,8 +406,8 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
         }
         const int ksw = chunk_swz<KCH>(r32), vsw = chunk_swz<VCH>(r32);
         // buffers by parity (a constant at every call after inlining)
-        auto kbuf = [&](int par) { return par ? &Kl1[grp][0] : &Kl0[grp][0]; };
-        auto vbuf = [&](int par) { return par ? &Vl1[grp][0] : &Vl0[grp][0]; };
+        auto kbuf = [&](int par) { return par == 0 ? &Kl0[grp][0] : par == 1 ? &Kl1[grp][0] : &Kl2[0]; };
+        auto vbuf = [&](int par) { return par == 0 ? &Vl0[grp][0] : par == 1 ? &Vl1[grp][0] : &Vl2[0]; };
         // Buffer resources over a kv head's K rows and V tiles.  A tile adds
         // the scalar offset kt*BN*D*2 bytes (the same for K rows and two
         // 32-position V tiles); every tile lies inside the cache (kv_stride is a
@@ -421,6 +431,13 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
             for (int i = 0; i < CH; ++i) lds_load16(r, vbuf(par) + (LT * i + 64 * wave) * 8, vgo[i], kt * BN * D * 2);
         };
         auto dma_done = [] { __builtin_amdgcn_s_waitcnt(0x0f70); };  // vmcnt(0): this thread's loads landed
+        // all but this thread's last n tile loads landed (n of 0, CH or 2 CH:
+        // an immediate; memory loads retire in order)
+        auto dma_wait_but = [](uint32_t n) {
+            if (n >= 2 * CH) __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * CH));
+            else if (n >= CH) __builtin_amdgcn_s_waitcnt(0x0f70 | CH);
+            else __builtin_amdgcn_s_waitcnt(0x0f70);
+        };
         f16x8 qf[NKK];
         // the first loads of an item, see above: the K tiles, the first V
         // tile and the queries
@@ -449,11 +466,21 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
             uint32_t t0;
             if (item_steps(I, t0) > 0) dma_v_of(rsrc_v(I.kvh), 0, t0 + grp);
         };
+        // pair mode, after the first loads: K(2) and V(1); returns their count
+        auto issue_item_deep = [&](const PItem& I) -> uint32_t {
+            uint32_t t0;
+            const uint32_t n = item_steps(I, t0);
+            if (n > 2) dma_k_of(rsrc_k(I.kvh), 2, t0 + 2);
+            if (n > 1) dma_v_of(rsrc_v(I.kvh), 1, t0 + 1);
+            return (n > 2 ? CH : 0) + (n > 1 ? CH : 0);
+        };
+        uint32_t deep_loads = 0;  // loads the prologue need not wait for
         if (it == 0 || !early) {
             if (it > 0) __syncthreads();  // the previous item's epilogue read LDS these loads overwrite
             issue_item_k(cur);
             issue_item_v(cur);
             issue_item_q(cur);
+            if constexpr (NB > 2) deep_loads = issue_item_deep(cur);
         }
 
         const uint32_t kvh = cur.kvh;
@@ -648,29 +675,33 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
         // prologue: this item's first loads are in flight (issued above or at the
         // end of the previous item); f32 and bf16 queries are loaded and
         // converted here.  All loads are complete before the key loop, whose
-        // waits then count only tile loads.
-        dma_done();
+        // waits then count only tile loads (in pair mode K(2) and V(1) may
+        // still be in flight; the first step waits for them).
+        dma_wait_but(deep_loads);
         if (a.q_dtype != kF16) {
             const size_t qbase = (size_t)myrow.b * a.q_stride + (size_t)myrow.h * D + hf * DQ + hh * 8;
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, qbase + kk * 16, a.q_dtype);
-            dma_done();
+            if (NB == 2) dma_done();
         }
-        __syncthreads();
+        if constexpr (NB > 2) lds_barrier();
+        else __syncthreads();
         f32x16 Sa[NS], Sb[NS];
         if (wsteps > 0) {
             qk(Sa, 0);
             xwrite(Sa, 0);
         }
-        // step 0 loads K(2) over K(0), whose last readers are the scores above
-        __syncthreads();
+        // step 0 loads K(NB) over K(0), whose last readers are the scores above
+        if constexpr (NB > 2) lds_barrier();
+        else __syncthreads();
 
-        // step st (parity p = st % 2): loads K(st+2) into K buffer p (it held
-        // K(st), last read by the previous step's scores) and V(st+1) into V
-        // buffer 1-p (it held V(st-1)); scores of st+1 (K buffer 1-p) overlap the
-        // softmax of st; P.V of st (V buffer p); one barrier.  With pos_start
-        // not a multiple of 32 a wave's queries straddle a tile boundary, so a
-        // tile with a successor may still need the mask.
+        // step st (buffer phase ph = st % NB, score parity sp = st % 2): loads
+        // K(st+NB) into K buffer ph (it held K(st), last read by the previous
+        // step's scores) and V(st+NB-1) into V buffer (ph+NB-1) % NB (it held
+        // V(st-1)); scores of st+1 (K buffer (ph+1) % NB) overlap the softmax
+        // of st; P.V of st (V buffer ph); one barrier.  With pos_start not a
+        // multiple of 32 a wave's queries straddle a tile boundary, so a tile
+        // with a successor may still need the mask.
         // the step that reads the tile holding kmax (the item's last tile, unless
         // a later split owns it), in this group's buffers
         const bool has_tail = ntiles > 0 && t0 + ntiles == kmax / BN + 1 && (kmax + 1) % BN != 0;
@@ -680,40 +711,63 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
         // the group's last step (or, for a group without tiles, the first) issues
         // the next item's loads
         const uint32_t last_st = gsteps > 0 ? gsteps - 1 : 0;
-        auto step = [&](int p, uint32_t st, f32x16 (&Scur)[NS], f32x16 (&Snext)[NS]) {
-            if (st + 2 < gsteps) dma_k(p, st + 2);
-            if (st + 1 < gsteps) dma_v(1 - p, st + 1);
+        auto step = [&](int ph, int sp, uint32_t st, f32x16 (&Scur)[NS], f32x16 (&Snext)[NS]) {
+            const bool lk = st + NB < gsteps, lv = st + NB - 1 < gsteps;
+            if (lk) dma_k(ph, st + NB);
+            if (lv) dma_v((ph + NB - 1) % NB, st + NB - 1);
             if (prefetch && st == last_st) {
                 // K buffers are free (no scores follow), V buffer 1-p too
                 issue_item_k(nxt);
-                if (p == 1 || gsteps == 0) issue_item_v(nxt);
+                if (ph == 1 || gsteps == 0) issue_item_v(nxt);
             }
             if (has_tail && st == tail_step) {  // workgroup-uniform
-                if (grp == tail_grp) zero_v_tail(p, st);
+                if (grp == tail_grp) zero_v_tail(ph, st);
                 lds_barrier();
             }
             if (st + 1 < wsteps) {
-                xadd(Scur, p);
+                xadd(Scur, sp);
                 mask(Scur, st);
                 update_max(Scur);
-                qk_pv(Snext, 1 - p, Scur, p);
-                xwrite(Snext, 1 - p);
+                qk_pv(Snext, (ph + 1) % NB, Scur, ph);
+                xwrite(Snext, 1 - sp);
             } else if (st < wsteps) {
-                xadd(Scur, p);
+                xadd(Scur, sp);
                 mask(Scur, st);
                 update_max(Scur);
                 f16x8 pf[NKC];
                 probs(Scur, pf);
-                pv(pf, p);
+                pv(pf, ph);
             }
-            // this step's own loads (none from the group's last step on, whose
-            // next-item loads are waited for by the next item)
-            if (!(prefetch && st >= last_st)) dma_done();
+            if constexpr (NB > 2) {
+                // the previous steps' loads (this step's have two steps to land)
+                dma_wait_but((lk ? CH : 0) + (lv ? CH : 0));
+            } else {
+                // this step's own loads (none from the group's last step on, whose
+                // next-item loads are waited for by the next item)
+                if (!(prefetch && st >= last_st)) dma_done();
+            }
             lds_barrier();
         };
-        for (uint32_t st = 0; st < nsteps; st += 2) {
-            step(0, st, Sa, Sb);
-            if (st + 1 < nsteps) step(1, st + 1, Sb, Sa);
+        if constexpr (NB == 2) {
+            for (uint32_t st = 0; st < nsteps; st += 2) {
+                step(0, 0, st, Sa, Sb);
+                if (st + 1 < nsteps) step(1, 1, st + 1, Sb, Sa);
+            }
+        } else {
+            // buffer phase period 3, score parity period 2
+            for (uint32_t st = 0; st < nsteps; st += 6) {
+                step(0, 0, st, Sa, Sb);
+                if (st + 1 >= nsteps) break;
+                step(1, 1, st + 1, Sb, Sa);
+                if (st + 2 >= nsteps) break;
+                step(2, 0, st + 2, Sa, Sb);
+                if (st + 3 >= nsteps) break;
+                step(0, 1, st + 3, Sb, Sa);
+                if (st + 4 >= nsteps) break;
+                step(1, 0, st + 4, Sa, Sb);
+                if (st + 5 >= nsteps) break;
+                step(2, 1, st + 5, Sb, Sa);
+            }
         }
 
         // the next item's first V tile when the last step still read V buffer 0,
@@ -732,7 +786,7 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
         // ones of the item's start need not stay live through the key loop.
         int tid_e;
         asm volatile("v_mov_b32 %0, %1" : "=v"(tid_e) : "v"((int)threadIdx.x));
-        const int gtid_e = tid_e % LT, lane_e = tid_e & 63;
+        const int gtid_e = NG > 1 ? tid_e % LT : tid_e, lane_e = tid_e & 63;
         const int qw_e = PAIR ? gtid_e >> 7 : gtid_e >> 6, hf_e = PAIR ? (gtid_e >> 6) & 1 : 0;
         if constexpr (NG > 1) {
             // Group 1 hands (m, l, O) to group 0 through LDS: m, l in s_ml and O
@@ -774,7 +828,7 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
             }
         }
         const PRow rw = row_of<SPLIT>(a, cur, qw_e * 32 + (lane_e & 31));
-        if (tid_e / LT == 0 && rw.valid) {  // group 1 handed its part over
+        if ((NG == 1 || tid_e / LT == 0) && rw.valid) {  // group 1 handed its part over
             if (SPLIT && a.n_split > 1) {
                 // split partials: (max, sum) and the unnormalised O of this
                 // row over this split's keys
