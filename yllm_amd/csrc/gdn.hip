@@ -234,24 +234,53 @@ __device__ inline f32x4 mfma_f32(float a, float b, const f32x4& c)
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Split-bf16 products (the chain kernel): x = hi + lo with hi = bf16(x) and
+// lo = bf16(x - hi), each rounded to nearest even, so |x - hi - lo| <=
+// 2^-18 |x|; a.b is taken as hi.hi + hi.lo + lo.hi (the dropped lo.lo and
+// the splits leave ~2^-16 of each product) with fp32 accumulation, on the
+// bf16 MFMA at 16x the rate of the fp32 one.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+__device__ inline void split_bf16(const float (&x)[8], bf16x8& hi, bf16x8& lo)
+{
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        hi[j] = (__bf16)x[j];
+        lo[j] = (__bf16)(x[j] - (float)hi[j]);
+    }
+}
+__device__ inline f32x4 mfma_x3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh, const bf16x8& bl, f32x4 c)
+{
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+}
+
 template <int D>
 struct ChunkWs {
-    // per (v-head, chunk): [W; Q~] [2kC][D] (token rows), K~^T [D][kC], P [kC][kC],
-    // U^T [D][kC] (the chain kernel overwrites it with Delta^T), gamma_last (+3 pad),
-    // Mc [D][D] (the state at the chunk's start, rows j)
+    // per (v-head, chunk):
+    //   Wb  [kC * D]  -W as bf16 hi / lo pairs in the chain kernel's register
+    //                 order: the 16 bytes ((w * D/32 + s) * 2 + hl) * 64 + l hold
+    //                 part hl (0 hi, 1 lo) of -W[16w + l%16][(l/16) D/4 + 8s .. +7]
+    //   Q   [kC][D]   Q~ rows (tokens)
+    //   Kb  [kC * D]  K~ likewise: the 16 bytes ((b * 2 + s) * 2 + hl) * 64 + l
+    //                 hold part hl of K~[16 (l/16) + 8s .. +7][16b + l%16]
+    //   P   [kC][kC], U^T [D][kC] (the chain kernel overwrites it with Delta^T),
+    //   gamma_last (+3 pad), Mc [D][D] (the state at the chunk's start, rows j)
     static constexpr size_t floats =
         (size_t)2 * kC * D + (size_t)kC * D + (size_t)kC * kC + (size_t)kC * D + 4 + (size_t)D * D;
-    float* WQ;
-    float* Kt;
+    float* Wb;
+    float* Q;
+    float* Kb;
     float* P;
     float* U;
     float* gl;
     float* Mc;
     __device__ ChunkWs(float* ws, uint32_t h, uint32_t c, uint32_t n_chunks)
     {
-        WQ = ws + ((size_t)h * n_chunks + c) * floats;
-        Kt = WQ + 2 * kC * D;
-        P = Kt + kC * D;
+        Wb = ws + ((size_t)h * n_chunks + c) * floats;
+        Q = Wb + kC * D;
+        Kb = Q + kC * D;
+        P = Kb + kC * D;
         U = P + kC * kC;
         gl = U + kC * D;
         Mc = gl + 4;
@@ -339,18 +368,24 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
     }
     __syncthreads();
 
-    // Q~ = diag(gamma) Q (rows kC..2kC-1 of [W; Q~]) and K~^T = (diag(e) K)^T
-    // (d_k rows of kC tokens: the chain kernel's operand loads are then 16
-    // contiguous bytes per lane)
+    // Q~ = diag(gamma) Q (token rows), and K~ = diag(e) K as bf16 hi / lo in
+    // the chain kernel's register order (ChunkWs)
     for (int e = tid; e < kC * D / 4; e += 256) {
         const int t = e / (D / 4), i = (e % (D / 4)) * 4;
         const f32x4 q = *reinterpret_cast<const f32x4*>(&Qn[t][i]);
-        *reinterpret_cast<f32x4*>(w.WQ + (size_t)(kC + t) * D + i) = q * sgam[t];
-        const int ik = e / (kC / 4), t4 = (e % (kC / 4)) * 4;
-        f32x4 kt;
+        *reinterpret_cast<f32x4*>(w.Q + (size_t)t * D + i) = q * sgam[t];
+    }
+    for (int e = tid; e < (D / 16) * 2 * 64; e += 256) {
+        const int l = e % 64, bs = e / 64, sk = bs % 2, b = bs / 2;
+        const int tk = 16 * (l >> 4) + 8 * sk, ik = 16 * b + (l & 15);
+        float x[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) kt[u] = Kn[t4 + u][ik] * see[t4 + u];
-        *reinterpret_cast<f32x4*>(w.Kt + (size_t)ik * kC + t4) = kt;
+        for (int u = 0; u < 8; ++u) x[u] = Kn[tk + u][ik] * see[tk + u];
+        bf16x8 hi, lo;
+        split_bf16(x, hi, lo);
+        bf16x8* dst = reinterpret_cast<bf16x8*>(w.Kb) + (size_t)bs * 128 + l;
+        dst[0] = hi;
+        dst[64] = lo;
     }
 
     // Gram matrices K K^T and Q K^T over the ten 16x16 tiles (tb, sb) with
@@ -411,9 +446,9 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
 
     // forward substitution (I + A) X = [diag(beta) V | diag(beta*gamma) K],
     // one right-hand-side column per thread, X kept in registers
+    const int col = tid;
+    float X[kC];
     if (tid < 2 * D) {
-        const int col = tid;
-        float X[kC];
         // rows past the last token have beta = 0, so their (clamped, valid)
         // V rows contribute nothing
         if (col < D) {
@@ -449,56 +484,66 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
 #pragma unroll
             for (int t = 0; t < kC; t += 4)
                 *reinterpret_cast<f32x4*>(w.U + (size_t)col * kC + t) = f32x4{X[t], X[t + 1], X[t + 2], X[t + 3]};
-        } else {
-#pragma unroll
-            for (int t = 0; t < kC; ++t) w.WQ[(size_t)t * D + (col - D)] = X[t];
         }
+    }
+    // -W through LDS (the rows of A are dead once every column is solved)
+    __syncthreads();
+    if (tid < 2 * D && col >= D) {
+#pragma unroll
+        for (int t = 0; t < kC; ++t) QA[t * KP + (col - D)] = -X[t];
+    }
+    __syncthreads();
+    // -W as bf16 hi / lo in the chain kernel's register order (ChunkWs)
+    for (int e = tid; e < 4 * (D / 32) * 64; e += 256) {
+        const int l = e % 64, ws_ = e / 64, sk = ws_ % (D / 32), wt = ws_ / (D / 32);
+        const float* src = QA + (16 * wt + (l & 15)) * KP + (l >> 4) * (D / 4) + 8 * sk;
+        float x[8];
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(src), x1 = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            x[u] = x0[u];
+            x[u + 4] = x1[u];
+        }
+        bf16x8 hi, lo;
+        split_bf16(x, hi, lo);
+        bf16x8* dst = reinterpret_cast<bf16x8*>(w.Wb) + (size_t)ws_ * 128 + l;
+        dst[0] = hi;
+        dst[64] = lo;
     }
 }
 
 // The recurrence across chunks, state only: per chunk, Delta = U - W M^T
 // and M <- gamma_last M + Delta^T K~ (the output is formed afterwards, all
-// chunks at once, by gdn_out_kernel).  A workgroup owns J = 16 state rows
-// (d_v indices j0..j0+15) of one head in LDS and walks the chunks in order;
-// it records each chunk's starting state (Mc) and Delta^T (in place of U^T)
-// for the output pass.
+// chunks at once, by gdn_out_kernel).  A workgroup of four waves owns J = 16
+// state rows (d_v indices j0..j0+15) of one head and walks the chunks in
+// order; it records each chunk's starting state (Mc) and Delta^T (in place
+// of U^T) for the output pass.
 //
-// Waves 0-3 compute, waves 4-7 stage every operand through LDS (the compute
-// waves issue no loads in the chunk loop): at the start of chunk c the
-// stagers write chunk c+1's W rows, K~^T rows, U^T slice and gamma_last
-// (~68 KB at d = 128, loaded into their registers during chunk c-1) into the
-// LDS buffer of parity c+1, record the chunk's starting state and issue half
-// of chunk c+2's loads, the other half after the first barrier.  Every
-// workgroup of a head needs the head's whole W and K~ for its 16 columns, so
-// a CU moves ~68 KB per chunk whatever the slice width, and a CU's memory
-// pipeline (~30-45 GB/s measured for such loads) rather than the MFMA sets
-// the pace: ~2.4 us per chunk.  (With every wave loading its own register
-// operands at the start of a chunk, phase A waited ~1.4 us for the loads to
-// issue: 3.2 us per chunk.)
-// Per chunk: phase A, compute wave w (row block w of W, d_k split over the
-// four lane groups) forms Delta rows 16w..16w+15; phase B, compute wave w
-// updates d_k blocks w, w+4 of the slice.  The barriers order LDS only (the
-// stagers' loads stay in flight across them).
+// Every operand element of a chunk is read by exactly one wave, so each wave
+// loads its own straight into registers, two chunks ahead (three register
+// sets): phase A, wave w forms the Delta tile of tokens 16w..16w+15 from -W
+// rows (its A operand), the U^T slice (the accumulator's start) and the state
+// rows in LDS (B); phase B, wave w updates the state tiles of d_k blocks
+// w D/64 .. (kept in its registers in fp32) from Delta^T in LDS (A) and K~
+// (B).  Only the state slice and the Delta tile pass through LDS, as bf16
+// hi / lo pairs; two barriers per chunk.  The products are split-bf16
+// (mfma_x3: three bf16 MFMAs per product, fp32 accumulation; the state and
+// Delta themselves stay fp32): per-chunk timestamps put the fp32-MFMA form
+// of this kernel at ~1 us of MFMA in a ~2 us chunk.  The prep kernel writes
+// -W and K~ already split, in the order the lanes read them (ChunkWs).
 template <int D>
-__global__ __launch_bounds__(512) void gdn_chain_kernel(GdnArgs a)
+__global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 {
-    constexpr int J = 16;       // state rows (d_v indices) per workgroup
-    constexpr int KQ = D / 4;   // d_k indices per lane group in phase A
-    constexpr int NCB = D / 16; // 16-wide d_k blocks of phase B
-    constexpr int MP = D + 4, WP = D + 4, KP = kC + 4;
-    constexpr int NW4 = kC * D / 4 / 256;  // float4s of W (and of K~^T) per stager thread
-    static_assert(J * kC / 4 <= 256, "one U^T float4 per stager thread");
-    __shared__ float Ml[J][MP];
-    __shared__ float Dl[kC][J + 1];
-    __shared__ float Wl[2][kC][WP];
-    __shared__ float Kl[2][D][KP];
-    __shared__ float Ul[2][J][KP];
-    __shared__ float Gl[2];
+    constexpr int J = 16;          // state rows (d_v indices) per workgroup
+    constexpr int NSA = D / 32;    // phase A k-steps (d_k, 8 per lane group each)
+    constexpr int NBW = D / 64;    // phase B: 16-wide d_k blocks per wave
+    static_assert(kC == 64 && D % 64 == 0, "four token tiles and four waves of d_k blocks");
+    constexpr int MP = D + 8, DP = kC + 8;  // bf16 row strides (16-byte rows, staggered banks)
+    __shared__ __attribute__((aligned(16))) __bf16 Mh[J][MP], Mlo[J][MP];   // the state slice, rows j
+    __shared__ __attribute__((aligned(16))) __bf16 Dh[J][DP], Dlo[J][DP];   // Delta^T of the chunk, rows j
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;  // 8 waves
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const bool stager = wave >= 4;
-    const int st = tid - 256;  // stager thread index
     // workgroup b = slice * n_v + h: consecutive workgroups go to different
     // XCDs, so the slices of one head (b mod 8 fixed when n_v is a multiple
     // of 8) share an L2 and read the head's chunk data once
@@ -506,140 +551,141 @@ __global__ __launch_bounds__(512) void gdn_chain_kernel(GdnArgs a)
     float* S = a.S + ((size_t)h * D + j0) * D;
     const uint32_t nlast = a.n_chunks - 1;
 
-    struct Stage {
-        f32x4 w[NW4], k[NW4];  // a stager's share of one chunk's W and K~^T
-        f32x4 u;               // ... of its U^T slice
+    // one chunk's register operands of this wave
+    struct Ops {
+        bf16x8 w[NSA][2];     // -W[16 wave + r][g D/4 + 8s .. +7], hi and lo
+        f32x4 u;              // U^T[j0 + r][16 wave + 4g .. +3]
+        bf16x8 k[NBW][2][2];  // K~[16g + 8s .. +7][16 (NBW wave + bb) + r], hi and lo
         float gl;
     };
-    // the first half of a chunk's loads (W rows, U^T slice, gamma_last), then the second (K~^T rows)
-    auto stage_load0 = [&](Stage& sg, uint32_t c) {
+    // the loads of one register set in two halves (-W and U; K~ and gamma_last)
+    auto load_a = [&](Ops& o, uint32_t c) {
         ChunkWs<D> w(a.ws, h, c, a.n_chunks);
+        const bf16x8* wb = reinterpret_cast<const bf16x8*>(w.Wb);
 #pragma unroll
-        for (int u = 0; u < NW4; ++u)
-            sg.w[u] = *reinterpret_cast<const f32x4*>(w.WQ + (size_t)(st + 256 * u) * 4);  // kC x D
-        const int ju = st / (kC / 4), tu = (st % (kC / 4)) * 4;
-        if (st < J * kC / 4) sg.u = *reinterpret_cast<const f32x4*>(w.U + (size_t)(j0 + ju) * kC + tu);
-        sg.gl = w.gl[0];
+        for (int sk = 0; sk < NSA; ++sk)
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl) o.w[sk][hl] = wb[((size_t)(wave * NSA + sk) * 2 + hl) * 64 + lane];
+        o.u = *reinterpret_cast<const f32x4*>(w.U + (size_t)(j0 + r) * kC + 16 * wave + 4 * g);
     };
-    auto stage_load1 = [&](Stage& sg, uint32_t c) {
+    auto load_b = [&](Ops& o, uint32_t c) {
         ChunkWs<D> w(a.ws, h, c, a.n_chunks);
+        const bf16x8* kb = reinterpret_cast<const bf16x8*>(w.Kb);
 #pragma unroll
-        for (int u = 0; u < NW4; ++u)
-            sg.k[u] = *reinterpret_cast<const f32x4*>(w.Kt + (size_t)(st + 256 * u) * 4);  // D x kC
-    };
-    auto stage_store = [&](const Stage& sg, int p) {
+        for (int bb = 0; bb < NBW; ++bb)
 #pragma unroll
-        for (int u = 0; u < NW4; ++u) {
-            const int e = st + 256 * u;
-            const int tw = e / (D / 4), iw = (e % (D / 4)) * 4;
-            *reinterpret_cast<f32x4*>(&Wl[p][tw][iw]) = sg.w[u];
-            const int ik = e / (kC / 4), tk = (e % (kC / 4)) * 4;
-            *reinterpret_cast<f32x4*>(&Kl[p][ik][tk]) = sg.k[u];
-        }
-        const int ju = st / (kC / 4), tu = (st % (kC / 4)) * 4;
-        if (st < J * kC / 4) *reinterpret_cast<f32x4*>(&Ul[p][ju][tu]) = sg.u;
-        if (st == 0) Gl[p] = sg.gl;
+            for (int sk = 0; sk < 2; ++sk)
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl)
+                    o.k[bb][sk][hl] = kb[((size_t)((NBW * wave + bb) * 2 + sk) * 2 + hl) * 64 + lane];
+        o.gl = w.gl[0];
     };
-
-    for (int e = tid; e < J * D / 4; e += 512) {
-        const int jj = e / (D / 4), i = (e % (D / 4)) * 4;
-        *reinterpret_cast<f32x4*>(&Ml[jj][i]) = *reinterpret_cast<const f32x4*>(S + (size_t)jj * D + i);
-    }
-    Stage sa, sb;  // a stager's register sets of even and odd chunks
-    if (stager) {
-        stage_load0(sa, 0);
-        stage_load1(sa, 0);
-        stage_store(sa, 0);
-        stage_load0(sb, min(1u, nlast));
-        stage_load1(sb, min(1u, nlast));
-    }
-    // everything of chunks 0 and 1 is complete before the loop (otherwise the
-    // compiler's wait insertion, merging the loop entry with the back edge,
-    // waits inside the loop for loads issued just before)
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    auto load = [&](Ops& o, uint32_t c) {
+        load_a(o, c);
+        load_b(o, c);
+    };
+    // the state tiles of this wave in fp32: mt[bb][e] = M[j0 + 4g + e][16 (NBW wave + bb) + r]
+    f32x4 mt[NBW];
+    auto put_state = [&] {
+#pragma unroll
+        for (int bb = 0; bb < NBW; ++bb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = 16 * (NBW * wave + bb) + r;
+                const __bf16 hi = (__bf16)mt[bb][e];
+                Mh[4 * g + e][i] = hi;
+                Mlo[4 * g + e][i] = (__bf16)(mt[bb][e] - (float)hi);
+            }
+    };
+#pragma unroll
+    for (int bb = 0; bb < NBW; ++bb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mt[bb][e] = S[(size_t)(4 * g + e) * D + 16 * (NBW * wave + bb) + r];
+    put_state();
+    Ops oa, ob, oc;  // chunks c, c+1, c+2 of a round of three
+    load(oa, 0);
+    load(ob, min(1u, nlast));
     __syncthreads();
 
-    // one chunk; `next` holds chunk c+1's operands, `fill` receives chunk c+2's
-    auto chunk = [&](uint32_t c, int p, const Stage& next, Stage& fill) {
+    // One chunk with operand set o; the loads of the set for chunk cf go out
+    // in between the MFMAs (the -W half in phase A, the K~ half in phase B):
+    // a wave that issued its 17 loads in one burst waited for the CU's
+    // memory pipeline instead of issuing MFMAs.
+    auto chunk = [&](uint32_t c, const Ops& o, Ops& of, uint32_t cf) {
         ChunkWs<D> w(a.ws, h, c, a.n_chunks);
-        if (stager) {
-            stage_store(next, p ^ 1);
-            // the chunk's starting state, for the output pass (before phase B rewrites Ml)
-            for (int e = st; e < J * D / 4; e += 256) {
-                const int jj = e / (D / 4), i = (e % (D / 4)) * 4;
-                *reinterpret_cast<f32x4*>(w.Mc + (size_t)(j0 + jj) * D + i) =
-                    *reinterpret_cast<const f32x4*>(&Ml[jj][i]);
+        // phase A: Delta rows 16 wave + 4g + e, column j0 + r = U - W M^T
+        {
+            f32x4 acc = o.u;
+            bf16x8 bh[NSA], bl[NSA];
+#pragma unroll
+            for (int sk = 0; sk < NSA; ++sk) {
+                bh[sk] = *reinterpret_cast<const bf16x8*>(&Mh[r][g * (D / 4) + 8 * sk]);
+                bl[sk] = *reinterpret_cast<const bf16x8*>(&Mlo[r][g * (D / 4) + 8 * sk]);
             }
-            stage_load0(fill, min(c + 2, nlast));
-        } else {
-            // phase A: Delta rows 16w..16w+15 = U - W M^T (lane (g, r) supplies
-            // M[j0 + r][g*KQ .. g*KQ+KQ-1] as the B operand)
-            f32x4 acc[4];
+            load_a(of, cf);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int sk = 0; sk < NSA; ++sk) acc = mfma_x3(o.w[sk][0], o.w[sk][1], bh[sk], bl[sk], acc);
 #pragma unroll
-            for (int i = 0; i < KQ / 4; ++i) {
-                const f32x4 wa = *reinterpret_cast<const f32x4*>(&Wl[p][16 * wave + r][g * KQ + 4 * i]);
-                const f32x4 mb = *reinterpret_cast<const f32x4*>(&Ml[r][g * KQ + 4 * i]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[e] = mfma_f32(wa[e], mb[e], acc[e]);
+            for (int k = 0; k < 3 * NSA; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
             }
-            const f32x4 x = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-            const f32x4 u = *reinterpret_cast<const f32x4*>(&Ul[p][r][16 * wave + 4 * g]);
-            const f32x4 dl = u - x;  // Delta[16 wave + 4g + i][j0 + r]
+            typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+            bf16x4 dh, dl;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) Dl[16 * wave + 4 * g + i][r] = dl[i];
-            *reinterpret_cast<f32x4*>(w.U + (size_t)(j0 + r) * kC + 16 * wave + 4 * g) = dl;
+            for (int e = 0; e < 4; ++e) {
+                dh[e] = (__bf16)acc[e];
+                dl[e] = (__bf16)(acc[e] - (float)dh[e]);
+            }
+            *reinterpret_cast<bf16x4*>(&Dh[r][16 * wave + 4 * g]) = dh;
+            *reinterpret_cast<bf16x4*>(&Dlo[r][16 * wave + 4 * g]) = dl;
+            *reinterpret_cast<f32x4*>(w.U + (size_t)(j0 + r) * kC + 16 * wave + 4 * g) = acc;
         }
         lds_barrier();
-        if (stager) {
-            stage_load1(fill, min(c + 2, nlast));
-        } else {
-            // phase B: M <- gamma_last M + Delta^T K~ for d_k blocks wave, wave+4, ...;
-            // a wave reads and writes only its own columns of Ml
-            const float gl = Gl[p];
-            constexpr int NB = NCB / 4;
-            f32x4 acc[NB][2];
+        // phase B: M <- gamma_last M + Delta^T K~ on this wave's d_k blocks;
+        // the chunk's starting state goes to Mc first
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const int cb = wave + 4 * b;
+        for (int bb = 0; bb < NBW; ++bb) {
+            const int i = 16 * (NBW * wave + bb) + r;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[b][0][i] = gl * Ml[4 * g + i][16 * cb + r];
-                acc[b][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-            for (int k4 = 0; k4 < 4; ++k4) {
-                f32x4 kb4[NB];
-#pragma unroll
-                for (int b = 0; b < NB; ++b)
-                    kb4[b] = *reinterpret_cast<const f32x4*>(&Kl[p][16 * (wave + 4 * b) + r][16 * g + 4 * k4]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float da = Dl[16 * g + 4 * k4 + e][r];
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[b][e & 1] = mfma_f32(da, kb4[b][e], acc[b][e & 1]);
-                }
-            }
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const f32x4 nm = acc[b][0] + acc[b][1];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) Ml[4 * g + i][16 * (wave + 4 * b) + r] = nm[i];
-            }
+            for (int e = 0; e < 4; ++e) w.Mc[(size_t)(j0 + 4 * g + e) * D + i] = mt[bb][e];
         }
+        bf16x8 ah[2], al[2];
+#pragma unroll
+        for (int sk = 0; sk < 2; ++sk) {
+            ah[sk] = *reinterpret_cast<const bf16x8*>(&Dh[r][16 * g + 8 * sk]);
+            al[sk] = *reinterpret_cast<const bf16x8*>(&Dlo[r][16 * g + 8 * sk]);
+        }
+        load_b(of, cf);
+#pragma unroll
+        for (int bb = 0; bb < NBW; ++bb) {
+            f32x4 acc = mt[bb] * o.gl;
+#pragma unroll
+            for (int sk = 0; sk < 2; ++sk) acc = mfma_x3(ah[sk], al[sk], o.k[bb][sk][0], o.k[bb][sk][1], acc);
+            mt[bb] = acc;
+        }
+#pragma unroll
+        for (int k = 0; k < 6 * NBW; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+        }
+        put_state();
         lds_barrier();
     };
-    for (uint32_t c = 0;; c += 2) {
-        chunk(c, 0, sb, sa);
+    // chunk c's operands are in a register set loaded two chunks before
+    for (uint32_t c = 0;; c += 3) {
+        chunk(c, oa, oc, min(c + 2, nlast));
         if (c + 1 > nlast) break;
-        chunk(c + 1, 1, sa, sb);
+        chunk(c + 1, ob, oa, min(c + 3, nlast));
         if (c + 2 > nlast) break;
+        chunk(c + 2, oc, ob, min(c + 4, nlast));
+        if (c + 3 > nlast) break;
     }
 
-    for (int e = tid; e < J * D / 4; e += 512) {
-        const int jj = e / (D / 4), i = (e % (D / 4)) * 4;
-        *reinterpret_cast<f32x4*>(S + (size_t)jj * D + i) = *reinterpret_cast<const f32x4*>(&Ml[jj][i]);
-    }
+#pragma unroll
+    for (int bb = 0; bb < NBW; ++bb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[(size_t)(4 * g + e) * D + 16 * (NBW * wave + bb) + r] = mt[bb][e];
 }
 
 // The chunk outputs, all chunks at once: O = (Q~ Mc^T + P Delta) / sqrt(d)
@@ -680,7 +726,7 @@ __global__ __launch_bounds__(512, 2) void gdn_out_kernel(GdnArgs a)
     // Q~ (rows kC..2kC-1 of [W; Q~]) and P into LDS
     for (int e = tid; e < kC * D / 4; e += 512) {
         const int t = e / (D / 4), i = (e % (D / 4)) * 4;
-        *reinterpret_cast<f32x4*>(&Ql[t][i]) = *reinterpret_cast<const f32x4*>(w.WQ + (size_t)(kC + t) * D + i);
+        *reinterpret_cast<f32x4*>(&Ql[t][i]) = *reinterpret_cast<const f32x4*>(w.Q + (size_t)t * D + i);
     }
     for (int e = tid; e < kC * kC / 4; e += 512) {
         const int t = e / (kC / 4), i = (e % (kC / 4)) * 4;
@@ -812,7 +858,7 @@ hipError_t launch_gdn_d(const GdnArgs& a, hipStream_t st)
         hipLaunchKernelGGL(gdn_step_kernel<D>, dim3(a.n_v * (D / 16)), dim3(256), 0, st, a);
     } else if (a.ws) {
         hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(a.n_chunks, a.n_v), dim3(256), 0, st, a);
-        hipLaunchKernelGGL(gdn_chain_kernel<D>, dim3(a.n_v * (D / 16)), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(gdn_chain_kernel<D>, dim3(a.n_v * (D / 16)), dim3(256), 0, st, a);
         hipLaunchKernelGGL(gdn_out_kernel<D>, dim3(a.n_chunks, a.n_v), dim3(512), 0, st, a);
     } else {
         hipLaunchKernelGGL(gdn_kernel<D>, dim3(a.n_v * (D / kCols)), dim3(256), 0, st, a);
