@@ -689,20 +689,23 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 }
 
 // The chunk outputs, all chunks at once: O = (Q~ Mc^T + P Delta) / sqrt(d)
-// for one (chunk, v head) per workgroup.  Q~ and P are staged in LDS; wave w
-// owns output columns (d_v) 16*(w % NJT).. and token row blocks of its
-// share, with its Mc rows and Delta^T rows as register operands (16-byte
-// loads).  fp32 MFMA, fp32 accumulation.
+// for one (chunk, v head) per workgroup.  Q~ and P are staged in LDS as bf16
+// hi / lo pairs (each element split once, read by every wave); wave w owns
+// output columns (d_v) 16*(w % NJT).. and token row blocks of its share,
+// with its Mc rows and Delta^T rows as register operands (16-byte loads,
+// split in registers).  Split-bf16 products (mfma_x3) with fp32
+// accumulation, as the chain kernel.
 template <int D>
 __global__ __launch_bounds__(512, 2) void gdn_out_kernel(GdnArgs a)
 {
     constexpr int KQ = D / 4;      // d_k indices per lane group
+    constexpr int NSQ = KQ / 8;    // k-steps of 8 per lane group over d_k
     constexpr int NJT = D / 16;    // 16-column output tiles
     constexpr int WPT = 8 / NJT;   // waves per column tile (1 at D = 128, 2 at 64)
     constexpr int RBW = 4 / WPT;   // 16-token row blocks per wave
-    constexpr int QP = D + 4, PP = kC + 4;
-    __shared__ float Ql[kC][QP];
-    __shared__ float Pl[kC][PP];
+    constexpr int QP = D + 8, PP = kC + 8;  // bf16 row strides
+    __shared__ __attribute__((aligned(16))) __bf16 Qh[kC][QP], Qlo[kC][QP];
+    __shared__ __attribute__((aligned(16))) __bf16 Ph[kC][PP], Plo[kC][PP];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -723,39 +726,62 @@ __global__ __launch_bounds__(512, 2) void gdn_out_kernel(GdnArgs a)
 #pragma unroll
         for (int i = 0; i < 4; ++i) db[i] = *reinterpret_cast<const f32x4*>(drow + 4 * i);
     }
-    // Q~ (rows kC..2kC-1 of [W; Q~]) and P into LDS
-    for (int e = tid; e < kC * D / 4; e += 512) {
-        const int t = e / (D / 4), i = (e % (D / 4)) * 4;
-        *reinterpret_cast<f32x4*>(&Ql[t][i]) = *reinterpret_cast<const f32x4*>(w.Q + (size_t)t * D + i);
+    // Q~ and P into LDS, split
+    for (int e = tid; e < kC * D / 8; e += 512) {
+        const int t = e / (D / 8), i = (e % (D / 8)) * 8;
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(w.Q + (size_t)t * D + i);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(w.Q + (size_t)t * D + i + 4);
+        float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        bf16x8 hi, lo;
+        split_bf16(x, hi, lo);
+        *reinterpret_cast<bf16x8*>(&Qh[t][i]) = hi;
+        *reinterpret_cast<bf16x8*>(&Qlo[t][i]) = lo;
     }
-    for (int e = tid; e < kC * kC / 4; e += 512) {
-        const int t = e / (kC / 4), i = (e % (kC / 4)) * 4;
-        *reinterpret_cast<f32x4*>(&Pl[t][i]) = *reinterpret_cast<const f32x4*>(w.P + (size_t)t * kC + i);
+    for (int e = tid; e < kC * kC / 8; e += 512) {
+        const int t = e / (kC / 8), i = (e % (kC / 8)) * 8;
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(w.P + (size_t)t * kC + i);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(w.P + (size_t)t * kC + i + 4);
+        float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        bf16x8 hi, lo;
+        split_bf16(x, hi, lo);
+        *reinterpret_cast<bf16x8*>(&Ph[t][i]) = hi;
+        *reinterpret_cast<bf16x8*>(&Plo[t][i]) = lo;
+    }
+    // the register operands split: B of Q~ Mc^T (d_k g KQ + 8s .. +7) and of
+    // P Delta (tokens 16g + 8s .. +7)
+    bf16x8 mh[NSQ], ml[NSQ], dh[2], dl[2];
+#pragma unroll
+    for (int sk = 0; sk < NSQ; ++sk) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = mb[2 * sk + u / 4][u % 4];
+        split_bf16(x, mh[sk], ml[sk]);
+    }
+#pragma unroll
+    for (int sk = 0; sk < 2; ++sk) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = db[2 * sk + u / 4][u % 4];
+        split_bf16(x, dh[sk], dl[sk]);
     }
     __syncthreads();
 
     const float scale = 1.0f / sqrtf((float)D);
 #pragma unroll
     for (int rr = 0; rr < RBW; ++rr) {
-        const int rb = rb0 + rr;
-        f32x4 acc[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int rb = rb0 + rr, tr = 16 * rb + r;
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
         // Q~ Mc^T: contraction over d_k, lane group g its KQ indices
 #pragma unroll
-        for (int i = 0; i < KQ / 4; ++i) {
-            const f32x4 qa = *reinterpret_cast<const f32x4*>(&Ql[16 * rb + r][g * KQ + 4 * i]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = mfma_f32(qa[e], mb[i][e], acc[e]);
-        }
+        for (int sk = 0; sk < NSQ; ++sk)
+            acc = mfma_x3(*reinterpret_cast<const bf16x8*>(&Qh[tr][g * KQ + 8 * sk]),
+                          *reinterpret_cast<const bf16x8*>(&Qlo[tr][g * KQ + 8 * sk]), mh[sk], ml[sk], acc);
         // P Delta: contraction over the chunk's tokens, lane group g tokens 16g..16g+15
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f32x4 pa = *reinterpret_cast<const f32x4*>(&Pl[16 * rb + r][16 * g + 4 * i]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = mfma_f32(pa[e], db[i][e], acc[e]);
-        }
-        const f32x4 o = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * scale;
+        for (int sk = 0; sk < 2; ++sk)
+            acc = mfma_x3(*reinterpret_cast<const bf16x8*>(&Ph[tr][16 * g + 8 * sk]),
+                          *reinterpret_cast<const bf16x8*>(&Plo[tr][16 * g + 8 * sk]), dh[sk], dl[sk], acc);
+        const f32x4 o = acc * scale;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = 16 * rb + 4 * g + i;
