@@ -225,8 +225,10 @@ __global__ __launch_bounds__(256, 1) void gdn_kernel(GdnArgs a)
 // M <- gamma_last M + Delta^T K~), recording each chunk's starting state and
 // Delta; gdn_out_kernel then forms O = Q~ Mc^T + P Delta for every chunk at
 // once.  Only the chain is sequential, and it carries 256 of the 448 MFMAs
-// per chunk and slice that a single walking kernel did.  All products are
-// fp32 MFMA (v_mfma_f32_16x16x4_f32) with fp32 accumulation.
+// per chunk and slice that a single walking kernel did.  The prep's Gram
+// products are fp32 MFMA (v_mfma_f32_16x16x4_f32); the chain's and the
+// output's are split bf16 (mfma_x3 below); every accumulation, stored value
+// and the state are fp32.
 constexpr int kC = 64;  // tokens per chunk of the chunked form
 
 __device__ inline f32x4 mfma_f32(float a, float b, const f32x4& c)
