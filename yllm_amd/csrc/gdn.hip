@@ -227,8 +227,8 @@ __global__ __launch_bounds__(256, 1) void gdn_kernel(GdnArgs a)
 // once.  Only the chain is sequential, and it carries 256 of the 448 MFMAs
 // per chunk and slice that a single walking kernel did.  The prep's Gram
 // products are fp32 MFMA (v_mfma_f32_16x16x4_f32); the chain's and the
-// output's are split bf16 (mfma_x3 below); every accumulation, stored value
-// and the state are fp32.
+// output's are split bf16 (mfma_x3 below; -W rounded to bf16); every
+// accumulation, stored value and the state are fp32.
 constexpr int kC = 64;  // tokens per chunk of the chunked form
 
 __device__ inline f32x4 mfma_f32(float a, float b, const f32x4& c)
@@ -260,16 +260,16 @@ __device__ inline f32x4 mfma_x3(const bf16x8& ah, const bf16x8& al, const bf16x8
 template <int D>
 struct ChunkWs {
     // per (v-head, chunk):
-    //   Wb  [kC * D]  -W as bf16 hi / lo pairs in the chain kernel's register
-    //                 order: the 16 bytes ((w * D/32 + s) * 2 + hl) * 64 + l hold
-    //                 part hl (0 hi, 1 lo) of -W[16w + l%16][(l/16) D/4 + 8s .. +7]
+    //   Wb  [kC * D / 2]  -W rounded to bf16 in the chain kernel's register
+    //                 order: the 16 bytes (w * D/32 + s) * 64 + l hold
+    //                 -W[16w + l%16][(l/16) D/4 + 8s .. +7]
     //   Q   [kC][D]   Q~ rows (tokens)
     //   Kb  [kC * D]  K~ likewise: the 16 bytes ((b * 2 + s) * 2 + hl) * 64 + l
     //                 hold part hl of K~[16 (l/16) + 8s .. +7][16b + l%16]
     //   P   [kC][kC], U^T [D][kC] (the chain kernel overwrites it with Delta^T),
     //   gamma_last (+3 pad), Mc [D][D] (the state at the chunk's start, rows j)
     static constexpr size_t floats =
-        (size_t)2 * kC * D + (size_t)kC * D + (size_t)kC * kC + (size_t)kC * D + 4 + (size_t)D * D;
+        (size_t)kC * D / 2 + (size_t)2 * kC * D + (size_t)kC * kC + (size_t)kC * D + 4 + (size_t)D * D;
     float* Wb;
     float* Q;
     float* Kb;
@@ -280,7 +280,7 @@ struct ChunkWs {
     __device__ ChunkWs(float* ws, uint32_t h, uint32_t c, uint32_t n_chunks)
     {
         Wb = ws + ((size_t)h * n_chunks + c) * floats;
-        Q = Wb + kC * D;
+        Q = Wb + kC * D / 2;
         Kb = Q + kC * D;
         P = Kb + kC * D;
         U = P + kC * kC;
@@ -446,56 +446,104 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
     }
     __syncthreads();
 
-    // forward substitution (I + A) X = [diag(beta) V | diag(beta*gamma) K],
-    // one right-hand-side column per thread, X kept in registers
-    const int col = tid;
-    float X[kC];
-    if (tid < 2 * D) {
-        // rows past the last token have beta = 0, so their (clamped, valid)
-        // V rows contribute nothing
-        if (col < D) {
-            const float* vp = a.v + (size_t)h * D + col;
+    // Forward substitution (I + A) X = [diag(beta) V | diag(beta*gamma) K]
+    // in 16-row blocks on fp32 MFMA: X_i = T_ii (B_i - sum_{j<i} A_ij X_j),
+    // T_ii = (I + A_ii)^-1.  The four T_ii come first, by substitution
+    // (threads 0..63: column tid % 16 of block tid / 16), and replace the
+    // diagonal blocks of A.  Wave w then owns the 16-column tiles w, w + 4,
+    // ... of X as MFMA accumulators (lane (g, r): rows 4g .. 4g+3 of each
+    // block, column r); in the products the contraction over the 16 rows of
+    // X_j runs in the order the accumulators hold them (step e takes row
+    // 4g + e from lane group g, against A_ij[m][4g + e]), so X stays in
+    // registers.  The column-per-thread substitution this replaces read
+    // every A row through LDS in every thread (11.5 us of a ~32 us
+    // workgroup).
+    constexpr int CTW = 2 * D / 64;  // 16-column tiles per wave
+    {
+        const int bi = tid >> 4, cc = tid & 15;
+        float tc[16];
+        if (tid < 64) {
 #pragma unroll
-            for (int t = 0; t < kC; ++t) X[t] = vp[(size_t)(t0 + min(t, nt - 1)) * a.v_stride];
+            for (int m = 0; m < 16; ++m) {
+                float acc = m == cc ? 1.0f : 0.0f;
 #pragma unroll
-            for (int t = 0; t < kC; ++t) X[t] *= sb[t];
-        } else {
-#pragma unroll
-            for (int t = 0; t < kC; ++t) X[t] = sb[t] * sgam[t] * Kn[t][col - D];
-        }
-        // row t of A is read (broadcast) one row ahead of its use
-        f32x4 cur[kC / 4], nxt[kC / 4];
-#pragma unroll
-        for (int s4 = 0; s4 < kC / 4; ++s4) cur[s4] = *reinterpret_cast<const f32x4*>(&Am[1][4 * s4]);
-#pragma unroll
-        for (int t = 1; t < kC; ++t) {
-            if (t + 1 < kC) {
-#pragma unroll
-                for (int s4 = 0; s4 < kC / 4; ++s4)
-                    if (4 * s4 < t + 1) nxt[s4] = *reinterpret_cast<const f32x4*>(&Am[t + 1][4 * s4]);
+                for (int k = 0; k < m; ++k) acc = fmaf(-Am[16 * bi + m][16 * bi + k], tc[k], acc);
+                tc[m] = acc;
             }
-            float acc[4] = {X[t], 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < t; ++s) acc[s & 3] = fmaf(-cur[s >> 2][s & 3], X[s], acc[s & 3]);
-            X[t] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-#pragma unroll
-            for (int s4 = 0; s4 < kC / 4; ++s4) cur[s4] = nxt[s4];
         }
-        if (col < D) {
-            // U^T row col: kC contiguous floats
+        __syncthreads();
+        if (tid < 64) {
 #pragma unroll
-            for (int t = 0; t < kC; t += 4)
-                *reinterpret_cast<f32x4*>(w.U + (size_t)col * kC + t) = f32x4{X[t], X[t + 1], X[t + 2], X[t + 3]};
+            for (int m = 0; m < 16; ++m) Am[16 * bi + m][16 * bi + cc] = tc[m];
         }
     }
-    // -W through LDS (the rows of A are dead once every column is solved)
-    __syncthreads();
-    if (tid < 2 * D && col >= D) {
+    // right-hand sides: tiles ct < CTW / 2 are V columns (tile w + 4 ct < D / 16
+    // for every wave), the rest K columns; rows past the last token have
+    // beta = 0, so their (clamped, valid) V rows contribute nothing
+    f32x4 X[CTW][4];
+    {
+        const float* vp = a.v + (size_t)h * D;
 #pragma unroll
-        for (int t = 0; t < kC; ++t) QA[t * KP + (col - D)] = -X[t];
+        for (int ct = 0; ct < CTW / 2; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = 16 * i + 4 * g + e;
+                    X[ct][i][e] = vp[(size_t)(t0 + min(t, nt - 1)) * a.v_stride + 16 * (wave + 4 * ct) + r];
+                }
+#pragma unroll
+        for (int ct = CTW / 2; ct < CTW; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = 16 * i + 4 * g + e;
+                    X[ct][i][e] = sgam[t] * Kn[t][16 * (wave + 4 * ct) + r - D];
+                }
+#pragma unroll
+        for (int ct = 0; ct < CTW; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) X[ct][i][e] *= sb[16 * i + 4 * g + e];
     }
+    __syncthreads();  // T_ii in place
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < i; ++j) {
+            const f32x4 av = *reinterpret_cast<const f32x4*>(&Am[16 * i + r][16 * j + 4 * g]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ct = 0; ct < CTW; ++ct) X[ct][i] = mfma_f32(-av[e], X[ct][j][e], X[ct][i]);
+        }
+        const f32x4 tv = *reinterpret_cast<const f32x4*>(&Am[16 * i + r][16 * i + 4 * g]);
+#pragma unroll
+        for (int ct = 0; ct < CTW; ++ct) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = mfma_f32(tv[e], X[ct][i][e], acc);
+            X[ct][i] = acc;
+        }
+    }
+    // U^T rows (the V columns): four consecutive tokens per lane
+#pragma unroll
+    for (int ct = 0; ct < CTW / 2; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<f32x4*>(w.U + (size_t)(16 * (wave + 4 * ct) + r) * kC + 16 * i + 4 * g) = X[ct][i];
+    // -W through LDS (A is dead once every wave has read it)
     __syncthreads();
-    // -W as bf16 hi / lo in the chain kernel's register order (ChunkWs)
+#pragma unroll
+    for (int ct = CTW / 2; ct < CTW; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) QA[(16 * i + 4 * g + e) * KP + 16 * (wave + 4 * ct) + r - D] = -X[ct][i][e];
+    __syncthreads();
+    // -W as bf16 in the chain kernel's register order (ChunkWs)
     for (int e = tid; e < 4 * (D / 32) * 64; e += 256) {
         const int l = e % 64, ws_ = e / 64, sk = ws_ % (D / 32), wt = ws_ / (D / 32);
         const float* src = QA + (16 * wt + (l & 15)) * KP + (l >> 4) * (D / 4) + 8 * sk;
@@ -506,11 +554,10 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
             x[u] = x0[u];
             x[u + 4] = x1[u];
         }
-        bf16x8 hi, lo;
-        split_bf16(x, hi, lo);
-        bf16x8* dst = reinterpret_cast<bf16x8*>(w.Wb) + (size_t)ws_ * 128 + l;
-        dst[0] = hi;
-        dst[64] = lo;
+        bf16x8 hi;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) hi[u] = (__bf16)x[u];
+        reinterpret_cast<bf16x8*>(w.Wb)[(size_t)ws_ * 64 + l] = hi;
     }
 }
 
@@ -530,9 +577,14 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
 // (B).  Only the state slice and the Delta tile pass through LDS, as bf16
 // hi / lo pairs; two barriers per chunk.  The products are split-bf16
 // (mfma_x3: three bf16 MFMAs per product, fp32 accumulation; the state and
-// Delta themselves stay fp32): per-chunk timestamps put the fp32-MFMA form
-// of this kernel at ~1 us of MFMA in a ~2 us chunk.  The prep kernel writes
-// -W and K~ already split, in the order the lanes read them (ChunkWs).
+// Delta themselves stay fp32), except that -W enters rounded to bf16 (W M^T
+// as W.Mhi + W.Mlo): an error in W M^T only perturbs the prediction the
+// delta rule subtracts, which the following tokens correct, so its rounding
+// shows in the outputs at ~1e-5 relative (K~ feeds the state directly and
+// keeps both parts), and it halves the bytes of -W each chunk moves.
+// Per-chunk timestamps put the fp32-MFMA form of this kernel at ~1 us of
+// MFMA in a ~2 us chunk.  The prep kernel writes -W and K~ in the order the
+// lanes read them (ChunkWs).
 template <int D>
 __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 {
@@ -555,7 +607,7 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 
     // one chunk's register operands of this wave
     struct Ops {
-        bf16x8 w[NSA][2];     // -W[16 wave + r][g D/4 + 8s .. +7], hi and lo
+        bf16x8 w[NSA];        // -W[16 wave + r][g D/4 + 8s .. +7] (bf16)
         f32x4 u;              // U^T[j0 + r][16 wave + 4g .. +3]
         bf16x8 k[NBW][2][2];  // K~[16g + 8s .. +7][16 (NBW wave + bb) + r], hi and lo
         float gl;
@@ -565,9 +617,7 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
         ChunkWs<D> w(a.ws, h, c, a.n_chunks);
         const bf16x8* wb = reinterpret_cast<const bf16x8*>(w.Wb);
 #pragma unroll
-        for (int sk = 0; sk < NSA; ++sk)
-#pragma unroll
-            for (int hl = 0; hl < 2; ++hl) o.w[sk][hl] = wb[((size_t)(wave * NSA + sk) * 2 + hl) * 64 + lane];
+        for (int sk = 0; sk < NSA; ++sk) o.w[sk] = wb[(size_t)(wave * NSA + sk) * 64 + lane];
         o.u = *reinterpret_cast<const f32x4*>(w.U + (size_t)(j0 + r) * kC + 16 * wave + 4 * g);
     };
     auto load_b = [&](Ops& o, uint32_t c) {
@@ -626,9 +676,12 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
             }
             load_a(of, cf);
 #pragma unroll
-            for (int sk = 0; sk < NSA; ++sk) acc = mfma_x3(o.w[sk][0], o.w[sk][1], bh[sk], bl[sk], acc);
+            for (int sk = 0; sk < NSA; ++sk) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.w[sk], bl[sk], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.w[sk], bh[sk], acc, 0, 0, 0);
+            }
 #pragma unroll
-            for (int k = 0; k < 3 * NSA; ++k) {
+            for (int k = 0; k < 2 * NSA; ++k) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
             }
