@@ -788,47 +788,64 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
         asm volatile("v_mov_b32 %0, %1" : "=v"(tid_e) : "v"((int)threadIdx.x));
         const int gtid_e = NG > 1 ? tid_e % LT : tid_e, lane_e = tid_e & 63;
         const int qw_e = PAIR ? gtid_e >> 7 : gtid_e >> 6, hf_e = PAIR ? (gtid_e >> 6) & 1 : 0;
+        int b_lo = 0, b_hi = NDB;  // the O blocks this thread stores
         if constexpr (NG > 1) {
-            // Group 1 hands (m, l, O) to group 0 through LDS: m, l in s_ml and O
+            // The two groups' (m, l, O) meet through LDS: m, l in s_ml and O
             // through V buffer 1 of both groups (the one buffer the next item's
-            // first loads leave free; 32 KB at d = 128), half the blocks at a time.
+            // first loads leave free; 32 KB at d = 128), half the blocks at a
+            // time.  Group 1 hands over blocks 0 .. HB-1, which group 0 merges
+            // and stores; then group 0 hands over blocks HB .., which group 1
+            // merges and stores, so both groups issue half of the output.
             constexpr int HB = NDB / 2;  // O blocks per round
             static_assert(HB * 16 * 256 * 4 <= (int)sizeof(Vl1), "merge area");
             float* oarea = reinterpret_cast<float*>(&Vl1[0][0]);
             if (grp == 1) {
                 s_ml[gtid_e] = m;
                 s_ml[256 + gtid_e] = l;
+#pragma unroll
+                for (int b = 0; b < HB; ++b)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oarea[(b * 16 + i) * 256 + gtid_e] = o[b][i];
             }
-            float a0 = 1.0f, a1 = 0.0f;
+            lds_barrier();
+            float mo = m, lo = l;  // the other group's (m, l)
+            auto merge_half = [&](int r) {
+                const float mg = fmaxf(m, mo);
+                const float cs = fast_exp2(m - mg), co = fast_exp2(mo - mg);
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                if (grp == 1) {
+                for (int b = 0; b < HB; ++b)
 #pragma unroll
-                    for (int b = 0; b < HB; ++b)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) oarea[(b * 16 + i) * 256 + gtid_e] = o[r * HB + b][i];
-                }
-                lds_barrier();
-                if (grp == 0) {
-                    if (r == 0) {
-                        const float m1 = s_ml[gtid_e], l1 = s_ml[256 + gtid_e];
-                        const float mg = fmaxf(m, m1);
-                        a0 = fast_exp2(m - mg);
-                        a1 = fast_exp2(m1 - mg);
-                        m = mg;
-                        l = l * a0 + l1 * a1;
-                    }
-#pragma unroll
-                    for (int b = 0; b < HB; ++b)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i)
-                            o[r * HB + b][i] = o[r * HB + b][i] * a0 + oarea[(b * 16 + i) * 256 + gtid_e] * a1;
-                }
-                if (r == 0) lds_barrier();  // round 0 read before round 1 overwrites
+                    for (int i = 0; i < 16; ++i)
+                        o[r * HB + b][i] = o[r * HB + b][i] * cs + oarea[(b * 16 + i) * 256 + gtid_e] * co;
+            };
+            if (grp == 0) {
+                mo = s_ml[gtid_e];
+                lo = s_ml[256 + gtid_e];
+                merge_half(0);
             }
+            lds_barrier();  // round 0 read before round 1 overwrites
+            if (grp == 0) {
+                s_ml[gtid_e] = m;
+                s_ml[256 + gtid_e] = l;
+#pragma unroll
+                for (int b = 0; b < HB; ++b)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oarea[(b * 16 + i) * 256 + gtid_e] = o[HB + b][i];
+            }
+            lds_barrier();
+            if (grp == 1) {
+                mo = s_ml[gtid_e];
+                lo = s_ml[256 + gtid_e];
+                merge_half(1);
+            }
+            const float mg = fmaxf(m, mo);
+            l = l * fast_exp2(m - mg) + lo * fast_exp2(mo - mg);
+            m = mg;
+            b_lo = grp * HB;
+            b_hi = b_lo + HB;
         }
         const PRow rw = row_of<SPLIT>(a, cur, qw_e * 32 + (lane_e & 31));
-        if ((NG == 1 || tid_e / LT == 0) && rw.valid) {  // group 1 handed its part over
+        if (rw.valid) {
             if (SPLIT && a.n_split > 1) {
                 // split partials: (max, sum) and the unnormalised O of this
                 // row over this split's keys
@@ -838,7 +855,8 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
                     *reinterpret_cast<f32x2*>(a.part_ml + 2 * pr) = f32x2{m, l};
                 }
 #pragma unroll
-                for (int b = 0; b < NDB; ++b)
+                for (int b = 0; b < NDB; ++b) {
+                    if (b < b_lo || b >= b_hi) continue;
 #pragma unroll
                     for (int i4 = 0; i4 < 4; ++i4) {
                         const uint32_t d = hf_e * DQ + b * 32 + 8 * i4 + 4 * (lane_e >> 5);
@@ -847,10 +865,12 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
                         for (int e = 0; e < 4; ++e) v[e] = o[b][4 * i4 + e];
                         *reinterpret_cast<f32x4*>(a.part_o + pr * D + d) = v;
                     }
+                }
             } else {
                 const float inv = 1.0f / l;
 #pragma unroll
                 for (int b = 0; b < NDB; ++b) {
+                    if (b < b_lo || b >= b_hi) continue;
 #pragma unroll
                     for (int i4 = 0; i4 < 4; ++i4) {
                         const uint32_t d = hf_e * DQ + b * 32 + 8 * i4 + 4 * (lane_e >> 5);
