@@ -266,8 +266,15 @@ struct ChunkWs {
     //   Q   [kC][D]   Q~ rows (tokens)
     //   Kb  [kC * D]  K~ likewise: the 16 bytes ((b * 2 + s) * 2 + hl) * 64 + l
     //                 hold part hl of K~[16 (l/16) + 8s .. +7][16b + l%16]
-    //   P   [kC][kC], U^T [D][kC] (the chain kernel overwrites it with Delta^T),
-    //   gamma_last (+3 pad), Mc [D][D] (the state at the chunk's start, rows j)
+    //   P   [kC][kC], U^T [D][kC] (the chain kernel overwrites the 4 KB of
+    //                 rows 16jt .. 16jt+15 with Delta^T's as bf16 hi / lo in the
+    //                 output kernel's register order: the 16 bytes
+    //                 ((jt * 2 + s) * 2 + hl) * 64 + l hold part hl of
+    //                 Delta^T[16jt + l%16][16 (l/16) + 8s .. +7]),
+    //   gamma_last (+3 pad), Mc [D*D] (the state at the chunk's start as bf16
+    //                 hi / lo in the output kernel's register order: the 16
+    //                 bytes ((jt * D/32 + s) * 2 + hl) * 64 + l hold part hl of
+    //                 M[16jt + l%16][(l/16) D/4 + 8s .. +7])
     static constexpr size_t floats =
         (size_t)kC * D / 2 + (size_t)2 * kC * D + (size_t)kC * kC + (size_t)kC * D + 4 + (size_t)D * D;
     float* Wb;
@@ -566,7 +573,10 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
 // chunks at once, by gdn_out_kernel).  A workgroup of four waves owns J = 16
 // state rows (d_v indices j0..j0+15) of one head and walks the chunks in
 // order; it records each chunk's starting state (Mc) and Delta^T (in place
-// of U^T) for the output pass.
+// of U^T) for the output pass, both as the bf16 hi / lo operands its waves
+// read from LDS anyway, 16 bytes per lane in the output kernel's register
+// order (stored as fp32 rows, four bytes per lane and row, the records cost
+// ~24 of the chain's ~80 us at 4096 tokens x 16 heads).
 //
 // Every operand element of a chunk is read by exactly one wave, so each wave
 // loads its own straight into registers, two chunks ahead (three register
@@ -596,12 +606,12 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
     __shared__ __attribute__((aligned(16))) __bf16 Mh[J][MP], Mlo[J][MP];   // the state slice, rows j
     __shared__ __attribute__((aligned(16))) __bf16 Dh[J][DP], Dlo[J][DP];   // Delta^T of the chunk, rows j
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, g = lane >> 4;
     // workgroup b = slice * n_v + h: consecutive workgroups go to different
     // XCDs, so the slices of one head (b mod 8 fixed when n_v is a multiple
     // of 8) share an L2 and read the head's chunk data once
-    const uint32_t h = blockIdx.x % a.n_v, j0 = (blockIdx.x / a.n_v) * J;
+    const uint32_t h = blockIdx.x % a.n_v, jt = blockIdx.x / a.n_v, j0 = jt * J;
     float* S = a.S + ((size_t)h * D + j0) * D;
     const uint32_t nlast = a.n_chunks - 1;
 
@@ -685,6 +695,20 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
             }
+            // the chunk's starting state for the output kernel: the split
+            // operands every wave read above, NSA / 2 of the 2 NSA (k-step,
+            // part) pieces per wave, picked by selects, stored after the
+            // MFMAs that read them (stored before them, the wave waited for
+            // every operand read before its first MFMA)
+#pragma unroll
+            for (int q = 0; q < NSA / 2; ++q) {
+                const int idx = wave * (NSA / 2) + q;
+                bf16x8 v = bh[0];
+#pragma unroll
+                for (int cc = 1; cc < 2 * NSA; ++cc)
+                    if (cc == idx) v = (cc & 1) ? bl[cc >> 1] : bh[cc >> 1];
+                reinterpret_cast<bf16x8*>(w.Mc)[(size_t)(jt * NSA * 2 + idx) * 64 + lane] = v;
+            }
             typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
             bf16x4 dh, dl;
 #pragma unroll
@@ -694,17 +718,9 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
             }
             *reinterpret_cast<bf16x4*>(&Dh[r][16 * wave + 4 * g]) = dh;
             *reinterpret_cast<bf16x4*>(&Dlo[r][16 * wave + 4 * g]) = dl;
-            *reinterpret_cast<f32x4*>(w.U + (size_t)(j0 + r) * kC + 16 * wave + 4 * g) = acc;
         }
         lds_barrier();
-        // phase B: M <- gamma_last M + Delta^T K~ on this wave's d_k blocks;
-        // the chunk's starting state goes to Mc first
-#pragma unroll
-        for (int bb = 0; bb < NBW; ++bb) {
-            const int i = 16 * (NBW * wave + bb) + r;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w.Mc[(size_t)(j0 + 4 * g + e) * D + i] = mt[bb][e];
-        }
+        // phase B: M <- gamma_last M + Delta^T K~ on this wave's d_k blocks
         bf16x8 ah[2], al[2];
 #pragma unroll
         for (int sk = 0; sk < 2; ++sk) {
@@ -724,17 +740,34 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
         }
+        // Delta^T for the output kernel (in place of this slice's U^T rows):
+        // the split operands every wave read above, (k-step, part) piece
+        // `wave` by wave `wave`
+        {
+            bf16x8 v = ah[0];
+#pragma unroll
+            for (int cc = 1; cc < 4; ++cc)
+                if (cc == wave) v = (cc & 1) ? al[cc >> 1] : ah[cc >> 1];
+            reinterpret_cast<bf16x8*>(w.U)[(size_t)(jt * 4 + wave) * 64 + lane] = v;
+        }
         put_state();
         lds_barrier();
     };
-    // chunk c's operands are in a register set loaded two chunks before
-    for (uint32_t c = 0;; c += 3) {
+    // chunk c's operands are in a register set loaded two chunks before.
+    // Whole rounds of three chunks in a loop without exits in between, the
+    // rest after it: with an exit test after every chunk the compiler's
+    // waits for the register sets at the loop head covered every load in
+    // flight (vmcnt(1)), once per round.
+    const uint32_t rounds = a.n_chunks / 3;
+    uint32_t c = 0;
+    for (uint32_t rd = 0; rd < rounds; ++rd, c += 3) {
         chunk(c, oa, oc, min(c + 2, nlast));
-        if (c + 1 > nlast) break;
         chunk(c + 1, ob, oa, min(c + 3, nlast));
-        if (c + 2 > nlast) break;
         chunk(c + 2, oc, ob, min(c + 4, nlast));
-        if (c + 3 > nlast) break;
+    }
+    if (c <= nlast) {
+        chunk(c, oa, oc, min(c + 2, nlast));
+        if (c + 1 <= nlast) chunk(c + 1, ob, oa, min(c + 3, nlast));
     }
 
 #pragma unroll
@@ -747,9 +780,9 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 // for one (chunk, v head) per workgroup.  Q~ and P are staged in LDS as bf16
 // hi / lo pairs (each element split once, read by every wave); wave w owns
 // output columns (d_v) 16*(w % NJT).. and token row blocks of its share,
-// with its Mc rows and Delta^T rows as register operands (16-byte loads,
-// split in registers).  Split-bf16 products (mfma_x3) with fp32
-// accumulation, as the chain kernel.
+// with its Mc rows and Delta^T rows as register operands (16-byte loads of
+// the chain kernel's split records).  Split-bf16 products (mfma_x3) with
+// fp32 accumulation, as the chain kernel.
 template <int D>
 __global__ __launch_bounds__(512, 2) void gdn_out_kernel(GdnArgs a)
 {
@@ -770,16 +803,23 @@ __global__ __launch_bounds__(512, 2) void gdn_out_kernel(GdnArgs a)
     const int jt = wave % NJT, rb0 = (wave / NJT) * RBW;
     ChunkWs<D> w(a.ws, h, c, a.n_chunks);
 
-    // register operands: Mc rows 16 jt + r (d_k range of lane group g) and
-    // Delta^T rows 16 jt + r (tokens 16g .. 16g+15); issued first
-    f32x4 mb[KQ / 4], db[4];
+    // register operands, written split by the chain kernel: B of Q~ Mc^T
+    // (Mc rows 16 jt + r, d_k g KQ + 8s .. +7) and of P Delta (Delta^T rows
+    // 16 jt + r, tokens 16g + 8s .. +7); issued first
+    bf16x8 mh[NSQ], ml[NSQ], dh[2], dl[2];
     {
-        const float* mrow = w.Mc + (size_t)(16 * jt + r) * D + g * KQ;
+        const bf16x8* mc = reinterpret_cast<const bf16x8*>(w.Mc) + (size_t)(jt * NSQ * 2) * 64 + lane;
 #pragma unroll
-        for (int i = 0; i < KQ / 4; ++i) mb[i] = *reinterpret_cast<const f32x4*>(mrow + 4 * i);
-        const float* drow = w.U + (size_t)(16 * jt + r) * kC + 16 * g;
+        for (int sk = 0; sk < NSQ; ++sk) {
+            mh[sk] = mc[(2 * sk) * 64];
+            ml[sk] = mc[(2 * sk + 1) * 64];
+        }
+        const bf16x8* dt = reinterpret_cast<const bf16x8*>(w.U) + (size_t)(jt * 4) * 64 + lane;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) db[i] = *reinterpret_cast<const f32x4*>(drow + 4 * i);
+        for (int sk = 0; sk < 2; ++sk) {
+            dh[sk] = dt[(2 * sk) * 64];
+            dl[sk] = dt[(2 * sk + 1) * 64];
+        }
     }
     // Q~ and P into LDS, split
     for (int e = tid; e < kC * D / 8; e += 512) {
@@ -801,23 +841,6 @@ __global__ __launch_bounds__(512, 2) void gdn_out_kernel(GdnArgs a)
         split_bf16(x, hi, lo);
         *reinterpret_cast<bf16x8*>(&Ph[t][i]) = hi;
         *reinterpret_cast<bf16x8*>(&Plo[t][i]) = lo;
-    }
-    // the register operands split: B of Q~ Mc^T (d_k g KQ + 8s .. +7) and of
-    // P Delta (tokens 16g + 8s .. +7)
-    bf16x8 mh[NSQ], ml[NSQ], dh[2], dl[2];
-#pragma unroll
-    for (int sk = 0; sk < NSQ; ++sk) {
-        float x[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = mb[2 * sk + u / 4][u % 4];
-        split_bf16(x, mh[sk], ml[sk]);
-    }
-#pragma unroll
-    for (int sk = 0; sk < 2; ++sk) {
-        float x[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = db[2 * sk + u / 4][u % 4];
-        split_bf16(x, dh[sk], dl[sk]);
     }
     __syncthreads();
 
