@@ -576,7 +576,9 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
 // of U^T) for the output pass, both as the bf16 hi / lo operands its waves
 // read from LDS anyway, 16 bytes per lane in the output kernel's register
 // order (stored as fp32 rows, four bytes per lane and row, the records cost
-// ~24 of the chain's ~80 us at 4096 tokens x 16 heads).
+// ~24 of the chain's ~80 us at 4096 tokens x 16 heads).  The records are
+// stored non-temporally: through the L2 they evicted the operand lines the
+// head's slices share (chain 70 -> 63 us, output pass 30 -> 33 us).
 //
 // Every operand element of a chunk is read by exactly one wave, so each wave
 // loads its own straight into registers, two chunks ahead (three register
@@ -707,7 +709,7 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 #pragma unroll
                 for (int cc = 1; cc < 2 * NSA; ++cc)
                     if (cc == idx) v = (cc & 1) ? bl[cc >> 1] : bh[cc >> 1];
-                reinterpret_cast<bf16x8*>(w.Mc)[(size_t)(jt * NSA * 2 + idx) * 64 + lane] = v;
+                __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(w.Mc) + (size_t)(jt * NSA * 2 + idx) * 64 + lane);
             }
             typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
             bf16x4 dh, dl;
@@ -748,7 +750,7 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 #pragma unroll
             for (int cc = 1; cc < 4; ++cc)
                 if (cc == wave) v = (cc & 1) ? al[cc >> 1] : ah[cc >> 1];
-            reinterpret_cast<bf16x8*>(w.U)[(size_t)(jt * 4 + wave) * 64 + lane] = v;
+            __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(w.U) + (size_t)(jt * 4 + wave) * 64 + lane);
         }
         put_state();
         lds_barrier();
