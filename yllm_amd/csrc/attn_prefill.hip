@@ -382,8 +382,12 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
         asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
         const int lane = tid & 63;
         // with one key group the group is a constant, so the LDS tile bases are
-        // too and fold into the reads' offset fields
-        const int grp = NG > 1 ? tid / LT : 0, gtid = NG > 1 ? tid % LT : tid, wave = gtid >> 6;
+        // too and fold into the reads' offset fields; with two it is read into
+        // a scalar register (the LDS destination of a direct-to-LDS load must
+        // be uniform, and from a per-lane group index the compiler wrapped
+        // every such load in a loop over the lanes' values)
+        const int grp = NG > 1 ? (int)__builtin_amdgcn_readfirstlane(tid / LT) : 0,
+                  gtid = NG > 1 ? tid % LT : tid, wave = gtid >> 6;
         // the wave's 32 queries (qw) and, in pair mode, its half of the dimensions (hf)
         const int qw = PAIR ? wave >> 1 : wave, hf = PAIR ? wave & 1 : 0;
         const int r32 = lane & 31, hh = lane >> 5;

@@ -186,7 +186,10 @@ __global__ __launch_bounds__(256, 2) void oproj_gemm_kernel(GemmArgs a)
     static_assert(BT * CPR % 256 == 0 && BO * CPR % 256 == 0, "whole load instructions per operand");
     __shared__ __attribute__((aligned(16))) _Float16 lds[kStages * ROWS * kBK];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index in a scalar register: the LDS destination of a
+    // direct-to-LDS load (M0) must be uniform, and with a per-lane index the
+    // compiler wrapped every such load in a loop over the lanes' values
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r32 = lane & 31, hh = lane >> 5;
     const int wt = wave >> 1, wo = wave & 1;
     // Tile order: the hardware deals consecutive workgroups to the 8 XCDs in
