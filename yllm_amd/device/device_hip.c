@@ -119,6 +119,19 @@ typedef struct {
     uint16_t* d_kvstage; /* engine-layout rows on their way to the host (kv_to_host) */
     uint32_t kvstage_rows;
     float* h_conv;      /* one layer's conv delay line, kept to undo a failed block */
+    /* A decode token runs the whole GDN mixer in one launch (yhip_gdn_decode),
+     * the conv delay line in HBM: per state slot two lines [kwidth][conv_chan]
+     * (the kernel reads one and writes the other; conv_cur names the current
+     * one), conv_loc where the current line is (STATE_* as for the state), and
+     * per slot the layer's conv weights, dt_bias, ssm_a and norm weights
+     * (gdnw_n floats).  fused_decode is 0 when the norm weights are of a type
+     * the kernel does not take. */
+    float* d_conv;
+    uint8_t *conv_loc, *conv_cur;
+    float* d_gdnw;
+    float* d_dec;       /* the token's qkv | z | alpha | beta_raw */
+    uint32_t gdnw_n, norm_dtype;
+    int fused_decode;
     /* staging for one call: q (or a GDN qkv row), k, v, gate, output */
     uint32_t cap, q_w, o_w;
     float *d_q, *d_k, *d_v, *d_g, *d_out;
@@ -148,11 +161,29 @@ enum { STATE_HOST = 0, STATE_BOTH = 1, STATE_DEV = 2 };
  * one synchronous copy.  Returns 0, or -1 when the copy fails (after a GPU
  * failure the layers updated on the GPU since their last copy keep a stale
  * host state). */
+/* Make e->ssm_conv of GDN layer `layer` current when the fused decode token
+ * left the current delay line in HBM. */
+static int sync_conv_to_host(Engine* e, HipCtx* c, uint32_t layer)
+{
+    const uint32_t li = layer - c->first;
+    const int32_t slot = c->gdn_slot[li];
+    const size_t conv_n = (size_t)c->kwidth * c->conv_chan;
+    if (slot < 0 || !c->conv_loc || c->conv_loc[slot] != STATE_DEV) return 0;
+    if (hipMemcpyAsync(e->ssm_conv + (size_t)c->gdn_ord[li] * conv_n,
+                       c->d_conv + ((size_t)slot * 2 + c->conv_cur[slot]) * conv_n, conv_n * 4,
+                       hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        return -1;
+    c->conv_loc[slot] = STATE_BOTH;
+    return 0;
+}
+
 static int sync_state_to_host(Engine* e, HipCtx* c, uint32_t layer)
 {
     const uint32_t li = layer - c->first;
     const int32_t slot = c->gdn_slot[li];
     const size_t state_n = (size_t)c->n_v * c->hvd * c->hvd;
+    if (sync_conv_to_host(e, c, layer) != 0) return -1;
     if (slot < 0 || c->state_loc[slot] != STATE_DEV) return 0;
     if (hipMemcpyAsync(e->ssm_state + (size_t)c->gdn_ord[li] * state_n, c->d_state + (size_t)slot * state_n,
                        state_n * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
@@ -243,6 +274,11 @@ static void release(HipCtx* c)
     free(c->state_loc);
     dfree(c->d_kvstage);
     free(c->h_conv);
+    dfree(c->d_conv);
+    dfree(c->d_gdnw);
+    dfree(c->d_dec);
+    free(c->conv_loc);
+    free(c->conv_cur);
     {
         int id = c->device_id;
         memset(c, 0, sizeof(*c));
@@ -457,6 +493,39 @@ static int q35_gdn(Engine* e, HipCtx* c, uint32_t layer, uint32_t B, const uint8
     proj(z, c->h_n, base, &mt[SLOT_GATE_ATTN], vd, hidden, B);
     proj(alpha, c->h_n, base, &mt[SLOT_SSM_ALPHA], nv, hidden, B);
     proj(beta, c->h_n, base, &mt[SLOT_SSM_BETA], nv, hidden, B);
+    if (B == 1 && c->fused_decode) {
+        /* one launch: gates, conv1d_update + silu, l2 norms, the state update
+         * and rmsnorm_gated (engine.c:788-847), the delay line and the state
+         * in HBM; beta follows alpha in c->h_ab */
+        const size_t conv_n = (size_t)c->kwidth * cc;
+        float* lines = c->d_conv + (size_t)slot * 2 * conv_n;
+        const float* w = c->d_gdnw + (size_t)slot * c->gdnw_n;
+        const int cur = c->conv_cur[slot];
+        float* d_z = c->d_dec + cc;
+        float* d_ab = d_z + vd;
+        ok = (c->state_loc[slot] != STATE_HOST ||
+              hipMemcpyAsync(dS, host_S, state_n * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess) &&
+             (c->conv_loc[slot] != STATE_HOST ||
+              hipMemcpyAsync(lines + cur * conv_n, conv_state, conv_n * 4, hipMemcpyHostToDevice, c->stream) ==
+                  hipSuccess) &&
+             hipMemcpyAsync(c->d_dec, qkv, (size_t)cc * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+             hipMemcpyAsync(d_z, z, (size_t)vd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+             hipMemcpyAsync(d_ab, alpha, (size_t)2 * nv * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+             yhip_gdn_decode(dS, lines + cur * conv_n, lines + (1 - cur) * conv_n, c->d_out, c->d_dec, d_z, d_ab,
+                             d_ab + nv, w, w + conv_n, w + conv_n + nv, w + conv_n + 2 * nv, c->norm_dtype, c->n_k,
+                             nv, hvd, c->kwidth, eps, eps, c->stream) == YHIP_OK &&
+             hipMemcpyAsync(c->h_o, c->d_out, (size_t)vd * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
+             hipStreamSynchronize(c->stream) == hipSuccess;
+        if (!ok) return -1;
+        c->state_loc[slot] = STATE_DEV;
+        c->conv_loc[slot] = STATE_DEV;
+        c->conv_cur[slot] = (uint8_t)(1 - cur);
+        proj(c->h_x, c->h_o, base, &mt[SLOT_SSM_OUT], hidden, vd, B);
+        return 0;
+    }
+    /* the host runs the conv: it needs the current delay line */
+    if (sync_conv_to_host(e, c, layer) != 0) return -1;
+    if (c->conv_loc) c->conv_loc[slot] = STATE_HOST;
     for (b = 0; b < B; b++) {
         float* bb = beta + (size_t)b * nv;
         const float* ab = alpha + (size_t)b * nv;
@@ -614,6 +683,7 @@ static int q35_fwd(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_t
     if (layer >= c->first && layer <= c->last && c->gdn_slot[layer - c->first] >= 0) {
         sync_state_to_host(e, c, layer);
         c->state_loc[c->gdn_slot[layer - c->first]] = STATE_HOST;
+        if (c->conv_loc) c->conv_loc[c->gdn_slot[layer - c->first]] = STATE_HOST;
     }
     if (batch)
         c->cpu_fwd_batch(e, layer, pos0, B);
@@ -812,6 +882,59 @@ static int plan_layers(Engine* e, HipCtx* c, char* err, size_t errlen)
     return 0;
 }
 
+/* HBM for the fused decode token (yhip_gdn_decode): two delay lines per state
+ * slot and the layer's conv weights, dt_bias, ssm_a and norm weights.  The
+ * norm weights are f32 or, like the engine reads every other type, f16 bits
+ * (engine.c:838-850); layers whose norm types differ keep the token on the
+ * chunk path. */
+static int setup_fused_decode(Engine* e, HipCtx* c, char* err, size_t errlen)
+{
+    const size_t conv_n = (size_t)c->kwidth * c->conv_chan;
+    const size_t dec_n = (size_t)c->conv_chan + c->value_dim + 2 * (size_t)c->n_v;
+    uint32_t l, ndt = 0;
+    int seen = 0;
+    c->fused_decode = 0;
+    if (c->kwidth > 8 || c->n_v < c->n_k) return 0;
+    for (l = c->first; l <= c->last; l++) {
+        const LlfTensorMeta* mt = &e->ws.model.metas[e->ws.model.base_idx[l]];
+        const uint32_t d = mt[SLOT_SSM_NORM].dtype == DT_F32 ? YHIP_F32 : YHIP_F16;
+        if (c->gdn_slot[l - c->first] < 0) continue;
+        if (seen && d != ndt) return 0;
+        ndt = d;
+        seen = 1;
+    }
+    c->norm_dtype = ndt;
+    c->gdnw_n = (uint32_t)((conv_n + 2 * c->n_v + c->hvd + 3) / 4 * 4);
+    c->conv_loc = (uint8_t*)calloc(c->n_gdn_slots, 1); /* STATE_HOST */
+    c->conv_cur = (uint8_t*)calloc(c->n_gdn_slots, 1);
+    if (!c->conv_loc || !c->conv_cur) return say(err, errlen, "out of host memory", NULL);
+    if (hip_ok(hipMalloc((void**)&c->d_conv, c->n_gdn_slots * 2 * conv_n * 4), err, errlen, "GDN delay lines") ||
+        hip_ok(hipMalloc((void**)&c->d_gdnw, (size_t)c->n_gdn_slots * c->gdnw_n * 4), err, errlen, "GDN weights") ||
+        hip_ok(hipMalloc((void**)&c->d_dec, dec_n * 4), err, errlen, "GDN decode staging"))
+        return -1;
+    for (l = c->first; l <= c->last; l++) {
+        const int32_t slot = c->gdn_slot[l - c->first];
+        const uint8_t* base = layer_base(e, l);
+        const LlfTensorMeta* mt = &e->ws.model.metas[e->ws.model.base_idx[l]];
+        float* w;
+        if (slot < 0) continue;
+        w = c->d_gdnw + (size_t)slot * c->gdnw_n;
+        if (hip_ok(hipMemcpy(w, base + mt[SLOT_SSM_CONV1D].offset, conv_n * 4, hipMemcpyHostToDevice), err, errlen,
+                   "GDN conv weights") ||
+            hip_ok(hipMemcpy(w + conv_n, base + mt[SLOT_SSM_DT].offset, (size_t)c->n_v * 4, hipMemcpyHostToDevice),
+                   err, errlen, "GDN dt_bias") ||
+            hip_ok(hipMemcpy(w + conv_n + c->n_v, base + mt[SLOT_SSM_A].offset, (size_t)c->n_v * 4,
+                             hipMemcpyHostToDevice),
+                   err, errlen, "GDN ssm_a") ||
+            hip_ok(hipMemcpy(w + conv_n + 2 * c->n_v, base + mt[SLOT_SSM_NORM].offset,
+                             (size_t)c->hvd * (ndt == YHIP_F32 ? 4 : 2), hipMemcpyHostToDevice),
+                   err, errlen, "GDN norm weights"))
+            return -1;
+    }
+    c->fused_decode = 1;
+    return 0;
+}
+
 static int hip_load_weights(Engine* e, char* err, size_t errlen)
 {
     HipCtx* c = ctx_of(e);
@@ -869,6 +992,7 @@ static int hip_load_weights(Engine* e, char* err, size_t errlen)
         if (!c->state_loc || !c->h_conv) return say(err, errlen, "out of host memory", NULL);
         if (hip_ok(hipMalloc((void**)&c->d_state, state_bytes * c->n_gdn_slots), err, errlen, "GDN state allocation"))
             return -1;
+        if (setup_fused_decode(e, c, err, errlen) != 0) return -1;
     }
     if (ensure_cap(c, e->pb_cap > 0 ? e->pb_cap : 64) != 0) return say(err, errlen, "staging allocation", NULL);
     c->ws_bytes = yhip_attn_decode_workspace(1, c->max_seq, c->max_seq, c->n_heads, c->n_kv, c->head_dim);
@@ -952,6 +1076,7 @@ static int move_kv(Engine* e, uint32_t n_pos, int to_host)
     if (!c || !c->stream || c->failed) return -1;
     if (n_pos > c->max_seq) n_pos = c->max_seq;
     if (!to_host && c->state_loc) memset(c->state_loc, STATE_HOST, c->n_gdn_slots);
+    if (!to_host && c->conv_loc) memset(c->conv_loc, STATE_HOST, c->n_gdn_slots);
     if (to_host && sync_states_to_host(e, c) != 0) return -1;
     for (l = c->first; l <= c->last && n_pos > 0; l++) {
         uint16_t* hk = e->kv + (size_t)l * e->max_seq * c->kv_dim;
