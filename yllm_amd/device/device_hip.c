@@ -130,6 +130,7 @@ typedef struct {
     uint8_t *conv_loc, *conv_cur;
     float* d_gdnw;
     float* d_dec;       /* the token's qkv | z | alpha | beta_raw */
+    float* h_raw;       /* a decode token's q | k before RoPE (llama / qwen) */
     uint32_t gdnw_n, norm_dtype;
     int fused_decode;
     /* staging for one call: q (or a GDN qkv row), k, v, gate, output */
@@ -279,6 +280,7 @@ static void release(HipCtx* c)
     dfree(c->d_dec);
     free(c->conv_loc);
     free(c->conv_cur);
+    free(c->h_raw);
     {
         int id = c->device_id;
         memset(c, 0, sizeof(*c));
@@ -404,7 +406,7 @@ static void head_norm(float* v, const LlfTensorMeta* t, const uint8_t* base, uin
 /* q, k, v of one token after bias, QK-norm and RoPE; the f16 K/V row goes to
  * host KV (engine.c:1015-1072) */
 static void token_qkv(Engine* e, const HipCtx* c, uint32_t layer, uint32_t pos, const uint8_t* base,
-                      const LlfTensorMeta* mt, float eps, float theta, float* q, float* k, float* v)
+                      const LlfTensorMeta* mt, float eps, float theta, float* q, float* k, float* v, float* raw)
 {
     uint16_t* hk = e->kv + (size_t)layer * e->max_seq * c->kv_dim + (size_t)pos * c->kv_dim;
     uint16_t* hv = e->kv + (size_t)(c->n_blocks + layer) * e->max_seq * c->kv_dim + (size_t)pos * c->kv_dim;
@@ -414,6 +416,10 @@ static void token_qkv(Engine* e, const HipCtx* c, uint32_t layer, uint32_t pos, 
     add_bias(v, &mt[SLOT_VBIAS], base, c->kv_dim);
     head_norm(q, &mt[SLOT_QNORM], base, c->n_heads, c->head_dim, eps);
     head_norm(k, &mt[SLOT_KNORM], base, c->n_kv, c->head_dim, eps);
+    if (raw) {  /* q | k before RoPE, for a kernel that rotates them itself */
+        memcpy(raw, q, (size_t)c->hidden * 4);
+        memcpy(raw + c->hidden, k, (size_t)c->kv_dim * 4);
+    }
     rope_heads(c->arch, q, c->n_heads, c->head_dim, pos, theta);
     rope_heads(c->arch, k, c->n_kv, c->head_dim, pos, theta);
     for (j = 0; j < c->kv_dim; j++) {
@@ -428,25 +434,26 @@ static void scalars(const Engine* e, float* eps, float* theta)
     memcpy(theta, &e->ws.model.h.rope_theta_bits, 4);
 }
 
-/* decode attention on the GPU: q, k, v (contiguous floats, as engine.c
- * lays them out in hb2) -> att_out */
-static int gpu_decode(HipCtx* c, Engine* e, uint32_t layer, uint32_t pos, const float* qkv, float* att_out)
+/* decode attention on the GPU: the token's q | k before RoPE (raw) and v ->
+ * att_out.  One launch rotates q and k with the reference's angles (the host
+ * rotated the same rows, bit for bit, into e->kv), stores the token's key and
+ * value and attends (yhip_attn_decode_rope). */
+static int gpu_decode(HipCtx* c, Engine* e, uint32_t layer, uint32_t pos, const float* raw, const float* v,
+                      float theta, float* att_out)
 {
     uint16_t *kc = layer_k(c, layer), *vc = layer_v(c, layer);
     size_t nq = c->hidden, nkv = c->kv_dim;
+    const uint32_t rope = c->arch == ARCH_QWEN ? YHIP_ROPE_HALF : YHIP_ROPE_PAIRS;
     if (ensure_cap(c, 1) != 0) return -1;
     if (catch_up(c, e, layer, pos) != 0) return -1;
-    if (hipMemcpyAsync(c->d_q, qkv, nq * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
-        hipMemcpyAsync(c->d_k, qkv + nq, nkv * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
-        hipMemcpyAsync(c->d_v, qkv + nq + nkv, nkv * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
+    if (hipMemcpyAsync(c->d_q, raw, nq * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        hipMemcpyAsync(c->d_k, raw + nq, nkv * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        hipMemcpyAsync(c->d_v, v, nkv * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
         return -1;
-    if (yhip_kv_store(kc, vc, c->d_k, c->d_v, YHIP_F32, pos, 1, c->n_kv, c->head_dim, c->kv_stride,
-                      c->stream) != YHIP_OK)
+    if (yhip_attn_decode_rope(c->d_out, c->d_q, c->d_k, c->d_v, kc, vc, pos, c->n_heads, c->n_kv, c->head_dim,
+                              c->kv_stride, rope, 0, theta, NULL, c->d_ws, c->ws_bytes, c->stream) != YHIP_OK)
         return -1;
     c->dev_len[c->kv_slot[layer - c->first]] = pos + 1;
-    if (yhip_attn_decode(c->d_out, c->d_q, kc, vc, pos, c->n_heads, c->n_kv, c->head_dim, c->kv_stride, NULL,
-                         c->d_ws, c->ws_bytes, c->stream) != YHIP_OK)
-        return -1;
     if (hipMemcpyAsync(att_out, c->d_out, nq * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return -1;
     return hipStreamSynchronize(c->stream) == hipSuccess ? 0 : -1;
 }
@@ -726,9 +733,9 @@ static int hip_fwd_block(Engine* e, uint32_t layer, uint32_t pos)
     matmul(q, x2, base + mt[SLOT_Q].offset, hidden, hidden, mt[SLOT_Q].dtype);
     matmul(k, x2, base + mt[SLOT_K].offset, kv_dim, hidden, mt[SLOT_K].dtype);
     matmul(v, x2, base + mt[SLOT_V].offset, kv_dim, hidden, mt[SLOT_V].dtype);
-    token_qkv(e, c, layer, pos, base, mt, eps, theta, q, k, v);
+    token_qkv(e, c, layer, pos, base, mt, eps, theta, q, k, v, c->h_raw);
 
-    if (gpu_decode(c, e, layer, pos, q, att_out) != 0) {
+    if (gpu_decode(c, e, layer, pos, c->h_raw, v, theta, att_out) != 0) {
         c->failed = 1;
         c->cpu_fwd(e, layer, pos);  /* x is still the block input */
         return -1;
@@ -806,7 +813,7 @@ static int hip_fwd_block_batch(Engine* e, uint32_t layer, uint32_t pos_start, ui
     matmul_batch(e->pbv, e->pb2, base + mt[SLOT_V].offset, kv_dim, hidden, mt[SLOT_V].dtype, B);
     for (b = 0; b < B; b++)
         token_qkv(e, c, layer, pos_start + b, base, mt, eps, theta, e->pbq + (size_t)b * hidden,
-                  e->pbk + (size_t)b * kv_dim, e->pbv + (size_t)b * kv_dim);
+                  e->pbk + (size_t)b * kv_dim, e->pbv + (size_t)b * kv_dim, NULL);
 
     if (gpu_prefill(c, e, layer, pos_start, B) != 0) {
         c->failed = 1;
@@ -995,6 +1002,8 @@ static int hip_load_weights(Engine* e, char* err, size_t errlen)
         if (setup_fused_decode(e, c, err, errlen) != 0) return -1;
     }
     if (ensure_cap(c, e->pb_cap > 0 ? e->pb_cap : 64) != 0) return say(err, errlen, "staging allocation", NULL);
+    c->h_raw = (float*)malloc(((size_t)c->hidden + c->kv_dim) * 4);
+    if (!c->h_raw) return say(err, errlen, "out of host memory", NULL);
     c->ws_bytes = yhip_attn_decode_workspace(1, c->max_seq, c->max_seq, c->n_heads, c->n_kv, c->head_dim);
     if (c->ws_bytes && hip_ok(hipMalloc(&c->d_ws, c->ws_bytes), err, errlen, "decode workspace")) return -1;
     if (hip_ok(hipStreamSynchronize(c->stream), err, errlen, "set-up")) return -1;
