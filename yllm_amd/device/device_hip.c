@@ -130,7 +130,7 @@ typedef struct {
     uint8_t *conv_loc, *conv_cur;
     float* d_gdnw;
     float* d_dec;       /* the token's qkv | z | alpha | beta_raw */
-    float* h_raw;       /* a decode token's q | k before RoPE (llama / qwen) */
+    float* h_raw;       /* a decode token's q | k before RoPE */
     uint32_t gdnw_n, norm_dtype;
     int fused_decode;
     /* staging for one call: q (or a GDN qkv row), k, v, gate, output */
@@ -603,6 +603,10 @@ static int q35_attn(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_
         uint16_t* hv = e->kv + (size_t)(c->n_blocks + layer) * e->max_seq * kvd + (size_t)pos * kvd;
         head_norm(q, &mt[SLOT_QNORM], base, c->n_heads, hd, eps);
         head_norm(k, &mt[SLOT_KNORM], base, c->n_kv, hd, eps);
+        if (B == 1) {  /* q | k before RoPE: the decode launch rotates them */
+            memcpy(c->h_raw, q, (size_t)qd * 4);
+            memcpy(c->h_raw + qd, k, (size_t)kvd * 4);
+        }
         for (h = 0; h < c->n_heads; h++) rope_inplace_mrope(q + (size_t)h * hd, hd, 64, pos, theta);
         for (h = 0; h < c->n_kv; h++) rope_inplace_mrope(k + (size_t)h * hd, hd, 64, pos, theta);
         for (j = 0; j < kvd; j++) {
@@ -611,20 +615,27 @@ static int q35_attn(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_
         }
     }
 
+    /* a decode token: M-RoPE over 64 dims, the KV store and the gated
+     * attention in one launch, from the unrotated q and k */
+    const float* qs = B == 1 ? c->h_raw : c->h_q;
+    const float* ks = B == 1 ? c->h_raw + qd : c->h_k;
     ok = catch_up(c, e, layer, pos0) == 0 &&
-         hipMemcpyAsync(c->d_q, c->h_q, (size_t)B * qd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+         hipMemcpyAsync(c->d_q, qs, (size_t)B * qd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
          hipMemcpyAsync(c->d_g, c->h_z, (size_t)B * qd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
-         hipMemcpyAsync(c->d_k, c->h_k, (size_t)B * kvd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+         hipMemcpyAsync(c->d_k, ks, (size_t)B * kvd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
          hipMemcpyAsync(c->d_v, c->h_v, (size_t)B * kvd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
-         yhip_kv_store(kc, vc, c->d_k, c->d_v, YHIP_F32, pos0, B, c->n_kv, hd, c->kv_stride, c->stream) == YHIP_OK;
+         (B == 1 ||
+          yhip_kv_store(kc, vc, c->d_k, c->d_v, YHIP_F32, pos0, B, c->n_kv, hd, c->kv_stride, c->stream) == YHIP_OK);
     if (!ok) return -1;
-    c->dev_len[c->kv_slot[layer - c->first]] = pos0 + B;
     if (B == 1)
-        ok = yhip_attn_decode(c->d_out, c->d_q, kc, vc, pos0, c->n_heads, c->n_kv, hd, c->kv_stride, c->d_g, c->d_ws,
-                              c->ws_bytes, c->stream) == YHIP_OK;
+        ok = yhip_attn_decode_rope(c->d_out, c->d_q, c->d_k, c->d_v, kc, vc, pos0, c->n_heads, c->n_kv, hd,
+                                   c->kv_stride, YHIP_ROPE_MROPE, 64, theta, c->d_g, c->d_ws, c->ws_bytes,
+                                   c->stream) == YHIP_OK;
     else
         ok = yhip_attn_prefill(c->d_out, YHIP_F32, qd, c->d_q, YHIP_F32, qd, kc, vc, pos0, B, c->n_heads, c->n_kv, hd,
                                c->kv_stride, c->d_g, qd, c->d_pws, c->pws_bytes, c->stream) == YHIP_OK;
+    if (!ok) return -1;
+    c->dev_len[c->kv_slot[layer - c->first]] = pos0 + B;
     ok = ok &&
          hipMemcpyAsync(c->h_o, c->d_out, (size_t)B * qd * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
          hipStreamSynchronize(c->stream) == hipSuccess;
@@ -1002,7 +1013,7 @@ static int hip_load_weights(Engine* e, char* err, size_t errlen)
         if (setup_fused_decode(e, c, err, errlen) != 0) return -1;
     }
     if (ensure_cap(c, e->pb_cap > 0 ? e->pb_cap : 64) != 0) return say(err, errlen, "staging allocation", NULL);
-    c->h_raw = (float*)malloc(((size_t)c->hidden + c->kv_dim) * 4);
+    c->h_raw = (float*)malloc(((size_t)(c->qdim > c->hidden ? c->qdim : c->hidden) + c->kv_dim) * 4);
     if (!c->h_raw) return say(err, errlen, "out of host memory", NULL);
     c->ws_bytes = yhip_attn_decode_workspace(1, c->max_seq, c->max_seq, c->n_heads, c->n_kv, c->head_dim);
     if (c->ws_bytes && hip_ok(hipMalloc(&c->d_ws, c->ws_bytes), err, errlen, "decode workspace")) return -1;
