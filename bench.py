@@ -9,6 +9,8 @@ batch of synthetic input, with all inputs resident in HBM:
               heads, head_dim 128, f16 Q/K/V drawn N(0,1)*0.5 from seed
               0x5EED0002, f32 output -- one yhip_attn_prefill launch.
   prefill8k   the same at 8192 tokens, 32 / 8 heads.
+  decode512   the reference's CPU-runnable decode: 14 query / 2 KV heads,
+              head_dim 64, 512 keys, fp32 q (64 rotating layer caches).
   decode32k   one query token per head over a 32768-key cache, 32 / 8 heads,
               head_dim 128 -- one yhip_attn_decode call (split + merge
               kernels).  Steps rotate over 6 layer caches (768 MiB) so the
@@ -34,7 +36,10 @@ batch of synthetic input, with all inputs resident in HBM:
               sigmoid gate fused in the epilogue, bf16 out.
   hybrid      the fifth configuration end to end: 3 GDN layers + 1 gated
               attention layer (16 / 2 heads, d 256, bf16), 4096-token
-              prefill then 256 decode steps; tokens/s over the whole pass.
+              prefill then 256 decode steps; tokens/s over the whole pass,
+              its roofline the sum of the phases' bounds (MFMA for the
+              prefill attention and the GDN chunks, HBM for the decode
+              steps' KV and recurrent-state traffic).
 
 The default line reports prefill2k as `value`, decode32k and gdn4k under
 "secondary".  The CPU baseline is the oracle restatement of the reference's
@@ -276,7 +281,7 @@ def decode_bytes(L: int, nkv: int, nh: int, hd: int) -> float:
 
 
 def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, steps: int, warmup: int,
-               cpu: bool, label: str):
+               cpu: bool, label: str, q_f32: bool = False):
     import torch
 
     from yllm_amd.attention import LayerKV, attn_decode, decode_workspace, decode_workspace_bytes, kv_store
@@ -286,7 +291,8 @@ def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, step
     nk = L * nkv * hd
     k = torch.from_numpy(synth(seed, nk).reshape(L, nkv * hd)).to(dev).half()
     v = torch.from_numpy(synth(seed, nk, nk).reshape(L, nkv * hd)).to(dev).half()
-    q = torch.from_numpy(synth(seed, nh * hd, 2 * nk)).to(dev)
+    # q: f16-representable values, or (q_f32) the fp32 draws themselves, which the kernel takes as f16 hi + lo
+    q = torch.from_numpy((synth_raw if q_f32 else synth)(seed, nh * hd, 2 * nk)).to(dev)
     caches = []
     for _ in range(n_layers):  # distinct HBM regions with the same contents
         c = LayerKV.empty(nkv, hd, L, device=dev, zero=False)
@@ -305,7 +311,8 @@ def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, step
         "ms_per_step": ms,
         "tokens_per_s": 1.0 / (ms * 1e-3),
         "config": {"workload": f"{label}: decode attention, 1 sequence, {L} keys, {nh} query / {nkv} KV heads, "
-                               f"head_dim {hd}, f16 KV N(0,1)*0.5 seed {hex(seed)}, split-K + LSE merge, "
+                               f"head_dim {hd}, f16 KV N(0,1)*0.5 seed {hex(seed)}, "
+                               f"{'fp32' if q_f32 else 'f16-valued'} q, split-K + LSE merge, "
                                f"{n_layers} rotating layer caches",
                    "keys": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd},
         "roofline": {"bound": "hbm", "kernel": "decode_split_kernel<%d> + decode_merge_kernel<%d>" % (hd, hd),
@@ -635,6 +642,30 @@ def run_oproj(B: int, hidden: int, qdim: int, steps: int, warmup: int, cpu: bool
     return res
 
 
+def hybrid_phase_bounds(T, n_dec, n_gdn, hg, dg, kw, nh, nkv, da) -> dict:
+    """Seconds each phase of the hybrid group takes at its roofline:
+    prefill attention at the f16 MFMA peak (causal FLOPs); each GDN layer's
+    chunked prefill at max(its algorithmic bytes at HBM peak, the
+    sequential form's flops at the fp32 MFMA peak); the prefill's conv,
+    gated norm and RoPE + KV store as HBM bytes; every decode token's
+    gated-attention KV read (keys 0..t, K and V once), its q / gate / out
+    and new K/V row, and per GDN layer the state read and written once plus
+    its conv delay line and token rows, at HBM peak."""
+    conv = 3 * hg * dg
+    pre_attn = prefill_flops(T, nh, da) / MFMA_F16_PEAK
+    gdn_chunk = n_gdn * max(gdn_bytes(T, hg, hg, dg) / HBM_PEAK, gdn_flops(T, hg, dg) / MFMA_F32_PEAK)
+    # conv: rows in, rows out, delay line; gated norm: x, z in, y out; RoPE + store: q/k/v rows in, bf16 q, K/V out
+    pre_io = (n_gdn * (T * conv * 4 * 2 + T * hg * dg * 4 * 3)
+              + T * (nh * da * (4 + 2) + nkv * da * 2 * (4 + 2))) / HBM_PEAK
+    dec = 0.0
+    for t in range(T, T + n_dec):
+        keys = t + 1
+        dec += keys * nkv * da * 2 * 2 + nh * da * 4 * 3 + nkv * da * 2 * (4 + 2)
+        dec += n_gdn * (hg * dg * dg * 4 * 2 + kw * conv * 4 * 2 + conv * 4 + hg * dg * 4 * 3)
+    return {"prefill_attention": pre_attn, "prefill_gdn_chunks": gdn_chunk, "prefill_conv_norm_rope": pre_io,
+            "decode_tokens": dec / HBM_PEAK}
+
+
 def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
     """The fifth configuration: one group of 3 Gated-DeltaNet layers and 1
     gated GQA attention layer, a 4096-token prefill then n_dec decode steps.
@@ -726,6 +757,8 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
 
     # one step is ~1300 launches: its graph is captured once and replayed
     ms, _ = time_steps(step, steps, warmup, dout, graph_per_step=True)
+    phases = hybrid_phase_bounds(T, n_dec, n_gdn, hg, dg, kw, nh, nkv, da)
+    ideal_ms = sum(phases.values()) * 1e3
     res = {
         "value": L / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "tokens_per_s": L / (ms * 1e-3),
         "config": {"workload": f"qwen35 hybrid group: {n_gdn} Gated-DeltaNet layers ({hg} heads, d {dg}, fp32: "
@@ -736,7 +769,14 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
                                f"(fused GDN token per layer, one launch; RoPE + KV store fused into the split-K decode) per step; N(0,1)*0.5 seed "
                                f"{hex(seed)}",
                    "prefill_tokens": T, "decode_steps": n_dec},
-        "roofline": None,
+        # no single kernel bounds the group: the roofline is the sum of its
+        # phases' bounds, as a step rate (achieved / peak = ideal / measured)
+        "roofline": {"bound": "mfma+hbm (sum of phase bounds)",
+                     "kernel": "decode phase: gdn_decode_head_kernel<%d> x %d + decode_split_kernel<%d, ROPE> + "
+                               "decode_merge_kernel<%d> per token" % (dg, n_gdn, da, da),
+                     "achieved": 1e3 / ms, "peak": 1e3 / ideal_ms, "unit": "steps/s", "frac": ideal_ms / ms,
+                     "ideal_ms": ideal_ms, "phase_bound_us": {k2: v2 * 1e6 for k2, v2 in phases.items()},
+                     "launch_ms": ms, "traffic": None},
     }
     if cpu:
         torch.cuda.synchronize()
@@ -973,7 +1013,7 @@ def cpu_decode(q, cache, out, L, nh, nkv, hd):
         want = O.decode(qn, kc, vc, L - 1, nh, nkv, hd)
         reps += 1
         dt = time.perf_counter() - t0
-        if dt > 3.0 or reps >= 20:
+        if dt > 3.0 or (reps >= 20 and dt > 0.5):
             break
     cores, model = _host_desc(O)
     per = dt / reps
@@ -1093,17 +1133,23 @@ def traffic_of(label: str):
 
 
 # the other configurations' lines in the default run, with their own step counts
-SECONDARY = ["decode32k", "prefill8k", "prefill2k_chunked", "decode128k", "decode_batch", "gated4k", "gdn4k", "hybrid"]
-SECONDARY_STEPS = {"decode32k": (200, 20), "prefill8k": (20, 3), "prefill2k_chunked": (10, 2), "decode128k": (50, 5), "decode_batch": (20, 3),
-                   "gated4k": (20, 3), "gdn4k": (10, 2), "hybrid": (3, 1)}
-SECONDARY_METRIC = {"decode32k": "attn decode GB/s", "prefill8k": "prefill attn TFLOP/s",
+SECONDARY = ["decode32k", "prefill8k", "prefill2k_chunked", "decode128k", "decode_batch", "gated4k", "gdn4k", "hybrid",
+             "decode512"]
+SECONDARY_STEPS = {"decode32k": (200, 20), "prefill8k": (20, 3), "prefill2k_chunked": (10, 2), "decode128k": (50, 5),
+                   "decode_batch": (20, 3), "gated4k": (20, 3), "gdn4k": (10, 2), "hybrid": (3, 1),
+                   "decode512": (200, 20)}
+SECONDARY_METRIC = {"decode32k": "attn decode GB/s", "decode512": "attn decode GB/s", "prefill8k": "prefill attn TFLOP/s",
                     "prefill2k_chunked": "prefill attn TFLOP/s",
                     "decode128k": "attn decode GB/s", "decode_batch": "attn decode GB/s",
                     "gated4k": "prefill attn TFLOP/s", "gdn4k": "GDN prefill tokens/s", "hybrid": "hybrid tokens/s"}
-DTYPES = {"gdn4k": "f32", "rope8k": "f32 rotation, f16 stores", "oproj8k": "f16 MFMA, f32 accumulate",
+DTYPES = {"gdn4k": "f32 state, gates and accumulation; chunk products in split bf16 (hi*hi + hi*lo + lo*hi on bf16 "
+                   "MFMA), the -W operand rounded to bf16, Gram products on f32 MFMA",
+          "decode512": "f32 q (f16 hi + lo), f16 K/V MFMA, f32 accumulate/softmax",
+          "rope8k": "f32 rotation, f16 stores", "oproj8k": "f16 MFMA, f32 accumulate",
           "oproj1": "f16 weights, f32 activations and accumulate", "kvstore8k": "f32 -> f16 (reference rounding)",
           "gated4k": "bf16 q, f16 K/V MFMA, f32 accumulate/softmax, bf16 out",
-          "hybrid": "f32 GDN; bf16/f16 MFMA attention, f32 accumulate"}
+          "hybrid": "GDN f32 state and accumulation (chunk products in split bf16); bf16/f16 MFMA attention, "
+                    "f32 accumulate"}
 
 
 def timing_of(w: str, steps: int) -> str:
@@ -1122,6 +1168,8 @@ def run_workload(w: str, steps: int, warmup: int, cpu: bool):
         return run_prefill_chunked(2048, 28, 4, 128, 64, 2, steps, warmup, cpu)
     if w == "prefill8k_chunked":
         return run_prefill_chunked(8192, 32, 8, 128, 64, 4, steps, warmup, cpu)
+    if w == "decode512":  # the reference's CPU-runnable case: 14 / 2 heads, d 64, 512 keys, fp32 q
+        return run_decode(512, 14, 2, 64, 1, 64, steps, warmup, cpu, "decode512", q_f32=True)
     if w == "decode32k":
         return run_decode(32768, 32, 8, 128, 4, 6, steps, warmup, cpu, "decode32k")
     if w == "decode128k":
@@ -1155,8 +1203,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="prefill2k",
-                    choices=["prefill2k", "prefill8k", "prefill2k_chunked", "prefill8k_chunked", "decode32k", "decode4k_d256", "decode128k", "decode_batch", "gdn4k",
-                             "rope8k", "oproj8k", "oproj64", "oproj1", "kvstore8k", "gated4k", "hybrid"])
+                    choices=["prefill2k", "prefill8k", "prefill2k_chunked", "prefill8k_chunked", "decode512", "decode32k",
+                             "decode4k_d256", "decode128k", "decode_batch", "gdn4k", "rope8k", "oproj8k", "oproj64",
+                             "oproj1", "kvstore8k", "gated4k", "hybrid"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the other configurations' secondary lines (" + ", ".join(SECONDARY) + ")")

@@ -34,13 +34,17 @@ struct Device;
  * (attention layers) and the HBM recurrent state (qwen35 GDN layers) and
  * installs fwd_block / fwd_block_batch (yllm.h:115-116); it fails with -1 and
  * a message for shapes the kernels do not take (head_dim not 64, 128 or 256;
- * more than 16 query heads per kv head; GDN head dim not 64 or 128), so the
- * caller can rebind the CPU device.  The GDN state stays in HBM between
- * calls: e->ssm_state is brought up to date when the host needs it -- before
- * a GDN block runs on the CPU (fallback), in device_hip_kv_to_host and in
- * free_dev -- not after every update (1 MiB per layer and token at the
- * fifth configuration's shape).  After a GPU failure, a layer updated on the
- * GPU since its last copy keeps its last host state when that copy fails. */
+ * more than 16 query heads per kv head; GDN head dim not 64 or 128, conv
+ * width above 8), so the caller can rebind the CPU device.  The GDN state
+ * and conv delay line stay in HBM between calls: e->ssm_state / ssm_conv
+ * are brought up to date when the host needs them -- before a GDN block
+ * runs on the CPU (fallback), in device_hip_kv_to_host and in free_dev --
+ * not after every update (1 MiB per layer and token for 16 heads of 128).
+ * A GDN block reads one of two HBM copies and writes the other, so a block
+ * that fails leaves the state from before it for the CPU fallback.  When
+ * the device cannot give that state back either, the block returns -2,
+ * writes NaN to its output rows (every later logit is NaN) and says so on
+ * stderr, instead of continuing on a stale host state. */
 struct Device* device_create_hip(int device_id, char* err, size_t errlen);
 
 /* KV-cache interface (device.h:58-63 cuda_after_prefill; cache.c:174-247).
@@ -56,12 +60,19 @@ struct Device* device_create_hip(int device_id, char* err, size_t errlen);
 int device_hip_kv_from_host(struct Engine* e, uint32_t n_pos);
 int device_hip_kv_to_host(struct Engine* e, uint32_t n_pos);
 
-/* Test hook for the fallback path: after `n_calls` more GPU block forwards
- * the backend behaves as if the GPU had failed (no GPU work is issued for
- * that call).  A failed block returns -1 after computing the block with the
- * engine's CPU forward from the host KV, and every later block stays on
- * the CPU.  n_calls < 0 disables the hook. */
+/* Test hooks for the fallback path.  device_hip_fail_after: after `n_calls`
+ * more GPU block forwards the backend behaves as if the GPU had failed.  A
+ * failed block returns -1 after computing the block with the engine's CPU
+ * forward from the host KV (and, for a GDN layer, the state copied back from
+ * HBM), and every later block stays on the CPU.  n_calls < 0 disables the
+ * hook.  device_hip_fail_mode sets where the failure strikes: 0 (the
+ * default) before the block issues any GPU work; 1 after its kernels ran and
+ * its output came back (as a failed result copy: the HBM state has moved on
+ * in the buffer the block wrote); 2 as 1 with every later device copy
+ * failing too (a device that is gone: a GDN state held only in HBM is then
+ * lost and reported, see device_create_hip). */
 void device_hip_fail_after(struct Engine* e, int n_calls);
+void device_hip_fail_mode(struct Engine* e, int mode);
 
 #ifdef __cplusplus
 }

@@ -98,8 +98,9 @@ int yhip_attn_decode(float* att_out, const float* q, const uint16_t* kcache,
  * yhip_attn_decode computes (engine.c:1054-1096; qwen35 910-960).  q, k, v are the token's raw
  * (unrotated) fp32 rows, [n_heads*head_dim] and [n_kv_heads*head_dim]; q is
  * not modified.  The key and value of position pos are rotated, rounded with
- * the reference f32->f16 rounding and stored into kcache / vcache, which
- * must not hold them yet.  rope, n_rot and theta as yhip_rope_kv_store
+ * the reference f32->f16 rounding and stored into kcache / vcache (row pos is
+ * overwritten and need not be initialised; the attention uses the new bits,
+ * never what the row held).  rope, n_rot and theta as yhip_rope_kv_store
  * (n_rot a multiple of 8); gate and workspace as yhip_attn_decode.  q and
  * att_out 16-byte aligned.  The cosines and sines are the host's cosf / sinf
  * of the reference's angles, so q and the stored key are rotated exactly as
@@ -265,18 +266,21 @@ int yhip_gdn_step(float* S, float* out, const float* q, const float* k, const fl
 /* T consecutive tokens (the per-token loop of the qwen35 batch forward,
  * engine.c:723-734, for the recurrence part): rows of q/k are qk_stride
  * floats apart, v rows v_stride, out rows out_stride (multiples of 4); gate
- * and beta are [T][n_v_heads].  S is updated in place to the state after
- * token T-1; out row t is the output of token t.
+ * and beta are [T][n_v_heads].  The state after token T-1 goes to S_out:
+ * NULL (or S) updates S in place; another buffer (16-byte aligned, not
+ * overlapping S) receives it and S keeps the state before the call, so a
+ * caller that alternates two buffers still holds the previous state when a
+ * later step of its own fails.  out row t is the output of token t.
  *
  * With a workspace of yhip_gdn_chunk_workspace(T, n_v_heads, head_dim)
  * bytes (16-byte aligned, no initialisation) and T >= 64, the chunked form
  * runs: 64-token chunks are reduced in parallel to matrix products (fp32
  * MFMA) and only the chunk-to-chunk state hand-over is sequential.  With
  * workspace NULL (or T < 64) the recurrence runs token by token. */
-int yhip_gdn_chunk(float* S, float* out, uint32_t out_stride, const float* q, const float* k, uint32_t qk_stride,
-                   const float* v, uint32_t v_stride, const float* gate, const float* beta, uint32_t T,
-                   uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps, void* workspace,
-                   size_t workspace_bytes, void* stream);
+int yhip_gdn_chunk(float* S, float* S_out, float* out, uint32_t out_stride, const float* q, const float* k,
+                   uint32_t qk_stride, const float* v, uint32_t v_stride, const float* gate, const float* beta,
+                   uint32_t T, uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps,
+                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes of the chunked form for T tokens (0 when T < 64). */
 size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_dim);
@@ -291,14 +295,15 @@ size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_di
  * dt_bias, ssm_a [n_v]; conv_w [conv_dim][kwidth] f32; norm_w [head_dim]
  * YHIP_F32 or YHIP_F16.  The delay line [kwidth][conv_dim] (row kwidth-1 the
  * newest input, as yhip_gdn_conv keeps it) is read from conv_in and written
- * to conv_out, which must not overlap it: swap the two every token.  S as
- * for yhip_gdn_step (updated in place, 16-byte aligned).  head_dim 64 or 128,
- * n_v_heads >= n_k_heads, kwidth 1..8. */
-int yhip_gdn_decode(float* S, const float* conv_in, float* conv_out, float* y, const float* qkv, const float* z,
-                    const float* alpha, const float* beta_raw, const float* conv_w, const float* dt_bias,
-                    const float* ssm_a, const void* norm_w, uint32_t norm_w_dtype, uint32_t n_k_heads,
-                    uint32_t n_v_heads, uint32_t head_dim, uint32_t kwidth, float l2_eps, float norm_eps,
-                    void* stream);
+ * to conv_out, which must not overlap it: swap the two every token.  S
+ * (16-byte aligned) holds the state before the token; the state after it
+ * goes to S_out as for yhip_gdn_chunk (NULL: in place).  head_dim 64 or
+ * 128, n_v_heads >= n_k_heads, kwidth 1..8. */
+int yhip_gdn_decode(float* S, float* S_out, const float* conv_in, float* conv_out, float* y, const float* qkv,
+                    const float* z, const float* alpha, const float* beta_raw, const float* conv_w,
+                    const float* dt_bias, const float* ssm_a, const void* norm_w, uint32_t norm_w_dtype,
+                    uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, uint32_t kwidth, float l2_eps,
+                    float norm_eps, void* stream);
 
 /* The GDN gates of T tokens (engine.c:788-793), in place like the engine:
  * beta[t][h] <- 1/(1+exp(-beta[t][h])), gate[t][h] <- log1p(exp(alpha[t][h]
@@ -309,7 +314,9 @@ int yhip_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt
 /* The causal conv1d + silu ahead of the recurrence for T tokens in order:
  * conv1d_update (matvec.c:956-968) then silu (engine.c:809-812) per token.
  * conv_state: the delay line, fp32 [kwidth][dim] (row kwidth-1 newest, the
- * engine's e->ssm_conv slot, engine.c:802), updated in place; conv_w: fp32
+ * engine's e->ssm_conv slot, engine.c:802) before the call; the line after
+ * it goes to conv_state_out (NULL or conv_state: in place; else a buffer not
+ * overlapping conv_state, which then keeps the line before the call); conv_w: fp32
  * [dim][kwidth] (the gguf layout the reference reads, w[ch*kwidth + i]).
  * x: T rows of dim channels x_stride floats apart (the qkv projection
  * rows); out: T rows out_stride apart, not overlapping x (a token's
@@ -317,7 +324,8 @@ int yhip_gdn_gates(float* beta, float* gate, const float* alpha, const float* dt
  * conv values themselves (bit for bit the reference's; with silu the
  * device expf adds its own rounding).  kwidth 1..8. */
 int yhip_gdn_conv(float* out, uint32_t out_stride, const float* x, uint32_t x_stride, float* conv_state,
-                  const float* conv_w, uint32_t T, uint32_t dim, uint32_t kwidth, int silu, void* stream);
+                  float* conv_state_out, const float* conv_w, uint32_t T, uint32_t dim, uint32_t kwidth, int silu,
+                  void* stream);
 
 /* Gated RMSNorm after the recurrence (rmsnorm_gated, matvec.c:1007-1021,
  * applied per v-head at engine.c:845-847): for token t and head h,

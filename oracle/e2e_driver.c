@@ -199,14 +199,14 @@ int ye_make_model(const char* path, uint32_t arch, uint32_t blocks, uint32_t hid
  * otherwise (qkv projection of 2*n_k*hvd + n_v*hvd conv channels, z gate,
  * f32 conv1d of width 4, ssm_a in [-1.5, -0.5], dt bias, alpha / beta
  * projections, gated-norm weight and ssm_out).  Every block has the SwiGLU
- * FFN.  Returns 0 or -1 with err set. */
+ * FFN, ffn wide (0: the usual 8/3 hidden).  Returns 0 or -1 with err set. */
 int ye_make_model_q35(const char* path, uint32_t blocks, uint32_t hidden, uint32_t heads, uint32_t kv_heads,
                       uint32_t head_dim, uint32_t n_k, uint32_t n_v, uint32_t hvd, uint32_t vocab, uint32_t seq,
-                      uint32_t seed, char* err, size_t errlen)
+                      uint32_t seed, uint32_t ffn, char* err, size_t errlen)
 {
     const uint32_t qdim = heads * head_dim, kv_dim = kv_heads * head_dim;
     const uint32_t vdim = n_v * hvd, conv = 2 * n_k * hvd + vdim, kwidth = 4;
-    const uint32_t inter = ((hidden * 8 / 3 + 63) / 64) * 64;
+    const uint32_t inter = ffn ? ffn : ((hidden * 8 / 3 + 63) / 64) * 64;
     Items t;
     LlfHeader h;
     uint32_t b;
@@ -284,12 +284,17 @@ static uint32_t argmax(const float* v, uint32_t n)
 /* Run prompt[0..n_prompt) as a batched prefill, then n_decode greedy decode
  * steps.  logits: [(n_decode+1)][vocab] (after the prefill, after each
  * step); tokens: [n_decode] chosen tokens.  use_hip: 0 = CPU device, 1 = HIP
- * backend.  fail_after >= 0 arms the backend's failure hook.  status[0] =
- * bind result (0 HIP, -1 fell back to CPU), status[1] = KV rows (all
- * layers, K and V) whose HBM copy differs from host KV at the end (HIP
- * without the hook only, else -1).  Returns 0 or -1 with err set. */
-int ye_run(const char* path, int use_hip, int device_id, int fail_after, const uint32_t* prompt, int n_prompt,
-           int n_decode, float* logits, uint32_t* tokens, int* status, char* err, size_t errlen)
+ * backend.  fail_after >= 0 arms the backend's failure hook, fail_mode says
+ * where it strikes (device_hip_fail_mode).  status[0] = bind result (0 HIP,
+ * -1 fell back to CPU), status[1] = KV rows (all layers, K and V) whose HBM
+ * copy differs from host KV at the end (HIP without the hook only, else -1).
+ * gdn_out (may be NULL): the engine's GDN delay lines then recurrent states
+ * at the end (e->ssm_conv, e->ssm_state; for HIP after device_hip_kv_to_host
+ * brought them to the host), up to gdn_cap floats; status[2] = the floats
+ * they hold.  Returns 0 or -1 with err set. */
+int ye_run(const char* path, int use_hip, int device_id, int fail_after, int fail_mode, const uint32_t* prompt,
+           int n_prompt, int n_decode, float* logits, uint32_t* tokens, int* status, float* gdn_out,
+           size_t gdn_cap, char* err, size_t errlen)
 {
     Engine e;
     uint32_t vocab, pos;
@@ -297,6 +302,7 @@ int ye_run(const char* path, int use_hip, int device_id, int fail_after, const u
     memset(&e, 0, sizeof e);
     status[0] = 0;
     status[1] = -1;
+    status[2] = 0;
     if (engine_init(&e, path, 0, 0, err, errlen) != 0) return -1;
     vocab = e.ws.model.h.vocab;
     if (use_hip) {
@@ -305,7 +311,10 @@ int ye_run(const char* path, int use_hip, int device_id, int fail_after, const u
             engine_free(&e);
             return -1;
         }
-        if (status[0] == 0 && fail_after >= 0) device_hip_fail_after(&e, fail_after);
+        if (status[0] == 0 && fail_after >= 0) {
+            device_hip_fail_mode(&e, fail_mode);
+            device_hip_fail_after(&e, fail_after);
+        }
     }
     if (engine_forward_prefill(&e, prompt, n_prompt, 0) != 0) {
         snprintf(err, errlen, "prefill failed");
@@ -352,6 +361,26 @@ int ye_run(const char* path, int use_hip, int device_id, int fail_after, const u
         }
         status[1] = diff;
         free(keep);
+    }
+    if (gdn_out && e.ssm_state && e.ssm_conv) {
+        /* the shapes engine_init sized the two arrays with (engine.c:283-305) */
+        const LlModel* m = &e.ws.model;
+        size_t n_gdn = 0, conv_n = 0, state_n = 0, got;
+        uint32_t l;
+        for (l = 1; l <= m->h.n_blocks; l++) {
+            const LlfTensorMeta* mt = &m->metas[m->base_idx[l]];
+            if (mt[SLOT_SSM_CONV1D].size == 0) continue;
+            if (n_gdn++ == 0) {
+                conv_n = (size_t)mt[SLOT_SSM_CONV1D].shape[0] * mt[SLOT_SSM_CONV1D].shape[1];
+                state_n = (size_t)mt[SLOT_SSM_A].shape[0] * mt[SLOT_SSM_NORM].shape[0] * mt[SLOT_SSM_NORM].shape[0];
+            }
+        }
+        got = n_gdn * (conv_n + state_n);
+        if (got <= gdn_cap) {
+            memcpy(gdn_out, e.ssm_conv, n_gdn * conv_n * 4);
+            memcpy(gdn_out + n_gdn * conv_n, e.ssm_state, n_gdn * state_n * 4);
+            status[2] = (int)got;
+        }
     }
     engine_free(&e);
     return 0;

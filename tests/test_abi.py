@@ -137,13 +137,13 @@ def test_synth_normal_is_splitmix_box_muller(hiplib, golden):
 def test_gdn_rejects_bad_args(hiplib):
     F = ctypes.c_float
     # head_dim outside {64, 128}
-    rc = hiplib.yhip_gdn_chunk(P, P, 4096, P, P, 4096, P, 4096, P, P, 8, 16, 16, 256, F(1e-6), None, 0, None)
+    rc = hiplib.yhip_gdn_chunk(P, None, P, 4096, P, P, 4096, P, 4096, P, P, 8, 16, 16, 256, F(1e-6), None, 0, None)
     assert rc == -22 and "head_dim" in _err(hiplib)
     # strides that do not cover the heads
-    rc = hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 1024, P, 2048, P, P, 8, 16, 16, 128, F(1e-6), None, 0, None)
+    rc = hiplib.yhip_gdn_chunk(P, None, P, 2048, P, P, 1024, P, 2048, P, P, 8, 16, 16, 128, F(1e-6), None, 0, None)
     assert rc == -22 and "strides" in _err(hiplib)
     # misaligned q
-    rc = hiplib.yhip_gdn_chunk(P, P, 2048, ctypes.c_void_p(0x1004), P, 2048, P, 2048, P, P, 8, 16, 16, 128, F(1e-6),
+    rc = hiplib.yhip_gdn_chunk(P, None, P, 2048, ctypes.c_void_p(0x1004), P, 2048, P, 2048, P, P, 8, 16, 16, 128, F(1e-6),
                                None, 0, None)
     assert rc == -22 and "aligned" in _err(hiplib)
     # null pointers
@@ -152,9 +152,9 @@ def test_gdn_rejects_bad_args(hiplib):
     rc = hiplib.yhip_gdn_gates(P, None, P, P, P, 4, 16, None)
     assert rc == -22 and "null" in _err(hiplib)
     # no tokens is a no-op
-    assert hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 2048, P, 2048, P, P, 0, 16, 16, 128, F(1e-6), None, 0, None) == 0
+    assert hiplib.yhip_gdn_chunk(P, None, P, 2048, P, P, 2048, P, 2048, P, P, 0, 16, 16, 128, F(1e-6), None, 0, None) == 0
     # a workspace that is too small for the chunked form
-    rc = hiplib.yhip_gdn_chunk(P, P, 2048, P, P, 2048, P, 2048, P, P, 128, 16, 16, 128, F(1e-6), P, 4096, None)
+    rc = hiplib.yhip_gdn_chunk(P, None, P, 2048, P, P, 2048, P, 2048, P, P, 128, 16, 16, 128, F(1e-6), P, 4096, None)
     assert rc == -28 and "workspace" in _err(hiplib)
     assert hiplib.yhip_gdn_chunk_workspace(63, 16, 128) == 0
     # per (head, chunk): -W in bf16, Q~ rows, K~ in bf16 hi / lo, P, U^T (Delta^T), gamma_last + pad, the
@@ -162,21 +162,30 @@ def test_gdn_rejects_bad_args(hiplib):
     assert hiplib.yhip_gdn_chunk_workspace(4096, 16, 128) == 64 * 16 * (64 * 128 // 2 + 2 * 64 * 128 + 64 * 64
                                                                      + 64 * 128 + 4 + 128 * 128) * 4
     assert hiplib.yhip_gdn_gates(P, P, P, P, P, 0, 16, None) == 0
+    # an out-of-place state that overlaps the state (16 heads x 128 x 128 floats = 1 MiB) is refused
+    S0 = ctypes.c_void_p(0x4000000)
+    rc = hiplib.yhip_gdn_chunk(S0, ctypes.c_void_p(0x4000000 + 4096), P, 2048, P, P, 2048, P, 2048, P, P, 8, 16, 16,
+                               128, F(1e-6), None, 0, None)
+    assert rc == -22 and "S_out" in _err(hiplib)
 
 
 def test_gdn_neighbours_reject_bad_args(hiplib):
     F = ctypes.c_float
     X, O = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x900000)  # never dereferenced
     # conv: kwidth outside 1..8, strides, overlap of out and x, nulls; T = 0 is a no-op
-    rc = hiplib.yhip_gdn_conv(O, 512, X, 512, P, P, 4, 512, 9, 1, None)
+    rc = hiplib.yhip_gdn_conv(O, 512, X, 512, P, None, P, 4, 512, 9, 1, None)
     assert rc == -22 and "kwidth" in _err(hiplib)
-    rc = hiplib.yhip_gdn_conv(O, 512, X, 256, P, P, 4, 512, 4, 1, None)
+    rc = hiplib.yhip_gdn_conv(O, 512, X, 256, P, None, P, 4, 512, 4, 1, None)
     assert rc == -22 and "strides" in _err(hiplib)
-    rc = hiplib.yhip_gdn_conv(X, 512, X, 512, P, P, 4, 512, 4, 1, None)
+    rc = hiplib.yhip_gdn_conv(X, 512, X, 512, P, None, P, 4, 512, 4, 1, None)
     assert rc == -22 and "overlap" in _err(hiplib)
-    rc = hiplib.yhip_gdn_conv(O, 512, X, 512, None, P, 4, 512, 4, 1, None)
+    rc = hiplib.yhip_gdn_conv(O, 512, X, 512, None, None, P, 4, 512, 4, 1, None)
     assert rc == -22 and "null" in _err(hiplib)
-    assert hiplib.yhip_gdn_conv(O, 512, X, 512, P, P, 0, 512, 4, 1, None) == 0
+    assert hiplib.yhip_gdn_conv(O, 512, X, 512, P, None, P, 0, 512, 4, 1, None) == 0
+    # an out-of-place delay line must not overlap the old one (4 rows x 512 channels)
+    rc = hiplib.yhip_gdn_conv(O, 512, X, 512, ctypes.c_void_p(0x4000000), ctypes.c_void_p(0x4000000 + 8188), P, 4,
+                              512, 4, 1, None)
+    assert rc == -22 and "conv_state_out" in _err(hiplib)
     # gated norm: head_dim not a multiple of 64 or above 256, weight dtype, strides
     rc = hiplib.yhip_gdn_gated_norm(P, 2048, P, 2048, P, 2048, P, 1, 4, 16, 100, F(1e-6), None)
     assert rc == -22 and "head_dim" in _err(hiplib)
@@ -245,9 +254,9 @@ def test_gdn_decode_rejects_bad_args(hiplib):
     F = ctypes.c_float
     A, B = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x900000)  # delay lines, never dereferenced
 
-    def call(S=P, cin=A, cout=B, nk=16, nv=16, d=128, kw=4, ndt=1):
-        return hiplib.yhip_gdn_decode(S, cin, cout, P, P, P, P, P, P, P, P, P, ndt, nk, nv, d, kw, F(1e-6), F(1e-6),
-                                      None)
+    def call(S=P, cin=A, cout=B, nk=16, nv=16, d=128, kw=4, ndt=1, So=None):
+        return hiplib.yhip_gdn_decode(S, So, cin, cout, P, P, P, P, P, P, P, P, P, ndt, nk, nv, d, kw, F(1e-6),
+                                      F(1e-6), None)
 
     assert call(d=256) == -22 and "head_dim" in _err(hiplib)
     assert call(nk=4, nv=2) == -22 and "n_k_heads" in _err(hiplib)
@@ -256,6 +265,10 @@ def test_gdn_decode_rejects_bad_args(hiplib):
     assert call(S=ctypes.c_void_p(0x1004)) == -22 and "aligned" in _err(hiplib)
     assert call(cout=ctypes.c_void_p(0x100000 + 64)) == -22 and "overlaps" in _err(hiplib)
     assert call(cin=None) == -22 and "null" in _err(hiplib)
+    # an out-of-place state must not overlap the state (16 heads x 128 x 128 floats = 1 MiB)
+    S0 = ctypes.c_void_p(0x4000000)
+    assert call(S=S0, So=ctypes.c_void_p(0x4000000 + (1 << 20) - 16)) == -22 and "S_out" in _err(hiplib)
+    assert call(S=S0, So=ctypes.c_void_p(0x4000000 + (1 << 20) + 8)) == -22 and "S_out" in _err(hiplib)
 
 
 def test_decode_rope_rejects_bad_args(hiplib):

@@ -36,13 +36,14 @@ def e2e():
     lib.ye_make_model.restype = c_int
     lib.ye_make_model.argtypes = [c_char_p] + [c_uint32] * 9 + [c_char_p, c_size_t]
     lib.ye_make_model_q35.restype = c_int
-    lib.ye_make_model_q35.argtypes = [c_char_p] + [c_uint32] * 11 + [c_char_p, c_size_t]
+    lib.ye_make_model_q35.argtypes = [c_char_p] + [c_uint32] * 12 + [c_char_p, c_size_t]
     lib.ye_resume.restype = c_int
     lib.ye_resume.argtypes = [c_char_p, c_int, c_int, POINTER(c_uint32), c_int, c_int, c_int, c_char_p,
                               POINTER(c_float), POINTER(c_uint32), POINTER(c_int), c_char_p, c_size_t]
+    lib.device_hip_fail_mode.restype = None
     lib.ye_run.restype = c_int
-    lib.ye_run.argtypes = [c_char_p, c_int, c_int, c_int, POINTER(c_uint32), c_int, c_int, POINTER(c_float),
-                           POINTER(c_uint32), POINTER(c_int), c_char_p, c_size_t]
+    lib.ye_run.argtypes = [c_char_p, c_int, c_int, c_int, c_int, POINTER(c_uint32), c_int, c_int, POINTER(c_float),
+                           POINTER(c_uint32), POINTER(c_int), POINTER(c_float), c_size_t, c_char_p, c_size_t]
     return lib
 
 
@@ -57,26 +58,36 @@ def make_model(lib, path, blocks, hidden, heads, kv_heads, vocab=512, seq=256, s
     return path
 
 
-def make_q35(lib, path, blocks, hidden, heads, kv_heads, head_dim, n_k, n_v, hvd, vocab=512, seq=256, seed=11):
+def make_q35(lib, path, blocks, hidden, heads, kv_heads, head_dim, n_k, n_v, hvd, vocab=512, seq=256, seed=11,
+             ffn=0):
     """Block b is gated attention when b % 4 == 0, a GDN layer otherwise."""
     err = ctypes.create_string_buffer(256)
     rc = lib.ye_make_model_q35(str(path).encode(), blocks, hidden, heads, kv_heads, head_dim, n_k, n_v, hvd, vocab,
-                               seq, seed, err, 256)
+                               seq, seed, ffn, err, 256)
     assert rc == 0, err.value.decode()
     return path
 
 
-def run(lib, path, prompt, n_decode, use_hip, fail_after=-1, vocab=512):
+FAIL_BEFORE, FAIL_AFTER, FAIL_LOST = 0, 1, 2  # device_hip_fail_mode
+
+
+def run(lib, path, prompt, n_decode, use_hip, fail_after=-1, vocab=512, fail_mode=FAIL_BEFORE, gdn_cap=0):
+    """logits [(n_decode+1), vocab], tokens, status [bind, KV rows differing, GDN floats], message; with
+    gdn_cap > 0 also the engine's GDN delay lines then states at the end (status[2] floats)."""
     prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
     logits = np.zeros((n_decode + 1, vocab), dtype=np.float32)
     tokens = np.zeros(max(n_decode, 1), dtype=np.uint32)
-    status = np.zeros(2, dtype=np.int32)
+    status = np.zeros(3, dtype=np.int32)
+    gdn = np.zeros(max(gdn_cap, 1), dtype=np.float32)
     err = ctypes.create_string_buffer(256)
-    rc = lib.ye_run(str(path).encode(), int(use_hip), 0, fail_after,
+    rc = lib.ye_run(str(path).encode(), int(use_hip), 0, fail_after, fail_mode,
                     prompt.ctypes.data_as(POINTER(c_uint32)), len(prompt), n_decode,
                     logits.ctypes.data_as(POINTER(c_float)), tokens.ctypes.data_as(POINTER(c_uint32)),
-                    status.ctypes.data_as(POINTER(c_int)), err, 256)
+                    status.ctypes.data_as(POINTER(c_int)), gdn.ctypes.data_as(POINTER(c_float)) if gdn_cap else None,
+                    gdn_cap, err, 256)
     assert rc == 0, err.value.decode()
+    if gdn_cap:
+        return logits, tokens[:n_decode], status, err.value.decode(), gdn[: status[2]]
     return logits, tokens[:n_decode], status, err.value.decode()
 
 
@@ -136,7 +147,7 @@ def test_plugin_exports_every_declared_symbol(e2e):
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     names = re.findall(r"\b(device_\w+)\s*\(", text)
     assert set(names) == {"device_create_hip", "device_hip_kv_from_host", "device_hip_kv_to_host",
-                          "device_hip_fail_after"}
+                          "device_hip_fail_after", "device_hip_fail_mode"}
     for n in names:
         assert hasattr(e2e, n), n
 
@@ -280,21 +291,99 @@ def test_qwen35_end_to_end_matches_cpu(e2e, cuda, tmp_path, blocks, hidden, head
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fail_after", [0, 5])
-def test_qwen35_failure_hook(e2e, cuda, tmp_path, fail_after):
-    """fail_after 0: every block on the CPU, bit for bit.  fail_after 5: the
-    prefill's 4 blocks and one decode block on the GPU, then the CPU, which
-    continues from the GDN state and KV the backend mirrored to the host."""
+@pytest.mark.parametrize("fail_after,fail_mode", [
+    (0, FAIL_BEFORE),   # every block on the CPU
+    (5, FAIL_BEFORE),   # prefill (4 blocks) and one decode block on the GPU, then the CPU
+    # after the kernels ran: the prefill's second GDN layer (its state and delay line were
+    # sent up from the host), the first decode token's second GDN layer (state in HBM only,
+    # the fused one-launch token) and its attention layer
+    (1, FAIL_AFTER),
+    (5, FAIL_AFTER),
+    (7, FAIL_AFTER),
+])
+def test_qwen35_failure_hook(e2e, cuda, tmp_path, fail_after, fail_mode):
+    """The CPU continues from the GDN state and KV the backend holds: after a
+    failed block the HBM state is the one from before that block (the block
+    wrote the other buffer of the pair), so the CPU recompute applies the
+    block's tokens once."""
     path = make_q35(e2e, tmp_path / "q.llf", 4, 256, 4, 2, 256, 2, 4, 64)
     prompt = prompt_of(40)
     want, wt, _, _ = run(e2e, path, prompt, 4, use_hip=False)
-    got, gt, status, msg = run(e2e, path, prompt, 4, use_hip=True, fail_after=fail_after)
+    got, gt, status, msg = run(e2e, path, prompt, 4, use_hip=True, fail_after=fail_after, fail_mode=fail_mode)
     assert status[0] == 0, msg
     if fail_after == 0:
         assert np.array_equal(got, want) and np.array_equal(gt, wt)
     else:
-        assert max(rel_l2(got[i], want[i]) for i in range(5)) <= TOL
+        errs = [rel_l2(got[i], want[i]) for i in range(5)]
+        print(f"qwen35 fail_after={fail_after} mode={fail_mode}: max rel_l2 {max(errs):.3e}")
+        assert max(errs) <= TOL
         assert np.array_equal(gt, wt)
+
+
+@pytest.mark.gpu
+def test_qwen35_lost_state_is_reported(e2e, cuda, tmp_path, capfd):
+    """A device that fails and then cannot give the HBM-resident GDN state
+    back: the block must not continue on the stale host state.  The failing
+    block (the first decode token's second GDN layer) reports the loss and
+    every later logit is NaN, while the prefill's logits are the CPU's."""
+    path = make_q35(e2e, tmp_path / "q.llf", 4, 256, 4, 2, 256, 2, 4, 64)
+    prompt = prompt_of(40)
+    want, _, _, _ = run(e2e, path, prompt, 3, use_hip=False)
+    got, _, status, msg = run(e2e, path, prompt, 3, use_hip=True, fail_after=5, fail_mode=FAIL_LOST)
+    assert status[0] == 0, msg
+    assert rel_l2(got[0], want[0]) <= TOL
+    assert np.isnan(got[1:]).all()
+    assert "recurrent state of layer 2 is lost" in capfd.readouterr().err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fail_after", [1, 3])
+def test_engine_failure_after_launch_gives_cpu_result(e2e, cuda, tmp_path, fail_after):
+    """llama blocks failing after their kernels ran (the prefill's second
+    block, a decode block): the CPU recompute from the host KV is exact for
+    that block and the run stays within the tolerance."""
+    path = make_model(e2e, tmp_path / "m.llf", 2, 512, 8, 2)
+    prompt = prompt_of(40)
+    want, wt, _, _ = run(e2e, path, prompt, 4, use_hip=False)
+    got, gt, status, msg = run(e2e, path, prompt, 4, use_hip=True, fail_after=fail_after, fail_mode=FAIL_AFTER)
+    assert status[0] == 0, msg
+    assert max(rel_l2(got[i], want[i]) for i in range(5)) <= TOL
+    assert np.array_equal(gt, wt)
+
+
+@pytest.mark.gpu
+def test_qwen35_end_to_end_fifth_config_shapes(e2e, cuda, tmp_path):
+    """The hybrid group at its real head shapes through the engine: three
+    GDN layers of 16 heads (d_k = d_v = 128, conv width 4) and a gated
+    attention layer of 16 / 2 heads of 256, a 1040-token prompt (batched
+    prefill in the engine's 64-token chunks) and 16 greedy decode steps,
+    against the engine's own fwd_block_qwen35 on the CPU.  The FFN is narrow
+    (it is not on the path).  Beyond logits and tokens: the HBM KV equals the
+    host KV, the first GDN layer's conv delay line (its inputs are embedding
+    rows, the same bits on both engines) equals the CPU engine's bit for bit,
+    and every GDN state stays within the tolerance."""
+    blocks, hidden, heads, kv, hd, n_k, n_v, hvd = 4, 2048, 16, 2, 256, 16, 16, 128
+    path = make_q35(e2e, tmp_path / "q5.llf", blocks, hidden, heads, kv, hd, n_k, n_v, hvd, seq=1152, ffn=128)
+    prompt = prompt_of(1040)
+    n_dec = 16
+    conv_n, state_n, n_gdn = 4 * (2 * n_k + n_v) * hvd, n_v * hvd * hvd, 3
+    cap = n_gdn * (conv_n + state_n)
+    want, wt, _, _, gw = run(e2e, path, prompt, n_dec, use_hip=False, gdn_cap=cap)
+    got, gt, status, msg, gg = run(e2e, path, prompt, n_dec, use_hip=True, gdn_cap=cap)
+    assert status[0] == 0, msg
+    errs = [rel_l2(got[i], want[i]) for i in range(n_dec + 1)]
+    print(f"e2e qwen35 fifth-config shapes, prompt 1040: max rel_l2 {max(errs):.3e}, tokens {gt.tolist()}")
+    assert max(errs) <= TOL
+    assert np.array_equal(np.argmax(got, axis=1), np.argmax(want, axis=1))
+    assert np.array_equal(gt, wt)
+    assert status[1] == 0
+    assert gw.size == cap and gg.size == cap
+    conv_w, conv_g = gw[: n_gdn * conv_n].reshape(n_gdn, conv_n), gg[: n_gdn * conv_n].reshape(n_gdn, conv_n)
+    st_w, st_g = gw[n_gdn * conv_n:].reshape(n_gdn, state_n), gg[n_gdn * conv_n:].reshape(n_gdn, state_n)
+    assert np.array_equal(conv_g[0].view(np.uint32), conv_w[0].view(np.uint32))
+    for i in range(n_gdn):
+        assert rel_l2(conv_g[i], conv_w[i]) <= TOL
+        assert rel_l2(st_g[i], st_w[i]) <= TOL, i
 
 
 @pytest.mark.gpu

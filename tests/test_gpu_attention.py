@@ -367,9 +367,9 @@ def test_prefill_parity(cuda, oracle, nh, nkv, hd, ps, B, qdt, odt):
                                             (16, 2, 256, 130, 4.0), (8, 8, 64, 100, 8.0)])
 def test_prefill_f32_queries_large_scores(cuda, oracle, nh, nkv, hd, B, qsig):
     """fp32 queries that f16 cannot represent, scaled up to scores of std
-    ~qsig/2 (|s| up to ~20 at qsig 8): the kernel's QK^T takes q rounded to
-    f16, an error of about |s| * 2^-11 per score, which stays within the
-    tolerance at these magnitudes (the peaked softmax of qsig 8 included)."""
+    ~qsig/2 (|s| up to ~20 at qsig 8), the peaked softmax of qsig 8 included:
+    the kernel takes fp32 q as f16 hi + lo parts, so the scores keep
+    fp32-level error."""
     from yllm_amd.attention import attn_prefill
 
     kvd = nkv * hd
@@ -384,6 +384,54 @@ def test_prefill_f32_queries_large_scores(cuda, oracle, nh, nkv, hd, B, qsig):
     print(f"prefill f32 q sigma {qsig} {nh}/{nkv} d={hd}: head-0 score std {s0.std():.2f} max {np.abs(s0).max():.1f}, "
           f"rel_l2={err:.3e}, worst row {rows:.3e}")
     assert err <= TOL and rows <= 3 * TOL
+
+
+@pytest.mark.parametrize("nh,nkv,hd,ps,B,plain", [
+    (8, 2, 128, 448, 64, False),    # the engine's 64-token call: packed rows, split keys
+    (16, 2, 256, 200, 64, False),   # the gated layer's head shape, pair mode
+    (32, 4, 128, 0, 1024, True),    # 256 (query block, head) items: the plain mode
+    (8, 8, 64, 0, 200, False),
+])
+def test_prefill_f32_queries_competing_large_scores(cuda, oracle, nh, nkv, hd, ps, B, plain):
+    """Scores of 60..100 (and up to twice that where both picks are one key)
+    with two keys competing: every query is built from two keys of its kv
+    head in its causal range, q = c (k1/|k1|^2 + k2/|k2|^2) + noise, so both
+    score about c/sqrt(d) and its softmax splits between them.  A score error
+    of |s| 2^-11 (q rounded to f16) moves these outputs by ~1e-3 overall and
+    ~4e-3 in the worst rows (computed in fp64 when the case was built); the
+    kernel takes fp32 q as f16 hi + lo parts (two MFMAs), so the scores keep
+    fp32-level error and the outputs stay well within 1e-3 of the fp32
+    oracle."""
+    from yllm_amd.attention import attn_prefill
+
+    kvd = nkv * hd
+    L = ps + B
+    K, V = gen(2100 + hd, (L, kvd)), gen(2200 + hd, (L, kvd))
+    rng = np.random.default_rng(2300 + hd)
+    q = np.empty((B, nh * hd), np.float32)
+    for b in range(B):
+        for h in range(nh):
+            kv = h * nkv // nh
+            j1, j2 = rng.integers(0, ps + b + 1, size=2)
+            k1, k2 = K[j1, kv * hd:(kv + 1) * hd], K[j2, kv * hd:(kv + 1) * hd]
+            c = rng.uniform(60.0, 100.0) * np.sqrt(hd)
+            q[b, h * hd:(h + 1) * hd] = c * (k1 / np.dot(k1, k1) + k2 / np.dot(k2, k2)) + rng.normal(0.0, 0.05, hd)
+    cache, kc, vc = make_cache(cuda, oracle, K, V, nkv, hd)
+    top = np.array([np.max(q[b, :hd] @ K[: ps + b + 1, :hd].T) / np.sqrt(hd) for b in range(B)])  # head 0
+    got = attn_prefill(torch.from_numpy(q).to(cuda), cache, ps, nh).cpu().numpy()
+    if plain:
+        rows = [0, 1, 127, 128, 500, B - 1]
+        errs = [rel_l2(got[t], oracle.decode(q[t], kc[: ps + t + 1], vc[: ps + t + 1], ps + t, nh, nkv, hd))
+                for t in rows]
+        err = max(errs)
+    else:
+        want = oracle.prefill(q, kc, vc, ps, B, nh, nkv, hd)
+        err = rel_l2(got, want)
+        errs = [rel_l2(got[i], want[i]) for i in range(B)]
+    print(f"prefill f32 q competing keys {nh}/{nkv} d={hd} ps={ps} B={B}: head-0 top score {top.min():.1f}.."
+          f"{top.max():.1f} (median {np.median(top):.1f}), rel_l2={err:.3e}, worst row {max(errs):.3e}")
+    assert np.median(top) >= 40.0
+    assert err <= TOL and max(errs) <= 3 * TOL
 
 
 def test_prefill_gated_parity(cuda, oracle):

@@ -143,8 +143,8 @@ def test_config5_gated_attention_prefill_then_decode(cuda, oracle):
     store of 4096 prompt rows, causal prefill with bf16 queries and the
     sigmoid gate, bf16 out; then 256 decode steps, each the token's RoPE +
     store fused into a gated decode over keys 0..t (attn_decode_rope, the
-    bench's decode step; test_gpu_rope checks it against the two launches
-    bit for bit)."""
+    bench's decode step; test_gpu_rope checks its stored key against the
+    oracle bit for bit and its output against the two-launch path to 1e-5)."""
     from yllm_amd.attention import (ROPE_MROPE, LayerKV, attn_decode_rope, attn_prefill, decode_workspace,
                                     decode_workspace_bytes, round_bf16, rope_kv_store)
 

@@ -382,3 +382,55 @@ def test_gdn_prefill_then_decode_tokens(cuda, oracle):
     err_s = rel_l2(S.cpu().numpy(), S_want)
     print(f"prefill {T0} + decode {T1}: prefill y {err_pre:.2e}, decode y {err_dec:.2e}, state {err_s:.2e}")
     assert err_pre <= TOL and err_dec <= TOL and err_s <= TOL
+
+
+@pytest.mark.parametrize("T,chunked", [(1, True), (33, False), (130, True)],
+                         ids=["T1", "T33-tokenwise", "T130-chunked"])
+def test_gdn_out_of_place_state_matches_in_place(cuda, T, chunked):
+    """A state written to S_out (as the device backend alternates two
+    buffers) is the in-place result bit for bit, with the same outputs, and
+    the state before the call is left untouched; likewise the conv delay line
+    with state_out and the fused decode token."""
+    from yllm_amd.gdn import gdn_chunk, gdn_conv, gdn_decode
+
+    n_k, n_v, d = 4, 8, 128
+    q, k, v, alpha, beta_raw, S0 = inputs(4100 + T, T, n_k, n_v, d, s0_scale=0.05)
+    gate, beta = -np.abs(alpha) * 0.1, 1.0 / (1.0 + np.exp(-beta_raw))
+    S_ip, S_in, qd, kd, vd, gd, bd = to_dev(cuda, S0, S0, q[:T], k[:T], v[:T], gate[:T], beta[:T])
+    S_op = torch.full_like(S_in, float("nan"))
+    out_ip = gdn_chunk(S_ip, qd, kd, vd, gd, bd, n_k, chunked=chunked)
+    out_op = gdn_chunk(S_in, qd, kd, vd, gd, bd, n_k, chunked=chunked, S_out=S_op)
+    torch.cuda.synchronize()
+    assert torch.equal(out_ip.view(torch.int32), out_op.view(torch.int32))
+    assert torch.equal(S_op.view(torch.int32), S_ip.view(torch.int32))
+    assert np.array_equal(S_in.cpu().numpy().view(np.uint32), S0.view(np.uint32))
+
+    Tc, dim, kw = T + 7, 320, 4  # one run (T <= 8) and several
+    x, st, w = conv_inputs(4200 + T, Tc, dim, kw)
+    xd, st_ip, st_in, wd = to_dev(cuda, x, st, st, w)
+    st_op = torch.full_like(st_in, float("nan"))
+    for rows in (slice(0, min(Tc, 8)), slice(0, Tc)):
+        st_ip.copy_(st_in)
+        o_ip = gdn_conv(xd[rows], st_ip, wd)
+        o_op = gdn_conv(xd[rows], st_in, wd, state_out=st_op)
+        assert torch.equal(o_ip, o_op) and torch.equal(st_op, st_ip)
+        assert np.array_equal(st_in.cpu().numpy().view(np.uint32), st.view(np.uint32))
+
+    if T == 1:
+        n_v2, dd, kw2 = 16, 128, 4
+        conv_dim = (2 * 16 + n_v2) * dd
+        qkv, z = gen(4301, conv_dim, 1.0), gen(4302, n_v2 * dd, 1.0)
+        al, br = gen(4303, n_v2, 1.0), gen(4304, n_v2, 1.0)
+        cw = gen(4305, conv_dim * kw2, 0.5).reshape(conv_dim, kw2)
+        dt, a = gen(4306, n_v2, 0.5), -np.abs(gen(4307, n_v2, 1.0)) - 0.1
+        nw = (gen(4308, dd, 0.1) + 1.0).astype(np.float32)
+        line = gen(4309, kw2 * conv_dim, 1.0).reshape(kw2, conv_dim)
+        S2 = gen(4310, n_v2 * dd * dd, 0.05).reshape(n_v2, dd, dd)
+        t = to_dev(cuda, S2, S2, line, np.zeros_like(line), np.zeros_like(line), qkv, z, al, br, cw, dt, a, nw)
+        Sa, Sb, l0, la, lb, qkv_t, z_t, al_t, br_t, cw_t, dt_t, a_t, nw_t = t
+        Sb_out = torch.full_like(Sb, float("nan"))
+        ya = gdn_decode(Sa, l0, la, qkv_t, z_t, al_t, br_t, cw_t, dt_t, a_t, nw_t, 16)
+        yb = gdn_decode(Sb, l0, lb, qkv_t, z_t, al_t, br_t, cw_t, dt_t, a_t, nw_t, 16, S_out=Sb_out)
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb) and torch.equal(Sb_out, Sa) and torch.equal(la, lb)
+        assert np.array_equal(Sb.cpu().numpy().view(np.uint32), S2.view(np.uint32))

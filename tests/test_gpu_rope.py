@@ -283,7 +283,9 @@ def test_decode_rope_matches_oracle_and_two_launches(cuda, oracle, kind, nh, nkv
     print(f"decode_rope {kind} {nh}/{nkv} d={d} pos={pos}: rel_l2 vs oracle {err:.2e}, vs two launches "
           f"{err2:.2e}; token K row vs oracle <= {ulps_ref} ulp, vs two launches <= {ulps_two} ulp")
     assert err <= TOL_ATT and err2 <= 1e-5
-    assert ulps_ref <= 1 and ulps_two <= 1
+    # the fused launch rotates with the host's cosf / sinf of the reference's angles: the stored key is the
+    # oracle's bit for bit; the two-launch path (device sincosf) may be an ulp apart
+    assert ulps_ref == 0 and ulps_two <= 1
     # everything but the token's K row is bit for bit the two-launch path's
     Ka[:, pos, :] = Kb[:, pos, :]
     assert np.array_equal(Ka, Kb) and np.array_equal(Va, Vb)

@@ -44,9 +44,9 @@ SIGNATURES = {
     "yhip_attn_prefill_workspace": (c_size_t, [c_uint32, c_uint32, c_uint32, c_uint32, c_uint32]),
     "yhip_gdn_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
                               c_uint32, c_uint32, c_float, c_void_p]),
-    "yhip_gdn_chunk": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32,
-                               c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, c_float, c_void_p,
-                               c_size_t, c_void_p]),
+    "yhip_gdn_chunk": (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_uint32, c_void_p,
+                               c_uint32, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, c_float,
+                               c_void_p, c_size_t, c_void_p]),
     "yhip_gdn_chunk_workspace": (c_size_t, [c_uint32, c_uint32, c_uint32]),
     "yhip_gdn_gates": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_void_p]),
     "yhip_rope_kv_store": (c_int, [c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p,
@@ -55,9 +55,9 @@ SIGNATURES = {
     "yhip_o_proj_workspace": (c_size_t, [c_uint32, c_uint32, c_uint32, c_uint32, c_uint32]),
     "yhip_o_proj": (c_int, [c_void_p, c_uint32, c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, c_uint32, c_uint32,
                             c_uint32, c_void_p, c_size_t, c_void_p]),
-    "yhip_gdn_decode": (c_int, [c_void_p] * 12 + [c_uint32] * 5 + [c_float, c_float, c_void_p]),
-    "yhip_gdn_conv": (c_int, [c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_void_p, c_uint32, c_uint32,
-                              c_uint32, c_int, c_void_p]),
+    "yhip_gdn_decode": (c_int, [c_void_p] * 13 + [c_uint32] * 5 + [c_float, c_float, c_void_p]),
+    "yhip_gdn_conv": (c_int, [c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32,
+                              c_uint32, c_uint32, c_int, c_void_p]),
     "yhip_gdn_gated_norm": (c_int, [c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32,
                                     c_uint32, c_uint32, c_uint32, c_float, c_void_p]),
     "yhip_synth_normal": (None, [c_uint64, c_uint64, c_float, POINTER(c_float), c_uint64]),

@@ -357,10 +357,23 @@ int yhip_attn_prefill(void* att_out, uint32_t out_dtype, uint32_t out_stride, co
     return done(yhip::launch_prefill(a, (hipStream_t)stream), fn);
 }
 
-static int gdn_common(const char* fn, float* S, float* out, uint32_t out_stride, const float* q, const float* k,
-                      uint32_t qk_stride, const float* v, uint32_t v_stride, const float* gate, const float* beta,
-                      uint32_t T, uint32_t n_k, uint32_t n_v, uint32_t head_dim, float eps, void* workspace,
-                      size_t workspace_bytes, void* stream)
+// S_out: NULL (or S) updates S in place; otherwise the state after the call
+// goes to S_out, which must not overlap S, and S is left as it was.
+static int state_out_ok(const char* fn, const float* S, float*& S_out, size_t floats)
+{
+    if (!S_out) S_out = const_cast<float*>(S);
+    if (S_out == S) return 0;
+    if ((uintptr_t)S_out & 15) return fail(YHIP_EINVAL, "%s: S_out must be 16-byte aligned", fn);
+    const char *a0 = (const char*)S, *a1 = a0 + floats * sizeof(float);
+    const char *b0 = (const char*)S_out, *b1 = b0 + floats * sizeof(float);
+    if (b0 < a1 && a0 < b1) return fail(YHIP_EINVAL, "%s: S_out overlaps S without being S", fn);
+    return 0;
+}
+
+static int gdn_common(const char* fn, float* S, float* S_out, float* out, uint32_t out_stride, const float* q,
+                      const float* k, uint32_t qk_stride, const float* v, uint32_t v_stride, const float* gate,
+                      const float* beta, uint32_t T, uint32_t n_k, uint32_t n_v, uint32_t head_dim, float eps,
+                      void* workspace, size_t workspace_bytes, void* stream)
 {
     if (!S || !out || !q || !k || !v || !gate || !beta) return fail(YHIP_EINVAL, "%s: null pointer", fn);
     if (head_dim != 64 && head_dim != 128) return fail(YHIP_EINVAL, "%s: head_dim %u not in {64,128}", fn, head_dim);
@@ -370,9 +383,16 @@ static int gdn_common(const char* fn, float* S, float* out, uint32_t out_stride,
         return fail(YHIP_EINVAL, "%s: strides must cover the heads and be multiples of 4", fn);
     if (((uintptr_t)S | (uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15)
         return fail(YHIP_EINVAL, "%s: S, q, k, v must be 16-byte aligned", fn);
-    if (T == 0) return done(hipSuccess, "");
+    const size_t state_floats = (size_t)n_v * head_dim * head_dim;
+    if (int rc = state_out_ok(fn, S, S_out, state_floats)) return rc;
+    if (T == 0)  // no token: the state after the call is the state before it
+        return done(S_out == S ? hipSuccess
+                               : hipMemcpyAsync(S_out, S, state_floats * sizeof(float), hipMemcpyDeviceToDevice,
+                                                (hipStream_t)stream),
+                    fn);
     yhip::GdnArgs a = {};
     a.S = S;
+    a.S_out = S_out;
     a.out = out;
     a.q = q;
     a.k = k;
@@ -403,18 +423,18 @@ int yhip_gdn_step(float* S, float* out, const float* q, const float* k, const fl
                   const float* beta, uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps,
                   void* stream)
 {
-    return gdn_common("yhip_gdn_step", S, out, n_v_heads * head_dim, q, k, n_k_heads * head_dim, v,
+    return gdn_common("yhip_gdn_step", S, S, out, n_v_heads * head_dim, q, k, n_k_heads * head_dim, v,
                       n_v_heads * head_dim, gate, beta, 1, n_k_heads, n_v_heads, head_dim, l2_eps, nullptr, 0,
                       stream);
 }
 
-int yhip_gdn_chunk(float* S, float* out, uint32_t out_stride, const float* q, const float* k, uint32_t qk_stride,
-                   const float* v, uint32_t v_stride, const float* gate, const float* beta, uint32_t T,
-                   uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps, void* workspace,
-                   size_t workspace_bytes, void* stream)
+int yhip_gdn_chunk(float* S, float* S_out, float* out, uint32_t out_stride, const float* q, const float* k,
+                   uint32_t qk_stride, const float* v, uint32_t v_stride, const float* gate, const float* beta,
+                   uint32_t T, uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps,
+                   void* workspace, size_t workspace_bytes, void* stream)
 {
-    return gdn_common("yhip_gdn_chunk", S, out, out_stride, q, k, qk_stride, v, v_stride, gate, beta, T, n_k_heads,
-                      n_v_heads, head_dim, l2_eps, workspace, workspace_bytes, stream);
+    return gdn_common("yhip_gdn_chunk", S, S_out, out, out_stride, q, k, qk_stride, v, v_stride, gate, beta, T,
+                      n_k_heads, n_v_heads, head_dim, l2_eps, workspace, workspace_bytes, stream);
 }
 
 size_t yhip_gdn_chunk_workspace(uint32_t T, uint32_t n_v_heads, uint32_t head_dim)
@@ -519,7 +539,8 @@ int yhip_o_proj(float* x, uint32_t x_stride, const void* att, uint32_t att_dtype
     return done(hipSuccess, "");
 }
 
-int yhip_gdn_decode(float* S, const float* conv_in, float* conv_out, float* y, const float* qkv, const float* z,
+int yhip_gdn_decode(float* S, float* S_out, const float* conv_in, float* conv_out, float* y, const float* qkv,
+                    const float* z,
                     const float* alpha, const float* beta_raw, const float* conv_w, const float* dt_bias,
                     const float* ssm_a, const void* norm_w, uint32_t norm_w_dtype, uint32_t n_k_heads,
                     uint32_t n_v_heads, uint32_t head_dim, uint32_t kwidth, float l2_eps, float norm_eps,
@@ -535,6 +556,7 @@ int yhip_gdn_decode(float* S, const float* conv_in, float* conv_out, float* y, c
     if (kwidth < 1 || kwidth > 8) return fail(YHIP_EINVAL, "%s: kwidth %u not in 1..8", fn, kwidth);
     if (norm_w_dtype != YHIP_F32 && norm_w_dtype != YHIP_F16) return fail(YHIP_EINVAL, "%s: bad norm_w dtype", fn);
     if ((uintptr_t)S % 16) return fail(YHIP_EINVAL, "%s: S must be 16-byte aligned", fn);
+    if (int rc = state_out_ok(fn, S, S_out, (size_t)n_v_heads * head_dim * head_dim)) return rc;
     const uint64_t conv_dim = (uint64_t)(2 * n_k_heads + n_v_heads) * head_dim;
     if (conv_dim * kwidth > 0x7fffffffull) return fail(YHIP_EINVAL, "%s: too many channels", fn);
     const size_t line = (size_t)conv_dim * kwidth * sizeof(float);
@@ -542,6 +564,7 @@ int yhip_gdn_decode(float* S, const float* conv_in, float* conv_out, float* y, c
         return fail(YHIP_EINVAL, "%s: conv_out overlaps conv_in", fn);
     yhip::GdnDecodeArgs a = {};
     a.S = S;
+    a.S_out = S_out;
     a.conv_in = conv_in;
     a.conv_out = conv_out;
     a.qkv = qkv;
@@ -565,7 +588,8 @@ int yhip_gdn_decode(float* S, const float* conv_in, float* conv_out, float* y, c
 }
 
 int yhip_gdn_conv(float* out, uint32_t out_stride, const float* x, uint32_t x_stride, float* conv_state,
-                  const float* conv_w, uint32_t T, uint32_t dim, uint32_t kwidth, int silu, void* stream)
+                  float* conv_state_out, const float* conv_w, uint32_t T, uint32_t dim, uint32_t kwidth, int silu,
+                  void* stream)
 {
     const char* fn = "yhip_gdn_conv";
     if (!out || !x || !conv_state || !conv_w) return fail(YHIP_EINVAL, "%s: null pointer", fn);
@@ -573,7 +597,16 @@ int yhip_gdn_conv(float* out, uint32_t out_stride, const float* x, uint32_t x_st
     if (x_stride < dim || out_stride < dim) return fail(YHIP_EINVAL, "%s: strides must cover dim channels", fn);
     if ((uint64_t)T * (x_stride > out_stride ? x_stride : out_stride) > 0xffffffffull)
         return fail(YHIP_EINVAL, "%s: too many elements", fn);
-    if (T == 0) return done(hipSuccess, "");
+    const size_t line_bytes = (size_t)kwidth * dim * sizeof(float);
+    if (!conv_state_out) conv_state_out = conv_state;
+    if (conv_state_out != conv_state && (const char*)conv_state_out < (const char*)conv_state + line_bytes &&
+        (const char*)conv_state < (const char*)conv_state_out + line_bytes)
+        return fail(YHIP_EINVAL, "%s: conv_state_out overlaps conv_state without being it", fn);
+    if (T == 0)  // no token: the delay line after the call is the one before it
+        return done(conv_state_out == conv_state ? hipSuccess
+                                                  : hipMemcpyAsync(conv_state_out, conv_state, line_bytes,
+                                                                   hipMemcpyDeviceToDevice, (hipStream_t)stream),
+                    fn);
     {
         const uintptr_t o0 = (uintptr_t)out, o1 = o0 + ((size_t)(T - 1) * out_stride + dim) * sizeof(float);
         const uintptr_t x0 = (uintptr_t)x, x1 = x0 + ((size_t)(T - 1) * x_stride + dim) * sizeof(float);
@@ -583,6 +616,7 @@ int yhip_gdn_conv(float* out, uint32_t out_stride, const float* x, uint32_t x_st
     a.out = out;
     a.x = x;
     a.state = conv_state;
+    a.state_out = conv_state_out;
     a.w = conv_w;
     a.out_stride = out_stride;
     a.x_stride = x_stride;

@@ -43,6 +43,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace yhip {
 namespace {
 
@@ -60,6 +62,20 @@ __device__ inline f32x4 mfma16(const f16x8& a, const f16x8& b, const f32x4& c)
 
 __device__ inline float sigmoid_ref(float g) { return 1.0f / (1.0f + expf(-g)); }
 
+// The by-value RoPE table (~1 KB of kernel arguments) is an argument of the
+// ROPE instantiations only; the others take this stand-in with the same
+// member names, whose fields they never read.
+struct DecodeRopeNone {
+    const float* k;
+    const float* v;
+    uint16_t* kc;
+    uint16_t* vc;
+    uint32_t kind, n_rot;
+    float cs[2][1];
+};
+template <bool ROPE>
+using DecodeRopeArg = typename std::conditional<ROPE, DecodeRope, DecodeRopeNone>::type;
+
 // one 32-key block of K and V as MFMA operands of one lane
 template <int D>
 struct Frag {
@@ -75,7 +91,8 @@ struct Frag {
 // cache and substitutes them for the cache rows it loaded.  The cosines and
 // sines come from the host's cosf / sinf, as the reference computes them.
 template <int D, bool ROPE>
-__global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_split_kernel(DecodeArgs a, DecodeRope rp)
+__global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_split_kernel(DecodeArgs a,
+                                                                                            DecodeRopeArg<ROPE> rp)
 {
     constexpr int kWaves = waves_of<D>();
     constexpr int kThreads = 64 * kWaves;
@@ -549,7 +566,9 @@ template <int D, bool ROPE>
 hipError_t launch_decode_d(const DecodeArgs& a, const DecodeRope& r, hipStream_t st)
 {
     dim3 grid(a.n_splits, a.n_kv, a.n_seq);
-    hipLaunchKernelGGL((decode_split_kernel<D, ROPE>), grid, dim3(64 * waves_of<D>()), 0, st, a, r);
+    DecodeRopeArg<ROPE> rr{};
+    if constexpr (ROPE) rr = r;
+    hipLaunchKernelGGL((decode_split_kernel<D, ROPE>), grid, dim3(64 * waves_of<D>()), 0, st, a, rr);
     constexpr uint32_t slices = D < kMergeSlice ? 1 : D / kMergeSlice;
     if (a.n_splits > 1)
         hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.n_heads * slices, a.n_seq), dim3(256), 0, st, a);

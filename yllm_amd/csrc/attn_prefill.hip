@@ -82,6 +82,22 @@ __device__ inline void load_q8(f16x8& dst, const void* q, size_t off, uint32_t d
     }
 }
 
+// fp32 query elements off..off+7 as f16 hi + lo parts: hi = f16(x), lo =
+// f16(x - hi), so hi + lo carries ~22 bits of x and K.hi + K.lo (two MFMAs
+// into one fp32 accumulator) keeps the score at fp32-level error
+__device__ inline void load_q8_split(f16x8& hi, f16x8& lo, const float* q, size_t off)
+{
+    const f32x4 a = *reinterpret_cast<const f32x4*>(q + off);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(q + off + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        hi[j] = (_Float16)a[j];
+        lo[j] = (_Float16)(a[j] - (float)hi[j]);
+        hi[j + 4] = (_Float16)b[j];
+        lo[j + 4] = (_Float16)(b[j] - (float)hi[j + 4]);
+    }
+}
+
 __device__ inline void store_out4(void* out, size_t off, uint32_t dt, f32x4 v)
 {
     if (dt == kF32) {
@@ -248,12 +264,16 @@ __device__ inline void item_keys(const PrefillArgs& a, const PItem& I, uint32_t&
 
 // SPLIT: the split mode (one item per workgroup, packed rows, a key range
 // per split); a separate instantiation keeps the plain mode's registers.
-template <int D, int NG, bool SPLIT>
-__global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128) ? 2 : 1) void prefill_kernel(
+// QS: fp32 queries as f16 hi + lo parts, two score MFMAs per k-chunk (32 more
+// registers per lane at d = 128: one workgroup of 4 waves per CU, one key
+// group).
+template <int D, int NG, bool SPLIT, bool QS = false>
+__global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128 && !QS) ? 2 : 1) void prefill_kernel(
     PrefillArgs a)
 {
     static_assert(NG == 1 || NG == 2, "one or two key groups");
     static_assert(!SPLIT || NG == 1, "the split mode runs one key group");
+    static_assert(!QS || NG == 1, "split queries run one key group");
     // Pair mode (head_dim 256): a wave's 32 queries with all 256 dimensions
     // need 64 registers of Q and 128 of O, which leaves one wave per SIMD.
     // Instead two waves share 32 queries and each owns half the dimensions
@@ -443,6 +463,7 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
             else __builtin_amdgcn_s_waitcnt(0x0f70);
         };
         f16x8 qf[NKK];
+        f16x8 ql[QS ? NKK : 1];  // QS: the lo parts
         // the first loads of an item, see above: the K tiles, the first V
         // tile and the queries
         auto item_steps = [&](const PItem& I, uint32_t& t0) {
@@ -583,6 +604,7 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
                 for (int j = 0; j < NS; ++j) {
                     const f16x8 kf = read_k(par, j, kk);
                     S[j] = kk == 0 ? mfma32(kf, qf[0], f32x16{}) : mfma32(kf, qf[kk], S[j]);
+                    if constexpr (QS) S[j] = mfma32(kf, ql[kk], S[j]);
                 }
         };
         // running max update of the lane's query from tile scores S (raw, masked)
@@ -651,6 +673,7 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
                     if (n + 2 < NQ) kf[(n + 2) % 3] = read_k(kpar, (n + 2) % NS, (n + 2) / NS);
                     Snext[n % NS] = n < NS ? mfma32(kf[n % 3], qf[0], f32x16{})
                                            : mfma32(kf[n % 3], qf[n / NS], Snext[n % NS]);
+                    if constexpr (QS) Snext[n % NS] = mfma32(kf[n % 3], ql[n / NS], Snext[n % NS]);
                 }
 #pragma unroll
                 for (int u = 0; u < MAXP; ++u) {
@@ -685,7 +708,10 @@ __global__ __launch_bounds__(256 * NG * (D > 128 ? 2 : 1), (NG == 1 && D <= 128)
         if (a.q_dtype != kF16) {
             const size_t qbase = (size_t)myrow.b * a.q_stride + (size_t)myrow.h * D + hf * DQ + hh * 8;
 #pragma unroll
-            for (int kk = 0; kk < NKK; ++kk) load_q8(qf[kk], a.q, qbase + kk * 16, a.q_dtype);
+            for (int kk = 0; kk < NKK; ++kk) {
+                if constexpr (QS) load_q8_split(qf[kk], ql[kk], reinterpret_cast<const float*>(a.q), qbase + kk * 16);
+                else load_q8(qf[kk], a.q, qbase + kk * 16, a.q_dtype);
+            }
             if (NB == 2) dma_done();
         }
         if constexpr (NB > 2) lds_barrier();
@@ -969,7 +995,7 @@ int n_cus()
 // threads of a prefill workgroup: 4 waves per key group, 8 in pair mode
 constexpr int prefill_threads(int D, int NG) { return 256 * NG * (D > 128 ? 2 : 1); }
 
-template <int D, int NG>
+template <int D, int NG, bool QS>
 hipError_t launch_prefill_d(PrefillArgs a, hipStream_t st)
 {
     // the XCD mapping needs whole kv groups per XCD group and an equal share
@@ -985,8 +1011,8 @@ hipError_t launch_prefill_d(PrefillArgs a, hipStream_t st)
     // resident workgroups: one round of the grid fills every slot once
     static const int per_cu = [] {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<D, NG, false>, prefill_threads(D, NG), 0) !=
-                hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<D, NG, false, QS>, prefill_threads(D, NG),
+                                                         0) != hipSuccess ||
             n < 1)
             n = 1;
         return n;
@@ -1008,17 +1034,17 @@ hipError_t launch_prefill_d(PrefillArgs a, hipStream_t st)
         if (a.xcd_map) grid = grid / 8u * 8u;  // whole XCD groups (items are a multiple of 8)
         if (grid == 0) grid = items;
     }
-    hipLaunchKernelGGL((prefill_kernel<D, NG, false>), dim3(grid), dim3(prefill_threads(D, NG)), 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<D, NG, false, QS>), dim3(grid), dim3(prefill_threads(D, NG)), 0, st, a);
     return hipGetLastError();
 }
 
-template <int D>
+template <int D, bool QS>
 hipError_t launch_prefill_split_d(const PrefillArgs& a, hipStream_t st)
 {
     const uint32_t ipg = a.n_rb * (a.pack ? 1u : a.gmax);
     const uint32_t groups = a.n_kv * a.n_split;
     const uint32_t grid = (groups + 7u) / 8u * 8u * ipg;
-    hipLaunchKernelGGL((prefill_kernel<D, 1, true>), dim3(grid), dim3(prefill_threads(D, 1)), 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<D, 1, true, QS>), dim3(grid), dim3(prefill_threads(D, 1)), 0, st, a);
     if (a.n_split > 1) {
         const uint64_t threads = (uint64_t)a.B * a.n_heads * (D / 4);
         hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, st, a);
@@ -1153,19 +1179,25 @@ void prefill_bind_workspace(PrefillArgs& a, void* workspace)
 
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t st)
 {
+    // fp32 queries keep fp32-level scores (hi + lo parts, one key group)
+    const bool qs = a.q_dtype == kF32;
     if (a.split_mode) {
         switch (a.D) {
-        case 64: return launch_prefill_split_d<64>(a, st);
-        case 128: return launch_prefill_split_d<128>(a, st);
-        case 256: return launch_prefill_split_d<256>(a, st);
+        case 64: return qs ? launch_prefill_split_d<64, true>(a, st) : launch_prefill_split_d<64, false>(a, st);
+        case 128: return qs ? launch_prefill_split_d<128, true>(a, st) : launch_prefill_split_d<128, false>(a, st);
+        case 256: return qs ? launch_prefill_split_d<256, true>(a, st) : launch_prefill_split_d<256, false>(a, st);
         default: return hipErrorInvalidValue;
         }
     }
     const int ng = prefill_groups(a);
     switch (a.D) {
-    case 64: return ng == 2 ? launch_prefill_d<64, 2>(a, st) : launch_prefill_d<64, 1>(a, st);
-    case 128: return ng == 2 ? launch_prefill_d<128, 2>(a, st) : launch_prefill_d<128, 1>(a, st);
-    case 256: return launch_prefill_d<256, 1>(a, st);
+    case 64:
+        return qs ? launch_prefill_d<64, 1, true>(a, st)
+                  : ng == 2 ? launch_prefill_d<64, 2, false>(a, st) : launch_prefill_d<64, 1, false>(a, st);
+    case 128:
+        return qs ? launch_prefill_d<128, 1, true>(a, st)
+                  : ng == 2 ? launch_prefill_d<128, 2, false>(a, st) : launch_prefill_d<128, 1, false>(a, st);
+    case 256: return qs ? launch_prefill_d<256, 1, true>(a, st) : launch_prefill_d<256, 1, false>(a, st);
     default: return hipErrorInvalidValue;
     }
 }

@@ -56,7 +56,8 @@ __global__ __launch_bounds__(256, 1) void gdn_kernel(GdnArgs a)
     const float scale = 1.0f / sqrtf((float)D);
 
     // this lane's slice of column j0+lane
-    float* Sp = a.S + ((size_t)h * D + j0 + lane) * D + wave * SL;
+    const float* Sp = a.S + ((size_t)h * D + j0 + lane) * D + wave * SL;
+    float* So = a.S_out + ((size_t)h * D + j0 + lane) * D + wave * SL;
     float s[SL];
 #pragma unroll
     for (int i = 0; i < SL; i += 4) {
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(256, 1) void gdn_kernel(GdnArgs a)
         x[1] = s[i + 1];
         x[2] = s[i + 2];
         x[3] = s[i + 3];
-        *reinterpret_cast<f32x4*>(Sp + i) = x;
+        *reinterpret_cast<f32x4*>(So + i) = x;
     }
 }
 
@@ -614,7 +615,8 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
     // XCDs, so the slices of one head (b mod 8 fixed when n_v is a multiple
     // of 8) share an L2 and read the head's chunk data once
     const uint32_t h = blockIdx.x % a.n_v, jt = blockIdx.x / a.n_v, j0 = jt * J;
-    float* S = a.S + ((size_t)h * D + j0) * D;
+    const float* S = a.S + ((size_t)h * D + j0) * D;
+    float* So = a.S_out + ((size_t)h * D + j0) * D;
     const uint32_t nlast = a.n_chunks - 1;
 
     // one chunk's register operands of this wave
@@ -775,7 +777,7 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 #pragma unroll
     for (int bb = 0; bb < NBW; ++bb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S[(size_t)(4 * g + e) * D + 16 * (NBW * wave + bb) + r] = mt[bb][e];
+        for (int e = 0; e < 4; ++e) So[(size_t)(4 * g + e) * D + 16 * (NBW * wave + bb) + r] = mt[bb][e];
 }
 
 // The chunk outputs, all chunks at once: O = (Q~ Mc^T + P Delta) / sqrt(d)
@@ -884,7 +886,8 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnArgs a)
     const uint32_t h = blockIdx.x / nblk, j = (blockIdx.x % nblk) * 16 + col;
     const uint32_t kh = h % a.n_k;
     const float scale = 1.0f / sqrtf((float)D);
-    float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
+    const float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
+    float* So = a.S_out + ((size_t)h * D + j) * D + part * SL;
     const float* kp = a.k + (size_t)kh * D + part * SL;
     const float* qp = a.q + (size_t)kh * D + part * SL;
     float s[SL], k[SL], q[SL];
@@ -940,7 +943,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnArgs a)
         f32x4 x;
 #pragma unroll
         for (int e = 0; e < 4; ++e) x[e] = s[i + e];
-        *reinterpret_cast<f32x4*>(Sp + i) = x;
+        *reinterpret_cast<f32x4*>(So + i) = x;
     }
     if (part == 0) a.out[(size_t)h * D + j] = o;
 }

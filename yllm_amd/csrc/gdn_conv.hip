@@ -15,10 +15,11 @@
 // roundings in the reference's order (its ISO C build does not contract
 // them; here contraction is switched off in the kernel), so the conv values
 // are bit for bit the reference's; silu uses the
-// device expf.  The new delay line is written by a second launch, after
-// every read of the old one (the delay line is updated in place), except
-// for T <= kRun (a decode step), where each thread owns all of its channel's
-// tokens and writes the channel's new rows itself.
+// device expf.  The new delay line goes to state_out.  In place
+// (state_out == state) with T > kRun it is written by a second launch, after
+// every read of the old one; for T <= kRun (a decode step) each thread owns
+// all of its channel's tokens and writes the channel's new rows itself, and
+// out of place the thread of a channel's last run does.
 //
 // rmsnorm_gated (matvec.c:1007-1021, engine.c:845-847 per v-head):
 //     y = x * w * (1 / sqrtf(sum(x^2) / n + eps)) * (z / (1 + expf(-z)))
@@ -67,19 +68,23 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnConvArgs a)
         for (int i = 0; i < KW; ++i) acc = acc + xw[r + i] * w[i];
         a.out[(size_t)t * a.out_stride + ch] = a.silu ? acc / (1.0f + expf(-acc)) : acc;
     }
-    if (OWN_STATE) {
-        // T <= kRun: this thread read every input of its channel, so it
-        // writes the new delay line itself: row r = X(T - KW + r) = xw[T - 1 + r]
+    // The new delay line, row r = X(T - KW + r) = xw[T - 1 - t0 + r].  With
+    // T <= kRun (OWN_STATE) this thread read every input of its channel; out
+    // of place, the thread of the channel's last run holds every input the
+    // new rows need (they start at X(T - KW) >= X(t0 - KW + 1)) and no other
+    // thread reads state_out.  In place with several runs, the second
+    // launch writes it after every read of the old line.
+    if (OWN_STATE || (a.state_out != a.state && t0 + kRun >= a.T)) {
 #pragma unroll
         for (int j = 0; j < KW - 1 + kRun; ++j) {
-            const int r = j - ((int)a.T - 1);
-            if (r >= 0 && r < KW) a.state[(size_t)r * a.dim + ch] = xw[j];
+            const int r = j - ((int)a.T - 1 - (int)t0);
+            if (r >= 0 && r < KW) a.state_out[(size_t)r * a.dim + ch] = xw[j];
         }
     }
 }
 
-// new delay line: row r = X(T - kwidth + r).  One thread per channel reads
-// the channel's old rows before it writes any (in place).
+// new delay line of an in-place call: row r = X(T - kwidth + r).  One thread
+// per channel reads the channel's old rows before it writes any.
 template <int KW>
 __global__ __launch_bounds__(256) void gdn_conv_state_kernel(GdnConvArgs a)
 {
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(GdnConvArgs a)
         nw[r] = tau >= 0 ? a.x[(size_t)tau * a.x_stride + ch] : a.state[(size_t)(tau + KW) * a.dim + ch];
     }
 #pragma unroll
-    for (int r = 0; r < KW; ++r) a.state[(size_t)r * a.dim + ch] = nw[r];
+    for (int r = 0; r < KW; ++r) a.state_out[(size_t)r * a.dim + ch] = nw[r];
 }
 
 template <int W_F16>
@@ -133,7 +138,8 @@ hipError_t launch_conv_kw(const GdnConvArgs& a, hipStream_t st)
         hipLaunchKernelGGL((gdn_conv_kernel<KW, true>), grid, dim3(256), 0, st, a);
     } else {
         hipLaunchKernelGGL((gdn_conv_kernel<KW, false>), grid, dim3(256), 0, st, a);
-        hipLaunchKernelGGL(gdn_conv_state_kernel<KW>, dim3((a.dim + 255) / 256), dim3(256), 0, st, a);
+        if (a.state_out == a.state)  // in place: the new line after every read of the old one
+            hipLaunchKernelGGL(gdn_conv_state_kernel<KW>, dim3((a.dim + 255) / 256), dim3(256), 0, st, a);
     }
     return hipGetLastError();
 }

@@ -57,7 +57,8 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(GdnDecodeArgs a)
     const uint32_t col = tid / TPC, part = tid % TPC, j = blk * kCols + col;
 
     // 1. loads: state slice, then this thread's conv channels
-    float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
+    const float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
+    float* So = a.S_out + ((size_t)h * D + j) * D + part * SL;
     float s[SL];
 #pragma unroll
     for (int i = 0; i < SL; i += 4) {
@@ -172,7 +173,7 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(GdnDecodeArgs a)
         f32x4 x;
 #pragma unroll
         for (int e = 0; e < 4; ++e) x[e] = s[i + e];
-        *reinterpret_cast<f32x4*>(Sp + i) = x;
+        *reinterpret_cast<f32x4*>(So + i) = x;
     }
     if (part == 0) a.y[(size_t)h * D + j] = o;
 }
@@ -205,7 +206,8 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     const uint32_t key_dim = a.n_k * D;
     const uint32_t j = tid / TPC, part = tid % TPC;
 
-    float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
+    const float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
+    float* So = a.S_out + ((size_t)h * D + j) * D + part * SL;
     float s[SL];
 #pragma unroll
     for (int i = 0; i < SL; i += 4) {
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
         f32x4 x;
 #pragma unroll
         for (int e = 0; e < 4; ++e) x[e] = s[i + e];
-        *reinterpret_cast<f32x4*>(Sp + i) = x;
+        *reinterpret_cast<f32x4*>(So + i) = x;
     }
     // rmsnorm_gated over the head's D outputs (matvec.c:1007-1021), as
     // gdn_gated_norm_kernel computes it

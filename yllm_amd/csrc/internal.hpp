@@ -147,7 +147,8 @@ const char* launch_oproj(const OProjArgs& a, void* ws, size_t ws_bytes, hipStrea
 struct GdnConvArgs {
     float* out;             // [T] rows out_stride apart (not overlapping x)
     const float* x;         // [T] rows x_stride apart
-    float* state;           // delay line [kwidth][dim], updated in place
+    float* state;           // delay line [kwidth][dim] before the call
+    float* state_out;       // after the call: state itself (in place) or a buffer not overlapping it
     const float* w;         // [dim][kwidth]
     uint32_t out_stride, x_stride, T, dim, kwidth;
     int silu;
@@ -165,7 +166,8 @@ hipError_t launch_gdn_gated_norm(const GdnNormArgs& a, hipStream_t st);
 
 // ---- gdn_decode.hip ----
 struct GdnDecodeArgs {
-    float* S;               // [n_v][D][D] state, updated in place
+    const float* S;         // [n_v][D][D] state before the token
+    float* S_out;           // the state after it (S itself, or a buffer not overlapping it)
     const float* conv_in;   // delay line [kwidth][conv_dim] before the token
     float* conv_out;        // delay line after the token (not overlapping conv_in)
     const float* qkv;       // [conv_dim] projected row: q | k | v
@@ -184,7 +186,8 @@ hipError_t launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t st);
 
 // ---- gdn.hip ----
 struct GdnArgs {
-    float* S;                        // [n_v][D][D] state, S[h][j][i]
+    const float* S;                  // [n_v][D][D] state before the call, S[h][j][i]
+    float* S_out;                    // the state after the call (S itself, or a buffer not overlapping it)
     float* out;                      // [T][out_stride], head h at h*D
     const float* q;                  // [T][qk_stride], k-head at kh*D
     const float* k;

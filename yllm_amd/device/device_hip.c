@@ -22,22 +22,32 @@
  * save (cache.c:174-247) and the CPU path of any layer stay valid.
  *
  * ARCH_QWEN35 (fwd_block_qwen35, engine.c:736-982) is covered too.  Its
- * Gated-DeltaNet layers keep their recurrent state in HBM (yhip_gdn_chunk:
- * l2norm + state update, one token or a whole batch, chunked); the
- * projections, gates, conv1d delay line, gated RMSNorm and FFN stay on the
- * engine's operators.  After every GPU update the state is copied back to
- * e->ssm_state, so the host copy is always current as the KV is.  Its gated
- * attention layers (d = 256, QK-norm, M-RoPE on 64 dims, sigmoid gate) use
- * the same KV store and decode / prefill entry points with the gate fused.
- * The reference's batch forward for qwen35 runs token by token
- * (engine.c:723-734); here a batch is one GPU call per layer.
+ * Gated-DeltaNet layers run the whole mixer after the projections on the
+ * GPU -- gates, conv1d + silu, l2norm, the recurrence and the gated RMSNorm
+ * (yhip_gdn_gates, yhip_gdn_conv, yhip_gdn_chunk, yhip_gdn_gated_norm; a
+ * decode token in one yhip_gdn_decode launch) -- with the recurrent state
+ * and the conv delay line resident in HBM; the projections and the FFN stay
+ * on the engine's operators.  e->ssm_state / e->ssm_conv are brought up to
+ * date only when the host needs them.  Its gated attention layers (d = 256,
+ * QK-norm, M-RoPE on 64 dims, sigmoid gate) use the same KV store and
+ * decode / prefill entry points with the gate fused.  The reference's batch
+ * forward for qwen35 runs token by token (engine.c:723-734); here a batch is
+ * one GPU call per layer.
  *
  * Failure handling: any HIP error in a block marks the backend failed; that
  * block is recomputed with the saved CPU forward (e->x is untouched until
  * the attention output is back) and -1 is returned; every later block runs
  * on the CPU.  device_mode stays DEV_MODE_CPU: the host holds x and a valid
  * KV copy at every block boundary, so every CPU branch of the engine is
- * correct with this backend bound.
+ * correct with this backend bound.  The GDN state and delay line live in two
+ * HBM buffers each: a block reads one and writes the other, and only a
+ * block that succeeded makes its output current, so after a failure --
+ * before, during or after the kernels -- HBM still holds the state from
+ * before the block, which the fallback copies to the host.  If that copy
+ * fails too (a device that is gone), the host state is stale: the block
+ * reports the loss on stderr, fills its output rows with NaN so the caller
+ * sees it in the logits, and returns -2 instead of continuing on wrong
+ * state.
  */
 #include <hip/hip_runtime_api.h>
 
@@ -112,26 +122,30 @@ typedef struct {
      * sync_state_to_host) */
     uint8_t* state_loc;
     uint32_t n_gdn_slots, conv_chan, kwidth, n_v, n_k, hvd, value_dim;
+    /* per state slot two HBM states [n_v][hvd][hvd] and two delay lines
+     * [kwidth][conv_chan]: a block reads the current one (state_cur /
+     * conv_cur) and writes the other, which becomes current only when the
+     * block succeeded; conv_loc is where the current line is (STATE_*) */
     float* d_state;
+    uint8_t* state_cur;
+    float* d_conv;
+    uint8_t *conv_loc, *conv_cur;
     float* d_gb;        /* gate [cap][n_v], then beta [cap][n_v] */
+    float* d_xc;        /* the conv + silu output rows [cap][conv_chan] */
+    float* d_z;         /* the z rows [cap][value_dim] */
     void* d_gws;        /* chunked-form workspace for cap tokens */
     size_t gws_bytes;
     uint16_t* d_kvstage; /* engine-layout rows on their way to the host (kv_to_host) */
     uint32_t kvstage_rows;
-    float* h_conv;      /* one layer's conv delay line, kept to undo a failed block */
-    /* A decode token runs the whole GDN mixer in one launch (yhip_gdn_decode),
-     * the conv delay line in HBM: per state slot two lines [kwidth][conv_chan]
-     * (the kernel reads one and writes the other; conv_cur names the current
-     * one), conv_loc where the current line is (STATE_* as for the state), and
-     * per slot the layer's conv weights, dt_bias, ssm_a and norm weights
-     * (gdnw_n floats).  fused_decode is 0 when the norm weights are of a type
-     * the kernel does not take. */
-    float* d_conv;
-    uint8_t *conv_loc, *conv_cur;
+    /* per slot the layer's conv weights, dt_bias, ssm_a and norm weights
+     * (gdnw_n floats, the norm weights f32 or f16 per norm_dt); a decode
+     * token runs the whole GDN mixer in one launch (yhip_gdn_decode) when
+     * fused_decode is set (n_v >= n_k) */
     float* d_gdnw;
+    uint8_t* norm_dt;
     float* d_dec;       /* the token's qkv | z | alpha | beta_raw */
     float* h_raw;       /* a decode token's q | k before RoPE */
-    uint32_t gdnw_n, norm_dtype;
+    uint32_t gdnw_n;
     int fused_decode;
     /* staging for one call: q (or a GDN qkv row), k, v, gate, output */
     uint32_t cap, q_w, o_w;
@@ -148,7 +162,10 @@ typedef struct {
     FwdFn cpu_fwd;
     FwdBatchFn cpu_fwd_batch;
     int failed;
-    int fail_after;
+    /* test hook (device_hip_fail_after / device_hip_fail_mode): calls left
+     * before the simulated failure, where it strikes (FAIL_*), a pending
+     * failure for the block being computed, and a device whose copies fail */
+    int fail_after, fail_mode, fail_pending, dead;
 } HipCtx;
 
 static HipCtx* ctx_of(const Engine* e)
@@ -158,37 +175,67 @@ static HipCtx* ctx_of(const Engine* e)
 
 enum { STATE_HOST = 0, STATE_BOTH = 1, STATE_DEV = 2 };
 
-/* Make e->ssm_state of GDN layer `layer` current when HBM holds its state:
- * one synchronous copy.  Returns 0, or -1 when the copy fails (after a GPU
- * failure the layers updated on the GPU since their last copy keep a stale
- * host state). */
-/* Make e->ssm_conv of GDN layer `layer` current when the fused decode token
- * left the current delay line in HBM. */
+/* where the test hook strikes (device_hip_fail_mode) */
+enum { FAIL_BEFORE = 0, FAIL_AFTER = 1, FAIL_LOST = 2 };
+
+static size_t state_elems(const HipCtx* c)
+{
+    return (size_t)c->n_v * c->hvd * c->hvd;
+}
+
+static size_t conv_elems(const HipCtx* c)
+{
+    return (size_t)c->kwidth * c->conv_chan;
+}
+
+/* HBM state / delay line `which` (0 or 1) of a state slot */
+static float* state_buf(const HipCtx* c, int32_t slot, int which)
+{
+    return c->d_state + ((size_t)slot * 2 + (size_t)which) * state_elems(c);
+}
+
+static float* conv_buf(const HipCtx* c, int32_t slot, int which)
+{
+    return c->d_conv + ((size_t)slot * 2 + (size_t)which) * conv_elems(c);
+}
+
+/* device -> host copy of n bytes, then wait; -1 when it fails (or the test
+ * hook has taken the device away) */
+static int copy_back(HipCtx* c, void* dst, const void* src, size_t n)
+{
+    if (c->dead) return -1;
+    if (hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        return -1;
+    return 0;
+}
+
+/* Make e->ssm_conv of GDN layer `layer` current when HBM holds its current
+ * delay line.  Returns 0, or -1 when the copy fails. */
 static int sync_conv_to_host(Engine* e, HipCtx* c, uint32_t layer)
 {
     const uint32_t li = layer - c->first;
     const int32_t slot = c->gdn_slot[li];
-    const size_t conv_n = (size_t)c->kwidth * c->conv_chan;
     if (slot < 0 || !c->conv_loc || c->conv_loc[slot] != STATE_DEV) return 0;
-    if (hipMemcpyAsync(e->ssm_conv + (size_t)c->gdn_ord[li] * conv_n,
-                       c->d_conv + ((size_t)slot * 2 + c->conv_cur[slot]) * conv_n, conv_n * 4,
-                       hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
-        hipStreamSynchronize(c->stream) != hipSuccess)
+    if (copy_back(c, e->ssm_conv + (size_t)c->gdn_ord[li] * conv_elems(c), conv_buf(c, slot, c->conv_cur[slot]),
+                  conv_elems(c) * 4) != 0)
         return -1;
     c->conv_loc[slot] = STATE_BOTH;
     return 0;
 }
 
+/* Make e->ssm_state (and e->ssm_conv) of GDN layer `layer` current when HBM
+ * holds its current state: one synchronous copy each.  Returns 0, or -1 when
+ * a copy fails: the host then keeps the state of its last copy, which is
+ * stale by every GPU update since. */
 static int sync_state_to_host(Engine* e, HipCtx* c, uint32_t layer)
 {
     const uint32_t li = layer - c->first;
     const int32_t slot = c->gdn_slot[li];
-    const size_t state_n = (size_t)c->n_v * c->hvd * c->hvd;
     if (sync_conv_to_host(e, c, layer) != 0) return -1;
     if (slot < 0 || c->state_loc[slot] != STATE_DEV) return 0;
-    if (hipMemcpyAsync(e->ssm_state + (size_t)c->gdn_ord[li] * state_n, c->d_state + (size_t)slot * state_n,
-                       state_n * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
-        hipStreamSynchronize(c->stream) != hipSuccess)
+    if (copy_back(c, e->ssm_state + (size_t)c->gdn_ord[li] * state_elems(c), state_buf(c, slot, c->state_cur[slot]),
+                  state_elems(c) * 4) != 0)
         return -1;
     c->state_loc[slot] = STATE_BOTH;
     return 0;
@@ -243,6 +290,8 @@ static void free_staging(HipCtx* c)
     dfree(c->d_out);
     dfree(c->d_rows);
     dfree(c->d_gb);
+    dfree(c->d_xc);
+    dfree(c->d_z);
     dfree(c->d_gws);
     free(c->h_n);
     free(c->h_q);
@@ -252,7 +301,7 @@ static void free_staging(HipCtx* c)
     free(c->h_ab);
     free(c->h_o);
     free(c->h_x);
-    c->d_q = c->d_k = c->d_v = c->d_g = c->d_out = c->d_gb = NULL;
+    c->d_q = c->d_k = c->d_v = c->d_g = c->d_out = c->d_gb = c->d_xc = c->d_z = NULL;
     c->d_rows = NULL;
     c->d_gws = NULL;
     c->h_n = c->h_q = c->h_z = c->h_k = c->h_v = c->h_ab = c->h_o = c->h_x = NULL;
@@ -273,13 +322,14 @@ static void release(HipCtx* c)
     free(c->gdn_slot);
     free(c->gdn_ord);
     free(c->state_loc);
+    free(c->state_cur);
     dfree(c->d_kvstage);
-    free(c->h_conv);
     dfree(c->d_conv);
     dfree(c->d_gdnw);
     dfree(c->d_dec);
     free(c->conv_loc);
     free(c->conv_cur);
+    free(c->norm_dt);
     free(c->h_raw);
     {
         int id = c->device_id;
@@ -313,8 +363,11 @@ static int ensure_cap(HipCtx* c, uint32_t rows)
         c->h_x = (float*)malloc((size_t)rows * c->hidden * 4);
         if (!c->h_n || !c->h_q || !c->h_z || !c->h_k || !c->h_v || !c->h_o || !c->h_x) return -1;
         if (c->n_gdn_slots) {
-            c->h_ab = (float*)malloc((size_t)rows * 3 * c->n_v * 4);
-            if (!c->h_ab || hipMalloc((void**)&c->d_gb, (size_t)rows * 2 * c->n_v * 4) != hipSuccess) return -1;
+            c->h_ab = (float*)malloc((size_t)rows * 2 * c->n_v * 4);
+            if (!c->h_ab || hipMalloc((void**)&c->d_gb, (size_t)rows * 2 * c->n_v * 4) != hipSuccess ||
+                hipMalloc((void**)&c->d_xc, (size_t)rows * c->conv_chan * 4) != hipSuccess ||
+                hipMalloc((void**)&c->d_z, (size_t)rows * c->value_dim * 4) != hipSuccess)
+                return -1;
             c->gws_bytes = yhip_gdn_chunk_workspace(rows, c->n_v, c->hvd);
             if (c->gws_bytes && hipMalloc(&c->d_gws, c->gws_bytes) != hipSuccess) return -1;
         }
@@ -358,16 +411,35 @@ static int catch_up(HipCtx* c, Engine* e, uint32_t layer, uint32_t upto)
 
 /* Whether this block call may use the GPU.  Returns 1 (yes), 0 (no: the
  * layer is outside the resident range, or the backend failed earlier) or -1
- * (the GPU fails at this call: the test hook's count ran out). */
+ * (the GPU fails at this call before any GPU work: the test hook's count ran
+ * out in FAIL_BEFORE mode).  In the other modes the block runs its GPU work
+ * and then fails at gpu_after (fail_pending). */
 static int gpu_turn(HipCtx* c, uint32_t layer, uint32_t pos_end)
 {
     if (layer < c->first || layer > c->last || pos_end > c->max_seq || c->failed) return 0;
     if (c->fail_after == 0) {
-        c->failed = 1;
-        return -1;
+        c->fail_after = -1;
+        if (c->fail_mode == FAIL_BEFORE) {
+            c->failed = 1;
+            return -1;
+        }
+        c->fail_pending = 1;
+        return 1;
     }
     if (c->fail_after > 0) c->fail_after--;
     return 1;
+}
+
+/* The point of a block after its kernels ran and its output came back: 0,
+ * or -1 when the test hook fails the block here (as a lost result copy
+ * would; FAIL_LOST also takes the device away for every later copy). */
+static int gpu_after(HipCtx* c)
+{
+    if (!c->fail_pending) return 0;
+    c->fail_pending = 0;
+    hipStreamSynchronize(c->stream);
+    if (c->fail_mode == FAIL_LOST) c->dead = 1;
+    return -1;
 }
 
 static const uint8_t* layer_base(const Engine* e, uint32_t layer)
@@ -455,7 +527,8 @@ static int gpu_decode(HipCtx* c, Engine* e, uint32_t layer, uint32_t pos, const 
         return -1;
     c->dev_len[c->kv_slot[layer - c->first]] = pos + 1;
     if (hipMemcpyAsync(att_out, c->d_out, nq * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return -1;
-    return hipStreamSynchronize(c->stream) == hipSuccess ? 0 : -1;
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return -1;
+    return gpu_after(c);
 }
 
 /* ---- ARCH_QWEN35 blocks (fwd_block_qwen35, engine.c:736-982) ---------- */
@@ -471,112 +544,77 @@ static void proj(float* y, const float* x, const uint8_t* base, const LlfTensorM
         matmul_batch(y, x, base + t->offset, out, in, t->dtype, B);
 }
 
-static float sigmoidf_(float x)
-{
-    return 1.0f / (1.0f + expf(-x));
-}
-
 /* GDN layer, engine.c:764-850 up to the output projection: c->h_n (normed
- * rows) -> c->h_x (ssm_out rows).  The conv delay line advances on the host;
- * the recurrence (l2norm of q/k, decay, delta rule, output) runs on the HBM
- * state.  On failure the delay line is restored and -1 returned. */
+ * rows) -> c->h_x (ssm_out rows).  The projections run on the host; the
+ * mixer after them on the GPU, from the HBM state and delay line current
+ * before the call into the other buffer of each pair.  Only when the
+ * output is back do those buffers become current, so a failed call leaves
+ * the state from before it.  Returns 0 or -1. */
 static int q35_gdn(Engine* e, HipCtx* c, uint32_t layer, uint32_t B, const uint8_t* base, const LlfTensorMeta* mt,
                    float eps)
 {
     const uint32_t hidden = c->hidden, cc = c->conv_chan, vd = c->value_dim, nv = c->n_v, hvd = c->hvd;
     const uint32_t kd = c->n_k * hvd, li = layer - c->first;
-    const size_t state_n = (size_t)nv * hvd * hvd;
+    const size_t state_n = state_elems(c), conv_n = conv_elems(c);
     const int32_t slot = c->gdn_slot[li];
-    float* conv_state = e->ssm_conv + (size_t)c->gdn_ord[li] * c->kwidth * cc;
-    float* host_S = e->ssm_state + (size_t)c->gdn_ord[li] * state_n;
-    float* dS = c->d_state + (size_t)slot * state_n;
-    const float* dt = (const float*)(base + mt[SLOT_SSM_DT].offset);
-    const float* a = (const float*)(base + mt[SLOT_SSM_A].offset);
-    float *qkv = c->h_q, *z = c->h_z, *alpha = c->h_ab, *beta = alpha + (size_t)B * nv, *gate = beta + (size_t)B * nv;
-    uint32_t b, h, ch;
+    const int scur = c->state_cur[slot], ccur = c->conv_cur[slot];
+    float *S_in = state_buf(c, slot, scur), *S_out = state_buf(c, slot, 1 - scur);
+    float *line_in = conv_buf(c, slot, ccur), *line_out = conv_buf(c, slot, 1 - ccur);
+    const float* w = c->d_gdnw + (size_t)slot * c->gdnw_n;  /* conv_w | dt_bias | ssm_a | norm_w */
+    const uint32_t ndt = c->norm_dt[slot];
+    float *qkv = c->h_q, *z = c->h_z, *alpha = c->h_ab, *beta = alpha + (size_t)B * nv;
     int ok;
 
     proj(qkv, c->h_n, base, &mt[SLOT_QKV], cc, hidden, B);
     proj(z, c->h_n, base, &mt[SLOT_GATE_ATTN], vd, hidden, B);
     proj(alpha, c->h_n, base, &mt[SLOT_SSM_ALPHA], nv, hidden, B);
     proj(beta, c->h_n, base, &mt[SLOT_SSM_BETA], nv, hidden, B);
+    /* the state and the delay line go up only when the host holds the
+     * current ones (first call, after a CPU block or a restore) */
+    ok = (c->state_loc[slot] != STATE_HOST ||
+          hipMemcpyAsync(S_in, e->ssm_state + (size_t)c->gdn_ord[li] * state_n, state_n * 4, hipMemcpyHostToDevice,
+                         c->stream) == hipSuccess) &&
+         (c->conv_loc[slot] != STATE_HOST ||
+          hipMemcpyAsync(line_in, e->ssm_conv + (size_t)c->gdn_ord[li] * conv_n, conv_n * 4, hipMemcpyHostToDevice,
+                         c->stream) == hipSuccess);
+    if (!ok) return -1;
     if (B == 1 && c->fused_decode) {
         /* one launch: gates, conv1d_update + silu, l2 norms, the state update
-         * and rmsnorm_gated (engine.c:788-847), the delay line and the state
-         * in HBM; beta follows alpha in c->h_ab */
-        const size_t conv_n = (size_t)c->kwidth * cc;
-        float* lines = c->d_conv + (size_t)slot * 2 * conv_n;
-        const float* w = c->d_gdnw + (size_t)slot * c->gdnw_n;
-        const int cur = c->conv_cur[slot];
+         * and rmsnorm_gated (engine.c:788-847); beta follows alpha in h_ab */
         float* d_z = c->d_dec + cc;
         float* d_ab = d_z + vd;
-        ok = (c->state_loc[slot] != STATE_HOST ||
-              hipMemcpyAsync(dS, host_S, state_n * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess) &&
-             (c->conv_loc[slot] != STATE_HOST ||
-              hipMemcpyAsync(lines + cur * conv_n, conv_state, conv_n * 4, hipMemcpyHostToDevice, c->stream) ==
-                  hipSuccess) &&
-             hipMemcpyAsync(c->d_dec, qkv, (size_t)cc * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+        ok = hipMemcpyAsync(c->d_dec, qkv, (size_t)cc * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
              hipMemcpyAsync(d_z, z, (size_t)vd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
              hipMemcpyAsync(d_ab, alpha, (size_t)2 * nv * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
-             yhip_gdn_decode(dS, lines + cur * conv_n, lines + (1 - cur) * conv_n, c->d_out, c->d_dec, d_z, d_ab,
-                             d_ab + nv, w, w + conv_n, w + conv_n + nv, w + conv_n + 2 * nv, c->norm_dtype, c->n_k,
-                             nv, hvd, c->kwidth, eps, eps, c->stream) == YHIP_OK &&
-             hipMemcpyAsync(c->h_o, c->d_out, (size_t)vd * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
-             hipStreamSynchronize(c->stream) == hipSuccess;
-        if (!ok) return -1;
-        c->state_loc[slot] = STATE_DEV;
-        c->conv_loc[slot] = STATE_DEV;
-        c->conv_cur[slot] = (uint8_t)(1 - cur);
-        proj(c->h_x, c->h_o, base, &mt[SLOT_SSM_OUT], hidden, vd, B);
-        return 0;
+             yhip_gdn_decode(S_in, S_out, line_in, line_out, c->d_out, c->d_dec, d_z, d_ab, d_ab + nv, w, w + conv_n,
+                             w + conv_n + nv, w + conv_n + 2 * nv, ndt, c->n_k, nv, hvd, c->kwidth, eps, eps,
+                             c->stream) == YHIP_OK;
+    } else {
+        /* the batch (or a decode token when n_v < n_k): the gates in place
+         * (alpha's rows become the log-decay gate, beta's the sigmoid,
+         * engine.c:788-793), conv1d + silu of every row (805-812), the
+         * recurrence over the rows in order with l2norm (826-831, chunked
+         * from 64 rows), rmsnorm_gated per v head (840-850) */
+        float *d_gate = c->d_gb, *d_beta = c->d_gb + (size_t)B * nv;
+        ok = hipMemcpyAsync(c->d_q, qkv, (size_t)B * cc * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+             hipMemcpyAsync(c->d_z, z, (size_t)B * vd * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+             hipMemcpyAsync(d_gate, alpha, (size_t)2 * B * nv * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+             yhip_gdn_gates(d_beta, d_gate, d_gate, w + conv_n, w + conv_n + nv, B, nv, c->stream) == YHIP_OK &&
+             yhip_gdn_conv(c->d_xc, cc, c->d_q, cc, line_in, line_out, w, B, cc, c->kwidth, 1, c->stream) ==
+                 YHIP_OK &&
+             yhip_gdn_chunk(S_in, S_out, c->d_out, vd, c->d_xc, c->d_xc + kd, cc, c->d_xc + 2 * kd, cc, d_gate,
+                            d_beta, B, c->n_k, nv, hvd, eps, c->d_gws, c->gws_bytes, c->stream) == YHIP_OK &&
+             yhip_gdn_gated_norm(c->d_out, vd, c->d_out, vd, c->d_z, vd, w + conv_n + 2 * nv, ndt, B, nv, hvd, eps,
+                                 c->stream) == YHIP_OK;
     }
-    /* the host runs the conv: it needs the current delay line */
-    if (sync_conv_to_host(e, c, layer) != 0) return -1;
-    if (c->conv_loc) c->conv_loc[slot] = STATE_HOST;
-    for (b = 0; b < B; b++) {
-        float* bb = beta + (size_t)b * nv;
-        const float* ab = alpha + (size_t)b * nv;
-        float* gb = gate + (size_t)b * nv;
-        for (h = 0; h < nv; h++) {
-            bb[h] = sigmoidf_(bb[h]);
-            gb[h] = log1pf(expf(ab[h] + dt[h])) * a[h];
-        }
-    }
-    memcpy(c->h_conv, conv_state, (size_t)c->kwidth * cc * 4);
-    for (b = 0; b < B; b++) {
-        float* row = qkv + (size_t)b * cc;
-        conv1d_update(conv_state, row, base + mt[SLOT_SSM_CONV1D].offset, cc, c->kwidth);
-        for (ch = 0; ch < cc; ch++) row[ch] = row[ch] * sigmoidf_(row[ch]);
-    }
-
-    /* the state lives in HBM between calls: it is sent only when the host
-     * holds the current one (first call, after a CPU block or a restore) and
-     * comes back only when the host needs it (sync_state_to_host) */
-    ok = (c->state_loc[slot] != STATE_HOST ||
-          hipMemcpyAsync(dS, host_S, state_n * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess) &&
-         hipMemcpyAsync(c->d_q, qkv, (size_t)B * cc * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
-         hipMemcpyAsync(c->d_gb, gate, (size_t)B * nv * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
-         hipMemcpyAsync(c->d_gb + (size_t)B * nv, beta, (size_t)B * nv * 4, hipMemcpyHostToDevice, c->stream) ==
-             hipSuccess;
     ok = ok &&
-         yhip_gdn_chunk(dS, c->d_out, vd, c->d_q, c->d_q + kd, cc, c->d_q + 2 * kd, cc, c->d_gb,
-                        c->d_gb + (size_t)B * nv, B, c->n_k, nv, hvd, eps, c->d_gws, c->gws_bytes,
-                        c->stream) == YHIP_OK &&
          hipMemcpyAsync(c->h_o, c->d_out, (size_t)B * vd * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
-         hipStreamSynchronize(c->stream) == hipSuccess;
-    if (!ok) {
-        memcpy(conv_state, c->h_conv, (size_t)c->kwidth * cc * 4);
-        return -1;
-    }
+         hipStreamSynchronize(c->stream) == hipSuccess && gpu_after(c) == 0;
+    if (!ok) return -1;
+    c->state_cur[slot] = (uint8_t)(1 - scur);
+    c->conv_cur[slot] = (uint8_t)(1 - ccur);
     c->state_loc[slot] = STATE_DEV;
-
-    /* gated RMSNorm per v head (engine.c:840-850), then ssm_out */
-    for (b = 0; b < B; b++)
-        for (h = 0; h < nv; h++) {
-            float* o = c->h_o + (size_t)b * vd + (size_t)h * hvd;
-            rmsnorm_gated(o, o, base + mt[SLOT_SSM_NORM].offset, z + (size_t)b * vd + (size_t)h * hvd, hvd, eps,
-                          mt[SLOT_SSM_NORM].dtype);
-        }
+    c->conv_loc[slot] = STATE_DEV;
     proj(c->h_x, c->h_o, base, &mt[SLOT_SSM_OUT], hidden, vd, B);
     return 0;
 }
@@ -638,7 +676,7 @@ static int q35_attn(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_
     c->dev_len[c->kv_slot[layer - c->first]] = pos0 + B;
     ok = ok &&
          hipMemcpyAsync(c->h_o, c->d_out, (size_t)B * qd * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
-         hipStreamSynchronize(c->stream) == hipSuccess;
+         hipStreamSynchronize(c->stream) == hipSuccess && gpu_after(c) == 0;
     if (!ok) return -1;
     proj(c->h_x, c->h_o, base, &mt[SLOT_O], hidden, qd, B);
     return 0;
@@ -688,20 +726,36 @@ static int q35_block(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32
 }
 
 /* fwd_block / fwd_block_batch for qwen35.  A GDN block computed on the CPU
- * first takes the current state from HBM (when HBM holds it), and leaves the
- * HBM state stale; it is re-sent before the layer's next GPU call. */
+ * first takes the current state and delay line from HBM (when HBM holds
+ * them; after a failed GPU block these are the ones from before it) and
+ * leaves the HBM copies stale; they are re-sent before the layer's next GPU
+ * call.  When that copy fails the host state is stale: the block output
+ * becomes NaN (the loss shows in the logits instead of as wrong tokens), a
+ * message goes to stderr and the block returns -2. */
 static int q35_fwd(Engine* e, HipCtx* c, uint32_t layer, uint32_t pos0, uint32_t B, int batch)
 {
+    float* X = batch ? e->pb : e->x;
     int turn = B > c->cap ? 0 : gpu_turn(c, layer, pos0 + B);
-    if (turn > 0 && q35_block(e, c, layer, pos0, B, batch ? e->pb : e->x) == 0) return 0;
+    if (turn > 0 && q35_block(e, c, layer, pos0, B, X) == 0) return 0;
     if (turn > 0) {
         c->failed = 1;
+        c->fail_pending = 0;
         turn = -1;
     }
     if (layer >= c->first && layer <= c->last && c->gdn_slot[layer - c->first] >= 0) {
-        sync_state_to_host(e, c, layer);
-        c->state_loc[c->gdn_slot[layer - c->first]] = STATE_HOST;
-        if (c->conv_loc) c->conv_loc[c->gdn_slot[layer - c->first]] = STATE_HOST;
+        const int32_t slot = c->gdn_slot[layer - c->first];
+        if (sync_state_to_host(e, c, layer) != 0) {
+            const size_t n = (size_t)B * c->hidden;
+            size_t i;
+            fprintf(stderr,
+                    "hip: the recurrent state of layer %u is lost (HBM held it and the device no longer answers);"
+                    " the block output is NaN\n",
+                    layer);
+            for (i = 0; i < n; i++) X[i] = NAN;
+            return -2;
+        }
+        c->state_loc[slot] = STATE_HOST;
+        c->conv_loc[slot] = STATE_HOST;
     }
     if (batch)
         c->cpu_fwd_batch(e, layer, pos0, B);
@@ -788,7 +842,8 @@ static int gpu_prefill(HipCtx* c, Engine* e, uint32_t layer, uint32_t pos_start,
                           c->stream) != YHIP_OK)
         return -1;
     if (hipMemcpyAsync(e->pb2, c->d_out, nq * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return -1;
-    return hipStreamSynchronize(c->stream) == hipSuccess ? 0 : -1;
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return -1;
+    return gpu_after(c);
 }
 
 /* fwd_block_batch: forward_block_batch_default (engine.c:435-590) with the
@@ -900,33 +955,32 @@ static int plan_layers(Engine* e, HipCtx* c, char* err, size_t errlen)
     return 0;
 }
 
-/* HBM for the fused decode token (yhip_gdn_decode): two delay lines per state
- * slot and the layer's conv weights, dt_bias, ssm_a and norm weights.  The
- * norm weights are f32 or, like the engine reads every other type, f16 bits
- * (engine.c:838-850); layers whose norm types differ keep the token on the
- * chunk path. */
-static int setup_fused_decode(Engine* e, HipCtx* c, char* err, size_t errlen)
+/* HBM for the GDN layers: two states and two delay lines per state slot
+ * (state_cur / conv_cur name the current ones), and per slot the layer's
+ * conv weights, dt_bias, ssm_a and gated-norm weights.  The norm weights are
+ * f32 or, like the engine reads every other type, f16 bits
+ * (engine.c:838-850).  A decode token is one yhip_gdn_decode launch when
+ * n_v >= n_k (fused_decode); otherwise it takes the batch path. */
+static int setup_gdn(Engine* e, HipCtx* c, char* err, size_t errlen)
 {
-    const size_t conv_n = (size_t)c->kwidth * c->conv_chan;
+    const size_t conv_n = conv_elems(c), state_n = state_elems(c);
     const size_t dec_n = (size_t)c->conv_chan + c->value_dim + 2 * (size_t)c->n_v;
-    uint32_t l, ndt = 0;
-    int seen = 0;
-    c->fused_decode = 0;
-    if (c->kwidth > 8 || c->n_v < c->n_k) return 0;
-    for (l = c->first; l <= c->last; l++) {
-        const LlfTensorMeta* mt = &e->ws.model.metas[e->ws.model.base_idx[l]];
-        const uint32_t d = mt[SLOT_SSM_NORM].dtype == DT_F32 ? YHIP_F32 : YHIP_F16;
-        if (c->gdn_slot[l - c->first] < 0) continue;
-        if (seen && d != ndt) return 0;
-        ndt = d;
-        seen = 1;
-    }
-    c->norm_dtype = ndt;
+    uint32_t l;
+    if (c->kwidth > 8) return say(err, errlen, "GDN conv width above 8 is not supported", NULL);
+    c->fused_decode = c->n_v >= c->n_k;
     c->gdnw_n = (uint32_t)((conv_n + 2 * c->n_v + c->hvd + 3) / 4 * 4);
-    c->conv_loc = (uint8_t*)calloc(c->n_gdn_slots, 1); /* STATE_HOST */
+    c->state_loc = (uint8_t*)calloc(c->n_gdn_slots, 1); /* STATE_HOST */
+    c->state_cur = (uint8_t*)calloc(c->n_gdn_slots, 1);
+    c->conv_loc = (uint8_t*)calloc(c->n_gdn_slots, 1);
     c->conv_cur = (uint8_t*)calloc(c->n_gdn_slots, 1);
-    if (!c->conv_loc || !c->conv_cur) return say(err, errlen, "out of host memory", NULL);
-    if (hip_ok(hipMalloc((void**)&c->d_conv, c->n_gdn_slots * 2 * conv_n * 4), err, errlen, "GDN delay lines") ||
+    c->norm_dt = (uint8_t*)calloc(c->n_gdn_slots, 1);
+    if (!c->state_loc || !c->state_cur || !c->conv_loc || !c->conv_cur || !c->norm_dt)
+        return say(err, errlen, "out of host memory", NULL);
+    /* the HBM state is loaded from e->ssm_state by each layer's first call */
+    if (hip_ok(hipMalloc((void**)&c->d_state, (size_t)c->n_gdn_slots * 2 * state_n * 4), err, errlen,
+               "GDN state allocation") ||
+        hip_ok(hipMalloc((void**)&c->d_conv, (size_t)c->n_gdn_slots * 2 * conv_n * 4), err, errlen,
+               "GDN delay lines") ||
         hip_ok(hipMalloc((void**)&c->d_gdnw, (size_t)c->n_gdn_slots * c->gdnw_n * 4), err, errlen, "GDN weights") ||
         hip_ok(hipMalloc((void**)&c->d_dec, dec_n * 4), err, errlen, "GDN decode staging"))
         return -1;
@@ -934,8 +988,11 @@ static int setup_fused_decode(Engine* e, HipCtx* c, char* err, size_t errlen)
         const int32_t slot = c->gdn_slot[l - c->first];
         const uint8_t* base = layer_base(e, l);
         const LlfTensorMeta* mt = &e->ws.model.metas[e->ws.model.base_idx[l]];
+        uint32_t ndt;
         float* w;
         if (slot < 0) continue;
+        ndt = mt[SLOT_SSM_NORM].dtype == DT_F32 ? YHIP_F32 : YHIP_F16;
+        c->norm_dt[slot] = (uint8_t)ndt;
         w = c->d_gdnw + (size_t)slot * c->gdnw_n;
         if (hip_ok(hipMemcpy(w, base + mt[SLOT_SSM_CONV1D].offset, conv_n * 4, hipMemcpyHostToDevice), err, errlen,
                    "GDN conv weights") ||
@@ -949,7 +1006,6 @@ static int setup_fused_decode(Engine* e, HipCtx* c, char* err, size_t errlen)
                    err, errlen, "GDN norm weights"))
             return -1;
     }
-    c->fused_decode = 1;
     return 0;
 }
 
@@ -958,7 +1014,7 @@ static int hip_load_weights(Engine* e, char* err, size_t errlen)
     HipCtx* c = ctx_of(e);
     const LlfHeader* h;
     uint32_t first, last;
-    size_t cache_bytes, state_bytes;
+    size_t cache_bytes;
     if (!c) return say(err, errlen, "no backend state", NULL);
     h = &e->ws.model.h;
     release(c);
@@ -1002,16 +1058,7 @@ static int hip_load_weights(Engine* e, char* err, size_t errlen)
         return -1;
     c->dev_len = (uint32_t*)calloc(c->n_kv_slots + 1, sizeof(uint32_t));
     if (!c->dev_len) return say(err, errlen, "out of host memory", NULL);
-    if (c->n_gdn_slots) {
-        /* the HBM state is loaded from e->ssm_state by each layer's first call */
-        state_bytes = (size_t)c->n_v * c->hvd * c->hvd * 4;
-        c->state_loc = (uint8_t*)calloc(c->n_gdn_slots, 1); /* STATE_HOST */
-        c->h_conv = (float*)malloc((size_t)c->kwidth * c->conv_chan * 4);
-        if (!c->state_loc || !c->h_conv) return say(err, errlen, "out of host memory", NULL);
-        if (hip_ok(hipMalloc((void**)&c->d_state, state_bytes * c->n_gdn_slots), err, errlen, "GDN state allocation"))
-            return -1;
-        if (setup_fused_decode(e, c, err, errlen) != 0) return -1;
-    }
+    if (c->n_gdn_slots && setup_gdn(e, c, err, errlen) != 0) return -1;
     if (ensure_cap(c, e->pb_cap > 0 ? e->pb_cap : 64) != 0) return say(err, errlen, "staging allocation", NULL);
     c->h_raw = (float*)malloc(((size_t)(c->qdim > c->hidden ? c->qdim : c->hidden) + c->kv_dim) * 4);
     if (!c->h_raw) return say(err, errlen, "out of host memory", NULL);
@@ -1041,7 +1088,8 @@ static void hip_free_dev(Engine* e)
     if (c) {
         if (c->stream) hipStreamSynchronize(c->stream);
         /* the engine continues on the CPU with e->ssm_state */
-        sync_states_to_host(e, c);
+        if (sync_states_to_host(e, c) != 0)
+            fprintf(stderr, "hip: free_dev could not copy the recurrent state back; e->ssm_state is stale\n");
         release(c);
     }
     if (e->fwd_block == hip_fwd_block) engine_attach_cpu_fwd(e);
@@ -1097,6 +1145,7 @@ static int move_kv(Engine* e, uint32_t n_pos, int to_host)
     if (n_pos > c->max_seq) n_pos = c->max_seq;
     if (!to_host && c->state_loc) memset(c->state_loc, STATE_HOST, c->n_gdn_slots);
     if (!to_host && c->conv_loc) memset(c->conv_loc, STATE_HOST, c->n_gdn_slots);
+    if (c->dead) return -1;
     if (to_host && sync_states_to_host(e, c) != 0) return -1;
     for (l = c->first; l <= c->last && n_pos > 0; l++) {
         uint16_t* hk = e->kv + (size_t)l * e->max_seq * c->kv_dim;
@@ -1150,4 +1199,10 @@ void device_hip_fail_after(Engine* e, int n_calls)
 {
     HipCtx* c = ctx_of(e);
     if (c) c->fail_after = n_calls < 0 ? -1 : n_calls;
+}
+
+void device_hip_fail_mode(Engine* e, int mode)
+{
+    HipCtx* c = ctx_of(e);
+    if (c) c->fail_mode = mode == FAIL_AFTER || mode == FAIL_LOST ? mode : FAIL_BEFORE;
 }

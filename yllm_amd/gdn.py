@@ -11,10 +11,11 @@ inference/core/engine.c):
                                                 engine.c:809-812) over T tokens
     gdn_gated_norm(x, z, w, n_heads)            rmsnorm_gated per v-head (matvec.c:1007-1021)
     gdn_decode(S, conv_in, conv_out, qkv, ...)  one decode token of the layer, all of the above
-                                                in two launches (engine.c:786-847)
+                                                in one launch (engine.c:786-847)
 
 S is the fp32 state [n_v, d, d] (S[h, j, :] is column j, the reference's
-transposed storage), updated in place.  Tensors are torch fp32 tensors on the
+transposed storage), updated in place unless S_out names another buffer (then
+S keeps the state before the call).  Tensors are torch fp32 tensors on the
 GPU; every call goes through libyllm_hip.so on the current stream, with no CPU
 fallback.
 """
@@ -70,17 +71,29 @@ def gdn_chunk_workspace_bytes(T: int, n_v: int, d: int) -> int:
     return int(lib().yhip_gdn_chunk_workspace(T, n_v, d))
 
 
+def _state_out(S: torch.Tensor, S_out: torch.Tensor | None) -> int:
+    if S_out is None:
+        return S.data_ptr()
+    _f32_gpu(S_out)
+    if S_out.shape != S.shape or not S_out.is_contiguous():
+        raise YhipError(-22, "gdn: S_out must be contiguous and shaped like S")
+    return S_out.data_ptr()
+
+
 def gdn_chunk(S: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor,
               beta: torch.Tensor, n_k: int, eps: float = L2_EPS, out: torch.Tensor | None = None,
-              workspace: torch.Tensor | None = None, chunked: bool = True) -> torch.Tensor:
+              workspace: torch.Tensor | None = None, chunked: bool = True,
+              S_out: torch.Tensor | None = None) -> torch.Tensor:
     """T tokens in order.  q, k: [T, >= n_k*d]; v: [T, >= n_v*d]; gate, beta:
-    [T, n_v].  Returns out [T, n_v*d]; S is left at the state after the last
-    token.  eps <= 0 skips the q/k normalisation.  chunked=True uses the
+    [T, n_v].  Returns out [T, n_v*d]; the state after the last token goes
+    to S (in place) or to S_out when given (S then keeps the state before the
+    call).  eps <= 0 skips the q/k normalisation.  chunked=True uses the
     chunked form (with `workspace`, allocated here when not given);
     chunked=False runs the token-by-token recurrence."""
     _f32_gpu(S, q, k, v, gate, beta)
     if S.dim() != 3 or S.shape[1] != S.shape[2] or not S.is_contiguous():
         raise YhipError(-22, "gdn: S must be contiguous [n_v, d, d]")
+    so = _state_out(S, S_out)
     n_v, d = S.shape[0], S.shape[1]
     T, qs = _rows(q)
     Tk, ks = _rows(k)
@@ -99,7 +112,7 @@ def gdn_chunk(S: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
         workspace = torch.empty(ws_bytes // 4, dtype=torch.float32, device=S.device)
     ws_ptr = workspace.data_ptr() if ws_bytes else None
-    check(lib().yhip_gdn_chunk(S.data_ptr(), out.data_ptr(), os_, q.data_ptr(), k.data_ptr(), qs, v.data_ptr(), vs,
+    check(lib().yhip_gdn_chunk(S.data_ptr(), so, out.data_ptr(), os_, q.data_ptr(), k.data_ptr(), qs, v.data_ptr(), vs,
                                gate.data_ptr(), beta.data_ptr(), T, n_k, n_v, d, float(eps), ws_ptr, ws_bytes,
                                _stream()))
     return out
@@ -123,9 +136,10 @@ def gdn_step(S: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 
 def gdn_conv(x: torch.Tensor, conv_state: torch.Tensor, conv_w: torch.Tensor, silu: bool = True,
-             out: torch.Tensor | None = None) -> torch.Tensor:
+             out: torch.Tensor | None = None, state_out: torch.Tensor | None = None) -> torch.Tensor:
     """x: [T, dim] rows (row stride free); conv_state: fp32 [kwidth, dim]
-    delay line, updated in place; conv_w: fp32 [dim, kwidth].  Returns
+    delay line, updated in place (or, with `state_out`, left as it was and
+    the new line written there); conv_w: fp32 [dim, kwidth].  Returns
     silu(conv) rows [T, dim] (a new tensor unless `out` is given; out must
     not overlap x)."""
     _f32_gpu(x, conv_state, conv_w)
@@ -143,8 +157,13 @@ def gdn_conv(x: torch.Tensor, conv_state: torch.Tensor, conv_w: torch.Tensor, si
     To, os_ = _rows(out)
     if To != T:
         raise YhipError(-22, "gdn_conv: out must have T rows")
-    check(lib().yhip_gdn_conv(out.data_ptr(), os_, x.data_ptr(), xs, conv_state.data_ptr(), conv_w.data_ptr(), T,
-                              dim, kwidth, int(silu), _stream()))
+    if state_out is not None:
+        _f32_gpu(state_out)
+        if state_out.shape != conv_state.shape or not state_out.is_contiguous():
+            raise YhipError(-22, "gdn_conv: state_out must be contiguous [kwidth, dim]")
+    so = state_out.data_ptr() if state_out is not None else conv_state.data_ptr()
+    check(lib().yhip_gdn_conv(out.data_ptr(), os_, x.data_ptr(), xs, conv_state.data_ptr(), so, conv_w.data_ptr(),
+                              T, dim, kwidth, int(silu), _stream()))
     return out
 
 
@@ -175,10 +194,11 @@ def gdn_gated_norm(x: torch.Tensor, z: torch.Tensor, w: torch.Tensor, n_heads: i
 def gdn_decode(S: torch.Tensor, conv_in: torch.Tensor, conv_out: torch.Tensor, qkv: torch.Tensor, z: torch.Tensor,
                alpha: torch.Tensor, beta_raw: torch.Tensor, conv_w: torch.Tensor, dt_bias: torch.Tensor,
                ssm_a: torch.Tensor, norm_w: torch.Tensor, n_k: int, l2_eps: float = L2_EPS,
-               norm_eps: float = L2_EPS, y: torch.Tensor | None = None) -> torch.Tensor:
+               norm_eps: float = L2_EPS, y: torch.Tensor | None = None,
+               S_out: torch.Tensor | None = None) -> torch.Tensor:
     """One decode token of a GDN layer (engine.c:786-847 after the
     projections): gates, conv1d + silu, l2norm, state update, gated RMSNorm.
-    S [n_v, d, d] updated in place; conv_in -> conv_out the delay line
+    S [n_v, d, d] updated in place (or into S_out); conv_in -> conv_out the delay line
     [kwidth, conv_dim] before / after the token (two buffers, swap them each
     token); qkv [conv_dim] = q | k | v; z [n_v*d]; alpha, beta_raw, dt_bias,
     ssm_a [n_v]; conv_w [conv_dim, kwidth]; norm_w [d] fp32 or f16.
@@ -201,7 +221,8 @@ def gdn_decode(S: torch.Tensor, conv_in: torch.Tensor, conv_out: torch.Tensor, q
     if y is None:
         y = torch.empty(n_v * d, dtype=torch.float32, device=S.device)
     _f32_gpu(y)
-    check(lib().yhip_gdn_decode(S.data_ptr(), conv_in.data_ptr(), conv_out.data_ptr(), y.data_ptr(), qkv.data_ptr(),
+    so = _state_out(S, S_out)
+    check(lib().yhip_gdn_decode(S.data_ptr(), so, conv_in.data_ptr(), conv_out.data_ptr(), y.data_ptr(), qkv.data_ptr(),
                                 z.data_ptr(), alpha.data_ptr(), beta_raw.data_ptr(), conv_w.data_ptr(),
                                 dt_bias.data_ptr(), ssm_a.data_ptr(), norm_w.data_ptr(),
                                 F16 if norm_w.dtype == torch.float16 else F32, n_k, n_v, d, kwidth, float(l2_eps),
