@@ -703,6 +703,7 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
     dt = torch.zeros(hg, device=dev)
     a = -torch.ones(hg, device=dev)
     S = [torch.zeros((hg, dg, dg), device=dev) for _ in range(n_gdn)]
+    S2 = [torch.zeros((hg, dg, dg), device=dev) for _ in range(n_gdn)]  # the decode tokens alternate S and S2
     cst = [torch.zeros((kw, conv), device=dev) for _ in range(n_gdn)]
     cst2 = [torch.zeros((kw, conv), device=dev) for _ in range(n_gdn)]
     beta = [torch.empty((L, hg), device=dev) for _ in range(n_gdn)]
@@ -729,12 +730,15 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
         gdn_gated_norm(gout[:T], g["z"][:T], g["norm_w"], hg, out=gout[:T])
 
     def gdn_layer_step(li, t):
-        # one launch per layer and token; the delay line alternates between
-        # cst and cst2 (an even number of decode tokens ends back in cst)
+        # one launch per layer and token; the state and the delay line
+        # alternate between two buffers each, as the device backend keeps
+        # them (an even number of decode tokens ends back in S and cst)
         g = gd[li]
-        c_in, c_out = (cst[li], cst2[li]) if (t - T) % 2 == 0 else (cst2[li], cst[li])
-        gdn_decode(S[li], c_in, c_out, g["qkv"][t], g["z"][t], g["alpha"][t], g["beta_raw"][t], g["conv_w"], dt, a,
-                   g["norm_w"], hg, y=gout[t])
+        even = (t - T) % 2 == 0
+        c_in, c_out = (cst[li], cst2[li]) if even else (cst2[li], cst[li])
+        s_in, s_out = (S[li], S2[li]) if even else (S2[li], S[li])
+        gdn_decode(s_in, c_in, c_out, g["qkv"][t], g["z"][t], g["alpha"][t], g["beta_raw"][t], g["conv_w"], dt, a,
+                   g["norm_w"], hg, y=gout[t], S_out=s_out)
 
     def step(i):
         for li in range(n_gdn):

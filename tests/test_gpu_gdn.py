@@ -319,13 +319,17 @@ def _oracle_layer(oracle, S, st, qkv, z, alpha, beta_raw, conv_w, dt, a, norm_w,
     return S, st, np.stack(ys)
 
 
+@pytest.mark.parametrize("oop", [False, True], ids=["in_place", "ping_pong"])
 @pytest.mark.parametrize("n_k,n_v,d,kw,w_f16", [
     (16, 16, 128, 4, False),  # the fifth configuration's GDN layer
     (2, 4, 64, 4, True),
     (4, 8, 128, 3, False),
     (1, 3, 64, 1, False),
 ])
-def test_gdn_decode_matches_oracle(cuda, oracle, n_k, n_v, d, kw, w_f16):
+def test_gdn_decode_matches_oracle(cuda, oracle, n_k, n_v, d, kw, w_f16, oop):
+    """In place (one workgroup per head) and with the state alternating
+    between two buffers as the device backend keeps it (several workgroups
+    per head, each storing its share of the columns)."""
     from yllm_amd.gdn import gdn_decode
 
     T = 5
@@ -338,9 +342,13 @@ def test_gdn_decode_matches_oracle(cuda, oracle, n_k, n_v, d, kw, w_f16):
     nw = torch.from_numpy(norm_w).to(cuda)
     nw = nw.view(torch.float16) if w_f16 else nw
     ys = []
+    S_b = torch.full_like(S, float("nan"))
     for t in range(T):
-        ys.append(gdn_decode(S, st_a, st_b, qkv_t[t], z_t[t], al[t], br[t], cw, dtt, at, nw, n_k).cpu().numpy())
+        ys.append(gdn_decode(S, st_a, st_b, qkv_t[t], z_t[t], al[t], br[t], cw, dtt, at, nw, n_k,
+                             S_out=S_b if oop else None).cpu().numpy())
         st_a, st_b = st_b, st_a
+        if oop:
+            S, S_b = S_b, S
     y = np.stack(ys)
     err_y = max(rel_l2(y[t], y_want[t]) for t in range(T))
     err_s = rel_l2(S.cpu().numpy(), S_want)
