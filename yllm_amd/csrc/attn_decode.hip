@@ -75,6 +75,8 @@ struct DecodeRopeNone {
 };
 template <bool ROPE>
 using DecodeRopeArg = typename std::conditional<ROPE, DecodeRope, DecodeRopeNone>::type;
+static_assert(offsetof(DecodeRope, cs) % 8 == 0 && alignof(DecodeRope) == 8,
+              "the cosine table is read with 8-byte loads from the kernel arguments");
 
 // one 32-key block of K and V as MFMA operands of one lane
 template <int D>
@@ -191,49 +193,24 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     // a rotated element's pair index (the cosine and sine it needs)
     auto pair_of = [&](uint32_t d) -> uint32_t { return far_pairs ? (d < half ? d : d - half) : d >> 1; };
     auto rotated = [&](uint32_t d) -> bool { return far_pairs ? d < span : rkind == kRopePairs; };
-    f32x4 qv[QPT], qp[ROPE ? QPT : 1], qc[ROPE ? QPT : 1], qs[ROPE ? QPT : 1];
-    {
-        const float* qbase = a.q + (size_t)seq * a.q_stride + (size_t)h0 * D;
+    // Every lane issues its q loads unconditionally, from a row that is valid
+    // for every lane (the padded head slots read head 0's and are zeroed
+    // afterwards): a load issued on some lanes only, into a zero-initialised
+    // register, made the compiler copy the result right after the load and
+    // wait for it -- before the K/V block loads were even issued (+1 us per
+    // launch at 16/2 heads of 256).
+    static_assert(16 * D4 % kThreads == 0, "whole rows of float4s per thread");
+    const float* qbase = a.q + (size_t)seq * a.q_stride + (size_t)h0 * D;
+    f32x4 qv[QPT];
 #pragma unroll
-        for (int r = 0; r < QPT; ++r) {
-            const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
-            qv[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (idx < 16 * D4 && hn < G) qv[r] = *reinterpret_cast<const f32x4*>(qbase + (size_t)idx * 4);
-            if constexpr (ROPE) {
-                qp[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-                if (far_pairs && idx < 16 * D4 && hn < G && d < span)
-                    qp[r] = *reinterpret_cast<const f32x4*>(qbase + (size_t)hn * D + (d < half ? d + half : d - half));
-                // the cosines and sines (kernel arguments) are read with the
-                // other loads, each lane its elements' pairs
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    qc[r][e] = 1.0f;
-                    qs[r][e] = 0.0f;
-                    if (idx < 16 * D4 && hn < G && rotated(d + e)) {
-                        qc[r][e] = rp.cs[0][pair_of(d + e)];
-                        qs[r][e] = rp.cs[1][pair_of(d + e)];
-                    }
-                }
-            }
-        }
+    for (int r = 0; r < QPT; ++r) {
+        const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
+        qv[r] = *reinterpret_cast<const f32x4*>(qbase + (size_t)(hn < G ? hn : 0u) * D + d);
     }
-    // ROPE: the new token (key len0 - 1) and, in the workgroup whose split
-    // holds it, its raw key element d and partner, and its value element
-    // (thread d < D)
+    // ROPE: the new token (key len0 - 1) is stored by the workgroup whose
+    // split holds it
     const uint32_t tpos = len - 1;
     const bool owns_tok = ROPE && kbeg <= tpos && tpos < kend;  // uniform over the workgroup
-    float kraw = 0.0f, kpart = 0.0f, vraw = 0.0f, kcos = 1.0f, ksin = 0.0f;
-    if (ROPE && owns_tok && threadIdx.x < (uint32_t)D) {
-        const uint32_t d = threadIdx.x;
-        const uint32_t pr = far_pairs ? (d < span ? (d < half ? d + half : d - half) : d) : (d ^ 1u);
-        kraw = rp.k[(size_t)kvh * D + d];
-        kpart = rp.k[(size_t)kvh * D + pr];
-        vraw = rp.v[(size_t)kvh * D + d];
-        if (rotated(d)) {
-            kcos = rp.cs[0][pair_of(d)];
-            ksin = rp.cs[1][pair_of(d)];
-        }
-    }
 
     // NBUF blocks of this wave in flight
     constexpr int NBUF = nbuf_of<D>();
@@ -242,10 +219,45 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     for (int i = 0; i < NBUF; ++i) load(f[i], wave + i * kWaves);
 
     if constexpr (ROPE) {
+        // The rotation's own loads go out after the first blocks' (waiting for
+        // them then waits for those blocks too, which the first step needs
+        // anyway; issued before, every wait for them held back the block
+        // loads): per float4, its partner float4 for pairs half a span apart,
+        // and its cosines and sines (kernel arguments) in 8-byte loads -- four
+        // consecutive pairs pj .. pj + 3 half a span apart (half is a
+        // multiple of 4), or two adjacent pairs d / 2, d / 2 + 1 for PAIRS --
+        // from clamped, always-valid indices; the kind selects afterwards.
+        // The owner also loads the token's raw key element d, its partner and
+        // its value element (thread d < D), with that element's pair.
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        f32x4 qp[QPT];
+        f32x2 tc[QPT][2], ts[QPT][2];
+#pragma unroll
+        for (int r = 0; r < QPT; ++r) {
+            const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
+            qp[r] = *reinterpret_cast<const f32x4*>(qbase + (size_t)(hn < G ? hn : 0u) * D +
+                                                    (d < half ? d + half : (d - half) % D));
+            const uint32_t pj = min(far_pairs ? (d < half ? d : d - half) : d >> 1, 124u);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                tc[r][u] = *reinterpret_cast<const f32x2*>(&rp.cs[0][pj + 2 * u]);
+                ts[r][u] = *reinterpret_cast<const f32x2*>(&rp.cs[1][pj + 2 * u]);
+            }
+        }
+        float kraw = 0.0f, kpart = 0.0f, vraw = 0.0f, kc1 = 1.0f, ks1 = 0.0f;
+        if (owns_tok && threadIdx.x < (uint32_t)D) {
+            const uint32_t d = threadIdx.x;
+            const uint32_t pr = far_pairs ? (d < span ? (d < half ? d + half : d - half) : d) : (d ^ 1u);
+            kraw = rp.k[(size_t)kvh * D + d];
+            kpart = rp.k[(size_t)kvh * D + pr];
+            vraw = rp.v[(size_t)kvh * D + d];
+            const uint32_t pj = min(pair_of(d), 127u);
+            kc1 = rp.cs[0][pj];
+            ks1 = rp.cs[1][pj];
+        }
         // element d with value x, partner value p and its pair's cosine c and
         // sine sn: the reference's (a, b) -> (a c - b s, a s + b c), a the
-        // pair's first element (the unrotated elements carry c = 1, sn = 0 and
-        // pass through unchanged)
+        // pair's first element; unrotated elements pass through unchanged
         auto rotate = [&](uint32_t d, float x, float p, float c, float sn) {
 #pragma clang fp contract(off)
             if (!rotated(d)) return x;
@@ -255,46 +267,46 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
 #pragma unroll
         for (int r = 0; r < QPT; ++r) {
             const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
-            if (idx < 16 * D4) {
-                f16x4 hi, lo;
+            const f32x4 c4 = far_pairs ? f32x4{tc[r][0][0], tc[r][0][1], tc[r][1][0], tc[r][1][1]}
+                                       : f32x4{tc[r][0][0], tc[r][0][0], tc[r][0][1], tc[r][0][1]};
+            const f32x4 s4 = far_pairs ? f32x4{ts[r][0][0], ts[r][0][1], ts[r][1][0], ts[r][1][1]}
+                                       : f32x4{ts[r][0][0], ts[r][0][0], ts[r][0][1], ts[r][0][1]};
+            f16x4 hi, lo;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    // partner: the same lane's float4 for PAIRS (element e ^ 1), else the loaded one
-                    const float p = far_pairs ? qp[r][e] : qv[r][e ^ 1];
-                    const float x = rotate(d + e, qv[r][e], p, qc[r][e], qs[r][e]);
-                    const _Float16 h = (_Float16)x;
-                    hi[e] = h;
-                    lo[e] = (_Float16)(x - (float)h);
-                }
-                *reinterpret_cast<f16x4*>(s_q + hn * QROW + d) = hi;
-                *reinterpret_cast<f16x4*>(s_q + (16 + hn) * QROW + d) = lo;
+            for (int e = 0; e < 4; ++e) {
+                // partner: the same lane's float4 for PAIRS (element e ^ 1), else the loaded one
+                const float x = hn < G ? rotate(d + e, qv[r][e], far_pairs ? qp[r][e] : qv[r][e ^ 1], c4[e], s4[e])
+                                       : 0.0f;
+                const _Float16 h = (_Float16)x;
+                hi[e] = h;
+                lo[e] = (_Float16)(x - (float)h);
             }
+            *reinterpret_cast<f16x4*>(s_q + hn * QROW + d) = hi;
+            *reinterpret_cast<f16x4*>(s_q + (16 + hn) * QROW + d) = lo;
         }
         if (owns_tok && threadIdx.x < (uint32_t)D) {
-            // the token's key and value with the reference rounding, into the
-            // cache and, for the substitution below, into LDS
+            // the token's key and value with the reference rounding, into LDS
+            // for the substitution below; they go to the cache after the key
+            // loop (issued here, the loop's waits for its blocks waited for
+            // these scattered 2-byte stores too)
             const uint32_t d = threadIdx.x;
-            const uint16_t kb = f32_to_f16_ref(rotate(d, kraw, kpart, kcos, ksin)), vb = f32_to_f16_ref(vraw);
-            rp.kc[k_index(kvh, tpos, d, D, a.kv_stride)] = kb;
-            rp.vc[v_index(kvh, tpos, d, D, a.kv_stride)] = vb;
-            s_knew[d] = kb;
-            s_vnew[d] = vb;
+            s_knew[d] = f32_to_f16_ref(rotate(d, kraw, kpart, kc1, ks1));
+            s_vnew[d] = f32_to_f16_ref(vraw);
         }
     } else {
 #pragma unroll
         for (int r = 0; r < QPT; ++r) {
             const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
-            if (idx < 16 * D4) {
-                f16x4 hi, lo;
+            f16x4 hi, lo;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const _Float16 h = (_Float16)qv[r][e];
-                    hi[e] = h;
-                    lo[e] = (_Float16)(qv[r][e] - (float)h);
-                }
-                *reinterpret_cast<f16x4*>(s_q + hn * QROW + d) = hi;
-                *reinterpret_cast<f16x4*>(s_q + (16 + hn) * QROW + d) = lo;
+            for (int e = 0; e < 4; ++e) {
+                const float x = hn < G ? qv[r][e] : 0.0f;
+                const _Float16 h = (_Float16)x;
+                hi[e] = h;
+                lo[e] = (_Float16)(x - (float)h);
             }
+            *reinterpret_cast<f16x4*>(s_q + hn * QROW + d) = hi;
+            *reinterpret_cast<f16x4*>(s_q + (16 + hn) * QROW + d) = lo;
         }
     }
     lds_barrier();
@@ -324,12 +336,28 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
                     f.k[0][c] = k0 ? kn : f.k[0][c];
                     f.k[1][c] = k1 ? kn : f.k[1][c];
                 }
+                // V: the token is element e = rr % 8 -- the same for every lane
+                // of the wave -- of the lanes of group rr >> 3, so only dword
+                // e / 2 of each fragment changes, in its half e % 2 (a select
+                // per element of every fragment cost the owner's wave 1.1 us at
+                // d = 256)
                 const bool vcol_here = (uint32_t)g == rr >> 3;
+                const uint32_t e = rr & 7u, sh = (e & 1u) * 16u, keep = sh ? 0x0000ffffu : 0xffff0000u;
+                auto put_v = [&](auto W) {
+                    constexpr int w = decltype(W)::value;
 #pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const _Float16 vn = __builtin_bit_cast(_Float16, s_vnew[b * 16 + n]);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) f.v[b][e] = (vcol_here && (uint32_t)e == (rr & 7u)) ? vn : f.v[b][e];
+                    for (int b = 0; b < NB; ++b) {
+                        u32x4 x = __builtin_bit_cast(u32x4, f.v[b]);
+                        const uint32_t vn = (uint32_t)s_vnew[b * 16 + n] << sh;
+                        x[w] = vcol_here ? (x[w] & keep) | vn : x[w];
+                        f.v[b] = __builtin_bit_cast(f16x8, x);
+                    }
+                };
+                switch (e >> 1) {  // uniform over the wave
+                case 0: put_v(std::integral_constant<int, 0>{}); break;
+                case 1: put_v(std::integral_constant<int, 1>{}); break;
+                case 2: put_v(std::integral_constant<int, 2>{}); break;
+                default: put_v(std::integral_constant<int, 3>{}); break;
                 }
             }
         }
@@ -407,6 +435,11 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     for (int i = 0; i < NBUF; ++i)
         if (j + i < nbw) compute(f[i], kbeg + (wave + (j + i) * kWaves) * kKeysPerBlock);
 
+    if (ROPE && owns_tok && threadIdx.x < (uint32_t)D) {  // the token's K and V into the cache
+        const uint32_t d = threadIdx.x;
+        rp.kc[k_index(kvh, tpos, d, D, a.kv_stride)] = s_knew[d];
+        rp.vc[v_index(kvh, tpos, d, D, a.kv_stride)] = s_vnew[d];
+    }
     // per-lane partial sums -> per head (the four lane groups hold one head)
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
@@ -414,7 +447,10 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         s_m[wave][n] = m;
         s_l[wave][n] = l;
     }
-    __syncthreads();
+    // LDS-only barriers in the combine: a full barrier also waited for the
+    // owner's token stores (scattered 2-byte K/V writes issued before the
+    // loop), which made that workgroup the launch's straggler (+1.6 us)
+    lds_barrier();
 
     // Combine the four waves: every lane rescales its own accumulators to the
     // head's maximum over the waves before staging them, so the sum below is
@@ -436,7 +472,7 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
             s_hl[n] = L;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // a single split writes the result directly, otherwise a partial
     const size_t grp = (size_t)seq * a.n_kv + kvh;  // (sequence, kv head) group
