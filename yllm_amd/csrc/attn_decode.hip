@@ -104,7 +104,10 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     __shared__ float s_m[kWaves][16];
     __shared__ float s_l[kWaves][16];
     __shared__ float s_hm[16], s_hl[16];  // per head: max and sum over the waves
-    __shared__ __attribute__((aligned(16))) uint16_t s_knew[ROPE ? D : 8], s_vnew[ROPE ? D : 8];  // the token's K, V bits
+    // the token's K bits by dimension, and its V bits by lane: element
+    // d = 16 b + n at [n][b], so lane n reads its NB values in one go
+    __shared__ __attribute__((aligned(16))) uint16_t s_knew[ROPE ? D : 8];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vt[ROPE ? 16 : 1][ROPE ? D / 16 : 8];
 
     const uint32_t seq = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
     // a length beyond the planned maximum is clamped, never read past
@@ -212,26 +215,23 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     const uint32_t tpos = len - 1;
     const bool owns_tok = ROPE && kbeg <= tpos && tpos < kend;  // uniform over the workgroup
 
-    // NBUF blocks of this wave in flight
-    constexpr int NBUF = nbuf_of<D>();
-    Frag<D> f[NBUF];
-#pragma unroll
-    for (int i = 0; i < NBUF; ++i) load(f[i], wave + i * kWaves);
-
+    // ROPE: the rotation's own loads go out with q, before the blocks (the
+    // staging below then waits for them and q only; issued after the blocks,
+    // in-order completion made it wait for the whole first round of blocks,
+    // +1.2 us per launch at 16/2 heads of 256 and 4352 keys): per float4, its
+    // partner float4 for pairs half a span apart, and its cosines and sines
+    // (kernel arguments) in 8-byte loads -- four consecutive pairs pj .. pj + 3
+    // half a span apart (half is a multiple of 4), or two adjacent pairs
+    // d / 2, d / 2 + 1 for PAIRS -- from clamped, always-valid indices; the
+    // kind selects afterwards.  The owner also loads the token's raw key
+    // element d, its partner and its value element (thread d < D), with that
+    // element's pair.
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    constexpr int RQ = ROPE ? QPT : 1;
+    f32x4 qp[RQ];
+    f32x2 tc[RQ][2], ts[RQ][2];
+    float kraw = 0.0f, kpart = 0.0f, vraw = 0.0f, kc1 = 1.0f, ks1 = 0.0f;
     if constexpr (ROPE) {
-        // The rotation's own loads go out after the first blocks' (waiting for
-        // them then waits for those blocks too, which the first step needs
-        // anyway; issued before, every wait for them held back the block
-        // loads): per float4, its partner float4 for pairs half a span apart,
-        // and its cosines and sines (kernel arguments) in 8-byte loads -- four
-        // consecutive pairs pj .. pj + 3 half a span apart (half is a
-        // multiple of 4), or two adjacent pairs d / 2, d / 2 + 1 for PAIRS --
-        // from clamped, always-valid indices; the kind selects afterwards.
-        // The owner also loads the token's raw key element d, its partner and
-        // its value element (thread d < D), with that element's pair.
-        typedef float f32x2 __attribute__((ext_vector_type(2)));
-        f32x4 qp[QPT];
-        f32x2 tc[QPT][2], ts[QPT][2];
 #pragma unroll
         for (int r = 0; r < QPT; ++r) {
             const uint32_t idx = threadIdx.x + r * kThreads, hn = idx / D4, d = (idx % D4) * 4;
@@ -244,7 +244,6 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
                 ts[r][u] = *reinterpret_cast<const f32x2*>(&rp.cs[1][pj + 2 * u]);
             }
         }
-        float kraw = 0.0f, kpart = 0.0f, vraw = 0.0f, kc1 = 1.0f, ks1 = 0.0f;
         if (owns_tok && threadIdx.x < (uint32_t)D) {
             const uint32_t d = threadIdx.x;
             const uint32_t pr = far_pairs ? (d < span ? (d < half ? d + half : d - half) : d) : (d ^ 1u);
@@ -255,14 +254,29 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
             kc1 = rp.cs[0][pj];
             ks1 = rp.cs[1][pj];
         }
+    }
+
+    // NBUF blocks of this wave in flight
+    constexpr int NBUF = nbuf_of<D>();
+    Frag<D> f[NBUF];
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i) load(f[i], wave + i * kWaves);
+    // nothing below moves above the block loads (a use of q or the rotation's
+    // loads scheduled among them waits for them before the rest are issued)
+    __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (ROPE) {
         // element d with value x, partner value p and its pair's cosine c and
         // sine sn: the reference's (a, b) -> (a c - b s, a s + b c), a the
         // pair's first element; unrotated elements pass through unchanged
-        auto rotate = [&](uint32_t d, float x, float p, float c, float sn) {
+        // (x c - p sn for a pair's first element, p sn + x c = x c + p sn for
+        // its second: two rounded products and one rounded sum either way,
+        // formed without a branch)
+        auto rotate = [&](float x, float p, float c, float sn, bool first, bool rot) {
 #pragma clang fp contract(off)
-            if (!rotated(d)) return x;
-            const bool first = far_pairs ? d < half : (d & 1u) == 0;
-            return first ? x * c - p * sn : p * sn + x * c;
+            const float u = x * c, t = p * sn;
+            const float r = first ? u - t : u + t;
+            return rot ? r : x;
         };
 #pragma unroll
         for (int r = 0; r < QPT; ++r) {
@@ -271,12 +285,16 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
                                        : f32x4{tc[r][0][0], tc[r][0][0], tc[r][0][1], tc[r][0][1]};
             const f32x4 s4 = far_pairs ? f32x4{ts[r][0][0], ts[r][0][1], ts[r][1][0], ts[r][1][1]}
                                        : f32x4{ts[r][0][0], ts[r][0][0], ts[r][0][1], ts[r][0][1]};
+            // span and half are multiples of 4: one answer per float4 for the
+            // kinds with pairs half a span apart
+            const bool rot = rotated(d), first4 = d < half;
             f16x4 hi, lo;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 // partner: the same lane's float4 for PAIRS (element e ^ 1), else the loaded one
-                const float x = hn < G ? rotate(d + e, qv[r][e], far_pairs ? qp[r][e] : qv[r][e ^ 1], c4[e], s4[e])
-                                       : 0.0f;
+                const float y = rotate(qv[r][e], far_pairs ? qp[r][e] : qv[r][e ^ 1], c4[e], s4[e],
+                                       far_pairs ? first4 : (e & 1) == 0, rot);
+                const float x = hn < G ? y : 0.0f;
                 const _Float16 h = (_Float16)x;
                 hi[e] = h;
                 lo[e] = (_Float16)(x - (float)h);
@@ -290,8 +308,8 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
             // loop (issued here, the loop's waits for its blocks waited for
             // these scattered 2-byte stores too)
             const uint32_t d = threadIdx.x;
-            s_knew[d] = f32_to_f16_ref(rotate(d, kraw, kpart, kc1, ks1));
-            s_vnew[d] = f32_to_f16_ref(vraw);
+            s_knew[d] = f32_to_f16_ref(rotate(kraw, kpart, kc1, ks1, far_pairs ? d < half : (d & 1u) == 0, rotated(d)));
+            s_vt[d % 16][d / 16] = f32_to_f16_ref(vraw);
         }
     } else {
 #pragma unroll
@@ -317,50 +335,27 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         qhi[c] = *reinterpret_cast<const f16x8*>(s_q + n * QROW + c * 32 + g * 8);
         qlo[c] = *reinterpret_cast<const f16x8*>(s_q + (16 + n) * QROW + c * 32 + g * 8);
     }
+    // ROPE: the token's score for head slot n, by the MFMA chain of the key
+    // loop with every A row the token's key (each output element is the same
+    // dot product, in the same order, as the one of the token's own row)
+    float stok = 0.0f;
+    if constexpr (ROPE) {
+        if (owns_tok) {
+            f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const f16x8 kn = *reinterpret_cast<const f16x8*>(&s_knew[c * 32 + g * 8]);
+                st = mfma16(kn, qhi[c], st);
+                st = mfma16(kn, qlo[c], st);
+            }
+            stok = st[0];
+        }
+    }
 
     auto compute = [&](Frag<D>& f, uint32_t key0) {
-        if constexpr (ROPE) {
-            // the block holding the token: its row came from the cache before
-            // the token was stored; lanes holding it take the new bits.  K row
-            // rr sits in half t = (rr >> 2) & 1 of lane n = 4 (rr >> 3) + rr % 4;
-            // V position rr in element rr % 8 of lane group rr >> 3.
-            // (value selects only: a store into a fragment chosen at run time
-            // moved the fragment sets to scratch memory)
-            if (owns_tok && tpos >= key0 && tpos < key0 + kKeysPerBlock) {  // uniform over the wave
-                const uint32_t rr = tpos - key0;
-                const bool krow_here = (uint32_t)n == 4 * (rr >> 3) + (rr & 3u);
-                const bool k0 = krow_here && !(rr & 4u), k1 = krow_here && (rr & 4u);
-#pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    const f16x8 kn = *reinterpret_cast<const f16x8*>(&s_knew[c * 32 + g * 8]);
-                    f.k[0][c] = k0 ? kn : f.k[0][c];
-                    f.k[1][c] = k1 ? kn : f.k[1][c];
-                }
-                // V: the token is element e = rr % 8 -- the same for every lane
-                // of the wave -- of the lanes of group rr >> 3, so only dword
-                // e / 2 of each fragment changes, in its half e % 2 (a select
-                // per element of every fragment cost the owner's wave 1.1 us at
-                // d = 256)
-                const bool vcol_here = (uint32_t)g == rr >> 3;
-                const uint32_t e = rr & 7u, sh = (e & 1u) * 16u, keep = sh ? 0x0000ffffu : 0xffff0000u;
-                auto put_v = [&](auto W) {
-                    constexpr int w = decltype(W)::value;
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) {
-                        u32x4 x = __builtin_bit_cast(u32x4, f.v[b]);
-                        const uint32_t vn = (uint32_t)s_vnew[b * 16 + n] << sh;
-                        x[w] = vcol_here ? (x[w] & keep) | vn : x[w];
-                        f.v[b] = __builtin_bit_cast(f16x8, x);
-                    }
-                };
-                switch (e >> 1) {  // uniform over the wave
-                case 0: put_v(std::integral_constant<int, 0>{}); break;
-                case 1: put_v(std::integral_constant<int, 1>{}); break;
-                case 2: put_v(std::integral_constant<int, 2>{}); break;
-                default: put_v(std::integral_constant<int, 3>{}); break;
-                }
-            }
-        }
+        // ROPE: the block holding the token (uniform over the wave)
+        const bool tok_here = ROPE && owns_tok && tpos >= key0 && tpos < key0 + kKeysPerBlock;
+        const uint32_t rr = tpos - key0;
         f32x4 s[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -377,6 +372,19 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[4 * t + i] = s[t][i] * a.c;
+        if constexpr (ROPE) {
+            // the block holding the token: its K and V rows came from the cache
+            // before the token was stored.  The token's score replaces the one
+            // of its row (key rr: lane group rr >> 3, element rr % 8 of x), and
+            // after the softmax its V bits replace the loaded ones.
+            if (tok_here) {
+                const uint32_t jt = rr & 7u;
+                const bool grp_here = (uint32_t)g == rr >> 3;
+                const float xt = stok * a.c;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = grp_here && (uint32_t)j == jt ? xt : x[j];
+            }
+        }
         const bool tail = key0 + kKeysPerBlock > kend;
         if (tail) {
 #pragma unroll
@@ -408,6 +416,49 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
                 for (int j = 0; j < 8; ++j)
                     if (key0 + 8 * g + j >= kend) f.v[b][j] = (_Float16)0.0f;
         }
+        if constexpr (ROPE) {
+            if (tok_here) {
+                // V: the token is element e = rr % 8 -- the same for every lane
+                // of the wave -- of the lanes of group rr >> 3, so only dword
+                // e / 2 of each fragment changes, in its half e % 2: masked
+                // merges with the lane's token values read unconditionally (a
+                // select on a value read from LDS became a branch per fragment,
+                // +1 us for the owner's wave at d = 256)
+                constexpr int NBH = NB / 8 > 0 ? NB / 8 : 1;  // 16-byte reads per lane
+                uint16_t vrow[NBH * 8];
+#pragma unroll
+                for (int u = 0; u < NBH; ++u) {
+                    if constexpr (NB >= 8) {
+                        const u32x4 w4 = *reinterpret_cast<const u32x4*>(&s_vt[n][8 * u]);
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            vrow[8 * u + 2 * k] = (uint16_t)(w4[k] & 0xffffu);
+                            vrow[8 * u + 2 * k + 1] = (uint16_t)(w4[k] >> 16);
+                        }
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < NB; ++k) vrow[k] = s_vt[n][k];
+                    }
+                }
+                const uint32_t e = rr & 7u, sh = (e & 1u) * 16u;
+                const uint32_t msk = (uint32_t)g == rr >> 3 ? 0xffffu << sh : 0u;
+                auto put_v = [&](auto W) {
+                    constexpr int w = decltype(W)::value;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        u32x4 x4 = __builtin_bit_cast(u32x4, f.v[b]);
+                        x4[w] = (x4[w] & ~msk) | (((uint32_t)vrow[b] << sh) & msk);
+                        f.v[b] = __builtin_bit_cast(f16x8, x4);
+                    }
+                };
+                switch (e >> 1) {  // uniform over the wave
+                case 0: put_v(std::integral_constant<int, 0>{}); break;
+                case 1: put_v(std::integral_constant<int, 1>{}); break;
+                case 2: put_v(std::integral_constant<int, 2>{}); break;
+                default: put_v(std::integral_constant<int, 3>{}); break;
+                }
+            }
+        }
         f16x8 pf;
 #pragma unroll
         for (int j = 0; j < 8; ++j) pf[j] = (_Float16)p[j];
@@ -438,7 +489,7 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     if (ROPE && owns_tok && threadIdx.x < (uint32_t)D) {  // the token's K and V into the cache
         const uint32_t d = threadIdx.x;
         rp.kc[k_index(kvh, tpos, d, D, a.kv_stride)] = s_knew[d];
-        rp.vc[v_index(kvh, tpos, d, D, a.kv_stride)] = s_vnew[d];
+        rp.vc[v_index(kvh, tpos, d, D, a.kv_stride)] = s_vt[d % 16][d / 16];
     }
     // per-lane partial sums -> per head (the four lane groups hold one head)
     l += __shfl_xor(l, 16, 64);
