@@ -240,8 +240,10 @@ def test_decode_rope_matches_oracle_and_two_launches(cuda, oracle, kind, nh, nkv
     and decode) and against yhip_rope_kv_store + yhip_attn_decode on a copy
     of the same cache.  The fused path takes the host's cosf / sinf of the
     reference's angles, the two-launch path the device's: q and the stored
-    key may differ by an fp32 / f16 ulp, the values and the earlier rows are
-    bit for bit the same."""
+    key may differ by an fp32 / f16 ulp, and a score an ulp apart can round
+    its probability to the neighbouring f16 (2^-11 of that key's weight), so
+    the two outputs agree to 1e-4 rel-L2 -- and bit for bit when nothing is
+    rotated; the values and the earlier rows are bit for bit the same."""
     from yllm_amd.attention import (ROPE_HALF, ROPE_MROPE, ROPE_NONE, ROPE_PAIRS, LayerKV, attn_decode,
                                     attn_decode_rope, kv_store, rope_kv_store)
 
@@ -282,7 +284,9 @@ def test_decode_rope_matches_oracle_and_two_launches(cuda, oracle, kind, nh, nkv
     ulps_two = f16_ulps(kb_row, Ka[:, pos, :].reshape(-1)).max()
     print(f"decode_rope {kind} {nh}/{nkv} d={d} pos={pos}: rel_l2 vs oracle {err:.2e}, vs two launches "
           f"{err2:.2e}; token K row vs oracle <= {ulps_ref} ulp, vs two launches <= {ulps_two} ulp")
-    assert err <= TOL_ATT and err2 <= 1e-5
+    assert err <= TOL_ATT and err2 <= 1e-4
+    if rope == ROPE_NONE:
+        assert np.array_equal(got, two)
     # the fused launch rotates with the host's cosf / sinf of the reference's angles: the stored key is the
     # oracle's bit for bit; the two-launch path (device sincosf) may be an ulp apart
     assert ulps_ref == 0 and ulps_two <= 1

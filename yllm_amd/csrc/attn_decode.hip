@@ -511,9 +511,13 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][n]);
         const float sc = m == -INFINITY ? 0.0f : fast_exp2(m - M);
+        // only the group's G heads are staged (the padded slots' LDS writes
+        // were most of the combine's LDS traffic at G <= 8)
+        if ((uint32_t)n < G) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
-            *reinterpret_cast<f32x4*>(&s_o[wave][n][b * 16 + 4 * g]) = o[b] * sc;
+            for (int b = 0; b < NB; ++b)
+                *reinterpret_cast<f32x4*>(&s_o[wave][n][b * 16 + 4 * g]) = o[b] * sc;
+        }
         if (wave == 0 && g == 0) {
             float L = 0.0f;
 #pragma unroll
@@ -680,6 +684,21 @@ uint64_t plan_target_wg(uint32_t n_seq)
     return env_wg > 0 ? (uint64_t)env_wg : (n_seq == 1 ? 256 : 3072);
 }
 
+// A context whose K and V take at most this many bytes per kv head is not
+// split: one workgroup per (sequence, kv head) writes the output directly,
+// without partials and the merge launch (~4.5 us of launch gap and merge).
+// Measured on MI355X, graph-replayed: 64 KiB 3.8 vs 6.5 us, 128 KiB 5.1-5.6
+// vs 6.6-8.1 us (14/2 d 64, 32/8 d 128, 8/8 d 64), 256 KiB a tie (7.8-10.2
+// both ways), 512 KiB 13-16 vs 7-10 us.  YHIP_DECODE_ONE_SPLIT overrides it.
+uint64_t plan_one_split_bytes()
+{
+    static const uint64_t b = [] {
+        const char* e = getenv("YHIP_DECODE_ONE_SPLIT");
+        return e ? (uint64_t)atoll(e) : (uint64_t)160 * 1024;
+    }();
+    return b;
+}
+
 uint64_t plan_min_split()
 {
     static const uint64_t min_sk = [] {
@@ -710,8 +729,8 @@ size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_
     // split size that leaves a nearly empty last round costs a whole round
     // (64 sequences of 1k..32k keys: 4.5 TB/s at 2048 workgroups, 5.9 at
     // 3072).  A split is a multiple of 128 keys (one 32-key block per wave);
-    // short contexts with few kv heads get splits down to 128 keys so they
-    // still spread over many CUs.
+    // longer contexts with few kv heads get splits down to 128 keys so they
+    // still spread over many CUs; short ones are not split at all.
     const uint64_t target_wg = plan_target_wg(n_seq), min_sk = plan_min_split();
     const uint64_t work = total_len * (uint64_t)n_kv;
     uint64_t sk = (work + target_wg - 1) / target_wg;
@@ -719,7 +738,7 @@ size_t decode_plan(uint32_t n_seq, uint32_t max_len, uint64_t total_len, uint32_
     if (sk < (max_len + kMaxSplits - 1) / kMaxSplits) sk = ((uint64_t)max_len + kMaxSplits - 1) / kMaxSplits;
     sk = (sk + 127) / 128 * 128;
     uint32_t ns;
-    if (sk >= max_len) {
+    if (sk >= max_len || (uint64_t)max_len * D * 4 <= plan_one_split_bytes()) {
         sk = ((uint64_t)max_len + 31) / 32 * 32;
         if (sk < 32) sk = 32;
         ns = 1;
