@@ -39,6 +39,39 @@ constexpr int kThreads = 256;
 constexpr int kCols = 16;  // state columns per workgroup
 constexpr int kMaxKw = 8;
 
+// Cross-lane sums in the VALU (DPP row permutations and gfx950's permlane
+// swaps) instead of ds_bpermute round trips through the LDS unit: every lane
+// of the group ends with the same total, added in the same order.
+template <int CTRL>
+__device__ inline float dpp_f(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+// over each 8-lane group: xor 1, xor 2 (quad permutations), then the other
+// quad of the group (half-row mirror)
+__device__ inline float sum8(float x)
+{
+    x += dpp_f<0xb1>(x);   // quad_perm [1, 0, 3, 2]
+    x += dpp_f<0x4e>(x);   // quad_perm [2, 3, 0, 1]
+    x += dpp_f<0x141>(x);  // row_half_mirror
+    return x;
+}
+__device__ inline float sum16(float x)
+{
+    x = sum8(x);
+    return x + dpp_f<0x140>(x);  // row_mirror: the other half of the row
+}
+__device__ inline float sum64(float x)
+{
+    x = sum16(x);
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);  // rows 0 + 1, 2 + 3
+    x = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+    const auto hv = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                     false, false);  // halves
+    return __builtin_bit_cast(float, (uint32_t)hv[0]) + __builtin_bit_cast(float, (uint32_t)hv[1]);
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(GdnDecodeArgs a)
 {
@@ -197,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(GdnDecodeArgs a)
 // Measured at 16 heads, d 128, in graphs of 400 tokens: 6.6 us per token
 // with NP = 1, 5.75 with NP = 8.  With NP > 1 a part reads columns other
 // parts write, so the state must go out of place (S_out != S).
-template <int D, int NP>
+template <int D, int NP, int KWM>
 __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
 {
 #pragma clang fp contract(off)
@@ -207,9 +240,13 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     constexpr uint32_t CPP = D / NP;  // columns stored per part
     static_assert(3 * D <= NT, "one conv channel per thread");
     static_assert(D % NP == 0, "whole columns per part");
+    static_assert(TPC == 8 || TPC == 16, "a state column's threads sum in one row");
     __shared__ float qs[D], ks[D], vs[D];
     __shared__ float l2p[2 * D / 64];  // per wave: sum of squares of its q or k channels
     __shared__ float ssq[NT / 64];
+    __shared__ float s_gate[2];  // beta, g of the head
+    constexpr int GW = 3 * D / 64;  // the first wave without a conv channel computes the gates
+    static_assert(GW < NT / 64, "a wave without a conv channel");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t b = blockIdx.x, h = (b % 8u) + 8u * (b / (8u * NP)), pt = (b / 8u) % NP;
@@ -220,6 +257,10 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     const uint32_t own0 = pt * CPP;
     const bool own_col = j - own0 < CPP;  // this part stores column j
 
+    // the head's gate inputs (engine.c:788-793) first: every load of the
+    // token is issued before any wait, so its chain holds one memory round
+    // trip
+    const float beta_raw = a.beta_raw[h], alpha = a.alpha[h], dt_bias = a.dt_bias[h], ssm_a = a.ssm_a[h];
     const float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
     float* So = a.S_out + ((size_t)h * D + j) * D + part * SL;
     float s[SL];
@@ -231,55 +272,60 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     }
     // this thread's conv channel: q (tid < D), k (< 2D) of head kh, v (< 3D) of head h
     const bool has_ch = tid < 3 * D;
-    const uint32_t ch = tid < D ? kh * D + tid
+    const uint32_t ch = !has_ch ? 0u
+                        : tid < D ? kh * D + tid
                         : tid < 2 * D ? key_dim + kh * D + (tid - D)
                                       : 2 * key_dim + h * D + (tid - 2 * D);
-    float X[kMaxKw], w[kMaxKw];
-    if (has_ch) {
+    // KWM taps are loaded by every thread from valid addresses (taps past
+    // kwidth repeat the last weight and the current row, and are not used): a
+    // load under a condition, into a register that starts at zero, made the
+    // compiler wait for every earlier load before the next one was issued
+    const uint32_t kw = a.kwidth;
+    float X[KWM], w[KWM];
 #pragma unroll
-        for (int r = 0; r < kMaxKw; ++r) {
-            if (r >= (int)a.kwidth) break;
-            w[r] = a.conv_w[(size_t)ch * a.kwidth + r];
-            X[r] = r + 1 < (int)a.kwidth ? a.conv_in[(size_t)(r + 1) * a.conv_dim + ch] : a.qkv[ch];
-        }
+    for (int r = 0; r < KWM; ++r) {
+        w[r] = a.conv_w[(size_t)ch * kw + min((uint32_t)r, kw - 1u)];
+        const float* src = (uint32_t)r + 1u < kw ? a.conv_in + (size_t)(r + 1) * a.conv_dim : a.qkv;
+        X[r] = src[ch];
     }
-    const float zv = part == 0 ? a.z[(size_t)h * D + j] : 0.0f;
-    const float wv = part == 0 ? (a.norm_w_f16 ? (float)reinterpret_cast<const _Float16*>(a.norm_w)[j]
-                                               : reinterpret_cast<const float*>(a.norm_w)[j])
-                               : 0.0f;
-    // gates (engine.c:788-793), read with the other loads: after a barrier
-    // their loads would add a memory round trip to the token's chain
-    const float bt = 1.0f / (1.0f + expf(-a.beta_raw[h]));
-    const float g = expf(log1pf(expf(a.alpha[h] + a.dt_bias[h])) * a.ssm_a[h]);
+    // z and the norm weight of column j, for every thread (part 0 uses them);
+    // the weight as two 16-bit loads whose indices are in bounds for both
+    // dtypes, joined where it is used
+    const float zv = a.z[(size_t)h * D + j];
+    const uint16_t* nw16 = reinterpret_cast<const uint16_t*>(a.norm_w);
+    const uint16_t w_lo = nw16[a.norm_w_f16 ? j : 2 * j], w_hi = nw16[a.norm_w_f16 ? j : 2 * j + 1];
     float y = 0.0f;
     if (has_ch) {
         float acc = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kMaxKw; ++r) {
-            if (r >= (int)a.kwidth) break;
-            acc = acc + X[r] * w[r];
-        }
+        for (int r = 0; r < KWM; ++r)
+            if ((uint32_t)r < kw) acc = acc + X[r] * w[r];
         y = acc / (1.0f + expf(-acc));
         if (tid < D) qs[tid] = y;
         else if (tid < 2 * D) ks[tid - D] = y;
         else vs[tid - 2 * D] = y;
-        // the delay line: head kh's q/k channels by part 0 of v head kh
-        // (n_v >= n_k), v channels by the part of their own head that
-        // stores that column
-        if (tid >= 2 * D ? (uint32_t)(tid - 2 * D) - own0 < CPP : (h == kh && pt == 0)) {
-#pragma unroll
-            for (int r = 0; r < kMaxKw; ++r) {
-                if (r >= (int)a.kwidth) break;
-                a.conv_out[(size_t)r * a.conv_dim + ch] = X[r];
-            }
+    }
+    // the norm weight and z's silu, while their loads have just landed: used
+    // only at the end, their waits there also waited for the state stores
+    // (in-order memory counter), and the output store's latency added to theirs
+    float wv = a.norm_w_f16 ? (float)__builtin_bit_cast(_Float16, w_lo)
+                            : __builtin_bit_cast(float, (uint32_t)w_lo | (uint32_t)w_hi << 16);
+    float zs = zv / (1.0f + expf(-zv));
+    asm volatile("" : "+v"(wv), "+v"(zs));
+    // the gates once per workgroup, by a wave that has no conv channel (every
+    // wave computing them cost ~0.3 us of VALU issue per SIMD)
+    if (wave == GW) {
+        const float bt_ = 1.0f / (1.0f + expf(-beta_raw));
+        const float g_ = expf(log1pf(expf(alpha + dt_bias)) * ssm_a);
+        if (lane == 0) {
+            s_gate[0] = bt_;
+            s_gate[1] = g_;
         }
     }
     // l2 norms: the q channels are waves 0 .. D/64-1, the k channels the next
     // D/64 waves; each wave sums its squares, one barrier publishes them
     // (the reference sums in order; this is a tree, equal to rounding)
-    float y2 = tid < 2 * D ? y * y : 0.0f;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) y2 += __shfl_xor(y2, m, 64);
+    const float y2 = sum64(tid < 2 * D ? y * y : 0.0f);
     if (lane == 0 && wave < 2 * D / 64) l2p[wave] = y2;
     lds_barrier();
     float qq = 0.0f, kk = 0.0f;
@@ -290,32 +336,59 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     }
     const float rq = 1.0f / fmaxf(sqrtf(qq), a.l2_eps), rk = 1.0f / fmaxf(sqrtf(kk), a.l2_eps);
 
-    float k[SL], q[SL];
+    const float bt = s_gate[0], g = s_gate[1];
+
+    auto sum_tpc = [](float x) { return TPC == 8 ? sum8(x) : sum16(x); };
+    float kr[SL], qr[SL];  // the thread's slice of the raw q, k rows
 #pragma unroll
     for (int i = 0; i < SL; ++i) {
-        k[i] = ks[part * SL + i] * rk;
-        q[i] = qs[part * SL + i] * rq;
+        kr[i] = ks[part * SL + i];
+        qr[i] = qs[part * SL + i];
     }
-    auto sum_tpc = [](float x) {
-#pragma unroll
-        for (int m = TPC / 2; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
-        return x;
-    };
-    float p = 0.0f;
-#pragma unroll
-    for (int i = 0; i < SL; ++i) {
-        s[i] *= g;
-        p = fmaf(s[i], k[i], p);
-    }
-    const float delta = (vs[j] - sum_tpc(p)) * bt;
-    float p2 = 0.0f;
+    // Column j's output for the norm's sum of squares only, from the state
+    // before the token: o_j = (g rq (S_j . q) + d_j rk rq (k . q)) / sqrt(D)
+    // with d_j = (v_j - g rk (S_j . k)) beta -- the update's algebra in
+    // another order, equal to the exact o_j within rounding, at three FMAs
+    // per state element.  Every part forms it for every column (the norm
+    // needs all D outputs; in place as out of place, so both give the same
+    // bits), and only its own columns the exact way.
+    float pa = 0.0f, pb = 0.0f, pkq = 0.0f;
 #pragma unroll
     for (int i = 0; i < SL; ++i) {
-        s[i] = fmaf(k[i], delta, s[i]);
-        p2 = fmaf(s[i], q[i], p2);
+        pa = fmaf(s[i], qr[i], pa);
+        pb = fmaf(s[i], kr[i], pb);
+        pkq = fmaf(kr[i], qr[i], pkq);
     }
-    const float o = sum_tpc(p2) * (1.0f / sqrtf((float)D));
+    pa = sum_tpc(pa);
+    pb = sum_tpc(pb);
+    pkq = sum_tpc(pkq);
+    const float dn = (vs[j] - g * rk * pb) * bt;
+    const float on = (g * rq * pa + dn * (rk * rq * pkq)) * (1.0f / sqrtf((float)D));
+
+    // the exact update and output of the part's own columns (CPP * TPC
+    // consecutive threads: whole waves), in the reference's order
+    float o = 0.0f;
     if (own_col) {
+        float k[SL], q[SL];
+#pragma unroll
+        for (int i = 0; i < SL; ++i) {
+            k[i] = kr[i] * rk;
+            q[i] = qr[i] * rq;
+        }
+        float p = 0.0f;
+#pragma unroll
+        for (int i = 0; i < SL; ++i) {
+            s[i] *= g;
+            p = fmaf(s[i], k[i], p);
+        }
+        const float delta = (vs[j] - sum_tpc(p)) * bt;
+        float p2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < SL; ++i) {
+            s[i] = fmaf(k[i], delta, s[i]);
+            p2 = fmaf(s[i], q[i], p2);
+        }
+        o = sum_tpc(p2) * (1.0f / sqrtf((float)D));
 #pragma unroll
         for (int i = 0; i < SL; i += 4) {
             f32x4 x;
@@ -326,16 +399,23 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     }
     // rmsnorm_gated over the head's D outputs (matvec.c:1007-1021), as
     // gdn_gated_norm_kernel computes it
-    float sq = part == 0 ? o * o : 0.0f;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) sq += __shfl_xor(sq, m, 64);
+    const float sq = sum64(part == 0 ? on * on : 0.0f);
     if (lane == 0) ssq[wave] = sq;
     lds_barrier();
     float ss = 0.0f;
 #pragma unroll
     for (int wv2 = 0; wv2 < NT / 64; ++wv2) ss += ssq[wv2];
     const float inv = 1.0f / sqrtf(ss / (float)D + a.norm_eps);
-    if (part == 0 && own_col) a.y[(size_t)h * D + j] = o * wv * inv * (zv / (1.0f + expf(-zv)));
+    if (part == 0 && own_col) a.y[(size_t)h * D + j] = o * wv * inv * zs;
+    // the delay line last (nothing here reads it; stored earlier, a wait for a
+    // load issued before it waited for the store too): head kh's q/k channels
+    // by part 0 of v head kh (n_v >= n_k), v channels by the part of their
+    // own head that stores that column
+    if (has_ch && (tid >= 2 * D ? (uint32_t)(tid - 2 * D) - own0 < CPP : (h == kh && pt == 0))) {
+#pragma unroll
+        for (int r = 0; r < KWM; ++r)
+            if ((uint32_t)r < kw) a.conv_out[(size_t)r * a.conv_dim + ch] = X[r];
+    }
 }
 
 }  // namespace
@@ -344,7 +424,10 @@ template <int D, int NP>
 void launch_head(const GdnDecodeArgs& a, hipStream_t st)
 {
     const uint32_t grid = 8u * NP * ((a.n_v + 7u) / 8u);
-    hipLaunchKernelGGL((gdn_decode_head_kernel<D, NP>), dim3(grid), dim3(1024), 0, st, a);
+    if (a.kwidth <= 4)
+        hipLaunchKernelGGL((gdn_decode_head_kernel<D, NP, 4>), dim3(grid), dim3(1024), 0, st, a);
+    else
+        hipLaunchKernelGGL((gdn_decode_head_kernel<D, NP, kMaxKw>), dim3(grid), dim3(1024), 0, st, a);
 }
 
 hipError_t launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t st)
