@@ -394,8 +394,8 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         float mx = x[0];
 #pragma unroll
         for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[j]);
-        mx = wave_max_xor(mx, 16);
-        mx = wave_max_xor(mx, 32);
+        mx = max_xor16(mx);
+        mx = max_xor32(mx);
         const float mn = fmaxf(m, mx);
         const float alpha = fast_exp2(m - mn);
         float p[8], ps = 0.0f;
@@ -492,8 +492,8 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         rp.vc[v_index(kvh, tpos, d, D, a.kv_stride)] = s_vt[d % 16][d / 16];
     }
     // per-lane partial sums -> per head (the four lane groups hold one head)
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = sum_xor16(l);
+    l = sum_xor32(l);
     if (g == 0) {
         s_m[wave][n] = m;
         s_l[wave][n] = l;
