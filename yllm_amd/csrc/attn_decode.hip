@@ -582,32 +582,38 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
     const uint32_t e4 = t % E4, sg = t / E4;
     const uint32_t d = d0 + 4 * e4;
 
-    f32x4 gt = f32x4{1.f, 1.f, 1.f, 1.f};
-    if (a.gate && sg == 0) {  // gate rows need not be 16-byte aligned
-        const float* gp = a.gate + (size_t)seq * a.gate_stride + (size_t)h * D + d;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) gt[e] = gp[e];
-    }
-
+    // Every load below is issued unconditionally from a valid address (the
+    // output row stands in for a missing gate; splits past ns read slot 0 and
+    // are masked by selects), the first round's partials and the gate before
+    // any wait: a load under a condition, into a register set beforehand, made
+    // the compiler wait for it before issuing the next one (one memory round
+    // trip per round of splits, 3.4 us per merge at 34 splits), and a loop
+    // around the first round waited for the gate first.  Gate rows need not be
+    // 16-byte aligned.
     constexpr uint32_t kRound = 8;
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    f32x2 ml[kRound];
+    f32x4 ov[kRound];
     float M = -INFINITY, L = 0.0f;
     f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t s0 = sg; s0 < ns; s0 += NG * kRound) {
+    auto issue = [&](uint32_t s0) {
+#pragma unroll
+        for (uint32_t r = 0; r < kRound; ++r) {
+            const uint32_t s = s0 + r * NG;
+            const size_t slot = (sbase + (s < ns ? s : 0u)) * a.gmax + hn;
+            ml[r] = *reinterpret_cast<const f32x2*>(a.part_ml + slot * 2);
+            ov[r] = *reinterpret_cast<const f32x4*>(a.part_o + slot * D + d);
+        }
+    };
+    auto fold = [&](uint32_t s0) {
         float ms[kRound], ls[kRound];
         f32x4 os[kRound];
 #pragma unroll
         for (uint32_t r = 0; r < kRound; ++r) {
-            const uint32_t s = s0 + r * NG;
-            if (s < ns) {
-                const size_t slot = (sbase + s) * a.gmax + hn;
-                ms[r] = a.part_ml[slot * 2];
-                ls[r] = a.part_ml[slot * 2 + 1];
-                os[r] = *reinterpret_cast<const f32x4*>(a.part_o + slot * D + d);
-            } else {
-                ms[r] = -INFINITY;
-                ls[r] = 0.0f;
-                os[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+            const bool ok = s0 + r * NG < ns;
+            ms[r] = ok ? ml[r][0] : -INFINITY;
+            ls[r] = ok ? ml[r][1] : 0.0f;
+            os[r] = ok ? ov[r] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
         float mr = M;
 #pragma unroll
@@ -624,11 +630,24 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
             }
             M = mr;
         }
+    };
+    issue(sg);
+    const float* gp = a.gate ? a.gate + (size_t)seq * a.gate_stride + (size_t)h * D + d
+                             : a.out + (size_t)seq * a.out_stride + (size_t)h * D + d;
+    f32x4 gt;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gt[e] = gp[e];
+    __builtin_amdgcn_sched_barrier(0);  // the round's loads and the gate in flight before any use
+    fold(sg);
+    for (uint32_t s0 = sg + NG * kRound; s0 < ns; s0 += NG * kRound) {  // more than NG * kRound splits
+        issue(s0);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(s0);
     }
     s_o[t] = O;
     s_m[t] = M;
     s_l[t] = L;
-    __syncthreads();
+    lds_barrier();  // the gate's load may still be in flight
     if (t < E4) {
         float Mt = -INFINITY;
 #pragma unroll
