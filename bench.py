@@ -305,6 +305,7 @@ def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, step
                              steps, warmup, out)
     nbytes = decode_bytes(L, nkv, nh, hd)
     achieved = nbytes / (kern_ms * 1e-3)
+    one = L * hd * 4 <= 160 * 1024  # the library's plan runs such a context unsplit
     res = {
         "value": nbytes / (ms * 1e-3) / 1e9,
         "unit": "GB/s",
@@ -312,10 +313,12 @@ def run_decode(L: int, nh: int, nkv: int, hd: int, cfg: int, n_layers: int, step
         "tokens_per_s": 1.0 / (ms * 1e-3),
         "config": {"workload": f"{label}: decode attention, 1 sequence, {L} keys, {nh} query / {nkv} KV heads, "
                                f"head_dim {hd}, f16 KV N(0,1)*0.5 seed {hex(seed)}, "
-                               f"{'fp32' if q_f32 else 'f16-valued'} q, split-K + LSE merge, "
+                               f"{'fp32' if q_f32 else 'f16-valued'} q, "
+                               f"{'one split per KV head (K+V <= 160 KiB per head), no merge' if one else 'split-K + LSE merge'}, "
                                f"{n_layers} rotating layer caches",
                    "keys": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd},
-        "roofline": {"bound": "hbm", "kernel": "decode_split_kernel<%d> + decode_merge_kernel<%d>" % (hd, hd),
+        "roofline": {"bound": "hbm", "kernel": ("decode_split_kernel<%d>" % hd if one else
+                                                "decode_split_kernel<%d> + decode_merge_kernel<%d>" % (hd, hd)),
                      "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK, "bytes_per_launch": nbytes, "launch_ms": kern_ms,
                      "traffic": traffic_of(label)},

@@ -939,6 +939,14 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a)
     const uint32_t b = row / a.n_heads, h = row % a.n_heads;
     const size_t split_stride = (size_t)a.n_heads * a.B;
     const size_t p0 = (size_t)h * a.B + b;
+    const uint32_t d = 4 * c4;
+    // the gate is read with the partials, not after them (a second memory
+    // round trip); without a gate the output row stands in as a valid address
+    const float* gp = a.gate ? a.gate + (size_t)b * a.gate_stride + (size_t)h * D + d
+                             : reinterpret_cast<const float*>(a.out);
+    f32x4 gt;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gt[e] = gp[e];
     float M = -1e30f, L = 0.0f;
     f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
     for (uint32_t s0 = 0; s0 < a.n_split; s0 += kRound) {
@@ -971,11 +979,9 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a)
     }
     // every query has key 0 in split 0, so L > 0
     f32x4 v = O * (1.0f / L);
-    const uint32_t d = 4 * c4;
     if (a.gate) {
-        const float* gp = a.gate + (size_t)b * a.gate_stride + (size_t)h * D + d;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] *= sigmoid_ref(gp[e]);
+        for (int e = 0; e < 4; ++e) v[e] *= sigmoid_ref(gt[e]);
     }
     store_out4(a.out, (size_t)b * a.out_stride + (size_t)h * D + d, a.out_dtype, v);
 }
