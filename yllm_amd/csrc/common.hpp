@@ -130,4 +130,30 @@ __device__ inline float sum_xor32(float x)
     return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
+template <int CTRL>
+__device__ inline float dpp_mov(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// The sum over each aligned group of N lanes (N = 16, 32, 64) in the order
+// of the __shfl_xor butterfly with masks N/2, ..., 2, 1, bit for bit its
+// result, by VALU lane exchanges instead of ds_bpermute round trips through
+// the LDS unit: permlane swaps for 32 and 16, a row rotation by 8 for xor 8,
+// a row rotation by 4 for xor 4 (after the xor-8 step lanes l and l ^ 8 hold
+// the same value, so lane (l + 4) mod 16 holds lane l ^ 4's), quad
+// permutations for 2 and 1.  (x + p and p + x are the same float.)
+template <int N>
+__device__ inline float xor_sum(float x)
+{
+    static_assert(N == 16 || N == 32 || N == 64, "groups of 16, 32 or 64 lanes");
+    if constexpr (N == 64) x = sum_xor32(x);
+    if constexpr (N >= 32) x = sum_xor16(x);
+    x += dpp_mov<0x128>(x);  // row_ror:8
+    x += dpp_mov<0x124>(x);  // row_ror:4
+    x += dpp_mov<0x4e>(x);   // quad_perm [2, 3, 0, 1]
+    x += dpp_mov<0xb1>(x);   // quad_perm [1, 0, 3, 2]
+    return x;
+}
+
 }  // namespace yhip

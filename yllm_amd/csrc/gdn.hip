@@ -129,8 +129,7 @@ __global__ __launch_bounds__(256, 1) void gdn_kernel(GdnArgs a)
                 x[u] = row[lane + 64 * u];
                 ss += x[u] * x[u];
             }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+            ss = xor_sum<64>(ss);
             const float rs = 1.0f / fmaxf(sqrtf(ss), a.eps);
 #pragma unroll
             for (int u = 0; u < D / 64; ++u) row[lane + 64 * u] = x[u] * rs;
@@ -343,11 +342,8 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
                     kk += kv[u][x] * kv[u][x];
                     qq += qv[u][x] * qv[u][x];
                 }
-#pragma unroll
-                for (int m = RL / 2; m >= 1; m >>= 1) {
-                    kk += __shfl_xor(kk, m, 64);
-                    qq += __shfl_xor(qq, m, 64);
-                }
+                kk = xor_sum<RL>(kk);
+                qq = xor_sum<RL>(qq);
                 kv[u] *= 1.0f / fmaxf(sqrtf(kk), a.eps);
                 qv[u] *= 1.0f / fmaxf(sqrtf(qq), a.eps);
             }
@@ -905,11 +901,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnArgs a)
     }
     const float vj = a.v[(size_t)h * D + j];
     const float g = expf(a.gate[h]), bt = a.beta[h];
-    auto sum16 = [](float x) {
-#pragma unroll
-        for (int m = 8; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
-        return x;
-    };
+    auto sum16 = [](float x) { return xor_sum<16>(x); };
     if (a.eps > 0.0f) {
         float kk = 0.0f, qq = 0.0f;
 #pragma unroll

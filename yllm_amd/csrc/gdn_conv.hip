@@ -117,8 +117,7 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(GdnNormArgs a)
         xv[k] = k < per ? x[k * 64 + lane] : 0.0f;
         ss += xv[k] * xv[k];
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    ss = xor_sum<64>(ss);
     const float inv = 1.0f / sqrtf(ss / (float)a.head_dim + a.eps);
 #pragma unroll
     for (uint32_t k = 0; k < 4; ++k) {

@@ -94,8 +94,7 @@ __global__ __launch_bounds__(256) void oproj_gemv_kernel(OProjArgs a)
     for (uint32_t r = 0; r < kRows; ++r)
 #pragma unroll
         for (int b = 0; b < NB; ++b)
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) acc[r][b] += __shfl_xor(acc[r][b], m, 64);
+            acc[r][b] = xor_sum<64>(acc[r][b]);
     if (lane == 0) {
 #pragma unroll
         for (uint32_t r = 0; r < kRows; ++r) {
