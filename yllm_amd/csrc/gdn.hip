@@ -319,6 +319,13 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
     const int nt = (int)min((uint32_t)kC, a.T - t0);
     ChunkWs<D> w(a.ws, h, c, a.n_chunks);
 
+    // the chunk's gates and betas (token = lane, clamped to the last token;
+    // wave 0 masks them): read with the q / k rows, unconditionally -- read
+    // under lane < nt they came after a wait for every q / k load, a second
+    // memory round trip
+    const size_t gi = (size_t)(t0 + min(lane, nt - 1)) * a.n_v + h;
+    const float g_raw = a.gate[gi], b_raw = a.beta[gi];
+
     // q and k rows of the chunk (zero past the last token): all loads issued
     // before any LDS store; the l2 norms are taken in registers (a row's D/4
     // float4s sit in D/4 consecutive lanes)
@@ -358,8 +365,8 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
     }
     // gates: inclusive prefix sum of the log-decays over the chunk
     if (wave == 0) {
-        float gv = lane < nt ? a.gate[(size_t)(t0 + lane) * a.n_v + h] : 0.0f;
-        const float bv = lane < nt ? a.beta[(size_t)(t0 + lane) * a.n_v + h] : 0.0f;
+        float gv = lane < nt ? g_raw : 0.0f;
+        const float bv = lane < nt ? b_raw : 0.0f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const float x = __shfl_up(gv, o, 64);
