@@ -726,8 +726,10 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
                       1e7, n_rot=64, q_out=q_out)
 
     def gdn_layer_prefill(li):
+        # the delay line out of place (cst -> cst2), as the device backend
+        # keeps it: one launch, where in place takes a second for the line
         g = gd[li]
-        gdn_conv(g["qkv"][:T], cst[li], g["conv_w"], out=xc[:T])
+        gdn_conv(g["qkv"][:T], cst[li], g["conv_w"], out=xc[:T], state_out=cst2[li])
         gdn_chunk(S[li], xc[:T, :kd], xc[:T, kd:2 * kd], xc[:T, 2 * kd:], gate[li][:T], beta[li][:T], hg,
                   out=gout[:T], workspace=ws)
         gdn_gated_norm(gout[:T], g["z"][:T], g["norm_w"], hg, out=gout[:T])
@@ -735,10 +737,10 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
     def gdn_layer_step(li, t):
         # one launch per layer and token; the state and the delay line
         # alternate between two buffers each, as the device backend keeps
-        # them (an even number of decode tokens ends back in S and cst)
+        # them (the prefill left the delay line in cst2)
         g = gd[li]
         even = (t - T) % 2 == 0
-        c_in, c_out = (cst[li], cst2[li]) if even else (cst2[li], cst[li])
+        c_in, c_out = (cst2[li], cst[li]) if even else (cst[li], cst2[li])
         s_in, s_out = (S[li], S2[li]) if even else (S2[li], S[li])
         gdn_decode(s_in, c_in, c_out, g["qkv"][t], g["z"][t], g["alpha"][t], g["beta_raw"][t], g["conv_w"], dt, a,
                    g["norm_w"], hg, y=gout[t], S_out=s_out)

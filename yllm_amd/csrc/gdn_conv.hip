@@ -100,33 +100,33 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(GdnConvArgs a)
     for (int r = 0; r < KW; ++r) a.state_out[(size_t)r * a.dim + ch] = nw[r];
 }
 
-template <int W_F16>
+// One wave per (token, head); PER = head_dim / 64 elements per lane.  x, z
+// and the weight are loaded together, before the sum (loaded after it, z and
+// the weight were a second memory round trip per wave).
+template <int W_F16, int PER>
 __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(GdnNormArgs a)
 {
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);  // (token, head) pair
     const int lane = threadIdx.x & 63;
     if (row >= a.T * a.n_heads) return;  // wave-uniform
     const uint32_t t = row / a.n_heads, h = row % a.n_heads;
-    const uint32_t per = a.head_dim / 64;
     const float* x = a.x + (size_t)t * a.x_stride + (size_t)h * a.head_dim;
     const float* z = a.z + (size_t)t * a.z_stride + (size_t)h * a.head_dim;
     float* y = a.y + (size_t)t * a.y_stride + (size_t)h * a.head_dim;
-    float xv[4], ss = 0.0f;
+    float xv[PER], zv[PER], wv[PER], ss = 0.0f;
 #pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-        xv[k] = k < per ? x[k * 64 + lane] : 0.0f;
-        ss += xv[k] * xv[k];
+    for (int k = 0; k < PER; ++k) {
+        const uint32_t i = k * 64 + lane;
+        xv[k] = x[i];
+        zv[k] = z[i];
+        wv[k] = W_F16 ? (float)reinterpret_cast<const _Float16*>(a.w)[i] : reinterpret_cast<const float*>(a.w)[i];
     }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) ss += xv[k] * xv[k];
     ss = xor_sum<64>(ss);
     const float inv = 1.0f / sqrtf(ss / (float)a.head_dim + a.eps);
 #pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-        if (k >= per) break;
-        const uint32_t i = k * 64 + lane;
-        const float wgt = W_F16 ? (float)reinterpret_cast<const _Float16*>(a.w)[i] : reinterpret_cast<const float*>(a.w)[i];
-        const float zg = z[i];
-        y[i] = xv[k] * wgt * inv * (zg / (1.0f + expf(-zg)));
-    }
+    for (int k = 0; k < PER; ++k) y[k * 64 + lane] = xv[k] * wv[k] * inv * (zv[k] / (1.0f + expf(-zv[k])));
 }
 
 template <int KW>
@@ -162,14 +162,25 @@ hipError_t launch_gdn_conv(const GdnConvArgs& a, hipStream_t st)
     return e;
 }
 
+template <int PER>
+void launch_norm_per(const GdnNormArgs& a, hipStream_t st)
+{
+    const dim3 grid((a.T * a.n_heads + 3) / 4);
+    if (a.w_f16)
+        hipLaunchKernelGGL((gdn_gated_norm_kernel<1, PER>), grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((gdn_gated_norm_kernel<0, PER>), grid, dim3(256), 0, st, a);
+}
+
 hipError_t launch_gdn_gated_norm(const GdnNormArgs& a, hipStream_t st)
 {
-    const uint32_t rows = a.T * a.n_heads;
-    const dim3 grid((rows + 3) / 4);
-    if (a.w_f16)
-        hipLaunchKernelGGL(gdn_gated_norm_kernel<1>, grid, dim3(256), 0, st, a);
-    else
-        hipLaunchKernelGGL(gdn_gated_norm_kernel<0>, grid, dim3(256), 0, st, a);
+    switch (a.head_dim) {
+    case 64: launch_norm_per<1>(a, st); break;
+    case 128: launch_norm_per<2>(a, st); break;
+    case 192: launch_norm_per<3>(a, st); break;
+    case 256: launch_norm_per<4>(a, st); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
