@@ -401,7 +401,11 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
     beta_raw = torch.from_numpy(synth_raw(seed, T * n_h, 3 * n + T * n_h).reshape(T, n_h)).to(dev)
     dt = torch.zeros(n_h, device=dev)
     a = -torch.ones(n_h, device=dev)
+    # the state goes out of place, as the device backend alternates two state
+    # buffers: S stays the zero state before the prompt, S2 takes the state
+    # after it
     S = torch.zeros((n_h, d, d), device=dev)
+    S2 = torch.empty_like(S)
     beta = torch.empty_like(beta_raw)
     gate = torch.empty_like(alpha)
     ws = torch.empty(max(gdn_chunk_workspace_bytes(T, n_h, d) // 4, 1), device=dev)
@@ -413,10 +417,9 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
 
     def step(i):
         qi, ki, vi, ai, bi, oi = sets[i % n_sets]
-        S.zero_()
         beta.copy_(bi)
         gdn_gates(ai, beta, dt, a, gate=gate)
-        gdn_chunk(S, qi, ki, vi, gate, beta, n_h, out=oi, workspace=ws, chunked=CHUNKED_GDN)
+        gdn_chunk(S, qi, ki, vi, gate, beta, n_h, out=oi, workspace=ws, chunked=CHUNKED_GDN, S_out=S2)
 
     ms, kern_ms = time_steps(step, steps, warmup, sets[(warmup + steps - 1) % n_sets][5])
     out = sets[(warmup + steps - 1) % n_sets][5]
@@ -706,7 +709,7 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
     dt = torch.zeros(hg, device=dev)
     a = -torch.ones(hg, device=dev)
     S = [torch.zeros((hg, dg, dg), device=dev) for _ in range(n_gdn)]
-    S2 = [torch.zeros((hg, dg, dg), device=dev) for _ in range(n_gdn)]  # the decode tokens alternate S and S2
+    S2 = [torch.zeros((hg, dg, dg), device=dev) for _ in range(n_gdn)]  # prefill and decode alternate S, S2
     cst = [torch.zeros((kw, conv), device=dev) for _ in range(n_gdn)]
     cst2 = [torch.zeros((kw, conv), device=dev) for _ in range(n_gdn)]
     beta = [torch.empty((L, hg), device=dev) for _ in range(n_gdn)]
@@ -726,22 +729,24 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
                       1e7, n_rot=64, q_out=q_out)
 
     def gdn_layer_prefill(li):
-        # the delay line out of place (cst -> cst2), as the device backend
-        # keeps it: one launch, where in place takes a second for the line
+        # the delay line and the state out of place (cst -> cst2, S -> S2),
+        # as the device backend keeps them: the conv in one launch, where in
+        # place takes a second for the line, and the chained recurrence on
+        # two workgroups per state slice
         g = gd[li]
         gdn_conv(g["qkv"][:T], cst[li], g["conv_w"], out=xc[:T], state_out=cst2[li])
         gdn_chunk(S[li], xc[:T, :kd], xc[:T, kd:2 * kd], xc[:T, 2 * kd:], gate[li][:T], beta[li][:T], hg,
-                  out=gout[:T], workspace=ws)
+                  out=gout[:T], workspace=ws, S_out=S2[li])
         gdn_gated_norm(gout[:T], g["z"][:T], g["norm_w"], hg, out=gout[:T])
 
     def gdn_layer_step(li, t):
         # one launch per layer and token; the state and the delay line
         # alternate between two buffers each, as the device backend keeps
-        # them (the prefill left the delay line in cst2)
+        # them (the prefill left the delay line in cst2 and the state in S2)
         g = gd[li]
         even = (t - T) % 2 == 0
         c_in, c_out = (cst2[li], cst[li]) if even else (cst[li], cst2[li])
-        s_in, s_out = (S[li], S2[li]) if even else (S2[li], S[li])
+        s_in, s_out = (S2[li], S[li]) if even else (S[li], S2[li])
         gdn_decode(s_in, c_in, c_out, g["qkv"][t], g["z"][t], g["alpha"][t], g["beta_raw"][t], g["conv_w"], dt, a,
                    g["norm_w"], hg, y=gout[t], S_out=s_out)
 
@@ -791,7 +796,8 @@ def run_hybrid(steps: int, warmup: int, cpu: bool, n_dec: int = 256):
         torch.cuda.synchronize()
         li = n_gdn - 1  # the shared output rows hold the last GDN layer's results
         res["cpu_baseline"] = cpu_hybrid(
-            {k2: v2.cpu().numpy() for k2, v2 in gd[li].items()}, S[li].cpu().numpy(), gout.cpu().numpy(),
+            {k2: v2.cpu().numpy() for k2, v2 in gd[li].items()}, (S2 if n_dec % 2 == 0 else S)[li].cpu().numpy(),
+            gout.cpu().numpy(),
             qkv.cpu().numpy(), at["gate"].cpu().numpy(), aout.float().cpu().numpy(), dout.cpu().numpy(),
             T, n_dec, n_gdn, hg, dg, kw, nh, nkv, da)
     return res

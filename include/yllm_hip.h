@@ -274,9 +274,11 @@ int yhip_gdn_step(float* S, float* out, const float* q, const float* k, const fl
  *
  * With a workspace of yhip_gdn_chunk_workspace(T, n_v_heads, head_dim)
  * bytes (16-byte aligned, no initialisation) and T >= 64, the chunked form
- * runs: 64-token chunks are reduced in parallel to matrix products (fp32
- * MFMA) and only the chunk-to-chunk state hand-over is sequential.  With
- * workspace NULL (or T < 64) the recurrence runs token by token. */
+ * runs: 64-token chunks are reduced in parallel to matrix products (MFMA)
+ * and only the chunk-to-chunk state hand-over is sequential.  Out of place
+ * (S_out another buffer) that sequential part runs on two workgroups per 16
+ * state rows when they fit the GPU (faster; the same bits as in place).
+ * With workspace NULL (or T < 64) the recurrence runs token by token. */
 int yhip_gdn_chunk(float* S, float* S_out, float* out, uint32_t out_stride, const float* q, const float* k,
                    uint32_t qk_stride, const float* v, uint32_t v_stride, const float* gate, const float* beta,
                    uint32_t T, uint32_t n_k_heads, uint32_t n_v_heads, uint32_t head_dim, float l2_eps,

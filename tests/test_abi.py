@@ -157,10 +157,9 @@ def test_gdn_rejects_bad_args(hiplib):
     rc = hiplib.yhip_gdn_chunk(P, None, P, 2048, P, P, 2048, P, 2048, P, P, 128, 16, 16, 128, F(1e-6), P, 4096, None)
     assert rc == -28 and "workspace" in _err(hiplib)
     assert hiplib.yhip_gdn_chunk_workspace(63, 16, 128) == 0
-    # per (head, chunk): -W in bf16, Q~ rows, K~ in bf16 hi / lo, P, U^T (Delta^T), gamma_last + pad, the
-    # chunk's starting state
+    # per (head, chunk): -W in bf16, Q~ and K~ in bf16 hi / lo, P likewise, U^T, gamma_last + pad
     assert hiplib.yhip_gdn_chunk_workspace(4096, 16, 128) == 64 * 16 * (64 * 128 // 2 + 2 * 64 * 128 + 64 * 64
-                                                                     + 64 * 128 + 4 + 128 * 128) * 4
+                                                                     + 64 * 128 + 4) * 4
     assert hiplib.yhip_gdn_gates(P, P, P, P, P, 0, 16, None) == 0
     # an out-of-place state that overlaps the state (16 heads x 128 x 128 floats = 1 MiB) is refused
     S0 = ctypes.c_void_p(0x4000000)

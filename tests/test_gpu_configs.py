@@ -101,7 +101,9 @@ def _gdn_layer_inputs(li, T, n_h, d, kw):
 def test_config5_gdn_layer_prefill_then_decode(cuda, oracle, li):
     """One of the group's three GDN layers: 4096-token prefill (conv + silu,
     gates, chunked recurrence, gated RMSNorm) then 256 fused decode tokens,
-    from a zero state and delay line; dt_bias 0, ssm_a -1."""
+    from a zero state and delay line; dt_bias 0, ssm_a -1.  The prefill's
+    state goes out of place, as the device backend keeps it (the chained
+    recurrence then runs two workgroups per state slice)."""
     from test_gpu_gdn import EPS, _oracle_layer
     from yllm_amd.gdn import gdn_chunk, gdn_chunk_workspace_bytes, gdn_conv, gdn_decode, gdn_gated_norm, gdn_gates
 
@@ -122,7 +124,9 @@ def test_config5_gdn_layer_prefill_then_decode(cuda, oracle, li):
     gate = torch.empty_like(beta)
     gdn_gates(al[:T0], beta, dtt, at, gate=gate)
     ws = torch.empty(gdn_chunk_workspace_bytes(T0, n_h, d) // 4, device=cuda)
-    out = gdn_chunk(S, xc[:, :kd], xc[:, kd:2 * kd], xc[:, 2 * kd:], gate, beta, n_h, workspace=ws)
+    S_pre = S
+    S = torch.full_like(S_pre, float("nan"))
+    out = gdn_chunk(S_pre, xc[:, :kd], xc[:, kd:2 * kd], xc[:, 2 * kd:], gate, beta, n_h, workspace=ws, S_out=S)
     y_pre = gdn_gated_norm(out, z_t[:T0], nw, n_h).cpu().numpy()
     ys = []
     for t in range(T0, T):

@@ -986,6 +986,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a)
     store_out4(a.out, (size_t)b * a.out_stride + (size_t)h * D + d, a.out_dtype, v);
 }
 
+}  // namespace
+
 int n_cus()
 {
     static const int n_cu = [] {
@@ -997,6 +999,8 @@ int n_cus()
     }();
     return n_cu;
 }
+
+namespace {
 
 // threads of a prefill workgroup: 4 waves per key group, 8 in pair mode
 constexpr int prefill_threads(int D, int NG) { return 256 * NG * (D > 128 ? 2 : 1); }

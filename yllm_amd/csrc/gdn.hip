@@ -14,8 +14,8 @@
 //
 // Three kernels.  A single token (a decode step) runs gdn_step_kernel; the
 // token-by-token kernel (gdn_kernel) serves short sequences and callers
-// without a workspace; the chunked form below (gdn_prep_kernel,
-// gdn_chain_kernel, gdn_out_kernel) serves prefill.
+// without a workspace; the chunked form below (gdn_prep_kernel, then
+// gdn_chain_kernel) serves prefill.
 //
 // Token by token.  A workgroup (4 waves) owns 64 columns of one head for the
 // whole sequence; lane l holds column j0+l and wave w the d_k slice
@@ -219,16 +219,13 @@ __global__ __launch_bounds__(256, 1) void gdn_kernel(GdnArgs a)
 //     M_last  = gamma_last M0 + Delta^T diag(e) K
 // (rows of Delta, V, K, Q, O are tokens).  With T = (I + A)^-1, U = T
 // diag(beta) V and W = T diag(beta*gamma) K, Delta = U - W M0^T.
-// Three launches: gdn_prep_kernel computes, for every (v-head, chunk) at
+// Two launches: gdn_prep_kernel computes, for every (v-head, chunk) at
 // once, W, Q~ = diag(gamma) Q, K~ = diag(e) K, P, U and gamma_last;
-// gdn_chain_kernel walks the chunks in order, state only (Delta = U - W M^T,
-// M <- gamma_last M + Delta^T K~), recording each chunk's starting state and
-// Delta; gdn_out_kernel then forms O = Q~ Mc^T + P Delta for every chunk at
-// once.  Only the chain is sequential, and it carries 256 of the 448 MFMAs
-// per chunk and slice that a single walking kernel did.  The prep's Gram
-// products are fp32 MFMA (v_mfma_f32_16x16x4_f32); the chain's and the
-// output's are split bf16 (mfma_x3 below; -W rounded to bf16); every
-// accumulation, stored value and the state are fp32.
+// gdn_chain_kernel walks the chunks in order (Delta = U - W M^T, the output
+// O = Q~ M^T + P Delta, M <- gamma_last M + Delta^T K~).  The prep's Gram
+// products are fp32 MFMA (v_mfma_f32_16x16x4_f32); the chain's are split
+// bf16 (mfma_x3 below; -W rounded to bf16); every accumulation, stored
+// value and the state are fp32.
 constexpr int kC = 64;  // tokens per chunk of the chunked form
 
 __device__ inline f32x4 mfma_f32(float a, float b, const f32x4& c)
@@ -263,27 +260,22 @@ struct ChunkWs {
     //   Wb  [kC * D / 2]  -W rounded to bf16 in the chain kernel's register
     //                 order: the 16 bytes (w * D/32 + s) * 64 + l hold
     //                 -W[16w + l%16][(l/16) D/4 + 8s .. +7]
-    //   Q   [kC][D]   Q~ rows (tokens)
+    //   Qb  [kC * D]  Q~ as bf16 hi / lo in the chain kernel's register order:
+    //                 the 16 bytes ((w * D/32 + s) * 2 + hl) * 64 + l hold part
+    //                 hl of Q~[16w + l%16][(l/16) D/4 + 8s .. +7]
     //   Kb  [kC * D]  K~ likewise: the 16 bytes ((b * 2 + s) * 2 + hl) * 64 + l
     //                 hold part hl of K~[16 (l/16) + 8s .. +7][16b + l%16]
-    //   P   [kC][kC], U^T [D][kC] (the chain kernel overwrites the 4 KB of
-    //                 rows 16jt .. 16jt+15 with Delta^T's as bf16 hi / lo in the
-    //                 output kernel's register order: the 16 bytes
-    //                 ((jt * 2 + s) * 2 + hl) * 64 + l hold part hl of
-    //                 Delta^T[16jt + l%16][16 (l/16) + 8s .. +7]),
-    //   gamma_last (+3 pad), Mc [D*D] (the state at the chunk's start as bf16
-    //                 hi / lo in the output kernel's register order: the 16
-    //                 bytes ((jt * D/32 + s) * 2 + hl) * 64 + l hold part hl of
-    //                 M[16jt + l%16][(l/16) D/4 + 8s .. +7])
-    static constexpr size_t floats =
-        (size_t)kC * D / 2 + (size_t)2 * kC * D + (size_t)kC * kC + (size_t)kC * D + 4 + (size_t)D * D;
+    //   Pb  [kC * kC] P likewise: the 16 bytes ((w * 2 + s) * 2 + hl) * 64 + l
+    //                 hold part hl of P[16w + l%16][16 (l/16) + 8s .. +7]
+    //   U^T [D][kC], gamma_last (+3 floats of padding, where chain lanes
+    //                 with no output to write store theirs)
+    static constexpr size_t floats = (size_t)kC * D / 2 + (size_t)2 * kC * D + (size_t)kC * kC + (size_t)kC * D + 4;
     float* Wb;
     float* Q;
     float* Kb;
     float* P;
     float* U;
     float* gl;
-    float* Mc;
     __device__ ChunkWs(float* ws, uint32_t h, uint32_t c, uint32_t n_chunks)
     {
         Wb = ws + ((size_t)h * n_chunks + c) * floats;
@@ -292,7 +284,6 @@ struct ChunkWs {
         P = Kb + kC * D;
         U = P + kC * kC;
         gl = U + kC * D;
-        Mc = gl + 4;
     }
 };
 
@@ -302,15 +293,16 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
     constexpr int KP = D + 4;  // LDS row stride of the q / k rows (16-byte rows, staggered banks)
     constexpr int AP = kC + 4;
     constexpr int KQ = D / 4;  // contraction indices per lane group in the Gram MFMAs
-    // A shares its LDS with the q rows: once Q~ is written out and each wave
-    // holds its Gram rows of Q in registers, Qn is dead.  84 -> 68 KiB, two
-    // workgroups per CU.
-    static_assert(kC * AP <= kC * KP, "A must fit in the q rows");
+    // A and P share their LDS with the q rows: once Q~ is written out and
+    // each wave holds its Gram rows of Q in registers, Qn is dead.  84 -> 68
+    // KiB at D = 128, two workgroups per CU.
+    constexpr int QAN = kC * KP > kC * AP + kC * kC ? kC * KP : kC * AP + kC * kC;
     __shared__ float Kn[kC][KP];
-    __shared__ float QA[kC * KP];
+    __shared__ float QA[QAN];
     __shared__ float sg[kC], sb[kC], sgam[kC], see[kC];
     float(*Qn)[KP] = reinterpret_cast<float(*)[KP]>(QA);
     float(*Am)[AP] = reinterpret_cast<float(*)[AP]>(QA);
+    float(*Pm)[kC] = reinterpret_cast<float(*)[kC]>(QA + kC * AP);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -381,12 +373,24 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
     }
     __syncthreads();
 
-    // Q~ = diag(gamma) Q (token rows), and K~ = diag(e) K as bf16 hi / lo in
-    // the chain kernel's register order (ChunkWs)
-    for (int e = tid; e < kC * D / 4; e += 256) {
-        const int t = e / (D / 4), i = (e % (D / 4)) * 4;
-        const f32x4 q = *reinterpret_cast<const f32x4*>(&Qn[t][i]);
-        *reinterpret_cast<f32x4*>(w.Q + (size_t)t * D + i) = q * sgam[t];
+    // Q~ = diag(gamma) Q and K~ = diag(e) K as bf16 hi / lo in the chain
+    // kernel's register order (ChunkWs)
+    for (int e = tid; e < 4 * (D / 32) * 64; e += 256) {
+        const int l = e % 64, ws_ = e / 64, sk = ws_ % (D / 32), wt = ws_ / (D / 32);
+        const int t = 16 * wt + (l & 15), i = (l >> 4) * (D / 4) + 8 * sk;
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(&Qn[t][i]);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(&Qn[t][i + 4]);
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {  // rounded products (not contracted into the split)
+            x[u] = __fmul_rn(x0[u], sgam[t]);
+            x[u + 4] = __fmul_rn(x1[u], sgam[t]);
+        }
+        bf16x8 hi, lo;
+        split_bf16(x, hi, lo);
+        bf16x8* dst = reinterpret_cast<bf16x8*>(w.Q) + (size_t)ws_ * 128 + l;
+        dst[0] = hi;
+        dst[64] = lo;
     }
     for (int e = tid; e < (D / 16) * 2 * 64; e += 256) {
         const int l = e % 64, bs = e / 64, sk = bs % 2, b = bs / 2;
@@ -446,14 +450,14 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
                     const int t = 16 * tb + 4 * g + i;
                     const float dec = s <= t ? expf(sg[t] - sg[s]) : 0.0f;
                     Am[t][s] = s < t ? sb[t] * dec * gkk[j][i] : 0.0f;
-                    w.P[t * kC + s] = dec * gqk[j][i];
+                    Pm[t][s] = dec * gqk[j][i];
                 }
             }
         }
         // P above the diagonal blocks: row block `wave`, column blocks wave+1 ..
         for (int cb = wave + 1; cb < kC / 16; ++cb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) w.P[(16 * wave + 4 * g + i) * kC + 16 * cb + r] = 0.0f;
+            for (int i = 0; i < 4; ++i) Pm[16 * wave + 4 * g + i][16 * cb + r] = 0.0f;
     }
     __syncthreads();
 
@@ -480,6 +484,26 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
 #pragma unroll
                 for (int k = 0; k < m; ++k) acc = fmaf(-Am[16 * bi + m][16 * bi + k], tc[k], acc);
                 tc[m] = acc;
+            }
+        } else {
+            // meanwhile the other three waves write P as bf16 hi / lo in the
+            // chain kernel's register order (ChunkWs)
+            for (int e = tid - 64; e < 4 * 2 * 64; e += 192) {
+                const int l = e % 64, ws_ = e / 64, sk = ws_ % 2, wt = ws_ / 2;
+                const int t = 16 * wt + (l & 15), s = 16 * (l >> 4) + 8 * sk;
+                const f32x4 x0 = *reinterpret_cast<const f32x4*>(&Pm[t][s]);
+                const f32x4 x1 = *reinterpret_cast<const f32x4*>(&Pm[t][s + 4]);
+                float x[8];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    x[u] = x0[u];
+                    x[u + 4] = x1[u];
+                }
+                bf16x8 hi, lo;
+                split_bf16(x, hi, lo);
+                bf16x8* dst = reinterpret_cast<bf16x8*>(w.P) + (size_t)ws_ * 128 + l;
+                dst[0] = hi;
+                dst[64] = lo;
             }
         }
         __syncthreads();
@@ -572,17 +596,16 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
     }
 }
 
-// The recurrence across chunks, state only: per chunk, Delta = U - W M^T
-// and M <- gamma_last M + Delta^T K~ (the output is formed afterwards, all
-// chunks at once, by gdn_out_kernel).  A workgroup of four waves owns J = 16
-// state rows (d_v indices j0..j0+15) of one head and walks the chunks in
-// order; it records each chunk's starting state (Mc) and Delta^T (in place
-// of U^T) for the output pass, both as the bf16 hi / lo operands its waves
-// read from LDS anyway, 16 bytes per lane in the output kernel's register
-// order (stored as fp32 rows, four bytes per lane and row, the records cost
-// ~24 of the chain's ~80 us at 4096 tokens x 16 heads).  The records are
-// stored non-temporally: through the L2 they evicted the operand lines the
-// head's slices share (chain 70 -> 63 us, output pass 30 -> 33 us).
+// The recurrence across chunks with each chunk's output: per chunk,
+// Delta = U - W M^T, O = (Q~ M^T + P Delta) / sqrt(d) and then
+// M <- gamma_last M + Delta^T K~.  A workgroup of four waves owns J = 16
+// state rows (d_v indices j0..j0+15) of one head, walks the chunks in order
+// and writes the output columns j0..j0+15.  Both output products reuse
+// operands the recurrence already holds: Q~ M^T has phase A's state
+// operands (B) and P Delta has phase B's Delta^T operands; only Q~ and P
+// rows are extra loads.  (A separate output pass over all chunks needed the
+// chunk's starting state and Delta recorded in the workspace: 96 KB written
+// and read again per chunk and head, and a third launch.)
 //
 // Every operand element of a chunk is read by exactly one wave, so each wave
 // loads its own straight into registers, two chunks ahead (three register
@@ -592,50 +615,74 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_kernel(GdnArgs a)
 // w D/64 .. (kept in its registers in fp32) from Delta^T in LDS (A) and K~
 // (B).  Only the state slice and the Delta tile pass through LDS, as bf16
 // hi / lo pairs; two barriers per chunk.  The products are split-bf16
-// (mfma_x3: three bf16 MFMAs per product, fp32 accumulation; the state and
-// Delta themselves stay fp32), except that -W enters rounded to bf16 (W M^T
-// as W.Mhi + W.Mlo): an error in W M^T only perturbs the prediction the
-// delta rule subtracts, which the following tokens correct, so its rounding
-// shows in the outputs at ~1e-5 relative (K~ feeds the state directly and
-// keeps both parts), and it halves the bytes of -W each chunk moves.
-// Per-chunk timestamps put the fp32-MFMA form of this kernel at ~1 us of
-// MFMA in a ~2 us chunk.  The prep kernel writes -W and K~ in the order the
+// (mfma_x3: three bf16 MFMAs per product, fp32 accumulation; the state,
+// Delta and the outputs themselves stay fp32), except that -W enters rounded
+// to bf16 (W M^T as W.Mhi + W.Mlo): an error in W M^T only perturbs the
+// prediction the delta rule subtracts, which the following tokens correct,
+// so its rounding shows in the outputs at ~1e-5 relative (K~ feeds the
+// state directly and keeps both parts), and it halves the bytes of -W each
+// chunk moves.  The prep kernel writes -W, K~, Q~ and P in the order the
 // lanes read them (ChunkWs).
-template <int D>
+//
+// An output tile (16 tokens x the 16 columns) is two halves summed in fp32:
+// half 0 is Q~ M^T over the first D/2 of d_k plus P Delta over the first
+// k-step of the chunk's tokens, half 1 the rest.  PARTS = 1: wave w forms
+// both halves of token tile w.  PARTS = 2 (two workgroups per slice, both
+// running the recurrence): part p writes token tiles 2p and 2p + 1, wave w
+// forms half w / 2 of tile 2p + w % 2, and the two halves meet in LDS.  The
+// chain is bound by the bytes each CU loads per chunk (the -W, K~ and U^T
+// operands 52 KB, the Q~ and P rows 48 KB); with two parts a CU loads 76 KB.
+// Both forms give the same bits.
+template <int D, int PARTS>
 __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 {
     constexpr int J = 16;          // state rows (d_v indices) per workgroup
     constexpr int NSA = D / 32;    // phase A k-steps (d_k, 8 per lane group each)
     constexpr int NBW = D / 64;    // phase B: 16-wide d_k blocks per wave
+    constexpr int NQ = NSA / PARTS, NP = 2 / PARTS;  // Q~ and P k-steps per wave
     static_assert(kC == 64 && D % 64 == 0, "four token tiles and four waves of d_k blocks");
+    static_assert(PARTS == 1 || PARTS == 2, "one or two workgroups per slice");
     constexpr int MP = D + 8, DP = kC + 8;  // bf16 row strides (16-byte rows, staggered banks)
     __shared__ __attribute__((aligned(16))) __bf16 Mh[J][MP], Mlo[J][MP];   // the state slice, rows j
     __shared__ __attribute__((aligned(16))) __bf16 Dh[J][DP], Dlo[J][DP];   // Delta^T of the chunk, rows j
+    __shared__ f32x4 Ox[PARTS == 2 ? 4 : 1][64];                            // output halves (PARTS = 2)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, g = lane >> 4;
-    // workgroup b = slice * n_v + h: consecutive workgroups go to different
-    // XCDs, so the slices of one head (b mod 8 fixed when n_v is a multiple
-    // of 8) share an L2 and read the head's chunk data once
-    const uint32_t h = blockIdx.x % a.n_v, jt = blockIdx.x / a.n_v, j0 = jt * J;
+    // workgroup b = (part * D/16 + slice) * n_v + h: consecutive workgroups
+    // go to different XCDs, so the slices of one head (b mod 8 fixed when n_v
+    // is a multiple of 8) share an L2 and read the head's chunk data once
+    const uint32_t h = blockIdx.x % a.n_v, sl = blockIdx.x / a.n_v, jt = sl % (D / 16), j0 = jt * J;
+    const int part = (int)(sl / (D / 16));
+    const int ot = PARTS == 1 ? wave : 2 * part + (wave & 1);  // the wave's output token tile
+    const int oh = PARTS == 1 ? 0 : wave >> 1;                 // and half (PARTS = 2)
     const float* S = a.S + ((size_t)h * D + j0) * D;
     float* So = a.S_out + ((size_t)h * D + j0) * D;
     const uint32_t nlast = a.n_chunks - 1;
+    const float scale = 1.0f / sqrtf((float)D);
 
     // one chunk's register operands of this wave
     struct Ops {
         bf16x8 w[NSA];        // -W[16 wave + r][g D/4 + 8s .. +7] (bf16)
         f32x4 u;              // U^T[j0 + r][16 wave + 4g .. +3]
+        bf16x8 q[NQ][2];      // Q~[16 ot + r][g D/4 + 8s .. +7] of its k-steps, hi and lo
         bf16x8 k[NBW][2][2];  // K~[16g + 8s .. +7][16 (NBW wave + bb) + r], hi and lo
+        bf16x8 p[NP][2];      // P[16 ot + r][16g + 8s .. +7] of its k-steps, hi and lo
         float gl;
     };
-    // the loads of one register set in two halves (-W and U; K~ and gamma_last)
+    // the loads of one register set in two halves (-W, U and Q~; K~, P and
+    // gamma_last)
     auto load_a = [&](Ops& o, uint32_t c) {
         ChunkWs<D> w(a.ws, h, c, a.n_chunks);
         const bf16x8* wb = reinterpret_cast<const bf16x8*>(w.Wb);
 #pragma unroll
         for (int sk = 0; sk < NSA; ++sk) o.w[sk] = wb[(size_t)(wave * NSA + sk) * 64 + lane];
         o.u = *reinterpret_cast<const f32x4*>(w.U + (size_t)(j0 + r) * kC + 16 * wave + 4 * g);
+        const bf16x8* qb = reinterpret_cast<const bf16x8*>(w.Q);
+#pragma unroll
+        for (int i = 0; i < NQ; ++i)
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl) o.q[i][hl] = qb[((size_t)(ot * NSA + oh * NQ + i) * 2 + hl) * 64 + lane];
     };
     auto load_b = [&](Ops& o, uint32_t c) {
         ChunkWs<D> w(a.ws, h, c, a.n_chunks);
@@ -647,6 +694,11 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
 #pragma unroll
                 for (int hl = 0; hl < 2; ++hl)
                     o.k[bb][sk][hl] = kb[((size_t)((NBW * wave + bb) * 2 + sk) * 2 + hl) * 64 + lane];
+        const bf16x8* pb = reinterpret_cast<const bf16x8*>(w.P);
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl) o.p[i][hl] = pb[((size_t)(ot * 2 + oh * NP + i) * 2 + hl) * 64 + lane];
         o.gl = w.gl[0];
     };
     auto load = [&](Ops& o, uint32_t c) {
@@ -666,6 +718,23 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
                 Mlo[4 * g + e][i] = (__bf16)(mt[bb][e] - (float)hi);
             }
     };
+    // output rows 16 ot + 4g + i of chunk c, column j0 + r, for i in [i0, i0
+    // + n); with PARTS = 2 the half of a previous chunk in LDS is added first
+    // (its partner wave stored it before the last barrier).  Lanes with
+    // nothing to write (chunk c < 0, or a token past the last) store to the
+    // chunk's padding word, so every chunk runs the same memory instructions.
+    auto put_out = [&](int64_t c, f32x4 o) {
+        if (PARTS == 2) o = o + Ox[(wave & 1) * 2 + (oh ^ 1)][lane];
+        const uint32_t cc = c < 0 ? 0u : (uint32_t)c;
+        float* pad = ChunkWs<D>(a.ws, h, cc, a.n_chunks).gl + 1;
+#pragma unroll
+        for (int i = 0; i < 4 / PARTS; ++i) {
+            const int ii = PARTS == 1 ? i : 2 * oh + i;
+            const uint32_t t = cc * kC + 16 * ot + 4 * g + ii;
+            float* dst = c >= 0 && t < a.T ? a.out + (size_t)t * a.out_stride + (size_t)h * D + j0 + r : pad;
+            *dst = o[ii] * scale;
+        }
+    };
 #pragma unroll
     for (int bb = 0; bb < NBW; ++bb)
 #pragma unroll
@@ -675,14 +744,16 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
     load(oa, 0);
     load(ob, min(1u, nlast));
     __syncthreads();
+    f32x4 oprev = f32x4{0.f, 0.f, 0.f, 0.f};  // PARTS = 2: this wave's half of the previous chunk
 
     // One chunk with operand set o; the loads of the set for chunk cf go out
-    // in between the MFMAs (the -W half in phase A, the K~ half in phase B):
-    // a wave that issued its 17 loads in one burst waited for the CU's
-    // memory pipeline instead of issuing MFMAs.
+    // in between the MFMAs (the -W / Q~ half in phase A, the K~ / P half in
+    // phase B): a wave that issued its loads in one burst waited for the
+    // CU's memory pipeline instead of issuing MFMAs.
     auto chunk = [&](uint32_t c, const Ops& o, Ops& of, uint32_t cf) {
-        ChunkWs<D> w(a.ws, h, c, a.n_chunks);
-        // phase A: Delta rows 16 wave + 4g + e, column j0 + r = U - W M^T
+        // phase A: Delta rows 16 wave + 4g + e, column j0 + r = U - W M^T;
+        // then the Q~ M^T part of the output halves
+        f32x4 o0 = f32x4{0.f, 0.f, 0.f, 0.f}, o1 = o0;
         {
             f32x4 acc = o.u;
             bf16x8 bh[NSA], bl[NSA];
@@ -691,6 +762,7 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
                 bh[sk] = *reinterpret_cast<const bf16x8*>(&Mh[r][g * (D / 4) + 8 * sk]);
                 bl[sk] = *reinterpret_cast<const bf16x8*>(&Mlo[r][g * (D / 4) + 8 * sk]);
             }
+            if (PARTS == 2) put_out((int64_t)c - 1, oprev);
             load_a(of, cf);
 #pragma unroll
             for (int sk = 0; sk < NSA; ++sk) {
@@ -702,20 +774,6 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
             }
-            // the chunk's starting state for the output kernel: the split
-            // operands every wave read above, NSA / 2 of the 2 NSA (k-step,
-            // part) pieces per wave, picked by selects, stored after the
-            // MFMAs that read them (stored before them, the wave waited for
-            // every operand read before its first MFMA)
-#pragma unroll
-            for (int q = 0; q < NSA / 2; ++q) {
-                const int idx = wave * (NSA / 2) + q;
-                bf16x8 v = bh[0];
-#pragma unroll
-                for (int cc = 1; cc < 2 * NSA; ++cc)
-                    if (cc == idx) v = (cc & 1) ? bl[cc >> 1] : bh[cc >> 1];
-                __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(w.Mc) + (size_t)(jt * NSA * 2 + idx) * 64 + lane);
-            }
             typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
             bf16x4 dh, dl;
 #pragma unroll
@@ -725,9 +783,22 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
             }
             *reinterpret_cast<bf16x4*>(&Dh[r][16 * wave + 4 * g]) = dh;
             *reinterpret_cast<bf16x4*>(&Dlo[r][16 * wave + 4 * g]) = dl;
+            if (PARTS == 1) {
+#pragma unroll
+                for (int i = 0; i < NSA / 2; ++i) o0 = mfma_x3(o.q[i][0], o.q[i][1], bh[i], bl[i], o0);
+#pragma unroll
+                for (int i = NSA / 2; i < NSA; ++i) o1 = mfma_x3(o.q[i][0], o.q[i][1], bh[i], bl[i], o1);
+            } else if (oh == 0) {  // uniform over the wave; the B operands are k-steps oh NQ ..
+#pragma unroll
+                for (int i = 0; i < NQ; ++i) o0 = mfma_x3(o.q[i][0], o.q[i][1], bh[i], bl[i], o0);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NQ; ++i) o0 = mfma_x3(o.q[i][0], o.q[i][1], bh[NQ + i], bl[NQ + i], o0);
+            }
         }
         lds_barrier();
-        // phase B: M <- gamma_last M + Delta^T K~ on this wave's d_k blocks
+        // phase B: M <- gamma_last M + Delta^T K~ on this wave's d_k blocks;
+        // then the P Delta part of the output halves
         bf16x8 ah[2], al[2];
 #pragma unroll
         for (int sk = 0; sk < 2; ++sk) {
@@ -747,17 +818,19 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
         }
-        // Delta^T for the output kernel (in place of this slice's U^T rows):
-        // the split operands every wave read above, (k-step, part) piece
-        // `wave` by wave `wave`
-        {
-            bf16x8 v = ah[0];
-#pragma unroll
-            for (int cc = 1; cc < 4; ++cc)
-                if (cc == wave) v = (cc & 1) ? al[cc >> 1] : ah[cc >> 1];
-            __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(w.U) + (size_t)(jt * 4 + wave) * 64 + lane);
-        }
         put_state();
+        if (PARTS == 1) {
+            o0 = mfma_x3(o.p[0][0], o.p[0][1], ah[0], al[0], o0);
+            o1 = mfma_x3(o.p[1][0], o.p[1][1], ah[1], al[1], o1);
+            put_out(c, o0 + o1);
+        } else {
+            if (oh == 0)
+                o0 = mfma_x3(o.p[0][0], o.p[0][1], ah[0], al[0], o0);
+            else
+                o0 = mfma_x3(o.p[0][0], o.p[0][1], ah[1], al[1], o0);
+            Ox[(wave & 1) * 2 + oh][lane] = o0;  // the partner adds it after the barrier
+            oprev = o0;
+        }
         lds_barrier();
     };
     // chunk c's operands are in a register set loaded two chunks before.
@@ -776,102 +849,13 @@ __global__ __launch_bounds__(256, 1) void gdn_chain_kernel(GdnArgs a)
         chunk(c, oa, oc, min(c + 2, nlast));
         if (c + 1 <= nlast) chunk(c + 1, ob, oa, min(c + 3, nlast));
     }
+    if (PARTS == 2) put_out(nlast, oprev);
 
+    if (part == 0) {
 #pragma unroll
-    for (int bb = 0; bb < NBW; ++bb)
+        for (int bb = 0; bb < NBW; ++bb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) So[(size_t)(4 * g + e) * D + 16 * (NBW * wave + bb) + r] = mt[bb][e];
-}
-
-// The chunk outputs, all chunks at once: O = (Q~ Mc^T + P Delta) / sqrt(d)
-// for one (chunk, v head) per workgroup.  Q~ and P are staged in LDS as bf16
-// hi / lo pairs (each element split once, read by every wave); wave w owns
-// output columns (d_v) 16*(w % NJT).. and token row blocks of its share,
-// with its Mc rows and Delta^T rows as register operands (16-byte loads of
-// the chain kernel's split records).  Split-bf16 products (mfma_x3) with
-// fp32 accumulation, as the chain kernel.
-template <int D>
-__global__ __launch_bounds__(512, 2) void gdn_out_kernel(GdnArgs a)
-{
-    constexpr int KQ = D / 4;      // d_k indices per lane group
-    constexpr int NSQ = KQ / 8;    // k-steps of 8 per lane group over d_k
-    constexpr int NJT = D / 16;    // 16-column output tiles
-    constexpr int WPT = 8 / NJT;   // waves per column tile (1 at D = 128, 2 at 64)
-    constexpr int RBW = 4 / WPT;   // 16-token row blocks per wave
-    constexpr int QP = D + 8, PP = kC + 8;  // bf16 row strides
-    __shared__ __attribute__((aligned(16))) __bf16 Qh[kC][QP], Qlo[kC][QP];
-    __shared__ __attribute__((aligned(16))) __bf16 Ph[kC][PP], Plo[kC][PP];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const uint32_t c = blockIdx.x, h = blockIdx.y;
-    const uint32_t t0 = c * kC;
-    const int nt = (int)min((uint32_t)kC, a.T - t0);
-    const int jt = wave % NJT, rb0 = (wave / NJT) * RBW;
-    ChunkWs<D> w(a.ws, h, c, a.n_chunks);
-
-    // register operands, written split by the chain kernel: B of Q~ Mc^T
-    // (Mc rows 16 jt + r, d_k g KQ + 8s .. +7) and of P Delta (Delta^T rows
-    // 16 jt + r, tokens 16g + 8s .. +7); issued first
-    bf16x8 mh[NSQ], ml[NSQ], dh[2], dl[2];
-    {
-        const bf16x8* mc = reinterpret_cast<const bf16x8*>(w.Mc) + (size_t)(jt * NSQ * 2) * 64 + lane;
-#pragma unroll
-        for (int sk = 0; sk < NSQ; ++sk) {
-            mh[sk] = mc[(2 * sk) * 64];
-            ml[sk] = mc[(2 * sk + 1) * 64];
-        }
-        const bf16x8* dt = reinterpret_cast<const bf16x8*>(w.U) + (size_t)(jt * 4) * 64 + lane;
-#pragma unroll
-        for (int sk = 0; sk < 2; ++sk) {
-            dh[sk] = dt[(2 * sk) * 64];
-            dl[sk] = dt[(2 * sk + 1) * 64];
-        }
-    }
-    // Q~ and P into LDS, split
-    for (int e = tid; e < kC * D / 8; e += 512) {
-        const int t = e / (D / 8), i = (e % (D / 8)) * 8;
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(w.Q + (size_t)t * D + i);
-        const f32x4 x1 = *reinterpret_cast<const f32x4*>(w.Q + (size_t)t * D + i + 4);
-        float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        bf16x8 hi, lo;
-        split_bf16(x, hi, lo);
-        *reinterpret_cast<bf16x8*>(&Qh[t][i]) = hi;
-        *reinterpret_cast<bf16x8*>(&Qlo[t][i]) = lo;
-    }
-    for (int e = tid; e < kC * kC / 8; e += 512) {
-        const int t = e / (kC / 8), i = (e % (kC / 8)) * 8;
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(w.P + (size_t)t * kC + i);
-        const f32x4 x1 = *reinterpret_cast<const f32x4*>(w.P + (size_t)t * kC + i + 4);
-        float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        bf16x8 hi, lo;
-        split_bf16(x, hi, lo);
-        *reinterpret_cast<bf16x8*>(&Ph[t][i]) = hi;
-        *reinterpret_cast<bf16x8*>(&Plo[t][i]) = lo;
-    }
-    __syncthreads();
-
-    const float scale = 1.0f / sqrtf((float)D);
-#pragma unroll
-    for (int rr = 0; rr < RBW; ++rr) {
-        const int rb = rb0 + rr, tr = 16 * rb + r;
-        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        // Q~ Mc^T: contraction over d_k, lane group g its KQ indices
-#pragma unroll
-        for (int sk = 0; sk < NSQ; ++sk)
-            acc = mfma_x3(*reinterpret_cast<const bf16x8*>(&Qh[tr][g * KQ + 8 * sk]),
-                          *reinterpret_cast<const bf16x8*>(&Qlo[tr][g * KQ + 8 * sk]), mh[sk], ml[sk], acc);
-        // P Delta: contraction over the chunk's tokens, lane group g tokens 16g..16g+15
-#pragma unroll
-        for (int sk = 0; sk < 2; ++sk)
-            acc = mfma_x3(*reinterpret_cast<const bf16x8*>(&Ph[tr][16 * g + 8 * sk]),
-                          *reinterpret_cast<const bf16x8*>(&Plo[tr][16 * g + 8 * sk]), dh[sk], dl[sk], acc);
-        const f32x4 o = acc * scale;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = 16 * rb + 4 * g + i;
-            if (t < nt) a.out[(size_t)(t0 + t) * a.out_stride + (size_t)h * D + 16 * jt + r] = o[i];
-        }
+            for (int e = 0; e < 4; ++e) So[(size_t)(4 * g + e) * D + 16 * (NBW * wave + bb) + r] = mt[bb][e];
     }
 }
 
@@ -966,8 +950,14 @@ hipError_t launch_gdn_d(const GdnArgs& a, hipStream_t st)
         hipLaunchKernelGGL(gdn_step_kernel<D>, dim3(a.n_v * (D / 16)), dim3(256), 0, st, a);
     } else if (a.ws) {
         hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(a.n_chunks, a.n_v), dim3(256), 0, st, a);
-        hipLaunchKernelGGL(gdn_chain_kernel<D>, dim3(a.n_v * (D / 16)), dim3(256), 0, st, a);
-        hipLaunchKernelGGL(gdn_out_kernel<D>, dim3(a.n_chunks, a.n_v), dim3(512), 0, st, a);
+        // two workgroups per state slice when they fit the GPU and the state
+        // goes out of place (in place, one part's final state could reach S
+        // before the other part has read it)
+        const uint32_t slices = a.n_v * (D / 16);
+        if (a.S_out != a.S && 2 * slices <= (uint32_t)n_cus())
+            hipLaunchKernelGGL((gdn_chain_kernel<D, 2>), dim3(2 * slices), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((gdn_chain_kernel<D, 1>), dim3(slices), dim3(256), 0, st, a);
     } else {
         hipLaunchKernelGGL(gdn_kernel<D>, dim3(a.n_v * (D / kCols)), dim3(256), 0, st, a);
     }

@@ -201,6 +201,8 @@ struct GdnArgs {
     uint32_t n_chunks;
 };
 hipError_t launch_gdn(const GdnArgs& a, hipStream_t st);
+// compute units of the current device (queried once; 256 if the query fails)
+int n_cus();
 // bytes of the chunked form's workspace, and its chunk length in tokens
 size_t gdn_chunk_workspace(uint32_t T, uint32_t n_v, uint32_t D);
 uint32_t gdn_chunk_tokens();
