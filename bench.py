@@ -68,7 +68,9 @@ MFMA_F32_PEAK = 157.3e12  # FLOP/s, dense fp32 MFMA
 METRIC = "attn decode GB/s (% HBM peak); prefill attn TFLOP/s (% MFMA peak)"
 SEED = 0x5EED0000
 ROTATE_BYTES = 300 << 20  # rotating input sets exceed the 256 MB MALL (Infinity Cache)
-GDN_CHUNKED_KERNELS = "gdn_prep_kernel<%d> + gdn_chain_kernel<%d> + gdn_out_kernel<%d>"
+# the chain runs two workgroups per 16 state rows when they fit the GPU's 256
+# CUs (its state goes out of place)
+GDN_CHUNKED_KERNELS = "gdn_prep_kernel<%d> + gdn_chain_kernel<%d, %d>"
 EAGER = False  # --eager: launch each step from the host (for counter collection)
 CHUNKED_GDN = True  # --gdn-tokenwise: time the token-by-token GDN kernel instead
 
@@ -437,7 +439,7 @@ def run_gdn(T: int, n_h: int, d: int, steps: int, warmup: int, cpu: bool):
                                f"{n_sets} rotating input sets (> 256 MB MALL)",
                    "tokens": T, "heads": n_h, "head_dim": d},
         "roofline": {"bound": "mfma" if t_mfma >= t_hbm else "hbm",
-                     "kernel": (GDN_CHUNKED_KERNELS % (d, d, d) if CHUNKED_GDN else
+                     "kernel": (GDN_CHUNKED_KERNELS % (d, d, 2 if 2 * n_h * d // 16 <= 256 else 1) if CHUNKED_GDN else
                                 "gdn_kernel<%d>" % d) + " (+ gdn_gates_kernel)",
                      **({"achieved": flops / kern_s / 1e12, "peak": MFMA_F32_PEAK / 1e12, "unit": "TFLOP/s"}
                         if t_mfma >= t_hbm else
