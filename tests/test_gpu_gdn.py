@@ -95,6 +95,33 @@ def test_gdn_chunk_matches_oracle(cuda, oracle, T, n_k, n_v, d, chunked):
     assert e_o <= TOL and e_s <= TOL and rows <= 3 * TOL
 
 
+@pytest.mark.parametrize("T,n_k,n_v,d", [(65, 2, 4, 64), (197, 4, 8, 128), (300, 16, 16, 128), (200, 32, 32, 128)],
+                         ids=["d64-2chunks", "d128-4chunks-ragged", "16heads", "32heads-one-part"])
+def test_gdn_chunk_out_of_place_matches_oracle(cuda, oracle, T, n_k, n_v, d):
+    """The chunked form with the state out of place: two workgroups per 16
+    state rows whenever they fit the GPU (32 heads of 128 do not: one per
+    slice), each writing half of every chunk's token tiles.  Against the
+    oracle, and bit for bit the in-place result."""
+    from yllm_amd.gdn import gdn_chunk
+
+    q, k, v, alpha, beta_raw, S0 = inputs(900 + T, T, n_k, n_v, d, s0_scale=0.02)
+    beta, gate = oracle_gates(oracle, alpha, beta_raw, np.zeros(n_v, np.float32), -np.ones(n_v, np.float32))
+    S_want, o_want, _, _ = oracle.gdn_sequence(S0.ravel(), q, k, v, gate, beta, T, n_k, d, n_v, d, EPS)
+    S_in, S_ip, qd, kd, vd, gd, bd = to_dev(cuda, S0, S0, q, k, v, gate, beta)
+    S_op = torch.full_like(S_in, float("nan"))
+    out_op = gdn_chunk(S_in, qd, kd, vd, gd, bd, n_k, EPS, S_out=S_op)
+    out_ip = gdn_chunk(S_ip, qd, kd, vd, gd, bd, n_k, EPS)
+    torch.cuda.synchronize()
+    out = out_op.cpu().numpy()
+    e_o, e_s = rel_l2(out, o_want), rel_l2(S_op.cpu().numpy().ravel(), S_want)
+    rows = max(rel_l2(out[t], o_want[t]) for t in range(T))
+    print(f"gdn chunk out of place T={T} {n_k}/{n_v} d={d}: out {e_o:.3e} (worst row {rows:.3e}) state {e_s:.3e}")
+    assert e_o <= TOL and e_s <= TOL and rows <= 3 * TOL
+    assert torch.equal(out_op.view(torch.int32), out_ip.view(torch.int32))
+    assert torch.equal(S_op.view(torch.int32), S_ip.view(torch.int32))
+    assert np.array_equal(S_in.cpu().numpy().view(np.uint32), S0.view(np.uint32))
+
+
 @pytest.mark.parametrize("chunked", [False, True], ids=["tokenwise", "chunked"])
 def test_gdn_chunk_interleaved_layout_and_prenormalised(cuda, oracle, chunked):
     """q, k, v as slices of one [T, conv_channels] row (the engine's qkv
