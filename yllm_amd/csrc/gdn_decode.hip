@@ -242,7 +242,7 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     static_assert(D % NP == 0, "whole columns per part");
     static_assert(TPC == 8 || TPC == 16, "a state column's threads sum in one row");
     __shared__ float qs[D], ks[D], vs[D];
-    __shared__ float l2p[2 * D / 64];  // per wave: sum of squares of its q or k channels
+    __shared__ float l2p[3 * (2 * D / 64)];  // per q/k wave: its q.q, k.k and q.k
     __shared__ float ssq[NT / 64];
     __shared__ float s_gate[2];  // beta, g of the head
     constexpr int GW = 3 * D / 64;  // the first wave without a conv channel computes the gates
@@ -270,12 +270,14 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
 #pragma unroll
         for (int e = 0; e < 4; ++e) s[i + e] = x[e];
     }
-    // this thread's conv channel: q (tid < D), k (< 2D) of head kh, v (< 3D) of head h
-    const bool has_ch = tid < 3 * D;
+    // this thread's conv channel: q_i (tid = 2i < 2D) and k_i (tid = 2i + 1)
+    // of head kh side by side, so one lane pair holds both for the q.k sum;
+    // v (2D <= tid < 3D) of head h
+    const bool has_ch = tid < 3 * D, qk_ch = tid < 2 * D, is_k = qk_ch && (tid & 1);
+    const uint32_t ci = (uint32_t)tid >> 1;
     const uint32_t ch = !has_ch ? 0u
-                        : tid < D ? kh * D + tid
-                        : tid < 2 * D ? key_dim + kh * D + (tid - D)
-                                      : 2 * key_dim + h * D + (tid - 2 * D);
+                        : qk_ch ? (is_k ? key_dim : 0u) + kh * D + ci
+                                : 2 * key_dim + h * D + (tid - 2 * D);
     // KWM taps are loaded by every thread from valid addresses (taps past
     // kwidth repeat the last weight and the current row, and are not used): a
     // load under a condition, into a register that starts at zero, made the
@@ -300,17 +302,23 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
 #pragma unroll
         for (int r = 0; r < KWM; ++r)
             if ((uint32_t)r < kw) acc = acc + X[r] * w[r];
-        y = acc / (1.0f + expf(-acc));
-        if (tid < D) qs[tid] = y;
-        else if (tid < 2 * D) ks[tid - D] = y;
-        else vs[tid - 2 * D] = y;
+        y = acc * __builtin_amdgcn_rcpf(1.0f + expf(-acc));
+        if (!qk_ch) vs[tid - 2 * D] = y;
+        else if (is_k) ks[ci] = y;
+        else qs[ci] = y;
     }
     // the norm weight and z's silu, while their loads have just landed: used
     // only at the end, their waits there also waited for the state stores
-    // (in-order memory counter), and the output store's latency added to theirs
-    float wv = a.norm_w_f16 ? (float)__builtin_bit_cast(_Float16, w_lo)
-                            : __builtin_bit_cast(float, (uint32_t)w_lo | (uint32_t)w_hi << 16);
-    float zs = zv / (1.0f + expf(-zv));
+    // (in-order memory counter), and the output store's latency added to
+    // theirs.  Only the lanes that write y form them (no memory instruction
+    // inside, so waves without such a lane skip it).
+    const bool writes_y = part == 0 && own_col;
+    float wv = 0.0f, zs = 0.0f;
+    if (writes_y) {
+        wv = a.norm_w_f16 ? (float)__builtin_bit_cast(_Float16, w_lo)
+                          : __builtin_bit_cast(float, (uint32_t)w_lo | (uint32_t)w_hi << 16);
+        zs = zv * __builtin_amdgcn_rcpf(1.0f + expf(-zv));
+    }
     asm volatile("" : "+v"(wv), "+v"(zs));
     // the gates once per workgroup, by a wave that has no conv channel (every
     // wave computing them cost ~0.3 us of VALU issue per SIMD)
@@ -322,19 +330,31 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
             s_gate[1] = g_;
         }
     }
-    // l2 norms: the q channels are waves 0 .. D/64-1, the k channels the next
-    // D/64 waves; each wave sums its squares, one barrier publishes them
-    // (the reference sums in order; this is a tree, equal to rounding)
-    const float y2 = sum64(tid < 2 * D ? y * y : 0.0f);
-    if (lane == 0 && wave < 2 * D / 64) l2p[wave] = y2;
-    lds_barrier();
-    float qq = 0.0f, kk = 0.0f;
-#pragma unroll
-    for (int w2 = 0; w2 < D / 64; ++w2) {
-        qq += l2p[w2];
-        kk += l2p[D / 64 + w2];
+    // l2 norms and q.k: the q/k channels are waves 0 .. 2D/64-1; each wave
+    // sums its q.q, k.k and q.k (q_i k_i from the lane pair), one barrier
+    // publishes them (the reference sums in order; this is a tree, equal to
+    // rounding)
+    if (__builtin_amdgcn_readfirstlane(wave) < 2 * D / 64) {  // the q/k waves only (uniform)
+        const float yo = dpp_mov<0xb1>(y);  // the lane pair's other channel
+        const float sqq = sum64(is_k ? 0.0f : y * y), skk = sum64(is_k ? y * y : 0.0f);
+        const float sqk = sum64(is_k ? 0.0f : y * yo);
+        if (lane == 0) {
+            l2p[3 * wave] = sqq;
+            l2p[3 * wave + 1] = skk;
+            l2p[3 * wave + 2] = sqk;
+        }
     }
-    const float rq = 1.0f / fmaxf(sqrtf(qq), a.l2_eps), rk = 1.0f / fmaxf(sqrtf(kk), a.l2_eps);
+    lds_barrier();
+    float qq = 0.0f, kk = 0.0f, pkq = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < 2 * D / 64; ++w2) {
+        qq += l2p[3 * w2];
+        kk += l2p[3 * w2 + 1];
+        pkq += l2p[3 * w2 + 2];
+    }
+    // 1 / max(sqrt(x), eps) as min(rsq(x), 1 / eps) (x = 0 gives 1 / eps)
+    const float rq = fminf(__builtin_amdgcn_rsqf(qq), 1.0f / a.l2_eps);
+    const float rk = fminf(__builtin_amdgcn_rsqf(kk), 1.0f / a.l2_eps);
 
     const float bt = s_gate[0], g = s_gate[1];
 
@@ -352,16 +372,14 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     // per state element.  Every part forms it for every column (the norm
     // needs all D outputs; in place as out of place, so both give the same
     // bits), and only its own columns the exact way.
-    float pa = 0.0f, pb = 0.0f, pkq = 0.0f;
+    float pa = 0.0f, pb = 0.0f;
 #pragma unroll
     for (int i = 0; i < SL; ++i) {
         pa = fmaf(s[i], qr[i], pa);
         pb = fmaf(s[i], kr[i], pb);
-        pkq = fmaf(kr[i], qr[i], pkq);
     }
     pa = sum_tpc(pa);
     pb = sum_tpc(pb);
-    pkq = sum_tpc(pkq);
     const float dn = (vs[j] - g * rk * pb) * bt;
     const float on = (g * rq * pa + dn * (rk * rq * pkq)) * (1.0f / sqrtf((float)D));
 
@@ -402,11 +420,13 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     const float sq = sum64(part == 0 ? on * on : 0.0f);
     if (lane == 0) ssq[wave] = sq;
     lds_barrier();
-    float ss = 0.0f;
+    if (writes_y) {
+        float ss = 0.0f;
 #pragma unroll
-    for (int wv2 = 0; wv2 < NT / 64; ++wv2) ss += ssq[wv2];
-    const float inv = 1.0f / sqrtf(ss / (float)D + a.norm_eps);
-    if (part == 0 && own_col) a.y[(size_t)h * D + j] = o * wv * inv * zs;
+        for (int wv2 = 0; wv2 < NT / 64; ++wv2) ss += ssq[wv2];
+        const float inv = __builtin_amdgcn_rsqf(ss / (float)D + a.norm_eps);
+        a.y[(size_t)h * D + j] = o * wv * inv * zs;
+    }
     // the delay line last (nothing here reads it; stored earlier, a wait for a
     // load issued before it waited for the store too): head kh's q/k channels
     // by part 0 of v head kh (n_v >= n_k), v channels by the part of their
