@@ -100,18 +100,27 @@ __global__ __launch_bounds__(256) void kv_block_kernel(uint16_t* __restrict__ kc
             }
         }
     };
+    // both rows' loads go out before any wait: from clamped, always-valid
+    // rows (a load under the bounds test waited for the first row's round
+    // trip before the second row's was issued); the stores keep the test
+    u16x8 kb[2], vb[2];
 #pragma unroll
     for (uint32_t it = 0; it < 2; ++it) {
         const uint32_t g = threadIdx.x + 256u * it;  // row g / 8, dimensions 8 (g % 8) ..
         const uint32_t r = g >> 3, c = (g & 7u) * 8u;
+        const uint32_t pos = min(max(p0 + r, pos_start), pos_start + B - 1u);
+        const size_t off = (size_t)(pos - pos_start) * kv_dim + j0 + c;
+        load8(k, off, kb[it]);
+        load8(v, off, vb[it]);
+    }
+#pragma unroll
+    for (uint32_t it = 0; it < 2; ++it) {
+        const uint32_t g = threadIdx.x + 256u * it;
+        const uint32_t r = g >> 3, c = (g & 7u) * 8u;
         const uint32_t pos = p0 + r;
         if (pos < pos_start || pos >= pos_start + B) continue;
-        const size_t off = (size_t)(pos - pos_start) * kv_dim + j0 + c;
-        u16x8 kb, vb;
-        load8(k, off, kb);
-        load8(v, off, vb);
-        *reinterpret_cast<u16x8*>(kc + k_index(h, pos, d0 + c, D, kv_stride)) = kb;
-        *reinterpret_cast<u16x8*>(&tv[r][c]) = vb;
+        *reinterpret_cast<u16x8*>(kc + k_index(h, pos, d0 + c, D, kv_stride)) = kb[it];
+        *reinterpret_cast<u16x8*>(&tv[r][c]) = vb[it];
     }
     __syncthreads();
 #pragma unroll
