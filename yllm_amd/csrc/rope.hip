@@ -85,7 +85,7 @@ __device__ void v_tile_block(const RopeArgs& a, uint32_t vb)
     const uint32_t tx = threadIdx.x & 63u, ty = threadIdx.x >> 6;
     for (uint32_t r = ty; r < 64u; r += 4u) {
         const uint32_t b = b0 + r, j = j0 + tx;
-        if (b < a.B && j < kv_dim) tile[r][tx] = f32_to_f16_ref(a.v[(size_t)b * a.v_stride + j]);
+        if (b < a.B && j < kv_dim) tile[r][tx] = f32_to_f16_ref(__builtin_nontemporal_load(a.v + (size_t)b * a.v_stride + j));
     }
     __syncthreads();
     for (uint32_t r = ty; r < 64u; r += 4u) {
@@ -175,12 +175,13 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a)
 #pragma unroll
             for (uint32_t r = 0; r < PPL; ++r) {
                 if (e1[r] == e0[r] + 1) {
-                    const float2 v = *reinterpret_cast<const float2*>(src + e0[r]);
-                    x0[u][r] = v.x;
-                    x1[u][r] = v.y;
+                    typedef float f32x2_ __attribute__((ext_vector_type(2)));
+                    const f32x2_ v = __builtin_nontemporal_load(reinterpret_cast<const f32x2_*>(src + e0[r]));
+                    x0[u][r] = v[0];
+                    x1[u][r] = v[1];
                 } else {
-                    x0[u][r] = src[e0[r]];
-                    x1[u][r] = src[e1[r]];
+                    x0[u][r] = __builtin_nontemporal_load(src + e0[r]);
+                    x1[u][r] = __builtin_nontemporal_load(src + e1[r]);
                 }
             }
         }
