@@ -48,11 +48,15 @@
 namespace yhip {
 namespace {
 
-// Cache policy of the K/V block loads (the buffer load's aux operand): 2,
-// non-temporal.  Every K/V byte of a decode step is read once; streamed
+// Cache policies of the K/V block loads (the buffer load's aux operand):
+// 0, the default, or 2, non-temporal.  Every K/V byte of a decode step is
+// read once; when a launch reads more than the caches keep from one step to
+// the next (8 rotating layer caches of 32k keys, 134 MB each), streamed
 // non-temporally the split kernel runs 9-14 % faster (32k keys 28.9 -> 26.4
-// us, 128k 94.0 -> 81.3, 64 ragged sequences 792 -> 738).
-constexpr int kKvPolicy = 2;
+// us, 128k 94.0 -> 81.3, 64 ragged sequences 792 -> 738); a small cache the
+// next token reads again (one layer of 8.9 MB in the hybrid group) is faster
+// kept (8.12 against 8.23 ms per group step).  decode_policy() picks.
+constexpr int kKvDefault = 0, kKvStream = 2;
 
 constexpr int kKeysPerBlock = 32;
 
@@ -98,7 +102,7 @@ struct Frag {
 // holds the token rotates the token's key, stores key and value into the
 // cache and substitutes them for the cache rows it loaded.  The cosines and
 // sines come from the host's cosf / sinf, as the reference computes them.
-template <int D, bool ROPE>
+template <int D, bool ROPE, int POL>
 __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_split_kernel(DecodeArgs a,
                                                                                             DecodeRopeArg<ROPE> rp)
 {
@@ -175,11 +179,11 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
 #pragma unroll
             for (int c = 0; c < NC; ++c)
                 f.k[t][c] = __builtin_bit_cast(
-                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rK, kb + (4 * t * D + c * 32) * 2, 0, kKvPolicy));
+                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rK, kb + (4 * t * D + c * 32) * 2, 0, POL));
 #pragma unroll
         for (int b = 0; b < NB; ++b)
             f.v[b] = __builtin_bit_cast(f16x8,
-                                        __builtin_amdgcn_raw_buffer_load_b128(rV, vb + b * 16 * kVTile * 2, 0, kKvPolicy));
+                                        __builtin_amdgcn_raw_buffer_load_b128(rV, vb + b * 16 * kVTile * 2, 0, POL));
     };
 
     // q is read once per workgroup: each thread loads float4s of the G heads'
@@ -678,13 +682,31 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
     }
 }
 
+// Non-temporal K/V loads when the launch reads at least 32 MiB of K and V
+// (an upper bound for a batch with device-side lengths); YHIP_DECODE_NT=0 or
+// 1 forces the choice.
+bool decode_streams(const DecodeArgs& a)
+{
+    static const int env = [] {
+        const char* e = getenv("YHIP_DECODE_NT");
+        return e ? atoi(e) : -1;
+    }();
+    if (env == 0 || env == 1) return env == 1;
+    const uint64_t keys = a.lens ? (uint64_t)a.split_keys * a.n_splits : a.len0;
+    const uint64_t bytes = (uint64_t)a.n_seq * a.n_kv * keys * a.D * 4u;
+    return bytes >= (32ull << 20);
+}
+
 template <int D, bool ROPE>
 hipError_t launch_decode_d(const DecodeArgs& a, const DecodeRope& r, hipStream_t st)
 {
     dim3 grid(a.n_splits, a.n_kv, a.n_seq);
     DecodeRopeArg<ROPE> rr{};
     if constexpr (ROPE) rr = r;
-    hipLaunchKernelGGL((decode_split_kernel<D, ROPE>), grid, dim3(64 * waves_of<D>()), 0, st, a, rr);
+    if (decode_streams(a))
+        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvStream>), grid, dim3(64 * waves_of<D>()), 0, st, a, rr);
+    else
+        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvDefault>), grid, dim3(64 * waves_of<D>()), 0, st, a, rr);
     constexpr uint32_t slices = D < kMergeSlice ? 1 : D / kMergeSlice;
     if (a.n_splits > 1)
         hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.n_heads * slices, a.n_seq), dim3(256), 0, st, a);

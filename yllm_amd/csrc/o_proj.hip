@@ -42,19 +42,21 @@ __global__ __launch_bounds__(256) void oproj_gemv_kernel(OProjArgs a)
 
 #pragma unroll 8
     for (uint32_t i0 = lane * 8u; i0 < a.qdim; i0 += 512u) {
+        // the weights are read once per call: non-temporal loads (one token,
+        // 4096 x 4096 f16: 9.3 -> 8.8 us)
         float w[kRows][8];
 #pragma unroll
         for (uint32_t r = 0; r < kRows; ++r) {
             const uint32_t o = min(o0 + r, a.hidden - 1);  // a missing last row repeats a real one, unused
             if (W_F16) {
-                const f16x8 v = *reinterpret_cast<const f16x8*>(reinterpret_cast<const _Float16*>(a.w) +
-                                                                (size_t)o * a.qdim + i0);
+                const f16x8 v = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(reinterpret_cast<const _Float16*>(a.w) +
+                                                                (size_t)o * a.qdim + i0));
 #pragma unroll
                 for (int e = 0; e < 8; ++e) w[r][e] = (float)v[e];
             } else {
                 const float* p = reinterpret_cast<const float*>(a.w) + (size_t)o * a.qdim + i0;
-                const f32x4 v0 = *reinterpret_cast<const f32x4*>(p);
-                const f32x4 v1 = *reinterpret_cast<const f32x4*>(p + 4);
+                const f32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+                const f32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     w[r][e] = v0[e];
