@@ -573,16 +573,17 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
 // them against its own running max, and the 16 subsets are then combined in
 // LDS with one more rescale.  The gate is loaded first, beside the partials.
 constexpr uint32_t kMergeSlice = 64;
+constexpr uint32_t kMergeRound = 8;  // partial loads per thread and round of the merge
 
-template <int D>
+template <int D, uint32_t NG>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
 {
     constexpr uint32_t SL = D < kMergeSlice ? D : kMergeSlice;  // dimensions per workgroup
     constexpr uint32_t E4 = SL / 4;     // float4 columns of the slice
-    constexpr uint32_t NG = 256 / E4;   // split subsets combined in parallel
     constexpr uint32_t NS = D / SL;     // slices per head
-    __shared__ f32x4 s_o[256];
-    __shared__ float s_m[256], s_l[256];
+    static_assert(E4 * NG <= 256, "at most 256 threads");
+    __shared__ f32x4 s_o[E4 * NG];      // NG split subsets, combined at the end
+    __shared__ float s_m[E4 * NG], s_l[E4 * NG];
     const uint32_t h = blockIdx.x / NS, d0 = (blockIdx.x % NS) * SL, seq = blockIdx.y, t = threadIdx.x;
     const uint32_t kvh = h * a.n_kv / a.n_heads;
     const uint32_t hn = h - (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
@@ -600,7 +601,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
     // trip per round of splits, 3.4 us per merge at 34 splits), and a loop
     // around the first round waited for the gate first.  Gate rows need not be
     // 16-byte aligned.
-    constexpr uint32_t kRound = 8;
+    constexpr uint32_t kRound = kMergeRound;
     typedef float f32x2 __attribute__((ext_vector_type(2)));
     f32x2 ml[kRound];
     f32x4 ov[kRound];
@@ -708,8 +709,25 @@ hipError_t launch_decode_d(const DecodeArgs& a, const DecodeRope& r, hipStream_t
     else
         hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvDefault>), grid, dim3(64 * waves_of<D>()), 0, st, a, rr);
     constexpr uint32_t slices = D < kMergeSlice ? 1 : D / kMergeSlice;
-    if (a.n_splits > 1)
-        hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.n_heads * slices, a.n_seq), dim3(256), 0, st, a);
+    constexpr uint32_t e4 = (D < kMergeSlice ? D : kMergeSlice) / 4;
+    if (a.n_splits > 1) {
+        // the fewest split subsets whose one round of loads (kMergeRound per
+        // thread) covers every split: one memory round trip and the smallest
+        // LDS combine (32 splits: 4 subsets, 25.2 us at 32k keys against 26.4
+        // with 16; 34 splits: 8, the d 256 token 11.25 against 12.0 us)
+        const dim3 grid(a.n_heads * slices, a.n_seq);
+        const uint32_t rounds = (a.n_splits + kMergeRound - 1) / kMergeRound;
+        if (rounds <= 1)
+            hipLaunchKernelGGL((decode_merge_kernel<D, 1>), grid, dim3(e4 * 1), 0, st, a);
+        else if (rounds <= 2)
+            hipLaunchKernelGGL((decode_merge_kernel<D, 2>), grid, dim3(e4 * 2), 0, st, a);
+        else if (rounds <= 4)
+            hipLaunchKernelGGL((decode_merge_kernel<D, 4>), grid, dim3(e4 * 4), 0, st, a);
+        else if (rounds <= 8)
+            hipLaunchKernelGGL((decode_merge_kernel<D, 8>), grid, dim3(e4 * 8), 0, st, a);
+        else
+            hipLaunchKernelGGL((decode_merge_kernel<D, 16>), grid, dim3(e4 * 16), 0, st, a);
+    }
     return hipGetLastError();
 }
 
