@@ -263,13 +263,6 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     const float beta_raw = a.beta_raw[h], alpha = a.alpha[h], dt_bias = a.dt_bias[h], ssm_a = a.ssm_a[h];
     const float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
     float* So = a.S_out + ((size_t)h * D + j) * D + part * SL;
-    float s[SL];
-#pragma unroll
-    for (int i = 0; i < SL; i += 4) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(Sp + i);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s[i + e] = x[e];
-    }
     // this thread's conv channel: q_i (tid = 2i < 2D) and k_i (tid = 2i + 1)
     // of head kh side by side, so one lane pair holds both for the q.k sum;
     // v (2D <= tid < 3D) of head h
@@ -296,6 +289,26 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     const float zv = a.z[(size_t)h * D + j];
     const uint16_t* nw16 = reinterpret_cast<const uint16_t*>(a.norm_w);
     const uint16_t w_lo = nw16[a.norm_w_f16 ? j : 2 * j], w_hi = nw16[a.norm_w_f16 ? j : 2 * j + 1];
+    // the state slice last: the conv channels, z and the weight are used first,
+    // and with in-order completion a wait for them does not wait for the state
+    float s[SL];
+#pragma unroll
+    for (int i = 0; i < SL; i += 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(Sp + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[i + e] = x[e];
+    }
+    // the gates once per workgroup, by a wave that has no conv channel (every
+    // wave computing them cost ~0.3 us of VALU issue per SIMD), from scalar
+    // loads, while the vector loads are in flight
+    if (wave == GW) {
+        const float bt_ = 1.0f / (1.0f + expf(-beta_raw));
+        const float g_ = expf(log1pf(expf(alpha + dt_bias)) * ssm_a);
+        if (lane == 0) {
+            s_gate[0] = bt_;
+            s_gate[1] = g_;
+        }
+    }
     float y = 0.0f;
     if (has_ch) {
         float acc = 0.0f;
@@ -320,16 +333,6 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
         zs = zv * __builtin_amdgcn_rcpf(1.0f + expf(-zv));
     }
     asm volatile("" : "+v"(wv), "+v"(zs));
-    // the gates once per workgroup, by a wave that has no conv channel (every
-    // wave computing them cost ~0.3 us of VALU issue per SIMD)
-    if (wave == GW) {
-        const float bt_ = 1.0f / (1.0f + expf(-beta_raw));
-        const float g_ = expf(log1pf(expf(alpha + dt_bias)) * ssm_a);
-        if (lane == 0) {
-            s_gate[0] = bt_;
-            s_gate[1] = g_;
-        }
-    }
     // l2 norms and q.k: the q/k channels are waves 0 .. 2D/64-1; each wave
     // sums its q.q, k.k and q.k (q_i k_i from the lane pair), one barrier
     // publishes them (the reference sums in order; this is a tree, equal to
@@ -353,8 +356,8 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
         pkq += l2p[3 * w2 + 2];
     }
     // 1 / max(sqrt(x), eps) as min(rsq(x), 1 / eps) (x = 0 gives 1 / eps)
-    const float rq = fminf(__builtin_amdgcn_rsqf(qq), 1.0f / a.l2_eps);
-    const float rk = fminf(__builtin_amdgcn_rsqf(kk), 1.0f / a.l2_eps);
+    const float rq = fminf(__builtin_amdgcn_rsqf(qq), a.l2_inv_eps);
+    const float rk = fminf(__builtin_amdgcn_rsqf(kk), a.l2_inv_eps);
 
     const float bt = s_gate[0], g = s_gate[1];
 
@@ -365,13 +368,12 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
         kr[i] = ks[part * SL + i];
         qr[i] = qs[part * SL + i];
     }
-    // Column j's output for the norm's sum of squares only, from the state
-    // before the token: o_j = (g rq (S_j . q) + d_j rk rq (k . q)) / sqrt(D)
-    // with d_j = (v_j - g rk (S_j . k)) beta -- the update's algebra in
-    // another order, equal to the exact o_j within rounding, at three FMAs
-    // per state element.  Every part forms it for every column (the norm
-    // needs all D outputs; in place as out of place, so both give the same
-    // bits), and only its own columns the exact way.
+    // Column j's output from the state before the token:
+    // o_j = (g rq (S_j . q) + d_j rk rq (k . q)) / sqrt(D) with
+    // d_j = (v_j - g rk (S_j . k)) beta -- the update's algebra in another
+    // order, equal to q . S_j' / sqrt(D) within rounding, at two FMAs per
+    // state element.  Every part forms it for every column (the norm needs
+    // all D outputs; in place as out of place, so both give the same bits).
     float pa = 0.0f, pb = 0.0f;
 #pragma unroll
     for (int i = 0; i < SL; ++i) {
@@ -383,30 +385,16 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     const float dn = (vs[j] - g * rk * pb) * bt;
     const float on = (g * rq * pa + dn * (rk * rq * pkq)) * (1.0f / sqrtf((float)D));
 
-    // the exact update and output of the part's own columns (CPP * TPC
-    // consecutive threads: whole waves), in the reference's order
-    float o = 0.0f;
+    // the new state of the part's own columns (CPP * TPC consecutive threads:
+    // whole waves): the decay and delta rule of gdn_state_update
+    // (matvec.c:975-1004) with the normalisations factored out of the sums --
+    // k . (g S_j) = g rk (kr . S_j) is the pb above, so the rule's delta is
+    // dn, and S_j' = g S_j + kr (rk dn).  The output q . S_j' / sqrt(D) is then
+    // on by the same algebra, so y takes on for every column.
     if (own_col) {
-        float k[SL], q[SL];
+        const float kd = rk * dn;
 #pragma unroll
-        for (int i = 0; i < SL; ++i) {
-            k[i] = kr[i] * rk;
-            q[i] = qr[i] * rq;
-        }
-        float p = 0.0f;
-#pragma unroll
-        for (int i = 0; i < SL; ++i) {
-            s[i] *= g;
-            p = fmaf(s[i], k[i], p);
-        }
-        const float delta = (vs[j] - sum_tpc(p)) * bt;
-        float p2 = 0.0f;
-#pragma unroll
-        for (int i = 0; i < SL; ++i) {
-            s[i] = fmaf(k[i], delta, s[i]);
-            p2 = fmaf(s[i], q[i], p2);
-        }
-        o = sum_tpc(p2) * (1.0f / sqrtf((float)D));
+        for (int i = 0; i < SL; ++i) s[i] = fmaf(kr[i], kd, s[i] * g);
 #pragma unroll
         for (int i = 0; i < SL; i += 4) {
             f32x4 x;
@@ -425,7 +413,7 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
 #pragma unroll
         for (int wv2 = 0; wv2 < NT / 64; ++wv2) ss += ssq[wv2];
         const float inv = __builtin_amdgcn_rsqf(ss / (float)D + a.norm_eps);
-        a.y[(size_t)h * D + j] = o * wv * inv * zs;
+        a.y[(size_t)h * D + j] = on * wv * inv * zs;
     }
     // the delay line last (nothing here reads it; stored earlier, a wait for a
     // load issued before it waited for the store too): head kh's q/k channels
@@ -465,18 +453,21 @@ hipError_t launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t st)
         return e ? atoi(e) : 8;
     }();
     if (!two) {
+        // the l2norm's 1 / eps once here, not by a division in every wave
+        GdnDecodeArgs b = a;
+        b.l2_inv_eps = 1.0f / a.l2_eps;
         const int np = a.S_out == a.S ? 1 : np_env;
         switch (a.D * 100 + np) {
-        case 6401: launch_head<64, 1>(a, st); break;
-        case 6402: launch_head<64, 2>(a, st); break;
-        case 6404: launch_head<64, 4>(a, st); break;
-        case 6408: launch_head<64, 8>(a, st); break;
-        case 6416: launch_head<64, 16>(a, st); break;
-        case 12801: launch_head<128, 1>(a, st); break;
-        case 12802: launch_head<128, 2>(a, st); break;
-        case 12804: launch_head<128, 4>(a, st); break;
-        case 12808: launch_head<128, 8>(a, st); break;
-        case 12816: launch_head<128, 16>(a, st); break;
+        case 6401: launch_head<64, 1>(b, st); break;
+        case 6402: launch_head<64, 2>(b, st); break;
+        case 6404: launch_head<64, 4>(b, st); break;
+        case 6408: launch_head<64, 8>(b, st); break;
+        case 6416: launch_head<64, 16>(b, st); break;
+        case 12801: launch_head<128, 1>(b, st); break;
+        case 12802: launch_head<128, 2>(b, st); break;
+        case 12804: launch_head<128, 4>(b, st); break;
+        case 12808: launch_head<128, 8>(b, st); break;
+        case 12816: launch_head<128, 16>(b, st); break;
         default: return hipErrorInvalidValue;
         }
         return hipGetLastError();

@@ -181,6 +181,7 @@ struct GdnDecodeArgs {
     float* y;               // [n_v * D]
     uint32_t n_k, n_v, D, kwidth, conv_dim, norm_w_f16;
     float l2_eps, norm_eps;
+    float l2_inv_eps;  // 1 / l2_eps, set by launch_gdn_decode
 };
 hipError_t launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t st);
 
