@@ -271,13 +271,15 @@ def test_decode_workspace_for_max_len_serves_every_position(cuda, oracle):
             assert err <= TOL, f"{n} keys: rel_l2 {err:.3e}"
 
 
+@pytest.mark.parametrize("nh,nkv", [(8, 2), (32, 8)])
 @pytest.mark.parametrize("max_len", [100, 5000])
-def test_decode_batch_empty_sequence_gives_zeros(cuda, oracle, max_len):
+def test_decode_batch_empty_sequence_gives_zeros(cuda, oracle, max_len, nh, nkv):
     """A sequence with no keys gets a zero output row, with one split
-    (max_len 100) as with several (5000), gated or not."""
+    (max_len 100) as with several (5000), gated or not; 8 kv heads take the
+    kv-head-first grids (a kv head's splits and merges on one XCD)."""
     from yllm_amd.attention import DecodeBatch, LayerKV, attn_decode_batch, kv_store
 
-    nh, nkv, hd = 8, 2, 128
+    hd = 128
     kvd = nkv * hd
     lens = [max_len, 0, 37]
     caches, wants, qs = [], [], []

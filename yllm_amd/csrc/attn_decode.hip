@@ -102,7 +102,7 @@ struct Frag {
 // holds the token rotates the token's key, stores key and value into the
 // cache and substitutes them for the cache rows it loaded.  The cosines and
 // sines come from the host's cosf / sinf, as the reference computes them.
-template <int D, bool ROPE, int POL>
+template <int D, bool ROPE, int POL, bool KVM>
 __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_split_kernel(DecodeArgs a,
                                                                                             DecodeRopeArg<ROPE> rp)
 {
@@ -119,7 +119,8 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     __shared__ __attribute__((aligned(16))) uint16_t s_knew[ROPE ? D : 8];
     __shared__ __attribute__((aligned(16))) uint16_t s_vt[ROPE ? 16 : 1][ROPE ? D / 16 : 8];
 
-    const uint32_t seq = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
+    // grid (n_splits, n_kv, n_seq), or (n_kv, n_splits, n_seq) with KVM
+    const uint32_t kvh = KVM ? blockIdx.x : blockIdx.y, split = KVM ? blockIdx.y : blockIdx.x, seq = blockIdx.z;
     // a length beyond the planned maximum is clamped, never read past
     const uint32_t len = min(min(a.lens ? a.lens[seq] : a.len0, a.kv_stride), a.split_keys * a.n_splits);
     const uint32_t kbeg = split * a.split_keys;
@@ -575,7 +576,7 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
 constexpr uint32_t kMergeSlice = 64;
 constexpr uint32_t kMergeRound = 8;  // partial loads per thread and round of the merge
 
-template <int D, uint32_t NG>
+template <int D, uint32_t NG, bool KVM>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
 {
     constexpr uint32_t SL = D < kMergeSlice ? D : kMergeSlice;  // dimensions per workgroup
@@ -584,7 +585,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
     static_assert(E4 * NG <= 256, "at most 256 threads");
     __shared__ f32x4 s_o[E4 * NG];      // NG split subsets, combined at the end
     __shared__ float s_m[E4 * NG], s_l[E4 * NG];
-    const uint32_t h = blockIdx.x / NS, d0 = (blockIdx.x % NS) * SL, seq = blockIdx.y, t = threadIdx.x;
+    // grid (n_heads * NS, n_seq), or (n_kv, G * NS, n_seq) with KVM (G query
+    // heads per kv head)
+    const uint32_t t = threadIdx.x;
+    const uint32_t h = KVM ? blockIdx.x * (gridDim.y / NS) + blockIdx.y / NS : blockIdx.x / NS;
+    const uint32_t d0 = ((KVM ? blockIdx.y : blockIdx.x) % NS) * SL;
+    const uint32_t seq = KVM ? blockIdx.z : blockIdx.y;
     const uint32_t kvh = h * a.n_kv / a.n_heads;
     const uint32_t hn = h - (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
     const uint32_t len = min(min(a.lens ? a.lens[seq] : a.len0, a.kv_stride), a.split_keys * a.n_splits);
@@ -698,37 +704,55 @@ bool decode_streams(const DecodeArgs& a)
     return bytes >= (32ull << 20);
 }
 
-template <int D, bool ROPE>
-hipError_t launch_decode_d(const DecodeArgs& a, const DecodeRope& r, hipStream_t st)
+template <int D, uint32_t NG, bool KVM>
+void launch_merge(const DecodeArgs& a, hipStream_t st)
 {
-    dim3 grid(a.n_splits, a.n_kv, a.n_seq);
+    constexpr uint32_t slices = D < kMergeSlice ? 1 : D / kMergeSlice;
+    constexpr uint32_t e4 = (D < kMergeSlice ? D : kMergeSlice) / 4;
+    const dim3 grid = KVM ? dim3(a.n_kv, a.n_heads / a.n_kv * slices, a.n_seq) : dim3(a.n_heads * slices, a.n_seq);
+    hipLaunchKernelGGL((decode_merge_kernel<D, NG, KVM>), grid, dim3(e4 * NG), 0, st, a);
+}
+
+template <int D, bool ROPE, bool KVM>
+hipError_t launch_decode_o(const DecodeArgs& a, const DecodeRope& r, hipStream_t st)
+{
+    const dim3 grid = KVM ? dim3(a.n_kv, a.n_splits, a.n_seq) : dim3(a.n_splits, a.n_kv, a.n_seq);
     DecodeRopeArg<ROPE> rr{};
     if constexpr (ROPE) rr = r;
     if (decode_streams(a))
-        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvStream>), grid, dim3(64 * waves_of<D>()), 0, st, a, rr);
+        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvStream, KVM>), grid, dim3(64 * waves_of<D>()), 0, st, a,
+                           rr);
     else
-        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvDefault>), grid, dim3(64 * waves_of<D>()), 0, st, a, rr);
-    constexpr uint32_t slices = D < kMergeSlice ? 1 : D / kMergeSlice;
-    constexpr uint32_t e4 = (D < kMergeSlice ? D : kMergeSlice) / 4;
+        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvDefault, KVM>), grid, dim3(64 * waves_of<D>()), 0, st, a,
+                           rr);
     if (a.n_splits > 1) {
         // the fewest split subsets whose one round of loads (kMergeRound per
         // thread) covers every split: one memory round trip and the smallest
         // LDS combine (32 splits: 4 subsets, 25.2 us at 32k keys against 26.4
         // with 16; 34 splits: 8, the d 256 token 11.25 against 12.0 us)
-        const dim3 grid(a.n_heads * slices, a.n_seq);
         const uint32_t rounds = (a.n_splits + kMergeRound - 1) / kMergeRound;
-        if (rounds <= 1)
-            hipLaunchKernelGGL((decode_merge_kernel<D, 1>), grid, dim3(e4 * 1), 0, st, a);
-        else if (rounds <= 2)
-            hipLaunchKernelGGL((decode_merge_kernel<D, 2>), grid, dim3(e4 * 2), 0, st, a);
-        else if (rounds <= 4)
-            hipLaunchKernelGGL((decode_merge_kernel<D, 4>), grid, dim3(e4 * 4), 0, st, a);
-        else if (rounds <= 8)
-            hipLaunchKernelGGL((decode_merge_kernel<D, 8>), grid, dim3(e4 * 8), 0, st, a);
-        else
-            hipLaunchKernelGGL((decode_merge_kernel<D, 16>), grid, dim3(e4 * 16), 0, st, a);
+        if (rounds <= 1) launch_merge<D, 1, KVM>(a, st);
+        else if (rounds <= 2) launch_merge<D, 2, KVM>(a, st);
+        else if (rounds <= 4) launch_merge<D, 4, KVM>(a, st);
+        else if (rounds <= 8) launch_merge<D, 8, KVM>(a, st);
+        else launch_merge<D, 16, KVM>(a, st);
     }
     return hipGetLastError();
+}
+
+// The hardware deals workgroups to the 8 XCDs in turn by their linear id.
+// With the kv head first in both grids (KVM, for kv head counts that are
+// multiples of 8 and whole query-head groups), a kv head's splits and the
+// merges of its query heads share XCDs (XCD kvh mod 8), so its q rows and
+// the partials the merges read stay in those XCDs' L2: 32k keys, 32 / 8 heads
+// 25.3 -> 24.6 us, 64 sequences 731 -> 706 us, 128k unchanged.  With 2 kv
+// heads the same order was slower (the hybrid group's d 256 token 11.2 ->
+// 11.6 us), so other shapes keep the split-major order.
+template <int D, bool ROPE>
+hipError_t launch_decode_d(const DecodeArgs& a, const DecodeRope& r, hipStream_t st)
+{
+    if (a.n_kv % 8u == 0 && a.n_heads % a.n_kv == 0) return launch_decode_o<D, ROPE, true>(a, r, st);
+    return launch_decode_o<D, ROPE, false>(a, r, st);
 }
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
