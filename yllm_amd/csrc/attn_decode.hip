@@ -125,8 +125,9 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     const uint32_t len = min(min(a.lens ? a.lens[seq] : a.len0, a.kv_stride), a.split_keys * a.n_splits);
     const uint32_t kbeg = split * a.split_keys;
     // query heads h with h*n_kv/n_heads == kvh form [h0, h1) (engine.c:1079)
-    const uint32_t h0 = (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
-    const uint32_t h1 = ((kvh + 1) * a.n_heads + a.n_kv - 1) / a.n_kv;
+    // (KVM launches have whole groups of gmax heads: no division)
+    const uint32_t h0 = KVM ? kvh * a.gmax : (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
+    const uint32_t h1 = KVM ? h0 + a.gmax : ((kvh + 1) * a.n_heads + a.n_kv - 1) / a.n_kv;
     const uint32_t G = h1 - h0;
     if (kbeg >= len) {  // uniform over the workgroup
         // a sequence without keys gets zeros (times the gate), as the merge
@@ -588,11 +589,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
     // grid (n_heads * NS, n_seq), or (n_kv, G * NS, n_seq) with KVM (G query
     // heads per kv head)
     const uint32_t t = threadIdx.x;
-    const uint32_t h = KVM ? blockIdx.x * (gridDim.y / NS) + blockIdx.y / NS : blockIdx.x / NS;
+    const uint32_t h = KVM ? blockIdx.x * a.gmax + blockIdx.y / NS : blockIdx.x / NS;
     const uint32_t d0 = ((KVM ? blockIdx.y : blockIdx.x) % NS) * SL;
     const uint32_t seq = KVM ? blockIdx.z : blockIdx.y;
-    const uint32_t kvh = h * a.n_kv / a.n_heads;
-    const uint32_t hn = h - (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
+    const uint32_t kvh = KVM ? blockIdx.x : h * a.n_kv / a.n_heads;
+    const uint32_t hn = KVM ? blockIdx.y / NS : h - (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
     const uint32_t len = min(min(a.lens ? a.lens[seq] : a.len0, a.kv_stride), a.split_keys * a.n_splits);
     const uint32_t ns = (len + a.split_keys - 1) / a.split_keys;
     const size_t sbase = ((size_t)seq * a.n_kv + kvh) * a.n_splits;
@@ -600,8 +601,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
     const uint32_t d = d0 + 4 * e4;
 
     // Every load below is issued unconditionally from a valid address (the
-    // output row stands in for a missing gate; splits past ns read slot 0 and
-    // are masked by selects), the first round's partials and the gate before
+    // output row stands in for a missing gate; slots past n_splits read slot 0,
+    // and every split past ns is masked by selects, so the addresses wait for
+    // no division), the first round's partials and the gate before
     // any wait: a load under a condition, into a register set beforehand, made
     // the compiler wait for it before issuing the next one (one memory round
     // trip per round of splits, 3.4 us per merge at 34 splits), and a loop
@@ -617,7 +619,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
 #pragma unroll
         for (uint32_t r = 0; r < kRound; ++r) {
             const uint32_t s = s0 + r * NG;
-            const size_t slot = (sbase + (s < ns ? s : 0u)) * a.gmax + hn;
+            const size_t slot = (sbase + (s < a.n_splits ? s : 0u)) * a.gmax + hn;
             ml[r] = *reinterpret_cast<const f32x2*>(a.part_ml + slot * 2);
             ov[r] = *reinterpret_cast<const f32x4*>(a.part_o + slot * D + d);
         }
