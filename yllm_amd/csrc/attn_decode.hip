@@ -113,7 +113,6 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     __shared__ __attribute__((aligned(16))) float s_o[kWaves][16][D + 4];
     __shared__ float s_m[kWaves][16];
     __shared__ float s_l[kWaves][16];
-    __shared__ float s_hm[16], s_hl[16];  // per head: max and sum over the waves
     // the token's K bits by dimension, and its V bits by lane: element
     // d = 16 b + n at [n][b], so lane n reads its NB values in one go
     __shared__ __attribute__((aligned(16))) uint16_t s_knew[ROPE ? D : 8];
@@ -506,51 +505,45 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     // per-lane partial sums -> per head (the four lane groups hold one head)
     l = sum_xor16(l);
     l = sum_xor32(l);
+    // Combine the four waves in one LDS round: each wave stages its own
+    // (m, l) and, for the group's G heads only (the padded slots' writes were
+    // most of the combine's LDS traffic at G <= 8), its unscaled
+    // accumulators; after one barrier the threads that form an output float4
+    // rescale the four waves' float4s to the head's maximum as they sum them.
+    // (Rescaling in the staging waves took a second barrier and LDS round.)
     if (g == 0) {
         s_m[wave][n] = m;
         s_l[wave][n] = l;
     }
-    // LDS-only barriers in the combine: a full barrier also waited for the
-    // owner's token stores (scattered 2-byte K/V writes issued before the
-    // loop), which made that workgroup the launch's straggler (+1.6 us)
-    lds_barrier();
-
-    // Combine the four waves: every lane rescales its own accumulators to the
-    // head's maximum over the waves before staging them, so the sum below is
-    // four float4 reads per output float4.
-    {
-        float M = -INFINITY;
+    if ((uint32_t)n < G) {
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][n]);
-        const float sc = m == -INFINITY ? 0.0f : fast_exp2(m - M);
-        // only the group's G heads are staged (the padded slots' LDS writes
-        // were most of the combine's LDS traffic at G <= 8)
-        if ((uint32_t)n < G) {
-#pragma unroll
-            for (int b = 0; b < NB; ++b)
-                *reinterpret_cast<f32x4*>(&s_o[wave][n][b * 16 + 4 * g]) = o[b] * sc;
-        }
-        if (wave == 0 && g == 0) {
-            float L = 0.0f;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w)
-                if (s_m[w][n] != -INFINITY) L += s_l[w][n] * fast_exp2(s_m[w][n] - M);
-            s_hm[n] = M;
-            s_hl[n] = L;
-        }
+        for (int b = 0; b < NB; ++b) *reinterpret_cast<f32x4*>(&s_o[wave][n][b * 16 + 4 * g]) = o[b];
     }
+    // an LDS-only barrier: a full barrier also waited for the owner's token
+    // stores (scattered 2-byte K/V writes issued before the loop), which made
+    // that workgroup the launch's straggler (+1.6 us)
     lds_barrier();
 
     // a single split writes the result directly, otherwise a partial
     const size_t grp = (size_t)seq * a.n_kv + kvh;  // (sequence, kv head) group
     for (uint32_t idx = threadIdx.x; idx < G * D4; idx += kThreads) {
         const uint32_t hn = idx / D4, d = (idx - hn * D4) * 4;
-        f32x4 O = *reinterpret_cast<const f32x4*>(&s_o[0][hn][d]);
+        float M = -INFINITY;
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) O += *reinterpret_cast<const f32x4*>(&s_o[w][hn][d]);
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hn]);
+        f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            // a wave without keys holds m = -inf, l = 0 and zero accumulators
+            const float mw = s_m[w][hn];
+            const float c = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
+            O += *reinterpret_cast<const f32x4*>(&s_o[w][hn][d]) * c;
+            L += s_l[w][hn] * c;
+        }
         if (a.n_splits == 1) {
             const uint32_t h = h0 + hn;
-            f32x4 r = O / s_hl[hn];
+            f32x4 r = O / L;
             if (a.gate) {
                 const float* gp = a.gate + (size_t)seq * a.gate_stride + (size_t)h * D + d;
 #pragma unroll
@@ -561,8 +554,8 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
             const size_t slot = (grp * a.n_splits + split) * a.gmax + hn;
             *reinterpret_cast<f32x4*>(a.part_o + slot * D + d) = O;
             if (d == 0) {
-                a.part_ml[slot * 2] = s_hm[hn];
-                a.part_ml[slot * 2 + 1] = s_hl[hn];
+                a.part_ml[slot * 2] = M;
+                a.part_ml[slot * 2 + 1] = L;
             }
         }
     }
