@@ -528,18 +528,26 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     const size_t grp = (size_t)seq * a.n_kv + kvh;  // (sequence, kv head) group
     for (uint32_t idx = threadIdx.x; idx < G * D4; idx += kThreads) {
         const uint32_t hn = idx / D4, d = (idx - hn * D4) * 4;
+        // every LDS read first (one round trip), then the arithmetic
+        float mw[kWaves], lw[kWaves];
+        f32x4 ow[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            mw[w] = s_m[w][hn];
+            lw[w] = s_l[w][hn];
+            ow[w] = *reinterpret_cast<const f32x4*>(&s_o[w][hn][d]);
+        }
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hn]);
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mw[w]);
         f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
         float L = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
             // a wave without keys holds m = -inf, l = 0 and zero accumulators
-            const float mw = s_m[w][hn];
-            const float c = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
-            O += *reinterpret_cast<const f32x4*>(&s_o[w][hn][d]) * c;
-            L += s_l[w][hn] * c;
+            const float c = mw[w] == -INFINITY ? 0.0f : fast_exp2(mw[w] - M);
+            O += ow[w] * c;
+            L += lw[w] * c;
         }
         if (a.n_splits == 1) {
             const uint32_t h = h0 + hn;
