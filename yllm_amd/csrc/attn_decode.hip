@@ -669,19 +669,26 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
     s_l[t] = L;
     lds_barrier();  // the gate's load may still be in flight
     if (t < E4) {
+        // every subset's (m, l, O) read first (one LDS round trip)
+        float mg[NG], lg[NG];
+        f32x4 og[NG];
+#pragma unroll
+        for (uint32_t g2 = 0; g2 < NG; ++g2) {
+            mg[g2] = s_m[g2 * E4 + t];
+            lg[g2] = s_l[g2 * E4 + t];
+            og[g2] = s_o[g2 * E4 + t];
+        }
         float Mt = -INFINITY;
 #pragma unroll
-        for (uint32_t g2 = 0; g2 < NG; ++g2) Mt = fmaxf(Mt, s_m[g2 * E4 + t]);
+        for (uint32_t g2 = 0; g2 < NG; ++g2) Mt = fmaxf(Mt, mg[g2]);
         float Lt = 0.0f;
         f32x4 Ot = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (uint32_t g2 = 0; g2 < NG; ++g2) {
-            const float mg = s_m[g2 * E4 + t];
-            if (mg != -INFINITY) {
-                const float c = fast_exp2(mg - Mt);
-                Lt += s_l[g2 * E4 + t] * c;
-                Ot += s_o[g2 * E4 + t] * c;
-            }
+            // a subset without splits holds m = -inf, l = 0 and O = 0
+            const float c = mg[g2] == -INFINITY ? 0.0f : fast_exp2(mg[g2] - Mt);
+            Lt += lg[g2] * c;
+            Ot += og[g2] * c;
         }
         f32x4 r = ns ? Ot / Lt : f32x4{0.f, 0.f, 0.f, 0.f};
         if (a.gate) {
