@@ -551,7 +551,7 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         }
         if (a.n_splits == 1) {
             const uint32_t h = h0 + hn;
-            f32x4 r = O / L;
+            f32x4 r = O * (1.0f / L);
             if (a.gate) {
                 const float* gp = a.gate + (size_t)seq * a.gate_stride + (size_t)h * D + d;
 #pragma unroll
@@ -664,6 +664,13 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
         __builtin_amdgcn_sched_barrier(0);
         fold(s0);
     }
+    // the gate's sigmoid before the barrier, off the combine's tail (only
+    // with a gate: without one the stand-in row may hold any bits)
+    f32x4 gs = f32x4{1.f, 1.f, 1.f, 1.f};
+    if (a.gate) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gs[e] = sigmoid_ref(gt[e]);
+    }
     s_o[t] = O;
     s_m[t] = M;
     s_l[t] = L;
@@ -690,11 +697,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
             Lt += lg[g2] * c;
             Ot += og[g2] * c;
         }
-        f32x4 r = ns ? Ot / Lt : f32x4{0.f, 0.f, 0.f, 0.f};
-        if (a.gate) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) r[e] *= sigmoid_ref(gt[e]);
-        }
+        f32x4 r = ns ? Ot * (1.0f / Lt) * gs : f32x4{0.f, 0.f, 0.f, 0.f};
         *reinterpret_cast<f32x4*>(a.out + (size_t)seq * a.out_stride + (size_t)h * D + d) = r;
     }
 }
