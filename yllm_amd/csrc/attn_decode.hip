@@ -616,13 +616,22 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a)
     f32x4 ov[kRound];
     float M = -INFINITY, L = 0.0f;
     f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+    // The thread's slots are whole splits apart: one 64-bit address for its
+    // slot of split 0, then 32-bit offsets (a split past n_splits reads split
+    // 0's slot); a 64-bit index product per load had the round's last load
+    // issued ~400 instructions after its first.
+    const size_t slot0 = sbase * a.gmax + hn;
+    const float* const pml = a.part_ml + slot0 * 2;
+    const float* const po = a.part_o + slot0 * D + d;
+    const uint32_t sm = a.gmax * 2u, so = a.gmax * (uint32_t)D;  // floats per split
     auto issue = [&](uint32_t s0) {
+        const uint32_t om0 = s0 * sm, oo0 = s0 * so;
 #pragma unroll
         for (uint32_t r = 0; r < kRound; ++r) {
-            const uint32_t s = s0 + r * NG;
-            const size_t slot = (sbase + (s < a.n_splits ? s : 0u)) * a.gmax + hn;
-            ml[r] = *reinterpret_cast<const f32x2*>(a.part_ml + slot * 2);
-            ov[r] = *reinterpret_cast<const f32x4*>(a.part_o + slot * D + d);
+            const bool in = s0 + r * NG < a.n_splits;
+            const uint32_t om = in ? om0 + r * NG * sm : 0u, oo = in ? oo0 + r * NG * so : 0u;
+            ml[r] = *reinterpret_cast<const f32x2*>(pml + om);
+            ov[r] = *reinterpret_cast<const f32x4*>(po + oo);
         }
     };
     auto fold = [&](uint32_t s0) {
