@@ -214,10 +214,11 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(GdnDecodeArgs a)
 // One launch for the whole token: a workgroup of 1024 threads computes a
 // whole v head (TPC = 1024 / D threads per state column, SL = D / TPC
 // elements each), so the gated RMSNorm's sum over the head's D outputs stays
-// in the workgroup.  Every thread issues its loads at once (state slice, one
-// conv channel: threads 0..2D-1 the q/k channels of k head kh, 2D..3D-1 the v
-// channels of head h), then conv + silu, l2 norms, gates, the state update
-// and the normalised, gated outputs.  The barriers order LDS only: a
+// in the workgroup.  Every thread issues its loads at once (one conv channel:
+// threads 0..2D-1 the q/k channels of k head kh, 2D..3D-1 the v channels of
+// head h; z and the norm weight; its state slice last), one wave forms the
+// gates while they are in flight, then conv + silu, l2 norms, the outputs,
+// the new state and the normalised, gated outputs.  The barriers order LDS only: a
 // __syncthreads before the norm's sum waited for the state stores to
 // complete (~1.3 us of a ~5.4 us workgroup).
 //
