@@ -169,12 +169,14 @@ def test_decode_reference_config1_fixture(cuda, oracle, golden):
 @pytest.mark.parametrize("nh,nkv,hd,L", [
     (14, 2, 64, 512), (32, 8, 128, 1), (32, 8, 128, 31), (32, 8, 128, 33), (32, 8, 128, 4097),
     (28, 4, 128, 2048), (6, 4, 64, 300), (16, 2, 256, 777), (8, 8, 128, 20000),
-    (32, 16, 64, 6000), (24, 8, 256, 9000), (12, 8, 128, 7000)])
+    (32, 16, 64, 6000), (24, 8, 256, 9000), (12, 8, 128, 7000),
+    (8, 2, 64, 600), (8, 2, 128, 300), (32, 8, 128, 300), (6, 2, 64, 257)])
 def test_decode_parity(cuda, oracle, nh, nkv, hd, L):
     """Split-K decode against the oracle; kv head counts that are multiples of
     8 with whole query-head groups run the kv-head-first grids (32/8, 8/8,
     32/16 with two kv heads per XCD, 24/8 at d 256), 12/8 the split-major
-    ones."""
+    ones; 600, 300 and 257 keys run unsplit with several blocks per wave and
+    a partial last block."""
     from yllm_amd.attention import attn_decode
 
     kvd = nkv * hd
@@ -277,7 +279,7 @@ def test_decode_workspace_for_max_len_serves_every_position(cuda, oracle):
 
 
 @pytest.mark.parametrize("nh,nkv", [(8, 2), (32, 8)])
-@pytest.mark.parametrize("max_len", [100, 5000])
+@pytest.mark.parametrize("max_len", [100, 300, 5000])
 def test_decode_batch_empty_sequence_gives_zeros(cuda, oracle, max_len, nh, nkv):
     """A sequence with no keys gets a zero output row, with one split
     (max_len 100) as with several (5000), gated or not; 8 kv heads take the
