@@ -352,6 +352,8 @@ def _oracle_layer(oracle, S, st, qkv, z, alpha, beta_raw, conv_w, dt, a, norm_w,
     (2, 4, 64, 4, True),
     (4, 8, 128, 3, False),
     (1, 3, 64, 1, False),
+    (4, 12, 128, 6, True),  # conv width past 4 (eight taps loaded), 12 heads: a partial group of 8
+    (8, 24, 64, 8, False),
 ])
 def test_gdn_decode_matches_oracle(cuda, oracle, n_k, n_v, d, kw, w_f16, oop):
     """In place (one workgroup per head) and with the state alternating
