@@ -64,6 +64,50 @@ constexpr int kKeysPerBlock = 32;
 template <int D> constexpr int waves_of() { return 4; }
 template <int D> constexpr int nbuf_of() { return D <= 128 ? 2 : 1; }
 template <int D> constexpr int wg_per_cu() { return D <= 128 ? 2 : 1; }
+// K blocks staged through LDS (the LK instantiations, d <= 128) for splits
+// of at most this many keys, instead of loaded as MFMA operands.  Same box:
+// 32k keys (splits of 1024) 23.9 -> 23.1 us, 14/2 heads, d 64, 512 keys
+// (one split) 5.07 -> 4.37 us; on longer splits the staged form ran slower
+// (128k keys, splits of 4096: 79.5 -> 82.5 us; the 64-sequence batch,
+// ~3000: 703 -> 706 us), so those keep the operand loads.
+constexpr uint32_t kLdsSplitKeys = 1024;
+
+// Staged K block of one wave: 32 rows of D halves, each 16-byte chunk at
+// column c ^ kswz(r) of its row.  The score MFMA reads 16 rows (krow + 4t
+// below: rows {0-3, 8-11, 16-19, 24-27}, + 4 for t = 1) at one column per
+// 16-lane group; the swizzle gives those 16 rows 16 distinct 16-byte bank
+// columns of a 256-byte bank window (64 banks): at d = 128 (256-byte rows)
+// r & 15 with bit 4 folded into bit 2, at d = 64 (128-byte rows, two per
+// window) bits 1, 3, 4 of r for the 8 rows of each parity.
+template <int D>
+__device__ inline uint32_t kswz(uint32_t r)
+{
+    if constexpr (D == 128) return (r & 15u) ^ (((r >> 4) & 1u) << 2);
+    else return ((r >> 1) & 1u) | (((r >> 3) & 1u) << 1) | (((r >> 4) & 1u) << 2);
+}
+
+// One 16-byte HBM -> LDS load per lane (lane i writes at lds + 16 i), with
+// the launch's cache policy.  A __device__ function: lambdas in a kernel are
+// host-device, and the host pass drops a kernel whose lambda calls this
+// gfx950-only builtin.
+template <int POL>
+__device__ inline void k_dma16(__amdgpu_buffer_rsrc_t r, _Float16* lds, uint32_t voff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, POL);
+}
+
+// s_waitcnt vmcnt(N) (lgkmcnt, expcnt not waited for), fenced against moves
+// of memory operations and of the scheduler across it
+template <int N>
+__device__ inline void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
 
 __device__ inline f32x4 mfma16(const f16x8& a, const f16x8& b, const f32x4& c)
 {
@@ -102,7 +146,7 @@ struct Frag {
 // holds the token rotates the token's key, stores key and value into the
 // cache and substitutes them for the cache rows it loaded.  The cosines and
 // sines come from the host's cosf / sinf, as the reference computes them.
-template <int D, bool ROPE, int POL, bool KVM>
+template <int D, bool ROPE, int POL, bool KVM, bool LK>
 __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_split_kernel(DecodeArgs a,
                                                                                             DecodeRopeArg<ROPE> rp)
 {
@@ -110,7 +154,14 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     constexpr int kThreads = 64 * kWaves;
     constexpr int NC = D / 32;  // 32-wide d chunks of the QK contraction
     constexpr int NB = D / 16;  // 16-row d blocks of the PV output
-    __shared__ __attribute__((aligned(16))) float s_o[kWaves][16][D + 4];
+    // LK: each wave's two staged K blocks (separate variables, so the
+    // compiler can tell a read of one from the loads in flight into the
+    // other); after the key loop a wave's combine rows take their place
+    constexpr int KBH = LK ? kKeysPerBlock * D : 8;  // halves of one staged block
+    __shared__ __attribute__((aligned(16))) _Float16 s_k0[kWaves][KBH];
+    __shared__ __attribute__((aligned(16))) _Float16 s_k1[kWaves][KBH];
+    __shared__ __attribute__((aligned(16))) _Float16 s_qk[LK ? 2 * 16 * (D + 8) : 8];
+    __shared__ __attribute__((aligned(16))) float s_o[LK ? 1 : kWaves][16][D + 4];
     __shared__ float s_m[kWaves][16];
     __shared__ float s_l[kWaves][16];
     // the token's K bits by dimension, and its V bits by lane: element
@@ -170,17 +221,44 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(Vt), 0, head_bytes, 0x00020000);
     const uint32_t k_lane = (krow * D + g * 8) * 2;      // bytes within a block's K rows
     const uint32_t v_lane = (n * kVTile + g * 8) * 2;    // row d = n (+16b), positions 8g..8g+7
-    auto load = [&](Frag<D>& f, uint32_t blk) {
+    // LK: a block's K rows are NJ loads of 1 KB each (whole rows, contiguous
+    // in HBM); load j, lane l fills chunk 64 j + l of the staged block, i.e.
+    // row r = (64 j + l) / CPR at column p = (64 j + l) % CPR, and so reads
+    // the row's chunk p ^ kswz(r).  The score MFMA's operands are then read
+    // from LDS.  (Loaded directly as operands, every load instruction covers
+    // 16 rows x 64 bytes, and the same stream ran ~5 % slower.)
+    static_assert(!LK || ((D == 64 || D == 128) && nbuf_of<D>() == 2), "the swizzle and the two staged blocks");
+    constexpr int CPR = D / 8;                 // 16-byte chunks per K row
+    constexpr int NJ = kKeysPerBlock * CPR / 64;
+    constexpr int NL = (LK ? NJ : 2 * NC) + NB;  // loads per block and lane
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave, in a scalar register
+    auto kdma_off = [&](int j) -> uint32_t {
+        const uint32_t P = 64u * j + lane, r = P / CPR, p = P % CPR;
+        return r * D * 2 + ((p ^ kswz<D>(r)) * 16);
+    };
+    auto load = [&](Frag<D>& f, uint32_t blk, int slot) {
         const uint32_t key0 = kbeg + blk * kKeysPerBlock;
         const bool ok = blk < nblk;
-        const uint32_t kb = ok ? key0 * D * 2 + k_lane : 0x80000000u;
         const uint32_t vb = ok ? (key0 / kVTile) * D * kVTile * 2 + v_lane : 0x80000000u;
+        if constexpr (LK) {
+            // the slot's fragment reads of the previous block are complete
+            // (their MFMAs have consumed them; this wait only pins that down)
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            _Float16* dst = slot == 0 ? &s_k0[wv][0] : &s_k1[wv][0];
+            const uint32_t kb0 = ok ? key0 * D * 2 : 0x80000000u;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int j = 0; j < NJ; ++j) k_dma16<POL>(rK, dst + 512 * j, kb0 + kdma_off(j));
+            // K before V in issue order: the score MFMAs wait for K alone
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            const uint32_t kb = ok ? key0 * D * 2 + k_lane : 0x80000000u;
 #pragma unroll
-            for (int c = 0; c < NC; ++c)
-                f.k[t][c] = __builtin_bit_cast(
-                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rK, kb + (4 * t * D + c * 32) * 2, 0, POL));
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                    f.k[t][c] = __builtin_bit_cast(
+                        f16x8, __builtin_amdgcn_raw_buffer_load_b128(rK, kb + (4 * t * D + c * 32) * 2, 0, POL));
+        }
 #pragma unroll
         for (int b = 0; b < NB; ++b)
             f.v[b] = __builtin_bit_cast(f16x8,
@@ -196,8 +274,12 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     constexpr int D4 = D / 4;
     constexpr int QROW = D + 8;                                 // halves per staged row
     constexpr int QPT = (16 * D4 + kThreads - 1) / kThreads;   // float4s per thread
-    static_assert(sizeof(s_o) >= 2 * 16 * QROW * sizeof(_Float16), "q staging fits the combine area");
-    _Float16* s_q = reinterpret_cast<_Float16*>(&s_o[0][0][0]);  // [2][16][QROW]: hi, lo
+    static_assert(LK || sizeof(s_o) >= 2 * 16 * QROW * sizeof(_Float16), "q staging fits the combine area");
+    // [2][16][QROW]: hi, lo (LK: its own area; the K blocks' loads are in
+    // flight meanwhile)
+    _Float16* s_q;
+    if constexpr (LK) s_q = s_qk;
+    else s_q = reinterpret_cast<_Float16*>(&s_o[0][0][0]);
     // ROPE: pairs (d, d + half) of the first `span` dims for HALF / MROPE
     // (half = span / 2), (d, d + 1) for PAIRS; a thread rotating a float4 of
     // the first kind also loads its partner float4 at d +- half
@@ -271,7 +353,7 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     constexpr int NBUF = nbuf_of<D>();
     Frag<D> f[NBUF];
 #pragma unroll
-    for (int i = 0; i < NBUF; ++i) load(f[i], wave + i * kWaves);
+    for (int i = 0; i < NBUF; ++i) load(f[i], wave + i * kWaves, i);
     // nothing below moves above the block loads (a use of q or the rotation's
     // loads scheduled among them waits for them before the rest are issued)
     __builtin_amdgcn_sched_barrier(0);
@@ -363,7 +445,18 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         }
     }
 
-    auto compute = [&](Frag<D>& f, uint32_t key0) {
+    // LK: the lane's fragment offsets in a staged block -- row krow + 4t,
+    // dims c*32 + 8g .. +7, i.e. chunk 4c + g of the row
+    uint32_t koff[2][NC];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const uint32_t r = krow + 4 * t;
+            koff[t][c] = r * D + (((4u * c + g) ^ kswz<D>(r)) * 8);  // in halves
+        }
+
+    auto compute = [&](Frag<D>& f, uint32_t key0, int slot) {
         // ROPE: the block holding the token (uniform over the wave)
         const bool tok_here = ROPE && owns_tok && tpos >= key0 && tpos < key0 + kKeysPerBlock;
         const uint32_t rr = tpos - key0;
@@ -373,8 +466,13 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
             s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                s[t] = mfma16(f.k[t][c], qhi[c], s[t]);
-                s[t] = mfma16(f.k[t][c], qlo[c], s[t]);
+                f16x8 kf;
+                if constexpr (LK)
+                    kf = *reinterpret_cast<const f16x8*>((slot == 0 ? &s_k0[wv][0] : &s_k1[wv][0]) + koff[t][c]);
+                else
+                    kf = f.k[t][c];
+                s[t] = mfma16(kf, qhi[c], s[t]);
+                s[t] = mfma16(kf, qlo[c], s[t]);
             }
         }
         // s[t][i] is head n, key key0 + 8g + 4t + i
@@ -489,13 +587,34 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
 #pragma unroll
         for (int i = 0; i < NBUF; ++i) {
             const uint32_t b = wave + (j + i) * kWaves;
-            compute(f[i], kbeg + b * kKeysPerBlock);
-            load(f[i], b + NBUF * kWaves);
+            // LK: the block's K has landed once at most its own V loads and
+            // the NBUF - 1 blocks issued after it are in flight (issue order
+            // is pinned by the waits' scheduling barriers and those in load;
+            // the compiler waits for V itself before the P.V MFMAs)
+            if constexpr (LK) wait_vm<(NBUF - 1) * NL + NB>();
+            compute(f[i], kbeg + b * kKeysPerBlock, i);
+            load(f[i], b + NBUF * kWaves, i);
+            if constexpr (LK) __builtin_amdgcn_sched_barrier(0);
         }
     }
+    if constexpr (LK) {  // two slots; the second's loads are the last issued
+        if (j < nbw) {
+            wait_vm<NL + NB>();
+            compute(f[0], kbeg + (wave + j * kWaves) * kKeysPerBlock, 0);
+        }
+        if (j + 1 < nbw) {
+            wait_vm<NB>();
+            compute(f[1], kbeg + (wave + (j + 1) * kWaves) * kKeysPerBlock, 1);
+        }
+    } else {
 #pragma unroll
-    for (int i = 0; i < NBUF; ++i)
-        if (j + i < nbw) compute(f[i], kbeg + (wave + (j + i) * kWaves) * kKeysPerBlock);
+        for (int i = 0; i < NBUF; ++i)
+            if (j + i < nbw) compute(f[i], kbeg + (wave + (j + i) * kWaves) * kKeysPerBlock, i);
+    }
+    // LK: every load into the staged blocks has landed (a slot past the
+    // wave's blocks may still be taking zeros) before the combine rows
+    // overwrite them
+    if constexpr (LK) wait_vm<0>();
 
     if (ROPE && owns_tok && threadIdx.x < (uint32_t)D) {  // the token's K and V into the cache
         const uint32_t d = threadIdx.x;
@@ -511,13 +630,22 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     // accumulators; after one barrier the threads that form an output float4
     // rescale the four waves' float4s to the head's maximum as they sum them.
     // (Rescaling in the staging waves took a second barrier and LDS round.)
+    // combine row r of wave w: LK, rows 0-7 in the wave's first staged
+    // block and rows 8-15 in its second (8 (D + 4) floats fit one block)
+    static_assert(!LK || 8 * (D + 4) * 4 <= KBH * 2, "combine rows fit a staged block");
+    auto orow = [&](uint32_t w, uint32_t r) -> float* {
+        if constexpr (LK)
+            return reinterpret_cast<float*>(r < 8 ? &s_k0[w][0] : &s_k1[w][0]) + (r & 7u) * (D + 4);
+        else
+            return &s_o[w][r][0];
+    };
     if (g == 0) {
         s_m[wave][n] = m;
         s_l[wave][n] = l;
     }
     if ((uint32_t)n < G) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) *reinterpret_cast<f32x4*>(&s_o[wave][n][b * 16 + 4 * g]) = o[b];
+        for (int b = 0; b < NB; ++b) *reinterpret_cast<f32x4*>(orow(wave, n) + b * 16 + 4 * g) = o[b];
     }
     // an LDS-only barrier: a full barrier also waited for the owner's token
     // stores (scattered 2-byte K/V writes issued before the loop), which made
@@ -535,7 +663,7 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
         for (int w = 0; w < kWaves; ++w) {
             mw[w] = s_m[w][hn];
             lw[w] = s_l[w][hn];
-            ow[w] = *reinterpret_cast<const f32x4*>(&s_o[w][hn][d]);
+            ow[w] = *reinterpret_cast<const f32x4*>(orow(w, hn) + d);
         }
         float M = -INFINITY;
 #pragma unroll
@@ -735,18 +863,29 @@ void launch_merge(const DecodeArgs& a, hipStream_t st)
     hipLaunchKernelGGL((decode_merge_kernel<D, NG, KVM>), grid, dim3(e4 * NG), 0, st, a);
 }
 
+template <int D, bool ROPE, bool KVM, bool LK>
+void launch_split(const DecodeArgs& a, const DecodeRopeArg<ROPE>& rr, hipStream_t st)
+{
+    const dim3 grid = KVM ? dim3(a.n_kv, a.n_splits, a.n_seq) : dim3(a.n_splits, a.n_kv, a.n_seq);
+    if (decode_streams(a))
+        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvStream, KVM, LK>), grid, dim3(64 * waves_of<D>()), 0, st,
+                           a, rr);
+    else
+        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvDefault, KVM, LK>), grid, dim3(64 * waves_of<D>()), 0, st,
+                           a, rr);
+}
+
 template <int D, bool ROPE, bool KVM>
 hipError_t launch_decode_o(const DecodeArgs& a, const DecodeRope& r, hipStream_t st)
 {
-    const dim3 grid = KVM ? dim3(a.n_kv, a.n_splits, a.n_seq) : dim3(a.n_splits, a.n_kv, a.n_seq);
     DecodeRopeArg<ROPE> rr{};
     if constexpr (ROPE) rr = r;
-    if (decode_streams(a))
-        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvStream, KVM>), grid, dim3(64 * waves_of<D>()), 0, st, a,
-                           rr);
-    else
-        hipLaunchKernelGGL((decode_split_kernel<D, ROPE, kKvDefault, KVM>), grid, dim3(64 * waves_of<D>()), 0, st, a,
-                           rr);
+    if constexpr (D <= 128) {
+        if (a.split_keys <= kLdsSplitKeys) launch_split<D, ROPE, KVM, true>(a, rr, st);
+        else launch_split<D, ROPE, KVM, false>(a, rr, st);
+    } else {
+        launch_split<D, ROPE, KVM, false>(a, rr, st);
+    }
     if (a.n_splits > 1) {
         // the fewest split subsets whose one round of loads (kMergeRound per
         // thread) covers every split: one memory round trip and the smallest
