@@ -13,7 +13,9 @@
 // with the next block's loads in flight while the current one is computed
 // (two register fragment sets for d <= 128): two waves per SIMD, each with
 // up to 32 KB outstanding.  Measured on MI355X at 32k keys: this beats a
-// 4-deep ring at one wave per SIMD and 8-wave workgroups.
+// 4-deep ring at one wave per SIMD and 8-wave workgroups.  On splits of up
+// to kLdsSplitKeys keys a block's K goes to LDS in whole-row 1 KB loads and
+// the score operands are read from there (see kLdsSplitKeys).
 //
 // MFMA formulation (v_mfma_f32_16x16x32_f16, per wave, per 32-key block):
 //   S^T[key][head] = K[key][:] . Q^T[:][head]       A = K rows, B = q (16 head
@@ -64,10 +66,11 @@ constexpr int kKeysPerBlock = 32;
 template <int D> constexpr int waves_of() { return 4; }
 template <int D> constexpr int nbuf_of() { return D <= 128 ? 2 : 1; }
 template <int D> constexpr int wg_per_cu() { return D <= 128 ? 2 : 1; }
-// K blocks staged through LDS (the LK instantiations, d <= 128) for splits
-// of at most this many keys, instead of loaded as MFMA operands.  Same box:
-// 32k keys (splits of 1024) 23.9 -> 23.1 us, 14/2 heads, d 64, 512 keys
-// (one split) 5.07 -> 4.37 us; on longer splits the staged form ran slower
+// K blocks staged through LDS (the LK instantiations) for splits of at most
+// this many keys, instead of loaded as MFMA operands.  Same box: 32k keys
+// (splits of 1024) 23.9 -> 23.1 us, 14/2 heads, d 64, 512 keys (one split)
+// 5.07 -> 4.37 us, 16/2 heads, d 256, 4352 keys (splits of 128) 10.6 ->
+// 10.0 us; on longer splits the staged form ran slower
 // (128k keys, splits of 4096: 79.5 -> 82.5 us; the 64-sequence batch,
 // ~3000: 703 -> 706 us), so those keep the operand loads.
 constexpr uint32_t kLdsSplitKeys = 1024;
@@ -82,7 +85,7 @@ constexpr uint32_t kLdsSplitKeys = 1024;
 template <int D>
 __device__ inline uint32_t kswz(uint32_t r)
 {
-    if constexpr (D == 128) return (r & 15u) ^ (((r >> 4) & 1u) << 2);
+    if constexpr (D >= 128) return (r & 15u) ^ (((r >> 4) & 1u) << 2);
     else return ((r >> 1) & 1u) | (((r >> 3) & 1u) << 1) | (((r >> 4) & 1u) << 2);
 }
 
@@ -157,11 +160,14 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     // LK: each wave's two staged K blocks (separate variables, so the
     // compiler can tell a read of one from the loads in flight into the
     // other); after the key loop a wave's combine rows take their place
+    // (d = 256: one block per wave, and the combine rows keep their own area)
+    constexpr int NBUF = nbuf_of<D>();
+    constexpr bool OK_ROWS = LK && NBUF == 2;  // combine rows in the staged blocks
     constexpr int KBH = LK ? kKeysPerBlock * D : 8;  // halves of one staged block
     __shared__ __attribute__((aligned(16))) _Float16 s_k0[kWaves][KBH];
-    __shared__ __attribute__((aligned(16))) _Float16 s_k1[kWaves][KBH];
-    __shared__ __attribute__((aligned(16))) _Float16 s_qk[LK ? 2 * 16 * (D + 8) : 8];
-    __shared__ __attribute__((aligned(16))) float s_o[LK ? 1 : kWaves][16][D + 4];
+    __shared__ __attribute__((aligned(16))) _Float16 s_k1[kWaves][NBUF == 2 ? KBH : 8];
+    __shared__ __attribute__((aligned(16))) _Float16 s_qk[OK_ROWS ? 2 * 16 * (D + 8) : 8];
+    __shared__ __attribute__((aligned(16))) float s_o[OK_ROWS ? 1 : kWaves][16][D + 4];
     __shared__ float s_m[kWaves][16];
     __shared__ float s_l[kWaves][16];
     // the token's K bits by dimension, and its V bits by lane: element
@@ -227,7 +233,7 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     // the row's chunk p ^ kswz(r).  The score MFMA's operands are then read
     // from LDS.  (Loaded directly as operands, every load instruction covers
     // 16 rows x 64 bytes, and the same stream ran ~5 % slower.)
-    static_assert(!LK || ((D == 64 || D == 128) && nbuf_of<D>() == 2), "the swizzle and the two staged blocks");
+    static_assert(!LK || D == 64 || D == 128 || D == 256, "the swizzle's row widths");
     constexpr int CPR = D / 8;                 // 16-byte chunks per K row
     constexpr int NJ = kKeysPerBlock * CPR / 64;
     constexpr int NL = (LK ? NJ : 2 * NC) + NB;  // loads per block and lane
@@ -274,11 +280,11 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     constexpr int D4 = D / 4;
     constexpr int QROW = D + 8;                                 // halves per staged row
     constexpr int QPT = (16 * D4 + kThreads - 1) / kThreads;   // float4s per thread
-    static_assert(LK || sizeof(s_o) >= 2 * 16 * QROW * sizeof(_Float16), "q staging fits the combine area");
-    // [2][16][QROW]: hi, lo (LK: its own area; the K blocks' loads are in
-    // flight meanwhile)
+    static_assert(OK_ROWS || sizeof(s_o) >= 2 * 16 * QROW * sizeof(_Float16), "q staging fits the combine area");
+    // [2][16][QROW]: hi, lo (combine rows in the staged blocks: its own area;
+    // the K blocks' loads are in flight meanwhile)
     _Float16* s_q;
-    if constexpr (LK) s_q = s_qk;
+    if constexpr (OK_ROWS) s_q = s_qk;
     else s_q = reinterpret_cast<_Float16*>(&s_o[0][0][0]);
     // ROPE: pairs (d, d + half) of the first `span` dims for HALF / MROPE
     // (half = span / 2), (d, d + 1) for PAIRS; a thread rotating a float4 of
@@ -350,7 +356,6 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     }
 
     // NBUF blocks of this wave in flight
-    constexpr int NBUF = nbuf_of<D>();
     Frag<D> f[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF; ++i) load(f[i], wave + i * kWaves, i);
@@ -597,7 +602,12 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
             if constexpr (LK) __builtin_amdgcn_sched_barrier(0);
         }
     }
-    if constexpr (LK) {  // two slots; the second's loads are the last issued
+    if constexpr (LK && NBUF == 1) {
+        if (j < nbw) {
+            wait_vm<NB>();
+            compute(f[0], kbeg + (wave + j * kWaves) * kKeysPerBlock, 0);
+        }
+    } else if constexpr (LK) {  // two slots; the second's loads are the last issued
         if (j < nbw) {
             wait_vm<NL + NB>();
             compute(f[0], kbeg + (wave + j * kWaves) * kKeysPerBlock, 0);
@@ -632,9 +642,9 @@ __global__ __launch_bounds__(64 * waves_of<D>(), wg_per_cu<D>()) void decode_spl
     // (Rescaling in the staging waves took a second barrier and LDS round.)
     // combine row r of wave w: LK, rows 0-7 in the wave's first staged
     // block and rows 8-15 in its second (8 (D + 4) floats fit one block)
-    static_assert(!LK || 8 * (D + 4) * 4 <= KBH * 2, "combine rows fit a staged block");
+    static_assert(!OK_ROWS || 8 * (D + 4) * 4 <= KBH * 2, "combine rows fit a staged block");
     auto orow = [&](uint32_t w, uint32_t r) -> float* {
-        if constexpr (LK)
+        if constexpr (OK_ROWS)
             return reinterpret_cast<float*>(r < 8 ? &s_k0[w][0] : &s_k1[w][0]) + (r & 7u) * (D + 4);
         else
             return &s_o[w][r][0];
@@ -880,12 +890,8 @@ hipError_t launch_decode_o(const DecodeArgs& a, const DecodeRope& r, hipStream_t
 {
     DecodeRopeArg<ROPE> rr{};
     if constexpr (ROPE) rr = r;
-    if constexpr (D <= 128) {
-        if (a.split_keys <= kLdsSplitKeys) launch_split<D, ROPE, KVM, true>(a, rr, st);
-        else launch_split<D, ROPE, KVM, false>(a, rr, st);
-    } else {
-        launch_split<D, ROPE, KVM, false>(a, rr, st);
-    }
+    if (a.split_keys <= kLdsSplitKeys) launch_split<D, ROPE, KVM, true>(a, rr, st);
+    else launch_split<D, ROPE, KVM, false>(a, rr, st);
     if (a.n_splits > 1) {
         // the fewest split subsets whose one round of loads (kMergeRound per
         // thread) covers every split: one memory round trip and the smallest
