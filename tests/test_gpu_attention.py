@@ -170,7 +170,9 @@ def test_decode_reference_config1_fixture(cuda, oracle, golden):
     (14, 2, 64, 512), (32, 8, 128, 1), (32, 8, 128, 31), (32, 8, 128, 33), (32, 8, 128, 4097),
     (28, 4, 128, 2048), (6, 4, 64, 300), (16, 2, 256, 777), (8, 8, 128, 20000),
     (32, 16, 64, 6000), (24, 8, 256, 9000), (12, 8, 128, 7000),
-    (8, 2, 64, 600), (8, 2, 128, 300), (32, 8, 128, 300), (6, 2, 64, 257)])
+    (8, 2, 64, 600), (8, 2, 128, 300), (32, 8, 128, 300), (6, 2, 64, 257),
+    # splits of 1280 keys (more than 1024): K loaded as MFMA operands
+    (8, 8, 64, 40000), (16, 8, 256, 40000)])
 def test_decode_parity(cuda, oracle, nh, nkv, hd, L):
     """Split-K decode against the oracle; kv head counts that are multiples of
     8 with whole query-head groups run the kv-head-first grids (32/8, 8/8,

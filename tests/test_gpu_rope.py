@@ -234,6 +234,8 @@ def test_rope_kv_store_full_size_sampled_rows(cuda, oracle):
     ("mrope", 16, 2, 256, 0, 64, True),        # the token is the only key
     ("none", 28, 4, 128, 127, 0, False),       # the token ends a 128-key split
     ("pairs", 8, 8, 64, 128, 0, False),        # the token starts a split
+    ("pairs", 32, 8, 128, 39999, 0, False),    # splits of 1280 keys: K loaded as MFMA operands
+    ("half", 16, 8, 256, 39999, 0, True),      # the same at d 256, gated
 ])
 def test_decode_rope_matches_oracle_and_two_launches(cuda, oracle, kind, nh, nkv, d, pos, n_rot, gated):
     """yhip_attn_decode_rope against the oracle (the reference's RoPE, store
