@@ -262,8 +262,13 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     // token is issued before any wait, so its chain holds one memory round
     // trip
     const float beta_raw = a.beta_raw[h], alpha = a.alpha[h], dt_bias = a.dt_bias[h], ssm_a = a.ssm_a[h];
-    const float* Sp = a.S + ((size_t)h * D + j) * D + part * SL;
-    float* So = a.S_out + ((size_t)h * D + j) * D + part * SL;
+    // a thread's SL elements of row j: float4 r at 4 (r TPC + part), so one
+    // 16-byte load instruction of a row's TPC threads covers 16 TPC whole,
+    // consecutive bytes (as consecutive SL-element runs per thread, every
+    // instruction took every other 16-byte chunk of its rows)
+    const float* Sp = a.S + ((size_t)h * D + j) * D + part * 4;
+    float* So = a.S_out + ((size_t)h * D + j) * D + part * 4;
+    auto el = [&](int i) -> uint32_t { return (uint32_t)(i / 4) * 4u * TPC + part * 4u + (uint32_t)(i % 4); };
     // this thread's conv channel: q_i (tid = 2i < 2D) and k_i (tid = 2i + 1)
     // of head kh side by side, so one lane pair holds both for the q.k sum;
     // v (2D <= tid < 3D) of head h
@@ -295,7 +300,7 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     float s[SL];
 #pragma unroll
     for (int i = 0; i < SL; i += 4) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(Sp + i);
+        const f32x4 x = *reinterpret_cast<const f32x4*>(Sp + i * TPC);
 #pragma unroll
         for (int e = 0; e < 4; ++e) s[i + e] = x[e];
     }
@@ -366,8 +371,8 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
     float kr[SL], qr[SL];  // the thread's slice of the raw q, k rows
 #pragma unroll
     for (int i = 0; i < SL; ++i) {
-        kr[i] = ks[part * SL + i];
-        qr[i] = qs[part * SL + i];
+        kr[i] = ks[el(i)];
+        qr[i] = qs[el(i)];
     }
     // Column j's output from the state before the token:
     // o_j = (g rq (S_j . q) + d_j rk rq (k . q)) / sqrt(D) with
@@ -401,7 +406,7 @@ __global__ __launch_bounds__(1024) void gdn_decode_head_kernel(GdnDecodeArgs a)
             f32x4 x;
 #pragma unroll
             for (int e = 0; e < 4; ++e) x[e] = s[i + e];
-            *reinterpret_cast<f32x4*>(So + i) = x;
+            *reinterpret_cast<f32x4*>(So + i * TPC) = x;
         }
     }
     // rmsnorm_gated over the head's D outputs (matvec.c:1007-1021), as
